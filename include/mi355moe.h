@@ -1,0 +1,120 @@
+/*
+ * mi355moe -- C ABI of the MI355X (gfx950) codebook-dequant MoE expert path.
+ *
+ * Every entry point takes plain device pointers, sizes and a HIP stream (as void*), validates its arguments on the
+ * host before launching anything, and returns MI_OK or an MI_ERR_* code.  The library allocates nothing: the caller
+ * owns every buffer, including the workspace.  Work is launched only on the given stream; calls that share a
+ * workspace must be ordered on one stream.  Nothing here is internally threaded.
+ *
+ * Reference interfaces (shallmall/kaggle-llm-endpoint, paths relative to launcher/glm53-flash/engine/glm53/):
+ *   ResidentFetch.apply(p, x, idx, w, layer, limit)        resident.py:100-108   -> mi_moe_decode / mi_moe_prefill
+ *   moe_matvec(planes, qtype, nblk, idx, X)                pallas_moe.py:238-307 -> mi_matvec
+ *   ragged_plan(idx, w, E, tm)                             pallas_moe.py:564-592 -> mi_ragged_plan
+ *   moe_ragged_gateup / moe_ragged_down                    pallas_moe.py:622-755 -> mi_moe_prefill
+ *   dequant_planes (XLA dequant of the planar tables)      planes.py:196-206     -> mi_dequant
+ *   quant8.dequant_tree + x @ W (int8 projections)         quant8.py:91-99       -> mi_int8_project
+ */
+#ifndef MI355MOE_H
+#define MI355MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------------------------------------------ */
+#define MI_OK              0
+#define MI_ERR_NULL        1  /* a required pointer is NULL                                                      */
+#define MI_ERR_QTYPE       2  /* unsupported qtype (the reference raises ValueError, planes.py:70,206)           */
+#define MI_ERR_SHAPE       3  /* rows/cols/experts outside what the kernels tile (pallas_moe.py:252-255 asserts) */
+#define MI_ERR_TOKENS      4  /* N, k or N*k outside the entry point's limits                                    */
+#define MI_ERR_WORKSPACE   5  /* workspace NULL or smaller than the *_workspace() size                           */
+#define MI_ERR_MISMATCH    6  /* gate/up/down tables do not chain (up != gate shape, down.cols != gate.rows)     */
+#define MI_ERR_LAUNCH      7  /* the HIP runtime reported an error at launch                                     */
+#define MI_ERR_ARG         8  /* any other invalid scalar argument                                               */
+
+/* ---- formats ----------------------------------------------------------------------------------------------- */
+#define MI_QT_CB3    1   /* 3-bit codes (10 per u32) + 8 bf16 centroids per (row, 128-column group)              */
+#define MI_QT_IQ3_S  2   /* llama.cpp IQ3_S in the reference's planar tables (planes.py:22-25)                   */
+
+/*
+ * One expert table: E experts of one matrix kind (gate, up or down), every expert R rows x K inputs, stored as
+ * planes of u32 [E * rows_p, R] -- the matrix row is the minor (fastest) axis, exactly as the reference stores its
+ * tables (planes.py:5-14).  plane[] order:
+ *   MI_QT_IQ3_S : {qs, sg, qh, sc, d}   -- the reference's planes, unchanged (planes.py:45)
+ *   MI_QT_CB3   : {qs, cb}              -- qs: ceil(K/10) code words per row (kernel bit layout, see formats.py);
+ *                                          cb: 4 u32 per (row, group) = bytes lo[0..3], lo[4..7], hi[0..3], hi[4..7]
+ *                                          of the 8 bf16 centroids.
+ * R must be a multiple of 256 (each wavefront lane owns 4 consecutive rows of a 256-row block); K a multiple of 256
+ * (IQ3_S) or 128 (CB3).
+ */
+typedef struct mi_table {
+    int32_t qtype;
+    int32_t rows;        /* R */
+    int32_t cols;        /* K */
+    int32_t n_experts;   /* E */
+    const uint32_t *plane[5];
+} mi_table;
+
+/* x dtypes for mi_matvec */
+#define MI_X_BF16  0     /* bf16 activations: dot products on bf16 pairs, exact products, f32 accumulation        */
+#define MI_X_F32   1     /* f32 activations: split into bf16 hi + lo, two exact bf16 dots per pair (~2^-17 rel)   */
+
+/*
+ * Fused routed-expert matvec, one output row vector per slot (moe_matvec, pallas_moe.py:238-307):
+ *   out[i, r] = sum_n W_{idx[i]}[r, n] * x_i[n]       for i < n_slots, r < R     (f32 accumulation, f32 out)
+ * x: n_slots rows of K values (bf16 bits or f32 per x_dtype), row stride x_stride elements.
+ * Slots that share an expert are grouped so each expert's codes are read once.  idx values outside [0, E) give a
+ * zero row.  n_slots <= MI_MAX_SLOTS.
+ */
+#define MI_MAX_SLOTS 128
+int mi_matvec(const mi_table *t, const int32_t *idx, int32_t n_slots, const void *x, int32_t x_dtype,
+              int32_t x_stride, float *out, void *workspace, size_t workspace_bytes, void *stream);
+size_t mi_matvec_workspace(const mi_table *t, int32_t n_slots);
+
+/*
+ * Fused MoE decode layer (ResidentFetch._apply_kernel composition, resident.py:110-120), tokens grouped by expert:
+ *   for each token n < N and slot j < k with e = idx[n, j]:
+ *     g = Wgate_e x_n, u = Wup_e x_n, h = silu(min(g, limit)) * clip(u, -limit, limit)   (model.py:119-122)
+ *     y = Wdown_e h
+ *   out[n] = sum_j w[n, j] y_{n,j}  (+ the shared expert's y for every token, weight 1, if shared_expert >= 0)
+ * x: bf16 [N, D] (D = gate.cols), idx int32 [N, k], w f32 [N, k].  h and every accumulation stay f32
+ * (resident.py:114-120).  out_f32 [N, D] and/or out_bf16 [N, D] (either may be NULL, not both).
+ * shared_expert: an expert index of the same tables applied to every token with weight 1, or -1.
+ * Limits: N <= 16, N*k <= MI_MAX_SLOTS, E <= 1024.  Deterministic (fixed-order reductions, no float atomics).
+ * The workspace must be zero-filled before its first use; every completed call leaves it reusable.
+ */
+int mi_moe_decode(const mi_table *gate, const mi_table *up, const mi_table *down, const uint16_t *x_bf16,
+                  int32_t N, int32_t k, const int32_t *idx, const float *w, int32_t shared_expert, float limit,
+                  float *out_f32, uint16_t *out_bf16, void *workspace, size_t workspace_bytes, void *stream);
+size_t mi_moe_decode_workspace(const mi_table *gate, const mi_table *down, int32_t N, int32_t k,
+                               int32_t shared_expert);
+
+/*
+ * Exact dequantized weights of expert e (natural input order): out f32 [R, K].  Restates dequant_planes
+ * (planes.py:196-206) / the codebook closed form; used to check the kernels' decode bit for bit.
+ */
+int mi_dequant(const mi_table *t, int32_t expert, float *out, void *stream);
+
+/*
+ * int8 per-output-channel projection (quant8.py:91-99 + x @ W):
+ *   y[b, o] = sum_i x[b, i] * bf16(f32(q[o, i]) * s[o])     f32 accumulation, bf16 out (+ optional f32 out)
+ * x bf16 [B, n_in]; qT int8 [n_out, n_in] (the reference's q [in, out] transposed once at load);
+ * s f32 [n_out].  1 <= B <= 32, n_in % 256 == 0, n_out % 16 == 0.  The weights are dequantized to bf16 in
+ * registers and contracted on the matrix cores (bf16 x bf16 products are exact, f32 accumulation).
+ * The workspace (zero-filled before first use, reusable after every completed call) holds split-K partials.
+ */
+int mi_int8_project(const uint16_t *x_bf16, int32_t B, const int8_t *qT, const float *s, int32_t n_in,
+                    int32_t n_out, uint16_t *y_bf16, float *y_f32, void *workspace, size_t workspace_bytes,
+                    void *stream);
+size_t mi_int8_project_workspace(int32_t B, int32_t n_in, int32_t n_out);
+
+const char *mi_strerror(int status);
+int mi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MI355MOE_H */

@@ -1,0 +1,12 @@
+"""MI355X-native (gfx950) codebook-dequant MoE expert path: HIP kernels behind a C ABI (include/mi355moe.h),
+loaded with ctypes, and the reference's ``ResidentFetch`` operator interface on top.
+
+The directory name is not a Python identifier; it is imported as ``kaggle_llm_endpoint_amd`` through
+``load_package()`` of ``__graft_entry__`` / ``tests/conftest.py``.
+"""
+from . import _lib, formats  # noqa: F401
+from .resident import (ExpertTable, ResidentFetch, dequant, int8_project, matvec, moe_decode,  # noqa: F401
+                       to_device_planes)
+
+__all__ = ["ExpertTable", "ResidentFetch", "dequant", "int8_project", "matvec", "moe_decode", "to_device_planes",
+           "formats"]

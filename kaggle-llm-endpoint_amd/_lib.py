@@ -1,0 +1,73 @@
+"""ctypes binding of the C ABI in include/mi355moe.h (the in-tree libmi355moe.so built by build.py).
+
+Loading fails loudly when the library is missing: there is no CPU fallback anywhere in the package.
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmi355moe.so")
+
+MI_OK = 0
+MI_QT_CB3 = 1
+MI_QT_IQ3_S = 2
+MI_X_BF16 = 0
+MI_X_F32 = 1
+MI_MAX_SLOTS = 128
+MAX_DECODE_TOKENS = 16
+
+QTYPES = {"CB3": MI_QT_CB3, "IQ3_S": MI_QT_IQ3_S}
+PLANE_KEYS = {"CB3": ("qs", "cb"), "IQ3_S": ("qs", "sg", "qh", "sc", "d")}
+
+# every symbol the header declares (tests check the library exports them)
+EXPORTS = ("mi_matvec", "mi_matvec_workspace", "mi_moe_decode", "mi_moe_decode_workspace", "mi_dequant",
+           "mi_int8_project", "mi_int8_project_workspace", "mi_strerror", "mi_version")
+
+
+class MiTable(ctypes.Structure):
+    _fields_ = [("qtype", ctypes.c_int32), ("rows", ctypes.c_int32), ("cols", ctypes.c_int32),
+                ("n_experts", ctypes.c_int32), ("plane", ctypes.c_void_p * 5)]
+
+
+class MiError(RuntimeError):
+    def __init__(self, fn, status, msg):
+        super().__init__("%s failed: status %d (%s)" % (fn, status, msg))
+        self.status = status
+
+
+_LIB = None
+
+
+def lib():
+    """The loaded library (raises if it has not been built)."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError("libmi355moe.so is not built: run `python kaggle-llm-endpoint_amd/build.py` "
+                           "(or __graft_entry__.build()) first")
+    L = ctypes.CDLL(LIB_PATH)
+    P, I, Z, F = ctypes.c_void_p, ctypes.c_int32, ctypes.c_size_t, ctypes.c_float
+    T = ctypes.POINTER(MiTable)
+    sig = {
+        "mi_matvec": (I, [T, P, I, P, I, I, P, P, Z, P]),
+        "mi_matvec_workspace": (Z, [T, I]),
+        "mi_moe_decode": (I, [T, T, T, P, I, I, P, P, I, F, P, P, P, Z, P]),
+        "mi_moe_decode_workspace": (Z, [T, T, I, I, I]),
+        "mi_dequant": (I, [T, I, P, P]),
+        "mi_int8_project": (I, [P, I, P, P, I, I, P, P, P, Z, P]),
+        "mi_int8_project_workspace": (Z, [I, I, I]),
+        "mi_strerror": (ctypes.c_char_p, [I]),
+        "mi_version": (I, []),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _LIB = L
+    return L
+
+
+def check(fn, status):
+    if status != MI_OK:
+        raise MiError(fn, status, lib().mi_strerror(status).decode())

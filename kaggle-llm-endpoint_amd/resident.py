@@ -1,0 +1,216 @@
+"""The drop-in operator: a ``ResidentFetch`` with the reference's constructor and ``apply`` signature
+(resident.py:68-108), backed by the HIP kernels of libmi355moe.so.
+
+``moe_dense`` duck-types its ``fetch`` argument (model.py:847-848):
+    y = fetch.apply(p, xf, idx, w, layer, cfg.swiglu_limit)
+with ``p = {"gate_q" | "up_q" | "down_q": {plane: u32 [1 or none, E*rows_p, R]}, ...}`` and ``self.qtypes[layer]``
+naming each table's format.  The same call works here with the planes held as torch int32 tensors on the GPU.
+
+Everything runs on the current torch (HIP) stream; there is no CPU path.
+"""
+import ctypes
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import MiTable, check, lib
+
+QK = 256
+
+
+def _plane_rows(qtype, K):
+    if qtype == "IQ3_S":
+        nblk = K // QK
+        W = 16 * nblk
+        return {"qs": W, "sg": W // 2, "qh": W // 8, "sc": W // 16, "d": (nblk + 1) // 2}
+    if qtype == "CB3":
+        return {"qs": -(-K // 10), "cb": 4 * (K // 128)}
+    raise ValueError(qtype)                     # the reference raises ValueError on an unknown qtype (planes.py:70)
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def to_device_planes(planes, device="cuda"):
+    """{plane: numpy u32 array} -> {plane: torch int32 tensor} on the device (bit-identical)."""
+    return {k: torch.from_numpy(np.ascontiguousarray(v).view(np.int32)).to(device) for k, v in planes.items()}
+
+
+class ExpertTable:
+    """One matrix kind (gate, up or down) of E experts, R rows x K inputs each, as device planes."""
+
+    def __init__(self, qtype, planes, rows, cols):
+        if qtype not in _lib.QTYPES:
+            raise ValueError("unsupported qtype %r" % (qtype,))
+        self.qtype, self.rows, self.cols = qtype, int(rows), int(cols)
+        keys = _lib.PLANE_KEYS[qtype]
+        rp = _plane_rows(qtype, cols)
+        self.planes = {}
+        for k in keys:
+            a = planes[k]
+            if a.dim() == 3:                       # the reference's leading chip axis [1, E*rows_p, R]
+                if a.shape[0] != 1:
+                    raise ValueError("one device holds the full expert set: leading axis must be 1")
+                a = a[0]
+            if a.dtype not in (torch.int32, torch.uint32) or not a.is_cuda:
+                raise ValueError("plane %r must be a 32-bit integer tensor on the GPU" % k)
+            if a.shape[-1] != self.rows or a.shape[0] % rp[k]:
+                raise ValueError("plane %r has shape %s, expected [E*%d, %d]" % (k, tuple(a.shape), rp[k], self.rows))
+            self.planes[k] = a.contiguous()
+        self.n_experts = self.planes["qs"].shape[0] // rp["qs"]
+        for k in keys:
+            if self.planes[k].shape[0] != self.n_experts * rp[k]:
+                raise ValueError("plane %r does not hold %d experts" % (k, self.n_experts))
+        self._c = MiTable()
+        self._c.qtype = _lib.QTYPES[qtype]
+        self._c.rows, self._c.cols, self._c.n_experts = self.rows, self.cols, self.n_experts
+        for i, k in enumerate(keys):
+            self._c.plane[i] = self.planes[k].data_ptr()
+
+    @property
+    def c(self):
+        return ctypes.byref(self._c)
+
+    def hbm_bytes_per_expert(self):
+        return sum(int(a.numel()) * 4 for a in self.planes.values()) // self.n_experts
+
+
+class _Workspaces:
+    """Zero-filled device workspaces, one per (device, stream, purpose); grown on demand.  The kernels leave their
+    completion counters at zero after every completed call, so a workspace is reused without clearing."""
+
+    def __init__(self):
+        self._ws = {}
+
+    def get(self, purpose, nbytes):
+        dev = torch.cuda.current_device()
+        key = (dev, torch.cuda.current_stream().cuda_stream, purpose)
+        buf = self._ws.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device="cuda")
+            self._ws[key] = buf
+        return buf
+
+
+WORKSPACES = _Workspaces()
+
+
+# ------------------------------------------------------------------------------------------------ kernel-level ops
+def matvec(table, idx, X):
+    """moe_matvec (pallas_moe.py:238-307): out[i, r] = sum_n W_{idx[i]}[r, n] X_i[n].
+    idx int32 [n_slots]; X [n_slots, K] bf16 or f32 (natural input order) -> f32 [n_slots, R]."""
+    idx = idx.to(torch.int32).contiguous()
+    n = int(idx.numel())
+    if X.dim() != 2 or X.shape[0] != n or X.shape[1] != table.cols:
+        raise ValueError("X must be [n_slots, K]")
+    if X.dtype == torch.bfloat16:
+        xd = _lib.MI_X_BF16
+    elif X.dtype == torch.float32:
+        xd = _lib.MI_X_F32
+    else:
+        raise ValueError("X must be bf16 or f32")
+    X = X.contiguous()
+    out = torch.empty((n, table.rows), dtype=torch.float32, device=X.device)
+    nbytes = lib().mi_matvec_workspace(table.c, n)
+    ws = WORKSPACES.get("matvec", nbytes)
+    check("mi_matvec", lib().mi_matvec(table.c, _ptr(idx), n, _ptr(X), xd, X.shape[1], _ptr(out), _ptr(ws),
+                                       ws.numel(), _stream()))
+    return out
+
+
+def dequant(table, expert):
+    """Exact f32 weights [R, K] of one expert (natural input order)."""
+    out = torch.empty((table.rows, table.cols), dtype=torch.float32, device="cuda")
+    check("mi_dequant", lib().mi_dequant(table.c, int(expert), _ptr(out), _stream()))
+    return out
+
+
+def moe_decode(gate, up, down, x, idx, w, limit, shared_expert=-1, want_f32=True, want_bf16=False):
+    """Fused decode MoE (resident.py:110-120 composition), tokens grouped by expert on the device.
+    x bf16 [N, D]; idx int32 [N, k]; w f32 [N, k] -> (out_f32 [N, D] or None, out_bf16 [N, D] or None)."""
+    if x.dtype != torch.bfloat16:
+        raise ValueError("decode activations are bf16")
+    N, k = idx.shape
+    x = x.contiguous()
+    idx = idx.to(torch.int32).contiguous()
+    w = w.to(torch.float32).contiguous()
+    D = down.rows
+    of = torch.empty((N, D), dtype=torch.float32, device=x.device) if want_f32 else None
+    ob = torch.empty((N, D), dtype=torch.bfloat16, device=x.device) if want_bf16 else None
+    nbytes = lib().mi_moe_decode_workspace(gate.c, down.c, N, k, int(shared_expert))
+    if nbytes == 0:
+        raise ValueError("mi_moe_decode: invalid tables or token counts (N=%d, k=%d)" % (N, k))
+    ws = WORKSPACES.get("decode", nbytes)
+    check("mi_moe_decode", lib().mi_moe_decode(gate.c, up.c, down.c, _ptr(x), N, k, _ptr(idx), _ptr(w),
+                                               int(shared_expert), float(limit), _ptr(of), _ptr(ob), _ptr(ws),
+                                               ws.numel(), _stream()))
+    return of, ob
+
+
+def int8_project(x, qT, s, want_f32=False):
+    """y = x @ bf16(f32(q) * s) (quant8.py:91-99): x bf16 [B, n_in], qT int8 [n_out, n_in], s f32 [n_out]."""
+    B, n_in = x.shape
+    n_out = qT.shape[0]
+    x = x.contiguous()
+    yb = torch.empty((B, n_out), dtype=torch.bfloat16, device=x.device)
+    yf = torch.empty((B, n_out), dtype=torch.float32, device=x.device) if want_f32 else None
+    nbytes = lib().mi_int8_project_workspace(B, n_in, n_out)
+    ws = WORKSPACES.get("int8", nbytes)
+    check("mi_int8_project", lib().mi_int8_project(_ptr(x), B, _ptr(qT), _ptr(s), n_in, n_out, _ptr(yb), _ptr(yf),
+                                                   _ptr(ws), ws.numel(), _stream()))
+    return (yb, yf) if want_f32 else yb
+
+
+# ------------------------------------------------------------------------------------------------ the operator
+class ResidentFetch:
+    """Drop-in for glm53.resident.ResidentFetch (resident.py:68-108): same constructor, ``qtypes`` and ``apply``.
+
+    apply(p, x, idx, w, layer, limit): x [N, D]; idx [N, k] int32 into E; w [N, k] f32 -> f32 [N, D] (routed experts
+    only; the caller adds the shared expert, model.py:847-855).  N*k <= gather_max_rows takes the fused decode
+    kernels (f32 end to end, resident.py:110-120); larger calls take the grouped prefill path (resident.py:144-165).
+    ``use_pallas`` / ``interpret`` / ``sweep_mode`` / ``chunk`` are accepted for signature compatibility; there is a
+    single MI355X kernel path per regime."""
+
+    def __init__(self, qtypes, D, ml, out_dtype=torch.bfloat16, gather_max_rows=64, chunk=8, use_pallas=True,
+                 interpret=False, sweep_mode="ragged", tm=32, combine="matmul"):
+        self.qtypes = qtypes
+        self.rows = {"gate_q": ml, "up_q": ml, "down_q": D}
+        self.cols = {"gate_q": D, "up_q": D, "down_q": ml}
+        self.nblk = {"gate_q": D // QK, "up_q": D // QK, "down_q": ml // QK}
+        self.out_dtype = out_dtype
+        self.gather_max_rows = gather_max_rows
+        self.chunk = chunk
+        self.use_pallas = use_pallas
+        self.interpret = interpret
+        self.sweep_mode = sweep_mode
+        self.tm = tm
+        self.combine = combine
+        self._tables = {}
+
+    def tables(self, p, layer):
+        """ExpertTable views of p's planes (cached per layer and storage)."""
+        key = (layer,) + tuple(p[k]["qs"].data_ptr() for k in ("gate_q", "up_q", "down_q"))
+        t = self._tables.get(key)
+        if t is None:
+            t = tuple(ExpertTable(self.qtypes[layer][k], p[k], self.rows[k], self.cols[k])
+                      for k in ("gate_q", "up_q", "down_q"))
+            self._tables = {key: t}
+        return t
+
+    def apply(self, p, x, idx, w, layer, limit):
+        gate, up, down = self.tables(p, layer)
+        N, k = idx.shape
+        if N * k <= self.gather_max_rows:
+            xb = x if x.dtype == torch.bfloat16 else x.to(torch.bfloat16)
+            if x.dtype != torch.bfloat16 and not torch.equal(xb.to(x.dtype), x):
+                raise ValueError("decode activations must be bf16-representable (the layer dtype)")
+            out, _ = moe_decode(gate, up, down, xb, idx, w, limit)
+            return out
+        from . import prefill
+        return prefill.moe_prefill(gate, up, down, x, idx, w, limit, tm=self.tm, combine=self.combine)

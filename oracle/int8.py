@@ -1,0 +1,40 @@
+"""int8 per-channel projection oracle (test infrastructure only).
+
+Reference: a quantized leaf is {"q": int8 [in, out], "s": f32 [1, out]} (quant8.py:17-18,26-32); every layer program
+replaces it by W = bf16(f32(q) * s) (quant8.py:91-99) and the projection is x @ W with f32 accumulation, bf16 out.
+"""
+import numpy as np
+
+from .bf16 import round_bf16
+
+
+def quantize_array(w, axis):
+    """w [in, out] -> (q int8, s f32); axis 0 = per-row scales [in,1], 1 = per-column [1,out] (quant8.py:26-32)."""
+    w32 = np.asarray(w, dtype=np.float32)
+    amax = np.max(np.abs(w32), axis=1 - axis, keepdims=True)
+    s = (np.maximum(amax, np.float32(1e-12)) / np.float32(127.0)).astype(np.float32)
+    q = np.clip(np.round(w32 / s), -127, 127).astype(np.int8)
+    return q, s
+
+
+def generate(rng, n_in, n_out):
+    """Benchmark inputs: q uniform in [-127, 127], s ~ U(0.5e-3, 2e-3) per output channel."""
+    q = rng.integers(-127, 128, (n_in, n_out), dtype=np.int8)
+    s = rng.uniform(0.5e-3, 2e-3, (1, n_out)).astype(np.float32)
+    return q, s
+
+
+def dequant_bf16(q, s):
+    """bf16(f32(q) * s) as f32 values (quant8.py:94)."""
+    return round_bf16(np.asarray(q, dtype=np.float32) * np.asarray(s, dtype=np.float32))
+
+
+def project_f32(x, q, s):
+    """x [B, in] (bf16 values) @ bf16(q*s) with f64 accumulation -> f32 [B, out] (before the bf16 output rounding)."""
+    W = dequant_bf16(q, s).astype(np.float64)
+    return (np.asarray(x, dtype=np.float64) @ W).astype(np.float32)
+
+
+def project_bf16(x, q, s):
+    """The projection's bf16 output, as f32 values."""
+    return round_bf16(project_f32(x, q, s))
