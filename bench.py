@@ -1,0 +1,300 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused 3-bit codebook MoE decode layer on one MI355X.
+
+Headline workload (one "step" = one MoE layer over one decode batch, inputs resident in HBM):
+  D = 6144, 64 routed experts (top-8) + 1 shared expert, SwiGLU intermediate 2048, gate/up/down all CB3 3-bit
+  codebook (10 codes per u32, 8 bf16 centroids per (row, 128-column group)), batch 1, router logits ~ N(0,1),
+  softmax top-8 renormalized, x bf16 ~ N(0,1).  Synthetic random weights generated on the GPU.
+metric: effective weight GB/s = stored bytes of every distinct expert read in the step / step time
+        (as % of the 8 TB/s HBM peak), plus microseconds per MoE layer at batch 1 / 8 / 16.
+
+Cache: the layer's weights are rotated over several independent copies (> 256 MB Infinity Cache) and the routing
+changes every step, so each step streams cold weights.  Steps are captured as HIP graphs (one per copy) and replayed;
+the timed region is bracketed by device synchronizations and HIP events on the launch stream.
+
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20]
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+HBM_PEAK_GBS = 8000.0
+D, E_ROUTED, TOPK, INTER = 6144, 64, 8, 2048
+SHARED = E_ROUTED                      # expert index of the shared expert (appended to every table)
+LIMIT = 10.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--copies", type=int, default=6, help="independent layer copies rotated between steps")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only-b1", action="store_true", help="headline only (profiling runs)")
+    return ap.parse_args()
+
+
+# ------------------------------------------------------------------------------------------------ synthetic weights
+def cb3_bytes(R, K):
+    return R * (4 * math.ceil(K / 10) + 16 * (K // 128))
+
+
+def random_cb3_planes(torch, gen, E, R, K):
+    """Device planes of E random CB3 experts (uniform codes, sorted N(0, 0.02) bf16 centroids) in the kernel layout:
+    qs int32 [E*Wd, R], cb int32 [E*G*4, R]."""
+    Wd, G = math.ceil(K / 10), K // 128
+    qs = torch.randint(-2 ** 31, 2 ** 31 - 1, (E, Wd, R), dtype=torch.int32, device="cuda", generator=gen)
+    odd = torch.zeros(Wd, dtype=torch.bool, device="cuda")
+    odd[1::2] = True
+    if Wd % 2:
+        odd[-1] = False
+    qs[:, odd, :] &= 0x7F7F7F7F                                   # second word of a pair: bit 7 of every byte unused
+    qs = qs.reshape(E * Wd, R)
+    cbs = []
+    for e in range(E):
+        c = torch.randn((R, G, 8), device="cuda", generator=gen) * 0.02
+        c = torch.sort(c, dim=-1).values.to(torch.bfloat16).view(torch.int16).to(torch.int32) & 0xFFFF
+        lo, hi = c & 0xFF, c >> 8
+        sh = torch.tensor([0, 8, 16, 24], device="cuda", dtype=torch.int32)
+        pack = lambda a: (a << sh).sum(-1).to(torch.int32)
+        w = torch.stack([pack(lo[..., 0:4]), pack(lo[..., 4:8]), pack(hi[..., 0:4]), pack(hi[..., 4:8])], -1)
+        cbs.append(w.permute(1, 2, 0).reshape(G * 4, R))           # [G, 4, R]
+    return {"qs": qs, "cb": torch.cat(cbs, 0).contiguous()}
+
+
+def softmax_topk(rng, N, E, k):
+    logits = rng.standard_normal((N, E))
+    p = np.exp(logits - logits.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    idx = np.argsort(-p, axis=-1)[:, :k].astype(np.int32)
+    w = np.take_along_axis(p, idx, -1)
+    return idx, (w / w.sum(-1, keepdims=True)).astype(np.float32)
+
+
+def zipf_topk(rng, N, E, k, s=1.1):
+    logp = -s * np.log(np.arange(1, E + 1, dtype=np.float64))
+    perm = rng.permutation(E)
+    idx = np.zeros((N, k), np.int32)
+    for n in range(N):
+        idx[n] = perm[np.argsort(-(logp + rng.gumbel(size=E)))[:k]]
+    logits = rng.standard_normal((N, k))
+    w = np.exp(logits - logits.max(-1, keepdims=True))
+    return idx, (w / w.sum(-1, keepdims=True)).astype(np.float32)
+
+
+# ------------------------------------------------------------------------------------------------ timing
+class Timer:
+    """Runs a list of per-step callables (one captured HIP graph each) and times exactly `steps` of them."""
+
+    def __init__(self, torch, fns):
+        self.torch = torch
+        self.graphs = []
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for f in fns:
+                f()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        for f in fns:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                f()
+            self.graphs.append(g)
+        torch.cuda.synchronize()
+
+    def run(self, steps, warmup):
+        torch = self.torch
+        n = len(self.graphs)
+        for i in range(warmup):
+            self.graphs[i % n].replay()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for i in range(steps):
+            self.graphs[i % n].replay()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / steps            # ms per step
+
+
+# ------------------------------------------------------------------------------------------------ CPU baseline
+def cpu_baseline():
+    """The oracle's NumPy restatement of the reference's plain-jnp decode path (gather -> f32 dequant -> matvec,
+    resident.py:122-135 / pallas_moe.py:310-323) on one batch-1 layer of the same workload, one thread."""
+    from threadpoolctl import threadpool_limits
+    from oracle import cb3 as ocb3, moe as omoe
+    rng = np.random.default_rng(1)
+    experts = 9
+    mats = {}
+    for e in range(experts):
+        for name, (R, K) in (("gate", (INTER, D)), ("up", (INTER, D)), ("down", (D, INTER))):
+            mats[(name, e)] = ocb3.generate(rng, R, K)
+    x = ocb3.bf16_normal(rng, (1, D))
+    idx = np.arange(8, dtype=np.int32)[None]
+    w = np.full((1, 8), 1.0 / 8, np.float32)
+    deq = lambda name, e: ocb3.dequant(*mats[(name, e)])
+    with threadpool_limits(1):
+        t0 = time.perf_counter()
+        y = omoe.decode_apply(deq, x, idx, w, LIMIT) + omoe.shared_apply(lambda m: deq(m, 8), x, LIMIT)
+        dt = time.perf_counter() - t0
+    assert np.isfinite(y).all()
+    nbytes = experts * (2 * cb3_bytes(INTER, D) + cb3_bytes(D, INTER))
+    return {"value": round(nbytes / dt / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": "one batch-1 MoE layer (8 routed + 1 shared CB3 experts, D=6144, I=2048): NumPy dequant + "
+                      "f64 matvec, %.2f s on 1 thread" % dt,
+            "seconds": round(dt, 3)}
+
+
+# ------------------------------------------------------------------------------------------------ main
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: the decode path runs on a single MI355X holding one layer's full expert "
+              "set (multi-GPU expert parallelism is a design note, not part of this build); run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import __graft_entry__ as ge
+    pkg = ge.load_package()
+    pkg._lib.lib()
+    torch.manual_seed(0)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(1234)
+    E = E_ROUTED + 1
+    L = args.copies
+    per_expert = 2 * cb3_bytes(INTER, D) + cb3_bytes(D, INTER)
+
+    layers = []
+    for c in range(L):
+        tabs = {}
+        for name, (R, K) in (("gate", (INTER, D)), ("up", (INTER, D)), ("down", (D, INTER))):
+            tabs[name] = pkg.ExpertTable("CB3", random_cb3_planes(torch, gen, E, R, K), R, K)
+        layers.append(tabs)
+    torch.cuda.synchronize()
+
+    rng = np.random.default_rng(2026)
+    extra = {}
+
+    def layer_fns(N, routing, phases=3):
+        """Per-copy step callables for batch N (fixed routing per copy, fresh per copy)."""
+        fns, nbytes = [], []
+        ws = torch.zeros(pkg.resident.decode_workspace_bytes(layers[0]["gate"], layers[0]["down"], N, TOPK, SHARED),
+                         dtype=torch.uint8, device="cuda")
+        out = torch.empty((N, D), dtype=torch.bfloat16, device="cuda")
+        for c in range(L):
+            idx, w = routing(rng, N, E_ROUTED, TOPK)
+            x = torch.randn((N, D), device="cuda", generator=gen).to(torch.bfloat16)
+            it, wt = torch.from_numpy(idx).cuda(), torch.from_numpy(w).cuda()
+            t = layers[c]
+            f = (lambda t=t, x=x, it=it, wt=wt: pkg.moe_decode(t["gate"], t["up"], t["down"], x, it, wt, LIMIT,
+                                                              shared_expert=SHARED, want_f32=False, out_bf16=out,
+                                                              workspace=ws, phases=phases))
+            fns.append(f)
+            n_exp = len(np.unique(idx)) + 1
+            nbytes.append(n_exp * (per_expert if phases == 3 else 2 * cb3_bytes(INTER, D)))
+        return fns, nbytes
+
+    def measure(N, routing, phases=3, steps=args.steps):
+        fns, nbytes = layer_fns(N, routing, phases)
+        ms = Timer(torch, fns).run(steps, args.warmup)
+        avg_bytes = float(np.mean([nbytes[i % L] for i in range(steps)]))
+        return ms, avg_bytes
+
+    # headline: batch 1 layer
+    ms1, bytes1 = measure(1, softmax_topk)
+    gbs1 = bytes1 / (ms1 * 1e-3) / 1e9
+    # dominant kernel alone (gate + up + SwiGLU launch)
+    msg, bytesg = measure(1, softmax_topk, phases=1)
+    gbsg = bytesg / (msg * 1e-3) / 1e9
+    extra["b1"] = {"us_per_layer": round(ms1 * 1e3, 2), "GBps": round(gbs1, 1), "pct_hbm": round(100 * gbs1 / HBM_PEAK_GBS, 1),
+                   "bytes_per_layer": int(bytes1)}
+    extra["b1_gateup_kernel"] = {"us": round(msg * 1e3, 2), "GBps": round(gbsg, 1), "bytes": int(bytesg)}
+    if not args.only_b1:
+        for N in (8, 16):
+            ms, b = measure(N, zipf_topk)
+            gbs = b / (ms * 1e-3) / 1e9
+            extra["b%d" % N] = {"us_per_layer": round(ms * 1e3, 2), "GBps": round(gbs, 1),
+                                "pct_hbm": round(100 * gbs / HBM_PEAK_GBS, 1), "bytes_per_layer": int(b)}
+        extra["int8_b8"] = bench_int8(torch, pkg, gen, args)
+        extra["cfg0_matvec"] = bench_matvec(torch, pkg, gen, args)
+
+    cpu = None if args.no_cpu else cpu_baseline()
+    res = {
+        "metric": "effective weight GB/s (% of HBM peak) + µs/MoE layer at batch 1/8/16",
+        "value": round(gbs1, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms1, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (random CB3 codes/centroids generated on the GPU; N(0,1) router logits and bf16 activations)",
+        "config": {"workload": "moe_decode_layer_b1_cb3", "hidden": D, "routed_experts": E_ROUTED, "topk": TOPK,
+                   "shared_experts": 1, "moe_intermediate": INTER, "batch": 1, "format": "CB3",
+                   "layer_copies": L, "parallelism": "single-gpu"},
+        "roofline": {"bound": "hbm", "achieved": round(gbsg, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbsg / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "grouped_kernel<gate/up, CB3> (gate + up partials)",
+                     "bytes_per_launch": int(bytesg), "us_per_launch": round(msg * 1e3, 2)},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(res))
+
+
+def bench_int8(torch, pkg, gen, args):
+    """Config: the int8 dense projections at batch 8 (Q, K, V, O 6144x6144; shared gate/up 6144->2048; shared down
+    2048->6144), per-output-channel scales, bf16 activations.  3 weight copies rotated (> Infinity Cache)."""
+    shapes = [(6144, 6144)] * 4 + [(6144, 2048)] * 2 + [(2048, 6144)]
+    B = 8
+    copies = 3
+    fns = []
+    total = sum(i * o + 4 * o for i, o in shapes)
+    for c in range(copies):
+        ops = []
+        for (n_in, n_out) in shapes:
+            qT = torch.randint(-127, 128, (n_out, n_in), dtype=torch.int8, device="cuda", generator=gen)
+            s = torch.rand((n_out,), device="cuda", generator=gen) * 1.5e-3 + 0.5e-3
+            x = torch.randn((B, n_in), device="cuda", generator=gen).to(torch.bfloat16)
+            y = torch.empty((B, n_out), dtype=torch.bfloat16, device="cuda")
+            ws = torch.zeros(pkg._lib.lib().mi_int8_project_workspace(B, n_in, n_out), dtype=torch.uint8,
+                             device="cuda")
+            ops.append((x, qT, s, y, ws))
+        fns.append(lambda ops=ops: [pkg.int8_project(x, qT, s, y_bf16=y, workspace=ws) for (x, qT, s, y, ws) in ops])
+    ms = Timer(torch, fns).run(args.steps, args.warmup)
+    gbs = total / (ms * 1e-3) / 1e9
+    return {"us_per_7_projections": round(ms * 1e3, 2), "GBps": round(gbs, 1), "pct_hbm": round(100 * gbs / HBM_PEAK_GBS, 1),
+            "bytes": int(total)}
+
+
+def bench_matvec(torch, pkg, gen, args):
+    """Config: one CB3 matvec, W 1024 x 2048, x bf16 [1, 2048] (launch-bound correctness config)."""
+    R, K = 1024, 2048
+    fns = []
+    for c in range(4):
+        tb = pkg.ExpertTable("CB3", random_cb3_planes(torch, gen, 1, R, K), R, K)
+        x = torch.randn((1, K), device="cuda", generator=gen).to(torch.bfloat16)
+        idx = torch.zeros((1,), dtype=torch.int32, device="cuda")
+        out = torch.empty((1, R), dtype=torch.float32, device="cuda")
+        ws = torch.zeros(pkg._lib.lib().mi_matvec_workspace(tb.c, 1), dtype=torch.uint8, device="cuda")
+        fns.append(lambda tb=tb, x=x, idx=idx, out=out, ws=ws: pkg.resident.matvec_into(tb, idx, x, out, ws))
+    ms = Timer(torch, fns).run(args.steps, args.warmup)
+    nbytes = cb3_bytes(R, K)
+    return {"us": round(ms * 1e3, 2), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1), "bytes": nbytes}
+
+
+if __name__ == "__main__":
+    main()

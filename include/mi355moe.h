@@ -93,6 +93,16 @@ size_t mi_moe_decode_workspace(const mi_table *gate, const mi_table *down, int32
                                int32_t shared_expert);
 
 /*
+ * mi_moe_decode split in its two launches (the reference runs them as separate kernels too, resident.py:116-119):
+ * phases = 1: gate + up + SwiGLU only (h stays in the workspace); 2: down + combine only (consumes the h a previous
+ * phase-1 call left in the same workspace, same arguments); 3: both (= mi_moe_decode).
+ */
+int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_table *down, const uint16_t *x_bf16,
+                         int32_t N, int32_t k, const int32_t *idx, const float *w, int32_t shared_expert,
+                         float limit, float *out_f32, uint16_t *out_bf16, void *workspace, size_t workspace_bytes,
+                         int32_t phases, void *stream);
+
+/*
  * Exact dequantized weights of expert e (natural input order): out f32 [R, K].  Restates dequant_planes
  * (planes.py:196-206) / the codebook closed form; used to check the kernels' decode bit for bit.
  */

@@ -2,40 +2,67 @@
 
     python kaggle-llm-endpoint_amd/build.py
 
-The library is a plain C-ABI shared object (include/mi355moe.h) that the package loads with ctypes.
+The library is a plain C-ABI shared object (include/mi355moe.h) that the package loads with ctypes.  The grouped
+kernels are compiled once per (mode, format) from k_grouped.hip; all units compile in parallel, then link.
 """
 import os
+import shutil
 import subprocess
 import sys
+import tempfile
+from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
+INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 LIB = os.path.join(HERE, "libmi355moe.so")
-SOURCES = ["moe_decode.hip", "int8_project.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
-    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
     # no packed-f32 VALU forms anywhere (they are disabled for this target's kernels)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-result",
 ]
 
+# (source, extra defines, object name)
+UNITS = [("moe_decode.hip", [], "moe_decode"), ("int8_project.hip", [], "int8_project")]
+UNITS += [("k_grouped.hip", ["-DMI_KMODE=%d" % m, "-DMI_KQT=%d" % q], "k_grouped_%d_%d" % (m, q))
+          for m in (0, 1, 2) for q in (1, 2)]
 
-def build(verbose=False):
-    srcs = [os.path.join(CSRC, s) for s in SOURCES if os.path.exists(os.path.join(CSRC, s))]
-    tmp = LIB + ".tmp"
-    cmd = [HIPCC] + FLAGS + ["-I", os.path.join(os.path.dirname(HERE), "include")] + srcs + ["-o", tmp]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
+
+def _filter(stderr):
     # hipcc's host pass warns that it does not know the packed-f32 feature: expected, filtered
-    err = "\n".join(l for l in res.stderr.splitlines() if "packed-fp32-ops" not in l)
-    if res.returncode != 0:
-        raise RuntimeError("hipcc failed (%d):\n%s" % (res.returncode, err))
-    if verbose and err.strip():
-        print(err, file=sys.stderr)
-    os.replace(tmp, LIB)
+    return "\n".join(l for l in stderr.splitlines() if "packed-fp32-ops" not in l)
+
+
+def build(verbose=False, jobs=None):
+    tmpdir = tempfile.mkdtemp(prefix="mi355moe_build_")
+    try:
+        def compile_unit(u):
+            src, defs, name = u
+            obj = os.path.join(tmpdir, name + ".o")
+            cmd = [HIPCC] + FLAGS + defs + ["-I", INCLUDE, "-c", os.path.join(CSRC, src), "-o", obj]
+            res = subprocess.run(cmd, capture_output=True, text=True)
+            return name, obj, res.returncode, _filter(res.stderr), cmd
+        jobs = jobs or min(len(UNITS), max(1, os.cpu_count() or 1))
+        with ThreadPoolExecutor(jobs) as ex:
+            results = list(ex.map(compile_unit, UNITS))
+        for name, obj, rc, err, cmd in results:
+            if verbose:
+                print(" ".join(cmd), flush=True)
+            if rc != 0:
+                raise RuntimeError("hipcc failed on %s (%d):\n%s" % (name, rc, err))
+            if verbose and err.strip():
+                print(err, file=sys.stderr)
+        tmp = LIB + ".tmp"
+        cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC"] + [r[1] for r in results] + ["-o", tmp]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError("link failed (%d):\n%s" % (res.returncode, _filter(res.stderr)))
+        os.replace(tmp, LIB)
+    finally:
+        shutil.rmtree(tmpdir, ignore_errors=True)
     return LIB
 
 

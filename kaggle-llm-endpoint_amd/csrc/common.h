@@ -4,7 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "../../include/mi355moe.h"
+#include "mi355moe.h"
 
 namespace mi {
 
@@ -56,18 +56,23 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
     return (float)__builtin_bit_cast(_Float16, (unsigned short)(h & 0xffffu));
 }
 
-// Agent-scope completion counter: returns the value before the increment.  Callers fence their stores first.
+// Completion counters.  On this multi-XCD part an agent-scope release writes back the XCD's L2 and an acquire
+// invalidates it, so they are issued as rarely as possible: after a workgroup barrier (which completes every wave's
+// stores to L2) ONE thread issues the release fence and the relaxed increment; only the workgroup that observes the
+// final count issues the acquire before reading the other workgroups' partials.
 __device__ __forceinline__ uint32_t counter_add(uint32_t *c, uint32_t v) {
-    return __hip_atomic_fetch_add(c, v, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    return __hip_atomic_fetch_add(c, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ void fence_release_agent() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); }
+__device__ __forceinline__ void fence_acquire_agent() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
 __device__ __forceinline__ void counter_reset(uint32_t *c) {
     __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ------------------------------------------------------------------------------------------------ expert grouping
 // The (slot -> expert) routing of one call, grouped on the device: every distinct expert (ascending id) gets
-// ceil(count / kMaxT) groups of at most kMaxT slots (ascending slot order); the shared expert, if any, gets
-// ceil(N / kMaxT) more groups whose slots are n_route + n.  Every workgroup recomputes it from idx (n_route <= 128
+// ceil(count / cap) groups of at most cap slots (ascending slot order; cap <= kMaxT is the launch's token class);
+// the shared expert, if any, gets ceil(N / cap) more groups whose slots are n_route + n.  Every workgroup recomputes it from idx (n_route <= 128
 // entries), so no host sync and no extra launch is needed.
 struct Group {
     int expert;   // -1: this workgroup has no group (grid padding)
@@ -84,7 +89,7 @@ struct GroupScratch {
 
 // Must be called by all threads of the block (blockDim.x >= 64).  Result in sc.g (after the final barrier).
 __device__ inline void find_group(GroupScratch &sc, const int32_t *__restrict__ idx, int n_route, int E,
-                                  int shared_expert, int N, int gi) {
+                                  int shared_expert, int N, int gi, int cap) {
     const int tid = threadIdx.x;
     for (int e = tid; e < E; e += blockDim.x) sc.count[e] = 0;
     __syncthreads();
@@ -99,7 +104,7 @@ __device__ inline void find_group(GroupScratch &sc, const int32_t *__restrict__ 
         const int per = (E + kWave - 1) / kWave;
         int e0 = tid * per, e1 = min(E, e0 + per);
         int ng = 0;
-        for (int e = e0; e < e1; ++e) ng += (sc.count[e] + kMaxT - 1) / kMaxT;
+        for (int e = e0; e < e1; ++e) ng += (sc.count[e] + cap - 1) / cap;
         // inclusive scan over the wavefront
         int incl = ng;
         for (int off = 1; off < kWave; off <<= 1) {
@@ -117,10 +122,10 @@ __device__ inline void find_group(GroupScratch &sc, const int32_t *__restrict__ 
             int r = gi - excl;
             for (int e = e0; e < e1; ++e) {
                 int c = (int)sc.count[e];
-                int ge = (c + kMaxT - 1) / kMaxT;
+                int ge = (c + cap - 1) / cap;
                 if (r < ge) {
                     sc.g.expert = e;
-                    sc.g.n = min(kMaxT, c - r * kMaxT);
+                    sc.g.n = min(cap, c - r * cap);
                     sc.lane_base[kWave] = r;      // chunk index within the expert
                     break;
                 }
@@ -129,10 +134,10 @@ __device__ inline void find_group(GroupScratch &sc, const int32_t *__restrict__ 
         }
         if (tid == 0 && gi >= total && shared_expert >= 0) {
             int r = gi - total;
-            int ns = (N + kMaxT - 1) / kMaxT;
+            int ns = (N + cap - 1) / cap;
             if (r < ns) {
                 sc.g.expert = shared_expert;
-                sc.g.n = min(kMaxT, N - r * kMaxT);
+                sc.g.n = min(cap, N - r * cap);
                 sc.lane_base[kWave] = -1 - r;     // marks a shared group
             }
         }
@@ -143,17 +148,17 @@ __device__ inline void find_group(GroupScratch &sc, const int32_t *__restrict__ 
         const int chunk = sc.lane_base[kWave];
         if (chunk < 0) {
             int r = -1 - chunk;
-            if (tid < sc.g.n) sc.g.slot[tid] = n_route + r * kMaxT + tid;
+            if (tid < sc.g.n) sc.g.slot[tid] = n_route + r * cap + tid;
         } else {
-            // compact the slots routed to e (ascending), keep positions [chunk*kMaxT, chunk*kMaxT + n)
+            // compact the slots routed to e (ascending), keep positions [chunk*cap, chunk*cap + n)
             int base = 0;
             for (int i0 = 0; i0 < n_route; i0 += kWave) {
                 int i = i0 + tid;
                 bool hit = (i < n_route) && (sc.idx[i] == e);
                 uint64_t m = __ballot(hit);
                 int pos = base + __popcll(m & ((1ull << tid) - 1ull));
-                int p = pos - chunk * kMaxT;
-                if (hit && p >= 0 && p < kMaxT) sc.g.slot[p] = i;
+                int p = pos - chunk * cap;
+                if (hit && p >= 0 && p < cap) sc.g.slot[p] = i;
                 base += __popcll(m);
             }
         }
@@ -162,11 +167,11 @@ __device__ inline void find_group(GroupScratch &sc, const int32_t *__restrict__ 
 }
 
 // Number of groups of one call is at most this (grid size of the grouped kernels).
-__host__ __device__ inline int max_groups(int n_route, int E, int N, int shared_expert) {
+__host__ __device__ inline int max_groups(int n_route, int E, int N, int shared_expert, int cap) {
     int routed = n_route < E ? n_route : E;
-    routed += n_route / kMaxT;                       // extra chunks of experts with more than kMaxT slots
+    routed += n_route / cap;                         // extra chunks of experts with more than cap slots
     if (routed > n_route) routed = n_route;
-    int shared = shared_expert >= 0 ? (N + kMaxT - 1) / kMaxT : 0;
+    int shared = shared_expert >= 0 ? (N + cap - 1) / cap : 0;
     return routed + shared;
 }
 

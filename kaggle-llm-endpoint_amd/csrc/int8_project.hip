@@ -97,12 +97,14 @@ __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
         for (int wv = 0; wv < kI8Waves; ++wv) v += red[wv][c][b];
         a.part[((size_t)ks * a.n_out + o0 + c) * 32 + b] = v;
     }
-    __threadfence();
     __syncthreads();
-    if (tid == 0) s_last = counter_add(a.cnt + tile, 1u) == (uint32_t)(a.KS - 1);
+    if (tid == 0) {
+        fence_release_agent();
+        s_last = counter_add(a.cnt + tile, 1u) == (uint32_t)(a.KS - 1);
+    }
     __syncthreads();
     if (!s_last) return;
-    __threadfence();
+    fence_acquire_agent();
     for (int i = tid; i < 16 * ntok; i += blockDim.x) {
         const int c = i / ntok, b = i - c * ntok;
         if (b >= a.B) continue;

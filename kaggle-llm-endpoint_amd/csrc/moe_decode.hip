@@ -1,254 +1,11 @@
-// Grouped codebook-dequant expert matvec kernels for gfx950 (MI355X) and their C ABI.
-//
-// One launch covers every (expert group, 256-row block, column split) task of a call.  A workgroup
-//   1. regroups the call's routing on the device (find_group: slots sorted by expert, <= 16 slots per group),
-//   2. stages the group's activation rows for its column split in LDS,
-//   3. streams the expert's planes once -- each lane owns 4 consecutive rows, so every plane access is one
-//      128-bit load and the wavefront reads 1 KB contiguous -- decoding codes to bf16 in registers and
-//      accumulating bf16-pair dot products in f32 for all the group's rows at once,
-//   4. writes its f32 partial sums and bumps an agent-scope completion counter; the workgroup that completes a
-//      (group, row block) -- or, for the down projection, a (row block, token) -- reduces the partials in a fixed
-//      order and runs the epilogue: SwiGLU (gate/up), the routing-weighted combine (down), or a plain store.
-// Results are therefore deterministic: no float atomics, every sum in a fixed order.
-#include "formats.h"
+// Grouped codebook-dequant expert matvec: host side of the C ABI (argument validation, split planning, workspace
+// layout, launches) and the exact dequant kernel.  The grouped kernels themselves live in grouped.h.
+#include "grouped.h"
 
 #include <stdio.h>
 #include <stdlib.h>
 
 namespace mi {
-
-__constant__ uint32_t kGridConst[512] = {
-#include "iq3s_grid.inc"
-};
-
-enum Mode { kGateUp = 0, kDown = 1, kMatvec = 2 };
-
-struct Table {
-    int qtype;
-    Cb3Table cb3;
-    Iq3Table iq3;
-};
-
-struct KArgs {
-    Table t0, t1;              // gate/up (kGateUp) or the single table
-    int R, K;                  // rows, cols of the table(s)
-    int E;
-    int n_route;               // routed slots (N*k, or n_slots for kMatvec)
-    int N, k;
-    int shared_expert;
-    int S;                     // column splits
-    int n_units;               // column units (CB3: word pairs, IQ3_S: blocks)
-    int RB;                    // row blocks (R / 256)
-    int xs_max;                // LDS dwords per staged row
-    int t_rows;                // LDS rows staged (class of the largest group)
-    // activations
-    const uint16_t *x_bf16;    // kGateUp: [N, K] tokens; kMatvec bf16: [n_slots, stride]
-    const float *x_f32;        // kDown: h [NS, K] by slot; kMatvec f32: [n_slots, stride]
-    int x_stride;
-    const int32_t *idx;
-    const float *w;
-    float limit;
-    // outputs / workspace
-    float *part;               // [S * nmat * NS * R] partial sums
-    uint32_t *cnt;             // completion counters
-    float *h;                  // kGateUp epilogue output [NS, R]
-    float *out_f32;            // kDown: [N, R]; kMatvec: [n_slots, R]
-    uint16_t *out_bf16;        // kDown: [N, R] (optional)
-    int NS;                    // slots incl. shared
-};
-
-__host__ __device__ inline int slot_token(int slot, int n_route, int k) {
-    return slot < n_route ? slot / k : slot - n_route;
-}
-
-template <int QT, int TC, bool HILO>
-__device__ __forceinline__ void accum_rows(const Table &tb, int e, int r0, int u0, int u1, int c0,
-                                           const uint32_t *grid, const uint32_t *xh, const uint32_t *xl, int xs,
-                                           float (&acc)[4][TC]) {
-    if constexpr (QT == MI_QT_CB3) cb3_accum<TC, HILO>(tb.cb3, e, r0, u0, u1, c0, xh, xl, xs, acc);
-    else iq3_accum<TC, HILO>(tb.iq3, e, r0, u0, u1, c0, grid, xh, xl, xs, acc);
-}
-
-// Accumulate with the smallest token class >= n and store the partials of the n real rows.
-template <int QT, bool HILO>
-__device__ void run_and_store(const Table &tb, int e, int r0, int u0, int u1, int c0, const uint32_t *grid,
-                              const uint32_t *xh, const uint32_t *xl, int xs, int n, const int *slots,
-                              float *part_base, int R) {
-#define MI_RUN_CLASS(TCV)                                                                          \
-    {                                                                                              \
-        float acc[4][TCV];                                                                         \
-        _Pragma("unroll") for (int i = 0; i < 4; ++i) _Pragma("unroll") for (int t = 0; t < TCV; ++t) acc[i][t] = 0.f; \
-        accum_rows<QT, TCV, HILO>(tb, e, r0, u0, u1, c0, grid, xh, xl, xs, acc);                   \
-        _Pragma("unroll") for (int t = 0; t < TCV; ++t) {                                          \
-            if (t < n) {                                                                           \
-                float4 v = make_float4(acc[0][t], acc[1][t], acc[2][t], acc[3][t]);                \
-                *(float4 *)(part_base + (size_t)slots[t] * R + r0) = v;                            \
-            }                                                                                      \
-        }                                                                                          \
-    }
-    if (n <= 1) MI_RUN_CLASS(1)
-    else if (n <= 2) MI_RUN_CLASS(2)
-    else if (n <= 4) MI_RUN_CLASS(4)
-    else if (n <= 8) MI_RUN_CLASS(8)
-    else MI_RUN_CLASS(16)
-#undef MI_RUN_CLASS
-}
-
-template <int MODE, int QT>
-__global__ void __launch_bounds__(MODE == kGateUp ? 128 : 64) grouped_kernel(KArgs a) {
-    extern __shared__ uint32_t xlds[];
-    __shared__ GroupScratch sc;
-    __shared__ uint32_t grid[512];
-    __shared__ int s_last;
-    __shared__ int s_tok[kMaxT];
-
-    const int tid = threadIdx.x;
-    const int task = blockIdx.x;
-    const int split = task % a.S;
-    const int rb = (task / a.S) % a.RB;
-    const int gi = task / (a.S * a.RB);
-
-    find_group(sc, a.idx, a.n_route, a.E, a.shared_expert, a.N, gi);
-    const int e = sc.g.expert;
-    if (e < 0) return;
-    const int n = sc.g.n;
-
-    constexpr bool iq3 = QT == MI_QT_IQ3_S;
-    if (iq3)
-        for (int i = tid; i < 512; i += blockDim.x) grid[i] = kGridConst[i];
-
-    // column range of the split
-    const int ucols = iq3 ? Iq3Table::kUnitCols : Cb3Table::kUnitCols;
-    const int u0 = (int)((long long)split * a.n_units / a.S);
-    const int u1 = (int)((long long)(split + 1) * a.n_units / a.S);
-    const int c0 = u0 * ucols;
-    const int c1 = min(a.K, u1 * ucols);
-    const int xs = (c1 - c0) >> 1;   // dwords per staged row
-    const bool hilo = (MODE == kDown) || (MODE == kMatvec && a.x_f32 != nullptr);
-    uint32_t *xh = xlds;
-    uint32_t *xl = xlds + (size_t)a.t_rows * a.xs_max;
-
-    // stage activation rows t < t_rows (rows >= n are zero)
-    if (tid < kMaxT) s_tok[tid] = tid < n ? sc.g.slot[tid] : -1;
-    __syncthreads();
-    const int q4 = xs >> 1;           // 4-column quads per row
-    for (int i = tid; i < a.t_rows * q4; i += blockDim.x) {
-        const int t = i / q4, q = i - t * q4;
-        const int slot = s_tok[t];
-        uint2 hv = make_uint2(0, 0), lv = make_uint2(0, 0);
-        if (slot >= 0) {
-            if (!hilo) {
-                const int row = (MODE == kGateUp) ? slot_token(slot, a.n_route, a.k) : slot;
-                const uint16_t *src = a.x_bf16 + (size_t)row * a.x_stride + c0 + 4 * q;
-                hv = *(const uint2 *)src;
-            } else {
-                const float4 f = *(const float4 *)(a.x_f32 + (size_t)slot * a.x_stride + c0 + 4 * q);
-                uint32_t h0, l0, h1, l1, h2, l2, h3, l3;
-                split_bf16(f.x, h0, l0);
-                split_bf16(f.y, h1, l1);
-                split_bf16(f.z, h2, l2);
-                split_bf16(f.w, h3, l3);
-                hv = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
-                lv = make_uint2(l0 | (l1 << 16), l2 | (l3 << 16));
-            }
-        }
-        *(uint2 *)(xh + t * xs + 2 * q) = hv;
-        if (hilo) *(uint2 *)(xl + t * xs + 2 * q) = lv;
-    }
-    __syncthreads();
-
-    const int wave = tid >> 6, lane = tid & 63;
-    const Table &tb = (MODE == kGateUp && wave == 1) ? a.t1 : a.t0;
-    const int r0 = rb * kRowBlock + lane * kRowsPerLane;
-    const int nmat = MODE == kGateUp ? 2 : 1;
-    float *part_base = a.part + (size_t)(split * nmat + wave) * a.NS * a.R;
-    if (MODE == kDown) run_and_store<QT, true>(tb, e, r0, u0, u1, c0, grid, xh, xl, xs, n, s_tok, part_base, a.R);
-    else if (MODE == kGateUp) run_and_store<QT, false>(tb, e, r0, u0, u1, c0, grid, xh, xl, xs, n, s_tok, part_base, a.R);
-    else if (hilo) run_and_store<QT, true>(tb, e, r0, u0, u1, c0, grid, xh, xl, xs, n, s_tok, part_base, a.R);
-    else run_and_store<QT, false>(tb, e, r0, u0, u1, c0, grid, xh, xl, xs, n, s_tok, part_base, a.R);
-    __threadfence();
-    __syncthreads();
-
-    if (MODE == kGateUp || MODE == kMatvec) {
-        // the workgroup completing (group, row block) reduces the splits in order and runs the epilogue
-        uint32_t *c = a.cnt + gi * a.RB + rb;
-        if (tid == 0) s_last = (counter_add(c, 1u) == (uint32_t)(a.S - 1));
-        __syncthreads();
-        if (!s_last) return;
-        __threadfence();
-        for (int i = tid; i < n * kRowBlock; i += blockDim.x) {
-            const int t = i / kRowBlock, r = rb * kRowBlock + (i - t * kRowBlock);
-            const int slot = s_tok[t];
-            if (MODE == kGateUp) {
-                float g = 0.f, u = 0.f;
-                for (int s = 0; s < a.S; ++s) {
-                    g += a.part[((size_t)(s * 2 + 0) * a.NS + slot) * a.R + r];
-                    u += a.part[((size_t)(s * 2 + 1) * a.NS + slot) * a.R + r];
-                }
-                a.h[(size_t)slot * a.R + r] = swiglu_clamped(g, u, a.limit);
-            } else {
-                float v = 0.f;
-                for (int s = 0; s < a.S; ++s) v += a.part[((size_t)s * a.NS + slot) * a.R + r];
-                a.out_f32[(size_t)slot * a.R + r] = v;
-            }
-        }
-        if (tid == 0) counter_reset(c);
-        return;
-    }
-
-    // kDown: one completion counter per (row block, token); the last contributor combines that token's rows.
-    // lane t < n handles slot t of the group.
-    int mylast = 0, mytok = -1;
-    if (lane < n) {
-        const int slot = s_tok[lane];
-        mytok = slot_token(slot, a.n_route, a.k);
-        int nvalid = 0;
-        for (int j = 0; j < a.k; ++j) {
-            const int ej = a.idx[mytok * a.k + j];
-            nvalid += (ej >= 0 && ej < a.E) ? 1 : 0;
-        }
-        nvalid += a.shared_expert >= 0 ? 1 : 0;
-        const uint32_t target = (uint32_t)(nvalid * a.S);
-        mylast = counter_add(a.cnt + (size_t)rb * a.N + mytok, 1u) == target - 1u;
-    }
-    uint64_t lastmask = __ballot(mylast);
-    while (lastmask) {
-        const int t = __builtin_ctzll(lastmask);
-        lastmask &= lastmask - 1;
-        const int tok = __shfl(mytok, t, kWave);
-        __threadfence();
-        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int j = 0; j < a.k; ++j) {
-            const int ej = a.idx[tok * a.k + j];
-            if (ej < 0 || ej >= a.E) continue;
-            const int slot = tok * a.k + j;
-            float4 ys = make_float4(0.f, 0.f, 0.f, 0.f);
-            for (int s = 0; s < a.S; ++s) {
-                const float4 p = *(const float4 *)(a.part + ((size_t)s * a.NS + slot) * a.R + r0);
-                ys.x += p.x; ys.y += p.y; ys.z += p.z; ys.w += p.w;
-            }
-            const float wj = a.w[tok * a.k + j];
-            acc.x += wj * ys.x; acc.y += wj * ys.y; acc.z += wj * ys.z; acc.w += wj * ys.w;
-        }
-        if (a.shared_expert >= 0) {
-            const int slot = a.n_route + tok;
-            float4 ys = make_float4(0.f, 0.f, 0.f, 0.f);
-            for (int s = 0; s < a.S; ++s) {
-                const float4 p = *(const float4 *)(a.part + ((size_t)s * a.NS + slot) * a.R + r0);
-                ys.x += p.x; ys.y += p.y; ys.z += p.z; ys.w += p.w;
-            }
-            acc.x += ys.x; acc.y += ys.y; acc.z += ys.z; acc.w += ys.w;
-        }
-        if (a.out_f32) *(float4 *)(a.out_f32 + (size_t)tok * a.R + r0) = acc;
-        if (a.out_bf16) {
-            uint2 b;
-            b.x = f32_to_bf16_rne(acc.x) | (f32_to_bf16_rne(acc.y) << 16);
-            b.y = f32_to_bf16_rne(acc.z) | (f32_to_bf16_rne(acc.w) << 16);
-            *(uint2 *)(a.out_bf16 + (size_t)tok * a.R + r0) = b;
-        }
-        if (lane == 0) counter_reset(a.cnt + (size_t)rb * a.N + tok);
-    }
-}
 
 // ------------------------------------------------------------------------------------------------ dequant (debug)
 __global__ void dequant_kernel(Table tb, int e, float *out) {
@@ -353,10 +110,10 @@ static Table make_table(const mi_table *t) {
 }
 
 static int n_units_of(const mi_table *t) {
-    if (t->qtype == MI_QT_CB3) return ((t->cols + 9) / 10 + 1) / 2;
-    return t->cols / 256;
+    if (t->qtype == MI_QT_CB3) return (t->cols + 639) / 640;   // super-tiles
+    return t->cols / 256;                                        // IQ3_S blocks
 }
-static int unit_cols(const mi_table *t) { return t->qtype == MI_QT_CB3 ? 20 : 256; }
+static int unit_cols(const mi_table *t) { return t->qtype == MI_QT_CB3 ? 640 : 256; }
 
 static int env_int(const char *name, int dflt) {
     const char *v = getenv(name);
@@ -398,7 +155,7 @@ static int choose_splits(const mi_table *t, int groups_est, int rows_lds, int by
 
 struct DecodePlan {
     int G, S1, S2, rows1, rows2, NS, RB1, RB2;
-    size_t off_cnt1, off_cnt2, off_part1, off_h, off_part2, total;
+    size_t off_cnt2, off_part1, off_part2, total;
 };
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -406,27 +163,23 @@ static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 static DecodePlan plan_decode(const mi_table *gate, const mi_table *down, int N, int k, int shared) {
     DecodePlan p{};
     const int n_route = N * k;
-    p.G = max_groups(n_route, gate->n_experts, N, shared);
+    // token class of the launch: an expert sees at most one slot per token under top-k routing, so groups are
+    // capped at N slots (any duplicate routing just forms additional groups)
+    p.rows1 = class_rows(N < kMaxT ? N : kMaxT);
+    p.rows2 = p.rows1;
+    p.G = max_groups(n_route, gate->n_experts, N, shared, p.rows1);
     p.NS = n_route + (shared >= 0 ? N : 0);
     p.RB1 = gate->rows / kRowBlock;
     p.RB2 = down->rows / kRowBlock;
-    int max_per_group = n_route < kMaxT ? n_route : kMaxT;
-    if (shared >= 0 && N > max_per_group) max_per_group = N < kMaxT ? N : kMaxT;
-    p.rows1 = class_rows(max_per_group);
-    p.rows2 = p.rows1;
     int est = N == 1 ? p.G : (p.G * 6 + 5) / 10;
     if (est < 1) est = 1;
     p.S1 = choose_splits(gate, est, p.rows1, 2, "MI355MOE_S1");
     p.S2 = choose_splits(down, est, p.rows2, 4, "MI355MOE_S2");
     size_t off = 0;
-    p.off_cnt1 = off;
-    off = align256(off + sizeof(uint32_t) * (size_t)p.G * p.RB1);
     p.off_cnt2 = off;
     off = align256(off + sizeof(uint32_t) * (size_t)p.RB2 * N);
     p.off_part1 = off;
     off = align256(off + sizeof(float) * (size_t)p.S1 * 2 * p.NS * gate->rows);
-    p.off_h = off;
-    off = align256(off + sizeof(float) * (size_t)p.NS * gate->rows);
     p.off_part2 = off;
     off = align256(off + sizeof(float) * (size_t)p.S2 * p.NS * down->rows);
     p.total = off;
@@ -436,6 +189,26 @@ static DecodePlan plan_decode(const mi_table *gate, const mi_table *down, int N,
 static int launch_status() {
     hipError_t err = hipGetLastError();
     return err == hipSuccess ? MI_OK : MI_ERR_LAUNCH;
+}
+
+// The grouped kernels are instantiated in separate translation units (k_grouped.hip, built once per (mode, format))
+// so the build compiles them in parallel; each unit exports one launcher.
+#define MI_DECL_LAUNCH(M, Q) \
+    void launch_grouped_##M##_##Q(int tcmax, dim3 grid, dim3 block, size_t lds, hipStream_t s, const KArgs &a);
+MI_DECL_LAUNCH(0, 1)
+MI_DECL_LAUNCH(0, 2)
+MI_DECL_LAUNCH(1, 1)
+MI_DECL_LAUNCH(1, 2)
+MI_DECL_LAUNCH(2, 1)
+MI_DECL_LAUNCH(2, 2)
+#undef MI_DECL_LAUNCH
+
+template <int MODE>
+static void launch_grouped(int qtype, int tcmax, dim3 grid, dim3 block, size_t lds, hipStream_t s, const KArgs &a) {
+    const bool cb3 = qtype == MI_QT_CB3;
+    if (MODE == kGateUp) (cb3 ? launch_grouped_0_1 : launch_grouped_0_2)(tcmax, grid, block, lds, s, a);
+    else if (MODE == kDown) (cb3 ? launch_grouped_1_1 : launch_grouped_1_2)(tcmax, grid, block, lds, s, a);
+    else (cb3 ? launch_grouped_2_1 : launch_grouped_2_2)(tcmax, grid, block, lds, s, a);
 }
 
 }  // namespace mi
@@ -450,12 +223,14 @@ size_t mi_moe_decode_workspace(const mi_table *gate, const mi_table *down, int32
     return plan_decode(gate, down, N, k, shared_expert).total;
 }
 
-int mi_moe_decode(const mi_table *gate, const mi_table *up, const mi_table *down, const uint16_t *x_bf16,
-                  int32_t N, int32_t k, const int32_t *idx, const float *w, int32_t shared_expert, float limit,
-                  float *out_f32, uint16_t *out_bf16, void *workspace, size_t workspace_bytes, void *stream) {
+int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_table *down, const uint16_t *x_bf16,
+                         int32_t N, int32_t k, const int32_t *idx, const float *w, int32_t shared_expert,
+                         float limit, float *out_f32, uint16_t *out_bf16, void *workspace, size_t workspace_bytes,
+                         int32_t phases, void *stream) {
     int st;
+    if (phases < 1 || phases > 3) return MI_ERR_ARG;
     if ((st = validate_table(gate)) || (st = validate_table(up)) || (st = validate_table(down))) return st;
-    if (!x_bf16 || !idx || !w || (!out_f32 && !out_bf16)) return MI_ERR_NULL;
+    if (!x_bf16 || !idx || !w || ((phases & 2) && !out_f32 && !out_bf16)) return MI_ERR_NULL;
     if (up->qtype != gate->qtype || up->rows != gate->rows || up->cols != gate->cols ||
         up->n_experts != gate->n_experts)
         return MI_ERR_MISMATCH;
@@ -480,7 +255,7 @@ int mi_moe_decode(const mi_table *gate, const mi_table *up, const mi_table *down
     a.limit = limit;
     a.NS = p.NS;
 
-    // phase 1: gate + up + SwiGLU -> h [NS, I]
+    // phase 1: gate + up -> split-K partials [S1, 2, NS, I]
     a.t0 = make_table(gate);
     a.t1 = make_table(up);
     a.R = gate->rows;
@@ -494,16 +269,15 @@ int mi_moe_decode(const mi_table *gate, const mi_table *up, const mi_table *down
     a.x_f32 = nullptr;
     a.x_stride = gate->cols;
     a.part = (float *)(ws + p.off_part1);
-    a.cnt = (uint32_t *)(ws + p.off_cnt1);
-    a.h = (float *)(ws + p.off_h);
     size_t lds1 = sizeof(uint32_t) * (size_t)a.t_rows * a.xs_max;
-    if (gate->qtype == MI_QT_CB3)
-        hipLaunchKernelGGL((grouped_kernel<kGateUp, MI_QT_CB3>), dim3(p.G * p.RB1 * p.S1), dim3(128), lds1, s, a);
-    else
-        hipLaunchKernelGGL((grouped_kernel<kGateUp, MI_QT_IQ3_S>), dim3(p.G * p.RB1 * p.S1), dim3(128), lds1, s, a);
-    if ((st = launch_status())) return st;
+    if (phases & 1) {
+        launch_grouped<kGateUp>(gate->qtype, a.t_rows, dim3(p.G * p.RB1 * p.S1), dim3(128), lds1, s, a);
+        if ((st = launch_status())) return st;
+    }
+    if (!(phases & 2)) return MI_OK;
 
-    // phase 2: down + routing-weighted combine (+ shared expert) -> out [N, D]
+    // phase 2: h = SwiGLU(sum of the phase-1 partials) staged per split, down + routing-weighted combine (+ shared
+    // expert) -> out [N, D].  Stream order makes the phase-1 partials visible to this launch.
     KArgs b = a;
     b.t0 = make_table(down);
     b.t1 = b.t0;
@@ -515,31 +289,37 @@ int mi_moe_decode(const mi_table *gate, const mi_table *up, const mi_table *down
     b.xs_max = max_xs(down, p.S2);
     b.t_rows = p.rows2;
     b.x_bf16 = nullptr;
-    b.x_f32 = a.h;
+    b.x_f32 = nullptr;
+    b.p1 = (const float *)(ws + p.off_part1);
+    b.S1 = p.S1;
     b.x_stride = gate->rows;
     b.part = (float *)(ws + p.off_part2);
     b.cnt = (uint32_t *)(ws + p.off_cnt2);
     b.out_f32 = out_f32;
     b.out_bf16 = out_bf16;
     size_t lds2 = sizeof(uint32_t) * 2 * (size_t)b.t_rows * b.xs_max;
-    if (down->qtype == MI_QT_CB3)
-        hipLaunchKernelGGL((grouped_kernel<kDown, MI_QT_CB3>), dim3(p.G * p.RB2 * p.S2), dim3(64), lds2, s, b);
-    else
-        hipLaunchKernelGGL((grouped_kernel<kDown, MI_QT_IQ3_S>), dim3(p.G * p.RB2 * p.S2), dim3(64), lds2, s, b);
+    launch_grouped<kDown>(down->qtype, b.t_rows, dim3(p.G * p.RB2 * p.S2), dim3(64), lds2, s, b);
     return launch_status();
+}
+
+int mi_moe_decode(const mi_table *gate, const mi_table *up, const mi_table *down, const uint16_t *x_bf16,
+                  int32_t N, int32_t k, const int32_t *idx, const float *w, int32_t shared_expert, float limit,
+                  float *out_f32, uint16_t *out_bf16, void *workspace, size_t workspace_bytes, void *stream) {
+    return mi_moe_decode_phases(gate, up, down, x_bf16, N, k, idx, w, shared_expert, limit, out_f32, out_bf16,
+                                workspace, workspace_bytes, 3, stream);
 }
 
 // Split count of mi_matvec: a function of (table, n_slots) only, so the workspace size is known beforehand.  The LDS
 // budget is checked for f32 activations (the larger staging), which also covers bf16.
 static int matvec_splits(const mi_table *t, int n_slots) {
-    const int G = max_groups(n_slots, t->n_experts, 0, -1);
     const int rows = class_rows(n_slots < kMaxT ? n_slots : kMaxT);
+    const int G = max_groups(n_slots, t->n_experts, 0, -1, rows);
     return choose_splits(t, G, rows, 4, "MI355MOE_SMV");
 }
 
 size_t mi_matvec_workspace(const mi_table *t, int32_t n_slots) {
     if (validate_table(t) || n_slots <= 0 || n_slots > MI_MAX_SLOTS) return 0;
-    const int G = max_groups(n_slots, t->n_experts, 0, -1);
+    const int G = max_groups(n_slots, t->n_experts, 0, -1, class_rows(n_slots < kMaxT ? n_slots : kMaxT));
     const int S = matvec_splits(t, n_slots);
     return align256(sizeof(uint32_t) * (size_t)G * (t->rows / kRowBlock)) +
            align256(sizeof(float) * (size_t)S * n_slots * t->rows);
@@ -555,9 +335,9 @@ int mi_matvec(const mi_table *t, const int32_t *idx, int32_t n_slots, const void
     if (x_stride < t->cols || x_stride % 4) return MI_ERR_ARG;
     const size_t need = mi_matvec_workspace(t, n_slots);
     if (!workspace || workspace_bytes < need) return MI_ERR_WORKSPACE;
-    const int G = max_groups(n_slots, t->n_experts, 0, -1);
-    const int RB = t->rows / kRowBlock;
     const int rows = class_rows(n_slots < kMaxT ? n_slots : kMaxT);
+    const int G = max_groups(n_slots, t->n_experts, 0, -1, rows);
+    const int RB = t->rows / kRowBlock;
     const int S = matvec_splits(t, n_slots);
     const int nu = n_units_of(t);
     KArgs a{};
@@ -585,10 +365,7 @@ int mi_matvec(const mi_table *t, const int32_t *idx, int32_t n_slots, const void
     a.part = (float *)(ws + align256(sizeof(uint32_t) * (size_t)G * RB));
     a.out_f32 = out;
     size_t lds = sizeof(uint32_t) * (x_dtype == MI_X_F32 ? 2 : 1) * (size_t)a.t_rows * a.xs_max;
-    if (t->qtype == MI_QT_CB3)
-        hipLaunchKernelGGL((grouped_kernel<kMatvec, MI_QT_CB3>), dim3(G * RB * S), dim3(64), lds, (hipStream_t)stream, a);
-    else
-        hipLaunchKernelGGL((grouped_kernel<kMatvec, MI_QT_IQ3_S>), dim3(G * RB * S), dim3(64), lds, (hipStream_t)stream, a);
+    launch_grouped<kMatvec>(t->qtype, a.t_rows, dim3(G * RB * S), dim3(64), lds, (hipStream_t)stream, a);
     return launch_status();
 }
 

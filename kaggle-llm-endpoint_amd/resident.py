@@ -105,7 +105,17 @@ WORKSPACES = _Workspaces()
 def matvec(table, idx, X):
     """moe_matvec (pallas_moe.py:238-307): out[i, r] = sum_n W_{idx[i]}[r, n] X_i[n].
     idx int32 [n_slots]; X [n_slots, K] bf16 or f32 (natural input order) -> f32 [n_slots, R]."""
-    idx = idx.to(torch.int32).contiguous()
+    n = int(idx.numel())
+    out = torch.empty((n, table.rows), dtype=torch.float32, device=X.device)
+    return matvec_into(table, idx, X, out, None)
+
+
+def matvec_into(table, idx, X, out, workspace):
+    """``matvec`` writing into ``out`` f32 [n_slots, R]; a preallocated zero-filled ``workspace`` (uint8 tensor of
+    at least mi_matvec_workspace bytes) makes the call allocation-free."""
+    if idx.dtype != torch.int32:
+        idx = idx.to(torch.int32)
+    idx = idx.contiguous()
     n = int(idx.numel())
     if X.dim() != 2 or X.shape[0] != n or X.shape[1] != table.cols:
         raise ValueError("X must be [n_slots, K]")
@@ -116,9 +126,9 @@ def matvec(table, idx, X):
     else:
         raise ValueError("X must be bf16 or f32")
     X = X.contiguous()
-    out = torch.empty((n, table.rows), dtype=torch.float32, device=X.device)
-    nbytes = lib().mi_matvec_workspace(table.c, n)
-    ws = WORKSPACES.get("matvec", nbytes)
+    ws = workspace
+    if ws is None:
+        ws = WORKSPACES.get("matvec", lib().mi_matvec_workspace(table.c, n))
     check("mi_matvec", lib().mi_matvec(table.c, _ptr(idx), n, _ptr(X), xd, X.shape[1], _ptr(out), _ptr(ws),
                                        ws.numel(), _stream()))
     return out
@@ -131,37 +141,57 @@ def dequant(table, expert):
     return out
 
 
-def moe_decode(gate, up, down, x, idx, w, limit, shared_expert=-1, want_f32=True, want_bf16=False):
+def decode_workspace_bytes(gate, down, N, k, shared_expert=-1):
+    n = lib().mi_moe_decode_workspace(gate.c, down.c, int(N), int(k), int(shared_expert))
+    if n == 0:
+        raise ValueError("mi_moe_decode: invalid tables or token counts (N=%d, k=%d)" % (N, k))
+    return n
+
+
+def moe_decode(gate, up, down, x, idx, w, limit, shared_expert=-1, want_f32=True, want_bf16=False, out_f32=None,
+               out_bf16=None, workspace=None, phases=3):
     """Fused decode MoE (resident.py:110-120 composition), tokens grouped by expert on the device.
-    x bf16 [N, D]; idx int32 [N, k]; w f32 [N, k] -> (out_f32 [N, D] or None, out_bf16 [N, D] or None)."""
+    x bf16 [N, D]; idx int32 [N, k]; w f32 [N, k] -> (out_f32 [N, D] or None, out_bf16 [N, D] or None).
+    Preallocated ``out_f32`` / ``out_bf16`` / ``workspace`` (a zero-filled uint8 device tensor) make the call
+    allocation-free (graph capture).  ``phases``: 1 = gate/up/SwiGLU only, 2 = down/combine only, 3 = both."""
     if x.dtype != torch.bfloat16:
         raise ValueError("decode activations are bf16")
     N, k = idx.shape
     x = x.contiguous()
-    idx = idx.to(torch.int32).contiguous()
-    w = w.to(torch.float32).contiguous()
+    if idx.dtype != torch.int32:
+        idx = idx.to(torch.int32)
+    if w.dtype != torch.float32:
+        w = w.to(torch.float32)
+    idx, w = idx.contiguous(), w.contiguous()
     D = down.rows
-    of = torch.empty((N, D), dtype=torch.float32, device=x.device) if want_f32 else None
-    ob = torch.empty((N, D), dtype=torch.bfloat16, device=x.device) if want_bf16 else None
-    nbytes = lib().mi_moe_decode_workspace(gate.c, down.c, N, k, int(shared_expert))
-    if nbytes == 0:
-        raise ValueError("mi_moe_decode: invalid tables or token counts (N=%d, k=%d)" % (N, k))
-    ws = WORKSPACES.get("decode", nbytes)
-    check("mi_moe_decode", lib().mi_moe_decode(gate.c, up.c, down.c, _ptr(x), N, k, _ptr(idx), _ptr(w),
-                                               int(shared_expert), float(limit), _ptr(of), _ptr(ob), _ptr(ws),
-                                               ws.numel(), _stream()))
+    of, ob = out_f32, out_bf16
+    if phases & 2:
+        if of is None and want_f32:
+            of = torch.empty((N, D), dtype=torch.float32, device=x.device)
+        if ob is None and want_bf16:
+            ob = torch.empty((N, D), dtype=torch.bfloat16, device=x.device)
+    ws = workspace
+    if ws is None:
+        ws = WORKSPACES.get("decode", decode_workspace_bytes(gate, down, N, k, shared_expert))
+    check("mi_moe_decode", lib().mi_moe_decode_phases(gate.c, up.c, down.c, _ptr(x), N, k, _ptr(idx), _ptr(w),
+                                                      int(shared_expert), float(limit), _ptr(of), _ptr(ob),
+                                                      _ptr(ws), ws.numel(), int(phases), _stream()))
     return of, ob
 
 
-def int8_project(x, qT, s, want_f32=False):
-    """y = x @ bf16(f32(q) * s) (quant8.py:91-99): x bf16 [B, n_in], qT int8 [n_out, n_in], s f32 [n_out]."""
+def int8_project(x, qT, s, want_f32=False, y_bf16=None, y_f32=None, workspace=None):
+    """y = x @ bf16(f32(q) * s) (quant8.py:91-99): x bf16 [B, n_in], qT int8 [n_out, n_in], s f32 [n_out].
+    Preallocated outputs / workspace make the call allocation-free."""
     B, n_in = x.shape
     n_out = qT.shape[0]
     x = x.contiguous()
-    yb = torch.empty((B, n_out), dtype=torch.bfloat16, device=x.device)
-    yf = torch.empty((B, n_out), dtype=torch.float32, device=x.device) if want_f32 else None
+    yb = y_bf16 if y_bf16 is not None else torch.empty((B, n_out), dtype=torch.bfloat16, device=x.device)
+    yf = y_f32 if y_f32 is not None else (
+        torch.empty((B, n_out), dtype=torch.float32, device=x.device) if want_f32 else None)
     nbytes = lib().mi_int8_project_workspace(B, n_in, n_out)
-    ws = WORKSPACES.get("int8", nbytes)
+    if nbytes == 0:
+        raise ValueError("mi_int8_project: unsupported shape B=%d n_in=%d n_out=%d" % (B, n_in, n_out))
+    ws = workspace if workspace is not None else WORKSPACES.get("int8", nbytes)
     check("mi_int8_project", lib().mi_int8_project(_ptr(x), B, _ptr(qT), _ptr(s), n_in, n_out, _ptr(yb), _ptr(yf),
                                                    _ptr(ws), ws.numel(), _stream()))
     return (yb, yf) if want_f32 else yb
