@@ -40,6 +40,8 @@ struct KArgs {
     int S;                     // column splits
     int n_units;               // column units (CB3: word pairs, IQ3_S: blocks)
     int RB;                    // row blocks (R / 256)
+    int RBW;                   // row blocks per workgroup (kDown / kMatvec: one per wavefront; kGateUp: 1)
+    int RBG;                   // row-block groups: ceil(RB / RBW)
     int xs_max;                // LDS dwords per staged row
     int t_rows;                // LDS rows staged (class of the largest group)
     // activations
@@ -107,19 +109,22 @@ __device__ __forceinline__ void run_and_store(const Table &tb, int e, int r0, in
 #undef MI_RUN_CLASS
 }
 
+// Workgroup shape: gate/up = 2 wavefronts (gate, up) over one row block; down / matvec = kRbWaves wavefronts over
+// kRbWaves consecutive row blocks, which share the staged activation slice.
+constexpr int kRbWaves = 4;
+
 template <int MODE, int QT, int TCMAX>
-__global__ void __launch_bounds__(MODE == kGateUp ? 128 : 64) grouped_kernel(KArgs a) {
+__global__ void __launch_bounds__(MODE == kGateUp ? 128 : 64 * kRbWaves) grouped_kernel(KArgs a) {
     extern __shared__ uint32_t xlds[];
     __shared__ GroupScratch sc;
     __shared__ uint32_t grid[512];
-    __shared__ int s_last;
     __shared__ int s_tok[kMaxT];
 
     const int tid = threadIdx.x;
     const int task = blockIdx.x;
     const int split = task % a.S;
-    const int rb = (task / a.S) % a.RB;
-    const int gi = task / (a.S * a.RB);
+    const int rbg = (task / a.S) % a.RBG;
+    const int gi = task / (a.S * a.RBG);
 
     find_group(sc, a.idx, a.n_route, a.E, a.shared_expert, a.N, gi, a.t_rows);
     const int e = sc.g.expert;
@@ -188,9 +193,15 @@ __global__ void __launch_bounds__(MODE == kGateUp ? 128 : 64) grouped_kernel(KAr
 
     const int wave = tid >> 6, lane = tid & 63;
     const Table &tb = (MODE == kGateUp && wave == 1) ? a.t1 : a.t0;
+    const int rb = rbg * a.RBW + (MODE == kGateUp ? 0 : wave);
+    if (rb >= a.RB) {           // wavefront past the last row block: it only helps stage
+        stage();
+        return;
+    }
     const int r0 = rb * kRowBlock + lane * kRowsPerLane;
     const int nmat = MODE == kGateUp ? 2 : 1;
-    float *part_base = a.part + (size_t)(split * nmat + wave) * a.NS * a.R;
+    const int mat = MODE == kGateUp ? wave : 0;   // gate/up: wave 0 = gate, wave 1 = up
+    float *part_base = a.part + (size_t)(split * nmat + mat) * a.NS * a.R;
     if (MODE == kDown)
         run_and_store<QT, true, TCMAX>(tb, e, r0, u0, u1, c0, grid, xh, xl, xs, n, s_tok, part_base, a.R, stage);
     else if (MODE == kGateUp)
@@ -201,33 +212,32 @@ __global__ void __launch_bounds__(MODE == kGateUp ? 128 : 64) grouped_kernel(KAr
         run_and_store<QT, false, TCMAX>(tb, e, r0, u0, u1, c0, grid, xh, xl, xs, n, s_tok, part_base, a.R, stage);
     // gate/up: the partials are reduced by the down launch while it stages h (kernel order publishes them)
     if (MODE == kGateUp) return;
-    __syncthreads();   // every wave's partial stores have completed to L2
+    // From here on every wavefront works alone on its own row block (no workgroup barriers).
+    fence_release_agent();   // this wavefront's partial stores, before its completion count
 
     if (MODE == kMatvec) {
-        // the workgroup completing (group, row block) reduces the splits in order and stores the rows
+        // the wavefront completing (group, row block) reduces the splits in order and stores the rows
         uint32_t *c = a.cnt + gi * a.RB + rb;
-        if (tid == 0) {
-            fence_release_agent();
-            s_last = (counter_add(c, 1u) == (uint32_t)(a.S - 1));
-        }
-        __syncthreads();
-        if (!s_last) return;
+        uint32_t prev = 0;
+        if (lane == 0) prev = counter_add(c, 1u);
+        if (__shfl(prev, 0, kWave) != (uint32_t)(a.S - 1)) return;
         fence_acquire_agent();
-        for (int i = tid; i < n * kRowBlock; i += blockDim.x) {
-            const int t = i / kRowBlock, r = rb * kRowBlock + (i - t * kRowBlock);
+        for (int t = 0; t < n; ++t) {
             const int slot = s_tok[t];
-            float v = 0.f;
-            for (int s = 0; s < a.S; ++s) v += a.part[((size_t)s * a.NS + slot) * a.R + r];
-            a.out_f32[(size_t)slot * a.R + r] = v;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int s = 0; s < a.S; ++s) {
+                const float4 p = *(const float4 *)(a.part + ((size_t)s * a.NS + slot) * a.R + r0);
+                v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
+            }
+            *(float4 *)(a.out_f32 + (size_t)slot * a.R + r0) = v;
         }
-        if (tid == 0) counter_reset(c);
+        if (lane == 0) counter_reset(c);
         return;
     }
 
     // kDown: one completion counter per (row block, token); the last contributor combines that token's rows.
     // lane t < n handles slot t of the group.
     int mylast = 0, mytok = -1;
-    fence_release_agent();
     if (lane < n) {
         const int slot = s_tok[lane];
         mytok = slot_token(slot, a.n_route, a.k);

@@ -140,6 +140,7 @@ static int max_xs(const mi_table *t, int S) {
 }
 
 // Pick the column split count: enough workgroups to cover the chip (~768 tasks), LDS within the budget.
+// (The target counts wavefronts: one per (group, row block, split) whatever the workgroup shape.)
 static int choose_splits(const mi_table *t, int groups_est, int rows_lds, int bytes_per_col, const char *env) {
     const int nu = n_units_of(t);
     const int RB = t->rows / kRowBlock;
@@ -154,7 +155,7 @@ static int choose_splits(const mi_table *t, int groups_est, int rows_lds, int by
 }
 
 struct DecodePlan {
-    int G, S1, S2, rows1, rows2, NS, RB1, RB2;
+    int G, S1, S2, rows1, rows2, NS, RB1, RB2, RBG2;
     size_t off_cnt2, off_part1, off_part2, total;
 };
 
@@ -171,6 +172,7 @@ static DecodePlan plan_decode(const mi_table *gate, const mi_table *down, int N,
     p.NS = n_route + (shared >= 0 ? N : 0);
     p.RB1 = gate->rows / kRowBlock;
     p.RB2 = down->rows / kRowBlock;
+    p.RBG2 = (p.RB2 + kRbWaves - 1) / kRbWaves;
     int est = N == 1 ? p.G : (p.G * 6 + 5) / 10;
     if (est < 1) est = 1;
     p.S1 = choose_splits(gate, est, p.rows1, 2, "MI355MOE_S1");
@@ -263,6 +265,8 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
     a.S = p.S1;
     a.n_units = n_units_of(gate);
     a.RB = p.RB1;
+    a.RBW = 1;
+    a.RBG = p.RB1;
     a.xs_max = max_xs(gate, p.S1);
     a.t_rows = p.rows1;
     a.x_bf16 = x_bf16;
@@ -286,6 +290,8 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
     b.S = p.S2;
     b.n_units = n_units_of(down);
     b.RB = p.RB2;
+    b.RBW = kRbWaves;
+    b.RBG = p.RBG2;
     b.xs_max = max_xs(down, p.S2);
     b.t_rows = p.rows2;
     b.x_bf16 = nullptr;
@@ -298,7 +304,7 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
     b.out_f32 = out_f32;
     b.out_bf16 = out_bf16;
     size_t lds2 = sizeof(uint32_t) * 2 * (size_t)b.t_rows * b.xs_max;
-    launch_grouped<kDown>(down->qtype, b.t_rows, dim3(p.G * p.RB2 * p.S2), dim3(64), lds2, s, b);
+    launch_grouped<kDown>(down->qtype, b.t_rows, dim3(p.G * p.RBG2 * p.S2), dim3(64 * kRbWaves), lds2, s, b);
     return launch_status();
 }
 
@@ -353,6 +359,8 @@ int mi_matvec(const mi_table *t, const int32_t *idx, int32_t n_slots, const void
     a.S = S;
     a.n_units = nu;
     a.RB = RB;
+    a.RBW = kRbWaves;
+    a.RBG = (RB + kRbWaves - 1) / kRbWaves;
     a.xs_max = max_xs(t, S);
     a.t_rows = rows;
     a.x_bf16 = x_dtype == MI_X_BF16 ? (const uint16_t *)x : nullptr;
@@ -365,7 +373,8 @@ int mi_matvec(const mi_table *t, const int32_t *idx, int32_t n_slots, const void
     a.part = (float *)(ws + align256(sizeof(uint32_t) * (size_t)G * RB));
     a.out_f32 = out;
     size_t lds = sizeof(uint32_t) * (x_dtype == MI_X_F32 ? 2 : 1) * (size_t)a.t_rows * a.xs_max;
-    launch_grouped<kMatvec>(t->qtype, a.t_rows, dim3(G * RB * S), dim3(64), lds, (hipStream_t)stream, a);
+    launch_grouped<kMatvec>(t->qtype, a.t_rows, dim3(G * a.RBG * S), dim3(64 * kRbWaves), lds, (hipStream_t)stream,
+                            a);
     return launch_status();
 }
 
