@@ -50,24 +50,20 @@ def cb3_bytes(R, K):
 
 def random_cb3_planes(torch, gen, E, R, K):
     """Device planes of E random CB3 experts (uniform codes, sorted N(0, 0.02) bf16 centroids) in the kernel layout:
-    qs int32 [E*Wd, R], cb int32 [E*G*4, R]."""
-    Wd, G = math.ceil(K / 10), K // 128
-    qs = torch.randint(-2 ** 31, 2 ** 31 - 1, (E, Wd, R), dtype=torch.int32, device="cuda", generator=gen)
-    odd = torch.zeros(Wd, dtype=torch.bool, device="cuda")
-    odd[1::2] = True
-    if Wd % 2:
-        odd[-1] = False
-    qs[:, odd, :] &= 0x7F7F7F7F                                   # second word of a pair: bit 7 of every byte unused
-    qs = qs.reshape(E * Wd, R)
+    qs int32 [E, CT*RT*256] tile words (every bit pattern is a valid set of codes; the padding columns of the last
+    tile multiply zero activations), cb int32 [E, G*R*4]."""
+    CT, G = math.ceil(K / 160), K // 128
+    qs = torch.randint(-2 ** 31, 2 ** 31 - 1, (E, CT * (R // 16) * 256), dtype=torch.int32, device="cuda",
+                       generator=gen)
     cbs = []
+    sh = torch.tensor([0, 8, 16, 24], device="cuda", dtype=torch.int32)
+    pack = lambda a: (a << sh).sum(-1).to(torch.int32)
     for e in range(E):
-        c = torch.randn((R, G, 8), device="cuda", generator=gen) * 0.02
+        c = torch.randn((G, R, 8), device="cuda", generator=gen) * 0.02
         c = torch.sort(c, dim=-1).values.to(torch.bfloat16).view(torch.int16).to(torch.int32) & 0xFFFF
         lo, hi = c & 0xFF, c >> 8
-        sh = torch.tensor([0, 8, 16, 24], device="cuda", dtype=torch.int32)
-        pack = lambda a: (a << sh).sum(-1).to(torch.int32)
         w = torch.stack([pack(lo[..., 0:4]), pack(lo[..., 4:8]), pack(hi[..., 0:4]), pack(hi[..., 4:8])], -1)
-        cbs.append(w.permute(1, 2, 0).reshape(G * 4, R))           # [G, 4, R]
+        cbs.append(w.reshape(1, G * R * 4))                         # [G, R, 4]
     return {"qs": qs, "cb": torch.cat(cbs, 0).contiguous()}
 
 

@@ -1,0 +1,207 @@
+// CB3 (3-bit codebook) experts on the gfx950 matrix cores.
+//
+// Device layout (written by formats.py; the same bytes per row as the canonical 10-codes-per-u32 packing, plus the
+// zero padding of the last column tile):
+//   code tile (ct, rt): rows 16 rt .. 16 rt + 15 x columns 160 ct .. 160 ct + 159, 1 KB = 64 lanes x 4 words, tiles
+//   ordered [expert][ct][rt].  Lane l = 16 q + i holds row 16 rt + i at the columns 160 ct + 32 m + 8 q + j
+//   (m = 0..4, j = 0..7), code n = 8 m + j -- exactly the A-operand slice lane l feeds to v_mfma_f32_16x16x32_bf16
+//   at k-step m.  Word pair p = 0, 1 (words 2p, 2p+1) holds the codes n = 20 p + c, c = 0..19:
+//       word 2p   byte b = code[c=b] | code[c=4+b] << 3 | (code[c=16+b] & 3) << 6
+//       word 2p+1 byte b = code[c=8+b] | code[c=12+b] << 3 | (code[c=16+b] >> 2) << 6      (b = 0..3)
+//   so one AND (and a shift) yields four byte-sized codebook selectors.  Columns past K hold code 0.
+//   codebook: [expert][group g of 128 columns][row] x 4 dwords: lo bytes of centroids 0-3, 4-7, hi bytes 0-3, 4-7.
+//
+// Decode: v_perm_b32 looks 4 codes up at once in the 8-byte {lo47:lo03} and {hi47:hi03} tables and two more perms
+// interleave the bytes into bf16 pairs, so 8 weights (one k-step of one lane) cost 8 perms and ~3 ALU ops; the
+// contraction with the activations runs on the matrix cores (16 tokens per instruction), which keeps the vector ALU
+// budget per HBM byte independent of the number of tokens sharing the expert.
+//
+// Column tiles (160) and codebook groups (128) realign every 640 columns (4 tiles = 5 groups): inside such a super
+// tile, column tile c uses group c for k-steps m < 4 - c and group c + 1 after, all at compile-time positions, so the
+// code ring (one super tile of code words), the five codebook slots and every LDS offset are static.
+#pragma once
+#include "common.h"
+
+namespace mi {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+struct Cb3Table {
+    const uint32_t *qs;
+    const uint32_t *cb;
+    int R, K, CT, G, RT;
+    static constexpr int kUnitCols = 160;   // column splits are whole column tiles
+};
+
+constexpr int kCb3TileCols = 160;
+constexpr int kCb3Rtw = 4;                    // row tiles per wavefront
+constexpr int kCb3WaveRows = 16 * kCb3Rtw;    // 64 rows per wavefront
+
+// wave-uniform base (SGPRs) + the lane's byte offset: the scalar-base addressing form for every stream load
+__device__ __forceinline__ uint4 ld_lane(const uint32_t *__restrict__ base, uint32_t lane_bytes) {
+    return *(const uint4 *)((const char *)base + lane_bytes);
+}
+
+// Selectors (4 codes each) of k-step M from the lane's 4 code words.
+template <int M>
+__device__ __forceinline__ void cb3_sel(const uint4 w, uint32_t &s0, uint32_t &s1) {
+    constexpr uint32_t k7 = 0x07070707u;
+    if constexpr (M == 0) {
+        s0 = w.x & k7;
+        s1 = (w.x >> 3) & k7;
+    } else if constexpr (M == 1) {
+        s0 = w.y & k7;
+        s1 = (w.y >> 3) & k7;
+    } else if constexpr (M == 2) {
+        s0 = ((w.x >> 6) & 0x03030303u) | ((w.y >> 4) & 0x04040404u);
+        s1 = w.z & k7;
+    } else if constexpr (M == 3) {
+        s0 = (w.z >> 3) & k7;
+        s1 = w.w & k7;
+    } else {
+        s0 = (w.w >> 3) & k7;
+        s1 = ((w.z >> 6) & 0x03030303u) | ((w.w >> 4) & 0x04040404u);
+    }
+}
+
+// 8 bf16 weights (k = 0..7 of the step) from two selectors and the row's codebook group.
+__device__ __forceinline__ bf16x8 cb3_weights8(uint32_t s0, uint32_t s1, const uint4 cb) {
+    const uint32_t lo0 = perm(cb.y, cb.x, s0), hi0 = perm(cb.w, cb.z, s0);
+    const uint32_t lo1 = perm(cb.y, cb.x, s1), hi1 = perm(cb.w, cb.z, s1);
+    uint4 v;
+    v.x = perm(hi0, lo0, 0x05010400u);
+    v.y = perm(hi0, lo0, 0x07030602u);
+    v.z = perm(hi1, lo1, 0x05010400u);
+    v.w = perm(hi1, lo1, 0x07030602u);
+    return __builtin_bit_cast(bf16x8, v);
+}
+
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, uint4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// Per-wavefront stream state.
+struct Cb3Wave {
+    const uint32_t *qt;    // expert's code tiles
+    const uint32_t *cbe;   // expert's codebook
+    int RT, G, CT, R;
+    int rt0;               // first row tile
+    int cta, ctb;          // column tiles [cta, ctb) of the wavefront's split
+    int g_last;            // last codebook group the split uses
+    uint32_t lane16;       // lane * 16 bytes
+    const uint32_t *xh;    // LDS: B-operand row of this lane (hi / bf16 part) at column 640 * (cta / 4)
+    const uint32_t *xl;    // LDS: lo part (two-instruction mode)
+    uint4 *cbl;            // LDS: this wavefront's codebook slots, 5 groups x 64 rows
+};
+
+// Codebook path: one 1 KB load brings a group's 16-byte codebooks of the wavefront's 64 rows (lane = row) into the
+// register slot of its super-tile position; right before the group is first needed it is written to the
+// wavefront's own LDS slot (same-wavefront LDS accesses stay in order, so no barrier) and the register slot is
+// reloaded with the next super tile's group.  The decoders read a row's 16 bytes from LDS per k-step, so a lane
+// never holds the 4 row tiles' codebooks in registers.
+struct Cb3Regs {
+    uint4 ring[4][kCb3Rtw];   // code words: slot c = column tile c of a super tile
+    uint4 cbv[5];             // codebook groups in flight: slot c = group c of the next super tile
+    f32x4 acc[kCb3Rtw];
+};
+
+__device__ __forceinline__ const uint32_t *cb3_tile(const Cb3Wave &w, int ct, int r) {
+    return w.qt + ((size_t)ct * w.RT + w.rt0 + r) * 256;
+}
+__device__ __forceinline__ const uint32_t *cb3_group(const Cb3Wave &w, int g) {
+    return w.cbe + ((size_t)g * w.R + 16 * w.rt0) * 4;
+}
+
+// k-steps M..4 of one row tile's column tile (recursion keeps every index static).
+template <bool TWO, int C, int M>
+__device__ __forceinline__ void cb3_steps(const uint4 wv, const uint4 *cbrow, int r, const uint4 (&xb)[5],
+                                          const uint4 (&xl)[5], f32x4 &acc) {
+    if constexpr (M < 5) {
+        constexpr int slot = (M < 4 - C) ? C : C + 1;
+        uint32_t s0, s1;
+        cb3_sel<M>(wv, s0, s1);
+        const bf16x8 a = cb3_weights8(s0, s1, cbrow[slot * 64 + 16 * r]);
+        acc = mfma16(a, xb[M], acc);
+        if constexpr (TWO) acc = mfma16(a, xl[M], acc);
+        cb3_steps<TWO, C, M + 1>(wv, cbrow, r, xb, xl, acc);
+    }
+}
+
+// Column tile C of super tile st: publish the codebook groups first needed here (C = 0: groups 0, 1; else group
+// C + 1) and reload their register slots with the next super tile's groups; read the B operands; then per row
+// tile take the ring slot, refill it with column tile C of the next super tile and decode + MFMA the 5 k-steps.
+// Loads the split does not need re-read data already loaded (cache hits), so the instruction stream -- and the
+// compiler's wait counts -- never depend on the split's bounds.
+template <bool TWO, int C>
+__device__ __forceinline__ void cb3_ctile(const Cb3Wave &w, Cb3Regs &s, int st) {
+    const int lane = threadIdx.x & 63;
+    const int gn = 5 * (st + 1);
+    if constexpr (C == 0) {
+        w.cbl[0 * 64 + lane] = s.cbv[0];
+        w.cbl[1 * 64 + lane] = s.cbv[1];
+        s.cbv[0] = ld_lane(cb3_group(w, min(gn, w.g_last)), w.lane16);
+        s.cbv[1] = ld_lane(cb3_group(w, min(gn + 1, w.g_last)), w.lane16);
+    } else {
+        w.cbl[(C + 1) * 64 + lane] = s.cbv[C + 1];
+        s.cbv[C + 1] = ld_lane(cb3_group(w, min(gn + C + 1, w.g_last)), w.lane16);
+    }
+    const int ct = 4 * st + C;
+    const int xo = 80 * (ct - (w.cta & ~3));                // dwords
+    uint4 xb[5], xl[5];
+#pragma unroll
+    for (int m = 0; m < 5; ++m) {
+        xb[m] = *(const uint4 *)(w.xh + xo + 16 * m);
+        if (TWO) xl[m] = *(const uint4 *)(w.xl + xo + 16 * m);
+        else xl[m] = xb[m];
+    }
+    const int ctn = (ct + 4 < w.ctb) ? ct + 4 : max(ct, w.cta);
+    const uint4 *cbrow = w.cbl + (lane & 15);
+#pragma unroll
+    for (int r = 0; r < kCb3Rtw; ++r) {
+        const uint4 wv = s.ring[C][r];
+        s.ring[C][r] = ld_lane(cb3_tile(w, ctn, r), w.lane16);
+        cb3_steps<TWO, C, 0>(wv, cbrow, r, xb, xl, s.acc[r]);
+    }
+}
+
+// Streams column tiles [cta, ctb) of the wavefront's 64 rows, as whole super tiles from the one holding cta: the
+// column tiles before cta run against zero activations (their loads re-read cta's data, so they cost vector ALU work
+// but no HBM traffic), which keeps the code ring and codebook slots at static positions.  The split's last super tile
+// may end early.  `stage` (ending in a workgroup barrier) runs after the first loads are issued.
+template <bool TWO, class Stage>
+__device__ __forceinline__ void cb3_accum_mfma(const Cb3Wave &w, f32x4 (&acc)[kCb3Rtw], Stage &&stage) {
+    Cb3Regs s;
+    const int sta = w.cta >> 2;
+    const int g_first = (kCb3TileCols * w.cta) >> 7;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int ct = min(max(4 * sta + c, w.cta), w.ctb - 1);
+#pragma unroll
+        for (int r = 0; r < kCb3Rtw; ++r) s.ring[c][r] = ld_lane(cb3_tile(w, ct, r), w.lane16);
+    }
+#pragma unroll
+    for (int c = 0; c < 5; ++c) s.cbv[c] = ld_lane(cb3_group(w, min(max(5 * sta + c, g_first), w.g_last)), w.lane16);
+#pragma unroll
+    for (int r = 0; r < kCb3Rtw; ++r) s.acc[r] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    stage();
+
+    const int st_full = w.ctb >> 2;      // super tiles that end inside the split
+    int st = sta;
+    for (; st < st_full; ++st) {
+        cb3_ctile<TWO, 0>(w, s, st);
+        cb3_ctile<TWO, 1>(w, s, st);
+        cb3_ctile<TWO, 2>(w, s, st);
+        cb3_ctile<TWO, 3>(w, s, st);
+    }
+    const int nct = w.ctb - 4 * st;      // 0..3 column tiles of a last, partial super tile
+    if (nct > 0) {
+        cb3_ctile<TWO, 0>(w, s, st);
+        if (nct > 1) cb3_ctile<TWO, 1>(w, s, st);
+        if (nct > 2) cb3_ctile<TWO, 2>(w, s, st);
+    }
+#pragma unroll
+    for (int r = 0; r < kCb3Rtw; ++r) acc[r] = s.acc[r];
+}
+
+}  // namespace mi

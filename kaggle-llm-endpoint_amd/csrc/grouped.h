@@ -1,18 +1,18 @@
-// Grouped codebook-dequant expert matvec kernels for gfx950 (MI355X) and their C ABI.
+// Grouped codebook-dequant expert matvec kernels for gfx950 (MI355X).
 //
-// One launch covers every (expert group, 256-row block, column split) task of a call.  A workgroup
+// One launch covers every (expert group, row range, column split) task of a call.  A workgroup of 4 wavefronts
 //   1. regroups the call's routing on the device (find_group: slots sorted by expert, <= 16 slots per group),
 //   2. issues its first weight loads, then stages the group's activation rows for its column split in LDS while
 //      they are in flight (the down projection rebuilds h = SwiGLU(gate, up) here from the gate/up partials),
-//   3. streams the expert's planes once -- each lane owns 4 consecutive rows, so every plane access is one
-//      128-bit load and the wavefront reads 1 KB contiguous -- decoding codes to bf16 in registers and
-//      accumulating bf16-pair dot products in f32 for all the group's rows at once,
-//   4. writes its f32 partial sums.  Gate/up stops there: the next launch reduces them.  Matvec and down bump an
-//      agent-scope completion counter; the workgroup that completes a (group, row block) -- or, for the down
-//      projection, a (row block, token) -- reduces the partials in a fixed order and stores the rows or runs the
-//      routing-weighted combine.
+//   3. streams the expert's planes once with 128-bit loads (every wavefront load is 1 KB contiguous) and decodes
+//      the codes to bf16 in registers: CB3 tiles feed the matrix cores (64 rows per wavefront, all of the group's
+//      tokens in one 16-column tile), IQ3_S rows feed bf16-pair dot products (256 rows per wavefront),
+//   4. writes its f32 partial sums; the next launch reduces them in a fixed order (the down launch rebuilds h from
+//      the gate/up partials, the combine kernel sums the down partials with the routing weights, the split
+//      reduction finishes a matvec).
 // Results are therefore deterministic: no float atomics, every sum in a fixed order.
 #pragma once
+#include "cb3_tiles.h"
 #include "formats.h"
 
 namespace mi {
@@ -38,26 +38,22 @@ struct KArgs {
     int N, k;
     int shared_expert;
     int S;                     // column splits
-    int n_units;               // column units (CB3: word pairs, IQ3_S: blocks)
-    int RB;                    // row blocks (R / 256)
-    int RBW;                   // row blocks per workgroup (kDown / kMatvec: one per wavefront; kGateUp: 1)
-    int RBG;                   // row-block groups: ceil(RB / RBW)
-    int xs_max;                // LDS dwords per staged row
+    int n_units;               // column units (CB3: 160-column tiles, IQ3_S: 256-column blocks)
+    int RB;                    // row groups of a matrix (R / rows per wavefront)
+    int RBW;                   // row groups per workgroup (kDown / kMatvec: 4, kGateUp: 2)
+    int RBG;                   // workgroup row ranges: ceil(RB / RBW)
+    int xs_max;                // LDS row pitch in dwords (largest over the splits)
     int t_rows;                // LDS rows staged (class of the largest group)
     // activations
     const uint16_t *x_bf16;    // kGateUp: [N, K] tokens; kMatvec bf16: [n_slots, stride]
     const float *x_f32;        // kMatvec f32 activations [n_slots, stride]
     int x_stride;
     const int32_t *idx;
-    const float *w;
     float limit;
-    // outputs / workspace
-    float *part;               // [S * nmat * NS * R] partial sums written by this launch
+    // partial sums
+    float *part;               // [S * nmat * NS * R] written by this launch
     const float *p1;           // kDown: the gate/up launch's partials [S1 * 2 * NS * K] (h is rebuilt from them)
     int S1;                    // kDown: column splits of the gate/up launch
-    uint32_t *cnt;             // completion counters
-    float *out_f32;            // kDown: [N, R]; kMatvec: [n_slots, R]
-    uint16_t *out_bf16;        // kDown: [N, R] (optional)
     int NS;                    // slots incl. shared
 };
 
@@ -67,33 +63,18 @@ __host__ __device__ inline int slot_token(int slot, int n_route, int k) {
 
 // `stage` stages the activation rows into LDS (ending in a workgroup barrier); the decoders call it right after
 // issuing their first weight loads, so the staging latency overlaps the first HBM round trip.
-template <int QT, int TC, bool HILO, class Stage>
-__device__ __forceinline__ void accum_rows(const Table &tb, int e, int r0, int u0, int u1, int c0,
-                                           const uint32_t *grid, const uint32_t *xh, const uint32_t *xl, int xs,
-                                           float (&acc)[4][TC], Stage &&stage) {
-    if constexpr (QT == MI_QT_CB3) {
-        // units are 640-column super-tiles; 1-2 activation rows take the static straight-line tile path
-        if constexpr (TC <= 2) cb3_accum_tiles<TC, HILO>(tb.cb3, e, r0, u0, u1, c0, xh, xl, xs, acc, stage);
-        else {
-            const int npairs = (tb.cb3.Wd + 1) / 2;
-            cb3_accum<TC, HILO>(tb.cb3, e, r0, 32 * u0, min(32 * u1, npairs), c0, xh, xl, xs, acc, stage);
-        }
-    } else {
-        iq3_accum<TC, HILO>(tb.iq3, e, r0, u0, u1, c0, grid, xh, xl, xs, acc, stage);
-    }
-}
 
-// Accumulate with the smallest token class >= n (classes above TCMAX are not compiled into the launch) and store the
-// partials of the n real rows.
-template <int QT, bool HILO, int TCMAX, class Stage>
-__device__ __forceinline__ void run_and_store(const Table &tb, int e, int r0, int u0, int u1, int c0, const uint32_t *grid,
-                              const uint32_t *xh, const uint32_t *xl, int xs, int n, const int *slots,
-                              float *part_base, int R, Stage &&stage) {
+// IQ3_S rows (4 per lane, 256 per wavefront): accumulate with the smallest token class >= n (classes above TCMAX
+// are not compiled into the launch) and store the partials of the n real rows.
+template <bool HILO, int TCMAX, class Stage>
+__device__ __forceinline__ void iq3_run_and_store(const Iq3Table &tb, int e, int r0, int u0, int u1, int c0,
+                                                  const uint32_t *grid, const uint32_t *xh, const uint32_t *xl, int xs,
+                                                  int n, const int *slots, float *part_base, int R, Stage &&stage) {
 #define MI_RUN_CLASS(TCV)                                                                          \
     {                                                                                              \
         float acc[4][TCV];                                                                         \
         _Pragma("unroll") for (int i = 0; i < 4; ++i) _Pragma("unroll") for (int t = 0; t < TCV; ++t) acc[i][t] = 0.f; \
-        accum_rows<QT, TCV, HILO>(tb, e, r0, u0, u1, c0, grid, xh, xl, xs, acc, stage);            \
+        iq3_accum<TCV, HILO>(tb, e, r0, u0, u1, c0, grid, xh, xl, xs, acc, stage);                 \
         _Pragma("unroll") for (int t = 0; t < TCV; ++t) {                                          \
             if (t < n) {                                                                           \
                 float4 v = make_float4(acc[0][t], acc[1][t], acc[2][t], acc[3][t]);                \
@@ -109,17 +90,73 @@ __device__ __forceinline__ void run_and_store(const Table &tb, int e, int r0, in
 #undef MI_RUN_CLASS
 }
 
-// Workgroup shape: gate/up = 2 wavefronts (gate, up) over one row block; down / matvec = kRbWaves wavefronts over
-// kRbWaves consecutive row blocks, which share the staged activation slice.
-constexpr int kRbWaves = 4;
+// CB3 rows (64 per wavefront, matrix cores).  B-operand lane (column jt = lane % 16 of the 16x16 tile, k-chunk q):
+//   bf16 activations: token jt;
+//   f32 activations, launches of at most 8 tokens per group: hi part of token jt (jt < 8) or lo part of token jt - 8
+//     (jt >= 8), and the two accumulator columns are added at the end -- one instruction covers hi and lo;
+//   f32 activations, launches of up to 16 tokens per group: hi and lo of token jt, two instructions per k-step.
+// Columns jt >= the staged rows read a clamped row; their accumulator columns are never stored.
+template <bool HILO, int TCMAX, class Stage>
+__device__ __forceinline__ void cb3_run_and_store(const Cb3Table &tb, int e, int rg, int u0, int u1, int c0,
+                                                  const uint32_t *xh, const uint32_t *xl, int xsp, int t_rows, int n,
+                                                  const int *slots, float *part_base, int R, uint4 *cbl,
+                                                  Stage &&stage) {
+    const int lane = threadIdx.x & 63, jt = lane & 15, q = lane >> 4;
+    Cb3Wave w;
+    w.RT = tb.RT;
+    w.G = tb.G;
+    w.CT = tb.CT;
+    w.R = tb.R;
+    w.qt = tb.qs + (size_t)e * tb.CT * tb.RT * 256;
+    w.cbe = tb.cb + (size_t)e * tb.G * tb.R * 4;
+    w.rt0 = rg * kCb3Rtw;
+    w.cta = u0;
+    w.ctb = u1;
+    w.g_last = min((kCb3TileCols * u1 - 1) >> 7, tb.G - 1);
+    w.lane16 = (uint32_t)lane * 16u;
+    w.cbl = cbl;
+    constexpr bool two = HILO && TCMAX > 8;
+    constexpr bool pair = HILO && !two;          // hi / lo in the two halves of the tile's columns
+    int row = pair ? (jt & 7) : jt;
+    row = min(row, t_rows - 1);
+    w.xh = ((pair && jt >= 8) ? xl : xh) + row * xsp + 4 * q;
+    w.xl = xl + row * xsp + 4 * q;
+    f32x4 acc[kCb3Rtw];
+    cb3_accum_mfma<two>(w, acc, stage);
+    if (pair) {
+#pragma unroll
+        for (int r = 0; r < kCb3Rtw; ++r)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[r][i] += __shfl_down(acc[r][i], 8, 16);
+    }
+    if (jt < n) {
+        float *dst = part_base + (size_t)slots[jt] * R + rg * kCb3WaveRows + 4 * q;
+#pragma unroll
+        for (int r = 0; r < kCb3Rtw; ++r) *(float4 *)(dst + 16 * r) = make_float4(acc[r][0], acc[r][1], acc[r][2], acc[r][3]);
+    }
+}
+
+// Workgroups are 4 wavefronts sharing one staged activation slice: gate/up = (gate, up) x 2 row groups, down /
+// matvec = 4 row groups.  A row group is the rows of one wavefront: 64 (CB3) or 256 (IQ3_S).
+constexpr int kWgWaves = 4;
+
+template <int QT>
+__host__ __device__ constexpr int wave_rows() { return QT == MI_QT_CB3 ? kCb3WaveRows : kRowBlock; }
+
+// CB3 kernels are held to 3 wavefronts per SIMD (<= 168 VGPRs): more HBM requests in flight per CU.
+template <int QT>
+__host__ __device__ constexpr int min_waves_per_simd() { return QT == MI_QT_CB3 ? 3 : 1; }
 
 template <int MODE, int QT, int TCMAX>
-__global__ void __launch_bounds__(MODE == kGateUp ? 128 : 64 * kRbWaves) grouped_kernel(KArgs a) {
+__global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) grouped_kernel(KArgs a) {
     extern __shared__ uint32_t xlds[];
     __shared__ GroupScratch sc;
-    __shared__ uint32_t grid[512];
+    __shared__ uint32_t grid[QT == MI_QT_IQ3_S ? 512 : 1];
+    __shared__ uint4 cbl[QT == MI_QT_CB3 ? kWgWaves * 5 * 64 : 1];   // CB3: per-wavefront codebook slots
     __shared__ int s_tok[kMaxT];
 
+    constexpr bool cb3 = QT == MI_QT_CB3;
+    constexpr int WR = wave_rows<QT>();
     const int tid = threadIdx.x;
     const int task = blockIdx.x;
     const int split = task % a.S;
@@ -127,21 +164,24 @@ __global__ void __launch_bounds__(MODE == kGateUp ? 128 : 64 * kRbWaves) grouped
     const int gi = task / (a.S * a.RBG);
 
     find_group(sc, a.idx, a.n_route, a.E, a.shared_expert, a.N, gi, a.t_rows);
-    const int e = sc.g.expert;
+    // LDS values and the wavefront index are wave-uniform: keep them (and every address built from them) scalar
+    const int e = __builtin_amdgcn_readfirstlane(sc.g.expert);
     if (e < 0) return;
-    const int n = sc.g.n;
+    const int n = __builtin_amdgcn_readfirstlane(sc.g.n);
 
-    constexpr bool iq3 = QT == MI_QT_IQ3_S;
-    if (iq3)
+    if constexpr (!cb3)
         for (int i = tid; i < 512; i += blockDim.x) grid[i] = kGridConst[i];
 
-    // column range of the split
-    const int ucols = iq3 ? Iq3Table::kUnitCols : Cb3Table::kUnitCols;
+    // column range of the split; CB3 stages its padded column tiles (columns >= K are zero)
+    const int ucols = cb3 ? Cb3Table::kUnitCols : Iq3Table::kUnitCols;
     const int u0 = (int)((long long)split * a.n_units / a.S);
     const int u1 = (int)((long long)(split + 1) * a.n_units / a.S);
-    const int c0 = u0 * ucols;
-    const int c1 = min(a.K, u1 * ucols);
-    const int xs = (c1 - c0) >> 1;   // dwords per staged row
+    // CB3 stages from the start of the super tile holding the split's first column tile (zeros before it)
+    const int c0 = cb3 ? 4 * kCb3TileCols * (u0 >> 2) : u0 * ucols;
+    const int cv = u0 * ucols;                // first column of the split
+    const int c1 = cb3 ? u1 * ucols : min(a.K, u1 * ucols);
+    const int xs = (c1 - c0) >> 1;            // dwords per staged row
+    const int xsp = cb3 ? xs + 4 : xs;        // row pitch (CB3: skewed so 16 rows spread over the LDS banks)
     const bool hilo = (MODE == kDown) || (MODE == kMatvec && a.x_f32 != nullptr);
     uint32_t *xh = xlds;
     uint32_t *xl = xlds + (size_t)a.t_rows * a.xs_max;
@@ -156,7 +196,7 @@ __global__ void __launch_bounds__(MODE == kGateUp ? 128 : 64 * kRbWaves) grouped
             const int slot = s_tok[t];
             const int c = c0 + 4 * q;
             uint2 hv = make_uint2(0, 0), lv = make_uint2(0, 0);
-            if (slot >= 0) {
+            if (slot >= 0 && c >= cv && c < a.K) {
                 if (!hilo) {
                     const int row = (MODE == kGateUp) ? slot_token(slot, a.n_route, a.k) : slot;
                     hv = *(const uint2 *)(a.x_bf16 + (size_t)row * a.x_stride + c);
@@ -185,108 +225,40 @@ __global__ void __launch_bounds__(MODE == kGateUp ? 128 : 64 * kRbWaves) grouped
                     lv = make_uint2(l0 | (l1 << 16), l2 | (l3 << 16));
                 }
             }
-            *(uint2 *)(xh + t * xs + 2 * q) = hv;
-            if (hilo) *(uint2 *)(xl + t * xs + 2 * q) = lv;
+            *(uint2 *)(xh + t * xsp + 2 * q) = hv;
+            if (hilo) *(uint2 *)(xl + t * xsp + 2 * q) = lv;
         }
         __syncthreads();
     };
 
-    const int wave = tid >> 6, lane = tid & 63;
-    const Table &tb = (MODE == kGateUp && wave == 1) ? a.t1 : a.t0;
-    const int rb = rbg * a.RBW + (MODE == kGateUp ? 0 : wave);
-    if (rb >= a.RB) {           // wavefront past the last row block: it only helps stage
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int mat = MODE == kGateUp ? (wave & 1) : 0;          // gate/up: odd wavefronts run the up matrix
+    const Table &tb = mat ? a.t1 : a.t0;
+    const int rg = rbg * a.RBW + (MODE == kGateUp ? (wave >> 1) : wave);
+    if (rg >= a.RB) {           // wavefront past the last row group: it only helps stage
         stage();
         return;
     }
-    const int r0 = rb * kRowBlock + lane * kRowsPerLane;
     const int nmat = MODE == kGateUp ? 2 : 1;
-    const int mat = MODE == kGateUp ? wave : 0;   // gate/up: wave 0 = gate, wave 1 = up
     float *part_base = a.part + (size_t)(split * nmat + mat) * a.NS * a.R;
-    if (MODE == kDown)
-        run_and_store<QT, true, TCMAX>(tb, e, r0, u0, u1, c0, grid, xh, xl, xs, n, s_tok, part_base, a.R, stage);
-    else if (MODE == kGateUp)
-        run_and_store<QT, false, TCMAX>(tb, e, r0, u0, u1, c0, grid, xh, xl, xs, n, s_tok, part_base, a.R, stage);
-    else if (hilo)
-        run_and_store<QT, true, TCMAX>(tb, e, r0, u0, u1, c0, grid, xh, xl, xs, n, s_tok, part_base, a.R, stage);
-    else
-        run_and_store<QT, false, TCMAX>(tb, e, r0, u0, u1, c0, grid, xh, xl, xs, n, s_tok, part_base, a.R, stage);
-    // gate/up: the partials are reduced by the down launch while it stages h (kernel order publishes them)
-    if (MODE == kGateUp) return;
-    // From here on every wavefront works alone on its own row block (no workgroup barriers).
-    fence_release_agent();   // this wavefront's partial stores, before its completion count
-
-    if (MODE == kMatvec) {
-        // the wavefront completing (group, row block) reduces the splits in order and stores the rows
-        uint32_t *c = a.cnt + gi * a.RB + rb;
-        uint32_t prev = 0;
-        if (lane == 0) prev = counter_add(c, 1u);
-        if (__shfl(prev, 0, kWave) != (uint32_t)(a.S - 1)) return;
-        fence_acquire_agent();
-        for (int t = 0; t < n; ++t) {
-            const int slot = s_tok[t];
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            for (int s = 0; s < a.S; ++s) {
-                const float4 p = *(const float4 *)(a.part + ((size_t)s * a.NS + slot) * a.R + r0);
-                v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
-            }
-            *(float4 *)(a.out_f32 + (size_t)slot * a.R + r0) = v;
-        }
-        if (lane == 0) counter_reset(c);
-        return;
+    if constexpr (cb3) {
+        if (hilo)
+            cb3_run_and_store<true, TCMAX>(tb.cb3, e, rg, u0, u1, c0, xh, xl, xsp, a.t_rows, n, s_tok, part_base, a.R,
+                                           cbl + wave * 5 * 64, stage);
+        else
+            cb3_run_and_store<false, TCMAX>(tb.cb3, e, rg, u0, u1, c0, xh, xl, xsp, a.t_rows, n, s_tok, part_base,
+                                            a.R, cbl + wave * 5 * 64, stage);
+    } else {
+        const int r0 = rg * WR + lane * kRowsPerLane;
+        if (hilo)
+            iq3_run_and_store<true, TCMAX>(tb.iq3, e, r0, u0, u1, c0, grid, xh, xl, xs, n, s_tok, part_base, a.R,
+                                           stage);
+        else
+            iq3_run_and_store<false, TCMAX>(tb.iq3, e, r0, u0, u1, c0, grid, xh, xl, xs, n, s_tok, part_base, a.R,
+                                            stage);
     }
-
-    // kDown: one completion counter per (row block, token); the last contributor combines that token's rows.
-    // lane t < n handles slot t of the group.
-    int mylast = 0, mytok = -1;
-    if (lane < n) {
-        const int slot = s_tok[lane];
-        mytok = slot_token(slot, a.n_route, a.k);
-        int nvalid = 0;
-        for (int j = 0; j < a.k; ++j) {
-            const int ej = a.idx[mytok * a.k + j];
-            nvalid += (ej >= 0 && ej < a.E) ? 1 : 0;
-        }
-        nvalid += a.shared_expert >= 0 ? 1 : 0;
-        const uint32_t target = (uint32_t)(nvalid * a.S);
-        mylast = counter_add(a.cnt + (size_t)rb * a.N + mytok, 1u) == target - 1u;
-    }
-    uint64_t lastmask = __ballot(mylast);
-    if (lastmask) fence_acquire_agent();
-    while (lastmask) {
-        const int t = __builtin_ctzll(lastmask);
-        lastmask &= lastmask - 1;
-        const int tok = __shfl(mytok, t, kWave);
-        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int j = 0; j < a.k; ++j) {
-            const int ej = a.idx[tok * a.k + j];
-            if (ej < 0 || ej >= a.E) continue;
-            const int slot = tok * a.k + j;
-            float4 ys = make_float4(0.f, 0.f, 0.f, 0.f);
-            for (int s = 0; s < a.S; ++s) {
-                const float4 p = *(const float4 *)(a.part + ((size_t)s * a.NS + slot) * a.R + r0);
-                ys.x += p.x; ys.y += p.y; ys.z += p.z; ys.w += p.w;
-            }
-            const float wj = a.w[tok * a.k + j];
-            acc.x += wj * ys.x; acc.y += wj * ys.y; acc.z += wj * ys.z; acc.w += wj * ys.w;
-        }
-        if (a.shared_expert >= 0) {
-            const int slot = a.n_route + tok;
-            float4 ys = make_float4(0.f, 0.f, 0.f, 0.f);
-            for (int s = 0; s < a.S; ++s) {
-                const float4 p = *(const float4 *)(a.part + ((size_t)s * a.NS + slot) * a.R + r0);
-                ys.x += p.x; ys.y += p.y; ys.z += p.z; ys.w += p.w;
-            }
-            acc.x += ys.x; acc.y += ys.y; acc.z += ys.z; acc.w += ys.w;
-        }
-        if (a.out_f32) *(float4 *)(a.out_f32 + (size_t)tok * a.R + r0) = acc;
-        if (a.out_bf16) {
-            uint2 b;
-            b.x = f32_to_bf16_rne(acc.x) | (f32_to_bf16_rne(acc.y) << 16);
-            b.y = f32_to_bf16_rne(acc.z) | (f32_to_bf16_rne(acc.w) << 16);
-            *(uint2 *)(a.out_bf16 + (size_t)tok * a.R + r0) = b;
-        }
-        if (lane == 0) counter_reset(a.cnt + (size_t)rb * a.N + tok);
-    }
+    // The partials are reduced by the next launch (gate/up: the down launch while it stages h; down: the combine;
+    // matvec: the split reduction): kernel order publishes them, so no completion counters or fences are needed.
 }
 
 }  // namespace mi

@@ -21,30 +21,22 @@ __global__ void dequant_kernel(Table tb, int e, float *out) {
     for (int c = c0; c < c0 + 16; ++c) {
         float v;
         if (tb.qtype == MI_QT_CB3) {
+            // tile layout of cb3_tiles.h: column c -> tile ct, k-step m, k-chunk q, position j; code n = 8m + j
             const Cb3Table &t = tb.cb3;
-            const int P = c / 20, o = c % 20;
-            const int w0 = 2 * P;
-            const bool has_u1 = w0 + 1 < t.Wd;
-            const uint32_t a = t.qs[((size_t)e * t.Wd + w0) * Rz + r];
-            const uint32_t b = has_u1 ? t.qs[((size_t)e * t.Wd + w0 + 1) * Rz + r] : 0u;
+            const int ct = c / kCb3TileCols, o = c % kCb3TileCols;
+            const int m = o >> 5, q = (o >> 3) & 3, j = o & 7;
+            const int nn = 8 * m + j, p = nn / 20, cc = nn % 20;
+            const int lane = 16 * q + (r & 15);
+            const uint32_t *wp = t.qs + (((size_t)e * t.CT + ct) * t.RT + (r >> 4)) * 256 + 4 * lane;
+            const uint32_t a = wp[2 * p], b = wp[2 * p + 1];
             uint32_t code;
-            if (!has_u1) {
-                if (o < 4) code = (a >> (8 * o)) & 7u;
-                else if (o < 8) code = (a >> (8 * (o - 4) + 3)) & 7u;
-                else if (o == 8) code = ((a >> 6) & 3u) | (((a >> 22) & 1u) << 2);
-                else code = ((a >> 14) & 3u) | (((a >> 30) & 1u) << 2);
-            } else if (o < 4) code = (a >> (8 * o)) & 7u;
-            else if (o < 8) code = (a >> (8 * (o - 4) + 3)) & 7u;
-            else if (o < 12) code = (b >> (8 * (o - 8))) & 7u;
-            else if (o < 16) code = (b >> (8 * (o - 12) + 3)) & 7u;
-            else {
-                const int j = o - 16;
-                code = ((a >> (8 * j + 6)) & 3u) | (((b >> (8 * j + 6)) & 1u) << 2);
-            }
-            const int g = c >> 7;
-            const size_t cbase = ((size_t)e * t.G + g) * 4;
-            const uint32_t lo = t.cb[(cbase + (code >> 2)) * Rz + r];
-            const uint32_t hi = t.cb[(cbase + 2 + (code >> 2)) * Rz + r];
+            if (cc < 4) code = (a >> (8 * cc)) & 7u;
+            else if (cc < 8) code = (a >> (8 * (cc - 4) + 3)) & 7u;
+            else if (cc < 12) code = (b >> (8 * (cc - 8))) & 7u;
+            else if (cc < 16) code = (b >> (8 * (cc - 12) + 3)) & 7u;
+            else code = ((a >> (8 * (cc - 16) + 6)) & 3u) | (((b >> (8 * (cc - 16) + 6)) & 1u) << 2);
+            const uint32_t *cw = t.cb + (((size_t)e * t.G + (c >> 7)) * t.R + r) * 4;
+            const uint32_t lo = cw[code >> 2], hi = cw[2 + (code >> 2)];
             const uint32_t sh = 8 * (code & 3u);
             v = bf16_to_f32(((lo >> sh) & 255u) | (((hi >> sh) & 255u) << 8));
         } else {
@@ -68,11 +60,69 @@ __global__ void dequant_kernel(Table tb, int e, float *out) {
     }
 }
 
+// ------------------------------------------------------------------------------------------------ finishing kernels
+// Routing-weighted combine of the down partials: out[n] = sum_j w[n, j] * sum_s part[s][n*k + j]  (+ the shared
+// expert's sum_s part[s][n_route + n]), experts in routing order, splits in order.  Invalid ids (outside [0, E))
+// contribute nothing.  One thread per 4 output rows of one token.
+__global__ void combine_kernel(const float *__restrict__ part, int S, int NS, int D, int N, int k,
+                               const int32_t *__restrict__ idx, const float *__restrict__ w, int E, int shared,
+                               int n_route, float *out_f32, uint16_t *out_bf16) {
+    const int q4 = D >> 2;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= N * q4) return;
+    const int tok = i / q4, r = 4 * (i - tok * q4);
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int j = 0; j <= k; ++j) {
+        int slot;
+        float wj;
+        if (j < k) {
+            const int e = idx[tok * k + j];
+            if (e < 0 || e >= E) continue;
+            slot = tok * k + j;
+            wj = w[tok * k + j];
+        } else {
+            if (shared < 0) break;
+            slot = n_route + tok;
+            wj = 1.0f;
+        }
+        float4 ys = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int s = 0; s < S; ++s) {
+            const float4 p = *(const float4 *)(part + ((size_t)s * NS + slot) * D + r);
+            ys.x += p.x; ys.y += p.y; ys.z += p.z; ys.w += p.w;
+        }
+        if (j < k) {
+            acc.x += wj * ys.x; acc.y += wj * ys.y; acc.z += wj * ys.z; acc.w += wj * ys.w;
+        } else {
+            acc.x += ys.x; acc.y += ys.y; acc.z += ys.z; acc.w += ys.w;
+        }
+    }
+    if (out_f32) *(float4 *)(out_f32 + (size_t)tok * D + r) = acc;
+    if (out_bf16) {
+        uint2 b;
+        b.x = f32_to_bf16_rne(acc.x) | (f32_to_bf16_rne(acc.y) << 16);
+        b.y = f32_to_bf16_rne(acc.z) | (f32_to_bf16_rne(acc.w) << 16);
+        *(uint2 *)(out_bf16 + (size_t)tok * D + r) = b;
+    }
+}
+
+// Split reduction of a matvec: out[slot] = sum_s part[s][slot], splits in order.
+__global__ void split_reduce_kernel(const float *__restrict__ part, int S, int NS, int R, float *__restrict__ out) {
+    const size_t n4 = (size_t)NS * R / 4;
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n4) return;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s = 0; s < S; ++s) {
+        const float4 p = ((const float4 *)(part + (size_t)s * NS * R))[i];
+        v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
+    }
+    ((float4 *)out)[i] = v;
+}
+
 // ------------------------------------------------------------------------------------------------ host side
 static int validate_table(const mi_table *t) {
     if (!t) return MI_ERR_NULL;
     if (t->qtype != MI_QT_CB3 && t->qtype != MI_QT_IQ3_S) return MI_ERR_QTYPE;
-    if (t->rows <= 0 || t->rows % kRowBlock) return MI_ERR_SHAPE;
+    if (t->rows <= 0 || t->rows % (t->qtype == MI_QT_CB3 ? kCb3WaveRows : kRowBlock)) return MI_ERR_SHAPE;
     if (t->n_experts <= 0 || t->n_experts > kMaxExperts) return MI_ERR_SHAPE;
     if (t->qtype == MI_QT_CB3) {
         if (t->cols <= 0 || t->cols % 128) return MI_ERR_SHAPE;
@@ -93,7 +143,8 @@ static Table make_table(const mi_table *t) {
         tb.cb3.cb = t->plane[1];
         tb.cb3.R = t->rows;
         tb.cb3.K = t->cols;
-        tb.cb3.Wd = (t->cols + 9) / 10;
+        tb.cb3.CT = (t->cols + kCb3TileCols - 1) / kCb3TileCols;
+        tb.cb3.RT = t->rows / 16;
         tb.cb3.G = t->cols / 128;
     } else {
         tb.iq3.qs = t->plane[0];
@@ -109,11 +160,13 @@ static Table make_table(const mi_table *t) {
     return tb;
 }
 
+static int cb3_ct(const mi_table *t) { return (t->cols + kCb3TileCols - 1) / kCb3TileCols; }
 static int n_units_of(const mi_table *t) {
-    if (t->qtype == MI_QT_CB3) return (t->cols + 639) / 640;   // super-tiles
+    if (t->qtype == MI_QT_CB3) return cb3_ct(t);                 // 160-column tiles
     return t->cols / 256;                                        // IQ3_S blocks
 }
-static int unit_cols(const mi_table *t) { return t->qtype == MI_QT_CB3 ? 640 : 256; }
+static int wave_rows_of(const mi_table *t) { return t->qtype == MI_QT_CB3 ? kCb3WaveRows : kRowBlock; }
+static int unit_cols(const mi_table *t) { return t->qtype == MI_QT_CB3 ? kCb3TileCols : 256; }
 
 static int env_int(const char *name, int dflt) {
     const char *v = getenv(name);
@@ -126,28 +179,94 @@ static int class_rows(int max_slots_per_group) {
     return c;
 }
 
-// Largest staged column range (in dwords) of S splits over the table's units.
-static int max_xs(const mi_table *t, int S) {
+// Staging of S splits over the table's units: the largest LDS row pitch (dwords) and the largest number of units a
+// wavefront streams (CB3 streams from the start of the super tile holding its first column tile, with a 4-dword skew
+// on the LDS rows).
+static void split_extent(const mi_table *t, int S, int *xs_max, int *units_max) {
     const int nu = n_units_of(t), uc = unit_cols(t);
-    int best = 0;
+    const bool cb3 = t->qtype == MI_QT_CB3;
+    const int cend = cb3 ? kCb3TileCols * cb3_ct(t) : t->cols;
+    int bx = 0, bu = 0;
     for (int s = 0; s < S; ++s) {
         const int u0 = (int)((long long)s * nu / S), u1 = (int)((long long)(s + 1) * nu / S);
-        const int c1 = u1 * uc < t->cols ? u1 * uc : t->cols;
-        const int xs = (c1 - u0 * uc) / 2;
-        if (xs > best) best = xs;
+        const int ua = cb3 ? 4 * (u0 / 4) : u0;
+        const int c1 = u1 * uc < cend ? u1 * uc : cend;
+        const int xs = (c1 - ua * uc) / 2 + (cb3 ? 4 : 0);
+        if (xs > bx) bx = xs;
+        if (u1 - ua > bu) bu = u1 - ua;
     }
-    return best;
+    if (xs_max) *xs_max = bx;
+    if (units_max) *units_max = bu;
+}
+static int max_xs(const mi_table *t, int S) {
+    int xs = 0;
+    split_extent(t, S, &xs, nullptr);
+    return xs;
 }
 
-// Pick the column split count: enough workgroups to cover the chip (~768 tasks), LDS within the budget.
-// (The target counts wavefronts: one per (group, row block, split) whatever the workgroup shape.)
-static int choose_splits(const mi_table *t, int groups_est, int rows_lds, int bytes_per_col, const char *env) {
+static int cu_count() {
+    static int n = 0;
+    if (n <= 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+    }
+    return n;
+}
+
+#define MI_DECL_OCC(M, Q) int occupancy_grouped_##M##_##Q(int tcmax, size_t lds);
+MI_DECL_OCC(0, 1)
+MI_DECL_OCC(0, 2)
+MI_DECL_OCC(1, 1)
+MI_DECL_OCC(1, 2)
+MI_DECL_OCC(2, 1)
+MI_DECL_OCC(2, 2)
+#undef MI_DECL_OCC
+
+// Resident workgroups per CU of a grouped-kernel launch (the runtime's occupancy for that instance and LDS size;
+// 2 when it cannot be queried), cached per (mode, format, token class, 512-byte LDS bucket).
+static int wgs_per_cu(int mode, int qtype, int tcmax, size_t lds) {
+    static int cache[3][2][5][161];
+    const int qi = qtype == MI_QT_CB3 ? 0 : 1;
+    int ti = 0;
+    while ((1 << ti) < tcmax && ti < 4) ++ti;
+    const size_t bucket = (lds + 511) / 512;
+    int *slot = bucket <= 160 ? &cache[mode][qi][ti][bucket] : nullptr;
+    if (slot && *slot > 0) return *slot;
+    const size_t l = bucket * 512;
+    int n;
+    if (mode == kGateUp) n = (qi ? occupancy_grouped_0_2 : occupancy_grouped_0_1)(tcmax, l);
+    else if (mode == kDown) n = (qi ? occupancy_grouped_1_2 : occupancy_grouped_1_1)(tcmax, l);
+    else n = (qi ? occupancy_grouped_2_2 : occupancy_grouped_2_1)(tcmax, l);
+    if (n <= 0) n = 2;
+    if (slot) *slot = n;
+    return n;
+}
+
+// Pick the column split count S.  A launch has wg_per_split * S workgroups; the runtime's occupancy gives the slots
+// (resident workgroups over the chip), so the workgroups run in ceil(total / slots) rounds of ~(units streamed per
+// split + a fixed cost) each -- minimise that, with the LDS staging of a split within 48 KB.
+static int choose_splits(const mi_table *t, int mode, int tcmax, int wg_per_split, int rows_lds, int bytes_per_col,
+                         const char *env) {
     const int nu = n_units_of(t);
-    const int RB = t->rows / kRowBlock;
-    int S = (768 + groups_est * RB / 2) / (groups_est * RB > 0 ? groups_est * RB : 1);
-    if (S < 1) S = 1;
-    if (S > nu) S = nu;
-    while (S < nu && (long long)max_xs(t, S) * 2 * bytes_per_col * rows_lds > 48 * 1024) ++S;
+    const double fixed = 2.0;          // per-task cost (first loads, staging, partial stores) in column units
+    int S = 1;
+    double best = 1e30;
+    for (int s = 1; s <= nu; ++s) {
+        int xs, units;
+        split_extent(t, s, &xs, &units);
+        const size_t lds = (size_t)xs * bytes_per_col * rows_lds;
+        if (lds > 48 * 1024) continue;
+        const long long slots = (long long)wgs_per_cu(mode, t->qtype, tcmax, lds) * cu_count();
+        const long long tot = (long long)wg_per_split * s;
+        const long long rounds = (tot + slots - 1) / slots;
+        const double cost = (double)rounds * (units + fixed);
+        if (cost < best - 1e-9) {
+            best = cost;
+            S = s;
+        }
+    }
     S = env_int(env, S);
     if (S < 1) S = 1;
     if (S > nu) S = nu;
@@ -155,8 +274,8 @@ static int choose_splits(const mi_table *t, int groups_est, int rows_lds, int by
 }
 
 struct DecodePlan {
-    int G, S1, S2, rows1, rows2, NS, RB1, RB2, RBG2;
-    size_t off_cnt2, off_part1, off_part2, total;
+    int G, S1, S2, rows1, rows2, NS, RB1, RB2, RBG1, RBG2;
+    size_t off_part1, off_part2, total;
 };
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -170,16 +289,15 @@ static DecodePlan plan_decode(const mi_table *gate, const mi_table *down, int N,
     p.rows2 = p.rows1;
     p.G = max_groups(n_route, gate->n_experts, N, shared, p.rows1);
     p.NS = n_route + (shared >= 0 ? N : 0);
-    p.RB1 = gate->rows / kRowBlock;
-    p.RB2 = down->rows / kRowBlock;
-    p.RBG2 = (p.RB2 + kRbWaves - 1) / kRbWaves;
+    p.RB1 = gate->rows / wave_rows_of(gate);
+    p.RB2 = down->rows / wave_rows_of(down);
+    p.RBG1 = (p.RB1 + 1) / 2;
+    p.RBG2 = (p.RB2 + kWgWaves - 1) / kWgWaves;
     int est = N == 1 ? p.G : (p.G * 6 + 5) / 10;
     if (est < 1) est = 1;
-    p.S1 = choose_splits(gate, est, p.rows1, 2, "MI355MOE_S1");
-    p.S2 = choose_splits(down, est, p.rows2, 4, "MI355MOE_S2");
+    p.S1 = choose_splits(gate, kGateUp, p.rows1, est * p.RBG1, p.rows1, 4, "MI355MOE_S1");
+    p.S2 = choose_splits(down, kDown, p.rows2, est * p.RBG2, p.rows2, 8, "MI355MOE_S2");
     size_t off = 0;
-    p.off_cnt2 = off;
-    off = align256(off + sizeof(uint32_t) * (size_t)p.RB2 * N);
     p.off_part1 = off;
     off = align256(off + sizeof(float) * (size_t)p.S1 * 2 * p.NS * gate->rows);
     p.off_part2 = off;
@@ -253,7 +371,6 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
     a.k = k;
     a.shared_expert = shared_expert;
     a.idx = idx;
-    a.w = w;
     a.limit = limit;
     a.NS = p.NS;
 
@@ -265,8 +382,8 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
     a.S = p.S1;
     a.n_units = n_units_of(gate);
     a.RB = p.RB1;
-    a.RBW = 1;
-    a.RBG = p.RB1;
+    a.RBW = 2;
+    a.RBG = p.RBG1;
     a.xs_max = max_xs(gate, p.S1);
     a.t_rows = p.rows1;
     a.x_bf16 = x_bf16;
@@ -275,13 +392,13 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
     a.part = (float *)(ws + p.off_part1);
     size_t lds1 = sizeof(uint32_t) * (size_t)a.t_rows * a.xs_max;
     if (phases & 1) {
-        launch_grouped<kGateUp>(gate->qtype, a.t_rows, dim3(p.G * p.RB1 * p.S1), dim3(128), lds1, s, a);
+        launch_grouped<kGateUp>(gate->qtype, a.t_rows, dim3(p.G * p.RBG1 * p.S1), dim3(64 * kWgWaves), lds1, s, a);
         if ((st = launch_status())) return st;
     }
     if (!(phases & 2)) return MI_OK;
 
-    // phase 2: h = SwiGLU(sum of the phase-1 partials) staged per split, down + routing-weighted combine (+ shared
-    // expert) -> out [N, D].  Stream order makes the phase-1 partials visible to this launch.
+    // phase 2: h = SwiGLU(sum of the phase-1 partials) staged per split, down -> split partials [S2, NS, D]; then the
+    // routing-weighted combine (+ shared expert) -> out [N, D].  Stream order publishes each launch's partials.
     KArgs b = a;
     b.t0 = make_table(down);
     b.t1 = b.t0;
@@ -290,7 +407,7 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
     b.S = p.S2;
     b.n_units = n_units_of(down);
     b.RB = p.RB2;
-    b.RBW = kRbWaves;
+    b.RBW = kWgWaves;
     b.RBG = p.RBG2;
     b.xs_max = max_xs(down, p.S2);
     b.t_rows = p.rows2;
@@ -300,11 +417,12 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
     b.S1 = p.S1;
     b.x_stride = gate->rows;
     b.part = (float *)(ws + p.off_part2);
-    b.cnt = (uint32_t *)(ws + p.off_cnt2);
-    b.out_f32 = out_f32;
-    b.out_bf16 = out_bf16;
     size_t lds2 = sizeof(uint32_t) * 2 * (size_t)b.t_rows * b.xs_max;
-    launch_grouped<kDown>(down->qtype, b.t_rows, dim3(p.G * p.RBG2 * p.S2), dim3(64 * kRbWaves), lds2, s, b);
+    launch_grouped<kDown>(down->qtype, b.t_rows, dim3(p.G * p.RBG2 * p.S2), dim3(64 * kWgWaves), lds2, s, b);
+    if ((st = launch_status())) return st;
+    const int D = down->rows, nthr = N * (D / 4);
+    hipLaunchKernelGGL(combine_kernel, dim3((nthr + 255) / 256), dim3(256), 0, s, b.part, p.S2, p.NS, D, N, k, idx, w,
+                       gate->n_experts, shared_expert, N * k, out_f32, out_bf16);
     return launch_status();
 }
 
@@ -320,15 +438,17 @@ int mi_moe_decode(const mi_table *gate, const mi_table *up, const mi_table *down
 static int matvec_splits(const mi_table *t, int n_slots) {
     const int rows = class_rows(n_slots < kMaxT ? n_slots : kMaxT);
     const int G = max_groups(n_slots, t->n_experts, 0, -1, rows);
-    return choose_splits(t, G, rows, 4, "MI355MOE_SMV");
+    const int RB = t->rows / wave_rows_of(t);
+    return choose_splits(t, kMatvec, rows, G * ((RB + kWgWaves - 1) / kWgWaves), rows, 8, "MI355MOE_SMV");
 }
 
 size_t mi_matvec_workspace(const mi_table *t, int32_t n_slots) {
     if (validate_table(t) || n_slots <= 0 || n_slots > MI_MAX_SLOTS) return 0;
     const int G = max_groups(n_slots, t->n_experts, 0, -1, class_rows(n_slots < kMaxT ? n_slots : kMaxT));
+    (void)G;
     const int S = matvec_splits(t, n_slots);
-    return align256(sizeof(uint32_t) * (size_t)G * (t->rows / kRowBlock)) +
-           align256(sizeof(float) * (size_t)S * n_slots * t->rows);
+    // one split writes the output directly; more keep their partials here for the split reduction
+    return S == 1 ? 256 : align256(sizeof(float) * (size_t)S * n_slots * t->rows);
 }
 
 int mi_matvec(const mi_table *t, const int32_t *idx, int32_t n_slots, const void *x, int32_t x_dtype,
@@ -343,7 +463,7 @@ int mi_matvec(const mi_table *t, const int32_t *idx, int32_t n_slots, const void
     if (!workspace || workspace_bytes < need) return MI_ERR_WORKSPACE;
     const int rows = class_rows(n_slots < kMaxT ? n_slots : kMaxT);
     const int G = max_groups(n_slots, t->n_experts, 0, -1, rows);
-    const int RB = t->rows / kRowBlock;
+    const int RB = t->rows / wave_rows_of(t);
     const int S = matvec_splits(t, n_slots);
     const int nu = n_units_of(t);
     KArgs a{};
@@ -359,8 +479,8 @@ int mi_matvec(const mi_table *t, const int32_t *idx, int32_t n_slots, const void
     a.S = S;
     a.n_units = nu;
     a.RB = RB;
-    a.RBW = kRbWaves;
-    a.RBG = (RB + kRbWaves - 1) / kRbWaves;
+    a.RBW = kWgWaves;
+    a.RBG = (RB + kWgWaves - 1) / kWgWaves;
     a.xs_max = max_xs(t, S);
     a.t_rows = rows;
     a.x_bf16 = x_dtype == MI_X_BF16 ? (const uint16_t *)x : nullptr;
@@ -368,13 +488,14 @@ int mi_matvec(const mi_table *t, const int32_t *idx, int32_t n_slots, const void
     a.x_stride = x_stride;
     a.idx = idx;
     a.NS = n_slots;
-    char *ws = (char *)workspace;
-    a.cnt = (uint32_t *)ws;
-    a.part = (float *)(ws + align256(sizeof(uint32_t) * (size_t)G * RB));
-    a.out_f32 = out;
+    a.part = S == 1 ? out : (float *)workspace;
     size_t lds = sizeof(uint32_t) * (x_dtype == MI_X_F32 ? 2 : 1) * (size_t)a.t_rows * a.xs_max;
-    launch_grouped<kMatvec>(t->qtype, a.t_rows, dim3(G * a.RBG * S), dim3(64 * kRbWaves), lds, (hipStream_t)stream,
+    launch_grouped<kMatvec>(t->qtype, a.t_rows, dim3(G * a.RBG * S), dim3(64 * kWgWaves), lds, (hipStream_t)stream,
                             a);
+    if ((st = launch_status()) || S == 1) return st;
+    const size_t n4 = (size_t)n_slots * t->rows / 4;
+    hipLaunchKernelGGL(split_reduce_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       a.part, S, n_slots, t->rows, out);
     return launch_status();
 }
 

@@ -3,8 +3,8 @@
 * IQ3_S: GGUF blocks -> the reference's planar tables, unchanged (planes.py:136-170); the kernels read those
   planes directly, so tables packed by the reference's own ``pack_planes`` drop in as they are.
 * CB3 (the benchmark's 3-bit codebook format): canonical rows (10 codes per u32, 8 bf16 centroids per 128-column
-  group) -> planes in the same "matrix row = minor axis" convention, with the code bits rearranged inside each word
-  pair so that the kernel gets byte-sized codebook selectors from one AND.  Same byte count as the canonical form.
+  group) -> 16-row x 160-column code tiles in the lane order of the matrix-core kernels (cb3_tile_words) and a
+  [group][row] codebook plane.  Same bytes per row as the canonical form plus the zero padding of the last tile.
 * int8 (quant8.py:17-18): {"q": int8 [in, out], "s": f32 [1, out]} -> qT int8 [out, in] + s f32 [out].
 """
 import numpy as np
@@ -64,38 +64,39 @@ def cb3_unpack_canonical(words, K):
     return c.reshape(words.shape[:-1] + (words.shape[-1] * 10,))[..., :K].astype(np.uint8)
 
 
-def cb3_device_words(codes):
-    """u8 codes [..., K] -> u32 [..., ceil(K/10)] in the kernel's word layout:
-    pair P (columns c = 20P..20P+19):  word 2P   byte j = code[c+j] | code[c+4+j] << 3 | (code[c+16+j] & 3) << 6
-                                       word 2P+1 byte j = code[c+8+j] | code[c+12+j] << 3 | (code[c+16+j] >> 2) << 6
-    trailing single word (odd count):  byte j = code[c+j] | code[c+4+j] << 3; code[c+8], code[c+9] low 2 bits in
-                                       bits 6-7 of bytes 0, 1 and high bits in bit 6 of bytes 2, 3."""
+CB3_TILE_ROWS = 16
+CB3_TILE_COLS = 160
+
+
+def cb3_tile_count(K):
+    """Column tiles per row (the last one zero-padded past K)."""
+    return -(-K // CB3_TILE_COLS)
+
+
+def cb3_tile_words(codes):
+    """u8 codes [E, R, K] -> u32 [E, CT*RT*256]: the matrix-core tile layout of the CB3 kernels.
+    Tile (ct, rt) = rows 16rt..16rt+15 x columns 160ct..160ct+159, 1 KB, tiles ordered [ct][rt].  Lane l = 16q + i
+    of a tile holds row 16rt + i at columns 160ct + 32m + 8q + j (m = 0..4, j = 0..7) as code n = 8m + j, in 4 words;
+    word pair p (words 2p, 2p+1) holds n = 20p + c, c = 0..19:
+        word 2p   byte b = code[c=b] | code[c=4+b] << 3 | (code[c=16+b] & 3) << 6
+        word 2p+1 byte b = code[c=8+b] | code[c=12+b] << 3 | (code[c=16+b] >> 2) << 6
+    Columns past K hold code 0."""
     codes = np.asarray(codes, dtype=np.uint32)
-    lead, K = codes.shape[:-1], codes.shape[-1]
-    Wd = cb3_words_per_row(K)
-    npair, tail = Wd // 2, Wd % 2
-    c = np.zeros(lead + (20 * npair + 10 * tail,), np.uint32)
+    E, R, K = codes.shape
+    if R % CB3_TILE_ROWS:
+        raise ValueError("CB3 tiles need rows in multiples of 16, got %d" % R)
+    CT, RT = cb3_tile_count(K), R // CB3_TILE_ROWS
+    c = np.zeros((E, R, CT * CB3_TILE_COLS), np.uint32)
     c[..., :K] = codes
-    out = np.zeros(lead + (Wd,), np.uint32)
-    if npair:
-        p = c[..., :20 * npair].reshape(lead + (npair, 20))
-        j = np.arange(4)
-        b0 = p[..., j] | (p[..., 4 + j] << 3) | ((p[..., 16 + j] & 3) << 6)            # [..., npair, 4]
-        b1 = p[..., 8 + j] | (p[..., 12 + j] << 3) | ((p[..., 16 + j] >> 2) << 6)
-        sh = (8 * j).astype(np.uint32)
-        out[..., 0:2 * npair:2] = (b0 << sh).sum(-1, dtype=np.uint64).astype(np.uint32)
-        out[..., 1:2 * npair:2] = (b1 << sh).sum(-1, dtype=np.uint64).astype(np.uint32)
-    if tail:
-        t = c[..., 20 * npair:]
-        j = np.arange(4)
-        b = t[..., j] | (t[..., 4 + j] << 3)
-        c8, c9 = t[..., 8], t[..., 9]
-        b[..., 0] |= (c8 & 3) << 6
-        b[..., 1] |= (c9 & 3) << 6
-        b[..., 2] |= (c8 >> 2) << 6
-        b[..., 3] |= (c9 >> 2) << 6
-        out[..., Wd - 1] = (b << (8 * j).astype(np.uint32)).sum(-1, dtype=np.uint64).astype(np.uint32)
-    return out
+    c = c.reshape(E, RT, 16, CT, 5, 4, 8).transpose(0, 3, 1, 5, 2, 4, 6)    # e, ct, rt, q, i, m, j
+    c = c.reshape(E, CT, RT, 64, 2, 20)                                      # lane = 16q + i; n = 8m + j = 20p + c
+    j = np.arange(4)
+    a = c[..., j] | (c[..., 4 + j] << 3) | ((c[..., 16 + j] & 3) << 6)
+    b = c[..., 8 + j] | (c[..., 12 + j] << 3) | ((c[..., 16 + j] >> 2) << 6)
+    sh = (8 * j).astype(np.uint32)
+    wa = (a << sh).sum(-1, dtype=np.uint64).astype(np.uint32)
+    wb = (b << sh).sum(-1, dtype=np.uint64).astype(np.uint32)
+    return np.stack([wa, wb], axis=-1).reshape(E, CT * RT * 256)
 
 
 def cb3_codebook_words(cb):
@@ -111,7 +112,7 @@ def cb3_codebook_words(cb):
 def cb3_pack_planes(words, cb, K):
     """Canonical CB3 experts -> device planes.
     words u32 [E, R, ceil(K/10)] (canonical), cb u16 [E, R, K/128, 8] (bf16 bits) ->
-    {"qs": u32 [E*Wd, R], "cb": u32 [E*G*4, R]}."""
+    {"qs": u32 [E, CT*RT*256] (cb3_tile_words), "cb": u32 [E, G*R*4] ([group][row][4 dwords])}."""
     words = np.asarray(words, dtype=np.uint32)
     E, R, Wd = words.shape
     if K % CB3_GROUP or Wd != cb3_words_per_row(K):
@@ -120,9 +121,14 @@ def cb3_pack_planes(words, cb, K):
     cb = np.asarray(cb, dtype=np.uint16)
     if cb.shape != (E, R, G, 8):
         raise ValueError("CB3 codebook must be [E, R, K/128, 8], got %s" % (cb.shape,))
-    dev = cb3_device_words(cb3_unpack_canonical(words, K))                   # [E, R, Wd]
-    cbw = cb3_codebook_words(cb).reshape(E, R, G * 4)                        # [E, R, G*4]
-    return {"qs": _expert_major(dev), "cb": _expert_major(cbw)}
+    qs = cb3_tile_words(cb3_unpack_canonical(words, K))
+    cbw = np.ascontiguousarray(cb3_codebook_words(cb).transpose(0, 2, 1, 3)).reshape(E, G * R * 4)
+    return {"qs": qs, "cb": cbw}
+
+
+def cb3_plane_words(R, K):
+    """u32 words per expert of each CB3 device plane."""
+    return {"qs": cb3_tile_count(K) * (R // CB3_TILE_ROWS) * 256, "cb": (K // CB3_GROUP) * R * 4}
 
 
 def cb3_hbm_bytes(R, K):

@@ -13,19 +13,18 @@ import ctypes
 import numpy as np
 import torch
 
-from . import _lib
+from . import _lib, formats
 from ._lib import MiTable, check, lib
 
 QK = 256
 
 
 def _plane_rows(qtype, K):
+    """IQ3_S: rows_p per expert of each plane [E*rows_p, R] (planes.py:62-63)."""
     if qtype == "IQ3_S":
         nblk = K // QK
         W = 16 * nblk
         return {"qs": W, "sg": W // 2, "qh": W // 8, "sc": W // 16, "d": (nblk + 1) // 2}
-    if qtype == "CB3":
-        return {"qs": -(-K // 10), "cb": 4 * (K // 128)}
     raise ValueError(qtype)                     # the reference raises ValueError on an unknown qtype (planes.py:70)
 
 
@@ -50,22 +49,39 @@ class ExpertTable:
             raise ValueError("unsupported qtype %r" % (qtype,))
         self.qtype, self.rows, self.cols = qtype, int(rows), int(cols)
         keys = _lib.PLANE_KEYS[qtype]
-        rp = _plane_rows(qtype, cols)
         self.planes = {}
         for k in keys:
             a = planes[k]
-            if a.dim() == 3:                       # the reference's leading chip axis [1, E*rows_p, R]
-                if a.shape[0] != 1:
-                    raise ValueError("one device holds the full expert set: leading axis must be 1")
-                a = a[0]
             if a.dtype not in (torch.int32, torch.uint32) or not a.is_cuda:
                 raise ValueError("plane %r must be a 32-bit integer tensor on the GPU" % k)
-            if a.shape[-1] != self.rows or a.shape[0] % rp[k]:
-                raise ValueError("plane %r has shape %s, expected [E*%d, %d]" % (k, tuple(a.shape), rp[k], self.rows))
-            self.planes[k] = a.contiguous()
-        self.n_experts = self.planes["qs"].shape[0] // rp["qs"]
+        if qtype == "CB3":
+            # tile planes (formats.cb3_pack_planes): [E, words] or flat, whole experts
+            pw = formats.cb3_plane_words(self.rows, self.cols)
+            if self.rows % 64:
+                raise ValueError("CB3 tables need rows in multiples of 64, got %d" % self.rows)
+            for k in keys:
+                a = planes[k].contiguous().reshape(-1)
+                if a.numel() % pw[k]:
+                    raise ValueError("plane %r has %d words, not whole experts of %d" % (k, a.numel(), pw[k]))
+                self.planes[k] = a
+            self.n_experts = self.planes["qs"].numel() // pw["qs"]
+            per = {k: pw[k] for k in keys}
+        else:
+            rp = _plane_rows(qtype, cols)
+            for k in keys:
+                a = planes[k]
+                if a.dim() == 3:                       # the reference's leading chip axis [1, E*rows_p, R]
+                    if a.shape[0] != 1:
+                        raise ValueError("one device holds the full expert set: leading axis must be 1")
+                    a = a[0]
+                if a.shape[-1] != self.rows or a.shape[0] % rp[k]:
+                    raise ValueError("plane %r has shape %s, expected [E*%d, %d]" % (k, tuple(a.shape), rp[k],
+                                                                                     self.rows))
+                self.planes[k] = a.contiguous()
+            self.n_experts = self.planes["qs"].shape[0] // rp["qs"]
+            per = {k: rp[k] * self.rows for k in keys}
         for k in keys:
-            if self.planes[k].shape[0] != self.n_experts * rp[k]:
+            if self.planes[k].numel() != self.n_experts * per[k]:
                 raise ValueError("plane %r does not hold %d experts" % (k, self.n_experts))
         self._c = MiTable()
         self._c.qtype = _lib.QTYPES[qtype]

@@ -62,41 +62,3 @@ def dequant(codes, cb):
 
 def hbm_bytes(R, K):
     return R * (4 * words_per_row(K) + 16 * (K // GROUP))
-
-
-def decode_device_words(dev, K):
-    """Codes from the kernel's word layout (an independent per-column restatement used to pin the packer):
-    column c = 20P + o of a word pair (words 2P, 2P+1 = a, b):
-      o < 4: a byte o bits 0-2;  o < 8: a byte o-4 bits 3-5;  o < 12: b byte o-8 bits 0-2;  o < 16: b byte o-12 bits 3-5;
-      o >= 16 (j = o-16): (a byte j bits 6-7) | (b byte j bit 6) << 2.
-    A trailing single word a (odd word count): o < 8 as above, o = 8: a bits 6-7 | a bit 22 << 2, o = 9: a bits
-    14-15 | a bit 30 << 2."""
-    dev = np.asarray(dev, dtype=np.uint32)
-    N, Wd = dev.shape
-    out = np.zeros((N, K), np.uint8)
-    for c in range(K):
-        P, o = divmod(c, 20)
-        a = dev[:, 2 * P]
-        single = 2 * P + 1 >= Wd
-        b = dev[:, 2 * P + 1] if not single else None
-        byte = lambda v, j: (v >> (8 * j)) & 255
-        if o < 4:
-            v = byte(a, o) & 7
-        elif o < 8:
-            v = (byte(a, o - 4) >> 3) & 7
-        elif single:
-            if o == 8:
-                v = ((a >> 6) & 3) | (((a >> 22) & 1) << 2)
-            elif o == 9:
-                v = ((a >> 14) & 3) | (((a >> 30) & 1) << 2)
-            else:
-                raise ValueError("column beyond the last word")
-        elif o < 12:
-            v = byte(b, o - 8) & 7
-        elif o < 16:
-            v = (byte(b, o - 12) >> 3) & 7
-        else:
-            j = o - 16
-            v = ((byte(a, j) >> 6) & 3) | (((byte(b, j) >> 6) & 1) << 2)
-        out[:, c] = v
-    return out
