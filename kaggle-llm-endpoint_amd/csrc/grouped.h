@@ -3,11 +3,11 @@
 // One launch covers every (expert group, row range, column split) task of a call.  A workgroup of 4 wavefronts
 //   1. regroups the call's routing on the device (find_group: slots sorted by expert, <= 16 slots per group),
 //   2. issues its first weight loads, then stages the group's activation rows for its column split in LDS while
-//      they are in flight (the down projection rebuilds h = SwiGLU(gate, up) here from the gate/up partials),
+//      they are in flight (f32 activations -- h for the down projection -- as bf16 hi + lo parts),
 //   3. streams the expert's planes once with 128-bit loads (every wavefront load is 1 KB contiguous) and decodes
 //      the codes to bf16 in registers: CB3 tiles feed the matrix cores (64 rows per wavefront, all of the group's
 //      tokens in one 16-column tile), IQ3_S rows feed bf16-pair dot products (256 rows per wavefront),
-//   4. writes its f32 partial sums; the next launch reduces them in a fixed order (the down launch rebuilds h from
+//   4. writes its f32 partial sums; the next launch reduces them in a fixed order (the SwiGLU kernel forms h from
 //      the gate/up partials, the combine kernel sums the down partials with the routing weights, the split
 //      reduction finishes a matvec).
 // Results are therefore deterministic: no float atomics, every sum in a fixed order.
@@ -46,14 +46,11 @@ struct KArgs {
     int t_rows;                // LDS rows staged (class of the largest group)
     // activations
     const uint16_t *x_bf16;    // kGateUp: [N, K] tokens; kMatvec bf16: [n_slots, stride]
-    const float *x_f32;        // kMatvec f32 activations [n_slots, stride]
+    const float *x_f32;        // kDown: h [NS, stride] by slot; kMatvec f32: [n_slots, stride]
     int x_stride;
     const int32_t *idx;
-    float limit;
     // partial sums
     float *part;               // [S * nmat * NS * R] written by this launch
-    const float *p1;           // kDown: the gate/up launch's partials [S1 * 2 * NS * K] (h is rebuilt from them)
-    int S1;                    // kDown: column splits of the gate/up launch
     int NS;                    // slots incl. shared
 };
 
@@ -201,21 +198,7 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
                     const int row = (MODE == kGateUp) ? slot_token(slot, a.n_route, a.k) : slot;
                     hv = *(const uint2 *)(a.x_bf16 + (size_t)row * a.x_stride + c);
                 } else {
-                    float4 f;
-                    if (MODE == kDown) {
-                        // h = silu(min(g, L)) * clip(u, -L, L) of the gate/up partials, splits summed in order
-                        float4 g = make_float4(0.f, 0.f, 0.f, 0.f), u = g;
-                        for (int s1 = 0; s1 < a.S1; ++s1) {
-                            const float4 pg = *(const float4 *)(a.p1 + ((size_t)(s1 * 2 + 0) * a.NS + slot) * a.K + c);
-                            const float4 pu = *(const float4 *)(a.p1 + ((size_t)(s1 * 2 + 1) * a.NS + slot) * a.K + c);
-                            g.x += pg.x; g.y += pg.y; g.z += pg.z; g.w += pg.w;
-                            u.x += pu.x; u.y += pu.y; u.z += pu.z; u.w += pu.w;
-                        }
-                        f = make_float4(swiglu_clamped(g.x, u.x, a.limit), swiglu_clamped(g.y, u.y, a.limit),
-                                        swiglu_clamped(g.z, u.z, a.limit), swiglu_clamped(g.w, u.w, a.limit));
-                    } else {
-                        f = *(const float4 *)(a.x_f32 + (size_t)slot * a.x_stride + c);
-                    }
+                    const float4 f = *(const float4 *)(a.x_f32 + (size_t)slot * a.x_stride + c);
                     uint32_t h0, l0, h1, l1, h2, l2, h3, l3;
                     split_bf16(f.x, h0, l0);
                     split_bf16(f.y, h1, l1);
@@ -257,8 +240,8 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
             iq3_run_and_store<false, TCMAX>(tb.iq3, e, r0, u0, u1, c0, grid, xh, xl, xs, n, s_tok, part_base, a.R,
                                             stage);
     }
-    // The partials are reduced by the next launch (gate/up: the down launch while it stages h; down: the combine;
-    // matvec: the split reduction): kernel order publishes them, so no completion counters or fences are needed.
+    // The partials are reduced by the next launch (gate/up: the SwiGLU kernel; down: the combine; matvec: the split
+    // reduction): kernel order publishes them, so no completion counters or fences are needed.
 }
 
 }  // namespace mi

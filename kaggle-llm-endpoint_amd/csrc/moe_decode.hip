@@ -105,6 +105,23 @@ __global__ void combine_kernel(const float *__restrict__ part, int S, int NS, in
     }
 }
 
+// h = silu(min(g, L)) * clip(u, -L, L) (model.py:119-122) of the gate/up split partials, splits summed in order:
+// h[slot][c] from p1[s][0 = gate | 1 = up][slot][c].  One thread per 4 columns of one slot.
+__global__ void swiglu_kernel(const float *__restrict__ p1, int S1, int NS, int I, float limit, float *__restrict__ h) {
+    const size_t n4 = (size_t)NS * I / 4;
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n4) return;
+    float4 g = make_float4(0.f, 0.f, 0.f, 0.f), u = g;
+    for (int s = 0; s < S1; ++s) {
+        const float4 pg = ((const float4 *)(p1 + (size_t)(2 * s) * NS * I))[i];
+        const float4 pu = ((const float4 *)(p1 + (size_t)(2 * s + 1) * NS * I))[i];
+        g.x += pg.x; g.y += pg.y; g.z += pg.z; g.w += pg.w;
+        u.x += pu.x; u.y += pu.y; u.z += pu.z; u.w += pu.w;
+    }
+    ((float4 *)h)[i] = make_float4(swiglu_clamped(g.x, u.x, limit), swiglu_clamped(g.y, u.y, limit),
+                                   swiglu_clamped(g.z, u.z, limit), swiglu_clamped(g.w, u.w, limit));
+}
+
 // Split reduction of a matvec: out[slot] = sum_s part[s][slot], splits in order.
 __global__ void split_reduce_kernel(const float *__restrict__ part, int S, int NS, int R, float *__restrict__ out) {
     const size_t n4 = (size_t)NS * R / 4;
@@ -275,7 +292,7 @@ static int choose_splits(const mi_table *t, int mode, int tcmax, int wg_per_spli
 
 struct DecodePlan {
     int G, S1, S2, rows1, rows2, NS, RB1, RB2, RBG1, RBG2;
-    size_t off_part1, off_part2, total;
+    size_t off_part1, off_h, off_part2, total;
 };
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -300,6 +317,8 @@ static DecodePlan plan_decode(const mi_table *gate, const mi_table *down, int N,
     size_t off = 0;
     p.off_part1 = off;
     off = align256(off + sizeof(float) * (size_t)p.S1 * 2 * p.NS * gate->rows);
+    p.off_h = off;
+    off = align256(off + sizeof(float) * (size_t)p.NS * gate->rows);
     p.off_part2 = off;
     off = align256(off + sizeof(float) * (size_t)p.S2 * p.NS * down->rows);
     p.total = off;
@@ -371,7 +390,6 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
     a.k = k;
     a.shared_expert = shared_expert;
     a.idx = idx;
-    a.limit = limit;
     a.NS = p.NS;
 
     // phase 1: gate + up -> split-K partials [S1, 2, NS, I]
@@ -397,8 +415,15 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
     }
     if (!(phases & 2)) return MI_OK;
 
-    // phase 2: h = SwiGLU(sum of the phase-1 partials) staged per split, down -> split partials [S2, NS, D]; then the
-    // routing-weighted combine (+ shared expert) -> out [N, D].  Stream order publishes each launch's partials.
+    // phase 2: h = SwiGLU(sum of the phase-1 partials) [NS, I]; down -> split partials [S2, NS, D]; the
+    // routing-weighted combine (+ shared expert) -> out [N, D].  Stream order publishes each launch's results.
+    float *h = (float *)(ws + p.off_h);
+    {
+        const size_t n4 = (size_t)p.NS * gate->rows / 4;
+        hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s,
+                           (const float *)(ws + p.off_part1), p.S1, p.NS, gate->rows, limit, h);
+        if ((st = launch_status())) return st;
+    }
     KArgs b = a;
     b.t0 = make_table(down);
     b.t1 = b.t0;
@@ -412,9 +437,7 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
     b.xs_max = max_xs(down, p.S2);
     b.t_rows = p.rows2;
     b.x_bf16 = nullptr;
-    b.x_f32 = nullptr;
-    b.p1 = (const float *)(ws + p.off_part1);
-    b.S1 = p.S1;
+    b.x_f32 = h;
     b.x_stride = gate->rows;
     b.part = (float *)(ws + p.off_part2);
     size_t lds2 = sizeof(uint32_t) * 2 * (size_t)b.t_rows * b.xs_max;
