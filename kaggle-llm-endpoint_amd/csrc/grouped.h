@@ -38,6 +38,7 @@ struct KArgs {
     int N, k;
     int shared_expert;
     int S;                     // column splits
+    int ualign;                // split boundaries at multiples of this many units
     int n_units;               // column units (CB3: 160-column tiles, IQ3_S: 256-column blocks)
     int RB;                    // row groups of a matrix (R / rows per wavefront)
     int RBW;                   // row groups per workgroup (kDown / kMatvec: 4, kGateUp: 2)
@@ -171,8 +172,9 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
 
     // column range of the split; CB3 stages its padded column tiles (columns >= K are zero)
     const int ucols = cb3 ? Cb3Table::kUnitCols : Iq3Table::kUnitCols;
-    const int u0 = (int)((long long)split * a.n_units / a.S);
-    const int u1 = (int)((long long)(split + 1) * a.n_units / a.S);
+    const int nb = (a.n_units + a.ualign - 1) / a.ualign;
+    const int u0 = min(a.n_units, a.ualign * (int)((long long)split * nb / a.S));
+    const int u1 = min(a.n_units, a.ualign * (int)((long long)(split + 1) * nb / a.S));
     // CB3 stages from the start of the super tile holding the split's first column tile (zeros before it)
     const int c0 = cb3 ? 4 * kCb3TileCols * (u0 >> 2) : u0 * ucols;
     const int cv = u0 * ucols;                // first column of the split

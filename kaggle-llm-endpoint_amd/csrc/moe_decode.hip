@@ -63,37 +63,61 @@ __global__ void dequant_kernel(Table tb, int e, float *out) {
 // ------------------------------------------------------------------------------------------------ finishing kernels
 // Routing-weighted combine of the down partials: out[n] = sum_j w[n, j] * sum_s part[s][n*k + j]  (+ the shared
 // expert's sum_s part[s][n_route + n]), experts in routing order, splits in order.  Invalid ids (outside [0, E))
-// contribute nothing.  One thread per 4 output rows of one token.
-__global__ void combine_kernel(const float *__restrict__ part, int S, int NS, int D, int N, int k,
-                               const int32_t *__restrict__ idx, const float *__restrict__ w, int E, int shared,
-                               int n_route, float *out_f32, uint16_t *out_bf16) {
+// contribute nothing.  One thread per 4 output rows of one token; the contributing slots are listed first so every
+// partial load of a chunk of experts is issued before the first add (the loads are independent).
+constexpr int kCombineChunk = 9;
+__global__ void __launch_bounds__(64) combine_kernel(const float *__restrict__ part, int S, int NS, int D, int N,
+                                                     int k, const int32_t *__restrict__ idx,
+                                                     const float *__restrict__ w, int E, int shared, int n_route,
+                                                     float *out_f32, uint16_t *out_bf16) {
     const int q4 = D >> 2;
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= N * q4) return;
     const int tok = i / q4, r = 4 * (i - tok * q4);
+    const int nj = k + (shared >= 0 ? 1 : 0);
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int j = 0; j <= k; ++j) {
-        int slot;
-        float wj;
-        if (j < k) {
-            const int e = idx[tok * k + j];
-            if (e < 0 || e >= E) continue;
-            slot = tok * k + j;
-            wj = w[tok * k + j];
-        } else {
-            if (shared < 0) break;
-            slot = n_route + tok;
-            wj = 1.0f;
+    for (int j0 = 0; j0 < nj; j0 += kCombineChunk) {
+        int slot[kCombineChunk];
+        float wt[kCombineChunk];
+#pragma unroll
+        for (int jj = 0; jj < kCombineChunk; ++jj) {
+            const int j = j0 + jj;
+            slot[jj] = -1;
+            wt[jj] = 0.f;
+            if (j < k) {
+                const int e = idx[tok * k + j];
+                if (e >= 0 && e < E) {
+                    slot[jj] = tok * k + j;
+                    wt[jj] = w[tok * k + j];
+                }
+            } else if (j < nj) {
+                slot[jj] = n_route + tok;
+                wt[jj] = 1.0f;
+            }
         }
-        float4 ys = make_float4(0.f, 0.f, 0.f, 0.f);
+        float4 ys[kCombineChunk];
+#pragma unroll
+        for (int jj = 0; jj < kCombineChunk; ++jj) ys[jj] = make_float4(0.f, 0.f, 0.f, 0.f);
         for (int s = 0; s < S; ++s) {
-            const float4 p = *(const float4 *)(part + ((size_t)s * NS + slot) * D + r);
-            ys.x += p.x; ys.y += p.y; ys.z += p.z; ys.w += p.w;
+            float4 p[kCombineChunk];
+#pragma unroll
+            for (int jj = 0; jj < kCombineChunk; ++jj)
+                p[jj] = slot[jj] >= 0 ? *(const float4 *)(part + ((size_t)s * NS + slot[jj]) * D + r)
+                                      : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int jj = 0; jj < kCombineChunk; ++jj) {
+                ys[jj].x += p[jj].x; ys[jj].y += p[jj].y; ys[jj].z += p[jj].z; ys[jj].w += p[jj].w;
+            }
         }
-        if (j < k) {
-            acc.x += wj * ys.x; acc.y += wj * ys.y; acc.z += wj * ys.z; acc.w += wj * ys.w;
-        } else {
-            acc.x += ys.x; acc.y += ys.y; acc.z += ys.z; acc.w += ys.w;
+#pragma unroll
+        for (int jj = 0; jj < kCombineChunk; ++jj) {
+            if (slot[jj] < 0) continue;
+            if (j0 + jj < k) {
+                acc.x += wt[jj] * ys[jj].x; acc.y += wt[jj] * ys[jj].y;
+                acc.z += wt[jj] * ys[jj].z; acc.w += wt[jj] * ys[jj].w;
+            } else {
+                acc.x += ys[jj].x; acc.y += ys[jj].y; acc.z += ys[jj].z; acc.w += ys[jj].w;
+            }
         }
     }
     if (out_f32) *(float4 *)(out_f32 + (size_t)tok * D + r) = acc;
@@ -107,11 +131,13 @@ __global__ void combine_kernel(const float *__restrict__ part, int S, int NS, in
 
 // h = silu(min(g, L)) * clip(u, -L, L) (model.py:119-122) of the gate/up split partials, splits summed in order:
 // h[slot][c] from p1[s][0 = gate | 1 = up][slot][c].  One thread per 4 columns of one slot.
-__global__ void swiglu_kernel(const float *__restrict__ p1, int S1, int NS, int I, float limit, float *__restrict__ h) {
+__global__ void __launch_bounds__(64) swiglu_kernel(const float *__restrict__ p1, int S1, int NS, int I, float limit,
+                                                    float *__restrict__ h) {
     const size_t n4 = (size_t)NS * I / 4;
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n4) return;
     float4 g = make_float4(0.f, 0.f, 0.f, 0.f), u = g;
+#pragma unroll 4
     for (int s = 0; s < S1; ++s) {
         const float4 pg = ((const float4 *)(p1 + (size_t)(2 * s) * NS * I))[i];
         const float4 pu = ((const float4 *)(p1 + (size_t)(2 * s + 1) * NS * I))[i];
@@ -196,16 +222,26 @@ static int class_rows(int max_slots_per_group) {
     return c;
 }
 
+// Split s of S over nu units: [u0, u1), boundaries at multiples of `align` units (CB3: align 4 = whole super tiles,
+// so no split streams lead-in column tiles).  The grouped kernel computes the same bounds.
+static void split_bounds(int nu, int S, int align, int s, int *u0, int *u1) {
+    const int nb = (nu + align - 1) / align;
+    const int a = align * (int)((long long)s * nb / S), b = align * (int)((long long)(s + 1) * nb / S);
+    *u0 = a < nu ? a : nu;
+    *u1 = b < nu ? b : nu;
+}
+
 // Staging of S splits over the table's units: the largest LDS row pitch (dwords) and the largest number of units a
 // wavefront streams (CB3 streams from the start of the super tile holding its first column tile, with a 4-dword skew
 // on the LDS rows).
-static void split_extent(const mi_table *t, int S, int *xs_max, int *units_max) {
+static void split_extent(const mi_table *t, int S, int align, int *xs_max, int *units_max) {
     const int nu = n_units_of(t), uc = unit_cols(t);
     const bool cb3 = t->qtype == MI_QT_CB3;
     const int cend = cb3 ? kCb3TileCols * cb3_ct(t) : t->cols;
     int bx = 0, bu = 0;
     for (int s = 0; s < S; ++s) {
-        const int u0 = (int)((long long)s * nu / S), u1 = (int)((long long)(s + 1) * nu / S);
+        int u0, u1;
+        split_bounds(nu, S, align, s, &u0, &u1);
         const int ua = cb3 ? 4 * (u0 / 4) : u0;
         const int c1 = u1 * uc < cend ? u1 * uc : cend;
         const int xs = (c1 - ua * uc) / 2 + (cb3 ? 4 : 0);
@@ -215,9 +251,12 @@ static void split_extent(const mi_table *t, int S, int *xs_max, int *units_max) 
     if (xs_max) *xs_max = bx;
     if (units_max) *units_max = bu;
 }
-static int max_xs(const mi_table *t, int S) {
+struct Split {
+    int S, align;
+};
+static int max_xs(const mi_table *t, Split sp) {
     int xs = 0;
-    split_extent(t, S, &xs, nullptr);
+    split_extent(t, sp.S, sp.align, &xs, nullptr);
     return xs;
 }
 
@@ -261,37 +300,43 @@ static int wgs_per_cu(int mode, int qtype, int tcmax, size_t lds) {
     return n;
 }
 
-// Pick the column split count S.  A launch has wg_per_split * S workgroups; the runtime's occupancy gives the slots
+// Pick the column splits.  A launch has wg_per_split * S workgroups; the runtime's occupancy gives the slots
 // (resident workgroups over the chip), so the workgroups run in ceil(total / slots) rounds of ~(units streamed per
-// split + a fixed cost) each -- minimise that, with the LDS staging of a split within 48 KB.
-static int choose_splits(const mi_table *t, int mode, int tcmax, int wg_per_split, int rows_lds, int bytes_per_col,
-                         const char *env) {
+// split + a fixed cost) each -- minimise that over S and the boundary alignment (CB3: column tiles, or whole super
+// tiles), with the LDS staging of a split within 48 KB.
+static Split choose_splits(const mi_table *t, int mode, int tcmax, int wg_per_split, int rows_lds, int bytes_per_col,
+                           const char *env) {
     const int nu = n_units_of(t);
     const double fixed = 2.0;          // per-task cost (first loads, staging, partial stores) in column units
-    int S = 1;
+    Split best_sp{1, 1};
     double best = 1e30;
-    for (int s = 1; s <= nu; ++s) {
-        int xs, units;
-        split_extent(t, s, &xs, &units);
-        const size_t lds = (size_t)xs * bytes_per_col * rows_lds;
-        if (lds > 48 * 1024) continue;
-        const long long slots = (long long)wgs_per_cu(mode, t->qtype, tcmax, lds) * cu_count();
-        const long long tot = (long long)wg_per_split * s;
-        const long long rounds = (tot + slots - 1) / slots;
-        const double cost = (double)rounds * (units + fixed);
-        if (cost < best - 1e-9) {
-            best = cost;
-            S = s;
+    const int aligns[2] = {t->qtype == MI_QT_CB3 ? 4 : 1, 1};
+    for (int ai = 0; ai < 2; ++ai) {
+        const int align = aligns[ai];
+        const int nb = (nu + align - 1) / align;
+        for (int s = 1; s <= nb; ++s) {
+            int xs, units;
+            split_extent(t, s, align, &xs, &units);
+            const size_t lds = (size_t)xs * bytes_per_col * rows_lds;
+            if (lds > 48 * 1024) continue;
+            const long long slots = (long long)wgs_per_cu(mode, t->qtype, tcmax, lds) * cu_count();
+            const long long tot = (long long)wg_per_split * s;
+            const long long rounds = (tot + slots - 1) / slots;
+            const double cost = (double)rounds * (units + fixed);
+            if (cost < best - 1e-9) {
+                best = cost;
+                best_sp = Split{s, align};
+            }
         }
     }
-    S = env_int(env, S);
-    if (S < 1) S = 1;
-    if (S > nu) S = nu;
-    return S;
+    const int forced = env_int(env, 0);
+    if (forced > 0) best_sp = Split{forced < nu ? forced : nu, 1};
+    return best_sp;
 }
 
 struct DecodePlan {
-    int G, S1, S2, rows1, rows2, NS, RB1, RB2, RBG1, RBG2;
+    int G, rows1, rows2, NS, RB1, RB2, RBG1, RBG2;
+    Split sp1, sp2;
     size_t off_part1, off_h, off_part2, total;
 };
 
@@ -312,15 +357,15 @@ static DecodePlan plan_decode(const mi_table *gate, const mi_table *down, int N,
     p.RBG2 = (p.RB2 + kWgWaves - 1) / kWgWaves;
     int est = N == 1 ? p.G : (p.G * 6 + 5) / 10;
     if (est < 1) est = 1;
-    p.S1 = choose_splits(gate, kGateUp, p.rows1, est * p.RBG1, p.rows1, 4, "MI355MOE_S1");
-    p.S2 = choose_splits(down, kDown, p.rows2, est * p.RBG2, p.rows2, 8, "MI355MOE_S2");
+    p.sp1 = choose_splits(gate, kGateUp, p.rows1, est * p.RBG1, p.rows1, 4, "MI355MOE_S1");
+    p.sp2 = choose_splits(down, kDown, p.rows2, est * p.RBG2, p.rows2, 8, "MI355MOE_S2");
     size_t off = 0;
     p.off_part1 = off;
-    off = align256(off + sizeof(float) * (size_t)p.S1 * 2 * p.NS * gate->rows);
+    off = align256(off + sizeof(float) * (size_t)p.sp1.S * 2 * p.NS * gate->rows);
     p.off_h = off;
     off = align256(off + sizeof(float) * (size_t)p.NS * gate->rows);
     p.off_part2 = off;
-    off = align256(off + sizeof(float) * (size_t)p.S2 * p.NS * down->rows);
+    off = align256(off + sizeof(float) * (size_t)p.sp2.S * p.NS * down->rows);
     p.total = off;
     return p;
 }
@@ -397,12 +442,13 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
     a.t1 = make_table(up);
     a.R = gate->rows;
     a.K = gate->cols;
-    a.S = p.S1;
+    a.S = p.sp1.S;
+    a.ualign = p.sp1.align;
     a.n_units = n_units_of(gate);
     a.RB = p.RB1;
     a.RBW = 2;
     a.RBG = p.RBG1;
-    a.xs_max = max_xs(gate, p.S1);
+    a.xs_max = max_xs(gate, p.sp1);
     a.t_rows = p.rows1;
     a.x_bf16 = x_bf16;
     a.x_f32 = nullptr;
@@ -410,7 +456,7 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
     a.part = (float *)(ws + p.off_part1);
     size_t lds1 = sizeof(uint32_t) * (size_t)a.t_rows * a.xs_max;
     if (phases & 1) {
-        launch_grouped<kGateUp>(gate->qtype, a.t_rows, dim3(p.G * p.RBG1 * p.S1), dim3(64 * kWgWaves), lds1, s, a);
+        launch_grouped<kGateUp>(gate->qtype, a.t_rows, dim3(p.G * p.RBG1 * p.sp1.S), dim3(64 * kWgWaves), lds1, s, a);
         if ((st = launch_status())) return st;
     }
     if (!(phases & 2)) return MI_OK;
@@ -420,8 +466,8 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
     float *h = (float *)(ws + p.off_h);
     {
         const size_t n4 = (size_t)p.NS * gate->rows / 4;
-        hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s,
-                           (const float *)(ws + p.off_part1), p.S1, p.NS, gate->rows, limit, h);
+        hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n4 + 63) / 64)), dim3(64), 0, s,
+                           (const float *)(ws + p.off_part1), p.sp1.S, p.NS, gate->rows, limit, h);
         if ((st = launch_status())) return st;
     }
     KArgs b = a;
@@ -429,22 +475,23 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
     b.t1 = b.t0;
     b.R = down->rows;
     b.K = down->cols;
-    b.S = p.S2;
+    b.S = p.sp2.S;
+    b.ualign = p.sp2.align;
     b.n_units = n_units_of(down);
     b.RB = p.RB2;
     b.RBW = kWgWaves;
     b.RBG = p.RBG2;
-    b.xs_max = max_xs(down, p.S2);
+    b.xs_max = max_xs(down, p.sp2);
     b.t_rows = p.rows2;
     b.x_bf16 = nullptr;
     b.x_f32 = h;
     b.x_stride = gate->rows;
     b.part = (float *)(ws + p.off_part2);
     size_t lds2 = sizeof(uint32_t) * 2 * (size_t)b.t_rows * b.xs_max;
-    launch_grouped<kDown>(down->qtype, b.t_rows, dim3(p.G * p.RBG2 * p.S2), dim3(64 * kWgWaves), lds2, s, b);
+    launch_grouped<kDown>(down->qtype, b.t_rows, dim3(p.G * p.RBG2 * p.sp2.S), dim3(64 * kWgWaves), lds2, s, b);
     if ((st = launch_status())) return st;
     const int D = down->rows, nthr = N * (D / 4);
-    hipLaunchKernelGGL(combine_kernel, dim3((nthr + 255) / 256), dim3(256), 0, s, b.part, p.S2, p.NS, D, N, k, idx, w,
+    hipLaunchKernelGGL(combine_kernel, dim3((nthr + 63) / 64), dim3(64), 0, s, b.part, p.sp2.S, p.NS, D, N, k, idx, w,
                        gate->n_experts, shared_expert, N * k, out_f32, out_bf16);
     return launch_status();
 }
@@ -458,7 +505,7 @@ int mi_moe_decode(const mi_table *gate, const mi_table *up, const mi_table *down
 
 // Split count of mi_matvec: a function of (table, n_slots) only, so the workspace size is known beforehand.  The LDS
 // budget is checked for f32 activations (the larger staging), which also covers bf16.
-static int matvec_splits(const mi_table *t, int n_slots) {
+static Split matvec_splits(const mi_table *t, int n_slots) {
     const int rows = class_rows(n_slots < kMaxT ? n_slots : kMaxT);
     const int G = max_groups(n_slots, t->n_experts, 0, -1, rows);
     const int RB = t->rows / wave_rows_of(t);
@@ -467,9 +514,7 @@ static int matvec_splits(const mi_table *t, int n_slots) {
 
 size_t mi_matvec_workspace(const mi_table *t, int32_t n_slots) {
     if (validate_table(t) || n_slots <= 0 || n_slots > MI_MAX_SLOTS) return 0;
-    const int G = max_groups(n_slots, t->n_experts, 0, -1, class_rows(n_slots < kMaxT ? n_slots : kMaxT));
-    (void)G;
-    const int S = matvec_splits(t, n_slots);
+    const int S = matvec_splits(t, n_slots).S;
     // one split writes the output directly; more keep their partials here for the split reduction
     return S == 1 ? 256 : align256(sizeof(float) * (size_t)S * n_slots * t->rows);
 }
@@ -487,7 +532,8 @@ int mi_matvec(const mi_table *t, const int32_t *idx, int32_t n_slots, const void
     const int rows = class_rows(n_slots < kMaxT ? n_slots : kMaxT);
     const int G = max_groups(n_slots, t->n_experts, 0, -1, rows);
     const int RB = t->rows / wave_rows_of(t);
-    const int S = matvec_splits(t, n_slots);
+    const Split sp = matvec_splits(t, n_slots);
+    const int S = sp.S;
     const int nu = n_units_of(t);
     KArgs a{};
     a.t0 = make_table(t);
@@ -500,11 +546,12 @@ int mi_matvec(const mi_table *t, const int32_t *idx, int32_t n_slots, const void
     a.k = 1;
     a.shared_expert = -1;
     a.S = S;
+    a.ualign = sp.align;
     a.n_units = nu;
     a.RB = RB;
     a.RBW = kWgWaves;
     a.RBG = (RB + kWgWaves - 1) / kWgWaves;
-    a.xs_max = max_xs(t, S);
+    a.xs_max = max_xs(t, sp);
     a.t_rows = rows;
     a.x_bf16 = x_dtype == MI_X_BF16 ? (const uint16_t *)x : nullptr;
     a.x_f32 = x_dtype == MI_X_F32 ? (const float *)x : nullptr;
