@@ -89,11 +89,13 @@ def zipf_topk(rng, N, E, k, s=1.1):
 
 # ------------------------------------------------------------------------------------------------ timing
 class Timer:
-    """Runs a list of per-step callables (one captured HIP graph each) and times exactly `steps` of them."""
+    """Times per-step callables (each one step of the hot path on its own weight copy, used in turn).  The timed
+    steps are captured back to back into one HIP graph, so the timed region is the GPU's own time for exactly
+    `steps` consecutive steps with no host submission gaps; the warmup steps are a graph of their own."""
 
     def __init__(self, torch, fns):
         self.torch = torch
-        self.graphs = []
+        self.fns = fns
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
@@ -101,23 +103,23 @@ class Timer:
                 f()
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
-        for f in fns:
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
-                f()
-            self.graphs.append(g)
-        torch.cuda.synchronize()
+
+    def _graph(self, n):
+        g = self.torch.cuda.CUDAGraph()
+        with self.torch.cuda.graph(g):
+            for i in range(n):
+                self.fns[i % len(self.fns)]()
+        return g
 
     def run(self, steps, warmup):
         torch = self.torch
-        n = len(self.graphs)
-        for i in range(warmup):
-            self.graphs[i % n].replay()
+        timed = self._graph(steps)
+        if warmup > 0:
+            self._graph(warmup).replay()
         torch.cuda.synchronize()
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
-        for i in range(steps):
-            self.graphs[i % n].replay()
+        timed.replay()
         end.record()
         torch.cuda.synchronize()
         return start.elapsed_time(end) / steps            # ms per step
