@@ -40,15 +40,15 @@ extern "C" {
 #define MI_QT_IQ3_S  2   /* llama.cpp IQ3_S in the reference's planar tables (planes.py:22-25)                   */
 
 /*
- * One expert table: E experts of one matrix kind (gate, up or down), every expert R rows x K inputs, stored as
- * planes of u32 [E * rows_p, R] -- the matrix row is the minor (fastest) axis, exactly as the reference stores its
- * tables (planes.py:5-14).  plane[] order:
- *   MI_QT_IQ3_S : {qs, sg, qh, sc, d}   -- the reference's planes, unchanged (planes.py:45)
- *   MI_QT_CB3   : {qs, cb}              -- qs: ceil(K/10) code words per row (kernel bit layout, see formats.py);
- *                                          cb: 4 u32 per (row, group) = bytes lo[0..3], lo[4..7], hi[0..3], hi[4..7]
- *                                          of the 8 bf16 centroids.
- * R must be a multiple of 256 (each wavefront lane owns 4 consecutive rows of a 256-row block); K a multiple of 256
- * (IQ3_S) or 128 (CB3).
+ * One expert table: E experts of one matrix kind (gate, up or down), every expert R rows x K inputs.  plane[] order:
+ *   MI_QT_IQ3_S : {qs, sg, qh, sc, d}   -- the reference's planes, unchanged: u32 [E * rows_p, R], the matrix row
+ *                                          on the minor axis (planes.py:5-14,45).  R % 256 == 0, K % 256 == 0.
+ *   MI_QT_CB3   : {qs, cb}              -- qs: u32 [E][ceil(K/160)][R/16][64][4] code tiles (16 rows x 160 columns,
+ *                                          1 KB each, in the lane order of the matrix-core decoder; formats.py
+ *                                          cb3_tile_words gives the bit map); cb: u32 [E][K/128][R][4] = bytes
+ *                                          lo[0..3], lo[4..7], hi[0..3], hi[4..7] of the 8 bf16 centroids of each
+ *                                          (group, row).  R % 64 == 0, K % 128 == 0.  The codes hold the canonical
+ *                                          10-per-u32 bytes per row plus the zero padding of the last tile.
  */
 typedef struct mi_table {
     int32_t qtype;
@@ -66,8 +66,8 @@ typedef struct mi_table {
  * Fused routed-expert matvec, one output row vector per slot (moe_matvec, pallas_moe.py:238-307):
  *   out[i, r] = sum_n W_{idx[i]}[r, n] * x_i[n]       for i < n_slots, r < R     (f32 accumulation, f32 out)
  * x: n_slots rows of K values (bf16 bits or f32 per x_dtype), row stride x_stride elements.
- * Slots that share an expert are grouped so each expert's codes are read once.  idx values outside [0, E) give a
- * zero row.  n_slots <= MI_MAX_SLOTS.
+ * Slots that share an expert are grouped so each expert's codes are read once.  Rows of slots whose idx is outside
+ * [0, E) are not written.  n_slots <= MI_MAX_SLOTS.  The workspace needs no initialisation.
  */
 #define MI_MAX_SLOTS 128
 int mi_matvec(const mi_table *t, const int32_t *idx, int32_t n_slots, const void *x, int32_t x_dtype,
@@ -84,7 +84,8 @@ size_t mi_matvec_workspace(const mi_table *t, int32_t n_slots);
  * (resident.py:114-120).  out_f32 [N, D] and/or out_bf16 [N, D] (either may be NULL, not both).
  * shared_expert: an expert index of the same tables applied to every token with weight 1, or -1.
  * Limits: N <= 16, N*k <= MI_MAX_SLOTS, E <= 1024.  Deterministic (fixed-order reductions, no float atomics).
- * The workspace must be zero-filled before its first use; every completed call leaves it reusable.
+ * Four launches on the stream: gate/up partials, SwiGLU, down partials, routing-weighted combine.  The workspace
+ * (mi_moe_decode_workspace bytes) holds the partials and h; it needs no initialisation.
  */
 int mi_moe_decode(const mi_table *gate, const mi_table *up, const mi_table *down, const uint16_t *x_bf16,
                   int32_t N, int32_t k, const int32_t *idx, const float *w, int32_t shared_expert, float limit,
@@ -93,9 +94,9 @@ size_t mi_moe_decode_workspace(const mi_table *gate, const mi_table *down, int32
                                int32_t shared_expert);
 
 /*
- * mi_moe_decode split in its two launches (the reference runs them as separate kernels too, resident.py:116-119):
- * phases = 1: gate + up + SwiGLU only (h stays in the workspace); 2: down + combine only (consumes the h a previous
- * phase-1 call left in the same workspace, same arguments); 3: both (= mi_moe_decode).
+ * mi_moe_decode split in two (the reference runs gate/up and down as separate kernels too, resident.py:116-119):
+ * phases = 1: the gate/up launch only (its partials stay in the workspace); 2: SwiGLU + down + combine only
+ * (consumes what a previous phase-1 call left in the same workspace, same arguments); 3: both (= mi_moe_decode).
  */
 int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_table *down, const uint16_t *x_bf16,
                          int32_t N, int32_t k, const int32_t *idx, const float *w, int32_t shared_expert,

@@ -1,0 +1,81 @@
+"""CPU: the C-ABI library loads, exports every entry point include/mi355moe.h declares, and rejects bad arguments on
+the host before any launch (no GPU needed: every call here returns before touching a device)."""
+import ctypes
+import os
+import re
+import subprocess
+import sys
+
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "mi355moe.h")
+
+
+@pytest.fixture(scope="module")
+def L(pkg):
+    if not os.path.exists(pkg._lib.LIB_PATH):
+        subprocess.run([sys.executable, os.path.join(REPO, "kaggle-llm-endpoint_amd", "build.py")], check=True)
+    return pkg._lib.lib()
+
+
+def declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mi_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_binding(pkg):
+    assert declared() == sorted(pkg._lib.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol(L):
+    for name in declared():
+        assert hasattr(L, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", L._name], capture_output=True, text=True).stdout
+    syms = set(re.findall(r"\bT (mi_[a-z0-9_]+)$", out, flags=re.M))
+    assert set(declared()) <= syms
+
+
+def test_status_strings_and_version(L, pkg):
+    assert L.mi_version() >= 1
+    for code in range(0, 9):
+        assert L.mi_strerror(code)
+    assert b"unknown" in L.mi_strerror(99)
+
+
+def _table(pkg, qtype=1, rows=256, cols=1280, E=4, planes=2):
+    t = pkg._lib.MiTable()
+    t.qtype, t.rows, t.cols, t.n_experts = qtype, rows, cols, E
+    for i in range(planes):
+        t.plane[i] = 0x1000 * (i + 1)            # never dereferenced: validation fails before any launch
+    return t
+
+
+def test_host_validation_codes(L, pkg):
+    lib = pkg._lib
+    P = ctypes.c_void_p
+    x, idx, w, out, ws = P(0x10000), P(0x20000), P(0x30000), P(0x40000), P(0x50000)
+    g, u, d = _table(pkg, rows=256, cols=1280), _table(pkg, rows=256, cols=1280), _table(pkg, rows=1280, cols=256)
+    call = lambda gg, uu, dd, N=1, k=2, shared=-1, limit=10.0, o=out: L.mi_moe_decode(
+        ctypes.byref(gg), ctypes.byref(uu), ctypes.byref(dd), x, N, k, idx, w, shared, ctypes.c_float(limit),
+        o, None, ws, 1 << 30, None)
+    assert call(_table(pkg, qtype=9), u, d) == 2                                   # MI_ERR_QTYPE
+    assert call(_table(pkg, rows=100), u, d) == 3                                  # MI_ERR_SHAPE (rows % 64)
+    assert call(_table(pkg, cols=1000), u, d) == 3                                 # MI_ERR_SHAPE (cols % 128)
+    assert call(_table(pkg, planes=1), u, d) == 1                                  # MI_ERR_NULL (codebook plane)
+    assert call(g, _table(pkg, rows=512, cols=1280), d) == 6                       # MI_ERR_MISMATCH (up shape)
+    assert call(g, u, _table(pkg, rows=1280, cols=512)) == 6                       # MI_ERR_MISMATCH (down.cols)
+    assert call(g, u, d, N=0) == 4 and call(g, u, d, N=17) == 4                    # MI_ERR_TOKENS
+    assert call(g, u, d, N=16, k=9) == 4                                           # N*k > MI_MAX_SLOTS
+    assert call(g, u, d, shared=4) == 8 and call(g, u, d, limit=0.0) == 8          # MI_ERR_ARG
+    assert call(g, u, d, o=None) == 1                                              # MI_ERR_NULL (no output)
+    assert L.mi_matvec(ctypes.byref(g), idx, 0, x, lib.MI_X_BF16, 1280, out, ws, 1 << 30, None) == 4
+    assert L.mi_matvec(ctypes.byref(g), idx, 4, x, 7, 1280, out, ws, 1 << 30, None) == 8
+    assert L.mi_matvec(ctypes.byref(g), idx, 4, x, lib.MI_X_BF16, 1000, out, ws, 1 << 30, None) == 8
+    assert L.mi_dequant(ctypes.byref(g), 4, out, None) == 8                        # expert out of range
+    assert L.mi_int8_project(x, 0, P(1), P(2), 256, 16, out, None, ws, 1 << 20, None) == 4
+    assert L.mi_int8_project(x, 8, P(1), P(2), 300, 16, out, None, ws, 1 << 20, None) == 3
+    assert L.mi_int8_project(x, 8, P(1), P(2), 256, 16, None, None, ws, 1 << 20, None) == 1
+    assert L.mi_int8_project_workspace(8, 6144, 6144) > 0
+    assert L.mi_int8_project_workspace(8, 300, 16) == 0
