@@ -111,6 +111,10 @@ def test_ragged_plan_invariants_and_brute_force(T, k, E, tm):
         for j in range(k):
             r = p["row_slot"][t, j]
             assert p["tok_row"][r] == t and p["w_row"][r] == w[t, j] and p["blk_expert"][r // tm] == idx[t, j]
+    # within an expert, rows follow the slot order t * k + j (the reference's stable argsort)
+    for e in range(E):
+        slots = np.flatnonzero(idx.reshape(-1) == e)
+        assert (np.diff(rows[slots]) > 0).all()
     # padding rows: token -1, weight 0; blocks past n_blocks repeat the last real block's expert
     pad = np.setdiff1d(np.arange(G * tm), rows)
     assert (p["tok_row"][pad] == -1).all() and (p["w_row"][pad] == 0).all()
