@@ -35,13 +35,8 @@ struct Cb3Table {
 };
 
 constexpr int kCb3TileCols = 160;
-constexpr int kCb3Rtw = 4;                    // row tiles per wavefront
-constexpr int kCb3WaveRows = 16 * kCb3Rtw;    // 64 rows per wavefront
-
-// wave-uniform base (SGPRs) + the lane's byte offset: the scalar-base addressing form for every stream load
-__device__ __forceinline__ uint4 ld_lane(const uint32_t *__restrict__ base, uint32_t lane_bytes) {
-    return *(const uint4 *)((const char *)base + lane_bytes);
-}
+constexpr int kCb3MaxRtw = 4;                 // row tiles per wavefront: RTW = 1, 2 or 4 (16, 32 or 64 rows)
+constexpr int kCb3RowAlign = 16 * kCb3MaxRtw; // CB3 tables have R % 64 == 0
 
 // Selectors (4 codes each) of k-step M from the lane's 4 code words.
 template <int M>
@@ -81,41 +76,58 @@ __device__ __forceinline__ f32x4 mfma16(bf16x8 a, uint4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
+// Stream loads are buffer loads: a wave-uniform descriptor (SGPRs) + the lane's byte offset + a scalar tile offset.
+// A load the split does not need uses a descriptor with an empty range instead: it returns zeros without touching
+// memory, so the instruction stream -- and the compiler's wait counts -- never depend on the split's bounds.
+__device__ __forceinline__ uint4 bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
+}
+constexpr int kBufferWord3 = 0x00020000;   // gfx9 buffer descriptor word 3 (32-bit data format)
+
 // Per-wavefront stream state.
 struct Cb3Wave {
-    const uint32_t *qt;    // expert's code tiles
-    const uint32_t *cbe;   // expert's codebook
-    int RT, G, CT, R;
-    int rt0;               // first row tile
+    __amdgpu_buffer_rsrc_t qb, qnull;      // expert's code tiles (full range / empty range)
+    __amdgpu_buffer_rsrc_t cbb, cbnull;    // expert's codebook
+    uint32_t ct_bytes;     // bytes per column tile row of tiles: RT * 1024
+    uint32_t rt_bytes;     // byte offset of the wavefront's first row tile inside a column tile: rt0 * 1024
+    uint32_t g_bytes;      // bytes per codebook group: R * 16
+    uint32_t row_bytes;    // byte offset of the wavefront's first row inside a group: 16 * rt0 * 16
     int cta, ctb;          // column tiles [cta, ctb) of the wavefront's split
-    int g_last;            // last codebook group the split uses
+    int g_first, g_last;   // codebook groups the split uses
     uint32_t lane16;       // lane * 16 bytes
+    uint32_t cblane16;     // (lane % (16 RTW)) * 16 bytes: the lane's row of a codebook group load
     const uint32_t *xh;    // LDS: B-operand row of this lane (hi / bf16 part) at column 640 * (cta / 4)
     const uint32_t *xl;    // LDS: lo part (two-instruction mode)
-    uint4 *cbl;            // LDS: this wavefront's codebook slots, 5 groups x 64 rows
+    uint4 *cbl;            // LDS: this wavefront's codebook slots, 5 groups x 64 lanes (rows 0 .. 16 RTW - 1)
 };
 
-// Codebook path: one 1 KB load brings a group's 16-byte codebooks of the wavefront's 64 rows (lane = row) into the
+// Codebook path: one 1 KB load brings a group's 16-byte codebooks of the wavefront's 16 RTW rows (lane = row; with
+// fewer than 64 rows the remaining lanes repeat them, same addresses, no extra traffic) into the
 // register slot of its super-tile position; right before the group is first needed it is written to the
 // wavefront's own LDS slot (same-wavefront LDS accesses stay in order, so no barrier) and the register slot is
 // reloaded with the next super tile's group.  The decoders read a row's 16 bytes from LDS per k-step, so a lane
 // never holds the 4 row tiles' codebooks in registers.
+template <int RTW>
 struct Cb3Regs {
-    uint4 ring[4][kCb3Rtw];   // code words: slot c = column tile c of a super tile
+    uint4 ring[4][RTW];       // code words: slot c = column tile c of a super tile
     uint4 cbv[5];             // codebook groups in flight: slot c = group c of the next super tile
-    f32x4 acc[kCb3Rtw];
+    f32x4 acc[RTW];
 };
 
-__device__ __forceinline__ const uint32_t *cb3_tile(const Cb3Wave &w, int ct, int r) {
-    return w.qt + ((size_t)ct * w.RT + w.rt0 + r) * 256;
+// Code tile (ct, row tile r of the wavefront) if the split streams it, else zeros.
+__device__ __forceinline__ uint4 cb3_tile(const Cb3Wave &w, int ct, int r) {
+    const bool need = ct >= w.cta && ct < w.ctb;
+    return bload(need ? w.qb : w.qnull, w.lane16, (uint32_t)ct * w.ct_bytes + w.rt_bytes + 1024u * r);
 }
-__device__ __forceinline__ const uint32_t *cb3_group(const Cb3Wave &w, int g) {
-    return w.cbe + ((size_t)g * w.R + 16 * w.rt0) * 4;
+// Codebook group g of the wavefront's rows if the split uses it, else zeros.
+__device__ __forceinline__ uint4 cb3_group(const Cb3Wave &w, int g) {
+    const bool need = g >= w.g_first && g <= w.g_last;
+    return bload(need ? w.cbb : w.cbnull, w.cblane16, (uint32_t)g * w.g_bytes + w.row_bytes);
 }
 
 // k-steps M..4 of one row tile's column tile (recursion keeps every index static).
 template <bool TWO, int C, int M>
-__device__ __forceinline__ void cb3_steps(const uint4 wv, const uint4 *cbrow, int r, const uint4 (&xb)[5],
+__device__ __forceinline__ void cb3_steps(const uint4 wv, const uint4 *cbrow, const int r, const uint4 (&xb)[5],
                                           const uint4 (&xl)[5], f32x4 &acc) {
     if constexpr (M < 5) {
         constexpr int slot = (M < 4 - C) ? C : C + 1;
@@ -131,20 +143,21 @@ __device__ __forceinline__ void cb3_steps(const uint4 wv, const uint4 *cbrow, in
 // Column tile C of super tile st: publish the codebook groups first needed here (C = 0: groups 0, 1; else group
 // C + 1) and reload their register slots with the next super tile's groups; read the B operands; then per row
 // tile take the ring slot, refill it with column tile C of the next super tile and decode + MFMA the 5 k-steps.
-// Loads the split does not need re-read data already loaded (cache hits), so the instruction stream -- and the
-// compiler's wait counts -- never depend on the split's bounds.
-template <bool TWO, int C>
-__device__ __forceinline__ void cb3_ctile(const Cb3Wave &w, Cb3Regs &s, int st) {
+template <bool TWO, int RTW, int C>
+__device__ __forceinline__ void cb3_ctile(const Cb3Wave &w, Cb3Regs<RTW> &s, int st) {
     const int lane = threadIdx.x & 63;
     const int gn = 5 * (st + 1);
+    // keep this tile's LDS publishes and loads here: hoisting a publish would wait for a load issued a super tile
+    // later than the one it needs
+    __builtin_amdgcn_sched_barrier(0);
     if constexpr (C == 0) {
         w.cbl[0 * 64 + lane] = s.cbv[0];
         w.cbl[1 * 64 + lane] = s.cbv[1];
-        s.cbv[0] = ld_lane(cb3_group(w, min(gn, w.g_last)), w.lane16);
-        s.cbv[1] = ld_lane(cb3_group(w, min(gn + 1, w.g_last)), w.lane16);
+        s.cbv[0] = cb3_group(w, gn);
+        s.cbv[1] = cb3_group(w, gn + 1);
     } else {
         w.cbl[(C + 1) * 64 + lane] = s.cbv[C + 1];
-        s.cbv[C + 1] = ld_lane(cb3_group(w, min(gn + C + 1, w.g_last)), w.lane16);
+        s.cbv[C + 1] = cb3_group(w, gn + C + 1);
     }
     const int ct = 4 * st + C;
     const int xo = 80 * (ct - (w.cta & ~3));                // dwords
@@ -155,53 +168,49 @@ __device__ __forceinline__ void cb3_ctile(const Cb3Wave &w, Cb3Regs &s, int st) 
         if (TWO) xl[m] = *(const uint4 *)(w.xl + xo + 16 * m);
         else xl[m] = xb[m];
     }
-    const int ctn = (ct + 4 < w.ctb) ? ct + 4 : max(ct, w.cta);
     const uint4 *cbrow = w.cbl + (lane & 15);
 #pragma unroll
-    for (int r = 0; r < kCb3Rtw; ++r) {
+    for (int r = 0; r < RTW; ++r) {
         const uint4 wv = s.ring[C][r];
-        s.ring[C][r] = ld_lane(cb3_tile(w, ctn, r), w.lane16);
+        s.ring[C][r] = cb3_tile(w, ct + 4, r);
         cb3_steps<TWO, C, 0>(wv, cbrow, r, xb, xl, s.acc[r]);
     }
 }
 
-// Streams column tiles [cta, ctb) of the wavefront's 64 rows, as whole super tiles from the one holding cta: the
-// column tiles before cta run against zero activations (their loads re-read cta's data, so they cost vector ALU work
-// but no HBM traffic), which keeps the code ring and codebook slots at static positions.  The split's last super tile
-// may end early.  `stage` (ending in a workgroup barrier) runs after the first loads are issued.
-template <bool TWO, class Stage>
-__device__ __forceinline__ void cb3_accum_mfma(const Cb3Wave &w, f32x4 (&acc)[kCb3Rtw], Stage &&stage) {
-    Cb3Regs s;
+// Streams column tiles [cta, ctb) of the wavefront's 16 RTW rows, as whole super tiles from the one holding cta: the
+// column tiles before cta decode zeros against zero activations (their loads touch no memory; they cost vector ALU
+// work only), which keeps the code ring and codebook slots at static positions.  The split's last super tile may end
+// early.  `stage` (ending in a workgroup barrier) runs after the first loads are issued.
+template <bool TWO, int RTW, class Stage>
+__device__ __forceinline__ void cb3_accum_mfma(const Cb3Wave &w, f32x4 (&acc)[RTW], Stage &&stage) {
+    Cb3Regs<RTW> s;
     const int sta = w.cta >> 2;
-    const int g_first = (kCb3TileCols * w.cta) >> 7;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const int ct = min(max(4 * sta + c, w.cta), w.ctb - 1);
+    for (int c = 0; c < 4; ++c)
 #pragma unroll
-        for (int r = 0; r < kCb3Rtw; ++r) s.ring[c][r] = ld_lane(cb3_tile(w, ct, r), w.lane16);
-    }
+        for (int r = 0; r < RTW; ++r) s.ring[c][r] = cb3_tile(w, 4 * sta + c, r);
 #pragma unroll
-    for (int c = 0; c < 5; ++c) s.cbv[c] = ld_lane(cb3_group(w, min(max(5 * sta + c, g_first), w.g_last)), w.lane16);
+    for (int c = 0; c < 5; ++c) s.cbv[c] = cb3_group(w, 5 * sta + c);
 #pragma unroll
-    for (int r = 0; r < kCb3Rtw; ++r) s.acc[r] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int r = 0; r < RTW; ++r) s.acc[r] = (f32x4){0.f, 0.f, 0.f, 0.f};
     stage();
 
     const int st_full = w.ctb >> 2;      // super tiles that end inside the split
     int st = sta;
     for (; st < st_full; ++st) {
-        cb3_ctile<TWO, 0>(w, s, st);
-        cb3_ctile<TWO, 1>(w, s, st);
-        cb3_ctile<TWO, 2>(w, s, st);
-        cb3_ctile<TWO, 3>(w, s, st);
+        cb3_ctile<TWO, RTW, 0>(w, s, st);
+        cb3_ctile<TWO, RTW, 1>(w, s, st);
+        cb3_ctile<TWO, RTW, 2>(w, s, st);
+        cb3_ctile<TWO, RTW, 3>(w, s, st);
     }
     const int nct = w.ctb - 4 * st;      // 0..3 column tiles of a last, partial super tile
     if (nct > 0) {
-        cb3_ctile<TWO, 0>(w, s, st);
-        if (nct > 1) cb3_ctile<TWO, 1>(w, s, st);
-        if (nct > 2) cb3_ctile<TWO, 2>(w, s, st);
+        cb3_ctile<TWO, RTW, 0>(w, s, st);
+        if (nct > 1) cb3_ctile<TWO, RTW, 1>(w, s, st);
+        if (nct > 2) cb3_ctile<TWO, RTW, 2>(w, s, st);
     }
 #pragma unroll
-    for (int r = 0; r < kCb3Rtw; ++r) acc[r] = s.acc[r];
+    for (int r = 0; r < RTW; ++r) acc[r] = s.acc[r];
 }
 
 }  // namespace mi

@@ -88,30 +88,35 @@ __device__ __forceinline__ void iq3_run_and_store(const Iq3Table &tb, int e, int
 #undef MI_RUN_CLASS
 }
 
-// CB3 rows (64 per wavefront, matrix cores).  B-operand lane (column jt = lane % 16 of the 16x16 tile, k-chunk q):
+// CB3 rows (16 RTW per wavefront, matrix cores).  B-operand lane (column jt = lane % 16 of the 16x16 tile, k-chunk q):
 //   bf16 activations: token jt;
 //   f32 activations, launches of at most 8 tokens per group: hi part of token jt (jt < 8) or lo part of token jt - 8
 //     (jt >= 8), and the two accumulator columns are added at the end -- one instruction covers hi and lo;
 //   f32 activations, launches of up to 16 tokens per group: hi and lo of token jt, two instructions per k-step.
 // Columns jt >= the staged rows read a clamped row; their accumulator columns are never stored.
-template <bool HILO, int TCMAX, class Stage>
+template <bool HILO, int TCMAX, int RTW, class Stage>
 __device__ __forceinline__ void cb3_run_and_store(const Cb3Table &tb, int e, int rg, int u0, int u1, int c0,
                                                   const uint32_t *xh, const uint32_t *xl, int xsp, int t_rows, int n,
                                                   const int *slots, float *part_base, int R, uint4 *cbl,
                                                   Stage &&stage) {
     const int lane = threadIdx.x & 63, jt = lane & 15, q = lane >> 4;
     Cb3Wave w;
-    w.RT = tb.RT;
-    w.G = tb.G;
-    w.CT = tb.CT;
-    w.R = tb.R;
-    w.qt = tb.qs + (size_t)e * tb.CT * tb.RT * 256;
-    w.cbe = tb.cb + (size_t)e * tb.G * tb.R * 4;
-    w.rt0 = rg * kCb3Rtw;
+    const uint32_t *qt = tb.qs + (size_t)e * tb.CT * tb.RT * 256;
+    const uint32_t *cbe = tb.cb + (size_t)e * tb.G * tb.R * 4;
+    w.qb = __builtin_amdgcn_make_buffer_rsrc((void *)qt, (short)0, 0x7fffffff, kBufferWord3);
+    w.qnull = __builtin_amdgcn_make_buffer_rsrc((void *)qt, (short)0, 0, kBufferWord3);
+    w.cbb = __builtin_amdgcn_make_buffer_rsrc((void *)cbe, (short)0, 0x7fffffff, kBufferWord3);
+    w.cbnull = __builtin_amdgcn_make_buffer_rsrc((void *)cbe, (short)0, 0, kBufferWord3);
+    w.ct_bytes = (uint32_t)tb.RT * 1024u;
+    w.rt_bytes = (uint32_t)(rg * RTW) * 1024u;
+    w.g_bytes = (uint32_t)tb.R * 16u;
+    w.row_bytes = (uint32_t)(rg * 16 * RTW) * 16u;
     w.cta = u0;
     w.ctb = u1;
+    w.g_first = (kCb3TileCols * u0) >> 7;
     w.g_last = min((kCb3TileCols * u1 - 1) >> 7, tb.G - 1);
     w.lane16 = (uint32_t)lane * 16u;
+    w.cblane16 = (uint32_t)(lane & (16 * RTW - 1)) * 16u;
     w.cbl = cbl;
     constexpr bool two = HILO && TCMAX > 8;
     constexpr bool pair = HILO && !two;          // hi / lo in the two halves of the tile's columns
@@ -119,18 +124,18 @@ __device__ __forceinline__ void cb3_run_and_store(const Cb3Table &tb, int e, int
     row = min(row, t_rows - 1);
     w.xh = ((pair && jt >= 8) ? xl : xh) + row * xsp + 4 * q;
     w.xl = xl + row * xsp + 4 * q;
-    f32x4 acc[kCb3Rtw];
-    cb3_accum_mfma<two>(w, acc, stage);
+    f32x4 acc[RTW];
+    cb3_accum_mfma<two, RTW>(w, acc, stage);
     if (pair) {
 #pragma unroll
-        for (int r = 0; r < kCb3Rtw; ++r)
+        for (int r = 0; r < RTW; ++r)
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[r][i] += __shfl_down(acc[r][i], 8, 16);
     }
     if (jt < n) {
-        float *dst = part_base + (size_t)slots[jt] * R + rg * kCb3WaveRows + 4 * q;
+        float *dst = part_base + (size_t)slots[jt] * R + rg * 16 * RTW + 4 * q;
 #pragma unroll
-        for (int r = 0; r < kCb3Rtw; ++r) *(float4 *)(dst + 16 * r) = make_float4(acc[r][0], acc[r][1], acc[r][2], acc[r][3]);
+        for (int r = 0; r < RTW; ++r) *(float4 *)(dst + 16 * r) = make_float4(acc[r][0], acc[r][1], acc[r][2], acc[r][3]);
     }
 }
 
@@ -138,14 +143,15 @@ __device__ __forceinline__ void cb3_run_and_store(const Cb3Table &tb, int e, int
 // matvec = 4 row groups.  A row group is the rows of one wavefront: 64 (CB3) or 256 (IQ3_S).
 constexpr int kWgWaves = 4;
 
-template <int QT>
-__host__ __device__ constexpr int wave_rows() { return QT == MI_QT_CB3 ? kCb3WaveRows : kRowBlock; }
+// Rows per wavefront: CB3 16 RTW (RTW row tiles), IQ3_S 256 (4 rows per lane).
+template <int QT, int RTW>
+__host__ __device__ constexpr int wave_rows() { return QT == MI_QT_CB3 ? 16 * RTW : kRowBlock; }
 
 // CB3 kernels are held to 3 wavefronts per SIMD (<= 168 VGPRs): more HBM requests in flight per CU.
 template <int QT>
 __host__ __device__ constexpr int min_waves_per_simd() { return QT == MI_QT_CB3 ? 3 : 1; }
 
-template <int MODE, int QT, int TCMAX>
+template <int MODE, int QT, int TCMAX, int RTW>
 __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) grouped_kernel(KArgs a) {
     extern __shared__ uint32_t xlds[];
     __shared__ GroupScratch sc;
@@ -154,7 +160,7 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
     __shared__ int s_tok[kMaxT];
 
     constexpr bool cb3 = QT == MI_QT_CB3;
-    constexpr int WR = wave_rows<QT>();
+    constexpr int WR = wave_rows<QT, RTW>();
     const int tid = threadIdx.x;
     const int task = blockIdx.x;
     const int split = task % a.S;
@@ -228,10 +234,10 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
     float *part_base = a.part + (size_t)(split * nmat + mat) * a.NS * a.R;
     if constexpr (cb3) {
         if (hilo)
-            cb3_run_and_store<true, TCMAX>(tb.cb3, e, rg, u0, u1, c0, xh, xl, xsp, a.t_rows, n, s_tok, part_base, a.R,
+            cb3_run_and_store<true, TCMAX, RTW>(tb.cb3, e, rg, u0, u1, c0, xh, xl, xsp, a.t_rows, n, s_tok, part_base, a.R,
                                            cbl + wave * 5 * 64, stage);
         else
-            cb3_run_and_store<false, TCMAX>(tb.cb3, e, rg, u0, u1, c0, xh, xl, xsp, a.t_rows, n, s_tok, part_base,
+            cb3_run_and_store<false, TCMAX, RTW>(tb.cb3, e, rg, u0, u1, c0, xh, xl, xsp, a.t_rows, n, s_tok, part_base,
                                             a.R, cbl + wave * 5 * 64, stage);
     } else {
         const int r0 = rg * WR + lane * kRowsPerLane;

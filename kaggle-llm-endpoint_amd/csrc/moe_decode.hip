@@ -165,7 +165,7 @@ __global__ void split_reduce_kernel(const float *__restrict__ part, int S, int N
 static int validate_table(const mi_table *t) {
     if (!t) return MI_ERR_NULL;
     if (t->qtype != MI_QT_CB3 && t->qtype != MI_QT_IQ3_S) return MI_ERR_QTYPE;
-    if (t->rows <= 0 || t->rows % (t->qtype == MI_QT_CB3 ? kCb3WaveRows : kRowBlock)) return MI_ERR_SHAPE;
+    if (t->rows <= 0 || t->rows % (t->qtype == MI_QT_CB3 ? kCb3RowAlign : kRowBlock)) return MI_ERR_SHAPE;
     if (t->n_experts <= 0 || t->n_experts > kMaxExperts) return MI_ERR_SHAPE;
     if (t->qtype == MI_QT_CB3) {
         if (t->cols <= 0 || t->cols % 128) return MI_ERR_SHAPE;
@@ -208,7 +208,8 @@ static int n_units_of(const mi_table *t) {
     if (t->qtype == MI_QT_CB3) return cb3_ct(t);                 // 160-column tiles
     return t->cols / 256;                                        // IQ3_S blocks
 }
-static int wave_rows_of(const mi_table *t) { return t->qtype == MI_QT_CB3 ? kCb3WaveRows : kRowBlock; }
+// Rows per wavefront: CB3 16 rtw (rtw row tiles), IQ3_S 256.
+static int wave_rows_of(const mi_table *t, int rtw) { return t->qtype == MI_QT_CB3 ? 16 * rtw : kRowBlock; }
 static int unit_cols(const mi_table *t) { return t->qtype == MI_QT_CB3 ? kCb3TileCols : 256; }
 
 static int env_int(const char *name, int dflt) {
@@ -271,7 +272,7 @@ static int cu_count() {
     return n;
 }
 
-#define MI_DECL_OCC(M, Q) int occupancy_grouped_##M##_##Q(int tcmax, size_t lds);
+#define MI_DECL_OCC(M, Q) int occupancy_grouped_##M##_##Q(int tcmax, int rtw, size_t lds);
 MI_DECL_OCC(0, 1)
 MI_DECL_OCC(0, 2)
 MI_DECL_OCC(1, 1)
@@ -281,62 +282,87 @@ MI_DECL_OCC(2, 2)
 #undef MI_DECL_OCC
 
 // Resident workgroups per CU of a grouped-kernel launch (the runtime's occupancy for that instance and LDS size;
-// 2 when it cannot be queried), cached per (mode, format, token class, 512-byte LDS bucket).
-static int wgs_per_cu(int mode, int qtype, int tcmax, size_t lds) {
-    static int cache[3][2][5][161];
+// 2 when it cannot be queried), cached per (mode, format, token class, rows per wavefront, 512-byte LDS bucket).
+static int wgs_per_cu(int mode, int qtype, int tcmax, int rtw, size_t lds) {
+    static int cache[3][2][5][3][161];
     const int qi = qtype == MI_QT_CB3 ? 0 : 1;
-    int ti = 0;
+    int ti = 0, ri = rtw == 4 ? 2 : rtw - 1;
     while ((1 << ti) < tcmax && ti < 4) ++ti;
     const size_t bucket = (lds + 511) / 512;
-    int *slot = bucket <= 160 ? &cache[mode][qi][ti][bucket] : nullptr;
+    int *slot = bucket <= 160 ? &cache[mode][qi][ti][ri][bucket] : nullptr;
     if (slot && *slot > 0) return *slot;
     const size_t l = bucket * 512;
     int n;
-    if (mode == kGateUp) n = (qi ? occupancy_grouped_0_2 : occupancy_grouped_0_1)(tcmax, l);
-    else if (mode == kDown) n = (qi ? occupancy_grouped_1_2 : occupancy_grouped_1_1)(tcmax, l);
-    else n = (qi ? occupancy_grouped_2_2 : occupancy_grouped_2_1)(tcmax, l);
+    if (mode == kGateUp) n = (qi ? occupancy_grouped_0_2 : occupancy_grouped_0_1)(tcmax, rtw, l);
+    else if (mode == kDown) n = (qi ? occupancy_grouped_1_2 : occupancy_grouped_1_1)(tcmax, rtw, l);
+    else n = (qi ? occupancy_grouped_2_2 : occupancy_grouped_2_1)(tcmax, rtw, l);
     if (n <= 0) n = 2;
     if (slot) *slot = n;
     return n;
 }
 
-// Pick the column splits.  A launch has wg_per_split * S workgroups; the runtime's occupancy gives the slots
-// (resident workgroups over the chip), so the workgroups run in ceil(total / slots) rounds of ~(units streamed per
-// split + a fixed cost) each -- minimise that over S and the boundary alignment (CB3: column tiles, or whole super
-// tiles), with the LDS staging of a split within 48 KB.
-static Split choose_splits(const mi_table *t, int mode, int tcmax, int wg_per_split, int rows_lds, int bytes_per_col,
-                           const char *env) {
+// Launch shape of one grouped launch: column splits (S, boundary alignment in units), rows per wavefront (rtw row
+// tiles for CB3) and the resulting row groups (RB per matrix, RBG workgroup row ranges).
+struct Shape {
+    Split sp;
+    int rtw, RB, RBG;
+};
+
+// Pick the launch shape.  A launch has groups * RBG * S workgroups of 4 wavefronts; the runtime's occupancy gives
+// the slots (resident workgroups over the chip), so the workgroups run in ceil(total / slots) rounds, each as long
+// as a wavefront's stream: the column units it streams (CB3: from the start of its first super tile) times the
+// kilobytes per unit (rtw for CB3), plus a fixed cost (first loads, staging, partial stores).  Minimise that over
+// S, the boundary alignment (CB3: column tiles or whole super tiles) and rtw, with a split's LDS staging within
+// 48 KB.  Environment overrides (experiments): <env>=S, <env>_RTW=rtw.
+static Shape choose_shape(const mi_table *t, int mode, int tcmax, int groups, int rows_lds, int bytes_per_col,
+                          const char *env) {
     const int nu = n_units_of(t);
-    const double fixed = 2.0;          // per-task cost (first loads, staging, partial stores) in column units
-    Split best_sp{1, 1};
-    double best = 1e30;
-    const int aligns[2] = {t->qtype == MI_QT_CB3 ? 4 : 1, 1};
-    for (int ai = 0; ai < 2; ++ai) {
-        const int align = aligns[ai];
-        const int nb = (nu + align - 1) / align;
-        for (int s = 1; s <= nb; ++s) {
-            int xs, units;
-            split_extent(t, s, align, &xs, &units);
-            const size_t lds = (size_t)xs * bytes_per_col * rows_lds;
-            if (lds > 48 * 1024) continue;
-            const long long slots = (long long)wgs_per_cu(mode, t->qtype, tcmax, lds) * cu_count();
-            const long long tot = (long long)wg_per_split * s;
-            const long long rounds = (tot + slots - 1) / slots;
-            const double cost = (double)rounds * (units + fixed);
-            if (cost < best - 1e-9) {
-                best = cost;
-                best_sp = Split{s, align};
+    const bool cb3 = t->qtype == MI_QT_CB3;
+    const int rg_per_wg = mode == kGateUp ? 2 : kWgWaves;
+    const double fixed = 8.0;          // per-task cost in kilobyte-units
+    char env_rtw[64];
+    snprintf(env_rtw, sizeof env_rtw, "%s_RTW", env);
+    const int forced_rtw = env_int(env_rtw, 0), forced_s = env_int(env, 0);
+    Shape best{{1, 1}, cb3 ? 4 : 1, 0, 0};
+    double best_cost = 1e30;
+    for (int rtw = cb3 ? 4 : 1; rtw >= 1; rtw /= 2) {
+        if (forced_rtw > 0 && cb3 && rtw != forced_rtw) continue;
+        const int RB = t->rows / wave_rows_of(t, rtw);
+        const int RBG = (RB + rg_per_wg - 1) / rg_per_wg;
+        const double kb_per_unit = cb3 ? rtw * 1.25 : 1.0;
+        const int aligns[2] = {cb3 ? 4 : 1, 1};
+        for (int ai = 0; ai < 2; ++ai) {
+            const int align = aligns[ai];
+            const int nb = (nu + align - 1) / align;
+            for (int s = 1; s <= nb; ++s) {
+                if (forced_s > 0 && (s != (forced_s < nu ? forced_s : nu) || align != 1)) continue;
+                int xs, units;
+                split_extent(t, s, align, &xs, &units);
+                const size_t lds = (size_t)xs * bytes_per_col * rows_lds;
+                if (lds > 48 * 1024) continue;
+                const long long slots = (long long)wgs_per_cu(mode, t->qtype, tcmax, rtw, lds) * cu_count();
+                const long long tot = (long long)groups * RBG * s;
+                const long long rounds = (tot + slots - 1) / slots;
+                const double cost = (double)rounds * (units * kb_per_unit + fixed);
+                if (cost < best_cost - 1e-9) {
+                    best_cost = cost;
+                    best = Shape{Split{s, align}, rtw, RB, RBG};
+                }
             }
         }
+        if (!cb3) break;
     }
-    const int forced = env_int(env, 0);
-    if (forced > 0) best_sp = Split{forced < nu ? forced : nu, 1};
-    return best_sp;
+    if (best.RB == 0) {            // nothing fits the LDS budget with the overrides: one split per unit
+        best.sp = Split{nu, 1};
+        best.RB = t->rows / wave_rows_of(t, best.rtw);
+        best.RBG = (best.RB + rg_per_wg - 1) / rg_per_wg;
+    }
+    return best;
 }
 
 struct DecodePlan {
-    int G, rows1, rows2, NS, RB1, RB2, RBG1, RBG2;
-    Split sp1, sp2;
+    int G, rows1, rows2, NS;
+    Shape s1, s2;
     size_t off_part1, off_h, off_part2, total;
 };
 
@@ -351,21 +377,17 @@ static DecodePlan plan_decode(const mi_table *gate, const mi_table *down, int N,
     p.rows2 = p.rows1;
     p.G = max_groups(n_route, gate->n_experts, N, shared, p.rows1);
     p.NS = n_route + (shared >= 0 ? N : 0);
-    p.RB1 = gate->rows / wave_rows_of(gate);
-    p.RB2 = down->rows / wave_rows_of(down);
-    p.RBG1 = (p.RB1 + 1) / 2;
-    p.RBG2 = (p.RB2 + kWgWaves - 1) / kWgWaves;
     int est = N == 1 ? p.G : (p.G * 6 + 5) / 10;
     if (est < 1) est = 1;
-    p.sp1 = choose_splits(gate, kGateUp, p.rows1, est * p.RBG1, p.rows1, 4, "MI355MOE_S1");
-    p.sp2 = choose_splits(down, kDown, p.rows2, est * p.RBG2, p.rows2, 8, "MI355MOE_S2");
+    p.s1 = choose_shape(gate, kGateUp, p.rows1, est, p.rows1, 4, "MI355MOE_S1");
+    p.s2 = choose_shape(down, kDown, p.rows2, est, p.rows2, 8, "MI355MOE_S2");
     size_t off = 0;
     p.off_part1 = off;
-    off = align256(off + sizeof(float) * (size_t)p.sp1.S * 2 * p.NS * gate->rows);
+    off = align256(off + sizeof(float) * (size_t)p.s1.sp.S * 2 * p.NS * gate->rows);
     p.off_h = off;
     off = align256(off + sizeof(float) * (size_t)p.NS * gate->rows);
     p.off_part2 = off;
-    off = align256(off + sizeof(float) * (size_t)p.sp2.S * p.NS * down->rows);
+    off = align256(off + sizeof(float) * (size_t)p.s2.sp.S * p.NS * down->rows);
     p.total = off;
     return p;
 }
@@ -378,7 +400,7 @@ static int launch_status() {
 // The grouped kernels are instantiated in separate translation units (k_grouped.hip, built once per (mode, format))
 // so the build compiles them in parallel; each unit exports one launcher.
 #define MI_DECL_LAUNCH(M, Q) \
-    void launch_grouped_##M##_##Q(int tcmax, dim3 grid, dim3 block, size_t lds, hipStream_t s, const KArgs &a);
+    void launch_grouped_##M##_##Q(int tcmax, int rtw, dim3 grid, dim3 block, size_t lds, hipStream_t s, const KArgs &a);
 MI_DECL_LAUNCH(0, 1)
 MI_DECL_LAUNCH(0, 2)
 MI_DECL_LAUNCH(1, 1)
@@ -388,11 +410,12 @@ MI_DECL_LAUNCH(2, 2)
 #undef MI_DECL_LAUNCH
 
 template <int MODE>
-static void launch_grouped(int qtype, int tcmax, dim3 grid, dim3 block, size_t lds, hipStream_t s, const KArgs &a) {
+static void launch_grouped(int qtype, int tcmax, int rtw, dim3 grid, size_t lds, hipStream_t s, const KArgs &a) {
     const bool cb3 = qtype == MI_QT_CB3;
-    if (MODE == kGateUp) (cb3 ? launch_grouped_0_1 : launch_grouped_0_2)(tcmax, grid, block, lds, s, a);
-    else if (MODE == kDown) (cb3 ? launch_grouped_1_1 : launch_grouped_1_2)(tcmax, grid, block, lds, s, a);
-    else (cb3 ? launch_grouped_2_1 : launch_grouped_2_2)(tcmax, grid, block, lds, s, a);
+    const dim3 block(64 * kWgWaves);
+    if (MODE == kGateUp) (cb3 ? launch_grouped_0_1 : launch_grouped_0_2)(tcmax, rtw, grid, block, lds, s, a);
+    else if (MODE == kDown) (cb3 ? launch_grouped_1_1 : launch_grouped_1_2)(tcmax, rtw, grid, block, lds, s, a);
+    else (cb3 ? launch_grouped_2_1 : launch_grouped_2_2)(tcmax, rtw, grid, block, lds, s, a);
 }
 
 }  // namespace mi
@@ -442,13 +465,13 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
     a.t1 = make_table(up);
     a.R = gate->rows;
     a.K = gate->cols;
-    a.S = p.sp1.S;
-    a.ualign = p.sp1.align;
+    a.S = p.s1.sp.S;
+    a.ualign = p.s1.sp.align;
     a.n_units = n_units_of(gate);
-    a.RB = p.RB1;
+    a.RB = p.s1.RB;
     a.RBW = 2;
-    a.RBG = p.RBG1;
-    a.xs_max = max_xs(gate, p.sp1);
+    a.RBG = p.s1.RBG;
+    a.xs_max = max_xs(gate, p.s1.sp);
     a.t_rows = p.rows1;
     a.x_bf16 = x_bf16;
     a.x_f32 = nullptr;
@@ -456,7 +479,7 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
     a.part = (float *)(ws + p.off_part1);
     size_t lds1 = sizeof(uint32_t) * (size_t)a.t_rows * a.xs_max;
     if (phases & 1) {
-        launch_grouped<kGateUp>(gate->qtype, a.t_rows, dim3(p.G * p.RBG1 * p.sp1.S), dim3(64 * kWgWaves), lds1, s, a);
+        launch_grouped<kGateUp>(gate->qtype, a.t_rows, p.s1.rtw, dim3(p.G * p.s1.RBG * p.s1.sp.S), lds1, s, a);
         if ((st = launch_status())) return st;
     }
     if (!(phases & 2)) return MI_OK;
@@ -467,7 +490,7 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
     {
         const size_t n4 = (size_t)p.NS * gate->rows / 4;
         hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n4 + 63) / 64)), dim3(64), 0, s,
-                           (const float *)(ws + p.off_part1), p.sp1.S, p.NS, gate->rows, limit, h);
+                           (const float *)(ws + p.off_part1), p.s1.sp.S, p.NS, gate->rows, limit, h);
         if ((st = launch_status())) return st;
     }
     KArgs b = a;
@@ -475,23 +498,23 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
     b.t1 = b.t0;
     b.R = down->rows;
     b.K = down->cols;
-    b.S = p.sp2.S;
-    b.ualign = p.sp2.align;
+    b.S = p.s2.sp.S;
+    b.ualign = p.s2.sp.align;
     b.n_units = n_units_of(down);
-    b.RB = p.RB2;
+    b.RB = p.s2.RB;
     b.RBW = kWgWaves;
-    b.RBG = p.RBG2;
-    b.xs_max = max_xs(down, p.sp2);
+    b.RBG = p.s2.RBG;
+    b.xs_max = max_xs(down, p.s2.sp);
     b.t_rows = p.rows2;
     b.x_bf16 = nullptr;
     b.x_f32 = h;
     b.x_stride = gate->rows;
     b.part = (float *)(ws + p.off_part2);
     size_t lds2 = sizeof(uint32_t) * 2 * (size_t)b.t_rows * b.xs_max;
-    launch_grouped<kDown>(down->qtype, b.t_rows, dim3(p.G * p.RBG2 * p.sp2.S), dim3(64 * kWgWaves), lds2, s, b);
+    launch_grouped<kDown>(down->qtype, b.t_rows, p.s2.rtw, dim3(p.G * p.s2.RBG * p.s2.sp.S), lds2, s, b);
     if ((st = launch_status())) return st;
     const int D = down->rows, nthr = N * (D / 4);
-    hipLaunchKernelGGL(combine_kernel, dim3((nthr + 63) / 64), dim3(64), 0, s, b.part, p.sp2.S, p.NS, D, N, k, idx, w,
+    hipLaunchKernelGGL(combine_kernel, dim3((nthr + 63) / 64), dim3(64), 0, s, b.part, p.s2.sp.S, p.NS, D, N, k, idx, w,
                        gate->n_experts, shared_expert, N * k, out_f32, out_bf16);
     return launch_status();
 }
@@ -505,16 +528,15 @@ int mi_moe_decode(const mi_table *gate, const mi_table *up, const mi_table *down
 
 // Split count of mi_matvec: a function of (table, n_slots) only, so the workspace size is known beforehand.  The LDS
 // budget is checked for f32 activations (the larger staging), which also covers bf16.
-static Split matvec_splits(const mi_table *t, int n_slots) {
+static Shape matvec_shape(const mi_table *t, int n_slots) {
     const int rows = class_rows(n_slots < kMaxT ? n_slots : kMaxT);
     const int G = max_groups(n_slots, t->n_experts, 0, -1, rows);
-    const int RB = t->rows / wave_rows_of(t);
-    return choose_splits(t, kMatvec, rows, G * ((RB + kWgWaves - 1) / kWgWaves), rows, 8, "MI355MOE_SMV");
+    return choose_shape(t, kMatvec, rows, G, rows, 8, "MI355MOE_SMV");
 }
 
 size_t mi_matvec_workspace(const mi_table *t, int32_t n_slots) {
     if (validate_table(t) || n_slots <= 0 || n_slots > MI_MAX_SLOTS) return 0;
-    const int S = matvec_splits(t, n_slots).S;
+    const int S = matvec_shape(t, n_slots).sp.S;
     // one split writes the output directly; more keep their partials here for the split reduction
     return S == 1 ? 256 : align256(sizeof(float) * (size_t)S * n_slots * t->rows);
 }
@@ -531,8 +553,8 @@ int mi_matvec(const mi_table *t, const int32_t *idx, int32_t n_slots, const void
     if (!workspace || workspace_bytes < need) return MI_ERR_WORKSPACE;
     const int rows = class_rows(n_slots < kMaxT ? n_slots : kMaxT);
     const int G = max_groups(n_slots, t->n_experts, 0, -1, rows);
-    const int RB = t->rows / wave_rows_of(t);
-    const Split sp = matvec_splits(t, n_slots);
+    const Shape sh = matvec_shape(t, n_slots);
+    const Split sp = sh.sp;
     const int S = sp.S;
     const int nu = n_units_of(t);
     KArgs a{};
@@ -548,9 +570,9 @@ int mi_matvec(const mi_table *t, const int32_t *idx, int32_t n_slots, const void
     a.S = S;
     a.ualign = sp.align;
     a.n_units = nu;
-    a.RB = RB;
+    a.RB = sh.RB;
     a.RBW = kWgWaves;
-    a.RBG = (RB + kWgWaves - 1) / kWgWaves;
+    a.RBG = sh.RBG;
     a.xs_max = max_xs(t, sp);
     a.t_rows = rows;
     a.x_bf16 = x_dtype == MI_X_BF16 ? (const uint16_t *)x : nullptr;
@@ -560,8 +582,7 @@ int mi_matvec(const mi_table *t, const int32_t *idx, int32_t n_slots, const void
     a.NS = n_slots;
     a.part = S == 1 ? out : (float *)workspace;
     size_t lds = sizeof(uint32_t) * (x_dtype == MI_X_F32 ? 2 : 1) * (size_t)a.t_rows * a.xs_max;
-    launch_grouped<kMatvec>(t->qtype, a.t_rows, dim3(G * a.RBG * S), dim3(64 * kWgWaves), lds, (hipStream_t)stream,
-                            a);
+    launch_grouped<kMatvec>(t->qtype, a.t_rows, sh.rtw, dim3(G * a.RBG * S), lds, (hipStream_t)stream, a);
     if ((st = launch_status()) || S == 1) return st;
     const size_t n4 = (size_t)n_slots * t->rows / 4;
     hipLaunchKernelGGL(split_reduce_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
