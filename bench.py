@@ -16,6 +16,7 @@ the timed region is bracketed by device synchronizations and HIP events on the l
 """
 import argparse
 import json
+import re
 import math
 import os
 import sys
@@ -158,6 +159,17 @@ def cpu_baseline():
             "us_per_layer": round(dt / reps * 1e6, 1)}
 
 
+def measured_traffic():
+    """HBM bytes per gate/up launch of this workload, as measured by the rocprofv3 FETCH_SIZE / WRITE_SIZE passes
+    (copy-calibrated) recorded in profiles/gateup_cb3_moe_b1_hbm_traffic.md; None when that record is absent."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "gateup_cb3_moe_b1_hbm_traffic.md")
+    try:
+        m = re.search(r"HBM bytes per gate/up launch: (\d+)", open(path).read())
+    except OSError:
+        return None
+    return int(m.group(1)) if m else None
+
+
 # ------------------------------------------------------------------------------------------------ main
 def main():
     args = parse()
@@ -249,7 +261,7 @@ def main():
                    "shared_experts": 1, "moe_intermediate": INTER, "batch": 1, "format": "CB3",
                    "layer_copies": L, "parallelism": "single-gpu"},
         "roofline": {"bound": "hbm", "achieved": round(gbsg, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbsg / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gbsg / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "kernel": "grouped_kernel<gate/up, CB3> (gate + up partials)",
                      "bytes_per_launch": int(bytesg), "us_per_launch": round(msg * 1e3, 2)},
         "cpu_baseline": cpu,

@@ -98,8 +98,9 @@ class ExpertTable:
 
 
 class _Workspaces:
-    """Zero-filled device workspaces, one per (device, stream, purpose); grown on demand.  The kernels leave their
-    completion counters at zero after every completed call, so a workspace is reused without clearing."""
+    """Device workspaces, one per (device, stream, purpose); grown on demand, zero-filled when allocated (the int8
+    kernel's completion counters start at zero and every completed call leaves them at zero; the decode and matvec
+    workspaces need no initialisation)."""
 
     def __init__(self):
         self._ws = {}
@@ -122,13 +123,13 @@ def matvec(table, idx, X):
     """moe_matvec (pallas_moe.py:238-307): out[i, r] = sum_n W_{idx[i]}[r, n] X_i[n].
     idx int32 [n_slots]; X [n_slots, K] bf16 or f32 (natural input order) -> f32 [n_slots, R]."""
     n = int(idx.numel())
-    out = torch.empty((n, table.rows), dtype=torch.float32, device=X.device)
+    out = torch.zeros((n, table.rows), dtype=torch.float32, device=X.device)      # rows of invalid ids stay 0
     return matvec_into(table, idx, X, out, None)
 
 
 def matvec_into(table, idx, X, out, workspace):
-    """``matvec`` writing into ``out`` f32 [n_slots, R]; a preallocated zero-filled ``workspace`` (uint8 tensor of
-    at least mi_matvec_workspace bytes) makes the call allocation-free."""
+    """``matvec`` writing into ``out`` f32 [n_slots, R]; a preallocated ``workspace`` (uint8 device tensor of at
+    least mi_matvec_workspace bytes) makes the call allocation-free."""
     if idx.dtype != torch.int32:
         idx = idx.to(torch.int32)
     idx = idx.contiguous()
@@ -168,8 +169,9 @@ def moe_decode(gate, up, down, x, idx, w, limit, shared_expert=-1, want_f32=True
                out_bf16=None, workspace=None, phases=3):
     """Fused decode MoE (resident.py:110-120 composition), tokens grouped by expert on the device.
     x bf16 [N, D]; idx int32 [N, k]; w f32 [N, k] -> (out_f32 [N, D] or None, out_bf16 [N, D] or None).
-    Preallocated ``out_f32`` / ``out_bf16`` / ``workspace`` (a zero-filled uint8 device tensor) make the call
-    allocation-free (graph capture).  ``phases``: 1 = gate/up/SwiGLU only, 2 = down/combine only, 3 = both."""
+    Preallocated ``out_f32`` / ``out_bf16`` / ``workspace`` (a uint8 device tensor of decode_workspace_bytes) make
+    the call allocation-free (graph capture).  ``phases``: 1 = the gate/up launch only, 2 = SwiGLU + down + combine
+    only (after a phase-1 call on the same workspace), 3 = all."""
     if x.dtype != torch.bfloat16:
         raise ValueError("decode activations are bf16")
     N, k = idx.shape
@@ -219,7 +221,8 @@ class ResidentFetch:
 
     apply(p, x, idx, w, layer, limit): x [N, D]; idx [N, k] int32 into E; w [N, k] f32 -> f32 [N, D] (routed experts
     only; the caller adds the shared expert, model.py:847-855).  N*k <= gather_max_rows takes the fused decode
-    kernels (f32 end to end, resident.py:110-120); larger calls take the grouped prefill path (resident.py:144-165).
+    kernels (f32 end to end, resident.py:110-120); larger calls would take the grouped prefill path
+    (resident.py:144-165), not built yet (NotImplementedError).
     ``use_pallas`` / ``interpret`` / ``sweep_mode`` / ``chunk`` are accepted for signature compatibility; there is a
     single MI355X kernel path per regime."""
 
@@ -258,5 +261,6 @@ class ResidentFetch:
                 raise ValueError("decode activations must be bf16-representable (the layer dtype)")
             out, _ = moe_decode(gate, up, down, xb, idx, w, limit)
             return out
-        from . import prefill
-        return prefill.moe_prefill(gate, up, down, x, idx, w, limit, tm=self.tm, combine=self.combine)
+        raise NotImplementedError("ResidentFetch.apply: N*k = %d > gather_max_rows = %d takes the grouped prefill path "
+                                  "(resident.py:144-165), which this build does not provide yet" % (N * k,
+                                                                                                     self.gather_max_rows))
