@@ -115,7 +115,7 @@ int mi_dequant(const mi_table *t, int32_t expert, float *out, void *stream);
  * x bf16 [B, n_in]; qT int8 [n_out, n_in] (the reference's q [in, out] transposed once at load);
  * s f32 [n_out].  1 <= B <= 32, n_in % 256 == 0, n_out % 16 == 0.  The weights are dequantized to bf16 in
  * registers and contracted on the matrix cores (bf16 x bf16 products are exact, f32 accumulation).
- * The workspace (zero-filled before first use, reusable after every completed call) holds split-K partials.
+ * The workspace holds split-K partials (no initialisation needed); a second launch sums them in order.
  */
 int mi_int8_project(const uint16_t *x_bf16, int32_t B, const int8_t *qT, const float *s, int32_t n_in,
                     int32_t n_out, uint16_t *y_bf16, float *y_f32, void *workspace, size_t workspace_bytes,

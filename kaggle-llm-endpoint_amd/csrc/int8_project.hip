@@ -1,127 +1,173 @@
 // int8 per-output-channel projections for gfx950: y = x @ bf16(f32(q) * s)   (quant8.py:91-99 + the x @ W uses).
 //
-// The weights stream once from HBM as int8 (qT: [n_out, n_in], input-contiguous), are dequantized in registers to
-// exactly the reference's bf16(f32(q) * s) (round to nearest even), and feed v_mfma_f32_16x16x32_bf16 with the
-// activations as the other operand (bf16 x bf16 products are exact; f32 accumulation).  A wavefront owns 16 output
-// channels x one column range; the 4 wavefronts of a workgroup split the range and reduce in LDS; KS workgroups
-// split the remaining columns and the one that completes a 16-channel tile sums the KS partials in order.
+// Weights qT [n_out, n_in] int8 (input-contiguous) stream once from HBM; every wavefront owns a 16-row tile of
+// outputs and one column split.  A lane loads 32 consecutive int8 of its row per 128-column block (4 lanes = one
+// 128-byte line per row), dequantizes them in registers to exactly the reference's bf16(f32(q) * s):
+//   f32: fma(q + 128, s, -128 s) rounds q * s once (q + 128 is an unsigned byte, so one v_cvt_f32_ubyte each);
+//   bf16: round to nearest even (v_cvt_pk_bf16_f32)
+// and feeds v_mfma_f32_16x16x32_bf16 (bf16 x bf16 products are exact, f32 accumulation) with the staged activations
+// as the B operand (up to 16 tokens per tile).  Inside a block the lane's 32 bytes are 4 k-steps of 8 columns:
+// step c of block p uses columns 128p + 32q + 8c .. +7 (q = lane / 16) for both operands.  Splits write f32
+// partials that split_reduce_i8 sums in order (no counters, deterministic); one split writes y directly.
 #include "common.h"
 
 namespace mi {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 struct I8Args {
-    const uint16_t *x;
-    const int8_t *q;
-    const float *s;
-    int B, n_in, n_out, KS;
-    uint16_t *y_bf16;
-    float *y_f32;
-    float *part;       // [KS, n_out, 32]
-    uint32_t *cnt;     // [n_out / 16]
+    const uint16_t *x;     // bf16 [B, n_in]
+    const int8_t *q;       // [n_out, n_in]
+    const float *s;        // [n_out]
+    int B, n_in, n_out, S;
+    int blocks;            // 128-column blocks per split
+    uint16_t *y_bf16;      // [B, n_out] (S == 1)
+    float *y_f32;          // [B, n_out] (S == 1)
+    float *part;           // [S, B, n_out] (S > 1)
 };
 
 constexpr int kI8Waves = 4;
+constexpr int kBufWord3 = 0x00020000;   // gfx9 buffer descriptor word 3 (32-bit data format)
+constexpr int kI8Ring = 4;          // 128-column blocks in flight per wavefront (2 KB each)
 
-__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-    return f32_to_bf16_rne(a) | (f32_to_bf16_rne(b) << 16);
+__device__ __forceinline__ uint32_t bf16_pair(float a, float b) {
+    const bf16x2 v = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(uint32_t, v);
 }
 
-template <int NT>   // token tiles of 16 (B <= 16 * NT)
+// 8 int8 weights (two dwords) of one row -> 8 bf16 = bf16(f32(q) * s), round to nearest even.
+__device__ __forceinline__ bf16x8 i8_weights8(uint32_t w0, uint32_t w1, float s, float ns128) {
+    const uint32_t u0 = w0 ^ 0x80808080u, u1 = w1 ^ 0x80808080u;       // q + 128, unsigned bytes
+    uint4 v;
+    v.x = bf16_pair(fmaf((float)(u0 & 255u), s, ns128), fmaf((float)((u0 >> 8) & 255u), s, ns128));
+    v.y = bf16_pair(fmaf((float)((u0 >> 16) & 255u), s, ns128), fmaf((float)(u0 >> 24), s, ns128));
+    v.z = bf16_pair(fmaf((float)(u1 & 255u), s, ns128), fmaf((float)((u1 >> 8) & 255u), s, ns128));
+    v.w = bf16_pair(fmaf((float)((u1 >> 16) & 255u), s, ns128), fmaf((float)(u1 >> 24), s, ns128));
+    return __builtin_bit_cast(bf16x8, v);
+}
+
+template <int TT>   // token tiles of 16 (B <= 16 * TT)
 __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
-    __shared__ float red[kI8Waves][16][16 * NT];
-    __shared__ int s_last;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int tile = blockIdx.x;               // 16 output channels
-    const int ks = blockIdx.y;
-    const int o0 = tile * 16;
-    const int i_row = lane & 15, kq = lane >> 4;
-    const int chunk = a.n_in / (a.KS * kI8Waves);      // columns per wavefront (multiple of 32)
-    const int k_begin = (ks * kI8Waves + wave) * chunk;
-    const float sc = a.s[o0 + i_row];
-    const int8_t *qrow = a.q + (size_t)(o0 + i_row) * a.n_in + k_begin + 8 * kq;
+    extern __shared__ uint32_t xs[];                 // [B][cols / 2] bf16 pairs of the split's columns
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int row_groups = (a.n_out + 16 * kI8Waves - 1) / (16 * kI8Waves);
+    const int rg = blockIdx.x % row_groups, split = blockIdx.x / row_groups;
+    const int o0 = (rg * kI8Waves + wave) * 16;
+    const bool active = o0 < a.n_out;                // wavefronts past the last 16-row tile only help stage
+    const int i = lane & 15, q = lane >> 4;
+    const int cols = 128 * a.blocks, k0 = split * cols;
 
-    f32x4 acc[NT];
+    // weights: lane's 32 bytes of block p at row o0 + i, columns k0 + 128 p + 32 q, as buffer loads from the
+    // wavefront's tile (blocks past the split use an empty-range descriptor: zeros, no memory traffic)
+    const int8_t *tile = a.q + (size_t)(active ? o0 : 0) * a.n_in + k0;
+    const __amdgpu_buffer_rsrc_t qb = __builtin_amdgcn_make_buffer_rsrc((void *)tile, (short)0, 0x7fffffff, kBufWord3);
+    const __amdgpu_buffer_rsrc_t qnull = __builtin_amdgcn_make_buffer_rsrc((void *)tile, (short)0, 0, kBufWord3);
+    const int voff = i * a.n_in + 32 * q;
+    auto load_block = [&](int p, uint4 &lo, uint4 &hi) {
+        const __amdgpu_buffer_rsrc_t r = p < a.blocks ? qb : qnull;
+        lo = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 128 * p, 0));
+        hi = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16, 128 * p, 0));
+    };
+    uint4 ring[kI8Ring][2];
+    if (active) {
 #pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
-
-    for (int k = 0; k < chunk; k += 32) {
-        const uint2 qv = *(const uint2 *)(qrow + k);
-        uint32_t wv[4];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const uint32_t u = h ? qv.y : qv.x;
-            const float f0 = (float)(int8_t)(u & 255u) * sc;
-            const float f1 = (float)(int8_t)((u >> 8) & 255u) * sc;
-            const float f2 = (float)(int8_t)((u >> 16) & 255u) * sc;
-            const float f3 = (float)(int8_t)(u >> 24) * sc;
-            wv[2 * h] = pack_bf16x2(f0, f1);
-            wv[2 * h + 1] = pack_bf16x2(f2, f3);
-        }
-        const bf16x8 A = __builtin_bit_cast(bf16x8, make_uint4(wv[0], wv[1], wv[2], wv[3]));
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const int tok = 16 * t + i_row;
-            uint4 xv = make_uint4(0, 0, 0, 0);
-            if (tok < a.B) xv = *(const uint4 *)(a.x + (size_t)tok * a.n_in + k_begin + k + 8 * kq);
-            const bf16x8 Bv = __builtin_bit_cast(bf16x8, xv);
-            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, Bv, acc[t], 0, 0, 0);
-        }
+        for (int d = 0; d < kI8Ring; ++d) load_block(d, ring[d][0], ring[d][1]);
     }
-    // C layout: lane holds rows (channels) 4*kq + r, column (token) i_row
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) red[wave][4 * kq + r][16 * t + i_row] = acc[t][r];
-    __syncthreads();
-
-    const int ntok = 16 * NT;
-    if (a.KS == 1) {
-        for (int i = tid; i < 16 * ntok; i += blockDim.x) {
-            const int c = i / ntok, b = i - c * ntok;
-            if (b >= a.B) continue;
-            float v = 0.f;
-#pragma unroll
-            for (int wv = 0; wv < kI8Waves; ++wv) v += red[wv][c][b];
-            if (a.y_f32) a.y_f32[(size_t)b * a.n_out + o0 + c] = v;
-            if (a.y_bf16) a.y_bf16[(size_t)b * a.n_out + o0 + c] = (uint16_t)f32_to_bf16_rne(v);
-        }
-        return;
-    }
-    for (int i = tid; i < 16 * ntok; i += blockDim.x) {
-        const int c = i / ntok, b = i - c * ntok;
-        float v = 0.f;
-#pragma unroll
-        for (int wv = 0; wv < kI8Waves; ++wv) v += red[wv][c][b];
-        a.part[((size_t)ks * a.n_out + o0 + c) * 32 + b] = v;
+    // stage the activations of the split (bf16 pairs), rows < B
+    const int cw = cols / 2;                         // dwords per staged row
+    for (int e = tid; e < a.B * (cw / 4); e += blockDim.x) {
+        const int b = e / (cw / 4), c4 = e - b * (cw / 4);
+        *(uint4 *)(xs + b * cw + 4 * c4) = *(const uint4 *)(a.x + (size_t)b * a.n_in + k0 + 8 * c4);
     }
     __syncthreads();
-    if (tid == 0) {
-        fence_release_agent();
-        s_last = counter_add(a.cnt + tile, 1u) == (uint32_t)(a.KS - 1);
+    if (!active) return;
+    const float sc = a.s[o0 + i];
+    const float ns128 = -128.0f * sc;
+
+    f32x4 acc[TT];
+#pragma unroll
+    for (int t = 0; t < TT; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    // B-operand rows: token jt of tile t (rows >= B read row B-1; those accumulator columns are not stored)
+    const uint32_t *xrow[TT];
+#pragma unroll
+    for (int t = 0; t < TT; ++t) xrow[t] = xs + min(16 * t + i, a.B - 1) * cw + 16 * q;
+
+    for (int p0 = 0; p0 < a.blocks; p0 += kI8Ring) {
+#pragma unroll
+        for (int d = 0; d < kI8Ring; ++d) {
+            const int p = p0 + d;
+            if (p >= a.blocks) break;
+            const uint4 w0 = ring[d][0], w1 = ring[d][1];
+            load_block(p + kI8Ring, ring[d][0], ring[d][1]);
+            const uint32_t W[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const bf16x8 A = i8_weights8(W[2 * c], W[2 * c + 1], sc, ns128);
+#pragma unroll
+                for (int t = 0; t < TT; ++t) {
+                    const uint4 xv = *(const uint4 *)(xrow[t] + 64 * p + 4 * c);
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, __builtin_bit_cast(bf16x8, xv), acc[t], 0, 0,
+                                                                     0);
+                }
+            }
+        }
     }
-    __syncthreads();
-    if (!s_last) return;
-    fence_acquire_agent();
-    for (int i = tid; i < 16 * ntok; i += blockDim.x) {
-        const int c = i / ntok, b = i - c * ntok;
+    // C layout: lane (jt = lane % 16, q) holds output rows o0 + 4q + r for token 16 t + jt
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+        const int b = 16 * t + i;
         if (b >= a.B) continue;
-        float v = 0.f;
-        for (int s = 0; s < a.KS; ++s) v += a.part[((size_t)s * a.n_out + o0 + c) * 32 + b];
-        if (a.y_f32) a.y_f32[(size_t)b * a.n_out + o0 + c] = v;
-        if (a.y_bf16) a.y_bf16[(size_t)b * a.n_out + o0 + c] = (uint16_t)f32_to_bf16_rne(v);
+        const int o = o0 + 4 * q;
+        if (a.S == 1) {
+            if (a.y_f32) *(float4 *)(a.y_f32 + (size_t)b * a.n_out + o) = make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
+            if (a.y_bf16) {
+                uint2 v;
+                v.x = f32_to_bf16_rne(acc[t][0]) | (f32_to_bf16_rne(acc[t][1]) << 16);
+                v.y = f32_to_bf16_rne(acc[t][2]) | (f32_to_bf16_rne(acc[t][3]) << 16);
+                *(uint2 *)(a.y_bf16 + (size_t)b * a.n_out + o) = v;
+            }
+        } else {
+            *(float4 *)(a.part + ((size_t)split * a.B + b) * a.n_out + o) = make_float4(acc[t][0], acc[t][1], acc[t][2],
+                                                                                     acc[t][3]);
+        }
     }
-    if (tid == 0) counter_reset(a.cnt + tile);
 }
 
-static int i8_splits(int n_in, int n_out) {
-    const int tiles = n_out / 16;
-    int KS = 1;
-    // enough workgroups to cover the chip; every wavefront keeps >= 256 columns (8 MFMA steps)
-    while (tiles * KS < 512 && n_in % (2 * KS * kI8Waves * 32) == 0 && n_in / (2 * KS * kI8Waves) >= 256) KS *= 2;
-    return KS;
+// y[b, o] = sum_s part[s, b, o], splits in order; f32 and/or bf16 out.  One thread per 4 outputs.
+__global__ void __launch_bounds__(256) split_reduce_i8(const float *__restrict__ part, int S, int n, float *y_f32,
+                                                       uint16_t *y_bf16) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n / 4) return;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s = 0; s < S; ++s) {
+        const float4 p = ((const float4 *)(part + (size_t)s * n))[i];
+        v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
+    }
+    if (y_f32) ((float4 *)y_f32)[i] = v;
+    if (y_bf16) {
+        uint2 b;
+        b.x = f32_to_bf16_rne(v.x) | (f32_to_bf16_rne(v.y) << 16);
+        b.y = f32_to_bf16_rne(v.z) | (f32_to_bf16_rne(v.w) << 16);
+        ((uint2 *)y_bf16)[i] = b;
+    }
+}
+
+// Column splits: enough wavefronts to cover the chip (about 3 per SIMD, 3072 over 256 CUs), every wavefront
+// streaming at least 4 blocks of 128 columns, the split's staged activations within 48 KB of LDS.
+static int i8_splits(int B, int n_in, int n_out) {
+    const int tiles = n_out / 16, nblk = n_in / 128;
+    int best = 1;
+    for (int S = 1; S <= nblk; ++S) {
+        if (nblk % S) continue;
+        if ((size_t)B * (n_in / S) * 2 > 48 * 1024) continue;
+        if (nblk / S < 4 && S > 1) break;
+        best = S;
+        if ((long long)tiles * S >= 3072) break;
+    }
+    return best;
 }
 
 }  // namespace mi
@@ -132,9 +178,8 @@ extern "C" {
 
 size_t mi_int8_project_workspace(int32_t B, int32_t n_in, int32_t n_out) {
     if (B <= 0 || B > 32 || n_in <= 0 || n_out <= 0 || n_in % 256 || n_out % 16) return 0;
-    const int KS = i8_splits(n_in, n_out);
-    const size_t cnt = ((sizeof(uint32_t) * (size_t)(n_out / 16)) + 255) & ~(size_t)255;
-    return cnt + sizeof(float) * (size_t)KS * n_out * 32;
+    const int S = i8_splits(B, n_in, n_out);
+    return S == 1 ? 256 : sizeof(float) * (size_t)S * B * n_out;
 }
 
 int mi_int8_project(const uint16_t *x_bf16, int32_t B, const int8_t *qT, const float *s, int32_t n_in,
@@ -152,15 +197,20 @@ int mi_int8_project(const uint16_t *x_bf16, int32_t B, const int8_t *qT, const f
     a.B = B;
     a.n_in = n_in;
     a.n_out = n_out;
-    a.KS = i8_splits(n_in, n_out);
+    a.S = i8_splits(B, n_in, n_out);
+    a.blocks = n_in / 128 / a.S;
     a.y_bf16 = y_bf16;
     a.y_f32 = y_f32;
-    const size_t cnt = ((sizeof(uint32_t) * (size_t)(n_out / 16)) + 255) & ~(size_t)255;
-    a.cnt = (uint32_t *)workspace;
-    a.part = (float *)((char *)workspace + cnt);
-    dim3 grid(n_out / 16, a.KS);
-    if (B <= 16) hipLaunchKernelGGL(int8_project_kernel<1>, grid, dim3(64 * kI8Waves), 0, (hipStream_t)stream, a);
-    else hipLaunchKernelGGL(int8_project_kernel<2>, grid, dim3(64 * kI8Waves), 0, (hipStream_t)stream, a);
+    a.part = (float *)workspace;
+    const dim3 grid((n_out + 16 * kI8Waves - 1) / (16 * kI8Waves) * a.S);
+    const size_t lds = sizeof(uint16_t) * (size_t)B * 128 * a.blocks;
+    hipStream_t st = (hipStream_t)stream;
+    if (B <= 16) hipLaunchKernelGGL(int8_project_kernel<1>, grid, dim3(64 * kI8Waves), lds, st, a);
+    else hipLaunchKernelGGL(int8_project_kernel<2>, grid, dim3(64 * kI8Waves), lds, st, a);
+    if (hipGetLastError() != hipSuccess) return MI_ERR_LAUNCH;
+    if (a.S == 1) return MI_OK;
+    const int n = B * n_out;
+    hipLaunchKernelGGL(split_reduce_i8, dim3((n / 4 + 255) / 256), dim3(256), 0, st, a.part, a.S, n, y_f32, y_bf16);
     return hipGetLastError() == hipSuccess ? MI_OK : MI_ERR_LAUNCH;
 }
 
