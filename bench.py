@@ -15,6 +15,7 @@ the timed region is bracketed by device synchronizations and HIP events on the l
     python bench.py [--gpus 1] [--steps 200] [--warmup 20]
 """
 import argparse
+import ctypes
 import json
 import re
 import math
@@ -277,27 +278,36 @@ def main():
 
 def bench_int8(torch, pkg, gen, args):
     """Config: the int8 dense projections at batch 8 (Q, K, V, O 6144x6144; shared gate/up 6144->2048; shared down
-    2048->6144), per-output-channel scales, bf16 activations.  3 weight copies rotated (> Infinity Cache)."""
-    shapes = [(6144, 6144)] * 4 + [(6144, 2048)] * 2 + [(2048, 6144)]
+    2048->6144), per-output-channel scales, bf16 activations.  A step is the layer's four dependent stages -- Q/K/V of
+    the attention input in one launch, O, the shared expert's gate and up in one launch, its down -- so projections
+    that share their input share a launch, as they can in the model.  3 weight copies rotated (> the last-level
+    cache)."""
+    stages = [[(6144, 6144)] * 3, [(6144, 6144)], [(6144, 2048)] * 2, [(2048, 6144)]]
     B = 8
     copies = 3
     fns = []
-    total = sum(i * o + 4 * o for i, o in shapes)
+    total = sum(i * o + 4 * o for st in stages for i, o in st)
     for c in range(copies):
         ops = []
-        for (n_in, n_out) in shapes:
-            qT = torch.randint(-127, 128, (n_out, n_in), dtype=torch.int8, device="cuda", generator=gen)
-            s = torch.rand((n_out,), device="cuda", generator=gen) * 1.5e-3 + 0.5e-3
+        for st in stages:
+            n_in = st[0][0]
             x = torch.randn((B, n_in), device="cuda", generator=gen).to(torch.bfloat16)
-            y = torch.empty((B, n_out), dtype=torch.bfloat16, device="cuda")
-            ws = torch.zeros(pkg._lib.lib().mi_int8_project_workspace(B, n_in, n_out), dtype=torch.uint8,
-                             device="cuda")
-            ops.append((x, qT, s, y, ws))
-        fns.append(lambda ops=ops: [pkg.int8_project(x, qT, s, y_bf16=y, workspace=ws) for (x, qT, s, y, ws) in ops])
+            projs, outs = [], []
+            for (_, n_out) in st:
+                qT = torch.randint(-127, 128, (n_out, n_in), dtype=torch.int8, device="cuda", generator=gen)
+                s = torch.rand((n_out,), device="cuda", generator=gen) * 1.5e-3 + 0.5e-3
+                projs.append((qT, s))
+                outs.append((torch.empty((B, n_out), dtype=torch.bfloat16, device="cuda"), None))
+            n_outs = (ctypes.c_int32 * len(st))(*[o for _, o in st])
+            ws = torch.zeros(max(256, pkg._lib.lib().mi_int8_project_many_workspace(B, n_in, n_outs, len(st))),
+                             dtype=torch.uint8, device="cuda")
+            ops.append((x, projs, outs, ws))
+        fns.append(lambda ops=ops: [pkg.int8_project_many(x, projs, outputs=outs, workspace=ws)
+                                    for (x, projs, outs, ws) in ops])
     ms = Timer(torch, fns).run(args.steps, args.warmup)
     gbs = total / (ms * 1e-3) / 1e9
     return {"us_per_7_projections": round(ms * 1e3, 2), "GBps": round(gbs, 1), "pct_hbm": round(100 * gbs / HBM_PEAK_GBS, 1),
-            "bytes": int(total)}
+            "bytes": int(total), "launches": "Q+K+V | O | gate+up | down"}
 
 
 def bench_matvec(torch, pkg, gen, args):

@@ -12,7 +12,7 @@
  *   ragged_plan(idx, w, E, tm)                             pallas_moe.py:564-592 -> mi_ragged_plan
  *   moe_ragged_gateup / moe_ragged_down                    pallas_moe.py:622-755 -> mi_moe_prefill
  *   dequant_planes (XLA dequant of the planar tables)      planes.py:196-206     -> mi_dequant
- *   quant8.dequant_tree + x @ W (int8 projections)         quant8.py:91-99       -> mi_int8_project
+ *   quant8.dequant_tree + x @ W (int8 projections)         quant8.py:91-99       -> mi_int8_project(_many)
  */
 #ifndef MI355MOE_H
 #define MI355MOE_H
@@ -121,6 +121,22 @@ int mi_int8_project(const uint16_t *x_bf16, int32_t B, const int8_t *qT, const f
                     int32_t n_out, uint16_t *y_bf16, float *y_f32, void *workspace, size_t workspace_bytes,
                     void *stream);
 size_t mi_int8_project_workspace(int32_t B, int32_t n_in, int32_t n_out);
+
+/*
+ * Several int8 projections of the same activations in one launch (Q, K, V of x; the shared expert's gate and up):
+ * projs[j] = {qT [n_out_j, n_in], s [n_out_j], n_out_j, y_bf16 and/or y_f32 [B, n_out_j]}, 1 <= n_proj <= 8.
+ * Each output equals what mi_int8_project gives for that projection alone.
+ */
+typedef struct mi_i8_proj {
+    const int8_t *qT;
+    const float *s;
+    int32_t n_out;
+    uint16_t *y_bf16;
+    float *y_f32;
+} mi_i8_proj;
+int mi_int8_project_many(const uint16_t *x_bf16, int32_t B, int32_t n_in, const mi_i8_proj *projs, int32_t n_proj,
+                         void *workspace, size_t workspace_bytes, void *stream);
+size_t mi_int8_project_many_workspace(int32_t B, int32_t n_in, const int32_t *n_out, int32_t n_proj);
 
 const char *mi_strerror(int status);
 int mi_version(void);

@@ -5,8 +5,8 @@ The directory name is not a Python identifier; it is imported as ``kaggle_llm_en
 ``load_package()`` of ``__graft_entry__`` / ``tests/conftest.py``.
 """
 from . import _lib, formats  # noqa: F401
-from .resident import (ExpertTable, ResidentFetch, dequant, int8_project, matvec, moe_decode,  # noqa: F401
-                       to_device_planes)
+from .resident import (ExpertTable, ResidentFetch, dequant, int8_project, int8_project_many, matvec,  # noqa: F401
+                       moe_decode, to_device_planes)
 
-__all__ = ["ExpertTable", "ResidentFetch", "dequant", "int8_project", "matvec", "moe_decode", "to_device_planes",
-           "formats"]
+__all__ = ["ExpertTable", "ResidentFetch", "dequant", "int8_project", "int8_project_many", "matvec", "moe_decode",
+           "to_device_planes", "formats"]

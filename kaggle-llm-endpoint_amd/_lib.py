@@ -21,12 +21,18 @@ PLANE_KEYS = {"CB3": ("qs", "cb"), "IQ3_S": ("qs", "sg", "qh", "sc", "d")}
 
 # every symbol the header declares (tests check the library exports them)
 EXPORTS = ("mi_matvec", "mi_matvec_workspace", "mi_moe_decode", "mi_moe_decode_phases", "mi_moe_decode_workspace",
-           "mi_dequant", "mi_int8_project", "mi_int8_project_workspace", "mi_strerror", "mi_version")
+           "mi_dequant", "mi_int8_project", "mi_int8_project_workspace", "mi_int8_project_many",
+           "mi_int8_project_many_workspace", "mi_strerror", "mi_version")
 
 
 class MiTable(ctypes.Structure):
     _fields_ = [("qtype", ctypes.c_int32), ("rows", ctypes.c_int32), ("cols", ctypes.c_int32),
                 ("n_experts", ctypes.c_int32), ("plane", ctypes.c_void_p * 5)]
+
+
+class MiI8Proj(ctypes.Structure):
+    _fields_ = [("qT", ctypes.c_void_p), ("s", ctypes.c_void_p), ("n_out", ctypes.c_int32),
+                ("y_bf16", ctypes.c_void_p), ("y_f32", ctypes.c_void_p)]
 
 
 class MiError(RuntimeError):
@@ -58,6 +64,8 @@ def lib():
         "mi_dequant": (I, [T, I, P, P]),
         "mi_int8_project": (I, [P, I, P, P, I, I, P, P, P, Z, P]),
         "mi_int8_project_workspace": (Z, [I, I, I]),
+        "mi_int8_project_many": (I, [P, I, I, ctypes.POINTER(MiI8Proj), I, P, Z, P]),
+        "mi_int8_project_many_workspace": (Z, [I, I, ctypes.POINTER(ctypes.c_int32), I]),
         "mi_strerror": (ctypes.c_char_p, [I]),
         "mi_version": (I, []),
     }

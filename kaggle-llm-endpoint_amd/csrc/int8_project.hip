@@ -11,21 +11,32 @@
 // partials that split_reduce_i8 sums in order (no counters, deterministic); one split writes y directly.
 #include "common.h"
 
+#include <stdlib.h>
+
 namespace mi {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-struct I8Args {
-    const uint16_t *x;     // bf16 [B, n_in]
+constexpr int kI8MaxProj = 8;      // projections sharing one activation matrix per launch
+
+struct I8Proj {
     const int8_t *q;       // [n_out, n_in]
     const float *s;        // [n_out]
-    int B, n_in, n_out, S;
-    int blocks;            // 128-column blocks per split
+    int n_out;
     uint16_t *y_bf16;      // [B, n_out] (S == 1)
     float *y_f32;          // [B, n_out] (S == 1)
     float *part;           // [S, B, n_out] (S > 1)
+};
+
+struct I8Args {
+    const uint16_t *x;     // bf16 [B, n_in], shared by every projection
+    int B, n_in, S;
+    int blocks;            // 128-column blocks per split
+    int n_proj;
+    int wg_start[kI8MaxProj + 1];   // first workgroup of each projection
+    I8Proj p[kI8MaxProj];
 };
 
 constexpr int kI8Waves = 4;
@@ -53,16 +64,20 @@ __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
     extern __shared__ uint32_t xs[];                 // [B][cols / 2] bf16 pairs of the split's columns
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int row_groups = (a.n_out + 16 * kI8Waves - 1) / (16 * kI8Waves);
-    const int rg = blockIdx.x % row_groups, split = blockIdx.x / row_groups;
+    int pj = 0;
+    while (pj + 1 < a.n_proj && (int)blockIdx.x >= a.wg_start[pj + 1]) ++pj;
+    const I8Proj &P = a.p[pj];
+    const int local = blockIdx.x - a.wg_start[pj];
+    const int row_groups = (P.n_out + 16 * kI8Waves - 1) / (16 * kI8Waves);
+    const int rg = local % row_groups, split = local / row_groups;
     const int o0 = (rg * kI8Waves + wave) * 16;
-    const bool active = o0 < a.n_out;                // wavefronts past the last 16-row tile only help stage
+    const bool active = o0 < P.n_out;                // wavefronts past the last 16-row tile only help stage
     const int i = lane & 15, q = lane >> 4;
     const int cols = 128 * a.blocks, k0 = split * cols;
 
     // weights: lane's 32 bytes of block p at row o0 + i, columns k0 + 128 p + 32 q, as buffer loads from the
     // wavefront's tile (blocks past the split use an empty-range descriptor: zeros, no memory traffic)
-    const int8_t *tile = a.q + (size_t)(active ? o0 : 0) * a.n_in + k0;
+    const int8_t *tile = P.q + (size_t)(active ? o0 : 0) * a.n_in + k0;
     const __amdgpu_buffer_rsrc_t qb = __builtin_amdgcn_make_buffer_rsrc((void *)tile, (short)0, 0x7fffffff, kBufWord3);
     const __amdgpu_buffer_rsrc_t qnull = __builtin_amdgcn_make_buffer_rsrc((void *)tile, (short)0, 0, kBufWord3);
     const int voff = i * a.n_in + 32 * q;
@@ -84,7 +99,7 @@ __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
     }
     __syncthreads();
     if (!active) return;
-    const float sc = a.s[o0 + i];
+    const float sc = P.s[o0 + i];
     const float ns128 = -128.0f * sc;
 
     f32x4 acc[TT];
@@ -122,43 +137,57 @@ __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
         if (b >= a.B) continue;
         const int o = o0 + 4 * q;
         if (a.S == 1) {
-            if (a.y_f32) *(float4 *)(a.y_f32 + (size_t)b * a.n_out + o) = make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
-            if (a.y_bf16) {
+            if (P.y_f32) *(float4 *)(P.y_f32 + (size_t)b * P.n_out + o) = make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
+            if (P.y_bf16) {
                 uint2 v;
                 v.x = f32_to_bf16_rne(acc[t][0]) | (f32_to_bf16_rne(acc[t][1]) << 16);
                 v.y = f32_to_bf16_rne(acc[t][2]) | (f32_to_bf16_rne(acc[t][3]) << 16);
-                *(uint2 *)(a.y_bf16 + (size_t)b * a.n_out + o) = v;
+                *(uint2 *)(P.y_bf16 + (size_t)b * P.n_out + o) = v;
             }
         } else {
-            *(float4 *)(a.part + ((size_t)split * a.B + b) * a.n_out + o) = make_float4(acc[t][0], acc[t][1], acc[t][2],
+            *(float4 *)(P.part + ((size_t)split * a.B + b) * P.n_out + o) = make_float4(acc[t][0], acc[t][1], acc[t][2],
                                                                                      acc[t][3]);
         }
     }
 }
 
-// y[b, o] = sum_s part[s, b, o], splits in order; f32 and/or bf16 out.  One thread per 4 outputs.
-__global__ void __launch_bounds__(256) split_reduce_i8(const float *__restrict__ part, int S, int n, float *y_f32,
-                                                       uint16_t *y_bf16) {
+// y[b, o] = sum_s part[s, b, o] of every projection, splits in order; f32 and/or bf16 out.  One thread per 4 outputs;
+// projection j owns threads [q4_start[j], q4_start[j + 1]).
+__global__ void __launch_bounds__(256) split_reduce_i8(I8Args a) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n / 4) return;
+    int pj = 0, base = 0;
+    while (pj < a.n_proj && i >= base + a.B * a.p[pj].n_out / 4) base += a.B * a.p[pj++].n_out / 4;
+    if (pj >= a.n_proj) return;
+    const I8Proj &P = a.p[pj];
+    const int n = a.B * P.n_out, li = i - base;
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s = 0; s < S; ++s) {
-        const float4 p = ((const float4 *)(part + (size_t)s * n))[i];
-        v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
+    for (int s0 = 0; s0 < a.S; s0 += 8) {             // 8 independent loads in flight, summed in split order
+        float4 p[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            p[j] = s0 + j < a.S ? ((const float4 *)(P.part + (size_t)(s0 + j) * n))[li] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            v.x += p[j].x; v.y += p[j].y; v.z += p[j].z; v.w += p[j].w;
+        }
     }
-    if (y_f32) ((float4 *)y_f32)[i] = v;
-    if (y_bf16) {
+    if (P.y_f32) ((float4 *)P.y_f32)[li] = v;
+    if (P.y_bf16) {
         uint2 b;
         b.x = f32_to_bf16_rne(v.x) | (f32_to_bf16_rne(v.y) << 16);
         b.y = f32_to_bf16_rne(v.z) | (f32_to_bf16_rne(v.w) << 16);
-        ((uint2 *)y_bf16)[i] = b;
+        ((uint2 *)P.y_bf16)[li] = b;
     }
 }
 
 // Column splits: enough wavefronts to cover the chip (about 3 per SIMD, 3072 over 256 CUs), every wavefront
-// streaming at least 4 blocks of 128 columns, the split's staged activations within 48 KB of LDS.
-static int i8_splits(int B, int n_in, int n_out) {
-    const int tiles = n_out / 16, nblk = n_in / 128;
+// streaming at least 4 blocks of 128 columns, the split's staged activations within 48 KB of LDS.  `tiles` counts
+// the 16-row tiles of every projection of the launch.
+static int i8_splits(int B, int n_in, int tiles) {
+    const int nblk = n_in / 128;
+    const char *env = getenv("MI355MOE_I8S");      // experiments: a forced split count (must divide n_in / 128)
+    if (env && atoi(env) > 0 && nblk % atoi(env) == 0 && (size_t)B * (n_in / atoi(env)) * 2 <= 48 * 1024)
+        return atoi(env);
     int best = 1;
     for (int S = 1; S <= nblk; ++S) {
         if (nblk % S) continue;
@@ -170,16 +199,80 @@ static int i8_splits(int B, int n_in, int n_out) {
     return best;
 }
 
+static int i8_tiles(const int32_t *n_out, int n_proj) {
+    int t = 0;
+    for (int j = 0; j < n_proj; ++j) t += n_out[j] / 16;
+    return t;
+}
+
 }  // namespace mi
 
 using namespace mi;
 
 extern "C" {
 
+size_t mi_int8_project_many_workspace(int32_t B, int32_t n_in, const int32_t *n_out, int32_t n_proj) {
+    if (B <= 0 || B > 32 || n_in <= 0 || n_in % 256 || !n_out || n_proj <= 0 || n_proj > kI8MaxProj) return 0;
+    size_t total = 0;
+    for (int j = 0; j < n_proj; ++j) {
+        if (n_out[j] <= 0 || n_out[j] % 16) return 0;
+        total += (size_t)n_out[j];
+    }
+    const int S = i8_splits(B, n_in, i8_tiles(n_out, n_proj));
+    return S == 1 ? 256 : sizeof(float) * (size_t)S * B * total;
+}
+
+int mi_int8_project_many(const uint16_t *x_bf16, int32_t B, int32_t n_in, const mi_i8_proj *projs, int32_t n_proj,
+                         void *workspace, size_t workspace_bytes, void *stream) {
+    if (!x_bf16 || !projs) return MI_ERR_NULL;
+    if (B <= 0 || B > 32) return MI_ERR_TOKENS;
+    if (n_proj <= 0 || n_proj > kI8MaxProj) return MI_ERR_ARG;
+    if (n_in <= 0 || n_in % 256) return MI_ERR_SHAPE;
+    int32_t n_out[kI8MaxProj];
+    for (int j = 0; j < n_proj; ++j) {
+        const mi_i8_proj &p = projs[j];
+        if (!p.qT || !p.s || (!p.y_bf16 && !p.y_f32)) return MI_ERR_NULL;
+        if (p.n_out <= 0 || p.n_out % 16) return MI_ERR_SHAPE;
+        n_out[j] = p.n_out;
+    }
+    const size_t need = mi_int8_project_many_workspace(B, n_in, n_out, n_proj);
+    if (!workspace || workspace_bytes < need) return MI_ERR_WORKSPACE;
+    I8Args a{};
+    a.x = x_bf16;
+    a.B = B;
+    a.n_in = n_in;
+    a.S = i8_splits(B, n_in, i8_tiles(n_out, n_proj));
+    a.blocks = n_in / 128 / a.S;
+    a.n_proj = n_proj;
+    size_t off = 0;
+    int wg = 0;
+    for (int j = 0; j < n_proj; ++j) {
+        I8Proj &p = a.p[j];
+        p.q = projs[j].qT;
+        p.s = projs[j].s;
+        p.n_out = projs[j].n_out;
+        p.y_bf16 = projs[j].y_bf16;
+        p.y_f32 = projs[j].y_f32;
+        p.part = (float *)workspace + off;
+        off += (size_t)a.S * B * p.n_out;
+        a.wg_start[j] = wg;
+        wg += (p.n_out + 16 * kI8Waves - 1) / (16 * kI8Waves) * a.S;
+    }
+    a.wg_start[n_proj] = wg;
+    const size_t lds = sizeof(uint16_t) * (size_t)B * 128 * a.blocks;
+    hipStream_t st = (hipStream_t)stream;
+    if (B <= 16) hipLaunchKernelGGL(int8_project_kernel<1>, dim3(wg), dim3(64 * kI8Waves), lds, st, a);
+    else hipLaunchKernelGGL(int8_project_kernel<2>, dim3(wg), dim3(64 * kI8Waves), lds, st, a);
+    if (hipGetLastError() != hipSuccess) return MI_ERR_LAUNCH;
+    if (a.S == 1) return MI_OK;
+    int n4 = 0;
+    for (int j = 0; j < n_proj; ++j) n4 += B * a.p[j].n_out / 4;
+    hipLaunchKernelGGL(split_reduce_i8, dim3((n4 + 255) / 256), dim3(256), 0, st, a);
+    return hipGetLastError() == hipSuccess ? MI_OK : MI_ERR_LAUNCH;
+}
+
 size_t mi_int8_project_workspace(int32_t B, int32_t n_in, int32_t n_out) {
-    if (B <= 0 || B > 32 || n_in <= 0 || n_out <= 0 || n_in % 256 || n_out % 16) return 0;
-    const int S = i8_splits(B, n_in, n_out);
-    return S == 1 ? 256 : sizeof(float) * (size_t)S * B * n_out;
+    return mi_int8_project_many_workspace(B, n_in, &n_out, 1);
 }
 
 int mi_int8_project(const uint16_t *x_bf16, int32_t B, const int8_t *qT, const float *s, int32_t n_in,
@@ -188,30 +281,8 @@ int mi_int8_project(const uint16_t *x_bf16, int32_t B, const int8_t *qT, const f
     if (!x_bf16 || !qT || !s || (!y_bf16 && !y_f32)) return MI_ERR_NULL;
     if (B <= 0 || B > 32) return MI_ERR_TOKENS;
     if (n_in <= 0 || n_out <= 0 || n_in % 256 || n_out % 16) return MI_ERR_SHAPE;
-    const size_t need = mi_int8_project_workspace(B, n_in, n_out);
-    if (!workspace || workspace_bytes < need) return MI_ERR_WORKSPACE;
-    I8Args a{};
-    a.x = x_bf16;
-    a.q = qT;
-    a.s = s;
-    a.B = B;
-    a.n_in = n_in;
-    a.n_out = n_out;
-    a.S = i8_splits(B, n_in, n_out);
-    a.blocks = n_in / 128 / a.S;
-    a.y_bf16 = y_bf16;
-    a.y_f32 = y_f32;
-    a.part = (float *)workspace;
-    const dim3 grid((n_out + 16 * kI8Waves - 1) / (16 * kI8Waves) * a.S);
-    const size_t lds = sizeof(uint16_t) * (size_t)B * 128 * a.blocks;
-    hipStream_t st = (hipStream_t)stream;
-    if (B <= 16) hipLaunchKernelGGL(int8_project_kernel<1>, grid, dim3(64 * kI8Waves), lds, st, a);
-    else hipLaunchKernelGGL(int8_project_kernel<2>, grid, dim3(64 * kI8Waves), lds, st, a);
-    if (hipGetLastError() != hipSuccess) return MI_ERR_LAUNCH;
-    if (a.S == 1) return MI_OK;
-    const int n = B * n_out;
-    hipLaunchKernelGGL(split_reduce_i8, dim3((n / 4 + 255) / 256), dim3(256), 0, st, a.part, a.S, n, y_f32, y_bf16);
-    return hipGetLastError() == hipSuccess ? MI_OK : MI_ERR_LAUNCH;
+    const mi_i8_proj p{qT, s, n_out, y_bf16, y_f32};
+    return mi_int8_project_many(x_bf16, B, n_in, &p, 1, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

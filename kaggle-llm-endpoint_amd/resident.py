@@ -215,6 +215,35 @@ def int8_project(x, qT, s, want_f32=False, y_bf16=None, y_f32=None, workspace=No
     return (yb, yf) if want_f32 else yb
 
 
+def int8_project_many(x, projections, want_f32=False, outputs=None, workspace=None):
+    """Several projections of the same activations in one launch (Q, K, V of x; the shared expert's gate and up):
+    projections = [(qT int8 [n_out_j, n_in], s f32 [n_out_j]), ...] (at most 8) -> a list with, per projection,
+    what ``int8_project`` returns.  ``outputs`` = [(y_bf16, y_f32 or None), ...] preallocated makes the call
+    allocation-free."""
+    B, n_in = x.shape
+    x = x.contiguous()
+    n = len(projections)
+    arr = (_lib.MiI8Proj * n)()
+    outs = []
+    for j, (qT, s) in enumerate(projections):
+        n_out = qT.shape[0]
+        if outputs is not None:
+            yb, yf = outputs[j]
+        else:
+            yb = torch.empty((B, n_out), dtype=torch.bfloat16, device=x.device)
+            yf = torch.empty((B, n_out), dtype=torch.float32, device=x.device) if want_f32 else None
+        arr[j] = _lib.MiI8Proj(qT.data_ptr(), s.data_ptr(), n_out, _ptr(yb), _ptr(yf))
+        outs.append((yb, yf) if want_f32 else yb)
+    n_outs = (ctypes.c_int32 * n)(*[int(qT.shape[0]) for qT, _ in projections])
+    nbytes = lib().mi_int8_project_many_workspace(B, n_in, n_outs, n)
+    if nbytes == 0:
+        raise ValueError("mi_int8_project_many: unsupported shapes (B=%d, n_in=%d, n_proj=%d)" % (B, n_in, n))
+    ws = workspace if workspace is not None else WORKSPACES.get("int8", nbytes)
+    check("mi_int8_project_many", lib().mi_int8_project_many(_ptr(x), B, n_in, arr, n, _ptr(ws), ws.numel(),
+                                                             _stream()))
+    return outs
+
+
 # ------------------------------------------------------------------------------------------------ the operator
 class ResidentFetch:
     """Drop-in for glm53.resident.ResidentFetch (resident.py:68-108): same constructor, ``qtypes`` and ``apply``.

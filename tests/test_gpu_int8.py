@@ -32,3 +32,22 @@ def test_int8_golden(pkg, gpu):
     yb = pkg.int8_project(torch.from_numpy(z["x"]).cuda().to(torch.bfloat16), torch.from_numpy(qT).cuda(),
                           torch.from_numpy(sv).cuda())
     assert rel_l2(yb.float().cpu().numpy(), z["y"]) < 1e-3
+
+
+def test_int8_project_many_equals_single(pkg, gpu):
+    """One launch over Q, K, V-like projections (and a narrower one) gives exactly what separate calls give."""
+    rng = np.random.default_rng(9)
+    B, n_in = 8, 1024
+    shapes = [512, 512, 256, 768]
+    qs = [oi8.generate(rng, n_in, n) for n in shapes]
+    x = round_bf16(rng.standard_normal((B, n_in)).astype(np.float32))
+    xt = torch.from_numpy(x).cuda().to(torch.bfloat16)
+    projs = []
+    for q, s in qs:
+        qT, sv = pkg.formats.int8_pack(q, s)
+        projs.append((torch.from_numpy(qT).cuda(), torch.from_numpy(sv).cuda()))
+    many = pkg.int8_project_many(xt, projs, want_f32=True)
+    for (q, s), (qT, sv), (yb, yf) in zip(qs, projs, many):
+        yb1, yf1 = pkg.int8_project(xt, qT, sv, want_f32=True)
+        assert rel_l2(yf.cpu().numpy(), yf1.cpu().numpy()) < 1e-6
+        assert rel_l2(yf.cpu().numpy(), oi8.project_f32(x, q, s)) < 1e-5
