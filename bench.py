@@ -29,6 +29,7 @@ REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, REPO)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0         # dense bf16 matrix-core peak of MI355X
 D, E_ROUTED, TOPK, INTER = 6144, 64, 8, 2048
 SHARED = E_ROUTED                      # expert index of the shared expert (appended to every table)
 LIMIT = 10.0
@@ -241,6 +242,7 @@ def main():
             gbs = b / (ms * 1e-3) / 1e9
             extra["b%d" % N] = {"us_per_layer": round(ms * 1e3, 2), "GBps": round(gbs, 1),
                                 "pct_hbm": round(100 * gbs / HBM_PEAK_GBS, 1), "bytes_per_layer": int(b)}
+        extra["prefill_t512"] = bench_prefill(torch, pkg, gen, args, layers, rng)
         extra["int8_b8"] = bench_int8(torch, pkg, gen, args)
         extra["cfg0_matvec"] = bench_matvec(torch, pkg, gen, args)
 
@@ -274,6 +276,35 @@ def main():
         b = torch.empty_like(a)
         b.copy_(a)
         torch.cuda.synchronize()
+
+
+def bench_prefill(torch, pkg, gen, args, layers, rng, T=512):
+    """Config: a prefill chunk of 512 tokens through the same layer (top-8 of 64 routed experts from N(0,1) router
+    logits, plus the shared expert on every token), grouped GEMMs on the matrix cores.  Algorithmic work: every
+    (token, expert) row costs 2 * 3 * D * I flops; weight bytes are those of every distinct expert the chunk uses."""
+    fns, nbytes = [], []
+    tb0 = layers[0]
+    ws = torch.zeros(pkg.resident.prefill_workspace_bytes(tb0["gate"], tb0["down"], T, TOPK, SHARED),
+                     dtype=torch.uint8, device="cuda")
+    out = torch.empty((T, D), dtype=torch.bfloat16, device="cuda")
+    per_expert = 2 * cb3_bytes(INTER, D) + cb3_bytes(D, INTER)
+    for t in layers:
+        idx, w = softmax_topk(rng, T, E_ROUTED, TOPK)
+        x = torch.randn((T, D), device="cuda", generator=gen).to(torch.bfloat16)
+        it, wt = torch.from_numpy(idx).cuda(), torch.from_numpy(w).cuda()
+        fns.append(lambda t=t, x=x, it=it, wt=wt: pkg.moe_prefill(t["gate"], t["up"], t["down"], x, it, wt, LIMIT,
+                                                                 shared_expert=SHARED, want_f32=False,
+                                                                 out_bf16=out, workspace=ws))
+        nbytes.append((len(np.unique(idx)) + 1) * per_expert)
+    steps = max(1, args.steps // 4)
+    ms = Timer(torch, fns).run(steps, max(1, args.warmup // 4))
+    rows = T * (TOPK + 1)
+    flops = rows * 2.0 * 3 * D * INTER
+    tflops = flops / (ms * 1e-3) / 1e12
+    gbs = float(np.mean(nbytes)) / (ms * 1e-3) / 1e9
+    return {"us_per_layer": round(ms * 1e3, 1), "tokens_per_s": round(T / (ms * 1e-3), 0),
+            "TFLOPs": round(tflops, 1), "pct_mfma_bf16_peak": round(100 * tflops / MFMA_BF16_PEAK_TFLOPS, 1),
+            "weight_GBps": round(gbs, 1), "rows": rows, "steps": steps}
 
 
 def bench_int8(torch, pkg, gen, args):

@@ -104,6 +104,44 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
                          int32_t phases, void *stream);
 
 /*
+ * The reference's prefill slot layout (ragged_plan, pallas_moe.py:564-592), built on the device:
+ *   S = T*k slots (token t, column j) sorted stably by expert idx[t, j]; every expert's rows padded to whole blocks
+ *   of tm rows; G = ceil(S / tm) + E blocks, Rp = G * tm rows.
+ *   blk_expert int32 [G]: expert of block g (blocks >= n_blocks repeat the last used expert; E - 1 if none)
+ *   n_blocks   int32 [1]
+ *   tok_row    int32 [Rp]: token of every sorted row, -1 = padding
+ *   w_row      f32   [Rp]: routing weight w[t, j] of every sorted row, 0 = padding
+ *   row_slot   int32 [T, k]: sorted row of every slot (-1 for an expert id outside [0, E), which the reference
+ *                            does not define)
+ * 1 <= E <= 1024, 1 <= tm <= 65536, T*k <= 2^22.  One workgroup; no workspace.
+ */
+int mi_ragged_plan(const int32_t *idx, const float *w, int32_t T, int32_t k, int32_t E, int32_t tm,
+                   int32_t *blk_expert, int32_t *n_blocks, int32_t *tok_row, float *w_row, int32_t *row_slot,
+                   void *stream);
+
+/*
+ * Fused MoE prefill layer (ResidentFetch._apply_ragged_kernel, resident.py:144-165) for CB3 tables, grouped GEMMs
+ * on the matrix cores:
+ *   plan   = ragged_plan over the T*k slots (+ one shared-expert column of weight 1 if shared_expert >= 0), tm = 96
+ *   h[row] = bf16(silu(min(g, L)) * clip(u, -L, L)),  g, u = Wgate_e x_t, Wup_e x_t in f32   (pallas_moe.py:622-690)
+ *   y[row] = bf16(Wdown_e h[row]), f32 accumulation                                           (pallas_moe.py:693-755)
+ *   out[t] = sum_j wt(t, j) y[row_slot(t, j)] in f32, wt = bf16(w[t, j]) for MI_COMBINE_MATMUL (resident.py:161-163)
+ *            or w[t, j] for MI_COMBINE_GATHER (resident.py:164-165); the shared column has weight 1.
+ * x bf16 [T, D], idx int32 [T, k], w f32 [T, k]; out_f32 and/or out_bf16 [T, D].  Every expert's weights are read
+ * once per block of 96 rows.  T*(k+1) <= 2^22, E <= 1024, gate.rows % 128 == 0, down.rows % 256 == 0.
+ * Four launches: plan, gate/up, down, combine.  The workspace (mi_moe_prefill_workspace bytes) holds the plan, h and
+ * y; it needs no initialisation.
+ */
+#define MI_COMBINE_MATMUL 0
+#define MI_COMBINE_GATHER 1
+int mi_moe_prefill(const mi_table *gate, const mi_table *up, const mi_table *down, const uint16_t *x_bf16,
+                   int32_t T, int32_t k, const int32_t *idx, const float *w, int32_t shared_expert, float limit,
+                   int32_t combine, float *out_f32, uint16_t *out_bf16, void *workspace, size_t workspace_bytes,
+                   void *stream);
+size_t mi_moe_prefill_workspace(const mi_table *gate, const mi_table *down, int32_t T, int32_t k,
+                                int32_t shared_expert);
+
+/*
  * Exact dequantized weights of expert e (natural input order): out f32 [R, K].  Restates dequant_planes
  * (planes.py:196-206) / the codebook closed form; used to check the kernels' decode bit for bit.
  */

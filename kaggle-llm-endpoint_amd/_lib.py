@@ -15,13 +15,17 @@ MI_X_BF16 = 0
 MI_X_F32 = 1
 MI_MAX_SLOTS = 128
 MAX_DECODE_TOKENS = 16
+MI_COMBINE_MATMUL = 0
+MI_COMBINE_GATHER = 1
+COMBINES = {"matmul": MI_COMBINE_MATMUL, "gather": MI_COMBINE_GATHER}
+PREFILL_TM = 96              # rows per block of mi_moe_prefill's own plan
 
 QTYPES = {"CB3": MI_QT_CB3, "IQ3_S": MI_QT_IQ3_S}
 PLANE_KEYS = {"CB3": ("qs", "cb"), "IQ3_S": ("qs", "sg", "qh", "sc", "d")}
 
 # every symbol the header declares (tests check the library exports them)
 EXPORTS = ("mi_matvec", "mi_matvec_workspace", "mi_moe_decode", "mi_moe_decode_phases", "mi_moe_decode_workspace",
-           "mi_dequant", "mi_int8_project", "mi_int8_project_workspace", "mi_int8_project_many",
+           "mi_ragged_plan", "mi_moe_prefill", "mi_moe_prefill_workspace", "mi_dequant", "mi_int8_project", "mi_int8_project_workspace", "mi_int8_project_many",
            "mi_int8_project_many_workspace", "mi_strerror", "mi_version")
 
 
@@ -61,6 +65,9 @@ def lib():
         "mi_moe_decode": (I, [T, T, T, P, I, I, P, P, I, F, P, P, P, Z, P]),
         "mi_moe_decode_phases": (I, [T, T, T, P, I, I, P, P, I, F, P, P, P, Z, I, P]),
         "mi_moe_decode_workspace": (Z, [T, T, I, I, I]),
+        "mi_ragged_plan": (I, [P, P, I, I, I, I, P, P, P, P, P, P]),
+        "mi_moe_prefill": (I, [T, T, T, P, I, I, P, P, I, F, I, P, P, P, Z, P]),
+        "mi_moe_prefill_workspace": (Z, [T, T, I, I, I]),
         "mi_dequant": (I, [T, I, P, P]),
         "mi_int8_project": (I, [P, I, P, P, I, I, P, P, P, Z, P]),
         "mi_int8_project_workspace": (Z, [I, I, I]),

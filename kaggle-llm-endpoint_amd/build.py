@@ -26,7 +26,8 @@ FLAGS = [
 ]
 
 # (source, extra defines, object name)
-UNITS = [("moe_decode.hip", [], "moe_decode"), ("int8_project.hip", [], "int8_project")]
+UNITS = [("moe_decode.hip", [], "moe_decode"), ("int8_project.hip", [], "int8_project"),
+         ("prefill.hip", [], "prefill")]
 UNITS += [("k_grouped.hip", ["-DMI_KMODE=%d" % m, "-DMI_KQT=%d" % q], "k_grouped_%d_%d" % (m, q))
           for m in (0, 1, 2) for q in (1, 2)]
 

@@ -1,0 +1,622 @@
+// Grouped prefill for CB3 experts on the gfx950 matrix cores (the reference's ragged prefill,
+// resident.py:144-165 with pallas_moe.py:564-592,622-755):
+//   ragged_plan_kernel  the reference's slot layout (pallas_moe.py:564-592) built on the device by one workgroup:
+//                       slots stably sorted by expert, every expert padded to whole blocks of tm rows;
+//   prefill_kernel      one workgroup per (block, row range) streams the block's expert once for all its rows:
+//                       each wavefront owns 64 weight rows x up to 96 rows of activations (6 MFMA token tiles),
+//                       decodes every weight once (the decoder of cb3_tiles.h) and reuses it across the token
+//                       tiles; the block's activation rows are staged one 160-column tile at a time in LDS;
+//                         gate/up: h = bf16(silu(min(g, L)) * clip(u, -L, L)), g and u f32    (pallas_moe.py:682)
+//                         down:    y = bf16(h Wd^T), f32 accumulation                        (pallas_moe.py:747)
+//   prefill_combine     out[t] = sum_j wt(t, j) * y[row_slot(t, j)] in f32 with wt = bf16(w) ("matmul" combine,
+//                       resident.py:161-163) or wt = w ("gather", resident.py:164-165).
+// The rounding points are the reference's: bf16 activations, bf16 weights (CB3 centroids are bf16 already), f32
+// accumulation, h and y rounded to bf16, routing weights rounded to bf16 by the matmul combine.
+#include "cb3_tiles.h"
+
+namespace mi {
+
+constexpr int kPfTT = 6;                   // token tiles of 16 rows per block
+constexpr int kPfTm = 16 * kPfTT;          // rows per block of the prefill's own plan
+constexpr int kPfWaves = 4;
+constexpr int kPfRtw = 4;                  // row tiles per wavefront (64 weight rows)
+constexpr int kPfXPitch = 84;              // dwords per staged activation row of one column tile (80 + skew)
+constexpr int kPlanThreads = 1024;
+constexpr int kPlanWaves = kPlanThreads / 64;
+constexpr int kPlanMaxE = 1024;
+constexpr long long kPlanMaxSlots = 1 << 22;
+
+struct PlanOut {
+    int32_t *blk_expert;   // [G]   expert of every block (blocks >= n_blocks repeat the last expert)
+    int32_t *n_blocks;     // [1]
+    int32_t *tok_row;      // [Rp]  token of every sorted row, -1 = padding
+    float *w_row;          // [Rp]  routing weight of every sorted row, 0 = padding
+    int32_t *row_slot;     // [T * kk] sorted row of every (token, slot); -1 for an expert id outside [0, E)
+    int32_t *blk_n;        // [G]   rows of every block that are not padding (NULL: not written)
+};
+
+// Slot s of the plan: token s / kk, column j = s % kk; columns j < k are the routed slots, column k (kk = k + 1) is
+// the shared expert (weight 1) when one is given.
+__device__ __forceinline__ int plan_expert(const int32_t *idx, int s, int k, int kk, int shared, int E) {
+    const int t = s / kk, j = s - t * kk;
+    const int e = j < k ? idx[t * k + j] : shared;
+    return (e >= 0 && e < E) ? e : -1;
+}
+
+// Inclusive prefix sum over the kPlanThreads threads of the workgroup (every thread calls it).
+__device__ int block_inclusive_scan(int v, int *wsum) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int o = __shfl_up(v, d, 64);
+        if (lane >= d) v += o;
+    }
+    if (lane == 63) wsum[wave] = v;
+    __syncthreads();
+    for (int i = 0; i < wave; ++i) v += wsum[i];
+    __syncthreads();
+    return v;
+}
+
+// The reference's ragged_plan (pallas_moe.py:564-592), stable: the rows of one expert follow slot order.  Counting
+// is order-free (LDS atomics); the rows are then assigned in rounds of kPlanThreads slots, where a slot's rank is the
+// number of earlier slots of its expert: earlier rounds (a running count), earlier wavefronts of the round (a prefix
+// over per-wavefront counts) and earlier lanes of its wavefront (a ballot match).
+__global__ void __launch_bounds__(kPlanThreads) ragged_plan_kernel(const int32_t *__restrict__ idx,
+                                                                   const float *__restrict__ w, int T, int k,
+                                                                   int shared, int E, int tm, PlanOut p) {
+    __shared__ int cnt[kPlanMaxE], bend[kPlanMaxE], run[kPlanMaxE];
+    __shared__ uint16_t cntw[kPlanWaves][kPlanMaxE];
+    __shared__ int wsum[kPlanWaves];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kk = k + (shared >= 0 ? 1 : 0);
+    const int S = T * kk;
+    const int G = (S + tm - 1) / tm + E;
+    const long long Rp = (long long)G * tm;
+
+    for (int i = tid; i < kPlanMaxE; i += kPlanThreads) {
+        cnt[i] = 0;
+        run[i] = 0;
+        for (int v = 0; v < kPlanWaves; ++v) cntw[v][i] = 0;
+    }
+    for (long long r = tid; r < Rp; r += kPlanThreads) {
+        p.tok_row[r] = -1;
+        p.w_row[r] = 0.0f;
+    }
+    __syncthreads();
+    for (int s = tid; s < S; s += kPlanThreads) {
+        const int e = plan_expert(idx, s, k, kk, shared, E);
+        if (e >= 0) atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+    // blocks per expert and their inclusive prefix (block end); padded rows start at (bend - nb) * tm
+    const int nb_own = tid < E ? (cnt[tid] + tm - 1) / tm : 0;
+    const int incl = block_inclusive_scan(nb_own, wsum);
+    if (tid < kPlanMaxE) bend[tid] = incl;
+    __syncthreads();
+    const int n_blocks = bend[kPlanMaxE - 1];
+    if (tid == 0) *p.n_blocks = n_blocks;
+
+    // rows, in rounds of kPlanThreads slots
+    int tot = 0;
+    for (int base = 0; base < S; base += kPlanThreads) {
+        const int s = base + tid;
+        const int e = s < S ? plan_expert(idx, s, k, kk, shared, E) : -1;
+        const bool valid = e >= 0;
+        uint64_t rem = __ballot(valid);
+        int rank = 0, n_same = 0;
+        while (rem) {
+            const int l = __builtin_ctzll(rem);
+            const int el = __builtin_amdgcn_readlane(e, l);
+            const uint64_t m = __ballot(valid && e == el);
+            if (valid && e == el) {
+                rank = __popcll(m & ((1ull << lane) - 1ull));
+                n_same = __popcll(m);
+            }
+            rem &= ~m;
+        }
+        if (valid && rank == 0) cntw[wave][e] = (uint16_t)n_same;
+        __syncthreads();
+        if (tid < E) {               // exclusive prefix over the wavefronts of this round
+            int acc = 0;
+            for (int v = 0; v < kPlanWaves; ++v) {
+                const int c = cntw[v][tid];
+                cntw[v][tid] = (uint16_t)acc;
+                acc += c;
+            }
+            tot = acc;
+        }
+        __syncthreads();
+        if (s < S) {
+            int row = -1;
+            if (valid) {
+                const int nb = (cnt[e] + tm - 1) / tm;
+                row = (bend[e] - nb) * tm + run[e] + cntw[wave][e] + rank;
+                const int t = s / kk, j = s - t * kk;
+                p.tok_row[row] = t;
+                p.w_row[row] = j < k ? w[t * k + j] : 1.0f;
+            }
+            p.row_slot[s] = row;
+        }
+        __syncthreads();
+        if (tid < E) {               // every wavefront's entry of this expert holds a prefix now: clear them all
+            for (int v = 0; v < kPlanWaves; ++v) cntw[v][tid] = 0;
+            run[tid] += tot;
+        }
+        __syncthreads();             // the clears land before the next round's counts
+    }
+
+    // block -> expert: the first expert whose block end exceeds g; blocks past n_blocks repeat the last one (the
+    // expert of block n_blocks - 1, or E - 1 when there is none, as the reference's clamp gives)
+    int last = E - 1;
+    if (n_blocks > 0) {
+        int lo = 0, hi = E - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (bend[mid] > n_blocks - 1) hi = mid;
+            else lo = mid + 1;
+        }
+        last = lo;
+    }
+    for (int g = tid; g < G; g += kPlanThreads) {
+        int e = last, n = 0;
+        if (g < n_blocks) {
+            int lo = 0, hi = E - 1;
+            while (lo < hi) {
+                const int mid = (lo + hi) >> 1;
+                if (bend[mid] > g) hi = mid;
+                else lo = mid + 1;
+            }
+            e = lo;
+            const int nb = (cnt[e] + tm - 1) / tm;
+            n = min(tm, cnt[e] - (g - (bend[e] - nb)) * tm);
+        }
+        p.blk_expert[g] = e;
+        if (p.blk_n) p.blk_n[g] = n;
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ grouped GEMM
+struct PfArgs {
+    Cb3Table t0, t1;                       // gate/up: gate, up; down: down (twice)
+    int R, K;                              // output columns (rows of the table), input columns
+    const int32_t *blk_expert, *blk_n, *n_blocks, *tok_row;
+    const uint16_t *x;                     // gate/up: x [T, K] gathered through tok_row; down: h [Rp, K]
+    uint32_t x_bytes;                      // bytes of x (< 2^31)
+    int gather;
+    uint16_t *out;                         // gate/up: h [Rp, R]; down: y [Rp, R]
+    float limit;
+    int wg_rows;                           // 64-row groups per workgroup: gate/up 2 (x gate, up), down 4
+    int RBG;                               // workgroups per block
+};
+
+template <int M>
+__device__ __forceinline__ void pf_steps(const uint4 (&wv)[kPfRtw], const uint4 *cbrow, int slot0, int slot1,
+                                         const uint32_t *xrow, int ntt, f32x4 (&acc)[kPfRtw][kPfTT]) {
+    if constexpr (M < 5) {
+        // one k-step at a time: left free, the scheduler hoists every step's LDS reads and decodes and spills
+        if constexpr (M > 0) __builtin_amdgcn_sched_barrier(0);
+        bf16x8 A[kPfRtw];
+        const int slot = M < slot1 ? slot0 : slot0 + 1;     // slot1 = 4 - C: first step of the next group
+#pragma unroll
+        for (int r = 0; r < kPfRtw; ++r) {
+            uint32_t s0, s1;
+            cb3_sel<M>(wv[r], s0, s1);
+            A[r] = cb3_weights8(s0, s1, cbrow[slot * 64 + 16 * r]);
+        }
+#pragma unroll
+        for (int tt = 0; tt < kPfTT; ++tt) {
+            if (tt < ntt) {
+                const uint4 b = *(const uint4 *)(xrow + tt * 16 * kPfXPitch + 16 * M);
+#pragma unroll
+                for (int r = 0; r < kPfRtw; ++r) acc[r][tt] = mfma16(A[r], b, acc[r][tt]);
+            }
+        }
+        pf_steps<M + 1>(wv, cbrow, slot0, slot1, xrow, ntt, acc);
+    }
+}
+
+// Code words of the wavefront's row tiles, two column tiles ahead (the matrix-core work per column tile is long
+// enough that a deeper ring only costs registers).
+struct PfRegs {
+    uint4 ring[2][kPfRtw];    // slot c & 1 = column tile c
+    uint4 cbv[5];             // codebook groups of the next super tile, as in Cb3Regs
+};
+
+// Column tile C of super tile st (codebook slots as in cb3_ctile), B operands from the staged tile.
+template <int C>
+__device__ __forceinline__ void pf_ctile(const Cb3Wave &w, PfRegs &s, int st, const uint32_t *xrow, int ntt,
+                                         f32x4 (&acc)[kPfRtw][kPfTT]) {
+    const int lane = threadIdx.x & 63;
+    const int gn = 5 * (st + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (C == 0) {
+        w.cbl[0 * 64 + lane] = s.cbv[0];
+        w.cbl[1 * 64 + lane] = s.cbv[1];
+        s.cbv[0] = cb3_group(w, gn);
+        s.cbv[1] = cb3_group(w, gn + 1);
+    } else {
+        w.cbl[(C + 1) * 64 + lane] = s.cbv[C + 1];
+        s.cbv[C + 1] = cb3_group(w, gn + C + 1);
+    }
+    const int ct = 4 * st + C;
+    uint4 wv[kPfRtw];
+#pragma unroll
+    for (int r = 0; r < kPfRtw; ++r) {
+        wv[r] = s.ring[C & 1][r];
+        s.ring[C & 1][r] = cb3_tile(w, ct + 2, r);
+    }
+    pf_steps<0>(wv, w.cbl + (lane & 15), C, 4 - C, xrow, ntt, acc);
+}
+
+template <int MODE>   // 0: gate/up -> h, 1: down -> y
+__global__ void __launch_bounds__(64 * kPfWaves, 2) prefill_kernel(PfArgs a) {
+    __shared__ uint4 cbl[kPfWaves * 5 * 64];                // per-wavefront codebook slots (20 KB)
+    __shared__ uint32_t xs[kPfTm * kPfXPitch];               // one column tile of the block's rows (31.5 KB);
+                                                             // gate/up epilogue: the gate accumulators of one pair
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = blockIdx.x / a.RBG, rbg = blockIdx.x - (blockIdx.x / a.RBG) * a.RBG;
+    if (g >= *a.n_blocks) return;
+    const int e = __builtin_amdgcn_readfirstlane(a.blk_expert[g]);
+    const int n = __builtin_amdgcn_readfirstlane(a.blk_n[g]);
+    const int row0 = g * kPfTm;
+    const int ntt = (n + 15) >> 4;
+    const int mat = MODE == 0 ? (wave & 1) : 0;
+    const Cb3Table &tb = mat ? a.t1 : a.t0;
+    const int rg = rbg * a.wg_rows + (MODE == 0 ? (wave >> 1) : wave);   // 64-row group of this wavefront
+
+    Cb3Wave w;
+    const uint32_t *qt = tb.qs + (size_t)e * tb.CT * tb.RT * 256;
+    const uint32_t *cbe = tb.cb + (size_t)e * tb.G * tb.R * 4;
+    w.qb = __builtin_amdgcn_make_buffer_rsrc((void *)qt, (short)0, 0x7fffffff, kBufferWord3);
+    w.qnull = __builtin_amdgcn_make_buffer_rsrc((void *)qt, (short)0, 0, kBufferWord3);
+    w.cbb = __builtin_amdgcn_make_buffer_rsrc((void *)cbe, (short)0, 0x7fffffff, kBufferWord3);
+    w.cbnull = __builtin_amdgcn_make_buffer_rsrc((void *)cbe, (short)0, 0, kBufferWord3);
+    w.ct_bytes = (uint32_t)tb.RT * 1024u;
+    w.rt_bytes = (uint32_t)(rg * kPfRtw) * 1024u;
+    w.g_bytes = (uint32_t)tb.R * 16u;
+    w.row_bytes = (uint32_t)(rg * 64) * 16u;
+    w.cta = 0;
+    w.ctb = tb.CT;
+    w.g_first = 0;
+    w.g_last = tb.G - 1;
+    w.lane16 = (uint32_t)lane * 16u;
+    w.cblane16 = (uint32_t)lane * 16u;
+    w.xh = w.xl = nullptr;
+    w.cbl = cbl + wave * 5 * 64;
+
+    PfRegs s;
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int r = 0; r < kPfRtw; ++r) s.ring[c][r] = cb3_tile(w, c, r);
+#pragma unroll
+    for (int c = 0; c < 5; ++c) s.cbv[c] = cb3_group(w, c);
+
+    // activation tile: kPfTm rows x 20 uint4 (160 columns) over 256 threads, as buffer loads; entries of rows >= n
+    // and of columns >= K take an offset past the buffer's range, which reads zero without touching memory
+    constexpr int kXU = kPfTm * 20;
+    constexpr int kXJ = (kXU + 64 * kPfWaves - 1) / (64 * kPfWaves);
+    constexpr uint32_t kXOut = 0x80000000u;                  // >= every buffer's byte range
+    const __amdgpu_buffer_rsrc_t xbuf =
+        __builtin_amdgcn_make_buffer_rsrc((void *)a.x, (short)0, (int)a.x_bytes, kBufferWord3);
+    const int c0 = tid % 20;
+    uint32_t xoff[kXJ];                                      // byte offset of the entry in its row tile, or kXOut
+#pragma unroll
+    for (int j = 0; j < kXJ; ++j) {
+        const int u = tid + 64 * kPfWaves * j, row = u / 20;
+        uint32_t o = kXOut;
+        if (u < kXU && row < n) {
+            const int src = a.gather ? a.tok_row[row0 + row] : row0 + row;
+            o = (uint32_t)src * (uint32_t)a.K * 2u + 16u * (uint32_t)(u - row * 20);
+        }
+        xoff[j] = o;
+    }
+    uint4 xr[kXJ];
+    auto load_x = [&](int ct) {
+        const int lim = (a.K - kCb3TileCols * ct) >> 3;       // uint4 columns of this tile inside the row
+#pragma unroll
+        for (int j = 0; j < kXJ; ++j) {
+            int c8 = c0 + (16 * j) % 20;                      // (tid + 256 j) % 20
+            c8 -= c8 >= 20 ? 20 : 0;
+            const uint32_t o = c8 < lim ? xoff[j] + (uint32_t)(2 * kCb3TileCols * ct) : kXOut;
+            xr[j] = bload(xbuf, o, 0);
+        }
+    };
+    auto store_x = [&]() {
+#pragma unroll
+        for (int j = 0; j < kXJ; ++j) {
+            const int u = tid + 64 * kPfWaves * j;
+            if (u < kXU) {
+                const int row = u / 20, c8 = u - row * 20;
+                *(uint4 *)(xs + row * kPfXPitch + 4 * c8) = xr[j];
+            }
+        }
+    };
+    load_x(0);
+
+    f32x4 acc[kPfRtw][kPfTT];
+#pragma unroll
+    for (int r = 0; r < kPfRtw; ++r)
+#pragma unroll
+        for (int t = 0; t < kPfTT; ++t) acc[r][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    const int jt = lane & 15, q = lane >> 4;
+    const uint32_t *xrow = xs + jt * kPfXPitch + 4 * q;
+    const int CT = tb.CT;
+
+    // every wavefront runs the same column tiles, so the barriers around each staging line up
+    auto step = [&](auto Cc, int st) {
+        constexpr int C = decltype(Cc)::value;
+        const int ct = 4 * st + C;
+        __syncthreads();                  // every wavefront is done with the previous tile
+        store_x();
+        __syncthreads();
+        if (ct + 1 < CT) load_x(ct + 1);
+        pf_ctile<C>(w, s, st, xrow, ntt, acc);
+    };
+    const int st_full = CT >> 2;
+    int st = 0;
+    for (; st < st_full; ++st) {
+        step(std::integral_constant<int, 0>{}, st);
+        step(std::integral_constant<int, 1>{}, st);
+        step(std::integral_constant<int, 2>{}, st);
+        step(std::integral_constant<int, 3>{}, st);
+    }
+    const int nct = CT - 4 * st;
+    if (nct > 0) step(std::integral_constant<int, 0>{}, st);
+    if (nct > 1) step(std::integral_constant<int, 1>{}, st);
+    if (nct > 2) step(std::integral_constant<int, 2>{}, st);
+
+    // epilogue: lane (jt, q) holds rows 16 r + 4 q + i (i = 0..3) of the wavefront's 64 rows for tokens 16 t + jt
+    const int rbase = rg * 64;
+    if constexpr (MODE == 0) {
+        float *gbuf = (float *)xs;                           // [64 rows][kPfTm] gate accumulators of one pair
+        for (int pair = 0; pair < 2; ++pair) {
+            __syncthreads();
+            if (wave == 2 * pair) {
+#pragma unroll
+                for (int r = 0; r < kPfRtw; ++r)
+#pragma unroll
+                    for (int t = 0; t < kPfTT; ++t)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) gbuf[(16 * r + 4 * q + i) * kPfTm + 16 * t + jt] = acc[r][t][i];
+            }
+            __syncthreads();
+            if (wave == 2 * pair + 1) {
+#pragma unroll
+                for (int t = 0; t < kPfTT; ++t) {
+                    const int tok = 16 * t + jt;
+                    if (tok < n) {
+#pragma unroll
+                        for (int r = 0; r < kPfRtw; ++r) {
+                            float hv[4];
+#pragma unroll
+                            for (int i = 0; i < 4; ++i)
+                                hv[i] = swiglu_clamped(gbuf[(16 * r + 4 * q + i) * kPfTm + tok], acc[r][t][i],
+                                                       a.limit);
+                            uint2 v;
+                            v.x = f32_to_bf16_rne(hv[0]) | (f32_to_bf16_rne(hv[1]) << 16);
+                            v.y = f32_to_bf16_rne(hv[2]) | (f32_to_bf16_rne(hv[3]) << 16);
+                            *(uint2 *)(a.out + (size_t)(row0 + tok) * a.R + rbase + 16 * r + 4 * q) = v;
+                        }
+                    }
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int t = 0; t < kPfTT; ++t) {
+            const int tok = 16 * t + jt;
+            if (tok < n) {
+#pragma unroll
+                for (int r = 0; r < kPfRtw; ++r) {
+                    uint2 v;
+                    v.x = f32_to_bf16_rne(acc[r][t][0]) | (f32_to_bf16_rne(acc[r][t][1]) << 16);
+                    v.y = f32_to_bf16_rne(acc[r][t][2]) | (f32_to_bf16_rne(acc[r][t][3]) << 16);
+                    *(uint2 *)(a.out + (size_t)(row0 + tok) * a.R + rbase + 16 * r + 4 * q) = v;
+                }
+            }
+        }
+    }
+}
+
+// out[t] = sum_j wt(t, j) * y[row_slot(t, j)] over the plan's kk columns in order, f32; wt = bf16(w) for the matmul
+// combine, w for the gather combine (the shared column has weight 1 either way).  One thread per 4 output columns.
+__global__ void __launch_bounds__(256) prefill_combine(const uint16_t *__restrict__ y, const int32_t *__restrict__ row_slot,
+                                                       const float *__restrict__ w, int T, int k, int kk, int D,
+                                                       int bf16_weights, float *out_f32, uint16_t *out_bf16) {
+    const int q4 = D >> 2;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= T * q4) return;
+    const int t = i / q4, c = 4 * (i - t * q4);
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int j = 0; j < kk; ++j) {
+        const int r = row_slot[t * kk + j];
+        if (r < 0) continue;
+        float wt = 1.0f;
+        if (j < k) {
+            wt = w[t * k + j];
+            if (bf16_weights) wt = bf16_to_f32(f32_to_bf16_rne(wt));
+        }
+        const uint2 v = *(const uint2 *)(y + (size_t)r * D + c);
+        acc.x += wt * bf16_to_f32(v.x & 0xffffu);
+        acc.y += wt * bf16_to_f32(v.x >> 16);
+        acc.z += wt * bf16_to_f32(v.y & 0xffffu);
+        acc.w += wt * bf16_to_f32(v.y >> 16);
+    }
+    if (out_f32) *(float4 *)(out_f32 + (size_t)t * D + c) = acc;
+    if (out_bf16) {
+        uint2 b;
+        b.x = f32_to_bf16_rne(acc.x) | (f32_to_bf16_rne(acc.y) << 16);
+        b.y = f32_to_bf16_rne(acc.z) | (f32_to_bf16_rne(acc.w) << 16);
+        *(uint2 *)(out_bf16 + (size_t)t * D + c) = b;
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ host side
+struct PfLayout {
+    int S, G;
+    long long Rp;
+    size_t off_be, off_nb, off_bn, off_tr, off_wr, off_rs, off_h, off_y, total;
+};
+
+static size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+static PfLayout pf_layout(int T, int kk, int E, int I, int D) {
+    PfLayout L{};
+    L.S = T * kk;
+    L.G = (L.S + kPfTm - 1) / kPfTm + E;
+    L.Rp = (long long)L.G * kPfTm;
+    size_t o = 0;
+    L.off_be = o; o = al256(o + 4 * (size_t)L.G);
+    L.off_nb = o; o = al256(o + 4);
+    L.off_bn = o; o = al256(o + 4 * (size_t)L.G);
+    L.off_tr = o; o = al256(o + 4 * (size_t)L.Rp);
+    L.off_wr = o; o = al256(o + 4 * (size_t)L.Rp);
+    L.off_rs = o; o = al256(o + 4 * (size_t)L.S);
+    L.off_h = o; o = al256(o + 2 * (size_t)L.Rp * I);
+    L.off_y = o; o = al256(o + 2 * (size_t)L.Rp * D);
+    L.total = o;
+    return L;
+}
+
+static Cb3Table pf_table(const mi_table *t) {
+    Cb3Table c{};
+    c.qs = t->plane[0];
+    c.cb = t->plane[1];
+    c.R = t->rows;
+    c.K = t->cols;
+    c.CT = (t->cols + kCb3TileCols - 1) / kCb3TileCols;
+    c.RT = t->rows / 16;
+    c.G = t->cols / 128;
+    return c;
+}
+
+static int pf_validate(const mi_table *g, const mi_table *u, const mi_table *d) {
+    if (!g || !u || !d) return MI_ERR_NULL;
+    for (const mi_table *t : {g, u, d}) {
+        if (t->qtype != MI_QT_CB3) return MI_ERR_QTYPE;     // the prefill kernels decode CB3 tiles
+        if (!t->plane[0] || !t->plane[1]) return MI_ERR_NULL;
+        if (t->n_experts <= 0 || t->n_experts > kPlanMaxE || t->cols <= 0 || t->cols % 128 || t->rows <= 0)
+            return MI_ERR_SHAPE;
+    }
+    if (g->rows % 128 || d->rows % 256) return MI_ERR_SHAPE;   // whole workgroup row ranges
+    if (u->rows != g->rows || u->cols != g->cols || u->n_experts != g->n_experts) return MI_ERR_MISMATCH;
+    if (d->cols != g->rows || d->n_experts != g->n_experts) return MI_ERR_MISMATCH;
+    return MI_OK;
+}
+
+static bool plan_sizes_ok(long long T, long long kk, long long E, long long tm) {
+    if (T <= 0 || kk <= 0 || E <= 0 || E > kPlanMaxE || tm <= 0 || tm > 65536) return false;
+    const long long S = T * kk;
+    if (S > kPlanMaxSlots) return false;
+    const long long G = (S + tm - 1) / tm + E;
+    return G * tm < (1ll << 31);
+}
+
+// The activation buffers are addressed with 32-bit byte offsets: x [T, D], h [Rp, I] and y [Rp, D] stay below 2 GiB.
+static bool pf_bytes_ok(long long T, long long kk, long long E, long long I, long long D) {
+    const long long Rp = ((T * kk + kPfTm - 1) / kPfTm + E) * kPfTm;
+    const long long lim = 1ll << 31;
+    return T * D * 2 < lim && Rp * I * 2 < lim && Rp * D * 2 < lim;
+}
+
+static int launch_plan(const int32_t *idx, const float *w, int T, int k, int shared, int E, int tm, PlanOut p,
+                       hipStream_t s) {
+    hipLaunchKernelGGL(ragged_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, idx, w, T, k, shared, E, tm, p);
+    return hipGetLastError() == hipSuccess ? MI_OK : MI_ERR_LAUNCH;
+}
+
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" {
+
+int mi_ragged_plan(const int32_t *idx, const float *w, int32_t T, int32_t k, int32_t E, int32_t tm,
+                   int32_t *blk_expert, int32_t *n_blocks, int32_t *tok_row, float *w_row, int32_t *row_slot,
+                   void *stream) {
+    if (!idx || !w || !blk_expert || !n_blocks || !tok_row || !w_row || !row_slot) return MI_ERR_NULL;
+    if (T <= 0 || k <= 0) return MI_ERR_TOKENS;
+    if (E <= 0 || E > kPlanMaxE || tm <= 0 || tm > 65536) return MI_ERR_ARG;
+    if (!plan_sizes_ok(T, k, E, tm)) return MI_ERR_TOKENS;
+    PlanOut p{blk_expert, n_blocks, tok_row, w_row, row_slot, nullptr};
+    return launch_plan(idx, w, T, k, -1, E, tm, p, (hipStream_t)stream);
+}
+
+size_t mi_moe_prefill_workspace(const mi_table *gate, const mi_table *down, int32_t T, int32_t k,
+                                int32_t shared_expert) {
+    if (!gate || !down || k <= 0) return 0;
+    const int kk = k + (shared_expert >= 0 ? 1 : 0);
+    if (!plan_sizes_ok(T, kk, gate->n_experts, kPfTm) || !pf_bytes_ok(T, kk, gate->n_experts, gate->rows, down->rows))
+        return 0;
+    return pf_layout(T, kk, gate->n_experts, gate->rows, down->rows).total;
+}
+
+int mi_moe_prefill(const mi_table *gate, const mi_table *up, const mi_table *down, const uint16_t *x_bf16, int32_t T,
+                   int32_t k, const int32_t *idx, const float *w, int32_t shared_expert, float limit, int32_t combine,
+                   float *out_f32, uint16_t *out_bf16, void *workspace, size_t workspace_bytes, void *stream) {
+    int st;
+    if ((st = pf_validate(gate, up, down))) return st;
+    if (!x_bf16 || !idx || !w || (!out_f32 && !out_bf16)) return MI_ERR_NULL;
+    const int E = gate->n_experts, I = gate->rows, D = down->rows;
+    if (T <= 0 || k <= 0) return MI_ERR_TOKENS;
+    if (shared_expert >= E || shared_expert < -1) return MI_ERR_ARG;
+    const int kk = k + (shared_expert >= 0 ? 1 : 0);
+    if (!plan_sizes_ok(T, kk, E, kPfTm) || !pf_bytes_ok(T, kk, E, I, D)) return MI_ERR_TOKENS;
+    if (!(limit > 0.0f) || (combine != MI_COMBINE_MATMUL && combine != MI_COMBINE_GATHER)) return MI_ERR_ARG;
+    const PfLayout L = pf_layout(T, kk, E, I, D);
+    if (!workspace || workspace_bytes < L.total) return MI_ERR_WORKSPACE;
+    char *ws = (char *)workspace;
+    hipStream_t s = (hipStream_t)stream;
+    PlanOut p;
+    p.blk_expert = (int32_t *)(ws + L.off_be);
+    p.n_blocks = (int32_t *)(ws + L.off_nb);
+    p.blk_n = (int32_t *)(ws + L.off_bn);
+    p.tok_row = (int32_t *)(ws + L.off_tr);
+    p.w_row = (float *)(ws + L.off_wr);
+    p.row_slot = (int32_t *)(ws + L.off_rs);
+    uint16_t *h = (uint16_t *)(ws + L.off_h), *y = (uint16_t *)(ws + L.off_y);
+    if ((st = launch_plan(idx, w, T, k, shared_expert, E, kPfTm, p, s))) return st;
+
+    PfArgs a{};
+    a.t0 = pf_table(gate);
+    a.t1 = pf_table(up);
+    a.R = I;
+    a.K = gate->cols;
+    a.blk_expert = p.blk_expert;
+    a.blk_n = p.blk_n;
+    a.n_blocks = p.n_blocks;
+    a.tok_row = p.tok_row;
+    a.x = x_bf16;
+    a.x_bytes = (uint32_t)((size_t)T * a.K * 2);
+    a.gather = 1;
+    a.out = h;
+    a.limit = limit;
+    a.wg_rows = 2;
+    a.RBG = I / 128;
+    hipLaunchKernelGGL(prefill_kernel<0>, dim3(L.G * a.RBG), dim3(64 * kPfWaves), 0, s, a);
+    if (hipGetLastError() != hipSuccess) return MI_ERR_LAUNCH;
+
+    PfArgs b = a;
+    b.t0 = b.t1 = pf_table(down);
+    b.R = D;
+    b.K = I;
+    b.x = h;
+    b.x_bytes = (uint32_t)(L.Rp * I * 2);
+    b.gather = 0;
+    b.out = y;
+    b.wg_rows = 4;
+    b.RBG = D / 256;
+    hipLaunchKernelGGL(prefill_kernel<1>, dim3(L.G * b.RBG), dim3(64 * kPfWaves), 0, s, b);
+    if (hipGetLastError() != hipSuccess) return MI_ERR_LAUNCH;
+
+    const long long nthr = (long long)T * (D / 4);
+    hipLaunchKernelGGL(prefill_combine, dim3((unsigned)((nthr + 255) / 256)), dim3(256), 0, s, (const uint16_t *)y,
+                       (const int32_t *)p.row_slot, w, T, k, kk, D, combine == MI_COMBINE_MATMUL ? 1 : 0, out_f32,
+                       out_bf16);
+    return hipGetLastError() == hipSuccess ? MI_OK : MI_ERR_LAUNCH;
+}
+
+}  // extern "C"

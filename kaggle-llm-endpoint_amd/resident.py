@@ -98,9 +98,8 @@ class ExpertTable:
 
 
 class _Workspaces:
-    """Device workspaces, one per (device, stream, purpose); grown on demand, zero-filled when allocated (the int8
-    kernel's completion counters start at zero and every completed call leaves them at zero; the decode and matvec
-    workspaces need no initialisation)."""
+    """Device workspaces, one per (device, stream, purpose); grown on demand.  No entry point needs its workspace
+    initialised; they are zero-filled when allocated only so that their contents are defined."""
 
     def __init__(self):
         self._ws = {}
@@ -197,6 +196,70 @@ def moe_decode(gate, up, down, x, idx, w, limit, shared_expert=-1, want_f32=True
     return of, ob
 
 
+def ragged_plan(idx, w, E, tm):
+    """ragged_plan (pallas_moe.py:564-592) on the device: idx int32 [T, k], w f32 [T, k] -> dict of device tensors
+    blk_expert int32 [G], n_blocks int32 [1], tok_row int32 [Rp], w_row f32 [Rp], row_slot int32 [T, k] with
+    G = ceil(T*k / tm) + E, Rp = G * tm (slots sorted stably by expert, every expert padded to whole blocks)."""
+    if idx.dtype != torch.int32:
+        idx = idx.to(torch.int32)
+    if w.dtype != torch.float32:
+        w = w.to(torch.float32)
+    idx, w = idx.contiguous(), w.contiguous()
+    T, k = idx.shape
+    G = -(-(T * k) // tm) + E
+    dev = idx.device
+    out = {"blk_expert": torch.empty(G, dtype=torch.int32, device=dev),
+           "n_blocks": torch.empty(1, dtype=torch.int32, device=dev),
+           "tok_row": torch.empty(G * tm, dtype=torch.int32, device=dev),
+           "w_row": torch.empty(G * tm, dtype=torch.float32, device=dev),
+           "row_slot": torch.empty((T, k), dtype=torch.int32, device=dev)}
+    check("mi_ragged_plan", lib().mi_ragged_plan(_ptr(idx), _ptr(w), T, k, int(E), int(tm),
+                                                 _ptr(out["blk_expert"]), _ptr(out["n_blocks"]),
+                                                 _ptr(out["tok_row"]), _ptr(out["w_row"]), _ptr(out["row_slot"]),
+                                                 _stream()))
+    return out
+
+
+def prefill_workspace_bytes(gate, down, T, k, shared_expert=-1):
+    n = lib().mi_moe_prefill_workspace(gate.c, down.c, int(T), int(k), int(shared_expert))
+    if n == 0:
+        raise ValueError("mi_moe_prefill: invalid tables or token counts (T=%d, k=%d)" % (T, k))
+    return n
+
+
+def moe_prefill(gate, up, down, x, idx, w, limit, shared_expert=-1, combine="matmul", want_f32=True,
+                want_bf16=False, out_f32=None, out_bf16=None, workspace=None):
+    """Grouped prefill MoE (resident.py:144-165 composition) on the matrix cores: slots sorted by expert
+    (ragged_plan), h = bf16(swiglu(x Wg^T, x Wu^T)), y = bf16(h Wd^T), out = sum_j wt * y with wt = bf16(w)
+    (``combine="matmul"``) or w (``"gather"``), f32 accumulation throughout.
+    x bf16 [T, D]; idx int32 [T, k]; w f32 [T, k] -> (out_f32 [T, D] or None, out_bf16 [T, D] or None).
+    Preallocated outputs and ``workspace`` (uint8, prefill_workspace_bytes) make the call allocation-free."""
+    if x.dtype != torch.bfloat16:
+        raise ValueError("prefill activations are bf16")
+    if combine not in _lib.COMBINES:
+        raise ValueError("combine must be 'matmul' or 'gather'")
+    T, k = idx.shape
+    x = x.contiguous()
+    if idx.dtype != torch.int32:
+        idx = idx.to(torch.int32)
+    if w.dtype != torch.float32:
+        w = w.to(torch.float32)
+    idx, w = idx.contiguous(), w.contiguous()
+    D = down.rows
+    of, ob = out_f32, out_bf16
+    if of is None and want_f32:
+        of = torch.empty((T, D), dtype=torch.float32, device=x.device)
+    if ob is None and want_bf16:
+        ob = torch.empty((T, D), dtype=torch.bfloat16, device=x.device)
+    ws = workspace
+    if ws is None:
+        ws = WORKSPACES.get("prefill", prefill_workspace_bytes(gate, down, T, k, shared_expert))
+    check("mi_moe_prefill", lib().mi_moe_prefill(gate.c, up.c, down.c, _ptr(x), T, k, _ptr(idx), _ptr(w),
+                                                 int(shared_expert), float(limit), _lib.COMBINES[combine],
+                                                 _ptr(of), _ptr(ob), _ptr(ws), ws.numel(), _stream()))
+    return of, ob
+
+
 def int8_project(x, qT, s, want_f32=False, y_bf16=None, y_f32=None, workspace=None):
     """y = x @ bf16(f32(q) * s) (quant8.py:91-99): x bf16 [B, n_in], qT int8 [n_out, n_in], s f32 [n_out].
     Preallocated outputs / workspace make the call allocation-free."""
@@ -250,8 +313,8 @@ class ResidentFetch:
 
     apply(p, x, idx, w, layer, limit): x [N, D]; idx [N, k] int32 into E; w [N, k] f32 -> f32 [N, D] (routed experts
     only; the caller adds the shared expert, model.py:847-855).  N*k <= gather_max_rows takes the fused decode
-    kernels (f32 end to end, resident.py:110-120); larger calls would take the grouped prefill path
-    (resident.py:144-165), not built yet (NotImplementedError).
+    kernels (f32 end to end, resident.py:110-120); larger calls take the grouped prefill GEMMs with the reference's
+    bf16 rounding points and ``combine`` (resident.py:144-165; CB3 tables; bf16 ``out_dtype``).
     ``use_pallas`` / ``interpret`` / ``sweep_mode`` / ``chunk`` are accepted for signature compatibility; there is a
     single MI355X kernel path per regime."""
 
@@ -290,6 +353,11 @@ class ResidentFetch:
                 raise ValueError("decode activations must be bf16-representable (the layer dtype)")
             out, _ = moe_decode(gate, up, down, xb, idx, w, limit)
             return out
-        raise NotImplementedError("ResidentFetch.apply: N*k = %d > gather_max_rows = %d takes the grouped prefill path "
-                                  "(resident.py:144-165), which this build does not provide yet" % (N * k,
-                                                                                                     self.gather_max_rows))
+        if gate.qtype != "CB3" or up.qtype != "CB3" or down.qtype != "CB3":
+            raise NotImplementedError("ResidentFetch.apply: the grouped prefill path (N*k = %d > gather_max_rows = %d) "
+                                      "is built for CB3 tables only" % (N * k, self.gather_max_rows))
+        if self.out_dtype != torch.bfloat16:
+            raise NotImplementedError("ResidentFetch.apply: the grouped prefill path follows the bf16 out_dtype "
+                                      "rounding points (resident.py:153-158)")
+        out, _ = moe_prefill(gate, up, down, x.to(torch.bfloat16), idx, w, limit, combine=self.combine)
+        return out

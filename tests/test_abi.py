@@ -80,3 +80,29 @@ def test_host_validation_codes(L, pkg):
     assert L.mi_int8_project(x, 8, P(1), P(2), 256, 64, None, None, ws, 1 << 20, None) == 1
     assert L.mi_int8_project_workspace(8, 6144, 6144) > 0
     assert L.mi_int8_project_workspace(8, 300, 64) == 0
+
+
+def test_prefill_host_validation(L, pkg):
+    P = ctypes.c_void_p
+    x, idx, w, out, ws = P(0x10000), P(0x20000), P(0x30000), P(0x40000), P(0x50000)
+    g, u, d = _table(pkg, rows=256, cols=1280), _table(pkg, rows=256, cols=1280), _table(pkg, rows=1280, cols=256)
+    call = lambda gg, uu, dd, T=4, k=2, shared=-1, limit=10.0, comb=0, o=out, wsb=1 << 30: L.mi_moe_prefill(
+        ctypes.byref(gg), ctypes.byref(uu), ctypes.byref(dd), x, T, k, idx, w, shared, ctypes.c_float(limit), comb,
+        o, None, ws, wsb, None)
+    assert call(_table(pkg, qtype=2, planes=5), u, d) == 2                       # MI_ERR_QTYPE: CB3 tables only
+    assert call(_table(pkg, rows=192), _table(pkg, rows=192), d) == 3             # gate rows % 128
+    assert call(g, u, _table(pkg, rows=1152, cols=256)) == 3                     # down rows % 256
+    assert call(g, u, _table(pkg, rows=1280, cols=512)) == 6                     # down.cols != gate.rows
+    assert call(g, u, d, T=0) == 4 and call(g, u, d, k=0) == 4                   # MI_ERR_TOKENS
+    assert call(g, u, d, T=1 << 22, k=8) == 4                                    # past the slot / byte limits
+    assert call(g, u, d, shared=4) == 8 and call(g, u, d, comb=2) == 8           # MI_ERR_ARG
+    assert call(g, u, d, limit=-1.0) == 8
+    assert call(g, u, d, o=None) == 1                                            # no output
+    assert call(g, u, d, wsb=16) == 5                                            # MI_ERR_WORKSPACE
+    assert L.mi_moe_prefill_workspace(ctypes.byref(g), ctypes.byref(d), 512, 8, 3) > 0
+    assert L.mi_moe_prefill_workspace(ctypes.byref(g), ctypes.byref(d), 0, 8, -1) == 0
+    outs = [P(0x60000 + 0x1000 * i) for i in range(5)]
+    plan = lambda T=4, k=2, E=8, tm=32, i=idx: L.mi_ragged_plan(i, w, T, k, E, tm, *outs, None)
+    assert plan(E=0) == 8 and plan(E=1025) == 8 and plan(tm=0) == 8              # MI_ERR_ARG
+    assert plan(T=0) == 4 and plan(T=1 << 21, k=4) == 4                          # MI_ERR_TOKENS
+    assert plan(i=None) == 1                                                     # MI_ERR_NULL

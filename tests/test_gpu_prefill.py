@@ -1,0 +1,129 @@
+"""GPU parity of the grouped prefill path (resident.py:144-165): the device ragged_plan, the CB3 grouped GEMMs on
+the matrix cores and the combine, against the CPU oracle.
+
+Bar: the plan is bit-exact against oracle.moe.ragged_plan (pallas_moe.py:564-592 restated in numpy); prefill
+outputs within rel-L2 <= 1e-3 of oracle.moe.prefill_apply, which rounds where the reference rounds (x, h and y to
+bf16, the matmul combine's routing weights to bf16) and accumulates in f64.  The kernels accumulate in f32, so an h
+or y element next to a bf16 rounding boundary may round the other way: the observed distance is ~1e-5.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe as omoe
+from oracle.bf16 import rel_l2, round_bf16
+from tests.util import Layer, softmax_topk_routing, zipf_routing
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def _t(a, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    return t.to(dtype) if dtype is not None else t
+
+
+def _routing(rng, kind, T, E, k):
+    if kind == "uniform":
+        return (rng.integers(0, E, (T, k)).astype(np.int32),
+                rng.random((T, k)).astype(np.float32))
+    if kind == "one":
+        return np.zeros((T, k), np.int32), rng.random((T, k)).astype(np.float32)
+    if kind == "softmax":
+        return softmax_topk_routing(rng, T, E, k)
+    return zipf_routing(rng, T, E, k)
+
+
+@pytest.mark.parametrize("T,k,E,tm,kind", [(1, 8, 64, 32, "uniform"), (512, 8, 64, 32, "uniform"),
+                                           (37, 4, 12, 16, "zipf"), (300, 8, 64, 96, "zipf"),
+                                           (2000, 8, 64, 32, "uniform"), (50, 2, 3, 1, "zipf"),
+                                           (64, 8, 1024, 7, "uniform"), (5, 3, 5, 1000, "zipf"),
+                                           (700, 3, 4, 32, "one")])
+def test_ragged_plan_bit_exact(pkg, gpu, T, k, E, tm, kind):
+    rng = np.random.default_rng(T * 31 + E)
+    idx, w = _routing(rng, kind, T, E, k)
+    got = {key: v.cpu().numpy() for key, v in pkg.ragged_plan(_t(idx), _t(w), E, tm).items()}
+    want = omoe.ragged_plan(idx, w, E, tm)
+    for key in ("blk_expert", "n_blocks", "tok_row", "row_slot"):
+        assert np.array_equal(got[key], want[key]), key
+    assert np.array_equal(got["w_row"].view(np.uint32), want["w_row"].view(np.uint32))
+
+
+def _oracle_prefill(L, x, idx, w, limit, E, shared, combine):
+    if shared is not None:
+        idx = np.concatenate([idx, np.full((idx.shape[0], 1), shared, np.int32)], axis=1)
+        w = np.concatenate([w, np.ones((w.shape[0], 1), np.float32)], axis=1)
+        E = E + 1
+    return omoe.prefill_apply(L.deq, x, idx, w, limit, E, combine=combine)
+
+
+@pytest.mark.parametrize("T,k,E,D,I,shared,combine,kind", [
+    (40, 4, 6, 512, 256, False, "matmul", "zipf"),
+    (40, 4, 6, 512, 256, True, "gather", "zipf"),
+    (200, 2, 3, 1280, 384, True, "matmul", "zipf"),       # experts with several blocks of 96 rows
+    (1, 8, 16, 512, 256, False, "matmul", "softmax"),
+    (97, 1, 2, 512, 256, False, "gather", "one"),         # one expert: a full block and a 1-row block
+    (33, 3, 5, 768, 128, True, "matmul", "uniform"),
+])
+def test_prefill_small(pkg, gpu, T, k, E, D, I, shared, combine, kind):
+    rng = np.random.default_rng(7 * T + E)
+    limit = 10.0
+    L = Layer(rng, "CB3", E + (1 if shared else 0), D, I)
+    tbs = L.tables(pkg)
+    idx, w = _routing(rng, kind, T, E, k)
+    x = round_bf16(rng.standard_normal((T, D)).astype(np.float32))
+    se = E if shared else -1
+    of, ob = pkg.moe_prefill(tbs["gate"], tbs["up"], tbs["down"], _t(x, torch.bfloat16), _t(idx), _t(w), limit,
+                             shared_expert=se, combine=combine, want_bf16=True)
+    want = _oracle_prefill(L, x, idx, w, limit, E, E if shared else None, combine)
+    err = rel_l2(of.cpu().numpy(), want)
+    assert err < TOL, err
+    assert torch.equal(ob, of.to(torch.bfloat16))
+    of2, _ = pkg.moe_prefill(tbs["gate"], tbs["up"], tbs["down"], _t(x, torch.bfloat16), _t(idx), _t(w), limit,
+                             shared_expert=se, combine=combine)
+    assert torch.equal(of, of2)                      # deterministic
+
+
+def test_prefill_limit_clamps(pkg, gpu):
+    """A small swiglu limit makes the clamps of model.py:119-122 active in the gate/up epilogue."""
+    rng = np.random.default_rng(4)
+    E, D, I, T, k, limit = 5, 512, 256, 60, 3, 0.05
+    L = Layer(rng, "CB3", E, D, I)
+    tbs = L.tables(pkg)
+    idx, w = zipf_routing(rng, T, E, k)
+    x = round_bf16(rng.standard_normal((T, D)).astype(np.float32))
+    of, _ = pkg.moe_prefill(tbs["gate"], tbs["up"], tbs["down"], _t(x, torch.bfloat16), _t(idx), _t(w), limit)
+    assert rel_l2(of.cpu().numpy(), _oracle_prefill(L, x, idx, w, limit, E, None, "matmul")) < TOL
+
+
+def test_prefill_full_shape(pkg, gpu):
+    """The benchmark layer's matrix shapes (hidden 6144, intermediate 2048) with two routed experts and the shared
+    expert: 200 tokens put 200 rows on each expert, three blocks of up to 96 rows each."""
+    rng = np.random.default_rng(2026)
+    E, D, I, T, k, limit = 2, 6144, 2048, 200, 2, 10.0
+    L = Layer(rng, "CB3", E + 1, D, I)
+    tbs = L.tables(pkg)
+    idx = np.tile(np.array([[0, 1]], np.int32), (T, 1))
+    idx[::2] = idx[::2, ::-1]
+    w = rng.random((T, k)).astype(np.float32)
+    x = round_bf16(rng.standard_normal((T, D)).astype(np.float32))
+    of, _ = pkg.moe_prefill(tbs["gate"], tbs["up"], tbs["down"], _t(x, torch.bfloat16), _t(idx), _t(w), limit,
+                            shared_expert=E)
+    err = rel_l2(of.cpu().numpy(), _oracle_prefill(L, x, idx, w, limit, E, E, "matmul"))
+    assert err < TOL, err
+
+
+def test_resident_fetch_prefill(pkg, gpu):
+    """ResidentFetch.apply with N*k > gather_max_rows takes the grouped prefill path (resident.py:104-108)."""
+    rng = np.random.default_rng(8)
+    E, D, I, T, k, limit = 8, 512, 256, 24, 4, 10.0
+    L = Layer(rng, "CB3", E, D, I)
+    p = {}
+    for name, key in (("gate", "gate_q"), ("up", "up_q"), ("down", "down_q")):
+        p[key] = pkg.to_device_planes(L.planes(name, pkg.formats))
+    fetch = pkg.ResidentFetch({0: {"gate_q": "CB3", "up_q": "CB3", "down_q": "CB3"}}, D, I)
+    idx, w = zipf_routing(rng, T, E, k)
+    x = round_bf16(rng.standard_normal((T, D)).astype(np.float32))
+    y = fetch.apply(p, _t(x, torch.bfloat16), _t(idx), _t(w), 0, limit)
+    assert y.dtype == torch.float32 and tuple(y.shape) == (T, D)
+    assert rel_l2(y.cpu().numpy(), _oracle_prefill(L, x, idx, w, limit, E, None, "matmul")) < TOL
