@@ -43,6 +43,7 @@ def parse():
     ap.add_argument("--copies", type=int, default=6, help="independent layer copies rotated between steps")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only-b1", action="store_true", help="headline only (profiling runs)")
+    ap.add_argument("--only-prefill", action="store_true", help="the 512-token prefill chunk only (profiling runs)")
     ap.add_argument("--calib", action="store_true",
                     help="end with one plain 256 MiB device copy (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
@@ -227,6 +228,9 @@ def main():
         avg_bytes = float(np.mean([nbytes[i % L] for i in range(steps)]))
         return ms, avg_bytes
 
+    if args.only_prefill:
+        print(json.dumps({"prefill_t512": bench_prefill(torch, pkg, gen, args, layers, rng)}))
+        return
     # headline: batch 1 layer
     ms1, bytes1 = measure(1, softmax_topk)
     gbs1 = bytes1 / (ms1 * 1e-3) / 1e9

@@ -16,11 +16,15 @@
 
 namespace mi {
 
-constexpr int kPfTT = 6;                   // token tiles of 16 rows per block
+constexpr int kPfTT = 5;                   // token tiles of 16 rows per block
 constexpr int kPfTm = 16 * kPfTT;          // rows per block of the prefill's own plan
 constexpr int kPfWaves = 4;
 constexpr int kPfRtw = 4;                  // row tiles per wavefront (64 weight rows)
-constexpr int kPfXPitch = 84;              // dwords per staged activation row of one column tile (80 + skew)
+constexpr int kPfXPitch = 88;              // dwords per staged activation row of one column tile (80 + 8: the
+                                           // fastest pitch for this read pattern on gfx950, measured)
+constexpr int kPfGPitch = kPfTm + 4;       // floats per row of the gate/up epilogue's exchange (skewed banks)
+constexpr int kXcds = 8;                   // accelerator complex dies of MI355X (one L2 each)
+constexpr uint32_t kXOut = 0x80000000u;    // activation offset past every buffer's byte range (reads zero)
 constexpr int kPlanThreads = 1024;
 constexpr int kPlanWaves = kPlanThreads / 64;
 constexpr int kPlanMaxE = 1024;
@@ -190,29 +194,40 @@ struct PfArgs {
     int RBG;                               // workgroups per block
 };
 
-template <int M>
-__device__ __forceinline__ void pf_steps(const uint4 (&wv)[kPfRtw], const uint4 *cbrow, int slot0, int slot1,
-                                         const uint32_t *xrow, int ntt, f32x4 (&acc)[kPfRtw][kPfTT]) {
+// k-steps M..4 of column tile C.  cbr[r] holds the codebook of row tile r's current group: it switches to LDS slot
+// C + 1 at step 4 - C and is carried into the next column tile, which starts in that group, so a super tile reads
+// each of its five groups from LDS once.  NTT (the block's token tiles) is a compile-time count, so a step's B
+// reads and matrix-core instructions form one straight-line block.
+template <int NTT, int C, int M>
+__device__ __forceinline__ void pf_steps(const uint4 (&wv)[kPfRtw], const uint4 *cbrow, uint4 (&cbr)[kPfRtw],
+                                         const uint32_t *xrow, f32x4 (&acc)[kPfRtw][NTT]) {
     if constexpr (M < 5) {
         // one k-step at a time: left free, the scheduler hoists every step's LDS reads and decodes and spills
         if constexpr (M > 0) __builtin_amdgcn_sched_barrier(0);
-        bf16x8 A[kPfRtw];
-        const int slot = M < slot1 ? slot0 : slot0 + 1;     // slot1 = 4 - C: first step of the next group
+        if constexpr (M == 4 - C) {
+#pragma unroll
+            for (int r = 0; r < kPfRtw; ++r) cbr[r] = cbrow[(C + 1) * 64 + 16 * r];
+        }
+        // the step's B operands first; then row tile by row tile, so the decode of row tile r + 1 (vector ALU)
+        // issues while the matrix-core instructions of row tile r run
+        uint4 b[NTT];
+#pragma unroll
+        for (int tt = 0; tt < NTT; ++tt) b[tt] = *(const uint4 *)(xrow + tt * 16 * kPfXPitch + 16 * M);
+        uint32_t s0, s1;
+        cb3_sel<M>(wv[0], s0, s1);
+        bf16x8 A = cb3_weights8(s0, s1, cbr[0]);
 #pragma unroll
         for (int r = 0; r < kPfRtw; ++r) {
-            uint32_t s0, s1;
-            cb3_sel<M>(wv[r], s0, s1);
-            A[r] = cb3_weights8(s0, s1, cbrow[slot * 64 + 16 * r]);
-        }
-#pragma unroll
-        for (int tt = 0; tt < kPfTT; ++tt) {
-            if (tt < ntt) {
-                const uint4 b = *(const uint4 *)(xrow + tt * 16 * kPfXPitch + 16 * M);
-#pragma unroll
-                for (int r = 0; r < kPfRtw; ++r) acc[r][tt] = mfma16(A[r], b, acc[r][tt]);
+            bf16x8 An = A;
+            if (r + 1 < kPfRtw) {
+                cb3_sel<M>(wv[r + 1], s0, s1);
+                An = cb3_weights8(s0, s1, cbr[r + 1]);
             }
+#pragma unroll
+            for (int tt = 0; tt < NTT; ++tt) acc[r][tt] = mfma16(A, b[tt], acc[r][tt]);
+            A = An;
         }
-        pf_steps<M + 1>(wv, cbrow, slot0, slot1, xrow, ntt, acc);
+        pf_steps<NTT, C, M + 1>(wv, cbrow, cbr, xrow, acc);
     }
 }
 
@@ -221,20 +236,24 @@ __device__ __forceinline__ void pf_steps(const uint4 (&wv)[kPfRtw], const uint4 
 struct PfRegs {
     uint4 ring[2][kPfRtw];    // slot c & 1 = column tile c
     uint4 cbv[5];             // codebook groups of the next super tile, as in Cb3Regs
+    uint4 cbr[kPfRtw];        // codebook of the current group, per row tile (lane (q, i): row 16 r + i)
 };
 
 // Column tile C of super tile st (codebook slots as in cb3_ctile), B operands from the staged tile.
-template <int C>
-__device__ __forceinline__ void pf_ctile(const Cb3Wave &w, PfRegs &s, int st, const uint32_t *xrow, int ntt,
-                                         f32x4 (&acc)[kPfRtw][kPfTT]) {
+template <int NTT, int C>
+__device__ __forceinline__ void pf_ctile(const Cb3Wave &w, PfRegs &s, int st, const uint32_t *xrow,
+                                         f32x4 (&acc)[kPfRtw][NTT]) {
     const int lane = threadIdx.x & 63;
     const int gn = 5 * (st + 1);
+    const uint4 *cbrow = w.cbl + (lane & 15);
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (C == 0) {
         w.cbl[0 * 64 + lane] = s.cbv[0];
         w.cbl[1 * 64 + lane] = s.cbv[1];
         s.cbv[0] = cb3_group(w, gn);
         s.cbv[1] = cb3_group(w, gn + 1);
+#pragma unroll
+        for (int r = 0; r < kPfRtw; ++r) s.cbr[r] = cbrow[16 * r];
     } else {
         w.cbl[(C + 1) * 64 + lane] = s.cbv[C + 1];
         s.cbv[C + 1] = cb3_group(w, gn + C + 1);
@@ -246,22 +265,24 @@ __device__ __forceinline__ void pf_ctile(const Cb3Wave &w, PfRegs &s, int st, co
         wv[r] = s.ring[C & 1][r];
         s.ring[C & 1][r] = cb3_tile(w, ct + 2, r);
     }
-    pf_steps<0>(wv, w.cbl + (lane & 15), C, 4 - C, xrow, ntt, acc);
+    pf_steps<NTT, C, 0>(wv, cbrow, s.cbr, xrow, acc);
 }
 
-template <int MODE>   // 0: gate/up -> h, 1: down -> y
-__global__ void __launch_bounds__(64 * kPfWaves, 2) prefill_kernel(PfArgs a) {
-    __shared__ uint4 cbl[kPfWaves * 5 * 64];                // per-wavefront codebook slots (20 KB)
-    __shared__ uint32_t xs[kPfTm * kPfXPitch];               // one column tile of the block's rows (31.5 KB);
-                                                             // gate/up epilogue: the gate accumulators of one pair
+struct PfShared {
+    uint4 cbl[kPfWaves * 5 * 64];                // per-wavefront codebook slots (20 KB)
+    uint32_t xs[2][kPfTm * kPfXPitch];           // column tiles ct (even/odd) of the block's rows, double-buffered;
+                                                 // gate/up epilogue: the gate accumulators of one (gate, up) pair
+    uint32_t xrowoff[kPfTm];                     // byte offset of every row's activations, or kXOut
+};
+
+// One workgroup: block g (expert e, rows row0 .. row0 + n - 1, NTT = ceil(n / 16) token tiles), row range rbg.
+template <int MODE, int NTT>
+__device__ __forceinline__ void prefill_body(const PfArgs &a, PfShared &sh, int g, int rbg, int e, int n) {
+    uint4 *cbl = sh.cbl;
+    uint32_t *xs = &sh.xs[0][0], *xrowoff = sh.xrowoff;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int g = blockIdx.x / a.RBG, rbg = blockIdx.x - (blockIdx.x / a.RBG) * a.RBG;
-    if (g >= *a.n_blocks) return;
-    const int e = __builtin_amdgcn_readfirstlane(a.blk_expert[g]);
-    const int n = __builtin_amdgcn_readfirstlane(a.blk_n[g]);
     const int row0 = g * kPfTm;
-    const int ntt = (n + 15) >> 4;
     const int mat = MODE == 0 ? (wave & 1) : 0;
     const Cb3Table &tb = mat ? a.t1 : a.t0;
     const int rg = rbg * a.wg_rows + (MODE == 0 ? (wave >> 1) : wave);   // 64-row group of this wavefront
@@ -294,66 +315,63 @@ __global__ void __launch_bounds__(64 * kPfWaves, 2) prefill_kernel(PfArgs a) {
 #pragma unroll
     for (int c = 0; c < 5; ++c) s.cbv[c] = cb3_group(w, c);
 
-    // activation tile: kPfTm rows x 20 uint4 (160 columns) over 256 threads, as buffer loads; entries of rows >= n
-    // and of columns >= K take an offset past the buffer's range, which reads zero without touching memory
-    constexpr int kXU = kPfTm * 20;
-    constexpr int kXJ = (kXU + 64 * kPfWaves - 1) / (64 * kPfWaves);
-    constexpr uint32_t kXOut = 0x80000000u;                  // >= every buffer's byte range
+    // activation tile: the block's 16 NTT rows x 20 uint4 (160 columns), staged by 240 threads as buffer loads, 12
+    // rows per pass (thread t: row t / 20 + 12 j, uint4 column t % 20), so every pass is a constant offset from the
+    // first; rows >= n and columns >= K take an offset past the buffer's range, which reads zero
+    constexpr int kXRows = (64 * kPfWaves) / 20;              // 12
+    constexpr int kXBuf = kPfTm * kPfXPitch;                  // dwords per tile buffer
+    constexpr int kXJ = (16 * NTT + kXRows - 1) / kXRows;
     const __amdgpu_buffer_rsrc_t xbuf =
         __builtin_amdgcn_make_buffer_rsrc((void *)a.x, (short)0, (int)a.x_bytes, kBufferWord3);
-    const int c0 = tid % 20;
-    uint32_t xoff[kXJ];                                      // byte offset of the entry in its row tile, or kXOut
-#pragma unroll
-    for (int j = 0; j < kXJ; ++j) {
-        const int u = tid + 64 * kPfWaves * j, row = u / 20;
+    if (tid < kPfTm) {
         uint32_t o = kXOut;
-        if (u < kXU && row < n) {
-            const int src = a.gather ? a.tok_row[row0 + row] : row0 + row;
-            o = (uint32_t)src * (uint32_t)a.K * 2u + 16u * (uint32_t)(u - row * 20);
-        }
-        xoff[j] = o;
+        if (tid < n) o = (uint32_t)(a.gather ? a.tok_row[row0 + tid] : row0 + tid) * (uint32_t)a.K * 2u;
+        xrowoff[tid] = o;
     }
+    __syncthreads();
+    const int xr0 = tid / 20, xc8 = tid - xr0 * 20;
+    const bool stager = tid < kXRows * 20;
     uint4 xr[kXJ];
     auto load_x = [&](int ct) {
         const int lim = (a.K - kCb3TileCols * ct) >> 3;       // uint4 columns of this tile inside the row
 #pragma unroll
         for (int j = 0; j < kXJ; ++j) {
-            int c8 = c0 + (16 * j) % 20;                      // (tid + 256 j) % 20
-            c8 -= c8 >= 20 ? 20 : 0;
-            const uint32_t o = c8 < lim ? xoff[j] + (uint32_t)(2 * kCb3TileCols * ct) : kXOut;
+            const int row = xr0 + kXRows * j;
+            uint32_t o = kXOut;
+            if (stager && row < 16 * NTT && xc8 < lim)
+                o = xrowoff[row] + 16u * (uint32_t)xc8 + (uint32_t)(2 * kCb3TileCols * ct);
             xr[j] = bload(xbuf, o, 0);
         }
     };
-    auto store_x = [&]() {
+    auto store_x = [&](int buf) {
 #pragma unroll
         for (int j = 0; j < kXJ; ++j) {
-            const int u = tid + 64 * kPfWaves * j;
-            if (u < kXU) {
-                const int row = u / 20, c8 = u - row * 20;
-                *(uint4 *)(xs + row * kPfXPitch + 4 * c8) = xr[j];
-            }
+            const int row = xr0 + kXRows * j;
+            if (stager && row < 16 * NTT) *(uint4 *)(xs + buf * kXBuf + row * kPfXPitch + 4 * xc8) = xr[j];
         }
     };
     load_x(0);
+    store_x(0);
 
-    f32x4 acc[kPfRtw][kPfTT];
+    f32x4 acc[kPfRtw][NTT];
 #pragma unroll
     for (int r = 0; r < kPfRtw; ++r)
 #pragma unroll
-        for (int t = 0; t < kPfTT; ++t) acc[r][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < NTT; ++t) acc[r][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
     const int jt = lane & 15, q = lane >> 4;
     const uint32_t *xrow = xs + jt * kPfXPitch + 4 * q;
     const int CT = tb.CT;
 
-    // every wavefront runs the same column tiles, so the barriers around each staging line up
+    // one barrier per column tile: tile ct sits in buffer ct & 1 (= C & 1); the next tile's loads are issued first
+    // (ahead of this tile's code and codebook loads, so waiting for them never waits for those) and stored into the
+    // other buffer after this tile's matrix-core work, which every wavefront finished reading one barrier earlier
     auto step = [&](auto Cc, int st) {
         constexpr int C = decltype(Cc)::value;
         const int ct = 4 * st + C;
-        __syncthreads();                  // every wavefront is done with the previous tile
-        store_x();
         __syncthreads();
         if (ct + 1 < CT) load_x(ct + 1);
-        pf_ctile<C>(w, s, st, xrow, ntt, acc);
+        pf_ctile<NTT, C>(w, s, st, xrow + (C & 1) * kXBuf, acc);
+        if (ct + 1 < CT) store_x((C + 1) & 1);
     };
     const int st_full = CT >> 2;
     int st = 0;
@@ -371,21 +389,21 @@ __global__ void __launch_bounds__(64 * kPfWaves, 2) prefill_kernel(PfArgs a) {
     // epilogue: lane (jt, q) holds rows 16 r + 4 q + i (i = 0..3) of the wavefront's 64 rows for tokens 16 t + jt
     const int rbase = rg * 64;
     if constexpr (MODE == 0) {
-        float *gbuf = (float *)xs;                           // [64 rows][kPfTm] gate accumulators of one pair
+        float *gbuf = (float *)xs;                           // [64 rows][kPfGPitch] gate accumulators of one pair
         for (int pair = 0; pair < 2; ++pair) {
             __syncthreads();
             if (wave == 2 * pair) {
 #pragma unroll
                 for (int r = 0; r < kPfRtw; ++r)
 #pragma unroll
-                    for (int t = 0; t < kPfTT; ++t)
+                    for (int t = 0; t < NTT; ++t)
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) gbuf[(16 * r + 4 * q + i) * kPfTm + 16 * t + jt] = acc[r][t][i];
+                        for (int i = 0; i < 4; ++i) gbuf[(16 * r + 4 * q + i) * kPfGPitch + 16 * t + jt] = acc[r][t][i];
             }
             __syncthreads();
             if (wave == 2 * pair + 1) {
 #pragma unroll
-                for (int t = 0; t < kPfTT; ++t) {
+                for (int t = 0; t < NTT; ++t) {
                     const int tok = 16 * t + jt;
                     if (tok < n) {
 #pragma unroll
@@ -393,7 +411,7 @@ __global__ void __launch_bounds__(64 * kPfWaves, 2) prefill_kernel(PfArgs a) {
                             float hv[4];
 #pragma unroll
                             for (int i = 0; i < 4; ++i)
-                                hv[i] = swiglu_clamped(gbuf[(16 * r + 4 * q + i) * kPfTm + tok], acc[r][t][i],
+                                hv[i] = swiglu_clamped(gbuf[(16 * r + 4 * q + i) * kPfGPitch + tok], acc[r][t][i],
                                                        a.limit);
                             uint2 v;
                             v.x = f32_to_bf16_rne(hv[0]) | (f32_to_bf16_rne(hv[1]) << 16);
@@ -406,7 +424,7 @@ __global__ void __launch_bounds__(64 * kPfWaves, 2) prefill_kernel(PfArgs a) {
         }
     } else {
 #pragma unroll
-        for (int t = 0; t < kPfTT; ++t) {
+        for (int t = 0; t < NTT; ++t) {
             const int tok = 16 * t + jt;
             if (tok < n) {
 #pragma unroll
@@ -418,6 +436,25 @@ __global__ void __launch_bounds__(64 * kPfWaves, 2) prefill_kernel(PfArgs a) {
                 }
             }
         }
+    }
+}
+
+template <int MODE>   // 0: gate/up -> h, 1: down -> y
+__global__ void __launch_bounds__(64 * kPfWaves, 2) prefill_kernel(PfArgs a) {
+    __shared__ PfShared sh;
+    // workgroups are dispatched to the XCDs round-robin: all workgroups of one block go to the same XCD (block
+    // g on XCD g % 8), so the block's activation rows are fetched into one L2 and read there by every workgroup
+    const int xcd = blockIdx.x % kXcds, li = blockIdx.x / kXcds;
+    const int g = (li / a.RBG) * kXcds + xcd, rbg = li % a.RBG;
+    if (g >= *a.n_blocks) return;
+    const int e = __builtin_amdgcn_readfirstlane(a.blk_expert[g]);
+    const int n = __builtin_amdgcn_readfirstlane(a.blk_n[g]);
+    switch ((n + 15) >> 4) {
+        case 1: prefill_body<MODE, 1>(a, sh, g, rbg, e, n); break;
+        case 2: prefill_body<MODE, 2>(a, sh, g, rbg, e, n); break;
+        case 3: prefill_body<MODE, 3>(a, sh, g, rbg, e, n); break;
+        case 4: prefill_body<MODE, 4>(a, sh, g, rbg, e, n); break;
+        default: prefill_body<MODE, kPfTT>(a, sh, g, rbg, e, n); break;
     }
 }
 
@@ -596,7 +633,8 @@ int mi_moe_prefill(const mi_table *gate, const mi_table *up, const mi_table *dow
     a.limit = limit;
     a.wg_rows = 2;
     a.RBG = I / 128;
-    hipLaunchKernelGGL(prefill_kernel<0>, dim3(L.G * a.RBG), dim3(64 * kPfWaves), 0, s, a);
+    const int g8 = (L.G + kXcds - 1) / kXcds * kXcds;       // blocks rounded up to whole XCD rounds
+    hipLaunchKernelGGL(prefill_kernel<0>, dim3(g8 * a.RBG), dim3(64 * kPfWaves), 0, s, a);
     if (hipGetLastError() != hipSuccess) return MI_ERR_LAUNCH;
 
     PfArgs b = a;
@@ -609,7 +647,7 @@ int mi_moe_prefill(const mi_table *gate, const mi_table *up, const mi_table *dow
     b.out = y;
     b.wg_rows = 4;
     b.RBG = D / 256;
-    hipLaunchKernelGGL(prefill_kernel<1>, dim3(L.G * b.RBG), dim3(64 * kPfWaves), 0, s, b);
+    hipLaunchKernelGGL(prefill_kernel<1>, dim3(g8 * b.RBG), dim3(64 * kPfWaves), 0, s, b);
     if (hipGetLastError() != hipSuccess) return MI_ERR_LAUNCH;
 
     const long long nthr = (long long)T * (D / 4);
