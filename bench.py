@@ -54,25 +54,6 @@ def cb3_bytes(R, K):
     return R * (4 * math.ceil(K / 10) + 16 * (K // 128))
 
 
-def random_cb3_planes(torch, gen, E, R, K):
-    """Device planes of E random CB3 experts (uniform codes, sorted N(0, 0.02) bf16 centroids) in the kernel layout:
-    qs int32 [E, CT*RT*256] tile words (every bit pattern is a valid set of codes; the padding columns of the last
-    tile multiply zero activations), cb int32 [E, G*R*4]."""
-    CT, G = math.ceil(K / 160), K // 128
-    qs = torch.randint(-2 ** 31, 2 ** 31 - 1, (E, CT * (R // 16) * 256), dtype=torch.int32, device="cuda",
-                       generator=gen)
-    cbs = []
-    sh = torch.tensor([0, 8, 16, 24], device="cuda", dtype=torch.int32)
-    pack = lambda a: (a << sh).sum(-1).to(torch.int32)
-    for e in range(E):
-        c = torch.randn((G, R, 8), device="cuda", generator=gen) * 0.02
-        c = torch.sort(c, dim=-1).values.to(torch.bfloat16).view(torch.int16).to(torch.int32) & 0xFFFF
-        lo, hi = c & 0xFF, c >> 8
-        w = torch.stack([pack(lo[..., 0:4]), pack(lo[..., 4:8]), pack(hi[..., 0:4]), pack(hi[..., 4:8])], -1)
-        cbs.append(w.reshape(1, G * R * 4))                         # [G, R, 4]
-    return {"qs": qs, "cb": torch.cat(cbs, 0).contiguous()}
-
-
 def softmax_topk(rng, N, E, k):
     logits = rng.standard_normal((N, E))
     p = np.exp(logits - logits.max(-1, keepdims=True))
@@ -196,15 +177,16 @@ def main():
     for c in range(L):
         tabs = {}
         for name, (R, K) in (("gate", (INTER, D)), ("up", (INTER, D)), ("down", (D, INTER))):
-            tabs[name] = pkg.ExpertTable("CB3", random_cb3_planes(torch, gen, E, R, K), R, K)
+            tabs[name] = pkg.random_cb3_table(E, R, K, gen)
         layers.append(tabs)
     torch.cuda.synchronize()
 
     rng = np.random.default_rng(2026)
     extra = {}
 
-    def layer_fns(N, routing, phases=3):
-        """Per-copy step callables for batch N (fixed routing per copy, fresh per copy)."""
+    def layer_fns(N, routing, phases=3, fused=False):
+        """Per-copy step callables for batch N (fixed routing per copy, fresh per copy): mi_moe_decode, or the
+        one-launch form mi_moe_decode_fused."""
         fns, nbytes = [], []
         ws = torch.zeros(pkg.resident.decode_workspace_bytes(layers[0]["gate"], layers[0]["down"], N, TOPK, SHARED),
                          dtype=torch.uint8, device="cuda")
@@ -216,14 +198,14 @@ def main():
             t = layers[c]
             f = (lambda t=t, x=x, it=it, wt=wt: pkg.moe_decode(t["gate"], t["up"], t["down"], x, it, wt, LIMIT,
                                                               shared_expert=SHARED, want_f32=False, out_bf16=out,
-                                                              workspace=ws, phases=phases))
+                                                              workspace=ws, phases=phases, fused=fused))
             fns.append(f)
             n_exp = len(np.unique(idx)) + 1
             nbytes.append(n_exp * (per_expert if phases == 3 else 2 * cb3_bytes(INTER, D)))
         return fns, nbytes
 
-    def measure(N, routing, phases=3, steps=args.steps):
-        fns, nbytes = layer_fns(N, routing, phases)
+    def measure(N, routing, phases=3, steps=args.steps, fused=False):
+        fns, nbytes = layer_fns(N, routing, phases, fused)
         ms = Timer(torch, fns).run(steps, args.warmup)
         avg_bytes = float(np.mean([nbytes[i % L] for i in range(steps)]))
         return ms, avg_bytes
@@ -231,15 +213,18 @@ def main():
     if args.only_prefill:
         print(json.dumps({"prefill_t512": bench_prefill(torch, pkg, gen, args, layers, rng)}))
         return
-    # headline: batch 1 layer
+    # headline: batch 1 layer (mi_moe_decode)
     ms1, bytes1 = measure(1, softmax_topk)
     gbs1 = bytes1 / (ms1 * 1e-3) / 1e9
-    # dominant kernel alone (gate + up + SwiGLU launch)
-    msg, bytesg = measure(1, softmax_topk, phases=1)
-    gbsg = bytesg / (msg * 1e-3) / 1e9
     extra["b1"] = {"us_per_layer": round(ms1 * 1e3, 2), "GBps": round(gbs1, 1), "pct_hbm": round(100 * gbs1 / HBM_PEAK_GBS, 1),
                    "bytes_per_layer": int(bytes1)}
+    # dominant kernel alone (the gate/up launch: gate and up partials)
+    msg, bytesg = measure(1, softmax_topk, phases=1)
+    gbsg = bytesg / (msg * 1e-3) / 1e9
     extra["b1_gateup_kernel"] = {"us": round(msg * 1e3, 2), "GBps": round(gbsg, 1), "bytes": int(bytesg)}
+    # the same layer as one persistent launch (mi_moe_decode_fused), for comparison
+    msf, bytesf = measure(1, softmax_topk, fused=True)
+    extra["b1_one_launch"] = {"us_per_layer": round(msf * 1e3, 2), "GBps": round(bytesf / (msf * 1e-3) / 1e9, 1)}
     if not args.only_b1:
         for N in (8, 16):
             ms, b = measure(N, zipf_topk)
@@ -269,7 +254,7 @@ def main():
                    "layer_copies": L, "parallelism": "single-gpu"},
         "roofline": {"bound": "hbm", "achieved": round(gbsg, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbsg / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                     "kernel": "grouped_kernel<gate/up, CB3> (gate + up partials)",
+                     "kernel": "grouped_kernel<gate/up, CB3> (gate + up partials, batch 1)",
                      "bytes_per_launch": int(bytesg), "us_per_launch": round(msg * 1e3, 2)},
         "cpu_baseline": cpu,
         "extra": extra,
@@ -350,7 +335,7 @@ def bench_matvec(torch, pkg, gen, args):
     R, K = 1024, 2048
     fns = []
     for c in range(4):
-        tb = pkg.ExpertTable("CB3", random_cb3_planes(torch, gen, 1, R, K), R, K)
+        tb = pkg.random_cb3_table(1, R, K, gen)
         x = torch.randn((1, K), device="cuda", generator=gen).to(torch.bfloat16)
         idx = torch.zeros((1,), dtype=torch.int32, device="cuda")
         out = torch.empty((1, R), dtype=torch.float32, device="cuda")

@@ -84,8 +84,9 @@ size_t mi_matvec_workspace(const mi_table *t, int32_t n_slots);
  * (resident.py:114-120).  out_f32 [N, D] and/or out_bf16 [N, D] (either may be NULL, not both).
  * shared_expert: an expert index of the same tables applied to every token with weight 1, or -1.
  * Limits: N <= 16, N*k <= MI_MAX_SLOTS, E <= 1024.  Deterministic (fixed-order reductions, no float atomics).
- * Four launches on the stream: gate/up partials, SwiGLU, down partials, routing-weighted combine.  The workspace
- * (mi_moe_decode_workspace bytes) holds the partials and h; it needs no initialisation.
+ * Four launches on the stream: gate/up partials, SwiGLU, down partials, routing-weighted combine (as
+ * mi_moe_decode_phases with phases = 3).  The workspace (mi_moe_decode_workspace bytes) holds the partials and h;
+ * calls that share a workspace must be ordered on one stream.
  */
 int mi_moe_decode(const mi_table *gate, const mi_table *up, const mi_table *down, const uint16_t *x_bf16,
                   int32_t N, int32_t k, const int32_t *idx, const float *w, int32_t shared_expert, float limit,
@@ -94,14 +95,45 @@ size_t mi_moe_decode_workspace(const mi_table *gate, const mi_table *down, int32
                                int32_t shared_expert);
 
 /*
- * mi_moe_decode split in two (the reference runs gate/up and down as separate kernels too, resident.py:116-119):
- * phases = 1: the gate/up launch only (its partials stay in the workspace); 2: SwiGLU + down + combine only
- * (consumes what a previous phase-1 call left in the same workspace, same arguments); 3: both (= mi_moe_decode).
+ * mi_moe_decode as ONE persistent launch (CB3 tables, N <= 8): gate/up, SwiGLU, down and the combine run as ordered
+ * tasks that hand their results over through completion counters kept in the workspace; each workgroup streams its
+ * gate/up tasks and then its down tasks with the next task's weights in flight.  Same arguments, workspace size and
+ * results as mi_moe_decode (up to the f32 summation order of the column splits).  The workspace must be zero-filled
+ * before its first use with this entry point; every call leaves its counter block zero again.  MI_ERR_QTYPE for
+ * IQ3_S tables, MI_ERR_TOKENS for N > 8.
+ */
+int mi_moe_decode_fused(const mi_table *gate, const mi_table *up, const mi_table *down, const uint16_t *x_bf16,
+                        int32_t N, int32_t k, const int32_t *idx, const float *w, int32_t shared_expert, float limit,
+                        float *out_f32, uint16_t *out_bf16, void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * mi_moe_decode as separate launches (the reference runs gate/up and down as separate kernels too,
+ * resident.py:116-119), any qtype: phases = 1: the gate/up launch only (its partials stay in the workspace);
+ * 2: SwiGLU + down + combine only (consumes what a previous phase-1 call left in the same workspace, same arguments);
+ * 3: both -- four launches: gate/up partials, SwiGLU, down partials, routing-weighted combine.  CB3 with N > 8: the
+ * gate/up and down launches are persistent (resident workgroups working through contiguous task ranges with the next
+ * task's weights in flight); otherwise one workgroup per (expert group, row range, column split).  It never touches
+ * the counter block of mi_moe_decode_fused.
  */
 int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_table *down, const uint16_t *x_bf16,
                          int32_t N, int32_t k, const int32_t *idx, const float *w, int32_t shared_expert,
                          float limit, float *out_f32, uint16_t *out_bf16, void *workspace, size_t workspace_bytes,
                          int32_t phases, void *stream);
+
+/*
+ * The launch plans of mi_moe_decode_fused and mi_moe_decode (no launch; for tests and tuning).  info[0..n_info):
+ *   [0] 1 if mi_moe_decode_fused applies; [1] its workgroups; [2] 0 (reserved);
+ *   [3..6] gate/up column splits, split alignment (column tiles), row tiles per wavefront, row ranges;
+ *   [7..10] the same for down; [11] dynamic LDS bytes; [12] groups bound; [13] token class (entries 1-13: the one
+ *   launch);
+ *   [14] u32 index of the error word in the workspace (nonzero after a call whose wait gave up: results invalid);
+ *   [15] bytes of the counter block at the start of the workspace (zero between calls);
+ *   [16..23] mi_moe_decode's launches: gate/up splits, row tiles per wavefront, workgroups (0: one per task), down
+ *   splits, row tiles per wavefront, workgroups (0: one per task), gate/up and down dynamic LDS bytes (persistent).
+ * Returns MI_OK or MI_ERR_ARG.
+ */
+int mi_moe_decode_plan(const mi_table *gate, const mi_table *down, int32_t N, int32_t k, int32_t shared_expert,
+                       int32_t *info, int32_t n_info);
 
 /*
  * The reference's prefill slot layout (ragged_plan, pallas_moe.py:564-592), built on the device:

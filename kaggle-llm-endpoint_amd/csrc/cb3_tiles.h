@@ -84,6 +84,27 @@ __device__ __forceinline__ uint4 bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, 
 }
 constexpr int kBufferWord3 = 0x00020000;   // gfx9 buffer descriptor word 3 (32-bit data format)
 
+// Staged activation rows: whole 64-dword chunks (the direct-to-LDS staging loads write 64 lanes x 4 bytes), plus a
+// 4-dword skew so the 16 rows of a B-operand read spread over the LDS banks.
+__host__ __device__ constexpr int cb3_row_pitch(int xs) { return ((xs + 63) & ~63) + 4; }
+// Byte offset past every staged source's range: a buffer load there returns zeros (columns outside the split).
+constexpr uint32_t kStageOut = 0x80000000u;
+
+// s_waitcnt vmcnt(N) (expcnt and lgkmcnt left alone): N vector memory operations may still be outstanding.
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// 16-byte store with the sc1 cache policy: written through this XCD's L2 to memory, so once the store has completed
+// (s_waitcnt vmcnt(0)) a workgroup on any XCD that has not cached the line reads the new value.
+constexpr int kCachePolicySc1 = 16;
+__device__ __forceinline__ void wt_store4(__amdgpu_buffer_rsrc_t r, uint32_t voff, f32x4 v) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, (int)voff, 0, kCachePolicySc1);
+}
+
 // Per-wavefront stream state.
 struct Cb3Wave {
     __amdgpu_buffer_rsrc_t qb, qnull;      // expert's code tiles (full range / empty range)
@@ -142,7 +163,7 @@ __device__ __forceinline__ void cb3_steps(const uint4 wv, const uint4 *cbrow, co
 
 // Column tile C of super tile st: publish the codebook groups first needed here (C = 0: groups 0, 1; else group
 // C + 1) and reload their register slots with the next super tile's groups; read the B operands; then per row
-// tile take the ring slot, refill it with column tile C of the next super tile and decode + MFMA the 5 k-steps.
+// tile decode + MFMA the ring slot's 5 k-steps and refill the slot with column tile C of the next super tile.
 template <bool TWO, int RTW, int C>
 __device__ __forceinline__ void cb3_ctile(const Cb3Wave &w, Cb3Regs<RTW> &s, int st) {
     const int lane = threadIdx.x & 63;
@@ -171,26 +192,29 @@ __device__ __forceinline__ void cb3_ctile(const Cb3Wave &w, Cb3Regs<RTW> &s, int
     const uint4 *cbrow = w.cbl + (lane & 15);
 #pragma unroll
     for (int r = 0; r < RTW; ++r) {
-        const uint4 wv = s.ring[C][r];
+        // decode the slot, then refill it: the load can reuse the slot's registers (refilling first would keep two
+        // copies of the ring live and cost a register copy per word every super tile)
+        cb3_steps<TWO, C, 0>(s.ring[C][r], cbrow, r, xb, xl, s.acc[r]);
         s.ring[C][r] = cb3_tile(w, ct + 4, r);
-        cb3_steps<TWO, C, 0>(wv, cbrow, r, xb, xl, s.acc[r]);
     }
 }
 
 // Streams column tiles [cta, ctb) of the wavefront's 16 RTW rows, as whole super tiles from the one holding cta: the
 // column tiles before cta decode zeros against zero activations (their loads touch no memory; they cost vector ALU
 // work only), which keeps the code ring and codebook slots at static positions.  The split's last super tile may end
-// early.  `stage` (ending in a workgroup barrier) runs after the first loads are issued.
+// early.  `stage` (ending in a workgroup barrier) runs after the first 4 RTW + 5 loads are issued.
 template <bool TWO, int RTW, class Stage>
 __device__ __forceinline__ void cb3_accum_mfma(const Cb3Wave &w, f32x4 (&acc)[RTW], Stage &&stage) {
     Cb3Regs<RTW> s;
     const int sta = w.cta >> 2;
+    // codebook groups first, then the code tiles in the order they are decoded: loads complete in issue order, so
+    // the first tile's decode waits for groups 0-1 and that tile only, not for the whole ring
+#pragma unroll
+    for (int c = 0; c < 5; ++c) s.cbv[c] = cb3_group(w, 5 * sta + c);
 #pragma unroll
     for (int c = 0; c < 4; ++c)
 #pragma unroll
         for (int r = 0; r < RTW; ++r) s.ring[c][r] = cb3_tile(w, 4 * sta + c, r);
-#pragma unroll
-    for (int c = 0; c < 5; ++c) s.cbv[c] = cb3_group(w, 5 * sta + c);
 #pragma unroll
     for (int r = 0; r < RTW; ++r) s.acc[r] = (f32x4){0.f, 0.f, 0.f, 0.f};
     stage();
@@ -211,6 +235,137 @@ __device__ __forceinline__ void cb3_accum_mfma(const Cb3Wave &w, f32x4 (&acc)[RT
     }
 #pragma unroll
     for (int r = 0; r < RTW; ++r) acc[r] = s.acc[r];
+}
+
+// ------------------------------------------------------------------------------------------------ staging
+// Stages activation rows r < t_rows of columns [c0, c1) (dword d of a row = columns c0 + 2d, c0 + 2d + 1) of one or
+// two bf16 planes into LDS (row pitch xsp dwords) with direct-to-LDS loads -- 64 lanes x 4 bytes per instruction, no
+// registers -- spread over the workgroup's wavefronts.  Row r reads plane row row_of(r) (negative: zeros); columns
+// outside [cv, cend) read zeros.  The loads complete in issue order with the wavefront's other loads, so a wait for
+// "all but the N loads issued since" (vm_wait<N>) followed by a workgroup barrier publishes the rows.
+template <bool HILO, class RowOf>
+__device__ __forceinline__ void dma_stage(uint32_t *xh, uint32_t *xl, int xsp, int t_rows, int c0, int cv, int c1,
+                                          int cend, const uint16_t *ph, const uint16_t *pl, int stride,
+                                          RowOf &&row_of, int wave, int lane) {
+    const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc((void *)ph, (short)0, 0x7fffffff, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t rl =
+        __builtin_amdgcn_make_buffer_rsrc((void *)(HILO ? pl : ph), (short)0, 0x7fffffff, kBufferWord3);
+    const int xs = (c1 - c0) >> 1, nch = (xs + 63) >> 6, per_row = (HILO ? 2 : 1) * nch;
+    for (int i = wave; i < t_rows * per_row; i += 4) {
+        const int t = i / per_row, r = i - t * per_row, plane = r / nch, ch = r - plane * nch;
+        const int row = row_of(t);
+        const int c = c0 + 2 * (64 * ch + lane);
+        const uint32_t voff =
+            (row >= 0 && c >= cv && c < cend) ? (uint32_t)((size_t)row * stride + c) * 2u : kStageOut;
+        uint32_t *dst = (plane ? xl : xh) + t * xsp + 64 * ch;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(plane ? rl : rh, (__attribute__((address_space(3))) void *)dst, 4,
+                                                 voff, 0, 0, 0);
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ continuous stream
+// A wavefront that works through a sequence of segments (each one (expert, row group, column split) of its own, as
+// cb3_accum_mfma handles one) keeps its code ring and codebook slots full across segment boundaries: during a
+// segment's last super tile the refills already fetch the first super tile of the next segment, so the next
+// segment's data is in flight while this one finishes and no wavefront waits for a fresh ring at a boundary.
+
+// Column tile C of super tile st of segment w: publish / reload the codebook slots and refill the ring from segment
+// `src` at its super tile src_st (w's next super tile, or the next segment's first); decode only if `dec` (the
+// column tiles of a last, partial super tile that lie past the segment are not decoded).
+template <bool TWO, int RTW, int C>
+__device__ __forceinline__ void cb3_ctile_src(const Cb3Wave &w, const Cb3Wave &src, int src_st, Cb3Regs<RTW> &s,
+                                              int st, bool dec) {
+    const int lane = threadIdx.x & 63;
+    const int gn = 5 * src_st;
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (C == 0) {
+        w.cbl[0 * 64 + lane] = s.cbv[0];
+        w.cbl[1 * 64 + lane] = s.cbv[1];
+        s.cbv[0] = cb3_group(src, gn);
+        s.cbv[1] = cb3_group(src, gn + 1);
+    } else {
+        w.cbl[(C + 1) * 64 + lane] = s.cbv[C + 1];
+        s.cbv[C + 1] = cb3_group(src, gn + C + 1);
+    }
+    const int ct = 4 * st + C, nct = 4 * src_st + C;
+    if (dec) {
+        const int xo = 80 * (ct - (w.cta & ~3));                // dwords
+        uint4 xb[5], xl[5];
+#pragma unroll
+        for (int m = 0; m < 5; ++m) {
+            xb[m] = *(const uint4 *)(w.xh + xo + 16 * m);
+            if (TWO) xl[m] = *(const uint4 *)(w.xl + xo + 16 * m);
+            else xl[m] = xb[m];
+        }
+        const uint4 *cbrow = w.cbl + (lane & 15);
+#pragma unroll
+        for (int r = 0; r < RTW; ++r) {
+            cb3_steps<TWO, C, 0>(s.ring[C][r], cbrow, r, xb, xl, s.acc[r]);
+            s.ring[C][r] = cb3_tile(src, nct, r);
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < RTW; ++r) s.ring[C][r] = cb3_tile(src, nct, r);
+    }
+}
+
+// Streams segment w and the ones `next` hands out.
+//   next(Cb3Wave &nw) -> bool   the wavefront's next segment (false: none); called at the start of a segment's last
+//                               super tile, so that segment's loads are issued while the current one finishes
+//   store(f32x4 (&acc)[RTW])    end of a segment: its accumulators (reset to zero afterwards)
+//   boundary(const Cb3Wave &nw) between two segments, after store (e.g. restaging activations: all wavefronts of the
+//                               workgroup reach it together if they handle one segment per task each)
+//   issue()                     once, before the first loads (e.g. direct-to-LDS staging loads, which then complete
+//                               ahead of the ring)
+//   stage()                     once, after the first 4 RTW + 5 loads are issued (ends in a workgroup barrier)
+template <bool TWO, int RTW, class Next, class Store, class Boundary, class Issue, class Stage>
+__device__ __forceinline__ void cb3_stream(Cb3Wave w, Next &&next, Store &&store, Boundary &&boundary, Issue &&issue,
+                                           Stage &&stage) {
+    Cb3Regs<RTW> s;
+    issue();
+    __builtin_amdgcn_sched_barrier(0);
+    {
+        const int sta = w.cta >> 2;
+#pragma unroll
+        for (int c = 0; c < 5; ++c) s.cbv[c] = cb3_group(w, 5 * sta + c);
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int r = 0; r < RTW; ++r) s.ring[c][r] = cb3_tile(w, 4 * sta + c, r);
+#pragma unroll
+        for (int r = 0; r < RTW; ++r) s.acc[r] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    stage();
+    for (;;) {
+        const int st_last = (w.ctb - 1) >> 2;       // the segment's last super tile (maybe partial)
+        int st = w.cta >> 2;
+        for (; st < st_last; ++st) {
+            cb3_ctile_src<TWO, RTW, 0>(w, w, st + 1, s, st, true);
+            cb3_ctile_src<TWO, RTW, 1>(w, w, st + 1, s, st, true);
+            cb3_ctile_src<TWO, RTW, 2>(w, w, st + 1, s, st, true);
+            cb3_ctile_src<TWO, RTW, 3>(w, w, st + 1, s, st, true);
+        }
+        Cb3Wave nw = w;
+        const bool more = next(nw);
+        if (!more) {                                // nothing follows: the refills touch no memory
+            nw.cta = nw.ctb = 0;
+            nw.g_first = 1;
+            nw.g_last = 0;
+        }
+        const int nst = nw.cta >> 2;
+        const int nct = w.ctb - 4 * st;             // 1..4 column tiles of the last super tile
+        cb3_ctile_src<TWO, RTW, 0>(w, nw, nst, s, st, true);
+        cb3_ctile_src<TWO, RTW, 1>(w, nw, nst, s, st, nct > 1);
+        cb3_ctile_src<TWO, RTW, 2>(w, nw, nst, s, st, nct > 2);
+        cb3_ctile_src<TWO, RTW, 3>(w, nw, nst, s, st, nct > 3);
+        store(s.acc);
+#pragma unroll
+        for (int r = 0; r < RTW; ++r) s.acc[r] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        if (!more) break;
+        boundary(nw);
+        w = nw;
+    }
 }
 
 }  // namespace mi

@@ -46,8 +46,10 @@ struct KArgs {
     int xs_max;                // LDS row pitch in dwords (largest over the splits)
     int t_rows;                // LDS rows staged (class of the largest group)
     // activations
-    const uint16_t *x_bf16;    // kGateUp: [N, K] tokens; kMatvec bf16: [n_slots, stride]
-    const float *x_f32;        // kDown: h [NS, stride] by slot; kMatvec f32: [n_slots, stride]
+    const uint16_t *x_bf16;    // kGateUp: [N, K] tokens; kDown: bf16 high part of h [NS, stride] by slot;
+                               // kMatvec bf16: [n_slots, stride]
+    const uint16_t *x_lo;      // kDown: bf16 remainder of h [NS, stride] (h = x_bf16 + x_lo to 16 mantissa bits)
+    const float *x_f32;        // kMatvec f32: [n_slots, stride] (split into bf16 high + remainder while staging)
     int x_stride;
     const int32_t *idx;
     // partial sums
@@ -94,7 +96,9 @@ __device__ __forceinline__ void iq3_run_and_store(const Iq3Table &tb, int e, int
 //     (jt >= 8), and the two accumulator columns are added at the end -- one instruction covers hi and lo;
 //   f32 activations, launches of up to 16 tokens per group: hi and lo of token jt, two instructions per k-step.
 // Columns jt >= the staged rows read a clamped row; their accumulator columns are never stored.
-template <bool HILO, int TCMAX, int RTW, class Stage>
+// WT: the partials are stored write-through (sc1), so a workgroup on another XCD can read them inside the same launch
+// once the storing workgroup has published a completion count.
+template <bool HILO, int TCMAX, int RTW, bool WT = false, class Stage>
 __device__ __forceinline__ void cb3_run_and_store(const Cb3Table &tb, int e, int rg, int u0, int u1, int c0,
                                                   const uint32_t *xh, const uint32_t *xl, int xsp, int t_rows, int n,
                                                   const int *slots, float *part_base, int R, uint4 *cbl,
@@ -133,11 +137,23 @@ __device__ __forceinline__ void cb3_run_and_store(const Cb3Table &tb, int e, int
             for (int i = 0; i < 4; ++i) acc[r][i] += __shfl_down(acc[r][i], 8, 16);
     }
     if (jt < n) {
-        float *dst = part_base + (size_t)slots[jt] * R + rg * 16 * RTW + 4 * q;
+        const size_t off = (size_t)slots[jt] * R + rg * 16 * RTW + 4 * q;
+        if constexpr (WT) {
+            const __amdgpu_buffer_rsrc_t pr =
+                __builtin_amdgcn_make_buffer_rsrc((void *)part_base, (short)0, 0x7fffffff, kBufferWord3);
 #pragma unroll
-        for (int r = 0; r < RTW; ++r) *(float4 *)(dst + 16 * r) = make_float4(acc[r][0], acc[r][1], acc[r][2], acc[r][3]);
+            for (int r = 0; r < RTW; ++r) wt_store4(pr, (uint32_t)(off + 16 * r) * 4u, acc[r]);
+        } else {
+            float *dst = part_base + off;
+#pragma unroll
+            for (int r = 0; r < RTW; ++r)
+                *(float4 *)(dst + 16 * r) = make_float4(acc[r][0], acc[r][1], acc[r][2], acc[r][3]);
+        }
     }
 }
+
+// Activation rows staged with direct-to-LDS loads by the grouped kernel: up to this many (token classes 1-4).
+constexpr int kDmaStageRows = 4;
 
 // Workgroups are 4 wavefronts sharing one staged activation slice: gate/up = (gate, up) x 2 row groups, down /
 // matvec = 4 row groups.  A row group is the rows of one wavefront: 64 (CB3) or 256 (IQ3_S).
@@ -147,9 +163,12 @@ constexpr int kWgWaves = 4;
 template <int QT, int RTW>
 __host__ __device__ constexpr int wave_rows() { return QT == MI_QT_CB3 ? 16 * RTW : kRowBlock; }
 
-// CB3 kernels are held to 3 wavefronts per SIMD (<= 168 VGPRs): more HBM requests in flight per CU.
+// CB3 kernels are held to MI_CB3_WAVES wavefronts per SIMD (3: <= 168 VGPRs): more HBM requests in flight per CU.
+#ifndef MI_CB3_WAVES
+#define MI_CB3_WAVES 3
+#endif
 template <int QT>
-__host__ __device__ constexpr int min_waves_per_simd() { return QT == MI_QT_CB3 ? 3 : 1; }
+__host__ __device__ constexpr int min_waves_per_simd() { return QT == MI_QT_CB3 ? MI_CB3_WAVES : 1; }
 
 template <int MODE, int QT, int TCMAX, int RTW>
 __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) grouped_kernel(KArgs a) {
@@ -186,7 +205,7 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
     const int cv = u0 * ucols;                // first column of the split
     const int c1 = cb3 ? u1 * ucols : min(a.K, u1 * ucols);
     const int xs = (c1 - c0) >> 1;            // dwords per staged row
-    const int xsp = cb3 ? xs + 4 : xs;        // row pitch (CB3: skewed so 16 rows spread over the LDS banks)
+    const int xsp = cb3 ? cb3_row_pitch(xs) : xs;   // row pitch (CB3: whole 64-dword chunks, skewed)
     const bool hilo = (MODE == kDown) || (MODE == kMatvec && a.x_f32 != nullptr);
     uint32_t *xh = xlds;
     uint32_t *xl = xlds + (size_t)a.t_rows * a.xs_max;
@@ -194,7 +213,44 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
     // activation rows t < t_rows (rows >= n are zero) of the split's columns, as bf16 pairs (hi/lo for f32)
     if (tid < kMaxT) s_tok[tid] = tid < n ? sc.g.slot[tid] : -1;
     __syncthreads();
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    // CB3 with bf16 sources (x, or h as its bf16 high part and remainder): the rows go straight from memory to LDS
+    // (buffer_load ... lds), issued BEFORE the first weight loads.  A wavefront's loads complete in issue order, so
+    // the staging then waits only for these loads, not for the weight ring behind them, and each tile's matrix-core
+    // work starts as soon as that tile arrives.
+    // (with many staged rows the 4-byte loads outnumber the register path's 8-byte ones: register staging there)
+    const bool dma = cb3 && (MODE != kMatvec || a.x_f32 == nullptr) && a.t_rows <= kDmaStageRows;
+    bool stage_ring = true;     // the wavefront issues its weight ring before staging (false: it only stages)
+    if (dma) {
+        const __amdgpu_buffer_rsrc_t rh =
+            __builtin_amdgcn_make_buffer_rsrc((void *)a.x_bf16, (short)0, 0x7fffffff, kBufferWord3);
+        const __amdgpu_buffer_rsrc_t rl =
+            __builtin_amdgcn_make_buffer_rsrc((void *)(hilo ? a.x_lo : a.x_bf16), (short)0, 0x7fffffff, kBufferWord3);
+        const int cend = min(c1, a.K);
+        const int nch = (xs + 63) >> 6, per_row = (hilo ? 2 : 1) * nch;
+        for (int i = wave; i < a.t_rows * per_row; i += kWgWaves) {
+            const int t = i / per_row, r = i - t * per_row, plane = r / nch, ch = r - plane * nch;
+            const int slot = s_tok[t];
+            const int c = c0 + 2 * (64 * ch + lane);
+            const int row = (MODE == kGateUp) ? slot_token(slot, a.n_route, a.k) : slot;
+            const uint32_t voff = (slot >= 0 && c >= cv && c < cend) ? (uint32_t)((size_t)row * a.x_stride + c) * 2u
+                                                                     : kStageOut;
+            uint32_t *dst = (plane ? xl : xh) + t * xsp + 64 * ch;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(plane ? rl : rh, (__attribute__((address_space(3))) void *)dst,
+                                                     4, voff, 0, 0, 0);
+        }
+        // the weight loads must not be scheduled ahead of the staging loads (the staging wait counts them)
+        __builtin_amdgcn_sched_barrier(0);
+    }
     auto stage = [&]() {
+        if (dma) {
+            // every load this wavefront issued before the weight ring has completed; then all wavefronts' rows
+            __builtin_amdgcn_sched_barrier(0);
+            if (stage_ring) vm_wait<4 * RTW + 5>();
+            else vm_wait<0>();
+            __syncthreads();
+            return;
+        }
         const int q4 = xs >> 1;           // 4-column quads per row
         for (int i = tid; i < a.t_rows * q4; i += blockDim.x) {
             const int t = i / q4, q = i - t * q4;
@@ -205,6 +261,9 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
                 if (!hilo) {
                     const int row = (MODE == kGateUp) ? slot_token(slot, a.n_route, a.k) : slot;
                     hv = *(const uint2 *)(a.x_bf16 + (size_t)row * a.x_stride + c);
+                } else if (a.x_f32 == nullptr) {
+                    hv = *(const uint2 *)(a.x_bf16 + (size_t)slot * a.x_stride + c);
+                    lv = *(const uint2 *)(a.x_lo + (size_t)slot * a.x_stride + c);
                 } else {
                     const float4 f = *(const float4 *)(a.x_f32 + (size_t)slot * a.x_stride + c);
                     uint32_t h0, l0, h1, l1, h2, l2, h3, l3;
@@ -222,11 +281,11 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
         __syncthreads();
     };
 
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int mat = MODE == kGateUp ? (wave & 1) : 0;          // gate/up: odd wavefronts run the up matrix
     const Table &tb = mat ? a.t1 : a.t0;
     const int rg = rbg * a.RBW + (MODE == kGateUp ? (wave >> 1) : wave);
     if (rg >= a.RB) {           // wavefront past the last row group: it only helps stage
+        stage_ring = false;
         stage();
         return;
     }

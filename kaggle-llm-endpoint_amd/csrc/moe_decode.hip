@@ -1,6 +1,6 @@
 // Grouped codebook-dequant expert matvec: host side of the C ABI (argument validation, split planning, workspace
 // layout, launches) and the exact dequant kernel.  The grouped kernels themselves live in grouped.h.
-#include "grouped.h"
+#include "pstream.h"
 
 #include <stdio.h>
 #include <stdlib.h>
@@ -130,9 +130,11 @@ __global__ void __launch_bounds__(64) combine_kernel(const float *__restrict__ p
 }
 
 // h = silu(min(g, L)) * clip(u, -L, L) (model.py:119-122) of the gate/up split partials, splits summed in order:
-// h[slot][c] from p1[s][0 = gate | 1 = up][slot][c].  One thread per 4 columns of one slot.
+// h[slot][c] from p1[s][0 = gate | 1 = up][slot][c].  h is stored as its bf16 high part (truncated) and the bf16
+// remainder (hi + lo keeps 16 mantissa bits of the f32 h), the two bf16 operands the down projection multiplies.
+// One thread per 4 columns of one slot.
 __global__ void __launch_bounds__(64) swiglu_kernel(const float *__restrict__ p1, int S1, int NS, int I, float limit,
-                                                    float *__restrict__ h) {
+                                                    uint16_t *__restrict__ h_hi, uint16_t *__restrict__ h_lo) {
     const size_t n4 = (size_t)NS * I / 4;
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n4) return;
@@ -144,8 +146,13 @@ __global__ void __launch_bounds__(64) swiglu_kernel(const float *__restrict__ p1
         g.x += pg.x; g.y += pg.y; g.z += pg.z; g.w += pg.w;
         u.x += pu.x; u.y += pu.y; u.z += pu.z; u.w += pu.w;
     }
-    ((float4 *)h)[i] = make_float4(swiglu_clamped(g.x, u.x, limit), swiglu_clamped(g.y, u.y, limit),
-                                   swiglu_clamped(g.z, u.z, limit), swiglu_clamped(g.w, u.w, limit));
+    const float hv[4] = {swiglu_clamped(g.x, u.x, limit), swiglu_clamped(g.y, u.y, limit),
+                         swiglu_clamped(g.z, u.z, limit), swiglu_clamped(g.w, u.w, limit)};
+    uint32_t hi[4], lo[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) split_bf16(hv[j], hi[j], lo[j]);
+    ((uint2 *)h_hi)[i] = make_uint2(hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16));
+    ((uint2 *)h_lo)[i] = make_uint2(lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16));
 }
 
 // Split reduction of a matvec: out[slot] = sum_s part[s][slot], splits in order.
@@ -245,7 +252,7 @@ static void split_extent(const mi_table *t, int S, int align, int *xs_max, int *
         split_bounds(nu, S, align, s, &u0, &u1);
         const int ua = cb3 ? 4 * (u0 / 4) : u0;
         const int c1 = u1 * uc < cend ? u1 * uc : cend;
-        const int xs = (c1 - ua * uc) / 2 + (cb3 ? 4 : 0);
+        const int xs = cb3 ? cb3_row_pitch((c1 - ua * uc) / 2) : (c1 - ua * uc) / 2;
         if (xs > bx) bx = xs;
         if (u1 - ua > bu) bu = u1 - ua;
     }
@@ -313,19 +320,21 @@ struct Shape {
 // as a wavefront's stream: the column units it streams (CB3: from the start of its first super tile) times the
 // kilobytes per unit (rtw for CB3), plus a fixed cost (first loads, staging, partial stores).  Minimise that over
 // S, the boundary alignment (CB3: column tiles or whole super tiles) and rtw, with a split's LDS staging within
-// 48 KB.  Environment overrides (experiments): <env>=S, <env>_RTW=rtw.
+// 48 KB.  Environment overrides (experiments): <env>=S, <env>_AL=alignment (default 1), <env>_RTW=rtw.
 static Shape choose_shape(const mi_table *t, int mode, int tcmax, int groups, int rows_lds, int bytes_per_col,
-                          const char *env) {
+                          const char *env, size_t lds_cap = 48 * 1024, long long fixed_slots = 0, int max_rtw = 4,
+                          double fixed = 8.0, int min_rtw = 1) {
     const int nu = n_units_of(t);
     const bool cb3 = t->qtype == MI_QT_CB3;
     const int rg_per_wg = mode == kGateUp ? 2 : kWgWaves;
-    const double fixed = 8.0;          // per-task cost in kilobyte-units
-    char env_rtw[64];
+    // fixed: per-task cost in kilobyte-units (start, routing, staging, stores; small when tasks are pipelined)
+    char env_rtw[64], env_al[64];
     snprintf(env_rtw, sizeof env_rtw, "%s_RTW", env);
-    const int forced_rtw = env_int(env_rtw, 0), forced_s = env_int(env, 0);
-    Shape best{{1, 1}, cb3 ? 4 : 1, 0, 0};
+    snprintf(env_al, sizeof env_al, "%s_AL", env);
+    const int forced_rtw = env_int(env_rtw, 0), forced_s = env_int(env, 0), forced_al = env_int(env_al, 1);
+    Shape best{{1, 1}, cb3 ? max_rtw : 1, 0, 0};
     double best_cost = 1e30;
-    for (int rtw = cb3 ? 4 : 1; rtw >= 1; rtw /= 2) {
+    for (int rtw = cb3 ? max_rtw : 1; rtw >= (cb3 ? min_rtw : 1); rtw /= 2) {
         if (forced_rtw > 0 && cb3 && rtw != forced_rtw) continue;
         const int RB = t->rows / wave_rows_of(t, rtw);
         const int RBG = (RB + rg_per_wg - 1) / rg_per_wg;
@@ -335,12 +344,13 @@ static Shape choose_shape(const mi_table *t, int mode, int tcmax, int groups, in
             const int align = aligns[ai];
             const int nb = (nu + align - 1) / align;
             for (int s = 1; s <= nb; ++s) {
-                if (forced_s > 0 && (s != (forced_s < nu ? forced_s : nu) || align != 1)) continue;
+                if (forced_s > 0 && (s != (forced_s < nb ? forced_s : nb) || align != forced_al)) continue;
                 int xs, units;
                 split_extent(t, s, align, &xs, &units);
                 const size_t lds = (size_t)xs * bytes_per_col * rows_lds;
-                if (lds > 48 * 1024) continue;
-                const long long slots = (long long)wgs_per_cu(mode, t->qtype, tcmax, rtw, lds) * cu_count();
+                if (lds > lds_cap) continue;
+                const long long slots =
+                    fixed_slots > 0 ? fixed_slots : (long long)wgs_per_cu(mode, t->qtype, tcmax, rtw, lds) * cu_count();
                 const long long tot = (long long)groups * RBG * s;
                 const long long rounds = (tot + slots - 1) / slots;
                 const double cost = (double)rounds * (units * kb_per_unit + fixed);
@@ -360,13 +370,52 @@ static Shape choose_shape(const mi_table *t, int mode, int tcmax, int groups, in
     return best;
 }
 
+#define MI_DECL_PSTREAM(M, T)                                                                    \
+    int occupancy_pstream_##M##_##T(int rtw, size_t lds);                                        \
+    void launch_pstream_##M##_##T(int rtw, dim3 grid, size_t lds, hipStream_t s, const PArgs &a);
+MI_DECL_PSTREAM(0, 8)
+MI_DECL_PSTREAM(0, 16)
+MI_DECL_PSTREAM(1, 8)
+MI_DECL_PSTREAM(1, 16)
+#undef MI_DECL_PSTREAM
+
+static int pstream_occupancy(int mode, int tc, int rtw, size_t lds) {
+    if (mode == kGateUp) return (tc <= 8 ? occupancy_pstream_0_8 : occupancy_pstream_0_16)(rtw, lds);
+    return (tc <= 8 ? occupancy_pstream_1_8 : occupancy_pstream_1_16)(rtw, lds);
+}
+static void pstream_launch(int mode, int tc, int rtw, dim3 grid, size_t lds, hipStream_t s, const PArgs &a) {
+    if (mode == kGateUp) (tc <= 8 ? launch_pstream_0_8 : launch_pstream_0_16)(rtw, grid, lds, s, a);
+    else (tc <= 8 ? launch_pstream_1_8 : launch_pstream_1_16)(rtw, grid, lds, s, a);
+}
+
+// Token counts above which the CB3 gate/up and down launches are persistent (below, a workgroup would get about one
+// task: the one-workgroup-per-task launches start their first tiles sooner).  Measured on MI355X at the benchmark
+// layer: batch 1 and 8 run faster as one workgroup per task, batch 16 as persistent ranges.
+constexpr int kPersistentMinTokens = 8;
+
 struct DecodePlan {
     int G, rows1, rows2, NS;
+    int persistent;             // CB3 gate/up and down as persistent launches
     Shape s1, s2;
+    int P1, P2;                 // persistent: workgroups of the two launches
+    size_t lds1, lds2;          // CB3: their dynamic LDS
     size_t off_part1, off_h, off_part2, total;
 };
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// A persistent CB3 launch: the grid is what stays resident (the runtime's occupancy for the instance and its LDS),
+// never more workgroups than the largest possible task count.
+static void plan_pstream(int mode, int tc, const Shape &sh, int G, size_t staging, size_t scratch, int *P,
+                         size_t *lds) {
+    *lds = staging > scratch ? staging : scratch;
+    int occ = pstream_occupancy(mode, tc, sh.rtw, *lds);
+    if (occ <= 0) occ = 1;
+    long long p = (long long)occ * cu_count();
+    const long long tasks = (long long)G * sh.RBG * sh.sp.S;
+    if (p > tasks) p = tasks;
+    *P = (int)(p < 1 ? 1 : p);
+}
 
 static DecodePlan plan_decode(const mi_table *gate, const mi_table *down, int N, int k, int shared) {
     DecodePlan p{};
@@ -379,8 +428,22 @@ static DecodePlan plan_decode(const mi_table *gate, const mi_table *down, int N,
     p.NS = n_route + (shared >= 0 ? N : 0);
     int est = N == 1 ? p.G : (p.G * 6 + 5) / 10;
     if (est < 1) est = 1;
-    p.s1 = choose_shape(gate, kGateUp, p.rows1, est, p.rows1, 4, "MI355MOE_S1");
-    p.s2 = choose_shape(down, kDown, p.rows2, est, p.rows2, 8, "MI355MOE_S2");
+    p.persistent = gate->qtype == MI_QT_CB3 && N > kPersistentMinTokens;
+    if (p.persistent) {
+        // persistent launches: tasks are pipelined, so the per-task fixed cost is small
+        const long long slots = 3LL * cu_count();
+        p.s1 = choose_shape(gate, kGateUp, p.rows1, est, p.rows1, 4, "MI355MOE_S1", 48 * 1024, slots, 4, 2.0);
+        p.s2 = choose_shape(down, kDown, p.rows2, est, p.rows2, 8, "MI355MOE_S2", 48 * 1024, slots, 4, 2.0);
+        const int tc = p.rows1 <= 8 ? 8 : 16;
+        const size_t scratch = 4 * (2 * (size_t)gate->n_experts + (size_t)n_route);
+        plan_pstream(kGateUp, tc, p.s1, p.G, sizeof(uint32_t) * (size_t)p.rows1 * max_xs(gate, p.s1.sp), scratch,
+                     &p.P1, &p.lds1);
+        plan_pstream(kDown, tc, p.s2, p.G, sizeof(uint32_t) * 2 * (size_t)p.rows2 * max_xs(down, p.s2.sp), scratch,
+                     &p.P2, &p.lds2);
+    } else {
+        p.s1 = choose_shape(gate, kGateUp, p.rows1, est, p.rows1, 4, "MI355MOE_S1");
+        p.s2 = choose_shape(down, kDown, p.rows2, est, p.rows2, 8, "MI355MOE_S2");
+    }
     size_t off = 0;
     p.off_part1 = off;
     off = align256(off + sizeof(float) * (size_t)p.s1.sp.S * 2 * p.NS * gate->rows);
@@ -389,6 +452,84 @@ static DecodePlan plan_decode(const mi_table *gate, const mi_table *down, int N,
     p.off_part2 = off;
     off = align256(off + sizeof(float) * (size_t)p.s2.sp.S * p.NS * down->rows);
     p.total = off;
+    return p;
+}
+
+// ------------------------------------------------------------------------------------------------ fused decode
+// Counter block of the fused decode kernel at the start of the decode workspace (its size depends on the table shapes
+// only, so a workspace sized for any N keeps it in place): ticket lists, per-group h counters, per-row-range down
+// counters, the error word (each on its own 128-byte line), then the dense per-(group, row range) split counters.
+struct CtrLayout {
+    size_t hcnt, cnt2, err, cnt1, bytes;     // word offsets, total bytes
+};
+static CtrLayout ctr_layout(const mi_table *gate, const mi_table *down) {
+    CtrLayout c{};
+    const size_t rbg2_max = (size_t)(down->rows + 63) / 64, rbg1_max = (size_t)(gate->rows + 31) / 32;
+    c.hcnt = 0;
+    c.cnt2 = c.hcnt + (size_t)kMaxGroups * kCtrStride;
+    c.err = c.cnt2 + rbg2_max * kCtrStride;
+    c.cnt1 = c.err + kCtrStride;
+    c.bytes = align256(4 * (c.cnt1 + (size_t)kMaxGroups * rbg1_max));
+    return c;
+}
+
+int occupancy_fused(int rtw, size_t lds);
+void launch_fused(int rtw, dim3 grid, size_t lds, hipStream_t s, const FArgs &a);
+
+// Static LDS of the fused kernel besides the dynamic staging area (group table, codebook slots, slot list, flag).
+constexpr size_t kFusedStaticLds = sizeof(GroupTable) + sizeof(uint4) * kWgWaves * 5 * 64 + sizeof(int) * (kMaxT + 1);
+constexpr size_t kLdsPerCu = 160 * 1024;
+
+struct FusedPlan {
+    int ok;                     // the one launch applies (CB3, at most 8 tokens per group)
+    int rows, G, NS, P;
+    Shape s1, s2;
+    size_t lds;
+    int xs_max;
+    size_t off_part1, off_h, off_part2, total;   // data offsets after the counter block; total incl. the block
+};
+
+// Plan of the fused launch: both phases stream with the same rows per wavefront (32 or 64: the SwiGLU of a row
+// range then fills whole 128-byte lines of h's bf16 planes); the column splits come from the separate launches' cost
+// model with the slots of the persistent grid (3 workgroups per CU) and a small per-task cost (tasks are pipelined).
+// Environment overrides (experiments): MI355MOE_FS1[_AL|_RTW], MI355MOE_FS2[_AL] as for choose_shape.
+static FusedPlan plan_fused(const mi_table *gate, const mi_table *down, int N, int k, int shared) {
+    FusedPlan p{};
+    if (gate->qtype != MI_QT_CB3 || N > kFusedMaxTokens) return p;
+    const int n_route = N * k;
+    p.rows = class_rows(N);
+    p.G = max_groups(n_route, gate->n_experts, N, shared, p.rows);
+    p.NS = n_route + (shared >= 0 ? N : 0);
+    int est = N == 1 ? p.G : (p.G * 6 + 5) / 10;
+    if (est < 1) est = 1;
+    const long long slots = 3LL * cu_count();
+    const size_t cap = kLdsPerCu / 3 - kFusedStaticLds - 256;
+    p.s1 = choose_shape(gate, kGateUp, p.rows, est, p.rows, 8, "MI355MOE_FS1", cap, slots, 4, 2.0, 2);
+    const int rtw = p.s1.rtw;
+    p.s2 = choose_shape(down, kDown, p.rows, est, p.rows, 8, "MI355MOE_FS2", cap, slots, rtw, 2.0, rtw);
+    if (p.s1.RB == 0 || p.s2.RB == 0 || p.s2.rtw != rtw || rtw < 2) return p;
+    const int xs1 = max_xs(gate, p.s1.sp), xs2 = max_xs(down, p.s2.sp);
+    p.xs_max = xs1 > xs2 ? xs1 : xs2;
+    size_t lds = sizeof(uint32_t) * 2 * (size_t)p.rows * p.xs_max;
+    const size_t scratch = 4 * (2 * (size_t)gate->n_experts + (size_t)n_route);
+    if (scratch > lds) lds = scratch;
+    p.lds = lds;
+    int occ = occupancy_fused(rtw, lds);
+    if (occ <= 0) return p;
+    long long P = (long long)occ * cu_count();
+    const long long tasks = (long long)p.G * (p.s1.RBG * p.s1.sp.S + p.s2.RBG * p.s2.sp.S);
+    if (P > tasks) P = tasks;
+    p.P = (int)(P < 1 ? 1 : P);
+    const CtrLayout cl = ctr_layout(gate, down);
+    size_t off = cl.bytes;
+    p.off_part1 = off;
+    off = align256(off + sizeof(float) * (size_t)p.s1.sp.S * 2 * p.NS * gate->rows);
+    p.off_h = off;
+    off = align256(off + sizeof(uint16_t) * 2 * (size_t)p.NS * gate->rows);
+    p.off_part2 = off;
+    off = align256(off + sizeof(float) * (size_t)p.s2.sp.S * p.NS * down->rows);
+    p.total = off;
+    p.ok = 1;
     return p;
 }
 
@@ -427,7 +568,11 @@ extern "C" {
 size_t mi_moe_decode_workspace(const mi_table *gate, const mi_table *down, int32_t N, int32_t k,
                                int32_t shared_expert) {
     if (validate_table(gate) || validate_table(down) || N <= 0 || k <= 0) return 0;
-    return plan_decode(gate, down, N, k, shared_expert).total;
+    if (N > kMaxT || N * k > MI_MAX_SLOTS) return 0;
+    // counter block, then the larger of the two layouts (the fused launch's and the separate launches')
+    const size_t sep = ctr_layout(gate, down).bytes + plan_decode(gate, down, N, k, shared_expert).total;
+    const size_t fused = plan_fused(gate, down, N, k, shared_expert).total;
+    return sep > fused ? sep : fused;
 }
 
 int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_table *down, const uint16_t *x_bf16,
@@ -447,9 +592,10 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
     if (shared_expert >= gate->n_experts || shared_expert < -1) return MI_ERR_ARG;
     if (!(limit > 0.0f)) return MI_ERR_ARG;
     const DecodePlan p = plan_decode(gate, down, N, k, shared_expert);
-    if (!workspace || workspace_bytes < p.total) return MI_ERR_WORKSPACE;
+    const size_t ctr_bytes = ctr_layout(gate, down).bytes;
+    if (!workspace || workspace_bytes < ctr_bytes + p.total) return MI_ERR_WORKSPACE;
     hipStream_t s = (hipStream_t)stream;
-    char *ws = (char *)workspace;
+    char *ws = (char *)workspace + ctr_bytes;        // the fused launch's counters stay untouched
 
     KArgs a{};
     a.E = gate->n_experts;
@@ -478,19 +624,47 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
     a.x_stride = gate->cols;
     a.part = (float *)(ws + p.off_part1);
     size_t lds1 = sizeof(uint32_t) * (size_t)a.t_rows * a.xs_max;
+    const bool cb3 = p.persistent;
+    const int tc = a.t_rows <= 8 ? 8 : 16;
+    PArgs pa{};
+    if (cb3) {
+        pa.t0 = a.t0.cb3;
+        pa.t1 = a.t1.cb3;
+        pa.R = a.R;
+        pa.K = a.K;
+        pa.E = a.E;
+        pa.n_route = a.n_route;
+        pa.N = N;
+        pa.k = k;
+        pa.shared_expert = shared_expert;
+        pa.NS = p.NS;
+        pa.t_rows = a.t_rows;
+        pa.S = a.S;
+        pa.al = a.ualign;
+        pa.nu = a.n_units;
+        pa.RB = a.RB;
+        pa.RBG = a.RBG;
+        pa.xs_max = a.xs_max;
+        pa.P = p.P1;
+        pa.x = x_bf16;
+        pa.x_lo = nullptr;
+        pa.idx = idx;
+        pa.part = a.part;
+    }
     if (phases & 1) {
-        launch_grouped<kGateUp>(gate->qtype, a.t_rows, p.s1.rtw, dim3(p.G * p.s1.RBG * p.s1.sp.S), lds1, s, a);
+        if (cb3) pstream_launch(kGateUp, tc, p.s1.rtw, dim3(p.P1), p.lds1, s, pa);
+        else launch_grouped<kGateUp>(gate->qtype, a.t_rows, p.s1.rtw, dim3(p.G * p.s1.RBG * p.s1.sp.S), lds1, s, a);
         if ((st = launch_status())) return st;
     }
     if (!(phases & 2)) return MI_OK;
 
     // phase 2: h = SwiGLU(sum of the phase-1 partials) [NS, I]; down -> split partials [S2, NS, D]; the
     // routing-weighted combine (+ shared expert) -> out [N, D].  Stream order publishes each launch's results.
-    float *h = (float *)(ws + p.off_h);
+    uint16_t *h_hi = (uint16_t *)(ws + p.off_h), *h_lo = h_hi + (size_t)p.NS * gate->rows;
     {
         const size_t n4 = (size_t)p.NS * gate->rows / 4;
         hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n4 + 63) / 64)), dim3(64), 0, s,
-                           (const float *)(ws + p.off_part1), p.s1.sp.S, p.NS, gate->rows, limit, h);
+                           (const float *)(ws + p.off_part1), p.s1.sp.S, p.NS, gate->rows, limit, h_hi, h_lo);
         if ((st = launch_status())) return st;
     }
     KArgs b = a;
@@ -506,12 +680,32 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
     b.RBG = p.s2.RBG;
     b.xs_max = max_xs(down, p.s2.sp);
     b.t_rows = p.rows2;
-    b.x_bf16 = nullptr;
-    b.x_f32 = h;
+    b.x_bf16 = h_hi;
+    b.x_lo = h_lo;
+    b.x_f32 = nullptr;
     b.x_stride = gate->rows;
     b.part = (float *)(ws + p.off_part2);
     size_t lds2 = sizeof(uint32_t) * 2 * (size_t)b.t_rows * b.xs_max;
-    launch_grouped<kDown>(down->qtype, b.t_rows, p.s2.rtw, dim3(p.G * p.s2.RBG * p.s2.sp.S), lds2, s, b);
+    if (cb3) {
+        PArgs pb = pa;
+        pb.t0 = b.t0.cb3;
+        pb.t1 = b.t0.cb3;
+        pb.R = b.R;
+        pb.K = b.K;
+        pb.S = b.S;
+        pb.al = b.ualign;
+        pb.nu = b.n_units;
+        pb.RB = b.RB;
+        pb.RBG = b.RBG;
+        pb.xs_max = b.xs_max;
+        pb.P = p.P2;
+        pb.x = h_hi;
+        pb.x_lo = h_lo;
+        pb.part = b.part;
+        pstream_launch(kDown, tc, p.s2.rtw, dim3(p.P2), p.lds2, s, pb);
+    } else {
+        launch_grouped<kDown>(down->qtype, b.t_rows, p.s2.rtw, dim3(p.G * p.s2.RBG * p.s2.sp.S), lds2, s, b);
+    }
     if ((st = launch_status())) return st;
     const int D = down->rows, nthr = N * (D / 4);
     hipLaunchKernelGGL(combine_kernel, dim3((nthr + 63) / 64), dim3(64), 0, s, b.part, p.s2.sp.S, p.NS, D, N, k, idx, w,
@@ -524,6 +718,95 @@ int mi_moe_decode(const mi_table *gate, const mi_table *up, const mi_table *down
                   float *out_f32, uint16_t *out_bf16, void *workspace, size_t workspace_bytes, void *stream) {
     return mi_moe_decode_phases(gate, up, down, x_bf16, N, k, idx, w, shared_expert, limit, out_f32, out_bf16,
                                 workspace, workspace_bytes, 3, stream);
+}
+
+int mi_moe_decode_fused(const mi_table *gate, const mi_table *up, const mi_table *down, const uint16_t *x_bf16,
+                        int32_t N, int32_t k, const int32_t *idx, const float *w, int32_t shared_expert, float limit,
+                        float *out_f32, uint16_t *out_bf16, void *workspace, size_t workspace_bytes, void *stream) {
+    int st;
+    if ((st = validate_table(gate)) || (st = validate_table(up)) || (st = validate_table(down))) return st;
+    if (gate->qtype != MI_QT_CB3) return MI_ERR_QTYPE;
+    if (N <= 0 || N > kFusedMaxTokens || k <= 0 || N * k > MI_MAX_SLOTS) return MI_ERR_TOKENS;
+    if (shared_expert >= gate->n_experts || shared_expert < -1) return MI_ERR_ARG;
+    const FusedPlan p = plan_fused(gate, down, N, k, shared_expert);
+    if (!p.ok) return MI_ERR_SHAPE;
+    if (!x_bf16 || !idx || !w || (!out_f32 && !out_bf16)) return MI_ERR_NULL;
+    if (up->qtype != gate->qtype || up->rows != gate->rows || up->cols != gate->cols ||
+        up->n_experts != gate->n_experts)
+        return MI_ERR_MISMATCH;
+    if (down->qtype != gate->qtype || down->cols != gate->rows || down->n_experts != gate->n_experts)
+        return MI_ERR_MISMATCH;
+    if (shared_expert < -1) return MI_ERR_ARG;
+    if (!(limit > 0.0f)) return MI_ERR_ARG;
+    if (!workspace || workspace_bytes < p.total) return MI_ERR_WORKSPACE;
+    char *ws = (char *)workspace;
+    uint32_t *ctr = (uint32_t *)workspace;
+    const CtrLayout cl = ctr_layout(gate, down);
+    FArgs a{};
+    a.gate = make_table(gate).cb3;
+    a.up = make_table(up).cb3;
+    a.down = make_table(down).cb3;
+    a.D = gate->cols;
+    a.I = gate->rows;
+    a.E = gate->n_experts;
+    a.N = N;
+    a.k = k;
+    a.n_route = N * k;
+    a.shared_expert = shared_expert;
+    a.NS = p.NS;
+    a.t_rows = p.rows;
+    a.limit = limit;
+    a.x = x_bf16;
+    a.idx = idx;
+    a.w = w;
+    a.part1 = (float *)(ws + p.off_part1);
+    a.h_hi = (uint16_t *)(ws + p.off_h);
+    a.h_lo = a.h_hi + (size_t)p.NS * gate->rows;
+    a.part2 = (float *)(ws + p.off_part2);
+    a.out_f32 = out_f32;
+    a.out_bf16 = out_bf16;
+    a.hcnt = ctr + cl.hcnt;
+    a.cnt2 = ctr + cl.cnt2;
+    a.err = ctr + cl.err;
+    a.cnt1 = ctr + cl.cnt1;
+    a.S1 = p.s1.sp.S;
+    a.al1 = p.s1.sp.align;
+    a.nu1 = n_units_of(gate);
+    a.RB1 = p.s1.RB;
+    a.RBG1 = p.s1.RBG;
+    a.S2 = p.s2.sp.S;
+    a.al2 = p.s2.sp.align;
+    a.nu2 = n_units_of(down);
+    a.RB2 = p.s2.RB;
+    a.RBG2 = p.s2.RBG;
+    a.xs_max = p.xs_max;
+    a.P = p.P;
+    launch_fused(p.s1.rtw, dim3(p.P), p.lds, (hipStream_t)stream, a);
+    return launch_status();
+}
+
+int mi_moe_decode_plan(const mi_table *gate, const mi_table *down, int32_t N, int32_t k, int32_t shared_expert,
+                       int32_t *info, int32_t n_info) {
+    if (validate_table(gate) || validate_table(down) || !info || N <= 0 || N > kMaxT || k <= 0 ||
+        N * k > MI_MAX_SLOTS)
+        return MI_ERR_ARG;
+    int32_t v[24] = {0};
+    {
+        const DecodePlan d = plan_decode(gate, down, N, k, shared_expert);
+        const int32_t f[8] = {d.s1.sp.S, d.s1.rtw, d.persistent ? d.P1 : 0, d.s2.sp.S, d.s2.rtw,
+                              d.persistent ? d.P2 : 0, (int32_t)d.lds1, (int32_t)d.lds2};
+        for (int i = 0; i < 8; ++i) v[16 + i] = f[i];
+    }
+    const FusedPlan p = plan_fused(gate, down, N, k, shared_expert);
+    if (p.ok) {
+        const int32_t f[14] = {1, p.P, 0, p.s1.sp.S, p.s1.sp.align, p.s1.rtw, p.s1.RBG, p.s2.sp.S, p.s2.sp.align,
+                               p.s2.rtw, p.s2.RBG, (int32_t)p.lds, p.G, p.rows};
+        for (int i = 0; i < 14; ++i) v[i] = f[i];
+    }
+    v[14] = (int32_t)ctr_layout(gate, down).err;
+    v[15] = (int32_t)ctr_layout(gate, down).bytes;
+    for (int i = 0; i < n_info && i < 24; ++i) info[i] = v[i];
+    return MI_OK;
 }
 
 // Split count of mi_matvec: a function of (table, n_slots) only, so the workspace size is known beforehand.  The LDS

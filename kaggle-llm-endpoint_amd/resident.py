@@ -97,9 +97,29 @@ class ExpertTable:
         return sum(int(a.numel()) * 4 for a in self.planes.values()) // self.n_experts
 
 
+def random_cb3_table(E, R, K, generator, scale=0.02):
+    """An ExpertTable of E random CB3 experts generated on the GPU in the kernel layout: uniform random code tiles
+    (every bit pattern of a tile word is a valid set of codes; the zero-activation padding columns of the last tile
+    multiply whatever codes they hold) and, per (group, row), 8 sorted N(0, scale) bf16 centroids.  For benchmarks
+    and size-independent tests at full shape, where generating canonical codes on the host is too slow."""
+    CT, G = (K + 159) // 160, K // 128
+    qs = torch.randint(-2 ** 31, 2 ** 31 - 1, (E, CT * (R // 16) * 256), dtype=torch.int32, device="cuda",
+                       generator=generator)
+    sh = torch.tensor([0, 8, 16, 24], device="cuda", dtype=torch.int32)
+    pack = lambda a: (a << sh).sum(-1).to(torch.int32)
+    cbs = []
+    for _ in range(E):
+        c = torch.randn((G, R, 8), device="cuda", generator=generator) * scale
+        c = torch.sort(c, dim=-1).values.to(torch.bfloat16).view(torch.int16).to(torch.int32) & 0xFFFF
+        lo, hi = c & 0xFF, c >> 8
+        cbs.append(torch.stack([pack(lo[..., 0:4]), pack(lo[..., 4:8]), pack(hi[..., 0:4]), pack(hi[..., 4:8])],
+                               -1).reshape(1, G * R * 4))
+    return ExpertTable("CB3", {"qs": qs, "cb": torch.cat(cbs, 0).contiguous()}, R, K)
+
+
 class _Workspaces:
-    """Device workspaces, one per (device, stream, purpose); grown on demand.  No entry point needs its workspace
-    initialised; they are zero-filled when allocated only so that their contents are defined."""
+    """Device workspaces, one per (device, stream, purpose); grown on demand.  They are zero-filled when allocated:
+    the decode workspace's counter block must start at zero (each mi_moe_decode call leaves it zero again)."""
 
     def __init__(self):
         self._ws = {}
@@ -164,13 +184,25 @@ def decode_workspace_bytes(gate, down, N, k, shared_expert=-1):
     return n
 
 
+def decode_plan(gate, down, N, k, shared_expert=-1):
+    """The launch plan of mi_moe_decode (dict), without launching anything."""
+    info = (ctypes.c_int32 * 24)()
+    check("mi_moe_decode_plan", lib().mi_moe_decode_plan(gate.c, down.c, int(N), int(k), int(shared_expert), info, 24))
+    keys = ("fused", "workgroups", "lists", "S1", "align1", "rtw1", "rbg1", "S2", "align2", "rtw2", "rbg2", "lds",
+            "groups", "token_class", "err_word", "ctr_bytes", "sep_S1", "sep_rtw1", "sep_P1", "sep_S2", "sep_rtw2",
+            "sep_P2", "sep_lds1", "sep_lds2")
+    return {key: int(info[i]) for i, key in enumerate(keys)}
+
+
 def moe_decode(gate, up, down, x, idx, w, limit, shared_expert=-1, want_f32=True, want_bf16=False, out_f32=None,
-               out_bf16=None, workspace=None, phases=3):
+               out_bf16=None, workspace=None, phases=3, fused=False):
     """Fused decode MoE (resident.py:110-120 composition), tokens grouped by expert on the device.
     x bf16 [N, D]; idx int32 [N, k]; w f32 [N, k] -> (out_f32 [N, D] or None, out_bf16 [N, D] or None).
-    Preallocated ``out_f32`` / ``out_bf16`` / ``workspace`` (a uint8 device tensor of decode_workspace_bytes) make
-    the call allocation-free (graph capture).  ``phases``: 1 = the gate/up launch only, 2 = SwiGLU + down + combine
-    only (after a phase-1 call on the same workspace), 3 = all."""
+    Preallocated ``out_f32`` / ``out_bf16`` / ``workspace`` (a zero-filled uint8 device tensor of
+    decode_workspace_bytes, kept for later calls) make the call allocation-free (graph capture).  ``fused=True``
+    runs the layer as one persistent launch (mi_moe_decode_fused: CB3, N <= 8); ``phases`` 1 / 2 run part of the
+    separate launches (mi_moe_decode_phases): 1 = the gate/up launch only, 2 = SwiGLU + down + combine only (after a
+    phase-1 call on the same workspace), 3 = all (mi_moe_decode)."""
     if x.dtype != torch.bfloat16:
         raise ValueError("decode activations are bf16")
     N, k = idx.shape
@@ -190,9 +222,19 @@ def moe_decode(gate, up, down, x, idx, w, limit, shared_expert=-1, want_f32=True
     ws = workspace
     if ws is None:
         ws = WORKSPACES.get("decode", decode_workspace_bytes(gate, down, N, k, shared_expert))
-    check("mi_moe_decode", lib().mi_moe_decode_phases(gate.c, up.c, down.c, _ptr(x), N, k, _ptr(idx), _ptr(w),
-                                                      int(shared_expert), float(limit), _ptr(of), _ptr(ob),
-                                                      _ptr(ws), ws.numel(), int(phases), _stream()))
+    if fused:
+        check("mi_moe_decode_fused", lib().mi_moe_decode_fused(gate.c, up.c, down.c, _ptr(x), N, k, _ptr(idx),
+                                                               _ptr(w), int(shared_expert), float(limit), _ptr(of),
+                                                               _ptr(ob), _ptr(ws), ws.numel(), _stream()))
+    elif phases == 3:
+        check("mi_moe_decode", lib().mi_moe_decode(gate.c, up.c, down.c, _ptr(x), N, k, _ptr(idx), _ptr(w),
+                                                   int(shared_expert), float(limit), _ptr(of), _ptr(ob), _ptr(ws),
+                                                   ws.numel(), _stream()))
+    else:
+        check("mi_moe_decode_phases", lib().mi_moe_decode_phases(gate.c, up.c, down.c, _ptr(x), N, k, _ptr(idx),
+                                                                 _ptr(w), int(shared_expert), float(limit), _ptr(of),
+                                                                 _ptr(ob), _ptr(ws), ws.numel(), int(phases),
+                                                                 _stream()))
     return of, ob
 
 

@@ -26,3 +26,13 @@ def gpu(pkg):
         pytest.skip("no GPU")
     pkg._lib.lib()          # fails loudly if the HIP library is not built
     return torch.device("cuda:0")
+
+
+@pytest.fixture(scope="session")
+def full_cb3_layer(pkg, gpu):
+    """Three CB3 experts at the benchmark's matrix shapes (hidden 6144, intermediate 2048) with the oracle's view of
+    them, built once per session (generating canonical codes on the host takes tens of seconds)."""
+    import numpy as np
+    from tests.util import Layer
+    L = Layer(np.random.default_rng(2026), "CB3", 3, 6144, 2048)
+    return L, L.tables(pkg)

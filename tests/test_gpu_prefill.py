@@ -96,13 +96,12 @@ def test_prefill_limit_clamps(pkg, gpu):
     assert rel_l2(of.cpu().numpy(), _oracle_prefill(L, x, idx, w, limit, E, None, "matmul")) < TOL
 
 
-def test_prefill_full_shape(pkg, gpu):
+def test_prefill_full_shape(pkg, gpu, full_cb3_layer):
     """The benchmark layer's matrix shapes (hidden 6144, intermediate 2048) with two routed experts and the shared
     expert: 200 tokens put 200 rows on each expert, three blocks of up to 96 rows each."""
     rng = np.random.default_rng(2026)
     E, D, I, T, k, limit = 2, 6144, 2048, 200, 2, 10.0
-    L = Layer(rng, "CB3", E + 1, D, I)
-    tbs = L.tables(pkg)
+    L, tbs = full_cb3_layer
     idx = np.tile(np.array([[0, 1]], np.int32), (T, 1))
     idx[::2] = idx[::2, ::-1]
     w = rng.random((T, k)).astype(np.float32)
