@@ -428,7 +428,7 @@ static DecodePlan plan_decode(const mi_table *gate, const mi_table *down, int N,
     p.NS = n_route + (shared >= 0 ? N : 0);
     int est = N == 1 ? p.G : (p.G * 6 + 5) / 10;
     if (est < 1) est = 1;
-    p.persistent = gate->qtype == MI_QT_CB3 && N > kPersistentMinTokens;
+    p.persistent = gate->qtype == MI_QT_CB3 && N > env_int("MI355MOE_PERSIST_ABOVE", kPersistentMinTokens);
     if (p.persistent) {
         // persistent launches: tasks are pipelined, so the per-task fixed cost is small
         const long long slots = 3LL * cu_count();
@@ -457,8 +457,8 @@ static DecodePlan plan_decode(const mi_table *gate, const mi_table *down, int N,
 
 // ------------------------------------------------------------------------------------------------ fused decode
 // Counter block of the fused decode kernel at the start of the decode workspace (its size depends on the table shapes
-// only, so a workspace sized for any N keeps it in place): ticket lists, per-group h counters, per-row-range down
-// counters, the error word (each on its own 128-byte line), then the dense per-(group, row range) split counters.
+// only, so a workspace sized for any N keeps it in place): per-group h counters, per-row-range down counters, the
+// error word (each on its own 128-byte line), then the dense per-(group, row range) split counters.
 struct CtrLayout {
     size_t hcnt, cnt2, err, cnt1, bytes;     // word offsets, total bytes
 };
