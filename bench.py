@@ -54,6 +54,10 @@ def cb3_bytes(R, K):
     return R * (4 * math.ceil(K / 10) + 16 * (K // 128))
 
 
+def iq3s_bytes(R, K):
+    return R * (K // 256) * 110       # 110-byte blocks of 256 weights (the planes hold exactly these bytes)
+
+
 def softmax_topk(rng, N, E, k):
     logits = rng.standard_normal((N, E))
     p = np.exp(logits - logits.max(-1, keepdims=True))
@@ -173,45 +177,53 @@ def main():
     L = args.copies
     per_expert = 2 * cb3_bytes(INTER, D) + cb3_bytes(D, INTER)
 
-    layers = []
-    for c in range(L):
-        tabs = {}
-        for name, (R, K) in (("gate", (INTER, D)), ("up", (INTER, D)), ("down", (D, INTER))):
-            tabs[name] = pkg.random_cb3_table(E, R, K, gen)
-        layers.append(tabs)
+    shapes = (("gate", (INTER, D)), ("up", (INTER, D)), ("down", (D, INTER)))
+    layers = [{name: pkg.random_cb3_table(E, R, K, gen) for name, (R, K) in shapes} for _ in range(L)]
     torch.cuda.synchronize()
+    iq3_layers = []                    # the reference's production format, for the IQ3_S lines (made on demand)
+    per_expert_iq3 = 2 * iq3s_bytes(INTER, D) + iq3s_bytes(D, INTER)
+
+    def iq3():
+        if not iq3_layers:
+            iq3_layers.extend({name: pkg.random_iq3s_table(E, R, K, gen) for name, (R, K) in shapes}
+                              for _ in range(L))
+            torch.cuda.synchronize()
+        return iq3_layers
 
     rng = np.random.default_rng(2026)
     extra = {}
 
-    def layer_fns(N, routing, phases=3, fused=False):
+    def layer_fns(N, routing, phases=3, fused=False, tables=None, pe=per_expert, pe_gu=None):
         """Per-copy step callables for batch N (fixed routing per copy, fresh per copy): mi_moe_decode, or the
         one-launch form mi_moe_decode_fused."""
+        tables = tables or layers
+        pe_gu = pe_gu or 2 * cb3_bytes(INTER, D)
         fns, nbytes = [], []
-        ws = torch.zeros(pkg.resident.decode_workspace_bytes(layers[0]["gate"], layers[0]["down"], N, TOPK, SHARED),
+        ws = torch.zeros(pkg.resident.decode_workspace_bytes(tables[0]["gate"], tables[0]["down"], N, TOPK, SHARED),
                          dtype=torch.uint8, device="cuda")
         out = torch.empty((N, D), dtype=torch.bfloat16, device="cuda")
         for c in range(L):
             idx, w = routing(rng, N, E_ROUTED, TOPK)
             x = torch.randn((N, D), device="cuda", generator=gen).to(torch.bfloat16)
             it, wt = torch.from_numpy(idx).cuda(), torch.from_numpy(w).cuda()
-            t = layers[c]
+            t = tables[c]
             f = (lambda t=t, x=x, it=it, wt=wt: pkg.moe_decode(t["gate"], t["up"], t["down"], x, it, wt, LIMIT,
                                                               shared_expert=SHARED, want_f32=False, out_bf16=out,
                                                               workspace=ws, phases=phases, fused=fused))
             fns.append(f)
             n_exp = len(np.unique(idx)) + 1
-            nbytes.append(n_exp * (per_expert if phases == 3 else 2 * cb3_bytes(INTER, D)))
+            nbytes.append(n_exp * (pe if phases == 3 else pe_gu))
         return fns, nbytes
 
-    def measure(N, routing, phases=3, steps=args.steps, fused=False):
-        fns, nbytes = layer_fns(N, routing, phases, fused)
+    def measure(N, routing, phases=3, steps=args.steps, fused=False, **kw):
+        fns, nbytes = layer_fns(N, routing, phases, fused, **kw)
         ms = Timer(torch, fns).run(steps, args.warmup)
         avg_bytes = float(np.mean([nbytes[i % L] for i in range(steps)]))
         return ms, avg_bytes
 
     if args.only_prefill:
-        print(json.dumps({"prefill_t512": bench_prefill(torch, pkg, gen, args, layers, rng)}))
+        print(json.dumps({"prefill_t512": bench_prefill(torch, pkg, gen, args, layers, rng, per_expert),
+                          "prefill_t512_iq3s": bench_prefill(torch, pkg, gen, args, iq3(), rng, per_expert_iq3)}))
         return
     # headline: batch 1 layer (mi_moe_decode)
     ms1, bytes1 = measure(1, softmax_topk)
@@ -231,7 +243,14 @@ def main():
             gbs = b / (ms * 1e-3) / 1e9
             extra["b%d" % N] = {"us_per_layer": round(ms * 1e3, 2), "GBps": round(gbs, 1),
                                 "pct_hbm": round(100 * gbs / HBM_PEAK_GBS, 1), "bytes_per_layer": int(b)}
-        extra["prefill_t512"] = bench_prefill(torch, pkg, gen, args, layers, rng)
+        # the reference's production format: IQ3_S tables (VALU decode path; matrix-core prefill)
+        for N, routing in ((1, softmax_topk), (8, zipf_topk)):
+            ms, b = measure(N, routing, tables=iq3(), pe=per_expert_iq3)
+            gbs = b / (ms * 1e-3) / 1e9
+            extra["b%d_iq3s" % N] = {"us_per_layer": round(ms * 1e3, 2), "GBps": round(gbs, 1),
+                                     "pct_hbm": round(100 * gbs / HBM_PEAK_GBS, 1), "bytes_per_layer": int(b)}
+        extra["prefill_t512"] = bench_prefill(torch, pkg, gen, args, layers, rng, per_expert)
+        extra["prefill_t512_iq3s"] = bench_prefill(torch, pkg, gen, args, iq3(), rng, per_expert_iq3)
         extra["int8_b8"] = bench_int8(torch, pkg, gen, args)
         extra["cfg0_matvec"] = bench_matvec(torch, pkg, gen, args)
 
@@ -267,7 +286,7 @@ def main():
         torch.cuda.synchronize()
 
 
-def bench_prefill(torch, pkg, gen, args, layers, rng, T=512):
+def bench_prefill(torch, pkg, gen, args, layers, rng, per_expert, T=512):
     """Config: a prefill chunk of 512 tokens through the same layer (top-8 of 64 routed experts from N(0,1) router
     logits, plus the shared expert on every token), grouped GEMMs on the matrix cores.  Algorithmic work: every
     (token, expert) row costs 2 * 3 * D * I flops; weight bytes are those of every distinct expert the chunk uses."""
@@ -276,7 +295,6 @@ def bench_prefill(torch, pkg, gen, args, layers, rng, T=512):
     ws = torch.zeros(pkg.resident.prefill_workspace_bytes(tb0["gate"], tb0["down"], T, TOPK, SHARED),
                      dtype=torch.uint8, device="cuda")
     out = torch.empty((T, D), dtype=torch.bfloat16, device="cuda")
-    per_expert = 2 * cb3_bytes(INTER, D) + cb3_bytes(D, INTER)
     for t in layers:
         idx, w = softmax_topk(rng, T, E_ROUTED, TOPK)
         x = torch.randn((T, D), device="cuda", generator=gen).to(torch.bfloat16)

@@ -1,20 +1,28 @@
-// Grouped prefill for CB3 experts on the gfx950 matrix cores (the reference's ragged prefill,
+// Grouped prefill for CB3 and IQ3_S experts on the gfx950 matrix cores (the reference's ragged prefill,
 // resident.py:144-165 with pallas_moe.py:564-592,622-755):
 //   ragged_plan_kernel  the reference's slot layout (pallas_moe.py:564-592) built on the device by one workgroup:
 //                       slots stably sorted by expert, every expert padded to whole blocks of tm rows;
 //   prefill_kernel      one workgroup per (block, row range) streams the block's expert once for all its rows:
-//                       each wavefront owns 64 weight rows x up to 96 rows of activations (6 MFMA token tiles),
-//                       decodes every weight once (the decoder of cb3_tiles.h) and reuses it across the token
-//                       tiles; the block's activation rows are staged one 160-column tile at a time in LDS;
+//                       each wavefront owns 64 weight rows x up to 80 rows of activations (5 MFMA token tiles),
+//                       decodes every weight once (CB3: the decoder of cb3_tiles.h; IQ3_S: the planes straight
+//                       into the A operand) and reuses it across the token tiles; the block's activation rows are
+//                       staged one column tile (160 / 128 columns) at a time in LDS;
 //                         gate/up: h = bf16(silu(min(g, L)) * clip(u, -L, L)), g and u f32    (pallas_moe.py:682)
 //                         down:    y = bf16(h Wd^T), f32 accumulation                        (pallas_moe.py:747)
 //   prefill_combine     out[t] = sum_j wt(t, j) * y[row_slot(t, j)] in f32 with wt = bf16(w) ("matmul" combine,
 //                       resident.py:161-163) or wt = w ("gather", resident.py:164-165).
-// The rounding points are the reference's: bf16 activations, bf16 weights (CB3 centroids are bf16 already), f32
-// accumulation, h and y rounded to bf16, routing weights rounded to bf16 by the matmul combine.
+// The rounding points are the reference's: bf16 activations, bf16 weights (CB3 centroids are bf16 already; IQ3_S
+// level * scale rounded once), f32 accumulation, h and y rounded to bf16, routing weights rounded to bf16 by the
+// matmul combine.
 #include "cb3_tiles.h"
+#include "formats.h"
 
 namespace mi {
+
+// IQ3_S grid levels (internal linkage: every translation unit that launches a kernel carries its own copy)
+static __constant__ uint32_t kPfGrid[512] = {
+#include "iq3s_grid.inc"
+};
 
 constexpr int kPfTT = 5;                   // token tiles of 16 rows per block
 constexpr int kPfTm = 16 * kPfTT;          // rows per block of the prefill's own plan
@@ -182,7 +190,8 @@ __global__ void __launch_bounds__(kPlanThreads) ragged_plan_kernel(const int32_t
 
 // ------------------------------------------------------------------------------------------------ grouped GEMM
 struct PfArgs {
-    Cb3Table t0, t1;                       // gate/up: gate, up; down: down (twice)
+    Cb3Table t0, t1;                       // CB3 tables -- gate/up: gate, up; down: down (twice)
+    Iq3Table i0, i1;                       // IQ3_S tables, the same roles
     int R, K;                              // output columns (rows of the table), input columns
     const int32_t *blk_expert, *blk_n, *n_blocks, *tok_row;
     const uint16_t *x;                     // gate/up: x [T, K] gathered through tok_row; down: h [Rp, K]
@@ -269,56 +278,204 @@ __device__ __forceinline__ void pf_ctile(const Cb3Wave &w, PfRegs &s, int st, co
 }
 
 struct PfShared {
-    uint4 cbl[kPfWaves * 5 * 64];                // per-wavefront codebook slots (20 KB)
+    union {
+        uint4 cbl[kPfWaves * 5 * 64];            // CB3: per-wavefront codebook slots (20 KB)
+        struct {
+            float4 grid[512];                    // IQ3_S: the grid's levels as f32 (8 KB)
+            uint4 smask[256];                    // IQ3_S: 8 sign bits -> sign bits of 4 bf16 pairs (4 KB)
+        } iq;
+    };
     uint32_t xs[2][kPfTm * kPfXPitch];           // column tiles ct (even/odd) of the block's rows, double-buffered;
                                                  // gate/up epilogue: the gate accumulators of one (gate, up) pair
     uint32_t xrowoff[kPfTm];                     // byte offset of every row's activations, or kXOut
 };
 
+// ------------------------------------------------------------------------------------------------ weight providers
+// A provider streams the weights of one wavefront's 64 rows (4 row tiles) of expert e, one column tile at a time, and
+// runs the tile's k-steps on the matrix cores against the staged activations.  Its state is two values the workgroup
+// body keeps as locals: Wave (addressing, fixed per wavefront) and Regs (the loads in flight).
+//   init(w, s, a, sh, mat, e, rg, wave, lane)   set up w, issue the first column tiles' loads into s
+//   n_tiles(a, mat)                             column tiles of a row
+//   tile<NTT, C>(w, s, st, xt, acc)             column tile 4 st + C; xt = the staged tile at row jt, lane group q
+//   kCols, kQOff                                columns per tile; dwords between lane groups' activations in a step
+
+// CB3: 160-column tiles of the code-tile layout; codebook slots per 640-column super tile (cb3_tiles.h).
+struct PfCb3 {
+    static constexpr int kCols = kCb3TileCols;
+    static constexpr int kQOff = 4;
+    using Wave = Cb3Wave;
+    using Regs = PfRegs;
+    static __device__ __forceinline__ int n_tiles(const PfArgs &a, int mat) { return (mat ? a.t1 : a.t0).CT; }
+    static __device__ __forceinline__ void init(Wave &w, Regs &s, const PfArgs &a, PfShared &sh, int mat, int e,
+                                                int rg, int wave, int lane) {
+        const Cb3Table &tb = mat ? a.t1 : a.t0;
+        const uint32_t *qt = tb.qs + (size_t)e * tb.CT * tb.RT * 256;
+        const uint32_t *cbe = tb.cb + (size_t)e * tb.G * tb.R * 4;
+        w.qb = __builtin_amdgcn_make_buffer_rsrc((void *)qt, (short)0, 0x7fffffff, kBufferWord3);
+        w.qnull = __builtin_amdgcn_make_buffer_rsrc((void *)qt, (short)0, 0, kBufferWord3);
+        w.cbb = __builtin_amdgcn_make_buffer_rsrc((void *)cbe, (short)0, 0x7fffffff, kBufferWord3);
+        w.cbnull = __builtin_amdgcn_make_buffer_rsrc((void *)cbe, (short)0, 0, kBufferWord3);
+        w.ct_bytes = (uint32_t)tb.RT * 1024u;
+        w.rt_bytes = (uint32_t)(rg * kPfRtw) * 1024u;
+        w.g_bytes = (uint32_t)tb.R * 16u;
+        w.row_bytes = (uint32_t)(rg * 64) * 16u;
+        w.cta = 0;
+        w.ctb = tb.CT;
+        w.g_first = 0;
+        w.g_last = tb.G - 1;
+        w.lane16 = (uint32_t)lane * 16u;
+        w.cblane16 = (uint32_t)lane * 16u;
+        w.xh = w.xl = nullptr;
+        w.cbl = sh.cbl + wave * 5 * 64;
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int r = 0; r < kPfRtw; ++r) s.ring[c][r] = cb3_tile(w, c, r);
+#pragma unroll
+        for (int c = 0; c < 5; ++c) s.cbv[c] = cb3_group(w, c);
+    }
+    template <int NTT, int C>
+    static __device__ __forceinline__ void tile(const Wave &w, Regs &s, int st, const uint32_t *xt,
+                                                f32x4 (&acc)[kPfRtw][NTT]) {
+        pf_ctile<NTT, C>(w, s, st, xt, acc);
+    }
+};
+
+// IQ3_S: the reference's planes (planes.py:136-170, row on the minor axis) decoded straight into the matrix cores'
+// A operand.  A column tile is 128 columns = 8 words = half a 256-weight block.  In k-steps 2m and 2m + 1 (m = 0, 1)
+// lane (row i, group q) holds weights 0..7 and 8..15 of word 4m + q of the tile: the k order inside a step is free
+// as long as the activations are read in the same order.  A weight is bf16(level * scale), scale = f16(d) * (1 + 2 sc)
+// in f32 (the product is exact), rounded once to nearest even as the reference's tiles are (pallas_moe.py:341-350,
+// with _decode_iq3_s :127-144); the sign is set on the rounded value (the rounding is symmetric).
+constexpr int kIq3TileCols = 128;
+
+__device__ __forceinline__ uint32_t pf_bf16_pair(float a, float b) {   // round to nearest even
+    const __bf16 v[2] = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+struct PfIq3Wave {
+    const char *qs, *sg, *qh, *sc, *dd;     // expert e's planes
+    uint32_t rpitch;                        // bytes per plane row (4 R)
+    uint32_t lrow;                          // the lane's byte offset in a plane row (row jt of the wavefront)
+    int q;                                  // the lane's group
+    int CT;                                 // column tiles of a row
+    const float4 *grid;                     // LDS: the grid's levels as f32
+    const uint4 *smask;                     // LDS: sign masks
+};
+struct PfIq3Regs {
+    // plane words of column tile ct in slot ct & 1, per row tile: qs of words q and 4 + q, their sg words, qh, sc, d
+    uint32_t v[2][kPfRtw][7];
+};
+
+struct PfIq3 {
+    static constexpr int kCols = kIq3TileCols;
+    static constexpr int kQOff = 8;
+    using Wave = PfIq3Wave;
+    using Regs = PfIq3Regs;
+    static __device__ __forceinline__ int n_tiles(const PfArgs &a, int mat) {
+        return (mat ? a.i1 : a.i0).K / kIq3TileCols;
+    }
+    static __device__ __forceinline__ void load(const Wave &w, int ct, uint32_t (&u)[7], int r) {
+        const uint32_t o = w.lrow + 64u * (uint32_t)r, P = w.rpitch;
+        const int q = w.q;
+        u[0] = *(const uint32_t *)(w.qs + (uint32_t)(8 * ct + q) * P + o);
+        u[1] = *(const uint32_t *)(w.qs + (uint32_t)(8 * ct + 4 + q) * P + o);
+        u[2] = *(const uint32_t *)(w.sg + (uint32_t)(4 * ct + (q >> 1)) * P + o);
+        u[3] = *(const uint32_t *)(w.sg + (uint32_t)(4 * ct + 2 + (q >> 1)) * P + o);
+        u[4] = *(const uint32_t *)(w.qh + (uint32_t)ct * P + o);
+        u[5] = *(const uint32_t *)(w.sc + (uint32_t)(ct >> 1) * P + o);
+        u[6] = *(const uint32_t *)(w.dd + (uint32_t)(ct >> 2) * P + o);
+    }
+    static __device__ __forceinline__ void init(Wave &w, Regs &s, const PfArgs &a, PfShared &sh, int mat, int e,
+                                                int rg, int wave, int lane) {
+        const Iq3Table &tb = mat ? a.i1 : a.i0;
+        const size_t R = (size_t)tb.R;
+        w.qs = (const char *)(tb.qs + (size_t)e * tb.W * R);
+        w.sg = (const char *)(tb.sg + (size_t)e * (tb.W / 2) * R);
+        w.qh = (const char *)(tb.qh + (size_t)e * (tb.W / 8) * R);
+        w.sc = (const char *)(tb.sc + (size_t)e * (tb.W / 16) * R);
+        w.dd = (const char *)(tb.d + (size_t)e * ((tb.nblk + 1) / 2) * R);
+        w.rpitch = 4u * (uint32_t)tb.R;
+        w.q = lane >> 4;
+        w.lrow = 4u * (uint32_t)(rg * 64 + (lane & 15));
+        w.CT = tb.K / kIq3TileCols;
+        w.grid = sh.iq.grid;
+        w.smask = sh.iq.smask;
+        (void)wave;
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int r = 0; r < kPfRtw; ++r) load(w, c, s.v[c][r], r);
+    }
+    // the 8 weights of step j of column tile ct for the row tile whose plane words are u
+    static __device__ __forceinline__ bf16x8 weights8(const Wave &w, const uint32_t (&u)[7], int ct, int j) {
+        const int m = j >> 1, half = j & 1, q = w.q;
+        const uint32_t word = m ? u[1] : u[0];
+        const uint32_t s8 = ((m ? u[3] : u[2]) >> (16 * (q & 1) + 8 * half)) & 255u;
+        const uint32_t qh4 = (u[4] >> (4 * (4 * m + q))) & 15u;
+        const uint32_t nib = (u[5] >> (4 * (4 * (ct & 1) + 2 * m + (q >> 1)))) & 15u;
+        const float scale = f16_bits_to_f32(u[6] >> (16 * ((ct >> 1) & 1))) * (float)(1u + 2u * nib);
+        const uint32_t i0 = ((word >> (16 * half)) & 255u) | (((qh4 >> (2 * half)) & 1u) << 8);
+        const uint32_t i1 = ((word >> (16 * half + 8)) & 255u) | (((qh4 >> (2 * half + 1)) & 1u) << 8);
+        const float4 g0 = w.grid[i0], g1 = w.grid[i1];
+        const uint4 sm = w.smask[s8];
+        uint4 A;
+        A.x = pf_bf16_pair(g0.x * scale, g0.y * scale) | sm.x;
+        A.y = pf_bf16_pair(g0.z * scale, g0.w * scale) | sm.y;
+        A.z = pf_bf16_pair(g1.x * scale, g1.y * scale) | sm.z;
+        A.w = pf_bf16_pair(g1.z * scale, g1.w * scale) | sm.w;
+        return __builtin_bit_cast(bf16x8, A);
+    }
+    template <int NTT, int C>
+    static __device__ __forceinline__ void tile(const Wave &w, Regs &s, int st, const uint32_t *xt,
+                                                f32x4 (&acc)[kPfRtw][NTT]) {
+        const int ct = 4 * st + C;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (j > 0) __builtin_amdgcn_sched_barrier(0);
+            uint4 b[NTT];
+#pragma unroll
+            for (int tt = 0; tt < NTT; ++tt)
+                b[tt] = *(const uint4 *)(xt + tt * 16 * kPfXPitch + 32 * (j >> 1) + 4 * (j & 1));
+            bf16x8 A = weights8(w, s.v[C & 1][0], ct, j);
+#pragma unroll
+            for (int r = 0; r < kPfRtw; ++r) {
+                bf16x8 An = A;
+                if (r + 1 < kPfRtw) An = weights8(w, s.v[C & 1][r + 1], ct, j);
+#pragma unroll
+                for (int tt = 0; tt < NTT; ++tt) acc[r][tt] = mfma16(A, b[tt], acc[r][tt]);
+                A = An;
+            }
+        }
+        // the slot's next column tile (ct + 2); past the row's end nothing is loaded (the slot is not read again)
+        if (ct + 2 < w.CT) {
+#pragma unroll
+            for (int r = 0; r < kPfRtw; ++r) load(w, ct + 2, s.v[C & 1][r], r);
+        }
+    }
+};
+
 // One workgroup: block g (expert e, rows row0 .. row0 + n - 1, NTT = ceil(n / 16) token tiles), row range rbg.
-template <int MODE, int NTT>
+template <int MODE, int NTT, class WP>
 __device__ __forceinline__ void prefill_body(const PfArgs &a, PfShared &sh, int g, int rbg, int e, int n) {
-    uint4 *cbl = sh.cbl;
     uint32_t *xs = &sh.xs[0][0], *xrowoff = sh.xrowoff;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int row0 = g * kPfTm;
     const int mat = MODE == 0 ? (wave & 1) : 0;
-    const Cb3Table &tb = mat ? a.t1 : a.t0;
     const int rg = rbg * a.wg_rows + (MODE == 0 ? (wave >> 1) : wave);   // 64-row group of this wavefront
 
-    Cb3Wave w;
-    const uint32_t *qt = tb.qs + (size_t)e * tb.CT * tb.RT * 256;
-    const uint32_t *cbe = tb.cb + (size_t)e * tb.G * tb.R * 4;
-    w.qb = __builtin_amdgcn_make_buffer_rsrc((void *)qt, (short)0, 0x7fffffff, kBufferWord3);
-    w.qnull = __builtin_amdgcn_make_buffer_rsrc((void *)qt, (short)0, 0, kBufferWord3);
-    w.cbb = __builtin_amdgcn_make_buffer_rsrc((void *)cbe, (short)0, 0x7fffffff, kBufferWord3);
-    w.cbnull = __builtin_amdgcn_make_buffer_rsrc((void *)cbe, (short)0, 0, kBufferWord3);
-    w.ct_bytes = (uint32_t)tb.RT * 1024u;
-    w.rt_bytes = (uint32_t)(rg * kPfRtw) * 1024u;
-    w.g_bytes = (uint32_t)tb.R * 16u;
-    w.row_bytes = (uint32_t)(rg * 64) * 16u;
-    w.cta = 0;
-    w.ctb = tb.CT;
-    w.g_first = 0;
-    w.g_last = tb.G - 1;
-    w.lane16 = (uint32_t)lane * 16u;
-    w.cblane16 = (uint32_t)lane * 16u;
-    w.xh = w.xl = nullptr;
-    w.cbl = cbl + wave * 5 * 64;
+    typename WP::Wave w;
+    typename WP::Regs s;
+    WP::init(w, s, a, sh, mat, e, rg, wave, lane);
 
-    PfRegs s;
-#pragma unroll
-    for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int r = 0; r < kPfRtw; ++r) s.ring[c][r] = cb3_tile(w, c, r);
-#pragma unroll
-    for (int c = 0; c < 5; ++c) s.cbv[c] = cb3_group(w, c);
-
-    // activation tile: the block's 16 NTT rows x 20 uint4 (160 columns), staged by 240 threads as buffer loads, 12
-    // rows per pass (thread t: row t / 20 + 12 j, uint4 column t % 20), so every pass is a constant offset from the
-    // first; rows >= n and columns >= K take an offset past the buffer's range, which reads zero
-    constexpr int kXRows = (64 * kPfWaves) / 20;              // 12
+    // activation tile: the block's 16 NTT rows x kXU uint4 (WP::kCols columns), staged as buffer loads by
+    // kXRows x kXU threads, kXRows rows per pass (thread t: row t / kXU + kXRows j, uint4 column t % kXU), so every
+    // pass is a constant offset from the first; rows >= n and columns >= K take an offset past the buffer's range,
+    // which reads zero
+    constexpr int kXU = WP::kCols / 8;                        // 20 (CB3) or 16 (IQ3_S)
+    constexpr int kXRows = (64 * kPfWaves) / kXU;             // 12 or 16
     constexpr int kXBuf = kPfTm * kPfXPitch;                  // dwords per tile buffer
     constexpr int kXJ = (16 * NTT + kXRows - 1) / kXRows;
     const __amdgpu_buffer_rsrc_t xbuf =
@@ -329,17 +486,17 @@ __device__ __forceinline__ void prefill_body(const PfArgs &a, PfShared &sh, int 
         xrowoff[tid] = o;
     }
     __syncthreads();
-    const int xr0 = tid / 20, xc8 = tid - xr0 * 20;
-    const bool stager = tid < kXRows * 20;
+    const int xr0 = tid / kXU, xc8 = tid - xr0 * kXU;
+    const bool stager = tid < kXRows * kXU;
     uint4 xr[kXJ];
     auto load_x = [&](int ct) {
-        const int lim = (a.K - kCb3TileCols * ct) >> 3;       // uint4 columns of this tile inside the row
+        const int lim = (a.K - WP::kCols * ct) >> 3;          // uint4 columns of this tile inside the row
 #pragma unroll
         for (int j = 0; j < kXJ; ++j) {
             const int row = xr0 + kXRows * j;
             uint32_t o = kXOut;
             if (stager && row < 16 * NTT && xc8 < lim)
-                o = xrowoff[row] + 16u * (uint32_t)xc8 + (uint32_t)(2 * kCb3TileCols * ct);
+                o = xrowoff[row] + 16u * (uint32_t)xc8 + (uint32_t)(2 * WP::kCols * ct);
             xr[j] = bload(xbuf, o, 0);
         }
     };
@@ -359,8 +516,8 @@ __device__ __forceinline__ void prefill_body(const PfArgs &a, PfShared &sh, int 
 #pragma unroll
         for (int t = 0; t < NTT; ++t) acc[r][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
     const int jt = lane & 15, q = lane >> 4;
-    const uint32_t *xrow = xs + jt * kPfXPitch + 4 * q;
-    const int CT = tb.CT;
+    const uint32_t *xrow = xs + jt * kPfXPitch + WP::kQOff * q;
+    const int CT = WP::n_tiles(a, mat);
 
     // one barrier per column tile: tile ct sits in buffer ct & 1 (= C & 1); the next tile's loads are issued first
     // (ahead of this tile's code and codebook loads, so waiting for them never waits for those) and stored into the
@@ -370,7 +527,7 @@ __device__ __forceinline__ void prefill_body(const PfArgs &a, PfShared &sh, int 
         const int ct = 4 * st + C;
         __syncthreads();
         if (ct + 1 < CT) load_x(ct + 1);
-        pf_ctile<NTT, C>(w, s, st, xrow + (C & 1) * kXBuf, acc);
+        WP::template tile<NTT, C>(w, s, st, xrow + (C & 1) * kXBuf, acc);
         if (ct + 1 < CT) store_x((C + 1) & 1);
     };
     const int st_full = CT >> 2;
@@ -439,7 +596,7 @@ __device__ __forceinline__ void prefill_body(const PfArgs &a, PfShared &sh, int 
     }
 }
 
-template <int MODE>   // 0: gate/up -> h, 1: down -> y
+template <int MODE, class WP>   // MODE 0: gate/up -> h, 1: down -> y
 __global__ void __launch_bounds__(64 * kPfWaves, 2) prefill_kernel(PfArgs a) {
     __shared__ PfShared sh;
     // workgroups are dispatched to the XCDs round-robin: all workgroups of one block go to the same XCD (block
@@ -449,12 +606,27 @@ __global__ void __launch_bounds__(64 * kPfWaves, 2) prefill_kernel(PfArgs a) {
     if (g >= *a.n_blocks) return;
     const int e = __builtin_amdgcn_readfirstlane(a.blk_expert[g]);
     const int n = __builtin_amdgcn_readfirstlane(a.blk_n[g]);
+    if constexpr (WP::kCols == kIq3TileCols) {
+        // the grid's levels as f32 and the sign masks (published by the barrier after the row offsets)
+        const int tid = threadIdx.x;
+        for (int i = tid; i < 512; i += 64 * kPfWaves) {
+            const uint32_t v = kPfGrid[i];
+            sh.iq.grid[i] = make_float4((float)(v & 255u), (float)((v >> 8) & 255u), (float)((v >> 16) & 255u),
+                                        (float)(v >> 24));
+        }
+        if (tid < 256) {
+            uint32_t m[4];
+#pragma unroll
+            for (int p = 0; p < 4; ++p) m[p] = (((uint32_t)tid >> (2 * p)) & 1u) << 15 | (((uint32_t)tid >> (2 * p + 1)) & 1u) << 31;
+            sh.iq.smask[tid] = make_uint4(m[0], m[1], m[2], m[3]);
+        }
+    }
     switch ((n + 15) >> 4) {
-        case 1: prefill_body<MODE, 1>(a, sh, g, rbg, e, n); break;
-        case 2: prefill_body<MODE, 2>(a, sh, g, rbg, e, n); break;
-        case 3: prefill_body<MODE, 3>(a, sh, g, rbg, e, n); break;
-        case 4: prefill_body<MODE, 4>(a, sh, g, rbg, e, n); break;
-        default: prefill_body<MODE, kPfTT>(a, sh, g, rbg, e, n); break;
+        case 1: prefill_body<MODE, 1, WP>(a, sh, g, rbg, e, n); break;
+        case 2: prefill_body<MODE, 2, WP>(a, sh, g, rbg, e, n); break;
+        case 3: prefill_body<MODE, 3, WP>(a, sh, g, rbg, e, n); break;
+        case 4: prefill_body<MODE, 4, WP>(a, sh, g, rbg, e, n); break;
+        default: prefill_body<MODE, kPfTT, WP>(a, sh, g, rbg, e, n); break;
     }
 }
 
@@ -530,13 +702,34 @@ static Cb3Table pf_table(const mi_table *t) {
     return c;
 }
 
+static Iq3Table pf_iq3_table(const mi_table *t) {
+    Iq3Table c{};
+    c.qs = t->plane[0];
+    c.sg = t->plane[1];
+    c.qh = t->plane[2];
+    c.sc = t->plane[3];
+    c.d = t->plane[4];
+    c.R = t->rows;
+    c.K = t->cols;
+    c.nblk = t->cols / 256;
+    c.W = 16 * c.nblk;
+    return c;
+}
+
+// The three tables share one format: CB3 (code tiles) or IQ3_S (the reference's planes, whole 256-weight blocks).
 static int pf_validate(const mi_table *g, const mi_table *u, const mi_table *d) {
     if (!g || !u || !d) return MI_ERR_NULL;
     for (const mi_table *t : {g, u, d}) {
-        if (t->qtype != MI_QT_CB3) return MI_ERR_QTYPE;     // the prefill kernels decode CB3 tiles
-        if (!t->plane[0] || !t->plane[1]) return MI_ERR_NULL;
+        if (t->qtype != MI_QT_CB3 && t->qtype != MI_QT_IQ3_S) return MI_ERR_QTYPE;
+        if (t->qtype != g->qtype) return MI_ERR_MISMATCH;
+        const int np = t->qtype == MI_QT_CB3 ? 2 : 5;
+        for (int i = 0; i < np; ++i)
+            if (!t->plane[i]) return MI_ERR_NULL;
         if (t->n_experts <= 0 || t->n_experts > kPlanMaxE || t->cols <= 0 || t->cols % 128 || t->rows <= 0)
             return MI_ERR_SHAPE;
+        if (t->qtype == MI_QT_IQ3_S && t->cols % 256) return MI_ERR_SHAPE;
+        // an expert's plane stays below 4 GiB (32-bit byte offsets)
+        if (t->qtype == MI_QT_IQ3_S && (long long)(t->cols / 16) * t->rows * 4 >= (1ll << 32)) return MI_ERR_SHAPE;
     }
     if (g->rows % 128 || d->rows % 256) return MI_ERR_SHAPE;   // whole workgroup row ranges
     if (u->rows != g->rows || u->cols != g->cols || u->n_experts != g->n_experts) return MI_ERR_MISMATCH;
@@ -617,9 +810,15 @@ int mi_moe_prefill(const mi_table *gate, const mi_table *up, const mi_table *dow
     uint16_t *h = (uint16_t *)(ws + L.off_h), *y = (uint16_t *)(ws + L.off_y);
     if ((st = launch_plan(idx, w, T, k, shared_expert, E, kPfTm, p, s))) return st;
 
+    const bool iq3 = gate->qtype == MI_QT_IQ3_S;
     PfArgs a{};
-    a.t0 = pf_table(gate);
-    a.t1 = pf_table(up);
+    if (iq3) {
+        a.i0 = pf_iq3_table(gate);
+        a.i1 = pf_iq3_table(up);
+    } else {
+        a.t0 = pf_table(gate);
+        a.t1 = pf_table(up);
+    }
     a.R = I;
     a.K = gate->cols;
     a.blk_expert = p.blk_expert;
@@ -634,11 +833,13 @@ int mi_moe_prefill(const mi_table *gate, const mi_table *up, const mi_table *dow
     a.wg_rows = 2;
     a.RBG = I / 128;
     const int g8 = (L.G + kXcds - 1) / kXcds * kXcds;       // blocks rounded up to whole XCD rounds
-    hipLaunchKernelGGL(prefill_kernel<0>, dim3(g8 * a.RBG), dim3(64 * kPfWaves), 0, s, a);
+    if (iq3) hipLaunchKernelGGL((prefill_kernel<0, PfIq3>), dim3(g8 * a.RBG), dim3(64 * kPfWaves), 0, s, a);
+    else hipLaunchKernelGGL((prefill_kernel<0, PfCb3>), dim3(g8 * a.RBG), dim3(64 * kPfWaves), 0, s, a);
     if (hipGetLastError() != hipSuccess) return MI_ERR_LAUNCH;
 
     PfArgs b = a;
-    b.t0 = b.t1 = pf_table(down);
+    if (iq3) b.i0 = b.i1 = pf_iq3_table(down);
+    else b.t0 = b.t1 = pf_table(down);
     b.R = D;
     b.K = I;
     b.x = h;
@@ -647,7 +848,8 @@ int mi_moe_prefill(const mi_table *gate, const mi_table *up, const mi_table *dow
     b.out = y;
     b.wg_rows = 4;
     b.RBG = D / 256;
-    hipLaunchKernelGGL(prefill_kernel<1>, dim3(g8 * b.RBG), dim3(64 * kPfWaves), 0, s, b);
+    if (iq3) hipLaunchKernelGGL((prefill_kernel<1, PfIq3>), dim3(g8 * b.RBG), dim3(64 * kPfWaves), 0, s, b);
+    else hipLaunchKernelGGL((prefill_kernel<1, PfCb3>), dim3(g8 * b.RBG), dim3(64 * kPfWaves), 0, s, b);
     if (hipGetLastError() != hipSuccess) return MI_ERR_LAUNCH;
 
     const long long nthr = (long long)T * (D / 4);

@@ -117,6 +117,21 @@ def random_cb3_table(E, R, K, generator, scale=0.02):
     return ExpertTable("CB3", {"qs": qs, "cb": torch.cat(cbs, 0).contiguous()}, R, K)
 
 
+def random_iq3s_table(E, R, K, generator, scale=0.02):
+    """An ExpertTable of E random IQ3_S experts in the reference's planes, generated on the GPU: uniform random qs,
+    sg, qh and sc words (every bit pattern is a valid set of grid indices, signs and scales) and per-block f16 d
+    uniform in [scale / 2, scale] (as oracle.iq3s.random_blocks draws them).  For benchmarks at full shape."""
+    rp = _plane_rows("IQ3_S", K)
+    planes = {}
+    for k in ("qs", "sg", "qh", "sc"):
+        planes[k] = torch.randint(-2 ** 31, 2 ** 31 - 1, (E * rp[k], R), dtype=torch.int32, device="cuda",
+                                  generator=generator)
+    d = torch.rand((E * rp["d"], R, 2), device="cuda", generator=generator) * (0.5 * scale) + 0.5 * scale
+    bits = d.to(torch.float16).view(torch.int16).to(torch.int32) & 0xFFFF
+    planes["d"] = (bits[..., 0] | (bits[..., 1] << 16)).contiguous()
+    return ExpertTable("IQ3_S", planes, R, K)
+
+
 class _Workspaces:
     """Device workspaces, one per (device, stream, purpose); grown on demand.  They are zero-filled when allocated:
     the decode workspace's counter block must start at zero (each mi_moe_decode call leaves it zero again)."""
@@ -356,7 +371,7 @@ class ResidentFetch:
     apply(p, x, idx, w, layer, limit): x [N, D]; idx [N, k] int32 into E; w [N, k] f32 -> f32 [N, D] (routed experts
     only; the caller adds the shared expert, model.py:847-855).  N*k <= gather_max_rows takes the fused decode
     kernels (f32 end to end, resident.py:110-120); larger calls take the grouped prefill GEMMs with the reference's
-    bf16 rounding points and ``combine`` (resident.py:144-165; CB3 tables; bf16 ``out_dtype``).
+    bf16 rounding points and ``combine`` (resident.py:144-165; CB3 or IQ3_S tables; bf16 ``out_dtype``).
     ``use_pallas`` / ``interpret`` / ``sweep_mode`` / ``chunk`` are accepted for signature compatibility; there is a
     single MI355X kernel path per regime."""
 
@@ -395,9 +410,9 @@ class ResidentFetch:
                 raise ValueError("decode activations must be bf16-representable (the layer dtype)")
             out, _ = moe_decode(gate, up, down, xb, idx, w, limit)
             return out
-        if gate.qtype != "CB3" or up.qtype != "CB3" or down.qtype != "CB3":
+        if not (gate.qtype == up.qtype == down.qtype):
             raise NotImplementedError("ResidentFetch.apply: the grouped prefill path (N*k = %d > gather_max_rows = %d) "
-                                      "is built for CB3 tables only" % (N * k, self.gather_max_rows))
+                                      "takes one format for gate, up and down" % (N * k, self.gather_max_rows))
         if self.out_dtype != torch.bfloat16:
             raise NotImplementedError("ResidentFetch.apply: the grouped prefill path follows the bf16 out_dtype "
                                       "rounding points (resident.py:153-158)")

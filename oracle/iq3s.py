@@ -43,8 +43,23 @@ def plane_rows(nblk):
 
 # ------------------------------------------------------------------------------------------------ block form
 def dequant_blocks(blk):
-    """uint8 [..., nblk, 110] -> f32 [..., nblk, 256]: restates iqquant.dequant_iq3_s (iqquant.py:123-132)."""
+    """uint8 [..., nblk, 110] -> f32 [..., nblk, 256]: restates iqquant.dequant_iq3_s (iqquant.py:123-132).
+    Every block decodes on its own, so large inputs are decoded in chunks of blocks (smaller temporaries)."""
     blk = np.asarray(blk, dtype=np.uint8)
+    n = blk.size // BLOCK_BYTES
+    if n > _CHUNK_BLOCKS:
+        flat = blk.reshape(n, BLOCK_BYTES)
+        out = np.empty((n, QK), np.float32)
+        for i in range(0, n, _CHUNK_BLOCKS):
+            out[i:i + _CHUNK_BLOCKS] = _dequant_blocks(flat[i:i + _CHUNK_BLOCKS])
+        return out.reshape(blk.shape[:-1] + (QK,))
+    return _dequant_blocks(blk)
+
+
+_CHUNK_BLOCKS = 8192
+
+
+def _dequant_blocks(blk):
     d = f16_bits_to_f32(blk[..., 0].astype(np.uint32) | (blk[..., 1].astype(np.uint32) << 8))      # [...]
     qs = blk[..., 2:66].astype(np.int64)                                                            # [..., 64]
     qh = np.unpackbits(blk[..., 66:74], axis=-1, bitorder="little").astype(np.int64)               # [..., 64]

@@ -89,7 +89,13 @@ def test_prefill_host_validation(L, pkg):
     call = lambda gg, uu, dd, T=4, k=2, shared=-1, limit=10.0, comb=0, o=out, wsb=1 << 30: L.mi_moe_prefill(
         ctypes.byref(gg), ctypes.byref(uu), ctypes.byref(dd), x, T, k, idx, w, shared, ctypes.c_float(limit), comb,
         o, None, ws, wsb, None)
-    assert call(_table(pkg, qtype=2, planes=5), u, d) == 2                       # MI_ERR_QTYPE: CB3 tables only
+    assert call(_table(pkg, qtype=9), u, d) == 2                                 # MI_ERR_QTYPE
+    assert call(_table(pkg, qtype=2, planes=5), u, d) == 6                       # one format for all three tables
+    iq = lambda rows, cols, planes=5: _table(pkg, qtype=2, rows=rows, cols=cols, planes=planes)
+    gi, ui, di = iq(256, 1280), iq(256, 1280), iq(1280, 256)
+    assert call(gi, ui, di, wsb=16) == 5                                         # IQ3_S tables pass validation
+    assert call(iq(256, 640), iq(256, 640), iq(1280, 256)) == 3                  # IQ3_S: whole 256-weight blocks
+    assert call(gi, ui, iq(1280, 256, planes=4)) == 1                            # IQ3_S: five planes
     assert call(_table(pkg, rows=192), _table(pkg, rows=192), d) == 3             # gate rows % 128
     assert call(g, u, _table(pkg, rows=1152, cols=256)) == 3                     # down rows % 256
     assert call(g, u, _table(pkg, rows=1280, cols=512)) == 6                     # down.cols != gate.rows

@@ -1,5 +1,5 @@
-"""GPU parity of the grouped prefill path (resident.py:144-165): the device ragged_plan, the CB3 grouped GEMMs on
-the matrix cores and the combine, against the CPU oracle.
+"""GPU parity of the grouped prefill path (resident.py:144-165): the device ragged_plan, the grouped GEMMs on
+the matrix cores (CB3 and IQ3_S tables) and the combine, against the CPU oracle.
 
 Bar: the plan is bit-exact against oracle.moe.ragged_plan (pallas_moe.py:564-592 restated in numpy); prefill
 outputs within rel-L2 <= 1e-3 of oracle.moe.prefill_apply, which rounds where the reference rounds (x, h and y to
@@ -57,18 +57,32 @@ def _oracle_prefill(L, x, idx, w, limit, E, shared, combine):
     return omoe.prefill_apply(L.deq, x, idx, w, limit, E, combine=combine)
 
 
-@pytest.mark.parametrize("T,k,E,D,I,shared,combine,kind", [
+SMALL = [
     (40, 4, 6, 512, 256, False, "matmul", "zipf"),
     (40, 4, 6, 512, 256, True, "gather", "zipf"),
-    (200, 2, 3, 1280, 384, True, "matmul", "zipf"),       # experts with several blocks of 96 rows
+    (200, 2, 3, 1280, 384, True, "matmul", "zipf"),       # experts with several blocks of 80 rows
     (1, 8, 16, 512, 256, False, "matmul", "softmax"),
-    (97, 1, 2, 512, 256, False, "gather", "one"),         # one expert: a full block and a 1-row block
+    (97, 1, 2, 512, 256, False, "gather", "one"),         # one expert: a full block and a 17-row block
     (33, 3, 5, 768, 128, True, "matmul", "uniform"),
-])
-def test_prefill_small(pkg, gpu, T, k, E, D, I, shared, combine, kind):
+]
+# IQ3_S: whole 256-weight blocks per row (K % 256 == 0)
+SMALL_IQ3 = [
+    (40, 4, 6, 512, 256, False, "matmul", "zipf"),
+    (40, 4, 6, 512, 256, True, "gather", "zipf"),
+    (200, 2, 3, 1024, 512, True, "matmul", "zipf"),
+    (1, 8, 16, 512, 256, False, "matmul", "softmax"),
+    (97, 1, 2, 512, 256, False, "gather", "one"),
+    (33, 3, 5, 768, 256, True, "matmul", "uniform"),
+    (81, 2, 2, 2560, 768, True, "gather", "zipf"),        # partial super tiles of 128-column tiles (K / 128 = 20, 6)
+]
+
+
+@pytest.mark.parametrize("qtype,T,k,E,D,I,shared,combine,kind",
+                         [("CB3",) + c for c in SMALL] + [("IQ3_S",) + c for c in SMALL_IQ3])
+def test_prefill_small(pkg, gpu, qtype, T, k, E, D, I, shared, combine, kind):
     rng = np.random.default_rng(7 * T + E)
     limit = 10.0
-    L = Layer(rng, "CB3", E + (1 if shared else 0), D, I)
+    L = Layer(rng, qtype, E + (1 if shared else 0), D, I)
     tbs = L.tables(pkg)
     idx, w = _routing(rng, kind, T, E, k)
     x = round_bf16(rng.standard_normal((T, D)).astype(np.float32))
@@ -84,11 +98,12 @@ def test_prefill_small(pkg, gpu, T, k, E, D, I, shared, combine, kind):
     assert torch.equal(of, of2)                      # deterministic
 
 
-def test_prefill_limit_clamps(pkg, gpu):
+@pytest.mark.parametrize("qtype", ["CB3", "IQ3_S"])
+def test_prefill_limit_clamps(pkg, gpu, qtype):
     """A small swiglu limit makes the clamps of model.py:119-122 active in the gate/up epilogue."""
     rng = np.random.default_rng(4)
     E, D, I, T, k, limit = 5, 512, 256, 60, 3, 0.05
-    L = Layer(rng, "CB3", E, D, I)
+    L = Layer(rng, qtype, E, D, I)
     tbs = L.tables(pkg)
     idx, w = zipf_routing(rng, T, E, k)
     x = round_bf16(rng.standard_normal((T, D)).astype(np.float32))
@@ -112,17 +127,35 @@ def test_prefill_full_shape(pkg, gpu, full_cb3_layer):
     assert err < TOL, err
 
 
-def test_resident_fetch_prefill(pkg, gpu):
+@pytest.mark.parametrize("qtype", ["CB3", "IQ3_S"])
+def test_resident_fetch_prefill(pkg, gpu, qtype):
     """ResidentFetch.apply with N*k > gather_max_rows takes the grouped prefill path (resident.py:104-108)."""
     rng = np.random.default_rng(8)
     E, D, I, T, k, limit = 8, 512, 256, 24, 4, 10.0
-    L = Layer(rng, "CB3", E, D, I)
+    L = Layer(rng, qtype, E, D, I)
     p = {}
     for name, key in (("gate", "gate_q"), ("up", "up_q"), ("down", "down_q")):
         p[key] = pkg.to_device_planes(L.planes(name, pkg.formats))
-    fetch = pkg.ResidentFetch({0: {"gate_q": "CB3", "up_q": "CB3", "down_q": "CB3"}}, D, I)
+    fetch = pkg.ResidentFetch({0: {"gate_q": qtype, "up_q": qtype, "down_q": qtype}}, D, I)
     idx, w = zipf_routing(rng, T, E, k)
     x = round_bf16(rng.standard_normal((T, D)).astype(np.float32))
     y = fetch.apply(p, _t(x, torch.bfloat16), _t(idx), _t(w), 0, limit)
     assert y.dtype == torch.float32 and tuple(y.shape) == (T, D)
     assert rel_l2(y.cpu().numpy(), _oracle_prefill(L, x, idx, w, limit, E, None, "matmul")) < TOL
+
+
+def test_prefill_full_shape_iq3s(pkg, gpu):
+    """IQ3_S at the benchmark layer's matrix shapes (hidden 6144, intermediate 2048): two routed experts and the
+    shared expert, 120 tokens (two blocks of 80 rows per expert)."""
+    rng = np.random.default_rng(2027)
+    E, D, I, T, k, limit = 2, 6144, 2048, 120, 2, 10.0
+    L = Layer(rng, "IQ3_S", E + 1, D, I)
+    tbs = L.tables(pkg)
+    idx = np.tile(np.array([[0, 1]], np.int32), (T, 1))
+    idx[::2] = idx[::2, ::-1]
+    w = rng.random((T, k)).astype(np.float32)
+    x = round_bf16(rng.standard_normal((T, D)).astype(np.float32))
+    of, _ = pkg.moe_prefill(tbs["gate"], tbs["up"], tbs["down"], _t(x, torch.bfloat16), _t(idx), _t(w), limit,
+                            shared_expert=E)
+    err = rel_l2(of.cpu().numpy(), _oracle_prefill(L, x, idx, w, limit, E, E, "matmul"))
+    assert err < TOL, err
