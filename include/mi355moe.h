@@ -42,7 +42,7 @@ extern "C" {
 /*
  * One expert table: E experts of one matrix kind (gate, up or down), every expert R rows x K inputs.  plane[] order:
  *   MI_QT_IQ3_S : {qs, sg, qh, sc, d}   -- the reference's planes, unchanged: u32 [E * rows_p, R], the matrix row
- *                                          on the minor axis (planes.py:5-14,45).  R % 256 == 0, K % 256 == 0.
+ *                                          on the minor axis (planes.py:5-14,45).  R % 64 == 0, K % 256 == 0.
  *   MI_QT_CB3   : {qs, cb}              -- qs: u32 [E][ceil(K/160)][R/16][64][4] code tiles (16 rows x 160 columns,
  *                                          1 KB each, in the lane order of the matrix-core decoder; formats.py
  *                                          cb3_tile_words gives the bit map); cb: u32 [E][K/128][R][4] = bytes

@@ -11,8 +11,6 @@ namespace mi {
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kWave = 64;
-constexpr int kRowsPerLane = 4;                      // every lane owns 4 consecutive matrix rows
-constexpr int kRowBlock = kWave * kRowsPerLane;      // 256 rows per wavefront
 constexpr int kMaxT = 16;                            // slots per expert group (one wavefront pass)
 constexpr int kMaxExperts = 1024;
 

@@ -12,8 +12,11 @@
 //      reduction finishes a matvec).
 // Results are therefore deterministic: no float atomics, every sum in a fixed order.
 #pragma once
+#include <type_traits>
+
 #include "cb3_tiles.h"
 #include "formats.h"
+#include "iq3_mfma.h"
 
 namespace mi {
 
@@ -63,32 +66,6 @@ __host__ __device__ inline int slot_token(int slot, int n_route, int k) {
 
 // `stage` stages the activation rows into LDS (ending in a workgroup barrier); the decoders call it right after
 // issuing their first weight loads, so the staging latency overlaps the first HBM round trip.
-
-// IQ3_S rows (4 per lane, 256 per wavefront): accumulate with the smallest token class >= n (classes above TCMAX
-// are not compiled into the launch) and store the partials of the n real rows.
-template <bool HILO, int TCMAX, class Stage>
-__device__ __forceinline__ void iq3_run_and_store(const Iq3Table &tb, int e, int r0, int u0, int u1, int c0,
-                                                  const uint32_t *grid, const uint32_t *xh, const uint32_t *xl, int xs,
-                                                  int n, const int *slots, float *part_base, int R, Stage &&stage) {
-#define MI_RUN_CLASS(TCV)                                                                          \
-    {                                                                                              \
-        float acc[4][TCV];                                                                         \
-        _Pragma("unroll") for (int i = 0; i < 4; ++i) _Pragma("unroll") for (int t = 0; t < TCV; ++t) acc[i][t] = 0.f; \
-        iq3_accum<TCV, HILO>(tb, e, r0, u0, u1, c0, grid, xh, xl, xs, acc, stage);                 \
-        _Pragma("unroll") for (int t = 0; t < TCV; ++t) {                                          \
-            if (t < n) {                                                                           \
-                float4 v = make_float4(acc[0][t], acc[1][t], acc[2][t], acc[3][t]);                \
-                *(float4 *)(part_base + (size_t)slots[t] * R + r0) = v;                            \
-            }                                                                                      \
-        }                                                                                          \
-    }
-    if (TCMAX == 1 || n <= 1) MI_RUN_CLASS(1)
-    else if (TCMAX == 2 || n <= 2) MI_RUN_CLASS((TCMAX >= 2 ? 2 : 1))
-    else if (TCMAX == 4 || n <= 4) MI_RUN_CLASS((TCMAX >= 4 ? 4 : 1))
-    else if (TCMAX == 8 || n <= 8) MI_RUN_CLASS((TCMAX >= 8 ? 8 : 1))
-    else MI_RUN_CLASS((TCMAX >= 16 ? 16 : 1))
-#undef MI_RUN_CLASS
-}
 
 // CB3 rows (16 RTW per wavefront, matrix cores).  B-operand lane (column jt = lane % 16 of the 16x16 tile, k-chunk q):
 //   bf16 activations: token jt;
@@ -159,22 +136,22 @@ constexpr int kDmaStageRows = 4;
 // matvec = 4 row groups.  A row group is the rows of one wavefront: 64 (CB3) or 256 (IQ3_S).
 constexpr int kWgWaves = 4;
 
-// Rows per wavefront: CB3 16 RTW (RTW row tiles), IQ3_S 256 (4 rows per lane).
+// Rows per wavefront: CB3 16 RTW (RTW row tiles), IQ3_S 64 (four interleaved row tiles).
 template <int QT, int RTW>
-__host__ __device__ constexpr int wave_rows() { return QT == MI_QT_CB3 ? 16 * RTW : kRowBlock; }
+__host__ __device__ constexpr int wave_rows() { return QT == MI_QT_CB3 ? 16 * RTW : kIq3WaveRows; }
 
-// CB3 kernels are held to MI_CB3_WAVES wavefronts per SIMD (3: <= 168 VGPRs): more HBM requests in flight per CU.
+// The kernels are held to MI_CB3_WAVES wavefronts per SIMD (3: <= 168 VGPRs): more HBM requests in flight per CU.
 #ifndef MI_CB3_WAVES
 #define MI_CB3_WAVES 3
 #endif
 template <int QT>
-__host__ __device__ constexpr int min_waves_per_simd() { return QT == MI_QT_CB3 ? MI_CB3_WAVES : 1; }
+__host__ __device__ constexpr int min_waves_per_simd() { return MI_CB3_WAVES; }
 
 template <int MODE, int QT, int TCMAX, int RTW>
 __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) grouped_kernel(KArgs a) {
     extern __shared__ uint32_t xlds[];
     __shared__ GroupScratch sc;
-    __shared__ uint32_t grid[QT == MI_QT_IQ3_S ? 512 : 1];
+    __shared__ typename std::conditional<QT == MI_QT_IQ3_S, Iq3Lds, char>::type iq;   // IQ3_S: grid and sign tables
     __shared__ uint4 cbl[QT == MI_QT_CB3 ? kWgWaves * 5 * 64 : 1];   // CB3: per-wavefront codebook slots
     __shared__ int s_tok[kMaxT];
 
@@ -192,8 +169,7 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
     if (e < 0) return;
     const int n = __builtin_amdgcn_readfirstlane(sc.g.n);
 
-    if constexpr (!cb3)
-        for (int i = tid; i < 512; i += blockDim.x) grid[i] = kGridConst[i];
+    if constexpr (!cb3) iq3_fill_lds(iq, kGridConst);     // published by the barrier after the slot list
 
     // column range of the split; CB3 stages its padded column tiles (columns >= K are zero)
     const int ucols = cb3 ? Cb3Table::kUnitCols : Iq3Table::kUnitCols;
@@ -205,7 +181,7 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
     const int cv = u0 * ucols;                // first column of the split
     const int c1 = cb3 ? u1 * ucols : min(a.K, u1 * ucols);
     const int xs = (c1 - c0) >> 1;            // dwords per staged row
-    const int xsp = cb3 ? cb3_row_pitch(xs) : xs;   // row pitch (CB3: whole 64-dword chunks, skewed)
+    const int xsp = cb3_row_pitch(xs);        // row pitch: whole 64-dword chunks, skewed by 4 banks per row
     const bool hilo = (MODE == kDown) || (MODE == kMatvec && a.x_f32 != nullptr);
     uint32_t *xh = xlds;
     uint32_t *xl = xlds + (size_t)a.t_rows * a.xs_max;
@@ -299,13 +275,12 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
             cb3_run_and_store<false, TCMAX, RTW>(tb.cb3, e, rg, u0, u1, c0, xh, xl, xsp, a.t_rows, n, s_tok, part_base,
                                             a.R, cbl + wave * 5 * 64, stage);
     } else {
-        const int r0 = rg * WR + lane * kRowsPerLane;
         if (hilo)
-            iq3_run_and_store<true, TCMAX>(tb.iq3, e, r0, u0, u1, c0, grid, xh, xl, xs, n, s_tok, part_base, a.R,
-                                           stage);
+            iq3m_run_and_store<true, TCMAX>(tb.iq3, e, rg * WR, u0, u1, c0, iq, xh, xl, xsp, a.t_rows, n, s_tok,
+                                            part_base, a.R, stage);
         else
-            iq3_run_and_store<false, TCMAX>(tb.iq3, e, r0, u0, u1, c0, grid, xh, xl, xs, n, s_tok, part_base, a.R,
-                                            stage);
+            iq3m_run_and_store<false, TCMAX>(tb.iq3, e, rg * WR, u0, u1, c0, iq, xh, xl, xsp, a.t_rows, n, s_tok,
+                                             part_base, a.R, stage);
     }
     // The partials are reduced by the next launch (gate/up: the SwiGLU kernel; down: the combine; matvec: the split
     // reduction): kernel order publishes them, so no completion counters or fences are needed.

@@ -172,7 +172,7 @@ __global__ void split_reduce_kernel(const float *__restrict__ part, int S, int N
 static int validate_table(const mi_table *t) {
     if (!t) return MI_ERR_NULL;
     if (t->qtype != MI_QT_CB3 && t->qtype != MI_QT_IQ3_S) return MI_ERR_QTYPE;
-    if (t->rows <= 0 || t->rows % (t->qtype == MI_QT_CB3 ? kCb3RowAlign : kRowBlock)) return MI_ERR_SHAPE;
+    if (t->rows <= 0 || t->rows % (t->qtype == MI_QT_CB3 ? kCb3RowAlign : kIq3WaveRows)) return MI_ERR_SHAPE;
     if (t->n_experts <= 0 || t->n_experts > kMaxExperts) return MI_ERR_SHAPE;
     if (t->qtype == MI_QT_CB3) {
         if (t->cols <= 0 || t->cols % 128) return MI_ERR_SHAPE;
@@ -215,8 +215,8 @@ static int n_units_of(const mi_table *t) {
     if (t->qtype == MI_QT_CB3) return cb3_ct(t);                 // 160-column tiles
     return t->cols / 256;                                        // IQ3_S blocks
 }
-// Rows per wavefront: CB3 16 rtw (rtw row tiles), IQ3_S 256.
-static int wave_rows_of(const mi_table *t, int rtw) { return t->qtype == MI_QT_CB3 ? 16 * rtw : kRowBlock; }
+// Rows per wavefront: CB3 16 rtw (rtw row tiles), IQ3_S 64 (four interleaved row tiles).
+static int wave_rows_of(const mi_table *t, int rtw) { return t->qtype == MI_QT_CB3 ? 16 * rtw : kIq3WaveRows; }
 static int unit_cols(const mi_table *t) { return t->qtype == MI_QT_CB3 ? kCb3TileCols : 256; }
 
 static int env_int(const char *name, int dflt) {
@@ -252,7 +252,7 @@ static void split_extent(const mi_table *t, int S, int align, int *xs_max, int *
         split_bounds(nu, S, align, s, &u0, &u1);
         const int ua = cb3 ? 4 * (u0 / 4) : u0;
         const int c1 = u1 * uc < cend ? u1 * uc : cend;
-        const int xs = cb3 ? cb3_row_pitch((c1 - ua * uc) / 2) : (c1 - ua * uc) / 2;
+        const int xs = cb3_row_pitch((c1 - ua * uc) / 2);
         if (xs > bx) bx = xs;
         if (u1 - ua > bu) bu = u1 - ua;
     }
@@ -338,7 +338,9 @@ static Shape choose_shape(const mi_table *t, int mode, int tcmax, int groups, in
         if (forced_rtw > 0 && cb3 && rtw != forced_rtw) continue;
         const int RB = t->rows / wave_rows_of(t, rtw);
         const int RBG = (RB + rg_per_wg - 1) / rg_per_wg;
-        const double kb_per_unit = cb3 ? rtw * 1.25 : 1.0;
+        // kilobytes a wavefront streams per unit: CB3 one 1 KB code tile per row tile + codebook; IQ3_S 64 rows of
+        // a 110-byte block
+        const double kb_per_unit = cb3 ? rtw * 1.25 : 64 * 110 / 1024.0;
         const int aligns[2] = {cb3 ? 4 : 1, 1};
         for (int ai = 0; ai < 2; ++ai) {
             const int align = aligns[ai];
