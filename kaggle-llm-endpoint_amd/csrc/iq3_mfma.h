@@ -23,7 +23,7 @@ constexpr int kIq3WaveRows = 64;
 // LDS tables of the decoder.
 struct Iq3Lds {
     uint2 level[512];      // grid entry -> its 4 odd levels as bf16 (two pairs)
-    uint4 smask[256];      // 8 sign bits -> the sign bits (15, 31) of 4 bf16 pairs
+    uint2 smask[16];       // 4 sign bits -> the sign bits (15, 31) of 2 bf16 pairs (32 banks: reads never conflict)
 };
 
 // Every thread of the workgroup takes part; a barrier must follow before the tables are read.
@@ -34,12 +34,9 @@ __device__ __forceinline__ void iq3_fill_lds(Iq3Lds &t, const uint32_t *grid) {
         const uint32_t b2 = __float_as_uint((float)((v >> 16) & 255u)) >> 16, b3 = __float_as_uint((float)(v >> 24)) >> 16;
         t.level[i] = make_uint2(b0 | (b1 << 16), b2 | (b3 << 16));
     }
-    for (int i = threadIdx.x; i < 256; i += blockDim.x) {
-        const uint32_t s = (uint32_t)i;
-        uint32_t m[4];
-#pragma unroll
-        for (int p = 0; p < 4; ++p) m[p] = ((s >> (2 * p)) & 1u) << 15 | ((s >> (2 * p + 1)) & 1u) << 31;
-        t.smask[i] = make_uint4(m[0], m[1], m[2], m[3]);
+    if (threadIdx.x < 16) {
+        const uint32_t s = threadIdx.x;
+        t.smask[s] = make_uint2((s & 1u) << 15 | ((s >> 1) & 1u) << 31, ((s >> 2) & 1u) << 15 | ((s >> 3) & 1u) << 31);
     }
 }
 
@@ -63,6 +60,8 @@ __device__ __forceinline__ void iq3m_accum(const Iq3Table &tb, int e, int row0, 
     const uint32_t *sc = tb.sc + (size_t)e * (W / 16) * R;
     const uint32_t *dd = tb.d + (size_t)e * ((tb.nblk + 1) / 2) * R;
     const int wsel = q >> 1, half = q & 1;
+    // lane shifts: the two grid indices in the qs word, the 8 signs in the sg word, the 2 high index bits in qh
+    const uint32_t qs_sh = 16 * half, sg_sh = 16 * wsel + 8 * half, qh_sh = 4 * wsel + 2 * half;
     // half-blocks h (8 words, 4 k-steps): word 8h + 2j + wsel in step j, its signs in sg row 4h + j, its high index
     // bits in qh row h (nibble 2j + wsel), its scale in sc row h / 2 (nibble 4 (h % 2) + j), d in row h / 4
     // (half h / 2 % 2)
@@ -96,8 +95,12 @@ __device__ __forceinline__ void iq3m_accum(const Iq3Table &tb, int e, int row0, 
             }
         }
         float dv[4];
+        uint32_t qhl[4];                                            // the lane's high index bits, step j at bit 8j
 #pragma unroll
-        for (int r = 0; r < 4; ++r) dv[r] = f16_bits_to_f32(u4c(d_c, r) >> (16 * ((h >> 1) & 1)));
+        for (int r = 0; r < 4; ++r) {
+            dv[r] = f16_bits_to_f32(u4c(d_c, r) >> (16 * ((h >> 1) & 1)));
+            qhl[r] = u4c(qh_c, r) >> qh_sh;
+        }
         const int xo = 64 * h;                                      // dwords of the half-block's first column
         const bool more = h + 1 < h1;
 #pragma unroll
@@ -109,14 +112,14 @@ __device__ __forceinline__ void iq3m_accum(const Iq3Table &tb, int e, int row0, 
             const int sn = 4 * (4 * (h & 1) + j);                      // the scale nibble's bit offset
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const uint32_t Q = u4c(rq[j], r), S = u4c(rs[j], r), QH = u4c(qh_c, r);
-                const uint32_t s8 = (S >> (16 * wsel + 8 * half)) & 255u;
-                const uint32_t qhn = QH >> (4 * (2 * j + wsel));
-                const uint32_t i0 = ((Q >> (16 * half)) & 255u) | ((qhn << (8 - 2 * half)) & 256u);
-                const uint32_t i1 = ((Q >> (16 * half + 8)) & 255u) | ((qhn << (7 - 2 * half)) & 256u);
+                const uint32_t t = u4c(rq[j], r) >> qs_sh;              // bytes 0, 1: the two grid indices
+                const uint32_t sb = u4c(rs[j], r) >> sg_sh;             // bits 0..7: the 8 weights' signs
+                const uint32_t hb = qhl[r] >> (8 * j);                   // bits 0, 1: the indices' high bits
+                const uint32_t i0 = (t & 255u) | ((hb << 8) & 256u);
+                const uint32_t i1 = ((t >> 8) & 255u) | ((hb << 7) & 256u);
                 const uint2 g0 = L.level[i0], g1 = L.level[i1];
-                const uint4 m = L.smask[s8];
-                const uint4 b = make_uint4(g0.x | m.x, g0.y | m.y, g1.x | m.z, g1.y | m.w);
+                const uint2 m0 = L.smask[sb & 15u], m1 = L.smask[(sb >> 4) & 15u];
+                const uint4 b = make_uint4(g0.x | m0.x, g0.y | m0.y, g1.x | m1.x, g1.y | m1.y);
                 const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
                 f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ah),
                                                                   __builtin_bit_cast(bf16x8, b), zero, 0, 0, 0);
