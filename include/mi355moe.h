@@ -38,11 +38,13 @@ extern "C" {
 /* ---- formats ----------------------------------------------------------------------------------------------- */
 #define MI_QT_CB3    1   /* 3-bit codes (10 per u32) + 8 bf16 centroids per (row, 128-column group)              */
 #define MI_QT_IQ3_S  2   /* llama.cpp IQ3_S in the reference's planar tables (planes.py:22-25)                   */
+#define MI_QT_IQ4_XS 3   /* llama.cpp IQ4_XS in the reference's planar tables (planes.py:26-28)                  */
 
 /*
  * One expert table: E experts of one matrix kind (gate, up or down), every expert R rows x K inputs.  plane[] order:
  *   MI_QT_IQ3_S : {qs, sg, qh, sc, d}   -- the reference's planes, unchanged: u32 [E * rows_p, R], the matrix row
  *                                          on the minor axis (planes.py:5-14,45).  R % 64 == 0, K % 256 == 0.
+ *   MI_QT_IQ4_XS: {qs, sl, sh, d}       -- likewise (planes.py:26-28,46).  R % 64 == 0, K % 256 == 0.
  *   MI_QT_CB3   : {qs, cb}              -- qs: u32 [E][ceil(K/160)][R/16][64][4] code tiles (16 rows x 160 columns,
  *                                          1 KB each, in the lane order of the matrix-core decoder; formats.py
  *                                          cb3_tile_words gives the bit map); cb: u32 [E][K/128][R][4] = bytes

@@ -11,6 +11,7 @@ LIB_PATH = os.path.join(HERE, "libmi355moe.so")
 MI_OK = 0
 MI_QT_CB3 = 1
 MI_QT_IQ3_S = 2
+MI_QT_IQ4_XS = 3
 MI_X_BF16 = 0
 MI_X_F32 = 1
 MI_MAX_SLOTS = 128
@@ -18,10 +19,10 @@ MAX_DECODE_TOKENS = 16
 MI_COMBINE_MATMUL = 0
 MI_COMBINE_GATHER = 1
 COMBINES = {"matmul": MI_COMBINE_MATMUL, "gather": MI_COMBINE_GATHER}
-PREFILL_TM = 96              # rows per block of mi_moe_prefill's own plan
+PREFILL_TM = 80              # rows per block of mi_moe_prefill's own plan
 
-QTYPES = {"CB3": MI_QT_CB3, "IQ3_S": MI_QT_IQ3_S}
-PLANE_KEYS = {"CB3": ("qs", "cb"), "IQ3_S": ("qs", "sg", "qh", "sc", "d")}
+QTYPES = {"CB3": MI_QT_CB3, "IQ3_S": MI_QT_IQ3_S, "IQ4_XS": MI_QT_IQ4_XS}
+PLANE_KEYS = {"CB3": ("qs", "cb"), "IQ3_S": ("qs", "sg", "qh", "sc", "d"), "IQ4_XS": ("qs", "sl", "sh", "d")}
 
 # every symbol the header declares (tests check the library exports them)
 EXPORTS = ("mi_matvec", "mi_matvec_workspace", "mi_moe_decode", "mi_moe_decode_fused", "mi_moe_decode_phases",

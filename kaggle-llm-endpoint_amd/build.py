@@ -3,7 +3,7 @@
     python kaggle-llm-endpoint_amd/build.py
 
 The library is a plain C-ABI shared object (include/mi355moe.h) that the package loads with ctypes.  The grouped
-kernels are compiled once per (mode, format) from k_grouped.hip, the persistent CB3 kernels once per (mode, token
+kernels are compiled once per (mode, format: CB3, IQ3_S, IQ4_XS) from k_grouped.hip, the persistent CB3 kernels once per (mode, token
 class) from k_pstream.hip; all units compile in parallel, then link.
 """
 import os
@@ -30,7 +30,7 @@ FLAGS = [
 UNITS = [("moe_decode.hip", [], "moe_decode"), ("int8_project.hip", [], "int8_project"),
          ("prefill.hip", [], "prefill")]
 UNITS += [("k_grouped.hip", ["-DMI_KMODE=%d" % m, "-DMI_KQT=%d" % q], "k_grouped_%d_%d" % (m, q))
-          for m in (0, 1, 2) for q in (1, 2)]
+          for m in (0, 1, 2) for q in (1, 2, 3)]
 UNITS += [("k_fused.hip", [], "k_fused")]
 UNITS += [("k_pstream.hip", ["-DMI_PMODE=%d" % m, "-DMI_PTC=%d" % tc], "k_pstream_%d_%d" % (m, tc))
           for m in (0, 1) for tc in (8, 16)]

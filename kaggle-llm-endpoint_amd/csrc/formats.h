@@ -1,5 +1,5 @@
-// The reference's planar IQ3_S tables as the gfx950 kernels address them (the decoders: iq3_mfma.h for decode and
-// matvec, prefill.hip for the prefill GEMMs).
+// The reference's planar IQ3_S and IQ4_XS tables as the gfx950 kernels address them (the decoders: iq3_mfma.h and
+// iq4_mfma.h for decode and matvec, prefill.hip for the prefill GEMMs).
 #pragma once
 #include "common.h"
 
@@ -17,6 +17,15 @@ struct Iq3Table {
     const uint32_t *qs, *sg, *qh, *sc, *d;
     int R, K, nblk, W;
     static constexpr int kUnitCols = 256;   // one 256-weight block
+};
+
+// The reference's planar IQ4_XS tables (planes.py:26-28): word w = qs bytes 4w .. 4w+3 of a row; byte j holds input
+// 32 (w/4) + 4 (w%4) + j in its low nibble and that + 16 in its high nibble; per block one u32 of low scale nibbles
+// (sl), one of high scale bit pairs (sh) and, per two blocks, one u32 of f16 d.
+struct Iq4Table {
+    const uint32_t *qs, *sl, *sh, *d;
+    int R, K, nblk, W;                      // W = 32 nblk words per row
+    static constexpr int kUnitCols = 256;
 };
 
 }  // namespace mi

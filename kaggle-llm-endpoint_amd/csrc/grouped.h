@@ -5,8 +5,8 @@
 //   2. issues its first weight loads, then stages the group's activation rows for its column split in LDS while
 //      they are in flight (f32 activations -- h for the down projection -- as bf16 hi + lo parts),
 //   3. streams the expert's planes once with 128-bit loads (every wavefront load is 1 KB contiguous) and decodes
-//      the codes to bf16 in registers: CB3 tiles feed the matrix cores (64 rows per wavefront, all of the group's
-//      tokens in one 16-column tile), IQ3_S rows feed bf16-pair dot products (256 rows per wavefront),
+//      the codes to bf16 in registers for the matrix cores, all of the group's tokens in one 16-column tile: CB3
+//      tiles (16-64 rows per wavefront), IQ3_S and IQ4_XS planes (64 rows per wavefront, iq3_mfma.h, iq4_mfma.h),
 //   4. writes its f32 partial sums; the next launch reduces them in a fixed order (the SwiGLU kernel forms h from
 //      the gate/up partials, the combine kernel sums the down partials with the routing weights, the split
 //      reduction finishes a matvec).
@@ -16,13 +16,16 @@
 
 #include "cb3_tiles.h"
 #include "formats.h"
-#include "iq3_mfma.h"
+#include "iq4_mfma.h"
 
 namespace mi {
 
 // internal linkage: every translation unit that launches a kernel carries its own copy
 static __constant__ uint32_t kGridConst[512] = {
 #include "iq3s_grid.inc"
+};
+static __constant__ int8_t kKvConst[16] = {
+#include "iq4nl_kvalues.inc"
 };
 
 enum Mode { kGateUp = 0, kDown = 1, kMatvec = 2 };
@@ -31,6 +34,7 @@ struct Table {
     int qtype;
     Cb3Table cb3;
     Iq3Table iq3;
+    Iq4Table iq4;
 };
 
 struct KArgs {
@@ -151,7 +155,9 @@ template <int MODE, int QT, int TCMAX, int RTW>
 __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) grouped_kernel(KArgs a) {
     extern __shared__ uint32_t xlds[];
     __shared__ GroupScratch sc;
-    __shared__ typename std::conditional<QT == MI_QT_IQ3_S, Iq3Lds, char>::type iq;   // IQ3_S: grid and sign tables
+    // IQ3_S: grid and sign tables; IQ4_XS: the level-pair table
+    __shared__ typename std::conditional<QT == MI_QT_IQ3_S, Iq3Lds,
+                                         typename std::conditional<QT == MI_QT_IQ4_XS, Iq4Lds, char>::type>::type iq;
     __shared__ uint4 cbl[QT == MI_QT_CB3 ? kWgWaves * 5 * 64 : 1];   // CB3: per-wavefront codebook slots
     __shared__ int s_tok[kMaxT];
 
@@ -169,10 +175,12 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
     if (e < 0) return;
     const int n = __builtin_amdgcn_readfirstlane(sc.g.n);
 
-    if constexpr (!cb3) iq3_fill_lds(iq, kGridConst);     // published by the barrier after the slot list
+    // published by the barrier after the slot list
+    if constexpr (QT == MI_QT_IQ3_S) iq3_fill_lds(iq, kGridConst);
+    if constexpr (QT == MI_QT_IQ4_XS) iq4_fill_lds(iq, kKvConst);
 
     // column range of the split; CB3 stages its padded column tiles (columns >= K are zero)
-    const int ucols = cb3 ? Cb3Table::kUnitCols : Iq3Table::kUnitCols;
+    const int ucols = cb3 ? Cb3Table::kUnitCols : 256;      // IQ formats: 256-weight blocks
     const int nb = (a.n_units + a.ualign - 1) / a.ualign;
     const int u0 = min(a.n_units, a.ualign * (int)((long long)split * nb / a.S));
     const int u1 = min(a.n_units, a.ualign * (int)((long long)(split + 1) * nb / a.S));
@@ -251,8 +259,21 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
                     lv = make_uint2(l0 | (l1 << 16), l2 | (l3 << 16));
                 }
             }
-            *(uint2 *)(xh + t * xsp + 2 * q) = hv;
-            if (hilo) *(uint2 *)(xl + t * xsp + 2 * q) = lv;
+            if constexpr (QT == MI_QT_IQ4_XS) {
+                // the decoder's column order inside each 32-column group (iq4_stage_pos)
+                uint16_t *dh = (uint16_t *)(xh + t * xsp), *dl = (uint16_t *)(xl + t * xsp);
+                const int o = 4 * q, g = o & ~31, p0 = g + iq4_stage_pos(o & 31);
+                const uint32_t hw[4] = {hv.x & 0xffffu, hv.x >> 16, hv.y & 0xffffu, hv.y >> 16};
+                const uint32_t lw[4] = {lv.x & 0xffffu, lv.x >> 16, lv.y & 0xffffu, lv.y >> 16};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    dh[p0 + 2 * j] = (uint16_t)hw[j];
+                    if (hilo) dl[p0 + 2 * j] = (uint16_t)lw[j];
+                }
+            } else {
+                *(uint2 *)(xh + t * xsp + 2 * q) = hv;
+                if (hilo) *(uint2 *)(xl + t * xsp + 2 * q) = lv;
+            }
         }
         __syncthreads();
     };
@@ -274,12 +295,19 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
         else
             cb3_run_and_store<false, TCMAX, RTW>(tb.cb3, e, rg, u0, u1, c0, xh, xl, xsp, a.t_rows, n, s_tok, part_base,
                                             a.R, cbl + wave * 5 * 64, stage);
-    } else {
+    } else if constexpr (QT == MI_QT_IQ3_S) {
         if (hilo)
             iq3m_run_and_store<true, TCMAX>(tb.iq3, e, rg * WR, u0, u1, c0, iq, xh, xl, xsp, a.t_rows, n, s_tok,
                                             part_base, a.R, stage);
         else
             iq3m_run_and_store<false, TCMAX>(tb.iq3, e, rg * WR, u0, u1, c0, iq, xh, xl, xsp, a.t_rows, n, s_tok,
+                                             part_base, a.R, stage);
+    } else {
+        if (hilo)
+            iq4m_run_and_store<true, TCMAX>(tb.iq4, e, rg * WR, u0, u1, c0, iq, xh, xl, xsp, a.t_rows, n, s_tok,
+                                            part_base, a.R, stage);
+        else
+            iq4m_run_and_store<false, TCMAX>(tb.iq4, e, rg * WR, u0, u1, c0, iq, xh, xl, xsp, a.t_rows, n, s_tok,
                                              part_base, a.R, stage);
     }
     // The partials are reduced by the next launch (gate/up: the SwiGLU kernel; down: the combine; matvec: the split

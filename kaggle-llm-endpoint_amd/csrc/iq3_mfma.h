@@ -13,6 +13,8 @@
 // lane group q holds 8 weights: word 2s + q / 2, weights 8 (q % 2) .. 8 (q % 2) + 7 (two grid indices); the
 // activations are read in the same column order (natural order: column 32 s + 8 q + e).
 #pragma once
+#include <type_traits>
+
 #include "cb3_tiles.h"
 #include "formats.h"
 
@@ -140,17 +142,18 @@ __device__ __forceinline__ void iq3m_accum(const Iq3Table &tb, int e, int row0, 
     }
 }
 
-// 64 rows from row0, store the partials of the n real rows.  A-operand rows (tokens of the 16-row tile):
+// 64 rows from row0 (4 interleaved tiles, lane (i, q) holding rows 4i + r), store the partials of the n real rows.
+// A-operand rows (tokens of the 16-row tile):
 //   bf16 activations: token m;
 //   f32 activations (HILO), groups of at most 8 tokens (TCMAX <= 8): hi part of token m (m < 8) or lo part of token
 //     m - 8 (m >= 8): one instruction; the two halves of the output are added at the end;
 //   f32 activations, up to 16 tokens: hi and lo of token m, two instructions per k-step.
 // A rows at or past the staged rows read a clamped row; their outputs are never stored.
-template <bool HILO, int TCMAX, class Stage>
-__device__ __forceinline__ void iq3m_run_and_store(const Iq3Table &tb, int e, int row0, int u0, int u1, int c0,
-                                                   const Iq3Lds &L, const uint32_t *xh, const uint32_t *xl, int xsp,
-                                                   int t_rows, int n, const int *slots, float *part_base, int R,
-                                                   Stage &&stage) {
+// accum<TWO>(xa, xb, acc) runs the rows' k-steps (xa / xb: the lane's A row in the staged activations + 4 q dwords).
+template <bool HILO, int TCMAX, class Accum>
+__device__ __forceinline__ void iqm_run_and_store(int row0, const uint32_t *xh, const uint32_t *xl, int xsp,
+                                                  int t_rows, int n, const int *slots, float *part_base, int R,
+                                                  Accum &&accum) {
     const int lane = threadIdx.x & 63, m = lane & 15, q = lane >> 4;
     constexpr bool two = HILO && TCMAX > 8;
     constexpr bool pair = HILO && !two;
@@ -161,7 +164,7 @@ __device__ __forceinline__ void iq3m_run_and_store(const Iq3Table &tb, int e, in
     f32x4 acc[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) acc[r] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    iq3m_accum<two>(tb, e, row0, u0, u1, c0, L, xa, xb, acc, stage);
+    accum(std::integral_constant<bool, two>{}, xa, xb, acc);
     if (pair) {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
@@ -176,6 +179,18 @@ __device__ __forceinline__ void iq3m_run_and_store(const Iq3Table &tb, int e, in
         const int t = 4 * q + i;
         if (t < n) *(float4 *)(dst + (size_t)slots[t] * R) = make_float4(acc[0][i], acc[1][i], acc[2][i], acc[3][i]);
     }
+}
+
+template <bool HILO, int TCMAX, class Stage>
+__device__ __forceinline__ void iq3m_run_and_store(const Iq3Table &tb, int e, int row0, int u0, int u1, int c0,
+                                                   const Iq3Lds &L, const uint32_t *xh, const uint32_t *xl, int xsp,
+                                                   int t_rows, int n, const int *slots, float *part_base, int R,
+                                                   Stage &&stage) {
+    iqm_run_and_store<HILO, TCMAX>(row0, xh, xl, xsp, t_rows, n, slots, part_base, R,
+                                   [&](auto two, const uint32_t *xa, const uint32_t *xb, f32x4(&acc)[4]) {
+                                       iq3m_accum<decltype(two)::value>(tb, e, row0, u0, u1, c0, L, xa, xb, acc,
+                                                                        stage);
+                                   });
 }
 
 }  // namespace mi

@@ -1,0 +1,125 @@
+// IQ4_XS rows of the grouped decode / matvec launches on the gfx950 matrix cores.
+//
+// The reference's planar IQ4_XS tables (planes.py:26-28) are read as stored.  As for IQ3_S (iq3_mfma.h) the weights
+// are the B operand of v_mfma_f32_16x16x32_bf16 and one k-step of 32 columns is one scale group (a 32-weight
+// sub-block, scale f16(d) * (6-bit s - 32)), applied in f32 to the k-step's partial.  The B operand holds the
+// non-linear levels kvalues_iq4nl (integers |v| <= 127, exact in bf16), so every weight enters exactly as the
+// reference's f32 dequantization defines it (iqquant.py:137-148, planes.py:230-243).
+//
+// A wavefront owns 64 rows, loaded 4 rows per uint4 as four interleaved 16-row tiles (tile r = rows 4i + r of lane
+// (i, q)).  In the k-step of sub-block s, lane group q takes plane word 4s + q: byte j of it holds the weights
+// 4q + j (low nibble) and 16 + 4q + j (high nibble) of the sub-block, and one LDS table lookup per byte turns it into
+// the bf16 pair of their levels.  The lane's 8 k-values are therefore sub-block columns {4q + j, 16 + 4q + j}
+// interleaved, and the activations are staged in that order: staged position 8q + 2j + h of each 32-column group
+// holds column 16h + 4q + j (iq4_stage_pos).
+#pragma once
+#include "iq3_mfma.h"
+
+namespace mi {
+
+// LDS table: byte (two 4-bit indices) -> bf16 pair (level of the low nibble, level of the high nibble).
+struct Iq4Lds {
+    uint32_t pair[256];
+};
+
+// Every thread of the workgroup takes part; a barrier must follow before the table is read.
+__device__ __forceinline__ void iq4_fill_lds(Iq4Lds &t, const int8_t *kv) {
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) {
+        const uint32_t lo = __float_as_uint((float)kv[i & 15]) >> 16, hi = __float_as_uint((float)kv[i >> 4]) >> 16;
+        t.pair[i] = lo | (hi << 16);
+    }
+}
+
+// Staged position (bf16 units, within a 32-column group) of column o (0..31) of the group.
+__host__ __device__ __forceinline__ int iq4_stage_pos(int o) { return 8 * ((o >> 2) & 3) + 2 * (o & 3) + (o >> 4); }
+
+// Rows row0 .. row0 + 63 of expert e over blocks [u0, u1), activations staged (permuted) from column c0:
+// acc[r][i] += sum_k W[row0 + 4 (lane % 16) + r][k] * x[token 4 (lane / 16) + i][k].
+template <bool TWO, class Stage>
+__device__ __forceinline__ void iq4m_accum(const Iq4Table &tb, int e, int row0, int u0, int u1, int c0,
+                                           const Iq4Lds &L, const uint32_t *xa, const uint32_t *xb, f32x4 (&acc)[4],
+                                           Stage &&stage) {
+    const int lane = threadIdx.x & 63, q = lane >> 4;
+    const size_t R = (size_t)tb.R;
+    const uint32_t lo = (uint32_t)(row0 + 4 * (lane & 15));
+    const uint32_t *qs = tb.qs + (size_t)e * tb.W * R;
+    const uint32_t *sl = tb.sl + (size_t)e * tb.nblk * R;
+    const uint32_t *sh = tb.sh + (size_t)e * tb.nblk * R;
+    const uint32_t *dd = tb.d + (size_t)e * ((tb.nblk + 1) / 2) * R;
+    const uint4 z4 = make_uint4(0, 0, 0, 0);
+    // half-blocks h (4 sub-blocks): the lane's word in sub-block 4 (h % 2) + j of block h / 2 is 16 h + 4 j + q
+    const int h0 = 2 * u0, h1 = 2 * u1;
+    uint4 ring[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ring[j] = ldl(qs + (size_t)(16 * h0 + 4 * j + q) * R, lo);
+    uint4 sl_c = ldl(sl + (size_t)u0 * R, lo), sh_c = ldl(sh + (size_t)u0 * R, lo);
+    uint4 sl_n = u0 + 1 < u1 ? ldl(sl + (size_t)(u0 + 1) * R, lo) : z4;
+    uint4 sh_n = u0 + 1 < u1 ? ldl(sh + (size_t)(u0 + 1) * R, lo) : z4;
+    uint4 d_c = ldl(dd + (size_t)(u0 >> 1) * R, lo);
+    uint4 d_n = (u0 & ~1) + 2 < u1 ? ldl(dd + (size_t)((u0 >> 1) + 1) * R, lo) : z4;
+    stage();
+    const uint32_t *xa0 = xa - (c0 >> 1), *xb0 = xb - (c0 >> 1);
+    for (int h = h0; h < h1; ++h) {
+        const int b = h >> 1;
+        if (h > h0 && (h & 1) == 0) {                               // a new block: its scales (and d)
+            sl_c = sl_n;
+            sh_c = sh_n;
+            sl_n = b + 1 < u1 ? ldl(sl + (size_t)(b + 1) * R, lo) : z4;
+            sh_n = b + 1 < u1 ? ldl(sh + (size_t)(b + 1) * R, lo) : z4;
+            if ((b & 1) == 0) {
+                d_c = d_n;
+                d_n = b + 2 < u1 ? ldl(dd + (size_t)((b >> 1) + 1) * R, lo) : z4;
+            }
+        }
+        float dv[4], m32[4];
+        uint32_t scw[4];                                            // sub-block i's 6-bit scale at bits 8i
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            dv[r] = f16_bits_to_f32(u4c(d_c, r) >> (16 * (b & 1)));
+            m32[r] = -32.0f * dv[r];
+            const uint32_t l = u4c(sl_c, r) >> (16 * (h & 1)), hb = u4c(sh_c, r) >> (8 * (h & 1));
+            scw[r] = (l & 15u) | ((l & 0xf0u) << 4) | ((l & 0xf00u) << 8) | ((l & 0xf000u) << 12) |
+                     ((hb & 3u) << 4) | ((hb & 0xcu) << 10) | ((hb & 0x30u) << 16) | ((hb & 0xc0u) << 22);
+        }
+        const int xo = 64 * h;                                      // dwords of the half-block's first column
+        const bool more = h + 1 < h1;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            __builtin_amdgcn_sched_barrier(0);
+            const uint4 ah = *(const uint4 *)(xa0 + xo + 16 * j);
+            uint4 al = ah;
+            if (TWO) al = *(const uint4 *)(xb0 + xo + 16 * j);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t u = u4c(ring[j], r);
+                const uint4 bw = make_uint4(L.pair[u & 255u], L.pair[(u >> 8) & 255u], L.pair[(u >> 16) & 255u],
+                                            L.pair[u >> 24]);
+                const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+                f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ah),
+                                                                  __builtin_bit_cast(bf16x8, bw), zero, 0, 0, 0);
+                if (TWO)
+                    p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, al),
+                                                                __builtin_bit_cast(bf16x8, bw), p, 0, 0, 0);
+                const float scale = fmaf((float)((scw[r] >> (8 * j)) & 63u), dv[r], m32[r]);   // d (s - 32), exact
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[r][i] = fmaf(scale, p[i], acc[r][i]);
+            }
+            // the ring slot takes step j of the next half-block
+            if (more) ring[j] = ldl(qs + (size_t)(16 * (h + 1) + 4 * j + q) * R, lo);
+        }
+    }
+}
+
+template <bool HILO, int TCMAX, class Stage>
+__device__ __forceinline__ void iq4m_run_and_store(const Iq4Table &tb, int e, int row0, int u0, int u1, int c0,
+                                                   const Iq4Lds &L, const uint32_t *xh, const uint32_t *xl, int xsp,
+                                                   int t_rows, int n, const int *slots, float *part_base, int R,
+                                                   Stage &&stage) {
+    iqm_run_and_store<HILO, TCMAX>(row0, xh, xl, xsp, t_rows, n, slots, part_base, R,
+                                   [&](auto two, const uint32_t *xa, const uint32_t *xb, f32x4(&acc)[4]) {
+                                       iq4m_accum<decltype(two)::value>(tb, e, row0, u0, u1, c0, L, xa, xb, acc,
+                                                                        stage);
+                                   });
+}
+
+}  // namespace mi

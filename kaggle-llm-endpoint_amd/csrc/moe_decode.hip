@@ -10,8 +10,8 @@ namespace mi {
 // ------------------------------------------------------------------------------------------------ dequant (debug)
 __global__ void dequant_kernel(Table tb, int e, float *out) {
     // one thread per (row, 16 columns); writes the exact f32 weights in natural order
-    const int R = tb.qtype == MI_QT_CB3 ? tb.cb3.R : tb.iq3.R;
-    const int K = tb.qtype == MI_QT_CB3 ? tb.cb3.K : tb.iq3.K;
+    const int R = tb.qtype == MI_QT_CB3 ? tb.cb3.R : tb.qtype == MI_QT_IQ3_S ? tb.iq3.R : tb.iq4.R;
+    const int K = tb.qtype == MI_QT_CB3 ? tb.cb3.K : tb.qtype == MI_QT_IQ3_S ? tb.iq3.K : tb.iq4.K;
     const int per_row = K / 16;
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (long long)R * per_row) return;
@@ -39,6 +39,17 @@ __global__ void dequant_kernel(Table tb, int e, float *out) {
             const uint32_t lo = cw[code >> 2], hi = cw[2 + (code >> 2)];
             const uint32_t sh = 8 * (code & 3u);
             v = bf16_to_f32(((lo >> sh) & 255u) | (((hi >> sh) & 255u) << 8));
+        } else if (tb.qtype == MI_QT_IQ4_XS) {
+            // column c: block b, sub-block i, word 4i + wq, byte j, nibble pos (c = 256 b + 32 i + 16 pos + 4 wq + j)
+            const Iq4Table &t = tb.iq4;
+            const int b = c >> 8, i = (c >> 5) & 7, pos = (c >> 4) & 1, wq = (c >> 2) & 3, j = c & 3;
+            const uint32_t q = t.qs[((size_t)e * t.W + 32 * b + 4 * i + wq) * Rz + r];
+            const uint32_t slw = t.sl[((size_t)e * t.nblk + b) * Rz + r];
+            const uint32_t shw = t.sh[((size_t)e * t.nblk + b) * Rz + r];
+            const uint32_t dw = t.d[((size_t)e * ((t.nblk + 1) / 2) + (b >> 1)) * Rz + r];
+            const int sv = (int)(((slw >> (4 * i)) & 15u) | (((shw >> (2 * i)) & 3u) << 4)) - 32;
+            const uint32_t nib = (q >> (8 * j + 4 * pos)) & 15u;
+            v = f16_bits_to_f32(dw >> (16 * (b & 1))) * (float)sv * (float)kKvConst[nib];
         } else {
             const Iq3Table &t = tb.iq3;
             const int w = c >> 4, jj = (c >> 2) & 3, kk = c & 3;
@@ -171,7 +182,7 @@ __global__ void split_reduce_kernel(const float *__restrict__ part, int S, int N
 // ------------------------------------------------------------------------------------------------ host side
 static int validate_table(const mi_table *t) {
     if (!t) return MI_ERR_NULL;
-    if (t->qtype != MI_QT_CB3 && t->qtype != MI_QT_IQ3_S) return MI_ERR_QTYPE;
+    if (t->qtype != MI_QT_CB3 && t->qtype != MI_QT_IQ3_S && t->qtype != MI_QT_IQ4_XS) return MI_ERR_QTYPE;
     if (t->rows <= 0 || t->rows % (t->qtype == MI_QT_CB3 ? kCb3RowAlign : kIq3WaveRows)) return MI_ERR_SHAPE;
     if (t->n_experts <= 0 || t->n_experts > kMaxExperts) return MI_ERR_SHAPE;
     if (t->qtype == MI_QT_CB3) {
@@ -179,7 +190,7 @@ static int validate_table(const mi_table *t) {
         if (!t->plane[0] || !t->plane[1]) return MI_ERR_NULL;
     } else {
         if (t->cols <= 0 || t->cols % 256) return MI_ERR_SHAPE;
-        for (int i = 0; i < 5; ++i)
+        for (int i = 0; i < (t->qtype == MI_QT_IQ3_S ? 5 : 4); ++i)
             if (!t->plane[i]) return MI_ERR_NULL;
     }
     return MI_OK;
@@ -196,6 +207,15 @@ static Table make_table(const mi_table *t) {
         tb.cb3.CT = (t->cols + kCb3TileCols - 1) / kCb3TileCols;
         tb.cb3.RT = t->rows / 16;
         tb.cb3.G = t->cols / 128;
+    } else if (t->qtype == MI_QT_IQ4_XS) {
+        tb.iq4.qs = t->plane[0];
+        tb.iq4.sl = t->plane[1];
+        tb.iq4.sh = t->plane[2];
+        tb.iq4.d = t->plane[3];
+        tb.iq4.R = t->rows;
+        tb.iq4.K = t->cols;
+        tb.iq4.nblk = t->cols / 256;
+        tb.iq4.W = 32 * (t->cols / 256);
     } else {
         tb.iq3.qs = t->plane[0];
         tb.iq3.sg = t->plane[1];
@@ -213,9 +233,9 @@ static Table make_table(const mi_table *t) {
 static int cb3_ct(const mi_table *t) { return (t->cols + kCb3TileCols - 1) / kCb3TileCols; }
 static int n_units_of(const mi_table *t) {
     if (t->qtype == MI_QT_CB3) return cb3_ct(t);                 // 160-column tiles
-    return t->cols / 256;                                        // IQ3_S blocks
+    return t->cols / 256;                                        // IQ3_S / IQ4_XS blocks
 }
-// Rows per wavefront: CB3 16 rtw (rtw row tiles), IQ3_S 64 (four interleaved row tiles).
+// Rows per wavefront: CB3 16 rtw (rtw row tiles), IQ3_S / IQ4_XS 64 (four interleaved row tiles).
 static int wave_rows_of(const mi_table *t, int rtw) { return t->qtype == MI_QT_CB3 ? 16 * rtw : kIq3WaveRows; }
 static int unit_cols(const mi_table *t) { return t->qtype == MI_QT_CB3 ? kCb3TileCols : 256; }
 
@@ -282,17 +302,20 @@ static int cu_count() {
 #define MI_DECL_OCC(M, Q) int occupancy_grouped_##M##_##Q(int tcmax, int rtw, size_t lds);
 MI_DECL_OCC(0, 1)
 MI_DECL_OCC(0, 2)
+MI_DECL_OCC(0, 3)
 MI_DECL_OCC(1, 1)
 MI_DECL_OCC(1, 2)
+MI_DECL_OCC(1, 3)
 MI_DECL_OCC(2, 1)
 MI_DECL_OCC(2, 2)
+MI_DECL_OCC(2, 3)
 #undef MI_DECL_OCC
 
 // Resident workgroups per CU of a grouped-kernel launch (the runtime's occupancy for that instance and LDS size;
 // 2 when it cannot be queried), cached per (mode, format, token class, rows per wavefront, 512-byte LDS bucket).
 static int wgs_per_cu(int mode, int qtype, int tcmax, int rtw, size_t lds) {
-    static int cache[3][2][5][3][161];
-    const int qi = qtype == MI_QT_CB3 ? 0 : 1;
+    static int cache[3][3][5][3][161];
+    const int qi = qtype - 1;                                   // MI_QT_CB3, MI_QT_IQ3_S, MI_QT_IQ4_XS
     int ti = 0, ri = rtw == 4 ? 2 : rtw - 1;
     while ((1 << ti) < tcmax && ti < 4) ++ti;
     const size_t bucket = (lds + 511) / 512;
@@ -300,9 +323,11 @@ static int wgs_per_cu(int mode, int qtype, int tcmax, int rtw, size_t lds) {
     if (slot && *slot > 0) return *slot;
     const size_t l = bucket * 512;
     int n;
-    if (mode == kGateUp) n = (qi ? occupancy_grouped_0_2 : occupancy_grouped_0_1)(tcmax, rtw, l);
-    else if (mode == kDown) n = (qi ? occupancy_grouped_1_2 : occupancy_grouped_1_1)(tcmax, rtw, l);
-    else n = (qi ? occupancy_grouped_2_2 : occupancy_grouped_2_1)(tcmax, rtw, l);
+    typedef int (*Occ)(int, int, size_t);
+    static const Occ occ[3][3] = {{occupancy_grouped_0_1, occupancy_grouped_0_2, occupancy_grouped_0_3},
+                                  {occupancy_grouped_1_1, occupancy_grouped_1_2, occupancy_grouped_1_3},
+                                  {occupancy_grouped_2_1, occupancy_grouped_2_2, occupancy_grouped_2_3}};
+    n = occ[mode][qi](tcmax, rtw, l);
     if (n <= 0) n = 2;
     if (slot) *slot = n;
     return n;
@@ -338,9 +363,9 @@ static Shape choose_shape(const mi_table *t, int mode, int tcmax, int groups, in
         if (forced_rtw > 0 && cb3 && rtw != forced_rtw) continue;
         const int RB = t->rows / wave_rows_of(t, rtw);
         const int RBG = (RB + rg_per_wg - 1) / rg_per_wg;
-        // kilobytes a wavefront streams per unit: CB3 one 1 KB code tile per row tile + codebook; IQ3_S 64 rows of
-        // a 110-byte block
-        const double kb_per_unit = cb3 ? rtw * 1.25 : 64 * 110 / 1024.0;
+        // kilobytes a wavefront streams per unit: CB3 one 1 KB code tile per row tile + codebook; IQ3_S / IQ4_XS 64
+        // rows of a 110 / 136-byte block
+        const double kb_per_unit = cb3 ? rtw * 1.25 : 64 * (t->qtype == MI_QT_IQ3_S ? 110 : 136) / 1024.0;
         const int aligns[2] = {cb3 ? 4 : 1, 1};
         for (int ai = 0; ai < 2; ++ai) {
             const int align = aligns[ai];
@@ -430,7 +455,8 @@ static DecodePlan plan_decode(const mi_table *gate, const mi_table *down, int N,
     p.NS = n_route + (shared >= 0 ? N : 0);
     int est = N == 1 ? p.G : (p.G * 6 + 5) / 10;
     if (est < 1) est = 1;
-    p.persistent = gate->qtype == MI_QT_CB3 && N > env_int("MI355MOE_PERSIST_ABOVE", kPersistentMinTokens);
+    p.persistent = gate->qtype == MI_QT_CB3 && down->qtype == MI_QT_CB3 &&
+                   N > env_int("MI355MOE_PERSIST_ABOVE", kPersistentMinTokens);
     if (p.persistent) {
         // persistent launches: tasks are pipelined, so the per-task fixed cost is small
         const long long slots = 3LL * cu_count();
@@ -497,7 +523,7 @@ struct FusedPlan {
 // Environment overrides (experiments): MI355MOE_FS1[_AL|_RTW], MI355MOE_FS2[_AL] as for choose_shape.
 static FusedPlan plan_fused(const mi_table *gate, const mi_table *down, int N, int k, int shared) {
     FusedPlan p{};
-    if (gate->qtype != MI_QT_CB3 || N > kFusedMaxTokens) return p;
+    if (gate->qtype != MI_QT_CB3 || down->qtype != MI_QT_CB3 || N > kFusedMaxTokens) return p;
     const int n_route = N * k;
     p.rows = class_rows(N);
     p.G = max_groups(n_route, gate->n_experts, N, shared, p.rows);
@@ -546,19 +572,22 @@ static int launch_status() {
     void launch_grouped_##M##_##Q(int tcmax, int rtw, dim3 grid, dim3 block, size_t lds, hipStream_t s, const KArgs &a);
 MI_DECL_LAUNCH(0, 1)
 MI_DECL_LAUNCH(0, 2)
+MI_DECL_LAUNCH(0, 3)
 MI_DECL_LAUNCH(1, 1)
 MI_DECL_LAUNCH(1, 2)
+MI_DECL_LAUNCH(1, 3)
 MI_DECL_LAUNCH(2, 1)
 MI_DECL_LAUNCH(2, 2)
+MI_DECL_LAUNCH(2, 3)
 #undef MI_DECL_LAUNCH
 
 template <int MODE>
 static void launch_grouped(int qtype, int tcmax, int rtw, dim3 grid, size_t lds, hipStream_t s, const KArgs &a) {
-    const bool cb3 = qtype == MI_QT_CB3;
-    const dim3 block(64 * kWgWaves);
-    if (MODE == kGateUp) (cb3 ? launch_grouped_0_1 : launch_grouped_0_2)(tcmax, rtw, grid, block, lds, s, a);
-    else if (MODE == kDown) (cb3 ? launch_grouped_1_1 : launch_grouped_1_2)(tcmax, rtw, grid, block, lds, s, a);
-    else (cb3 ? launch_grouped_2_1 : launch_grouped_2_2)(tcmax, rtw, grid, block, lds, s, a);
+    typedef void (*Launch)(int, int, dim3, dim3, size_t, hipStream_t, const KArgs &);
+    static const Launch fn[3][3] = {{launch_grouped_0_1, launch_grouped_0_2, launch_grouped_0_3},
+                                    {launch_grouped_1_1, launch_grouped_1_2, launch_grouped_1_3},
+                                    {launch_grouped_2_1, launch_grouped_2_2, launch_grouped_2_3}};
+    fn[MODE][qtype - 1](tcmax, rtw, grid, dim3(64 * kWgWaves), lds, s, a);
 }
 
 }  // namespace mi
@@ -588,8 +617,7 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
     if (up->qtype != gate->qtype || up->rows != gate->rows || up->cols != gate->cols ||
         up->n_experts != gate->n_experts)
         return MI_ERR_MISMATCH;
-    if (down->qtype != gate->qtype || down->cols != gate->rows || down->n_experts != gate->n_experts)
-        return MI_ERR_MISMATCH;
+    if (down->cols != gate->rows || down->n_experts != gate->n_experts) return MI_ERR_MISMATCH;
     if (N <= 0 || N > kMaxT || k <= 0 || N * k > MI_MAX_SLOTS) return MI_ERR_TOKENS;
     if (shared_expert >= gate->n_experts || shared_expert < -1) return MI_ERR_ARG;
     if (!(limit > 0.0f)) return MI_ERR_ARG;

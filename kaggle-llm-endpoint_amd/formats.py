@@ -1,6 +1,6 @@
 """Host-side packers that turn stored weights into the device tables the HIP kernels read (load-time work, NumPy).
 
-* IQ3_S: GGUF blocks -> the reference's planar tables, unchanged (planes.py:136-170); the kernels read those
+* IQ3_S, IQ4_XS: GGUF blocks -> the reference's planar tables, unchanged (planes.py:136-170); the kernels read those
   planes directly, so tables packed by the reference's own ``pack_planes`` drop in as they are.
 * CB3 (the benchmark's 3-bit codebook format): canonical rows (10 codes per u32, 8 bf16 centroids per 128-column
   group) -> 16-row x 160-column code tiles in the lane order of the matrix-core kernels (cb3_tile_words) and a
@@ -50,6 +50,36 @@ def iq3s_pack_planes(blocks):
 
 def iq3s_hbm_bytes(R, K):
     return R * (K // QK) * IQ3S_BLOCK_BYTES
+
+
+# ------------------------------------------------------------------------------------------------ IQ4_XS
+IQ4XS_BLOCK_BYTES = 136
+
+
+def iq4xs_plane_rows(nblk):
+    """rows_p per expert (planes.py:64-65)."""
+    return {"qs": 32 * nblk, "sl": nblk, "sh": nblk, "d": (nblk + 1) // 2}
+
+
+def iq4xs_pack_planes(blocks):
+    """uint8 [E, R, nblk, 136] GGUF IQ4_XS blocks -> {plane: u32 [E*rows_p, R]} in the reference's planar layout
+    (field split of planes.py:161-163: d | sh (zero-extended to 32 bits) | sl | qs)."""
+    blocks = np.asarray(blocks, dtype=np.uint8)
+    E, R, nblk, bb = blocks.shape
+    if bb != IQ4XS_BLOCK_BYTES:
+        raise ValueError("IQ4_XS blocks are %d bytes, got %d" % (IQ4XS_BLOCK_BYTES, bb))
+    d = blocks[..., 0:2].reshape(E, R, 2 * nblk)
+    if nblk % 2:
+        d = np.concatenate([d, np.zeros((E, R, 2), np.uint8)], axis=-1)
+    sh = np.concatenate([blocks[..., 2:4], np.zeros((E, R, nblk, 2), np.uint8)], axis=-1)
+    raw = {"qs": blocks[..., 8:136], "sl": blocks[..., 4:8], "sh": sh}
+    out = {k: _expert_major(_le_words(v)) for k, v in raw.items()}
+    out["d"] = _expert_major(np.ascontiguousarray(d).view("<u4"))
+    return {k: out[k] for k in ("qs", "sl", "sh", "d")}
+
+
+def iq4xs_hbm_bytes(R, K):
+    return R * (K // QK) * IQ4XS_BLOCK_BYTES
 
 
 # ------------------------------------------------------------------------------------------------ CB3

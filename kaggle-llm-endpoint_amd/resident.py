@@ -20,11 +20,13 @@ QK = 256
 
 
 def _plane_rows(qtype, K):
-    """IQ3_S: rows_p per expert of each plane [E*rows_p, R] (planes.py:62-63)."""
+    """IQ3_S / IQ4_XS: rows_p per expert of each plane [E*rows_p, R] (planes.py:56-70)."""
+    nblk = K // QK
     if qtype == "IQ3_S":
-        nblk = K // QK
         W = 16 * nblk
         return {"qs": W, "sg": W // 2, "qh": W // 8, "sc": W // 16, "d": (nblk + 1) // 2}
+    if qtype == "IQ4_XS":
+        return {"qs": 32 * nblk, "sl": nblk, "sh": nblk, "d": (nblk + 1) // 2}
     raise ValueError(qtype)                     # the reference raises ValueError on an unknown qtype (planes.py:70)
 
 
@@ -130,6 +132,22 @@ def random_iq3s_table(E, R, K, generator, scale=0.02):
     bits = d.to(torch.float16).view(torch.int16).to(torch.int32) & 0xFFFF
     planes["d"] = (bits[..., 0] | (bits[..., 1] << 16)).contiguous()
     return ExpertTable("IQ3_S", planes, R, K)
+
+
+def random_iq4xs_table(E, R, K, generator, scale=0.02):
+    """An ExpertTable of E random IQ4_XS experts in the reference's planes, generated on the GPU: uniform random qs, sl
+    and sh words (every bit pattern is a valid set of indices and scales) and per-block f16 d uniform in
+    [scale / 2, scale].  For benchmarks at full shape."""
+    rp = _plane_rows("IQ4_XS", K)
+    planes = {}
+    for k in ("qs", "sl", "sh"):
+        planes[k] = torch.randint(-2 ** 31, 2 ** 31 - 1, (E * rp[k], R), dtype=torch.int32, device="cuda",
+                                  generator=generator)
+    planes["sh"] &= 0xFFFF                     # 16 bits of high scale pairs per block (zero-extended)
+    d = torch.rand((E * rp["d"], R, 2), device="cuda", generator=generator) * (0.5 * scale) + 0.5 * scale
+    bits = d.to(torch.float16).view(torch.int16).to(torch.int32) & 0xFFFF
+    planes["d"] = (bits[..., 0] | (bits[..., 1] << 16)).contiguous()
+    return ExpertTable("IQ4_XS", planes, R, K)
 
 
 class _Workspaces:

@@ -9,9 +9,11 @@ from .bf16 import round_bf16
 
 
 def silu(z):
-    """z * sigmoid(z) (model.py:114-115), evaluated in f64."""
+    """z * sigmoid(z) (model.py:114-115), evaluated in f64 (exp(-z) overflowing to inf for very negative z gives the
+    correct limit -0)."""
     z = np.asarray(z, dtype=np.float64)
-    return z / (1.0 + np.exp(-z))
+    with np.errstate(over="ignore"):
+        return z / (1.0 + np.exp(-z))
 
 
 def swiglu_clamped(g, u, limit):

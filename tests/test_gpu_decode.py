@@ -1,4 +1,4 @@
-"""GPU parity of the fused codebook-dequant kernels against the CPU oracle (both 3-bit formats).
+"""GPU parity of the fused codebook-dequant kernels against the CPU oracle (CB3, IQ3_S and IQ4_XS tables).
 
 Bar: dequantized weights bit-exact; matvec / decode outputs within rel-L2 <= 1e-3 of the f64 oracle (the
 reference computes f32 end to end in decode, resident.py:114-120; the kernels reach ~1e-6 -- 1e-3 is the
@@ -22,7 +22,8 @@ def _t(a, dtype=None):
 
 
 @pytest.mark.parametrize("qtype,R,K", [("CB3", 256, 1280), ("CB3", 512, 2048), ("CB3", 256, 384),
-                                       ("IQ3_S", 256, 512), ("IQ3_S", 512, 2048)])
+                                       ("IQ3_S", 256, 512), ("IQ3_S", 512, 2048), ("IQ4_XS", 256, 512),
+                                       ("IQ4_XS", 512, 2048)])
 def test_dequant_bit_exact(pkg, gpu, qtype, R, K):
     rng = np.random.default_rng(11)
     L = Layer(rng, qtype, 3, K, R)                  # gate is R x K
@@ -50,7 +51,24 @@ def test_dequant_real_gguf_iq3s(pkg, gpu):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
-@pytest.mark.parametrize("qtype", ["CB3", "IQ3_S"])
+def test_dequant_real_gguf_iq4xs(pkg, gpu):
+    """The reference's real IQ4_XS sample (blk.11.ffn_down_exps) tiled to 256 rows."""
+    import json
+    import os
+    from oracle import iq4xs as oiq4
+    d = os.path.join(os.path.dirname(__file__), "golden", "gguf")
+    s = json.load(open(os.path.join(d, "gguf_samples.json")))["IQ4_XS"]
+    raw = np.fromfile(os.path.join(d, s["file"]), np.uint8).reshape(s["rows"], s["ne0"] // 256, 136)
+    reps = -(-256 // s["rows"])
+    blocks = np.tile(raw, (reps, 1, 1))[:256][None]
+    planes = pkg.to_device_planes(pkg.formats.iq4xs_pack_planes(blocks))
+    tb = pkg.ExpertTable("IQ4_XS", planes, 256, s["ne0"])
+    got = pkg.dequant(tb, 0).cpu().numpy()
+    want = oiq4.dequant_blocks(blocks[0]).reshape(256, s["ne0"])
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("qtype", ["CB3", "IQ3_S", "IQ4_XS"])
 @pytest.mark.parametrize("xdt", ["bf16", "f32"])
 def test_matvec_grouped(pkg, gpu, qtype, xdt):
     """moe_matvec semantics (pallas_moe.py:238-307): per-slot outputs, duplicate experts, an out-of-range id."""
@@ -69,7 +87,7 @@ def test_matvec_grouped(pkg, gpu, qtype, xdt):
     assert rel_l2(got, want) < 1e-5
 
 
-@pytest.mark.parametrize("qtype", ["CB3", "IQ3_S"])
+@pytest.mark.parametrize("qtype", ["CB3", "IQ3_S", "IQ4_XS"])
 @pytest.mark.parametrize("N,k,E,routing", [(1, 8, 16, "softmax"), (4, 4, 12, "zipf"), (8, 8, 20, "zipf"),
                                            (16, 8, 24, "zipf"), (3, 2, 2, "zipf")])
 def test_decode_small(pkg, gpu, qtype, N, k, E, routing):
@@ -123,3 +141,19 @@ def test_resident_fetch_apply(pkg, gpu):
     y = fetch.apply(p, _t(x, torch.bfloat16), _t(idx), _t(w), 0, limit)
     assert y.dtype == torch.float32 and tuple(y.shape) == (N, D)
     assert rel_l2(y.cpu().numpy(), omoe.decode_apply(L.deq, x, idx, w, limit)) < 1e-5
+
+
+@pytest.mark.parametrize("qtype,down_qtype", [("IQ3_S", "IQ4_XS"), ("CB3", "IQ3_S"), ("IQ4_XS", "CB3")])
+@pytest.mark.parametrize("N", [1, 8, 16])
+def test_decode_mixed_formats(pkg, gpu, qtype, down_qtype, N):
+    """Gate/up in one format and down in another (the reference's layers mix formats per matrix kind)."""
+    rng = np.random.default_rng(300 + N)
+    E, D, I, k, limit = 10, 512, 256, 8, 10.0
+    L = Layer(rng, qtype, E + 1, D, I, down_qtype=down_qtype)
+    tbs = L.tables(pkg)
+    idx, w = zipf_routing(rng, N, E, k)
+    x = round_bf16(rng.standard_normal((N, D)).astype(np.float32))
+    of, _ = pkg.moe_decode(tbs["gate"], tbs["up"], tbs["down"], _t(x, torch.bfloat16), _t(idx), _t(w), limit,
+                           shared_expert=E)
+    want = omoe.decode_apply(L.deq, x, idx, w, limit) + omoe.shared_apply(lambda m: L.deq(m, E), x, limit)
+    assert rel_l2(of.cpu().numpy(), want) < 1e-5

@@ -1,35 +1,44 @@
-"""Test helpers: seeded expert tables in both 3-bit formats, their device planes and the oracle's view of them."""
+"""Test helpers: seeded expert tables in every format (CB3, IQ3_S, IQ4_XS), their device planes and the oracle's
+view of them."""
 import numpy as np
 
-from oracle import cb3 as ocb3, iq3s as oiq3
+from oracle import cb3 as ocb3, iq3s as oiq3, iq4xs as oiq4
 
 MATS = ("gate", "up", "down")
 
 
 class Layer:
-    """E experts x {gate, up, down} in one format; ``deq(name, e)`` is the oracle's exact f32 [R, K]."""
+    """E experts x {gate, up, down}; gate/up in ``qtype``, down in ``down_qtype`` (default: the same).  ``deq(name,
+    e)`` is the oracle's exact f32 [R, K]."""
 
-    def __init__(self, rng, qtype, E, D, I, scale=0.02):
+    def __init__(self, rng, qtype, E, D, I, scale=0.02, down_qtype=None):
         self.qtype, self.E, self.D, self.I = qtype, E, D, I
+        self.qtypes = {"gate": qtype, "up": qtype, "down": down_qtype or qtype}
         self.shapes = {"gate": (I, D), "up": (I, D), "down": (D, I)}
         self.raw = {}
         for name, (R, K) in self.shapes.items():
-            if qtype == "CB3":
+            qt = self.qtypes[name]
+            if qt == "CB3":
                 codes, cb = zip(*[ocb3.generate(rng, R, K) for _ in range(E)])
                 self.raw[name] = (np.stack(codes), np.stack(cb))
-            else:
+            elif qt == "IQ3_S":
                 self.raw[name] = oiq3.random_blocks(rng, E, R, K // 256, scale=scale)
+            else:
+                self.raw[name] = oiq4.random_blocks(rng, E, R, K // 256, scale=scale)
         self._cache = {}
 
     def deq(self, name, e):
         key = (name, e)
         if key not in self._cache:
-            if self.qtype == "CB3":
+            qt = self.qtypes[name]
+            R, K = self.shapes[name]
+            if qt == "CB3":
                 codes, cb = self.raw[name]
                 w = ocb3.dequant(codes[e], cb[e])
-            else:
-                R, K = self.shapes[name]
+            elif qt == "IQ3_S":
                 w = oiq3.dequant_blocks(self.raw[name][e]).reshape(R, K)
+            else:
+                w = oiq4.dequant_blocks(self.raw[name][e]).reshape(R, K)
             if len(self._cache) > 64:
                 self._cache.clear()
             self._cache[key] = w
@@ -37,18 +46,21 @@ class Layer:
 
     def planes(self, name, fm):
         R, K = self.shapes[name]
-        if self.qtype == "CB3":
+        qt = self.qtypes[name]
+        if qt == "CB3":
             codes, cb = self.raw[name]
             words = np.stack([ocb3.pack_canonical(c) for c in codes])
             return fm.cb3_pack_planes(words, cb, K)
-        return fm.iq3s_pack_planes(self.raw[name])
+        if qt == "IQ3_S":
+            return fm.iq3s_pack_planes(self.raw[name])
+        return fm.iq4xs_pack_planes(self.raw[name])
 
     def tables(self, pkg, device="cuda"):
         out = {}
         for name in MATS:
             R, K = self.shapes[name]
-            out[name] = pkg.ExpertTable(self.qtype, pkg.to_device_planes(self.planes(name, pkg.formats), device),
-                                        R, K)
+            out[name] = pkg.ExpertTable(self.qtypes[name], pkg.to_device_planes(self.planes(name, pkg.formats),
+                                                                                device), R, K)
         return out
 
 
