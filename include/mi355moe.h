@@ -154,18 +154,19 @@ int mi_ragged_plan(const int32_t *idx, const float *w, int32_t T, int32_t k, int
                    void *stream);
 
 /*
- * Fused MoE prefill layer (ResidentFetch._apply_ragged_kernel, resident.py:144-165) for CB3 or IQ3_S tables (one
- * format for all three), grouped GEMMs on the matrix cores:
+ * Fused MoE prefill layer (ResidentFetch._apply_ragged_kernel, resident.py:144-165) for CB3, IQ3_S or IQ4_XS tables
+ * (gate and up in one format, down in the same or another), grouped GEMMs on the matrix cores:
  *   plan   = ragged_plan over the T*k slots (+ one shared-expert column of weight 1 if shared_expert >= 0), tm = 80
- *   W      = bf16(dequantized weight): CB3 centroids as stored; IQ3_S bf16(level * f16(d) * (1 + 2 sc)), rounded
- *            once to nearest even as the reference's tiles are (pallas_moe.py:341-350)
+ *   W      = bf16(dequantized weight): CB3 centroids as stored; IQ3_S bf16(level * f16(d) * (1 + 2 sc)); IQ4_XS
+ *            bf16(kvalue * f16(d) * (s - 32)), rounded once to nearest even as the reference's tiles are
+ *            (pallas_moe.py:341-350)
  *   h[row] = bf16(silu(min(g, L)) * clip(u, -L, L)),  g, u = Wgate_e x_t, Wup_e x_t in f32   (pallas_moe.py:622-690)
  *   y[row] = bf16(Wdown_e h[row]), f32 accumulation                                           (pallas_moe.py:693-755)
  *   out[t] = sum_j wt(t, j) y[row_slot(t, j)] in f32, wt = bf16(w[t, j]) for MI_COMBINE_MATMUL (resident.py:161-163)
  *            or w[t, j] for MI_COMBINE_GATHER (resident.py:164-165); the shared column has weight 1.
  * x bf16 [T, D], idx int32 [T, k], w f32 [T, k]; out_f32 and/or out_bf16 [T, D].  Every expert's weights are read
- * once per block of 80 rows.  T*(k+1) <= 2^22, E <= 1024, gate.rows % 128 == 0, down.rows % 256 == 0; IQ3_S also
- * needs cols % 256 == 0.  MI_ERR_MISMATCH when the three tables' formats differ.
+ * once per block of 80 rows.  T*(k+1) <= 2^22, E <= 1024, gate.rows % 128 == 0, down.rows % 256 == 0; IQ3_S and
+ * IQ4_XS also need cols % 256 == 0.  MI_ERR_MISMATCH when gate and up differ in format or shape.
  * Four launches: plan, gate/up, down, combine.  The workspace (mi_moe_prefill_workspace bytes) holds the plan, h and
  * y; it needs no initialisation.
  */

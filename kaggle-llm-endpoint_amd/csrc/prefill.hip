@@ -1,4 +1,4 @@
-// Grouped prefill for CB3 and IQ3_S experts on the gfx950 matrix cores (the reference's ragged prefill,
+// Grouped prefill for CB3, IQ3_S and IQ4_XS experts on the gfx950 matrix cores (the reference's ragged prefill,
 // resident.py:144-165 with pallas_moe.py:564-592,622-755):
 //   ragged_plan_kernel  the reference's slot layout (pallas_moe.py:564-592) built on the device by one workgroup:
 //                       slots stably sorted by expert, every expert padded to whole blocks of tm rows;
@@ -11,9 +11,11 @@
 //                         down:    y = bf16(h Wd^T), f32 accumulation                        (pallas_moe.py:747)
 //   prefill_combine     out[t] = sum_j wt(t, j) * y[row_slot(t, j)] in f32 with wt = bf16(w) ("matmul" combine,
 //                       resident.py:161-163) or wt = w ("gather", resident.py:164-165).
-// The rounding points are the reference's: bf16 activations, bf16 weights (CB3 centroids are bf16 already; IQ3_S
-// level * scale rounded once), f32 accumulation, h and y rounded to bf16, routing weights rounded to bf16 by the
+// The rounding points are the reference's: bf16 activations, bf16 weights (CB3 centroids are bf16 already; IQ3_S /
+// IQ4_XS level * scale rounded once), f32 accumulation, h and y rounded to bf16, routing weights rounded to bf16 by the
 // matmul combine.
+#include <type_traits>
+
 #include "cb3_tiles.h"
 #include "formats.h"
 
@@ -22,6 +24,9 @@ namespace mi {
 // IQ3_S grid levels (internal linkage: every translation unit that launches a kernel carries its own copy)
 static __constant__ uint32_t kPfGrid[512] = {
 #include "iq3s_grid.inc"
+};
+static __constant__ int8_t kPfKv[16] = {
+#include "iq4nl_kvalues.inc"
 };
 
 constexpr int kPfTT = 5;                   // token tiles of 16 rows per block
@@ -192,6 +197,7 @@ __global__ void __launch_bounds__(kPlanThreads) ragged_plan_kernel(const int32_t
 struct PfArgs {
     Cb3Table t0, t1;                       // CB3 tables -- gate/up: gate, up; down: down (twice)
     Iq3Table i0, i1;                       // IQ3_S tables, the same roles
+    Iq4Table k0, k1;                       // IQ4_XS tables, the same roles
     int R, K;                              // output columns (rows of the table), input columns
     const int32_t *blk_expert, *blk_n, *n_blocks, *tok_row;
     const uint16_t *x;                     // gate/up: x [T, K] gathered through tok_row; down: h [Rp, K]
@@ -284,6 +290,7 @@ struct PfShared {
             float4 grid[512];                    // IQ3_S: the grid's levels as f32 (8 KB)
             uint4 smask[256];                    // IQ3_S: 8 sign bits -> sign bits of 4 bf16 pairs (4 KB)
         } iq;
+        float2 iq4pair[256];                     // IQ4_XS: byte -> (level of its low nibble, of its high nibble)
     };
     uint32_t xs[2][kPfTm * kPfXPitch];           // column tiles ct (even/odd) of the block's rows, double-buffered;
                                                  // gate/up epilogue: the gate accumulators of one (gate, up) pair
@@ -438,6 +445,103 @@ struct PfIq3 {
 #pragma unroll
             for (int tt = 0; tt < NTT; ++tt)
                 b[tt] = *(const uint4 *)(xt + tt * 16 * kPfXPitch + 32 * (j >> 1) + 4 * (j & 1));
+            bf16x8 A = weights8(w, s.v[C & 1][0], ct, j);
+#pragma unroll
+            for (int r = 0; r < kPfRtw; ++r) {
+                bf16x8 An = A;
+                if (r + 1 < kPfRtw) An = weights8(w, s.v[C & 1][r + 1], ct, j);
+#pragma unroll
+                for (int tt = 0; tt < NTT; ++tt) acc[r][tt] = mfma16(A, b[tt], acc[r][tt]);
+                A = An;
+            }
+        }
+        // the slot's next column tile (ct + 2); past the row's end nothing is loaded (the slot is not read again)
+        if (ct + 2 < w.CT) {
+#pragma unroll
+            for (int r = 0; r < kPfRtw; ++r) load(w, ct + 2, s.v[C & 1][r], r);
+        }
+    }
+};
+
+// IQ4_XS: the reference's planes (planes.py:26-28, 136-170) decoded straight into the A operand.  A column tile is
+// 128 columns (4 sub-blocks of 32, half a block); the k-step of sub-block i takes, for lane group q, plane word 4i + q:
+// byte j of it holds sub-block columns 4q + j (low nibble) and 16 + 4q + j (high nibble).  The lane's A elements are
+// columns 4q .. 4q+3 then 16 + 4q .. 16 + 4q + 3, so the activations are read as two 8-byte pieces of the staged
+// tile.  A weight is bf16(level * f16(d) * (s - 32)): the f32 product is exact and rounded once to nearest even, as
+// the reference's tiles are (pallas_moe.py:147-162, 341-350).
+struct PfIq4Wave {
+    const char *qs, *sl, *sh, *dd;          // expert e's planes
+    uint32_t rpitch;                        // bytes per plane row (4 R)
+    uint32_t lrow;                          // the lane's byte offset in a plane row (row jt of the wavefront)
+    int q, CT;
+    const float2 *pair;                     // LDS: byte -> its two levels as f32
+};
+struct PfIq4Regs {
+    uint32_t v[2][kPfRtw][7];   // column tile ct in slot ct & 1, per row tile: the 4 words, sl, sh, d
+};
+
+struct PfIq4 {
+    static constexpr int kCols = 128;
+    static constexpr int kQOff = 2;        // dwords: columns 4q .. 4q+3 of a 32-column group
+    using Wave = PfIq4Wave;
+    using Regs = PfIq4Regs;
+    static __device__ __forceinline__ int n_tiles(const PfArgs &a, int mat) { return (mat ? a.k1 : a.k0).K / 128; }
+    static __device__ __forceinline__ void load(const Wave &w, int ct, uint32_t (&u)[7], int r) {
+        const uint32_t o = w.lrow + 64u * (uint32_t)r, P = w.rpitch;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) u[j] = *(const uint32_t *)(w.qs + (uint32_t)(16 * ct + 4 * j + w.q) * P + o);
+        u[4] = *(const uint32_t *)(w.sl + (uint32_t)(ct >> 1) * P + o);
+        u[5] = *(const uint32_t *)(w.sh + (uint32_t)(ct >> 1) * P + o);
+        u[6] = *(const uint32_t *)(w.dd + (uint32_t)(ct >> 2) * P + o);
+    }
+    static __device__ __forceinline__ void init(Wave &w, Regs &s, const PfArgs &a, PfShared &sh, int mat, int e,
+                                                int rg, int wave, int lane) {
+        const Iq4Table &tb = mat ? a.k1 : a.k0;
+        const size_t R = (size_t)tb.R;
+        w.qs = (const char *)(tb.qs + (size_t)e * tb.W * R);
+        w.sl = (const char *)(tb.sl + (size_t)e * tb.nblk * R);
+        w.sh = (const char *)(tb.sh + (size_t)e * tb.nblk * R);
+        w.dd = (const char *)(tb.d + (size_t)e * ((tb.nblk + 1) / 2) * R);
+        w.rpitch = 4u * (uint32_t)tb.R;
+        w.q = lane >> 4;
+        w.lrow = 4u * (uint32_t)(rg * 64 + (lane & 15));
+        w.CT = tb.K / 128;
+        w.pair = sh.iq4pair;
+        (void)wave;
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int r = 0; r < kPfRtw; ++r) load(w, c, s.v[c][r], r);
+    }
+    // the 8 weights of step j (sub-block 4 (ct % 2) + j) for the row tile whose plane words are u
+    static __device__ __forceinline__ bf16x8 weights8(const Wave &w, const uint32_t (&u)[7], int ct, int j) {
+        const int i = 4 * (ct & 1) + j;
+        const int sv = (int)(((u[4] >> (4 * i)) & 15u) | (((u[5] >> (2 * i)) & 3u) << 4)) - 32;
+        const float scale = f16_bits_to_f32(u[6] >> (16 * ((ct >> 1) & 1))) * (float)sv;
+        const uint32_t x = u[j];
+        const float2 p0 = w.pair[x & 255u], p1 = w.pair[(x >> 8) & 255u], p2 = w.pair[(x >> 16) & 255u],
+                     p3 = w.pair[x >> 24];
+        uint4 A;
+        A.x = pf_bf16_pair(p0.x * scale, p1.x * scale);
+        A.y = pf_bf16_pair(p2.x * scale, p3.x * scale);
+        A.z = pf_bf16_pair(p0.y * scale, p1.y * scale);
+        A.w = pf_bf16_pair(p2.y * scale, p3.y * scale);
+        return __builtin_bit_cast(bf16x8, A);
+    }
+    template <int NTT, int C>
+    static __device__ __forceinline__ void tile(const Wave &w, Regs &s, int st, const uint32_t *xt,
+                                                f32x4 (&acc)[kPfRtw][NTT]) {
+        const int ct = 4 * st + C;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (j > 0) __builtin_amdgcn_sched_barrier(0);
+            uint4 b[NTT];
+#pragma unroll
+            for (int tt = 0; tt < NTT; ++tt) {
+                const uint2 lo = *(const uint2 *)(xt + tt * 16 * kPfXPitch + 16 * j);
+                const uint2 hi = *(const uint2 *)(xt + tt * 16 * kPfXPitch + 16 * j + 8);
+                b[tt] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+            }
             bf16x8 A = weights8(w, s.v[C & 1][0], ct, j);
 #pragma unroll
             for (int r = 0; r < kPfRtw; ++r) {
@@ -621,6 +725,11 @@ __global__ void __launch_bounds__(64 * kPfWaves, 2) prefill_kernel(PfArgs a) {
             sh.iq.smask[tid] = make_uint4(m[0], m[1], m[2], m[3]);
         }
     }
+    if constexpr (std::is_same<WP, PfIq4>::value) {
+        // the level pairs (published by the barrier after the row offsets)
+        for (int i = threadIdx.x; i < 256; i += 64 * kPfWaves)
+            sh.iq4pair[i] = make_float2((float)kPfKv[i & 15], (float)kPfKv[i >> 4]);
+    }
     switch ((n + 15) >> 4) {
         case 1: prefill_body<MODE, 1, WP>(a, sh, g, rbg, e, n); break;
         case 2: prefill_body<MODE, 2, WP>(a, sh, g, rbg, e, n); break;
@@ -716,21 +825,35 @@ static Iq3Table pf_iq3_table(const mi_table *t) {
     return c;
 }
 
-// The three tables share one format: CB3 (code tiles) or IQ3_S (the reference's planes, whole 256-weight blocks).
+static Iq4Table pf_iq4_table(const mi_table *t) {
+    Iq4Table c{};
+    c.qs = t->plane[0];
+    c.sl = t->plane[1];
+    c.sh = t->plane[2];
+    c.d = t->plane[3];
+    c.R = t->rows;
+    c.K = t->cols;
+    c.nblk = t->cols / 256;
+    c.W = 32 * c.nblk;
+    return c;
+}
+
+// Gate and up share one format, down may use another: CB3 (code tiles), IQ3_S or IQ4_XS (the reference's planes,
+// whole 256-weight blocks).
 static int pf_validate(const mi_table *g, const mi_table *u, const mi_table *d) {
     if (!g || !u || !d) return MI_ERR_NULL;
     for (const mi_table *t : {g, u, d}) {
-        if (t->qtype != MI_QT_CB3 && t->qtype != MI_QT_IQ3_S) return MI_ERR_QTYPE;
-        if (t->qtype != g->qtype) return MI_ERR_MISMATCH;
-        const int np = t->qtype == MI_QT_CB3 ? 2 : 5;
+        if (t->qtype != MI_QT_CB3 && t->qtype != MI_QT_IQ3_S && t->qtype != MI_QT_IQ4_XS) return MI_ERR_QTYPE;
+        const int np = t->qtype == MI_QT_CB3 ? 2 : t->qtype == MI_QT_IQ3_S ? 5 : 4;
         for (int i = 0; i < np; ++i)
             if (!t->plane[i]) return MI_ERR_NULL;
         if (t->n_experts <= 0 || t->n_experts > kPlanMaxE || t->cols <= 0 || t->cols % 128 || t->rows <= 0)
             return MI_ERR_SHAPE;
-        if (t->qtype == MI_QT_IQ3_S && t->cols % 256) return MI_ERR_SHAPE;
-        // an expert's plane stays below 4 GiB (32-bit byte offsets)
-        if (t->qtype == MI_QT_IQ3_S && (long long)(t->cols / 16) * t->rows * 4 >= (1ll << 32)) return MI_ERR_SHAPE;
+        if (t->qtype != MI_QT_CB3 && t->cols % 256) return MI_ERR_SHAPE;
+        // an expert's qs plane stays below 4 GiB (32-bit byte offsets)
+        if (t->qtype != MI_QT_CB3 && (long long)(t->cols / 8) * t->rows * 4 >= (1ll << 32)) return MI_ERR_SHAPE;
     }
+    if (u->qtype != g->qtype) return MI_ERR_MISMATCH;
     if (g->rows % 128 || d->rows % 256) return MI_ERR_SHAPE;   // whole workgroup row ranges
     if (u->rows != g->rows || u->cols != g->cols || u->n_experts != g->n_experts) return MI_ERR_MISMATCH;
     if (d->cols != g->rows || d->n_experts != g->n_experts) return MI_ERR_MISMATCH;
@@ -810,11 +933,13 @@ int mi_moe_prefill(const mi_table *gate, const mi_table *up, const mi_table *dow
     uint16_t *h = (uint16_t *)(ws + L.off_h), *y = (uint16_t *)(ws + L.off_y);
     if ((st = launch_plan(idx, w, T, k, shared_expert, E, kPfTm, p, s))) return st;
 
-    const bool iq3 = gate->qtype == MI_QT_IQ3_S;
     PfArgs a{};
-    if (iq3) {
+    if (gate->qtype == MI_QT_IQ3_S) {
         a.i0 = pf_iq3_table(gate);
         a.i1 = pf_iq3_table(up);
+    } else if (gate->qtype == MI_QT_IQ4_XS) {
+        a.k0 = pf_iq4_table(gate);
+        a.k1 = pf_iq4_table(up);
     } else {
         a.t0 = pf_table(gate);
         a.t1 = pf_table(up);
@@ -833,12 +958,15 @@ int mi_moe_prefill(const mi_table *gate, const mi_table *up, const mi_table *dow
     a.wg_rows = 2;
     a.RBG = I / 128;
     const int g8 = (L.G + kXcds - 1) / kXcds * kXcds;       // blocks rounded up to whole XCD rounds
-    if (iq3) hipLaunchKernelGGL((prefill_kernel<0, PfIq3>), dim3(g8 * a.RBG), dim3(64 * kPfWaves), 0, s, a);
-    else hipLaunchKernelGGL((prefill_kernel<0, PfCb3>), dim3(g8 * a.RBG), dim3(64 * kPfWaves), 0, s, a);
+    const dim3 block(64 * kPfWaves);
+    if (gate->qtype == MI_QT_IQ3_S) hipLaunchKernelGGL((prefill_kernel<0, PfIq3>), dim3(g8 * a.RBG), block, 0, s, a);
+    else if (gate->qtype == MI_QT_IQ4_XS) hipLaunchKernelGGL((prefill_kernel<0, PfIq4>), dim3(g8 * a.RBG), block, 0, s, a);
+    else hipLaunchKernelGGL((prefill_kernel<0, PfCb3>), dim3(g8 * a.RBG), block, 0, s, a);
     if (hipGetLastError() != hipSuccess) return MI_ERR_LAUNCH;
 
     PfArgs b = a;
-    if (iq3) b.i0 = b.i1 = pf_iq3_table(down);
+    if (down->qtype == MI_QT_IQ3_S) b.i0 = b.i1 = pf_iq3_table(down);
+    else if (down->qtype == MI_QT_IQ4_XS) b.k0 = b.k1 = pf_iq4_table(down);
     else b.t0 = b.t1 = pf_table(down);
     b.R = D;
     b.K = I;
@@ -848,8 +976,9 @@ int mi_moe_prefill(const mi_table *gate, const mi_table *up, const mi_table *dow
     b.out = y;
     b.wg_rows = 4;
     b.RBG = D / 256;
-    if (iq3) hipLaunchKernelGGL((prefill_kernel<1, PfIq3>), dim3(g8 * b.RBG), dim3(64 * kPfWaves), 0, s, b);
-    else hipLaunchKernelGGL((prefill_kernel<1, PfCb3>), dim3(g8 * b.RBG), dim3(64 * kPfWaves), 0, s, b);
+    if (down->qtype == MI_QT_IQ3_S) hipLaunchKernelGGL((prefill_kernel<1, PfIq3>), dim3(g8 * b.RBG), block, 0, s, b);
+    else if (down->qtype == MI_QT_IQ4_XS) hipLaunchKernelGGL((prefill_kernel<1, PfIq4>), dim3(g8 * b.RBG), block, 0, s, b);
+    else hipLaunchKernelGGL((prefill_kernel<1, PfCb3>), dim3(g8 * b.RBG), block, 0, s, b);
     if (hipGetLastError() != hipSuccess) return MI_ERR_LAUNCH;
 
     const long long nthr = (long long)T * (D / 4);

@@ -389,7 +389,7 @@ class ResidentFetch:
     apply(p, x, idx, w, layer, limit): x [N, D]; idx [N, k] int32 into E; w [N, k] f32 -> f32 [N, D] (routed experts
     only; the caller adds the shared expert, model.py:847-855).  N*k <= gather_max_rows takes the fused decode
     kernels (f32 end to end, resident.py:110-120); larger calls take the grouped prefill GEMMs with the reference's
-    bf16 rounding points and ``combine`` (resident.py:144-165; CB3 or IQ3_S tables; bf16 ``out_dtype``).
+    bf16 rounding points and ``combine`` (resident.py:144-165; CB3, IQ3_S or IQ4_XS tables; bf16 ``out_dtype``).
     ``use_pallas`` / ``interpret`` / ``sweep_mode`` / ``chunk`` are accepted for signature compatibility; there is a
     single MI355X kernel path per regime."""
 
@@ -428,9 +428,9 @@ class ResidentFetch:
                 raise ValueError("decode activations must be bf16-representable (the layer dtype)")
             out, _ = moe_decode(gate, up, down, xb, idx, w, limit)
             return out
-        if not (gate.qtype == up.qtype == down.qtype):
+        if gate.qtype != up.qtype:
             raise NotImplementedError("ResidentFetch.apply: the grouped prefill path (N*k = %d > gather_max_rows = %d) "
-                                      "takes one format for gate, up and down" % (N * k, self.gather_max_rows))
+                                      "takes one format for gate and up" % (N * k, self.gather_max_rows))
         if self.out_dtype != torch.bfloat16:
             raise NotImplementedError("ResidentFetch.apply: the grouped prefill path follows the bf16 out_dtype "
                                       "rounding points (resident.py:153-158)")
