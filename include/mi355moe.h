@@ -39,12 +39,14 @@ extern "C" {
 #define MI_QT_CB3    1   /* 3-bit codes (10 per u32) + 8 bf16 centroids per (row, 128-column group)              */
 #define MI_QT_IQ3_S  2   /* llama.cpp IQ3_S in the reference's planar tables (planes.py:22-25)                   */
 #define MI_QT_IQ4_XS 3   /* llama.cpp IQ4_XS in the reference's planar tables (planes.py:26-28)                  */
+#define MI_QT_IQ2_S  4   /* llama.cpp IQ2_S in the reference's planar tables (planes.py:17-21)                   */
 
 /*
  * One expert table: E experts of one matrix kind (gate, up or down), every expert R rows x K inputs.  plane[] order:
  *   MI_QT_IQ3_S : {qs, sg, qh, sc, d}   -- the reference's planes, unchanged: u32 [E * rows_p, R], the matrix row
  *                                          on the minor axis (planes.py:5-14,45).  R % 64 == 0, K % 256 == 0.
  *   MI_QT_IQ4_XS: {qs, sl, sh, d}       -- likewise (planes.py:26-28,46).  R % 64 == 0, K % 256 == 0.
+ *   MI_QT_IQ2_S : {qs, sg, qh, sc, d}   -- likewise (planes.py:17-21,45).  R % 64 == 0, K % 256 == 0.
  *   MI_QT_CB3   : {qs, cb}              -- qs: u32 [E][ceil(K/160)][R/16][64][4] code tiles (16 rows x 160 columns,
  *                                          1 KB each, in the lane order of the matrix-core decoder; formats.py
  *                                          cb3_tile_words gives the bit map); cb: u32 [E][K/128][R][4] = bytes
@@ -154,19 +156,19 @@ int mi_ragged_plan(const int32_t *idx, const float *w, int32_t T, int32_t k, int
                    void *stream);
 
 /*
- * Fused MoE prefill layer (ResidentFetch._apply_ragged_kernel, resident.py:144-165) for CB3, IQ3_S or IQ4_XS tables
- * (gate and up in one format, down in the same or another), grouped GEMMs on the matrix cores:
+ * Fused MoE prefill layer (ResidentFetch._apply_ragged_kernel, resident.py:144-165) for CB3, IQ2_S, IQ3_S or IQ4_XS
+ * tables (gate and up in one format, down in the same or another), grouped GEMMs on the matrix cores:
  *   plan   = ragged_plan over the T*k slots (+ one shared-expert column of weight 1 if shared_expert >= 0), tm = 80
- *   W      = bf16(dequantized weight): CB3 centroids as stored; IQ3_S bf16(level * f16(d) * (1 + 2 sc)); IQ4_XS
- *            bf16(kvalue * f16(d) * (s - 32)), rounded once to nearest even as the reference's tiles are
- *            (pallas_moe.py:341-350)
+ *   W      = bf16(dequantized weight): CB3 centroids as stored; IQ2_S bf16(level * f16(d) * (0.5 + sc) * 0.25);
+ *            IQ3_S bf16(level * f16(d) * (1 + 2 sc)); IQ4_XS bf16(kvalue * f16(d) * (s - 32)), rounded once to
+ *            nearest even as the reference's tiles are (pallas_moe.py:341-350)
  *   h[row] = bf16(silu(min(g, L)) * clip(u, -L, L)),  g, u = Wgate_e x_t, Wup_e x_t in f32   (pallas_moe.py:622-690)
  *   y[row] = bf16(Wdown_e h[row]), f32 accumulation                                           (pallas_moe.py:693-755)
  *   out[t] = sum_j wt(t, j) y[row_slot(t, j)] in f32, wt = bf16(w[t, j]) for MI_COMBINE_MATMUL (resident.py:161-163)
  *            or w[t, j] for MI_COMBINE_GATHER (resident.py:164-165); the shared column has weight 1.
  * x bf16 [T, D], idx int32 [T, k], w f32 [T, k]; out_f32 and/or out_bf16 [T, D].  Every expert's weights are read
- * once per block of 80 rows.  T*(k+1) <= 2^22, E <= 1024, gate.rows % 128 == 0, down.rows % 256 == 0; IQ3_S and
- * IQ4_XS also need cols % 256 == 0.  MI_ERR_MISMATCH when gate and up differ in format or shape.
+ * once per block of 80 rows.  T*(k+1) <= 2^22, E <= 1024, gate.rows % 128 == 0, down.rows % 256 == 0; the IQ
+ * formats also need cols % 256 == 0.  MI_ERR_MISMATCH when gate and up differ in format or shape.
  * Four launches: plan, gate/up, down, combine.  The workspace (mi_moe_prefill_workspace bytes) holds the plan, h and
  * y; it needs no initialisation.
  */

@@ -1,5 +1,5 @@
-// The reference's planar IQ3_S and IQ4_XS tables as the gfx950 kernels address them (the decoders: iq3_mfma.h and
-// iq4_mfma.h for decode and matvec, prefill.hip for the prefill GEMMs).
+// The reference's planar IQ2_S, IQ3_S and IQ4_XS tables as the gfx950 kernels address them (the decoders:
+// iq2_mfma.h, iq3_mfma.h and iq4_mfma.h for decode and matvec, prefill.hip for the prefill GEMMs).
 #pragma once
 #include "common.h"
 
@@ -25,6 +25,15 @@ struct Iq3Table {
 struct Iq4Table {
     const uint32_t *qs, *sl, *sh, *d;
     int R, K, nblk, W;                      // W = 32 nblk words per row
+    static constexpr int kUnitCols = 256;
+};
+
+// The reference's planar IQ2_S tables (planes.py:17-21): word w of a row covers inputs 32w .. 32w+31, byte j of the
+// qs and sg words is group j = inputs 32w+8j .. 32w+8j+7 (low index bits, signs); byte w%4 of qh / sc u32 w/4 holds
+// the word's high index bits (2 per group) and its two 4-bit scales (one per 16 inputs).
+struct Iq2Table {
+    const uint32_t *qs, *sg, *qh, *sc, *d;
+    int R, K, nblk, W;                      // W = 8 nblk words per row
     static constexpr int kUnitCols = 256;
 };
 

@@ -6,7 +6,8 @@
 //      they are in flight (f32 activations -- h for the down projection -- as bf16 hi + lo parts),
 //   3. streams the expert's planes once with 128-bit loads (every wavefront load is 1 KB contiguous) and decodes
 //      the codes to bf16 in registers for the matrix cores, all of the group's tokens in one 16-column tile: CB3
-//      tiles (16-64 rows per wavefront), IQ3_S and IQ4_XS planes (64 rows per wavefront, iq3_mfma.h, iq4_mfma.h),
+//      tiles (16-64 rows per wavefront), IQ2_S, IQ3_S and IQ4_XS planes (64 rows per wavefront, iq2_mfma.h,
+//      iq3_mfma.h, iq4_mfma.h),
 //   4. writes its f32 partial sums; the next launch reduces them in a fixed order (the SwiGLU kernel forms h from
 //      the gate/up partials, the combine kernel sums the down partials with the routing weights, the split
 //      reduction finishes a matvec).
@@ -16,6 +17,7 @@
 
 #include "cb3_tiles.h"
 #include "formats.h"
+#include "iq2_mfma.h"
 #include "iq4_mfma.h"
 
 namespace mi {
@@ -23,6 +25,9 @@ namespace mi {
 // internal linkage: every translation unit that launches a kernel carries its own copy
 static __constant__ uint32_t kGridConst[512] = {
 #include "iq3s_grid.inc"
+};
+static __constant__ uint32_t kGrid2Const[2048] = {
+#include "iq2s_grid.inc"
 };
 static __constant__ int8_t kKvConst[16] = {
 #include "iq4nl_kvalues.inc"
@@ -35,6 +40,7 @@ struct Table {
     Cb3Table cb3;
     Iq3Table iq3;
     Iq4Table iq4;
+    Iq2Table iq2;
 };
 
 struct KArgs {
@@ -148,16 +154,19 @@ __host__ __device__ constexpr int wave_rows() { return QT == MI_QT_CB3 ? 16 * RT
 #ifndef MI_CB3_WAVES
 #define MI_CB3_WAVES 3
 #endif
+// IQ2_S holds two partials per row tile and k-step (two scale groups per word): 2 wavefronts per SIMD (<= 256 VGPRs).
 template <int QT>
-__host__ __device__ constexpr int min_waves_per_simd() { return MI_CB3_WAVES; }
+__host__ __device__ constexpr int min_waves_per_simd() { return QT == MI_QT_IQ2_S ? 2 : MI_CB3_WAVES; }
 
 template <int MODE, int QT, int TCMAX, int RTW>
 __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) grouped_kernel(KArgs a) {
     extern __shared__ uint32_t xlds[];
     __shared__ GroupScratch sc;
-    // IQ3_S: grid and sign tables; IQ4_XS: the level-pair table
-    __shared__ typename std::conditional<QT == MI_QT_IQ3_S, Iq3Lds,
-                                         typename std::conditional<QT == MI_QT_IQ4_XS, Iq4Lds, char>::type>::type iq;
+    // IQ3_S, IQ2_S: grid and sign tables; IQ4_XS: the level-pair table
+    __shared__ typename std::conditional<
+        QT == MI_QT_IQ3_S, Iq3Lds,
+        typename std::conditional<QT == MI_QT_IQ4_XS, Iq4Lds,
+                                  typename std::conditional<QT == MI_QT_IQ2_S, Iq2Lds, char>::type>::type>::type iq;
     __shared__ uint4 cbl[QT == MI_QT_CB3 ? kWgWaves * 5 * 64 : 1];   // CB3: per-wavefront codebook slots
     __shared__ int s_tok[kMaxT];
 
@@ -178,6 +187,7 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
     // published by the barrier after the slot list
     if constexpr (QT == MI_QT_IQ3_S) iq3_fill_lds(iq, kGridConst);
     if constexpr (QT == MI_QT_IQ4_XS) iq4_fill_lds(iq, kKvConst);
+    if constexpr (QT == MI_QT_IQ2_S) iq2_fill_lds(iq, kGrid2Const);
 
     // column range of the split; CB3 stages its padded column tiles (columns >= K are zero)
     const int ucols = cb3 ? Cb3Table::kUnitCols : 256;      // IQ formats: 256-weight blocks
@@ -301,6 +311,13 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
                                             part_base, a.R, stage);
         else
             iq3m_run_and_store<false, TCMAX>(tb.iq3, e, rg * WR, u0, u1, c0, iq, xh, xl, xsp, a.t_rows, n, s_tok,
+                                             part_base, a.R, stage);
+    } else if constexpr (QT == MI_QT_IQ2_S) {
+        if (hilo)
+            iq2m_run_and_store<true, TCMAX>(tb.iq2, e, rg * WR, u0, u1, c0, iq, xh, xl, xsp, a.t_rows, n, s_tok,
+                                            part_base, a.R, stage);
+        else
+            iq2m_run_and_store<false, TCMAX>(tb.iq2, e, rg * WR, u0, u1, c0, iq, xh, xl, xsp, a.t_rows, n, s_tok,
                                              part_base, a.R, stage);
     } else {
         if (hilo)

@@ -10,8 +10,14 @@ namespace mi {
 // ------------------------------------------------------------------------------------------------ dequant (debug)
 __global__ void dequant_kernel(Table tb, int e, float *out) {
     // one thread per (row, 16 columns); writes the exact f32 weights in natural order
-    const int R = tb.qtype == MI_QT_CB3 ? tb.cb3.R : tb.qtype == MI_QT_IQ3_S ? tb.iq3.R : tb.iq4.R;
-    const int K = tb.qtype == MI_QT_CB3 ? tb.cb3.K : tb.qtype == MI_QT_IQ3_S ? tb.iq3.K : tb.iq4.K;
+    const int R = tb.qtype == MI_QT_CB3    ? tb.cb3.R
+                  : tb.qtype == MI_QT_IQ3_S  ? tb.iq3.R
+                  : tb.qtype == MI_QT_IQ4_XS ? tb.iq4.R
+                                             : tb.iq2.R;
+    const int K = tb.qtype == MI_QT_CB3    ? tb.cb3.K
+                  : tb.qtype == MI_QT_IQ3_S  ? tb.iq3.K
+                  : tb.qtype == MI_QT_IQ4_XS ? tb.iq4.K
+                                             : tb.iq2.K;
     const int per_row = K / 16;
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (long long)R * per_row) return;
@@ -39,6 +45,21 @@ __global__ void dequant_kernel(Table tb, int e, float *out) {
             const uint32_t lo = cw[code >> 2], hi = cw[2 + (code >> 2)];
             const uint32_t sh = 8 * (code & 3u);
             v = bf16_to_f32(((lo >> sh) & 255u) | (((hi >> sh) & 255u) << 8));
+        } else if (tb.qtype == MI_QT_IQ2_S) {
+            // column c: word w, group j, position k (c = 32 w + 8 j + k); block w / 8
+            const Iq2Table &t = tb.iq2;
+            const int w = c >> 5, j = (c >> 3) & 3, k = c & 7;
+            const uint32_t q = t.qs[((size_t)e * t.W + w) * Rz + r];
+            const uint32_t sgw = t.sg[((size_t)e * t.W + w) * Rz + r];
+            const uint32_t qhb = (t.qh[((size_t)e * (t.W / 4) + (w >> 2)) * Rz + r] >> (8 * (w & 3))) & 255u;
+            const uint32_t scb = (t.sc[((size_t)e * (t.W / 4) + (w >> 2)) * Rz + r] >> (8 * (w & 3))) & 255u;
+            const uint32_t dw = t.d[((size_t)e * ((t.nblk + 1) / 2) + (w >> 4)) * Rz + r];
+            const float scale = f16_bits_to_f32(dw >> (((w >> 3) & 1) * 16)) *
+                                (0.5f + (float)((scb >> (4 * (j >> 1))) & 15u)) * 0.25f;
+            const uint32_t idx = ((q >> (8 * j)) & 255u) | (((qhb >> (2 * j)) & 3u) << 8);
+            const uint32_t lv = (kGrid2Const[2 * idx + (k >> 2)] >> (8 * (k & 3))) & 255u;
+            const uint32_t sb = (sgw >> (8 * j + k)) & 1u;
+            v = scale * (float)lv * (sb ? -1.0f : 1.0f);
         } else if (tb.qtype == MI_QT_IQ4_XS) {
             // column c: block b, sub-block i, word 4i + wq, byte j, nibble pos (c = 256 b + 32 i + 16 pos + 4 wq + j)
             const Iq4Table &t = tb.iq4;
@@ -182,7 +203,8 @@ __global__ void split_reduce_kernel(const float *__restrict__ part, int S, int N
 // ------------------------------------------------------------------------------------------------ host side
 static int validate_table(const mi_table *t) {
     if (!t) return MI_ERR_NULL;
-    if (t->qtype != MI_QT_CB3 && t->qtype != MI_QT_IQ3_S && t->qtype != MI_QT_IQ4_XS) return MI_ERR_QTYPE;
+    if (t->qtype != MI_QT_CB3 && t->qtype != MI_QT_IQ3_S && t->qtype != MI_QT_IQ4_XS && t->qtype != MI_QT_IQ2_S)
+        return MI_ERR_QTYPE;
     if (t->rows <= 0 || t->rows % (t->qtype == MI_QT_CB3 ? kCb3RowAlign : kIq3WaveRows)) return MI_ERR_SHAPE;
     if (t->n_experts <= 0 || t->n_experts > kMaxExperts) return MI_ERR_SHAPE;
     if (t->qtype == MI_QT_CB3) {
@@ -190,7 +212,7 @@ static int validate_table(const mi_table *t) {
         if (!t->plane[0] || !t->plane[1]) return MI_ERR_NULL;
     } else {
         if (t->cols <= 0 || t->cols % 256) return MI_ERR_SHAPE;
-        for (int i = 0; i < (t->qtype == MI_QT_IQ3_S ? 5 : 4); ++i)
+        for (int i = 0; i < (t->qtype == MI_QT_IQ4_XS ? 4 : 5); ++i)
             if (!t->plane[i]) return MI_ERR_NULL;
     }
     return MI_OK;
@@ -207,6 +229,16 @@ static Table make_table(const mi_table *t) {
         tb.cb3.CT = (t->cols + kCb3TileCols - 1) / kCb3TileCols;
         tb.cb3.RT = t->rows / 16;
         tb.cb3.G = t->cols / 128;
+    } else if (t->qtype == MI_QT_IQ2_S) {
+        tb.iq2.qs = t->plane[0];
+        tb.iq2.sg = t->plane[1];
+        tb.iq2.qh = t->plane[2];
+        tb.iq2.sc = t->plane[3];
+        tb.iq2.d = t->plane[4];
+        tb.iq2.R = t->rows;
+        tb.iq2.K = t->cols;
+        tb.iq2.nblk = t->cols / 256;
+        tb.iq2.W = 8 * (t->cols / 256);
     } else if (t->qtype == MI_QT_IQ4_XS) {
         tb.iq4.qs = t->plane[0];
         tb.iq4.sl = t->plane[1];
@@ -233,9 +265,9 @@ static Table make_table(const mi_table *t) {
 static int cb3_ct(const mi_table *t) { return (t->cols + kCb3TileCols - 1) / kCb3TileCols; }
 static int n_units_of(const mi_table *t) {
     if (t->qtype == MI_QT_CB3) return cb3_ct(t);                 // 160-column tiles
-    return t->cols / 256;                                        // IQ3_S / IQ4_XS blocks
+    return t->cols / 256;                                        // IQ2_S / IQ3_S / IQ4_XS blocks
 }
-// Rows per wavefront: CB3 16 rtw (rtw row tiles), IQ3_S / IQ4_XS 64 (four interleaved row tiles).
+// Rows per wavefront: CB3 16 rtw (rtw row tiles), IQ2_S / IQ3_S / IQ4_XS 64 (four interleaved row tiles).
 static int wave_rows_of(const mi_table *t, int rtw) { return t->qtype == MI_QT_CB3 ? 16 * rtw : kIq3WaveRows; }
 static int unit_cols(const mi_table *t) { return t->qtype == MI_QT_CB3 ? kCb3TileCols : 256; }
 
@@ -303,19 +335,22 @@ static int cu_count() {
 MI_DECL_OCC(0, 1)
 MI_DECL_OCC(0, 2)
 MI_DECL_OCC(0, 3)
+MI_DECL_OCC(0, 4)
 MI_DECL_OCC(1, 1)
 MI_DECL_OCC(1, 2)
 MI_DECL_OCC(1, 3)
+MI_DECL_OCC(1, 4)
 MI_DECL_OCC(2, 1)
 MI_DECL_OCC(2, 2)
 MI_DECL_OCC(2, 3)
+MI_DECL_OCC(2, 4)
 #undef MI_DECL_OCC
 
 // Resident workgroups per CU of a grouped-kernel launch (the runtime's occupancy for that instance and LDS size;
 // 2 when it cannot be queried), cached per (mode, format, token class, rows per wavefront, 512-byte LDS bucket).
 static int wgs_per_cu(int mode, int qtype, int tcmax, int rtw, size_t lds) {
-    static int cache[3][3][5][3][161];
-    const int qi = qtype - 1;                                   // MI_QT_CB3, MI_QT_IQ3_S, MI_QT_IQ4_XS
+    static int cache[3][4][5][3][161];
+    const int qi = qtype - 1;                                   // MI_QT_CB3, MI_QT_IQ3_S, MI_QT_IQ4_XS, MI_QT_IQ2_S
     int ti = 0, ri = rtw == 4 ? 2 : rtw - 1;
     while ((1 << ti) < tcmax && ti < 4) ++ti;
     const size_t bucket = (lds + 511) / 512;
@@ -324,9 +359,10 @@ static int wgs_per_cu(int mode, int qtype, int tcmax, int rtw, size_t lds) {
     const size_t l = bucket * 512;
     int n;
     typedef int (*Occ)(int, int, size_t);
-    static const Occ occ[3][3] = {{occupancy_grouped_0_1, occupancy_grouped_0_2, occupancy_grouped_0_3},
-                                  {occupancy_grouped_1_1, occupancy_grouped_1_2, occupancy_grouped_1_3},
-                                  {occupancy_grouped_2_1, occupancy_grouped_2_2, occupancy_grouped_2_3}};
+    static const Occ occ[3][4] = {
+        {occupancy_grouped_0_1, occupancy_grouped_0_2, occupancy_grouped_0_3, occupancy_grouped_0_4},
+        {occupancy_grouped_1_1, occupancy_grouped_1_2, occupancy_grouped_1_3, occupancy_grouped_1_4},
+        {occupancy_grouped_2_1, occupancy_grouped_2_2, occupancy_grouped_2_3, occupancy_grouped_2_4}};
     n = occ[mode][qi](tcmax, rtw, l);
     if (n <= 0) n = 2;
     if (slot) *slot = n;
@@ -363,9 +399,10 @@ static Shape choose_shape(const mi_table *t, int mode, int tcmax, int groups, in
         if (forced_rtw > 0 && cb3 && rtw != forced_rtw) continue;
         const int RB = t->rows / wave_rows_of(t, rtw);
         const int RBG = (RB + rg_per_wg - 1) / rg_per_wg;
-        // kilobytes a wavefront streams per unit: CB3 one 1 KB code tile per row tile + codebook; IQ3_S / IQ4_XS 64
-        // rows of a 110 / 136-byte block
-        const double kb_per_unit = cb3 ? rtw * 1.25 : 64 * (t->qtype == MI_QT_IQ3_S ? 110 : 136) / 1024.0;
+        // kilobytes a wavefront streams per unit: CB3 one 1 KB code tile per row tile + codebook; IQ2_S / IQ3_S /
+        // IQ4_XS 64 rows of an 82 / 110 / 136-byte block
+        const int block_bytes = t->qtype == MI_QT_IQ3_S ? 110 : t->qtype == MI_QT_IQ2_S ? 82 : 136;
+        const double kb_per_unit = cb3 ? rtw * 1.25 : 64 * block_bytes / 1024.0;
         const int aligns[2] = {cb3 ? 4 : 1, 1};
         for (int ai = 0; ai < 2; ++ai) {
             const int align = aligns[ai];
@@ -573,20 +610,23 @@ static int launch_status() {
 MI_DECL_LAUNCH(0, 1)
 MI_DECL_LAUNCH(0, 2)
 MI_DECL_LAUNCH(0, 3)
+MI_DECL_LAUNCH(0, 4)
 MI_DECL_LAUNCH(1, 1)
 MI_DECL_LAUNCH(1, 2)
 MI_DECL_LAUNCH(1, 3)
+MI_DECL_LAUNCH(1, 4)
 MI_DECL_LAUNCH(2, 1)
 MI_DECL_LAUNCH(2, 2)
 MI_DECL_LAUNCH(2, 3)
+MI_DECL_LAUNCH(2, 4)
 #undef MI_DECL_LAUNCH
 
 template <int MODE>
 static void launch_grouped(int qtype, int tcmax, int rtw, dim3 grid, size_t lds, hipStream_t s, const KArgs &a) {
     typedef void (*Launch)(int, int, dim3, dim3, size_t, hipStream_t, const KArgs &);
-    static const Launch fn[3][3] = {{launch_grouped_0_1, launch_grouped_0_2, launch_grouped_0_3},
-                                    {launch_grouped_1_1, launch_grouped_1_2, launch_grouped_1_3},
-                                    {launch_grouped_2_1, launch_grouped_2_2, launch_grouped_2_3}};
+    static const Launch fn[3][4] = {{launch_grouped_0_1, launch_grouped_0_2, launch_grouped_0_3, launch_grouped_0_4},
+                                    {launch_grouped_1_1, launch_grouped_1_2, launch_grouped_1_3, launch_grouped_1_4},
+                                    {launch_grouped_2_1, launch_grouped_2_2, launch_grouped_2_3, launch_grouped_2_4}};
     fn[MODE][qtype - 1](tcmax, rtw, grid, dim3(64 * kWgWaves), lds, s, a);
 }
 

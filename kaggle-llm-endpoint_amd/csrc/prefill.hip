@@ -1,4 +1,4 @@
-// Grouped prefill for CB3, IQ3_S and IQ4_XS experts on the gfx950 matrix cores (the reference's ragged prefill,
+// Grouped prefill for CB3, IQ2_S, IQ3_S and IQ4_XS experts on the gfx950 matrix cores (the reference's ragged prefill,
 // resident.py:144-165 with pallas_moe.py:564-592,622-755):
 //   ragged_plan_kernel  the reference's slot layout (pallas_moe.py:564-592) built on the device by one workgroup:
 //                       slots stably sorted by expert, every expert padded to whole blocks of tm rows;
@@ -11,8 +11,8 @@
 //                         down:    y = bf16(h Wd^T), f32 accumulation                        (pallas_moe.py:747)
 //   prefill_combine     out[t] = sum_j wt(t, j) * y[row_slot(t, j)] in f32 with wt = bf16(w) ("matmul" combine,
 //                       resident.py:161-163) or wt = w ("gather", resident.py:164-165).
-// The rounding points are the reference's: bf16 activations, bf16 weights (CB3 centroids are bf16 already; IQ3_S /
-// IQ4_XS level * scale rounded once), f32 accumulation, h and y rounded to bf16, routing weights rounded to bf16 by the
+// The rounding points are the reference's: bf16 activations, bf16 weights (CB3 centroids are bf16 already; IQ2_S /
+// IQ3_S / IQ4_XS level * scale rounded once), f32 accumulation, h and y rounded to bf16, routing weights rounded to bf16 by the
 // matmul combine.
 #include <type_traits>
 
@@ -24,6 +24,9 @@ namespace mi {
 // IQ3_S grid levels (internal linkage: every translation unit that launches a kernel carries its own copy)
 static __constant__ uint32_t kPfGrid[512] = {
 #include "iq3s_grid.inc"
+};
+static __constant__ uint32_t kPfGrid2[2048] = {
+#include "iq2s_grid.inc"
 };
 static __constant__ int8_t kPfKv[16] = {
 #include "iq4nl_kvalues.inc"
@@ -198,6 +201,7 @@ struct PfArgs {
     Cb3Table t0, t1;                       // CB3 tables -- gate/up: gate, up; down: down (twice)
     Iq3Table i0, i1;                       // IQ3_S tables, the same roles
     Iq4Table k0, k1;                       // IQ4_XS tables, the same roles
+    Iq2Table j0, j1;                       // IQ2_S tables, the same roles
     int R, K;                              // output columns (rows of the table), input columns
     const int32_t *blk_expert, *blk_n, *n_blocks, *tok_row;
     const uint16_t *x;                     // gate/up: x [T, K] gathered through tok_row; down: h [Rp, K]
@@ -291,6 +295,10 @@ struct PfShared {
             uint4 smask[256];                    // IQ3_S: 8 sign bits -> sign bits of 4 bf16 pairs (4 KB)
         } iq;
         float2 iq4pair[256];                     // IQ4_XS: byte -> (level of its low nibble, of its high nibble)
+        struct {
+            uint4 level[1024];                   // IQ2_S: grid entry -> its 8 levels as bf16 (16 KB)
+            uint4 smask[256];                    // IQ2_S: 8 sign bits -> sign bits of 4 bf16 pairs (4 KB)
+        } iq2;
     };
     uint32_t xs[2][kPfTm * kPfXPitch];           // column tiles ct (even/odd) of the block's rows, double-buffered;
                                                  // gate/up epilogue: the gate accumulators of one (gate, up) pair
@@ -445,6 +453,103 @@ struct PfIq3 {
 #pragma unroll
             for (int tt = 0; tt < NTT; ++tt)
                 b[tt] = *(const uint4 *)(xt + tt * 16 * kPfXPitch + 32 * (j >> 1) + 4 * (j & 1));
+            bf16x8 A = weights8(w, s.v[C & 1][0], ct, j);
+#pragma unroll
+            for (int r = 0; r < kPfRtw; ++r) {
+                bf16x8 An = A;
+                if (r + 1 < kPfRtw) An = weights8(w, s.v[C & 1][r + 1], ct, j);
+#pragma unroll
+                for (int tt = 0; tt < NTT; ++tt) acc[r][tt] = mfma16(A, b[tt], acc[r][tt]);
+                A = An;
+            }
+        }
+        // the slot's next column tile (ct + 2); past the row's end nothing is loaded (the slot is not read again)
+        if (ct + 2 < w.CT) {
+#pragma unroll
+            for (int r = 0; r < kPfRtw; ++r) load(w, ct + 2, s.v[C & 1][r], r);
+        }
+    }
+};
+
+// IQ2_S: the reference's planes (planes.py:17-21, 136-170) decoded straight into the A operand.  A column tile is
+// 128 columns = 4 words (half a 256-weight block).  In k-step j lane (row i, group q) holds group j of word q of the
+// tile, i.e. columns 32q + 8j .. 32q + 8j + 7: the k order inside a step is free as long as the activations are read
+// in the same order, and this one lets a lane read only its own word of each plane.  A weight is bf16(level * scale),
+// scale = f16(d) * (0.5 + sc) * 0.25 in f32 (the product is exact), rounded once to nearest even as the reference's
+// tiles are (pallas_moe.py:105-124, 341-350); the sign is set on the rounded value (the rounding is symmetric).
+struct PfIq2Wave {
+    const char *qs, *sg, *qh, *sc, *dd;     // expert e's planes
+    uint32_t rpitch;                        // bytes per plane row (4 R)
+    uint32_t lrow;                          // the lane's byte offset in a plane row (row jt of the wavefront)
+    int q, CT;
+    const uint4 *level;                     // LDS: grid entry -> 8 bf16 levels
+    const uint4 *smask;                     // LDS: sign masks
+};
+struct PfIq2Regs {
+    uint32_t v[2][kPfRtw][5];   // column tile ct in slot ct & 1, per row tile: the lane's qs and sg words, qh, sc, d
+};
+
+struct PfIq2 {
+    static constexpr int kCols = 128;
+    static constexpr int kQOff = 16;       // dwords: word q of the tile
+    using Wave = PfIq2Wave;
+    using Regs = PfIq2Regs;
+    static __device__ __forceinline__ int n_tiles(const PfArgs &a, int mat) { return (mat ? a.j1 : a.j0).K / 128; }
+    static __device__ __forceinline__ void load(const Wave &w, int ct, uint32_t (&u)[5], int r) {
+        const uint32_t o = w.lrow + 64u * (uint32_t)r, P = w.rpitch;
+        u[0] = *(const uint32_t *)(w.qs + (uint32_t)(4 * ct + w.q) * P + o);
+        u[1] = *(const uint32_t *)(w.sg + (uint32_t)(4 * ct + w.q) * P + o);
+        u[2] = *(const uint32_t *)(w.qh + (uint32_t)ct * P + o);        // byte q: word 4 ct + q
+        u[3] = *(const uint32_t *)(w.sc + (uint32_t)ct * P + o);
+        u[4] = *(const uint32_t *)(w.dd + (uint32_t)(ct >> 2) * P + o);
+    }
+    static __device__ __forceinline__ void init(Wave &w, Regs &s, const PfArgs &a, PfShared &sh, int mat, int e,
+                                                int rg, int wave, int lane) {
+        const Iq2Table &tb = mat ? a.j1 : a.j0;
+        const size_t R = (size_t)tb.R;
+        w.qs = (const char *)(tb.qs + (size_t)e * tb.W * R);
+        w.sg = (const char *)(tb.sg + (size_t)e * tb.W * R);
+        w.qh = (const char *)(tb.qh + (size_t)e * (tb.W / 4) * R);
+        w.sc = (const char *)(tb.sc + (size_t)e * (tb.W / 4) * R);
+        w.dd = (const char *)(tb.d + (size_t)e * ((tb.nblk + 1) / 2) * R);
+        w.rpitch = 4u * (uint32_t)tb.R;
+        w.q = lane >> 4;
+        w.lrow = 4u * (uint32_t)(rg * 64 + (lane & 15));
+        w.CT = tb.K / 128;
+        w.level = sh.iq2.level;
+        w.smask = sh.iq2.smask;
+        (void)wave;
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int r = 0; r < kPfRtw; ++r) load(w, c, s.v[c][r], r);
+    }
+    // the 8 weights of step j (group j of the lane's word) for the row tile whose plane words are u
+    static __device__ __forceinline__ bf16x8 weights8(const Wave &w, const uint32_t (&u)[5], int ct, int j) {
+        const int q = w.q;
+        const uint32_t idx = ((u[0] >> (8 * j)) & 255u) | (((u[2] >> (8 * q + 2 * j)) & 3u) << 8);
+        const uint32_t s8 = (u[1] >> (8 * j)) & 255u;
+        const uint32_t nib = (u[3] >> (8 * q + 4 * (j >> 1))) & 15u;
+        const float scale = f16_bits_to_f32(u[4] >> (16 * ((ct >> 1) & 1))) * (0.5f + (float)nib) * 0.25f;
+        const uint4 g = w.level[idx];
+        const uint4 sm = w.smask[s8];
+        uint4 A;
+        A.x = pf_bf16_pair(__uint_as_float(g.x << 16) * scale, __uint_as_float(g.x & 0xffff0000u) * scale) | sm.x;
+        A.y = pf_bf16_pair(__uint_as_float(g.y << 16) * scale, __uint_as_float(g.y & 0xffff0000u) * scale) | sm.y;
+        A.z = pf_bf16_pair(__uint_as_float(g.z << 16) * scale, __uint_as_float(g.z & 0xffff0000u) * scale) | sm.z;
+        A.w = pf_bf16_pair(__uint_as_float(g.w << 16) * scale, __uint_as_float(g.w & 0xffff0000u) * scale) | sm.w;
+        return __builtin_bit_cast(bf16x8, A);
+    }
+    template <int NTT, int C>
+    static __device__ __forceinline__ void tile(const Wave &w, Regs &s, int st, const uint32_t *xt,
+                                                f32x4 (&acc)[kPfRtw][NTT]) {
+        const int ct = 4 * st + C;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (j > 0) __builtin_amdgcn_sched_barrier(0);
+            uint4 b[NTT];
+#pragma unroll
+            for (int tt = 0; tt < NTT; ++tt) b[tt] = *(const uint4 *)(xt + tt * 16 * kPfXPitch + 4 * j);
             bf16x8 A = weights8(w, s.v[C & 1][0], ct, j);
 #pragma unroll
             for (int r = 0; r < kPfRtw; ++r) {
@@ -710,7 +815,7 @@ __global__ void __launch_bounds__(64 * kPfWaves, 2) prefill_kernel(PfArgs a) {
     if (g >= *a.n_blocks) return;
     const int e = __builtin_amdgcn_readfirstlane(a.blk_expert[g]);
     const int n = __builtin_amdgcn_readfirstlane(a.blk_n[g]);
-    if constexpr (WP::kCols == kIq3TileCols) {
+    if constexpr (std::is_same<WP, PfIq3>::value) {
         // the grid's levels as f32 and the sign masks (published by the barrier after the row offsets)
         const int tid = threadIdx.x;
         for (int i = tid; i < 512; i += 64 * kPfWaves) {
@@ -723,6 +828,27 @@ __global__ void __launch_bounds__(64 * kPfWaves, 2) prefill_kernel(PfArgs a) {
 #pragma unroll
             for (int p = 0; p < 4; ++p) m[p] = (((uint32_t)tid >> (2 * p)) & 1u) << 15 | (((uint32_t)tid >> (2 * p + 1)) & 1u) << 31;
             sh.iq.smask[tid] = make_uint4(m[0], m[1], m[2], m[3]);
+        }
+    }
+    if constexpr (std::is_same<WP, PfIq2>::value) {
+        // the grid's levels as bf16 and the sign masks (published by the barrier after the row offsets)
+        const int tid = threadIdx.x;
+        for (int i = tid; i < 1024; i += 64 * kPfWaves) {
+            const uint32_t lo = kPfGrid2[2 * i], hi = kPfGrid2[2 * i + 1];
+            uint32_t v[4];
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const uint32_t wd = p < 2 ? lo : hi, sft = 16 * (p & 1);
+                v[p] = (__float_as_uint((float)((wd >> sft) & 255u)) >> 16) |
+                       (__float_as_uint((float)((wd >> (sft + 8)) & 255u)) & 0xffff0000u);
+            }
+            sh.iq2.level[i] = make_uint4(v[0], v[1], v[2], v[3]);
+        }
+        if (tid < 256) {
+            uint32_t m[4];
+#pragma unroll
+            for (int p = 0; p < 4; ++p) m[p] = (((uint32_t)tid >> (2 * p)) & 1u) << 15 | (((uint32_t)tid >> (2 * p + 1)) & 1u) << 31;
+            sh.iq2.smask[tid] = make_uint4(m[0], m[1], m[2], m[3]);
         }
     }
     if constexpr (std::is_same<WP, PfIq4>::value) {
@@ -825,6 +951,20 @@ static Iq3Table pf_iq3_table(const mi_table *t) {
     return c;
 }
 
+static Iq2Table pf_iq2_table(const mi_table *t) {
+    Iq2Table c{};
+    c.qs = t->plane[0];
+    c.sg = t->plane[1];
+    c.qh = t->plane[2];
+    c.sc = t->plane[3];
+    c.d = t->plane[4];
+    c.R = t->rows;
+    c.K = t->cols;
+    c.nblk = t->cols / 256;
+    c.W = 8 * c.nblk;
+    return c;
+}
+
 static Iq4Table pf_iq4_table(const mi_table *t) {
     Iq4Table c{};
     c.qs = t->plane[0];
@@ -838,13 +978,14 @@ static Iq4Table pf_iq4_table(const mi_table *t) {
     return c;
 }
 
-// Gate and up share one format, down may use another: CB3 (code tiles), IQ3_S or IQ4_XS (the reference's planes,
-// whole 256-weight blocks).
+// Gate and up share one format, down may use another: CB3 (code tiles), IQ2_S, IQ3_S or IQ4_XS (the reference's
+// planes, whole 256-weight blocks).
 static int pf_validate(const mi_table *g, const mi_table *u, const mi_table *d) {
     if (!g || !u || !d) return MI_ERR_NULL;
     for (const mi_table *t : {g, u, d}) {
-        if (t->qtype != MI_QT_CB3 && t->qtype != MI_QT_IQ3_S && t->qtype != MI_QT_IQ4_XS) return MI_ERR_QTYPE;
-        const int np = t->qtype == MI_QT_CB3 ? 2 : t->qtype == MI_QT_IQ3_S ? 5 : 4;
+        if (t->qtype != MI_QT_CB3 && t->qtype != MI_QT_IQ3_S && t->qtype != MI_QT_IQ4_XS && t->qtype != MI_QT_IQ2_S)
+            return MI_ERR_QTYPE;
+        const int np = t->qtype == MI_QT_CB3 ? 2 : t->qtype == MI_QT_IQ4_XS ? 4 : 5;
         for (int i = 0; i < np; ++i)
             if (!t->plane[i]) return MI_ERR_NULL;
         if (t->n_experts <= 0 || t->n_experts > kPlanMaxE || t->cols <= 0 || t->cols % 128 || t->rows <= 0)
@@ -940,6 +1081,9 @@ int mi_moe_prefill(const mi_table *gate, const mi_table *up, const mi_table *dow
     } else if (gate->qtype == MI_QT_IQ4_XS) {
         a.k0 = pf_iq4_table(gate);
         a.k1 = pf_iq4_table(up);
+    } else if (gate->qtype == MI_QT_IQ2_S) {
+        a.j0 = pf_iq2_table(gate);
+        a.j1 = pf_iq2_table(up);
     } else {
         a.t0 = pf_table(gate);
         a.t1 = pf_table(up);
@@ -961,12 +1105,14 @@ int mi_moe_prefill(const mi_table *gate, const mi_table *up, const mi_table *dow
     const dim3 block(64 * kPfWaves);
     if (gate->qtype == MI_QT_IQ3_S) hipLaunchKernelGGL((prefill_kernel<0, PfIq3>), dim3(g8 * a.RBG), block, 0, s, a);
     else if (gate->qtype == MI_QT_IQ4_XS) hipLaunchKernelGGL((prefill_kernel<0, PfIq4>), dim3(g8 * a.RBG), block, 0, s, a);
+    else if (gate->qtype == MI_QT_IQ2_S) hipLaunchKernelGGL((prefill_kernel<0, PfIq2>), dim3(g8 * a.RBG), block, 0, s, a);
     else hipLaunchKernelGGL((prefill_kernel<0, PfCb3>), dim3(g8 * a.RBG), block, 0, s, a);
     if (hipGetLastError() != hipSuccess) return MI_ERR_LAUNCH;
 
     PfArgs b = a;
     if (down->qtype == MI_QT_IQ3_S) b.i0 = b.i1 = pf_iq3_table(down);
     else if (down->qtype == MI_QT_IQ4_XS) b.k0 = b.k1 = pf_iq4_table(down);
+    else if (down->qtype == MI_QT_IQ2_S) b.j0 = b.j1 = pf_iq2_table(down);
     else b.t0 = b.t1 = pf_table(down);
     b.R = D;
     b.K = I;
@@ -978,6 +1124,7 @@ int mi_moe_prefill(const mi_table *gate, const mi_table *up, const mi_table *dow
     b.RBG = D / 256;
     if (down->qtype == MI_QT_IQ3_S) hipLaunchKernelGGL((prefill_kernel<1, PfIq3>), dim3(g8 * b.RBG), block, 0, s, b);
     else if (down->qtype == MI_QT_IQ4_XS) hipLaunchKernelGGL((prefill_kernel<1, PfIq4>), dim3(g8 * b.RBG), block, 0, s, b);
+    else if (down->qtype == MI_QT_IQ2_S) hipLaunchKernelGGL((prefill_kernel<1, PfIq2>), dim3(g8 * b.RBG), block, 0, s, b);
     else hipLaunchKernelGGL((prefill_kernel<1, PfCb3>), dim3(g8 * b.RBG), block, 0, s, b);
     if (hipGetLastError() != hipSuccess) return MI_ERR_LAUNCH;
 

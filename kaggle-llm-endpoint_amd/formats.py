@@ -52,6 +52,36 @@ def iq3s_hbm_bytes(R, K):
     return R * (K // QK) * IQ3S_BLOCK_BYTES
 
 
+# ------------------------------------------------------------------------------------------------ IQ2_S
+IQ2S_BLOCK_BYTES = 82
+
+
+def iq2s_plane_rows(nblk):
+    """rows_p per expert (planes.py:60-61)."""
+    W = 8 * nblk
+    return {"qs": W, "sg": W, "qh": W // 4, "sc": W // 4, "d": (nblk + 1) // 2}
+
+
+def iq2s_pack_planes(blocks):
+    """uint8 [E, R, nblk, 82] GGUF IQ2_S blocks -> {plane: u32 [E*rows_p, R]} in the reference's planar layout
+    (field split of planes.py:157-158: d | qs | sg | qh | sc)."""
+    blocks = np.asarray(blocks, dtype=np.uint8)
+    E, R, nblk, bb = blocks.shape
+    if bb != IQ2S_BLOCK_BYTES:
+        raise ValueError("IQ2_S blocks are %d bytes, got %d" % (IQ2S_BLOCK_BYTES, bb))
+    d = blocks[..., 0:2].reshape(E, R, 2 * nblk)
+    if nblk % 2:
+        d = np.concatenate([d, np.zeros((E, R, 2), np.uint8)], axis=-1)
+    raw = {"qs": blocks[..., 2:34], "sg": blocks[..., 34:66], "qh": blocks[..., 66:74], "sc": blocks[..., 74:82]}
+    out = {k: _expert_major(_le_words(v)) for k, v in raw.items()}
+    out["d"] = _expert_major(np.ascontiguousarray(d).view("<u4"))
+    return {k: out[k] for k in ("qs", "sg", "qh", "sc", "d")}
+
+
+def iq2s_hbm_bytes(R, K):
+    return R * (K // QK) * IQ2S_BLOCK_BYTES
+
+
 # ------------------------------------------------------------------------------------------------ IQ4_XS
 IQ4XS_BLOCK_BYTES = 136
 

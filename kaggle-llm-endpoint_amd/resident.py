@@ -20,8 +20,11 @@ QK = 256
 
 
 def _plane_rows(qtype, K):
-    """IQ3_S / IQ4_XS: rows_p per expert of each plane [E*rows_p, R] (planes.py:56-70)."""
+    """IQ2_S / IQ3_S / IQ4_XS: rows_p per expert of each plane [E*rows_p, R] (planes.py:56-70)."""
     nblk = K // QK
+    if qtype == "IQ2_S":
+        W = 8 * nblk
+        return {"qs": W, "sg": W, "qh": W // 4, "sc": W // 4, "d": (nblk + 1) // 2}
     if qtype == "IQ3_S":
         W = 16 * nblk
         return {"qs": W, "sg": W // 2, "qh": W // 8, "sc": W // 16, "d": (nblk + 1) // 2}
@@ -132,6 +135,21 @@ def random_iq3s_table(E, R, K, generator, scale=0.02):
     bits = d.to(torch.float16).view(torch.int16).to(torch.int32) & 0xFFFF
     planes["d"] = (bits[..., 0] | (bits[..., 1] << 16)).contiguous()
     return ExpertTable("IQ3_S", planes, R, K)
+
+
+def random_iq2s_table(E, R, K, generator, scale=0.02):
+    """An ExpertTable of E random IQ2_S experts in the reference's planes, generated on the GPU: uniform random qs,
+    sg, qh and sc words (every bit pattern is a valid set of grid indices, signs and scales) and per-block f16 d
+    uniform in [scale / 2, scale].  For benchmarks at full shape."""
+    rp = _plane_rows("IQ2_S", K)
+    planes = {}
+    for k in ("qs", "sg", "qh", "sc"):
+        planes[k] = torch.randint(-2 ** 31, 2 ** 31 - 1, (E * rp[k], R), dtype=torch.int32, device="cuda",
+                                  generator=generator)
+    d = torch.rand((E * rp["d"], R, 2), device="cuda", generator=generator) * (0.5 * scale) + 0.5 * scale
+    bits = d.to(torch.float16).view(torch.int16).to(torch.int32) & 0xFFFF
+    planes["d"] = (bits[..., 0] | (bits[..., 1] << 16)).contiguous()
+    return ExpertTable("IQ2_S", planes, R, K)
 
 
 def random_iq4xs_table(E, R, K, generator, scale=0.02):
@@ -389,7 +407,8 @@ class ResidentFetch:
     apply(p, x, idx, w, layer, limit): x [N, D]; idx [N, k] int32 into E; w [N, k] f32 -> f32 [N, D] (routed experts
     only; the caller adds the shared expert, model.py:847-855).  N*k <= gather_max_rows takes the fused decode
     kernels (f32 end to end, resident.py:110-120); larger calls take the grouped prefill GEMMs with the reference's
-    bf16 rounding points and ``combine`` (resident.py:144-165; CB3, IQ3_S or IQ4_XS tables; bf16 ``out_dtype``).
+    bf16 rounding points and ``combine`` (resident.py:144-165; CB3, IQ2_S, IQ3_S or IQ4_XS tables; bf16
+    ``out_dtype``).
     ``use_pallas`` / ``interpret`` / ``sweep_mode`` / ``chunk`` are accepted for signature compatibility; there is a
     single MI355X kernel path per regime."""
 

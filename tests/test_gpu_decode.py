@@ -1,4 +1,4 @@
-"""GPU parity of the fused codebook-dequant kernels against the CPU oracle (CB3, IQ3_S and IQ4_XS tables).
+"""GPU parity of the fused codebook-dequant kernels against the CPU oracle (CB3, IQ2_S, IQ3_S and IQ4_XS tables).
 
 Bar: dequantized weights bit-exact; matvec / decode outputs within rel-L2 <= 1e-3 of the f64 oracle (the
 reference computes f32 end to end in decode, resident.py:114-120; the kernels reach ~1e-6 -- 1e-3 is the
@@ -23,7 +23,8 @@ def _t(a, dtype=None):
 
 @pytest.mark.parametrize("qtype,R,K", [("CB3", 256, 1280), ("CB3", 512, 2048), ("CB3", 256, 384),
                                        ("IQ3_S", 256, 512), ("IQ3_S", 512, 2048), ("IQ4_XS", 256, 512),
-                                       ("IQ4_XS", 512, 2048)])
+                                       ("IQ4_XS", 512, 2048), ("IQ2_S", 256, 512), ("IQ2_S", 512, 2048),
+                                       ("IQ2_S", 256, 768)])
 def test_dequant_bit_exact(pkg, gpu, qtype, R, K):
     rng = np.random.default_rng(11)
     L = Layer(rng, qtype, 3, K, R)                  # gate is R x K
@@ -68,7 +69,23 @@ def test_dequant_real_gguf_iq4xs(pkg, gpu):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
-@pytest.mark.parametrize("qtype", ["CB3", "IQ3_S", "IQ4_XS"])
+def test_dequant_real_gguf_iq2s(pkg, gpu):
+    """The reference's real IQ2_S sample (blk.3.ffn_gate_exps, 2 rows x 4096) tiled to 256 rows."""
+    import json
+    import os
+    from oracle import iq2s as oiq2
+    d = os.path.join(os.path.dirname(__file__), "golden", "gguf")
+    s = json.load(open(os.path.join(d, "gguf_samples.json")))["IQ2_S"]
+    raw = np.fromfile(os.path.join(d, s["file"]), np.uint8).reshape(s["rows"], s["ne0"] // 256, 82)
+    blocks = np.tile(raw, (256 // s["rows"], 1, 1))[None]
+    planes = pkg.to_device_planes(pkg.formats.iq2s_pack_planes(blocks))
+    tb = pkg.ExpertTable("IQ2_S", planes, 256, s["ne0"])
+    got = pkg.dequant(tb, 0).cpu().numpy()
+    want = oiq2.dequant_blocks(blocks[0]).reshape(256, s["ne0"])
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("qtype", ["CB3", "IQ2_S", "IQ3_S", "IQ4_XS"])
 @pytest.mark.parametrize("xdt", ["bf16", "f32"])
 def test_matvec_grouped(pkg, gpu, qtype, xdt):
     """moe_matvec semantics (pallas_moe.py:238-307): per-slot outputs, duplicate experts, an out-of-range id."""
@@ -87,7 +104,7 @@ def test_matvec_grouped(pkg, gpu, qtype, xdt):
     assert rel_l2(got, want) < 1e-5
 
 
-@pytest.mark.parametrize("qtype", ["CB3", "IQ3_S", "IQ4_XS"])
+@pytest.mark.parametrize("qtype", ["CB3", "IQ2_S", "IQ3_S", "IQ4_XS"])
 @pytest.mark.parametrize("N,k,E,routing", [(1, 8, 16, "softmax"), (4, 4, 12, "zipf"), (8, 8, 20, "zipf"),
                                            (16, 8, 24, "zipf"), (3, 2, 2, "zipf")])
 def test_decode_small(pkg, gpu, qtype, N, k, E, routing):
@@ -143,7 +160,8 @@ def test_resident_fetch_apply(pkg, gpu):
     assert rel_l2(y.cpu().numpy(), omoe.decode_apply(L.deq, x, idx, w, limit)) < 1e-5
 
 
-@pytest.mark.parametrize("qtype,down_qtype", [("IQ3_S", "IQ4_XS"), ("CB3", "IQ3_S"), ("IQ4_XS", "CB3")])
+@pytest.mark.parametrize("qtype,down_qtype", [("IQ3_S", "IQ4_XS"), ("CB3", "IQ3_S"), ("IQ4_XS", "CB3"),
+                                              ("IQ2_S", "IQ4_XS"), ("IQ2_S", "IQ3_S")])
 @pytest.mark.parametrize("N", [1, 8, 16])
 def test_decode_mixed_formats(pkg, gpu, qtype, down_qtype, N):
     """Gate/up in one format and down in another (the reference's layers mix formats per matrix kind)."""
