@@ -58,6 +58,14 @@ def iq3s_bytes(R, K):
     return R * (K // 256) * 110       # 110-byte blocks of 256 weights (the planes hold exactly these bytes)
 
 
+def iq4xs_bytes(R, K):
+    return R * (K // 256) * 136       # 136-byte blocks of 256 weights
+
+
+def iq2s_bytes(R, K):
+    return R * (K // 256) * 82        # 82-byte blocks of 256 weights
+
+
 def softmax_topk(rng, N, E, k):
     logits = rng.standard_normal((N, E))
     p = np.exp(logits - logits.max(-1, keepdims=True))
@@ -180,15 +188,29 @@ def main():
     shapes = (("gate", (INTER, D)), ("up", (INTER, D)), ("down", (D, INTER)))
     layers = [{name: pkg.random_cb3_table(E, R, K, gen) for name, (R, K) in shapes} for _ in range(L)]
     torch.cuda.synchronize()
-    iq3_layers = []                    # the reference's production format, for the IQ3_S lines (made on demand)
-    per_expert_iq3 = 2 * iq3s_bytes(INTER, D) + iq3s_bytes(D, INTER)
+    # the reference's GGUF formats, for their own lines; made on demand, one layout at a time.  A layout names the
+    # gate/up format and the down format ("iq2s_iq4xs": the production mix of the reference's GGUF layers).
+    makers = {"iq3s": (pkg.random_iq3s_table, iq3s_bytes), "iq4xs": (pkg.random_iq4xs_table, iq4xs_bytes),
+              "iq2s": (pkg.random_iq2s_table, iq2s_bytes)}
+    made = {}
 
-    def iq3():
-        if not iq3_layers:
-            iq3_layers.extend({name: pkg.random_iq3s_table(E, R, K, gen) for name, (R, K) in shapes}
-                              for _ in range(L))
+    def fmts(layout):
+        gu, _, dn = layout.partition("_")
+        return gu, dn or gu
+
+    def iq_layers(layout):
+        if layout not in made:
+            made.clear()
+            torch.cuda.empty_cache()
+            gu, dn = fmts(layout)
+            made[layout] = [{name: makers[dn if name == "down" else gu][0](E, R, K, gen) for name, (R, K) in shapes}
+                            for _ in range(L)]
             torch.cuda.synchronize()
-        return iq3_layers
+        return made[layout]
+
+    def iq_pe(layout):
+        gu, dn = fmts(layout)
+        return 2 * makers[gu][1](INTER, D) + makers[dn][1](D, INTER)
 
     rng = np.random.default_rng(2026)
     extra = {}
@@ -223,7 +245,12 @@ def main():
 
     if args.only_prefill:
         print(json.dumps({"prefill_t512": bench_prefill(torch, pkg, gen, args, layers, rng, per_expert),
-                          "prefill_t512_iq3s": bench_prefill(torch, pkg, gen, args, iq3(), rng, per_expert_iq3)}))
+                          "prefill_t512_iq3s": bench_prefill(torch, pkg, gen, args, iq_layers("iq3s"), rng,
+                                                             iq_pe("iq3s")),
+                          "prefill_t512_iq4xs": bench_prefill(torch, pkg, gen, args, iq_layers("iq4xs"), rng,
+                                                              iq_pe("iq4xs")),
+                          "prefill_t512_iq2s_iq4xs": bench_prefill(torch, pkg, gen, args, iq_layers("iq2s_iq4xs"),
+                                                                   rng, iq_pe("iq2s_iq4xs"))}))
         return
     # headline: batch 1 layer (mi_moe_decode)
     ms1, bytes1 = measure(1, softmax_topk)
@@ -243,14 +270,15 @@ def main():
             gbs = b / (ms * 1e-3) / 1e9
             extra["b%d" % N] = {"us_per_layer": round(ms * 1e3, 2), "GBps": round(gbs, 1),
                                 "pct_hbm": round(100 * gbs / HBM_PEAK_GBS, 1), "bytes_per_layer": int(b)}
-        # the reference's production format: IQ3_S tables (VALU decode path; matrix-core prefill)
-        for N, routing in ((1, softmax_topk), (8, zipf_topk)):
-            ms, b = measure(N, routing, tables=iq3(), pe=per_expert_iq3)
-            gbs = b / (ms * 1e-3) / 1e9
-            extra["b%d_iq3s" % N] = {"us_per_layer": round(ms * 1e3, 2), "GBps": round(gbs, 1),
-                                     "pct_hbm": round(100 * gbs / HBM_PEAK_GBS, 1), "bytes_per_layer": int(b)}
         extra["prefill_t512"] = bench_prefill(torch, pkg, gen, args, layers, rng, per_expert)
-        extra["prefill_t512_iq3s"] = bench_prefill(torch, pkg, gen, args, iq3(), rng, per_expert_iq3)
+        # the reference's GGUF formats: IQ3_S and IQ4_XS tables (decode and prefill on the matrix cores)
+        for fmt in ("iq3s", "iq4xs", "iq2s", "iq2s_iq4xs"):
+            for N, routing in ((1, softmax_topk), (8, zipf_topk)):
+                ms, b = measure(N, routing, tables=iq_layers(fmt), pe=iq_pe(fmt))
+                gbs = b / (ms * 1e-3) / 1e9
+                extra["b%d_%s" % (N, fmt)] = {"us_per_layer": round(ms * 1e3, 2), "GBps": round(gbs, 1),
+                                             "pct_hbm": round(100 * gbs / HBM_PEAK_GBS, 1), "bytes_per_layer": int(b)}
+            extra["prefill_t512_" + fmt] = bench_prefill(torch, pkg, gen, args, iq_layers(fmt), rng, iq_pe(fmt))
         extra["int8_b8"] = bench_int8(torch, pkg, gen, args)
         extra["cfg0_matvec"] = bench_matvec(torch, pkg, gen, args)
 
