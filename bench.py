@@ -280,6 +280,7 @@ def main():
                                              "pct_hbm": round(100 * gbs / HBM_PEAK_GBS, 1), "bytes_per_layer": int(b)}
             extra["prefill_t512_" + fmt] = bench_prefill(torch, pkg, gen, args, iq_layers(fmt), rng, iq_pe(fmt))
         extra["int8_b8"] = bench_int8(torch, pkg, gen, args)
+        extra["route"] = bench_route(torch, pkg, gen, args)
         extra["cfg0_matvec"] = bench_matvec(torch, pkg, gen, args)
 
     cpu = None if args.no_cpu else cpu_baseline()
@@ -340,6 +341,21 @@ def bench_prefill(torch, pkg, gen, args, layers, rng, per_expert, T=512):
     return {"us_per_layer": round(ms * 1e3, 1), "tokens_per_s": round(T / (ms * 1e-3), 0),
             "TFLOPs": round(tflops, 1), "pct_mfma_bf16_peak": round(100 * tflops / MFMA_BF16_PEAK_TFLOPS, 1),
             "weight_GBps": round(gbs, 1), "rows": rows, "steps": steps}
+
+
+def bench_route(torch, pkg, gen, args):
+    """Config: the MoE block's router (moe_route) over the benchmark layer's 64 routed experts, D = 6144, top-8 with
+    normalised, scaled weights, at 1, 8 and 512 tokens.  Work: the f32 router matrix (1.5 MB) read per call."""
+    out = {}
+    rw = torch.randn((D, E_ROUTED), device="cuda", generator=gen) / math.sqrt(D)
+    bias = torch.randn(E_ROUTED, device="cuda", generator=gen) * 0.05
+    for N in (1, 8, 512):
+        x = torch.randn((N, D), device="cuda", generator=gen).to(torch.bfloat16)
+        ws = torch.empty(pkg._lib.lib().mi_moe_route_workspace(N, D, E_ROUTED), dtype=torch.uint8, device="cuda")
+        fns = [lambda x=x, ws=ws: pkg.route(x, rw, bias, TOPK, True, 2.5, workspace=ws)]
+        ms = Timer(torch, fns).run(args.steps, args.warmup)
+        out["n%d" % N] = {"us": round(ms * 1e3, 2), "GBps": round(rw.numel() * 4 / (ms * 1e-3) / 1e9, 1)}
+    return out
 
 
 def bench_int8(torch, pkg, gen, args):

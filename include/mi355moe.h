@@ -10,6 +10,7 @@
  *   ResidentFetch.apply(p, x, idx, w, layer, limit)        resident.py:100-108   -> mi_moe_decode / mi_moe_prefill
  *   moe_matvec(planes, qtype, nblk, idx, X)                pallas_moe.py:238-307 -> mi_matvec
  *   ragged_plan(idx, w, E, tm)                             pallas_moe.py:564-592 -> mi_ragged_plan
+ *   moe_route(p, x, cfg)                                   model.py:798-808      -> mi_moe_route
  *   moe_ragged_gateup / moe_ragged_down                    pallas_moe.py:622-755 -> mi_moe_prefill
  *   dequant_planes (XLA dequant of the planar tables)      planes.py:196-206     -> mi_dequant
  *   quant8.dequant_tree + x @ W (int8 projections)         quant8.py:91-99       -> mi_int8_project(_many)
@@ -138,6 +139,21 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
  */
 int mi_moe_decode_plan(const mi_table *gate, const mi_table *down, int32_t N, int32_t k, int32_t shared_expert,
                        int32_t *info, int32_t n_info);
+
+/*
+ * The MoE block's router (moe_route, model.py:798-808), the step before ResidentFetch.apply (model.py:843-848):
+ *   logits = f32(x) @ router_w, scores = sigmoid(logits), idx = top_k(scores + bias, k) (largest first, equal values
+ *   lower expert id first, as lax.top_k), w = scores[idx], w /= (sum_j w + 1e-20) if norm_topk, w *= scaling.
+ * x bf16 [N, D] (4-byte aligned), router_w f32 [D, E] (the reference's layout), bias f32 [E] or NULL (zero);
+ * idx_out int32 [N, k], w_out f32 [N, k].  N <= 2^19, D even, E <= 1024, 1 <= k <= min(E, 32), norm_topk 0 or 1.
+ * f32 dot products (the reference's f32 matmul on its own hardware may round the logits differently: choices
+ * within a few ulps of each other can order differently).  Two launches; the workspace (mi_moe_route_workspace
+ * bytes) holds the partial logits and needs no initialisation.
+ */
+int mi_moe_route(const uint16_t *x_bf16, const float *router_w, const float *bias, int32_t N, int32_t D, int32_t E,
+                 int32_t k, int32_t norm_topk, float scaling, int32_t *idx_out, float *w_out, void *workspace,
+                 size_t workspace_bytes, void *stream);
+size_t mi_moe_route_workspace(int32_t N, int32_t D, int32_t E);
 
 /*
  * The reference's prefill slot layout (ragged_plan, pallas_moe.py:564-592), built on the device:

@@ -6,9 +6,9 @@ The directory name is not a Python identifier; it is imported as ``kaggle_llm_en
 """
 from . import _lib, formats  # noqa: F401
 from .resident import (ExpertTable, ResidentFetch, dequant, int8_project, int8_project_many, matvec,  # noqa: F401
-                       moe_decode, moe_prefill, ragged_plan, random_cb3_table, random_iq2s_table,
-                       random_iq3s_table, random_iq4xs_table, to_device_planes)
+                       moe_decode, moe_prefill, moe_route, ragged_plan, random_cb3_table, random_iq2s_table,
+                       random_iq3s_table, random_iq4xs_table, route, to_device_planes)
 
 __all__ = ["ExpertTable", "ResidentFetch", "dequant", "int8_project", "int8_project_many", "matvec", "moe_decode",
-           "moe_prefill", "ragged_plan", "random_cb3_table", "random_iq2s_table", "random_iq3s_table",
+           "moe_prefill", "moe_route", "ragged_plan", "route", "random_cb3_table", "random_iq2s_table", "random_iq3s_table",
            "random_iq4xs_table", "to_device_planes", "formats"]

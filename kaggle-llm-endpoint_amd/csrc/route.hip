@@ -1,0 +1,173 @@
+// Router of the GLM MoE block on gfx950: the reference's moe_route (model.py:798-808), the step that produces the
+// routing the expert kernels consume.
+//   logits = f32(x) @ f32(router_w)      x bf16 [N, D], router_w f32 [D, E] (the reference's layout, model.py:17)
+//   scores = sigmoid(logits)
+//   idx    = top_k(scores + bias, k)     largest first; equal values: the lower expert id first (lax.top_k)
+//   w      = scores[idx]; with norm_topk w / (sum_j w + 1e-20); times scaling
+// Two launches on the caller's stream:
+//   route_logits_kernel  partial logits per 256-column chunk of D and 16-token block: a lane owns one expert, its
+//                        router column is read coalesced across the wavefront (E consecutive floats per row of
+//                        router_w), the token rows are wave-uniform loads; the 4 wavefronts' column quarters are
+//                        summed in LDS in a fixed order;
+//   route_select_kernel  one wavefront per token: the chunk partials summed in chunk order, sigmoid, bias, k rounds
+//                        of a wavefront argmax (value, then lower id), the weights normalised and scaled.
+// Deterministic: every sum in a fixed order, no atomics.
+#include <math.h>
+
+#include "common.h"
+
+namespace mi {
+
+constexpr int kRouteDc = 256;                 // columns of D per logits workgroup (64 per wavefront)
+constexpr int kRouteTb = 16;                  // tokens per logits workgroup
+constexpr int kRouteMaxE = 1024;
+constexpr int kRouteMaxK = 32;
+constexpr int kRoutePer = kRouteMaxE / 64;    // experts per lane in the select kernel
+
+__device__ __forceinline__ float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t v) { return __uint_as_float(v & 0xffff0000u); }
+
+// part[c][t][e] = sum over the columns d of chunk c of f32(x[t][d]) * w[d][e]
+__global__ void __launch_bounds__(256) route_logits_kernel(const uint16_t *__restrict__ x,
+                                                           const float *__restrict__ w, int N, int D, int E,
+                                                           float *__restrict__ part) {
+    __shared__ float red[4][kRouteTb][65];
+    const int c = blockIdx.x, t0 = blockIdx.y * kRouteTb;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nt = min(kRouteTb, N - t0);
+    const int d0 = c * kRouteDc + wave * (kRouteDc / 4);
+    const int d1 = min(D, d0 + kRouteDc / 4);
+    for (int e0 = 0; e0 < E; e0 += 64) {
+        const int e = e0 + lane;
+        const bool live = e < E;
+        float acc[kRouteTb];
+#pragma unroll
+        for (int t = 0; t < kRouteTb; ++t) acc[t] = 0.0f;
+        for (int d = d0; d < d1; d += 2) {                       // D is even: whole bf16 pairs
+            const float w0 = live ? w[(size_t)d * E + e] : 0.0f;
+            const float w1 = live ? w[(size_t)(d + 1) * E + e] : 0.0f;
+#pragma unroll
+            for (int t = 0; t < kRouteTb; ++t) {
+                if (t < nt) {
+                    const uint32_t xx = *(const uint32_t *)(x + (size_t)(t0 + t) * D + d);
+                    acc[t] = fmaf(bf16_hi(xx), w1, fmaf(bf16_lo(xx), w0, acc[t]));
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < kRouteTb; ++t) red[wave][t][lane] = acc[t];
+        __syncthreads();
+        for (int i = threadIdx.x; i < nt * 64; i += 256) {
+            const int t = i >> 6, l = i & 63;
+            if (e0 + l < E) {
+                const float s = ((red[0][t][l] + red[1][t][l]) + red[2][t][l]) + red[3][t][l];
+                part[((size_t)c * N + t0 + t) * E + e0 + l] = s;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// (value, id) ordering of top_k: larger value first, equal values: lower id first
+__device__ __forceinline__ bool route_better(float v, int i, float v2, int i2) { return v > v2 || (v == v2 && i < i2); }
+
+__global__ void __launch_bounds__(256) route_select_kernel(const float *__restrict__ part, int nc,
+                                                           const float *__restrict__ bias, int N, int E, int k,
+                                                           int norm, float scaling, int32_t *__restrict__ idx,
+                                                           float *__restrict__ wout) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (t >= N) return;                                          // the whole wavefront
+    float sc[kRoutePer], ch[kRoutePer];
+#pragma unroll
+    for (int j = 0; j < kRoutePer; ++j) {
+        const int e = 64 * j + lane;
+        sc[j] = 0.0f;
+        ch[j] = -INFINITY;
+        if (e < E) {
+            float l = 0.0f;
+            for (int c = 0; c < nc; ++c) l += part[((size_t)c * N + t) * E + e];
+            const float s = 1.0f / (1.0f + expf(-l));
+            sc[j] = s;
+            ch[j] = s + (bias ? bias[e] : 0.0f);
+        }
+    }
+    int sel_i[kRouteMaxK];
+    float sel_w[kRouteMaxK];
+    float sum = 0.0f;
+#pragma unroll
+    for (int r = 0; r < kRouteMaxK; ++r) {
+        if (r >= k) break;
+        // the lane's best (its ids rise with j, so the first maximum is the lowest id)
+        float bv = -INFINITY, bs = 0.0f;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int j = 0; j < kRoutePer; ++j) {
+            const int e = 64 * j + lane;
+            if (e < E && route_better(ch[j], e, bv, bi)) {
+                bv = ch[j];
+                bi = e;
+                bs = sc[j];
+            }
+        }
+        // wavefront argmax; every lane ends with the winner
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) {
+            const float ov = __shfl_xor(bv, m), os = __shfl_xor(bs, m);
+            const int oi = __shfl_xor(bi, m);
+            if (route_better(ov, oi, bv, bi)) {
+                bv = ov;
+                bi = oi;
+                bs = os;
+            }
+        }
+        sel_i[r] = bi;
+        sel_w[r] = bs;
+        sum += bs;
+        // the owner drops the winner from later rounds
+#pragma unroll
+        for (int j = 0; j < kRoutePer; ++j)
+            if (64 * j + lane == bi) ch[j] = -INFINITY;
+    }
+    const float inv = norm ? 1.0f / (sum + 1e-20f) : 1.0f;
+#pragma unroll
+    for (int r = 0; r < kRouteMaxK; ++r) {
+        if (r >= k) break;
+        if (lane == r) {
+            idx[(size_t)t * k + r] = sel_i[r];
+            const float v = norm ? sel_w[r] * inv : sel_w[r];
+            wout[(size_t)t * k + r] = v * scaling;
+        }
+    }
+}
+
+static int route_chunks(int D) { return (D + kRouteDc - 1) / kRouteDc; }
+
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" size_t mi_moe_route_workspace(int32_t N, int32_t D, int32_t E) {
+    if (N <= 0 || D <= 0 || E <= 0) return 0;
+    return (size_t)route_chunks(D) * (size_t)N * (size_t)E * sizeof(float);
+}
+
+extern "C" int mi_moe_route(const uint16_t *x_bf16, const float *router_w, const float *bias, int32_t N, int32_t D,
+                            int32_t E, int32_t k, int32_t norm_topk, float scaling, int32_t *idx_out, float *w_out,
+                            void *workspace, size_t workspace_bytes, void *stream) {
+    if (!x_bf16 || !router_w || !idx_out || !w_out) return MI_ERR_NULL;
+    if (N <= 0 || N > (1 << 19)) return MI_ERR_TOKENS;
+    if (D <= 0 || D % 2 || E <= 0 || E > kRouteMaxE || (long long)D * E >= (1ll << 31)) return MI_ERR_SHAPE;
+    if ((uintptr_t)x_bf16 % 4) return MI_ERR_ARG;             // the rows are read as bf16 pairs
+    if (k <= 0 || k > E || k > kRouteMaxK || (norm_topk != 0 && norm_topk != 1)) return MI_ERR_ARG;
+    const size_t need = mi_moe_route_workspace(N, D, E);
+    if (!workspace || workspace_bytes < need) return MI_ERR_WORKSPACE;
+    hipStream_t s = (hipStream_t)stream;
+    float *part = (float *)workspace;
+    const int nc = route_chunks(D);
+    hipLaunchKernelGGL(route_logits_kernel, dim3(nc, (N + kRouteTb - 1) / kRouteTb), dim3(256), 0, s, x_bf16,
+                       router_w, N, D, E, part);
+    if (hipGetLastError() != hipSuccess) return MI_ERR_LAUNCH;
+    hipLaunchKernelGGL(route_select_kernel, dim3((N + 3) / 4), dim3(256), 0, s, (const float *)part, nc, bias, N, E,
+                       k, norm_topk, scaling, idx_out, w_out);
+    return hipGetLastError() == hipSuccess ? MI_OK : MI_ERR_LAUNCH;
+}

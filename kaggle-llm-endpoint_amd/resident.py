@@ -313,6 +313,37 @@ def ragged_plan(idx, w, E, tm):
     return out
 
 
+def route(x, router_w, bias, k, norm_topk=True, scaling=1.0, workspace=None):
+    """The router (moe_route, model.py:798-808) on the device: x bf16 [N, D], router_w f32 [D, E], bias f32 [E] or
+    None -> (idx int32 [N, k], w f32 [N, k]).  sigmoid scores, top-k of scores + bias (lower id first on equal
+    values), weights = scores (renormalised over the k with ``norm_topk``) times ``scaling``."""
+    if x.dtype != torch.bfloat16:
+        x = x.to(torch.bfloat16)
+    x = x.contiguous()
+    router_w = router_w.to(torch.float32).contiguous()
+    if bias is not None:
+        bias = bias.to(torch.float32).contiguous()
+    N, D = x.shape
+    E = router_w.shape[1]
+    if router_w.shape[0] != D or (bias is not None and tuple(bias.shape) != (E,)):
+        raise ValueError("route: router_w must be [D, E] = [%d, E] and bias [E]" % D)
+    need = lib().mi_moe_route_workspace(N, D, E)
+    if workspace is None:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+    idx = torch.empty((N, k), dtype=torch.int32, device=x.device)
+    w = torch.empty((N, k), dtype=torch.float32, device=x.device)
+    check("mi_moe_route", lib().mi_moe_route(_ptr(x), _ptr(router_w), _ptr(bias), N, D, E, int(k),
+                                             1 if norm_topk else 0, float(scaling), _ptr(idx), _ptr(w),
+                                             _ptr(workspace), workspace.numel(), _stream()))
+    return idx, w
+
+
+def moe_route(p, x, cfg):
+    """The reference's moe_route(p, x, cfg) (model.py:798-808): p["router_w"] [D, E], p["router_bias"] [E];
+    cfg.topk, cfg.norm_topk, cfg.scaling -> (idx int32 [N, k], w f32 [N, k])."""
+    return route(x, p["router_w"], p.get("router_bias"), cfg.topk, cfg.norm_topk, cfg.scaling)
+
+
 def prefill_workspace_bytes(gate, down, T, k, shared_expert=-1):
     n = lib().mi_moe_prefill_workspace(gate.c, down.c, int(T), int(k), int(shared_expert))
     if n == 0:

@@ -62,6 +62,21 @@ def shared_apply(deq_shared, x, limit):
 
 
 # ------------------------------------------------------------------------------------------------ prefill
+def route(x, router_w, bias, k, norm_topk=True, scaling=1.0):
+    """Restates moe_route (model.py:798-808) in f64: logits = x @ router_w ([N, D] @ [D, E]), scores = sigmoid,
+    idx = top_k(scores + bias, k) with lax.top_k's order (larger first, equal values: lower index first, here a
+    stable sort), w = scores[idx], renormalised over the k (+1e-20) with norm_topk, times scaling.
+    -> (idx int32 [N, k], w f64 [N, k], choice f64 [N, E])."""
+    logits = np.asarray(x, np.float64) @ np.asarray(router_w, np.float64)
+    scores = 1.0 / (1.0 + np.exp(-logits))
+    choice = scores + (0.0 if bias is None else np.asarray(bias, np.float64))
+    order = np.argsort(-choice, axis=-1, kind="stable")[:, :k]
+    w = np.take_along_axis(scores, order, -1)
+    if norm_topk:
+        w = w / (w.sum(-1, keepdims=True) + 1e-20)
+    return order.astype(np.int32), w * scaling, choice
+
+
 def ragged_plan(idx, w, E, tm):
     """Restates pallas_moe.ragged_plan (pallas_moe.py:564-592) in numpy.  idx int [T, k], w f32 [T, k] ->
     dict(blk_expert int32 [G], n_blocks int32 [1], tok_row int32 [Rp] (-1 pad), w_row f32 [Rp],

@@ -112,3 +112,25 @@ def test_prefill_host_validation(L, pkg):
     assert plan(E=0) == 8 and plan(E=1025) == 8 and plan(tm=0) == 8              # MI_ERR_ARG
     assert plan(T=0) == 4 and plan(T=1 << 21, k=4) == 4                          # MI_ERR_TOKENS
     assert plan(i=None) == 1                                                     # MI_ERR_NULL
+
+
+def test_route_host_validation(L):
+    """mi_moe_route rejects bad shapes and arguments before any launch (fake, aligned device pointers)."""
+    P = ctypes.c_void_p
+    x, rw, idx, w, ws = P(0x1000), P(0x2000), P(0x3000), P(0x4000), P(0x5000)
+    need = L.mi_moe_route_workspace(4, 6144, 64)
+    assert need == 24 * 4 * 64 * 4                              # 256-column chunks x N x E floats
+
+    def call(N=4, D=6144, E=64, k=8, norm=1, x_=x, ws_bytes=need, idx_=idx):
+        return L.mi_moe_route(x_, rw, None, N, D, E, k, norm, 2.5, idx_, w, ws, ws_bytes, None)
+
+    assert call(x_=None) == 1                                    # MI_ERR_NULL
+    assert call(idx_=None) == 1
+    assert call(N=0) == 4                                        # MI_ERR_TOKENS
+    assert call(D=6143) == 3                                     # MI_ERR_SHAPE: odd D
+    assert call(E=1025) == 3
+    assert call(k=0) == 8 and call(k=65, E=64) == 8 and call(k=33, E=256) == 8   # MI_ERR_ARG
+    assert call(norm=2) == 8
+    assert call(x_=P(0x1002)) == 8                               # rows read as bf16 pairs: 4-byte alignment
+    assert call(ws_bytes=need - 1) == 5                          # MI_ERR_WORKSPACE
+    assert L.mi_moe_route_workspace(0, 6144, 64) == 0

@@ -142,3 +142,53 @@ def test_prefill_flow_agrees_with_decode_at_bf16_tolerance():
     a = moe.prefill_apply(deq, x, idx, w, L, E, tm=4, combine="matmul")
     b = moe.prefill_apply(deq, x, idx, w, L, E, tm=4, combine="gather")
     assert ob.rel_l2(a, b) < 1e-2
+
+
+def _route_brute(x, rw, bias, k, norm, scaling):
+    """moe_route by k rounds of an explicit argmax (first maximum = lowest id), with torch's sigmoid."""
+    logits = torch.from_numpy(np.asarray(x, np.float64)) @ torch.from_numpy(np.asarray(rw, np.float64))
+    scores = torch.sigmoid(logits).numpy()
+    choice = scores + (0.0 if bias is None else np.asarray(bias, np.float64))
+    idx, w = [], []
+    for n in range(choice.shape[0]):
+        c = list(choice[n])
+        row_i = []
+        for _ in range(k):
+            best = max(range(len(c)), key=lambda e: (c[e], -e))
+            row_i.append(best)
+            c[best] = -np.inf
+        ws = [scores[n, e] for e in row_i]
+        if norm:
+            tot = sum(ws)
+            ws = [v / (tot + 1e-20) for v in ws]
+        idx.append(row_i)
+        w.append([v * scaling for v in ws])
+    return np.array(idx, np.int32), np.array(w)
+
+
+@pytest.mark.parametrize("norm", [True, False])
+def test_route_equals_argmax_rounds(norm):
+    rng = np.random.default_rng(8)
+    N, D, E, k = 6, 40, 12, 4
+    x = ob.round_bf16(rng.standard_normal((N, D)).astype(np.float32))
+    rw = rng.standard_normal((D, E)).astype(np.float32) * 0.2
+    bias = rng.standard_normal(E).astype(np.float32) * 0.1
+    i1, w1, _ = moe.route(x, rw, bias, k, norm, 2.5)
+    i2, w2 = _route_brute(x, rw, bias, k, norm, 2.5)
+    assert np.array_equal(i1, i2)
+    np.testing.assert_allclose(w1, w2, rtol=1e-13)
+    if norm:
+        np.testing.assert_allclose(w1.sum(-1), 2.5, rtol=1e-12)
+
+
+def test_route_ties_bias_and_weights():
+    """Equal choices: lower id first (lax.top_k).  The bias moves the selection, the weights stay the scores."""
+    E, k = 10, 3
+    x = np.zeros((2, 8), np.float32)
+    rw = np.zeros((8, E), np.float32)
+    idx, w, _ = moe.route(x, rw, None, k, True, 1.0)              # every score 0.5, every choice equal
+    assert idx.tolist() == [[0, 1, 2]] * 2 and np.allclose(w, 1.0 / 3)
+    bias = np.zeros(E, np.float32)
+    bias[[7, 4, 9]] = [3.0, 2.0, 1.0]
+    idx, w, _ = moe.route(x, rw, bias, k, False, 2.0)
+    assert idx.tolist() == [[7, 4, 9]] * 2 and np.allclose(w, 0.5 * 2.0)
