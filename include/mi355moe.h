@@ -11,6 +11,7 @@
  *   moe_matvec(planes, qtype, nblk, idx, X)                pallas_moe.py:238-307 -> mi_matvec
  *   ragged_plan(idx, w, E, tm)                             pallas_moe.py:564-592 -> mi_ragged_plan
  *   moe_route(p, x, cfg)                                   model.py:798-808      -> mi_moe_route
+ *   pack_layer_from_gguf / pack_planes                     resident.py:29-60, planes.py:136-170 -> mi_pack_planes
  *   moe_ragged_gateup / moe_ragged_down                    pallas_moe.py:622-755 -> mi_moe_prefill
  *   dequant_planes (XLA dequant of the planar tables)      planes.py:196-206     -> mi_dequant
  *   quant8.dequant_tree + x @ W (int8 projections)         quant8.py:91-99       -> mi_int8_project(_many)
@@ -139,6 +140,15 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
  */
 int mi_moe_decode_plan(const mi_table *gate, const mi_table *down, int32_t N, int32_t k, int32_t shared_expert,
                        int32_t *info, int32_t n_info);
+
+/*
+ * GGUF blocks -> the reference's planar tables, on the device (planes.py:136-170 as resident.py:29-60 applies it
+ * when loading a layer): blocks = one expert tensor as stored in the file, u8 [E][R][K/256][block bytes] (2-byte
+ * aligned); planes = the table's plane pointers in mi_table order, u32 [E * rows_p, R] each (IQ2_S / IQ3_S: 5
+ * planes, IQ4_XS: 4).  Bit-exact byte movement, one launch.  E <= 65535, K % 256 == 0.
+ */
+int mi_pack_planes(int32_t qtype, const uint8_t *blocks, int32_t E, int32_t R, int32_t K, void *const *planes,
+                   void *stream);
 
 /*
  * The MoE block's router (moe_route, model.py:798-808), the step before ResidentFetch.apply (model.py:843-848):

@@ -4,11 +4,11 @@ loaded with ctypes, and the reference's ``ResidentFetch`` operator interface on 
 The directory name is not a Python identifier; it is imported as ``kaggle_llm_endpoint_amd`` through
 ``load_package()`` of ``__graft_entry__`` / ``tests/conftest.py``.
 """
-from . import _lib, formats  # noqa: F401
+from . import _lib, formats, gguf  # noqa: F401
 from .resident import (ExpertTable, ResidentFetch, dequant, int8_project, int8_project_many, matvec,  # noqa: F401
-                       moe_decode, moe_prefill, moe_route, ragged_plan, random_cb3_table, random_iq2s_table,
+                       moe_decode, moe_prefill, moe_route, pack_planes_device, ragged_plan, random_cb3_table, random_iq2s_table,
                        random_iq3s_table, random_iq4xs_table, route, to_device_planes)
 
 __all__ = ["ExpertTable", "ResidentFetch", "dequant", "int8_project", "int8_project_many", "matvec", "moe_decode",
-           "moe_prefill", "moe_route", "ragged_plan", "route", "random_cb3_table", "random_iq2s_table", "random_iq3s_table",
+           "moe_prefill", "moe_route", "pack_planes_device", "ragged_plan", "route", "gguf", "random_cb3_table", "random_iq2s_table", "random_iq3s_table",
            "random_iq4xs_table", "to_device_planes", "formats"]

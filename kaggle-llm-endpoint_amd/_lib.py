@@ -30,7 +30,8 @@ PLANE_KEYS = {"CB3": ("qs", "cb"), "IQ3_S": ("qs", "sg", "qh", "sc", "d"), "IQ4_
 EXPORTS = ("mi_matvec", "mi_matvec_workspace", "mi_moe_decode", "mi_moe_decode_fused", "mi_moe_decode_phases",
            "mi_moe_decode_workspace", "mi_moe_decode_plan",
            "mi_ragged_plan", "mi_moe_prefill", "mi_moe_prefill_workspace", "mi_dequant", "mi_int8_project", "mi_int8_project_workspace", "mi_int8_project_many",
-           "mi_int8_project_many_workspace", "mi_moe_route", "mi_moe_route_workspace", "mi_strerror", "mi_version")
+           "mi_int8_project_many_workspace", "mi_moe_route", "mi_moe_route_workspace", "mi_pack_planes", "mi_strerror",
+           "mi_version")
 
 
 class MiTable(ctypes.Structure):
@@ -81,6 +82,7 @@ def lib():
         "mi_int8_project_many_workspace": (Z, [I, I, ctypes.POINTER(ctypes.c_int32), I]),
         "mi_moe_route": (I, [P, P, P, I, I, I, I, I, F, P, P, P, Z, P]),
         "mi_moe_route_workspace": (Z, [I, I, I]),
+        "mi_pack_planes": (I, [I, P, I, I, I, ctypes.POINTER(ctypes.c_void_p), P]),
         "mi_strerror": (ctypes.c_char_p, [I]),
         "mi_version": (I, []),
     }

@@ -313,6 +313,24 @@ def ragged_plan(idx, w, E, tm):
     return out
 
 
+def pack_planes_device(blocks, qtype, E, R, K):
+    """GGUF blocks on the device (u8 tensor holding [E][R][K/256][block bytes], the expert tensor as stored) -> the
+    reference's planes {plane: int32 [E * rows_p, R]} (planes.py:136-170), split on the device by mi_pack_planes."""
+    if qtype not in ("IQ2_S", "IQ3_S", "IQ4_XS"):
+        raise ValueError(qtype)
+    bb = {"IQ2_S": 82, "IQ3_S": 110, "IQ4_XS": 136}[qtype]
+    if blocks.dtype != torch.uint8 or blocks.numel() != E * R * (K // QK) * bb or K % QK:
+        raise ValueError("pack_planes_device: %d bytes are not %d x %d %s weights" % (blocks.numel(), R, K, qtype))
+    blocks = blocks.contiguous()
+    rp = _plane_rows(qtype, K)
+    keys = _lib.PLANE_KEYS[qtype]
+    planes = {k: torch.empty((E * rp[k], R), dtype=torch.int32, device=blocks.device) for k in keys}
+    arr = (ctypes.c_void_p * len(keys))(*[planes[k].data_ptr() for k in keys])
+    check("mi_pack_planes", lib().mi_pack_planes(_lib.QTYPES[qtype], _ptr(blocks), int(E), int(R), int(K), arr,
+                                                 _stream()))
+    return planes
+
+
 def route(x, router_w, bias, k, norm_topk=True, scaling=1.0, workspace=None):
     """The router (moe_route, model.py:798-808) on the device: x bf16 [N, D], router_w f32 [D, E], bias f32 [E] or
     None -> (idx int32 [N, k], w f32 [N, k]).  sigmoid scores, top-k of scores + bias (lower id first on equal
