@@ -42,6 +42,8 @@ extern "C" {
 #define MI_QT_IQ3_S  2   /* llama.cpp IQ3_S in the reference's planar tables (planes.py:22-25)                   */
 #define MI_QT_IQ4_XS 3   /* llama.cpp IQ4_XS in the reference's planar tables (planes.py:26-28)                  */
 #define MI_QT_IQ2_S  4   /* llama.cpp IQ2_S in the reference's planar tables (planes.py:17-21)                   */
+#define MI_QT_Q2_K   5   /* ggml Q2_K (the MTP layer's experts) in the reference's planar tables (planes.py:34-41) */
+#define MI_QT_Q3_K   6   /* ggml Q3_K, likewise                                                                  */
 
 /*
  * One expert table: E experts of one matrix kind (gate, up or down), every expert R rows x K inputs.  plane[] order:
@@ -49,6 +51,8 @@ extern "C" {
  *                                          on the minor axis (planes.py:5-14,45).  R % 64 == 0, K % 256 == 0.
  *   MI_QT_IQ4_XS: {qs, sl, sh, d}       -- likewise (planes.py:26-28,46).  R % 64 == 0, K % 256 == 0.
  *   MI_QT_IQ2_S : {qs, sg, qh, sc, d}   -- likewise (planes.py:17-21,45).  R % 64 == 0, K % 256 == 0.
+ *   MI_QT_Q2_K  : {qs, sc, d}           -- likewise (planes.py:34-41,46).  R % 64 == 0, K % 256 == 0.
+ *   MI_QT_Q3_K  : {qs, hm, sc, d}       -- likewise (sc: the 16 six-bit scales unpacked to bytes).
  *   MI_QT_CB3   : {qs, cb}              -- qs: u32 [E][ceil(K/160)][R/16][64][4] code tiles (16 rows x 160 columns,
  *                                          1 KB each, in the lane order of the matrix-core decoder; formats.py
  *                                          cb3_tile_words gives the bit map); cb: u32 [E][K/128][R][4] = bytes

@@ -13,6 +13,8 @@ MI_QT_CB3 = 1
 MI_QT_IQ3_S = 2
 MI_QT_IQ4_XS = 3
 MI_QT_IQ2_S = 4
+MI_QT_Q2_K = 5
+MI_QT_Q3_K = 6
 MI_X_BF16 = 0
 MI_X_F32 = 1
 MI_MAX_SLOTS = 128
@@ -22,9 +24,10 @@ MI_COMBINE_GATHER = 1
 COMBINES = {"matmul": MI_COMBINE_MATMUL, "gather": MI_COMBINE_GATHER}
 PREFILL_TM = 80              # rows per block of mi_moe_prefill's own plan
 
-QTYPES = {"CB3": MI_QT_CB3, "IQ3_S": MI_QT_IQ3_S, "IQ4_XS": MI_QT_IQ4_XS, "IQ2_S": MI_QT_IQ2_S}
+QTYPES = {"CB3": MI_QT_CB3, "IQ3_S": MI_QT_IQ3_S, "IQ4_XS": MI_QT_IQ4_XS, "IQ2_S": MI_QT_IQ2_S, "Q2_K": MI_QT_Q2_K,
+          "Q3_K": MI_QT_Q3_K}
 PLANE_KEYS = {"CB3": ("qs", "cb"), "IQ3_S": ("qs", "sg", "qh", "sc", "d"), "IQ4_XS": ("qs", "sl", "sh", "d"),
-              "IQ2_S": ("qs", "sg", "qh", "sc", "d")}
+              "IQ2_S": ("qs", "sg", "qh", "sc", "d"), "Q2_K": ("qs", "sc", "d"), "Q3_K": ("qs", "hm", "sc", "d")}
 
 # every symbol the header declares (tests check the library exports them)
 EXPORTS = ("mi_matvec", "mi_matvec_workspace", "mi_moe_decode", "mi_moe_decode_fused", "mi_moe_decode_phases",

@@ -31,7 +31,7 @@ UNITS = [("moe_decode.hip", [], "moe_decode"), ("int8_project.hip", [], "int8_pr
          ("prefill.hip", [], "prefill"), ("route.hip", [], "route"),
          ("pack.hip", [], "pack")]
 UNITS += [("k_grouped.hip", ["-DMI_KMODE=%d" % m, "-DMI_KQT=%d" % q], "k_grouped_%d_%d" % (m, q))
-          for m in (0, 1, 2) for q in (1, 2, 3, 4)]
+          for m in (0, 1, 2) for q in (1, 2, 3, 4, 5, 6)]
 UNITS += [("k_fused.hip", [], "k_fused")]
 UNITS += [("k_pstream.hip", ["-DMI_PMODE=%d" % m, "-DMI_PTC=%d" % tc], "k_pstream_%d_%d" % (m, tc))
           for m in (0, 1) for tc in (8, 16)]

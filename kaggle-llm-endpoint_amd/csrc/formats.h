@@ -37,4 +37,14 @@ struct Iq2Table {
     static constexpr int kUnitCols = 256;
 };
 
+// The reference's planar K-quant tables (planes.py:34-41): qs u32 [16 nblk, R] (word w: byte j holds the 2-bit values
+// of inputs 256 b + 128 n + 32 s + 4 (w % 8) + j at shift 2s, b = w / 16, n = (w % 16) / 8); sc u32 [4 nblk, R]
+// (the block's 16 scale bytes); d u32 [nblk, R] (f16 d | f16 dmin << 16 for Q2_K); Q3_K also hm u32 [8 nblk, R]
+// (the hmask bytes: bit 4n + s of byte l).
+struct KqTable {
+    const uint32_t *qs, *sc, *d, *hm;       // hm: Q3_K only
+    int R, K, nblk;
+    static constexpr int kUnitCols = 256;
+};
+
 }  // namespace mi

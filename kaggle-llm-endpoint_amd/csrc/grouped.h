@@ -19,6 +19,7 @@
 #include "formats.h"
 #include "iq2_mfma.h"
 #include "iq4_mfma.h"
+#include "kq_mfma.h"
 
 namespace mi {
 
@@ -41,6 +42,7 @@ struct Table {
     Iq3Table iq3;
     Iq4Table iq4;
     Iq2Table iq2;
+    KqTable kq;
 };
 
 struct KArgs {
@@ -154,7 +156,8 @@ __host__ __device__ constexpr int wave_rows() { return QT == MI_QT_CB3 ? 16 * RT
 #ifndef MI_CB3_WAVES
 #define MI_CB3_WAVES 3
 #endif
-// IQ2_S holds two partials per row tile and k-step (two scale groups per word): 2 wavefronts per SIMD (<= 256 VGPRs).
+// IQ2_S holds two partials per row tile and k-step (two scale groups per word) beside its LDS grid entries: 2
+// wavefronts per SIMD (<= 256 VGPRs).  The K-quant decoders fit the common bound.
 template <int QT>
 __host__ __device__ constexpr int min_waves_per_simd() { return QT == MI_QT_IQ2_S ? 2 : MI_CB3_WAVES; }
 
@@ -165,8 +168,11 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
     // IQ3_S, IQ2_S: grid and sign tables; IQ4_XS: the level-pair table
     __shared__ typename std::conditional<
         QT == MI_QT_IQ3_S, Iq3Lds,
-        typename std::conditional<QT == MI_QT_IQ4_XS, Iq4Lds,
-                                  typename std::conditional<QT == MI_QT_IQ2_S, Iq2Lds, char>::type>::type>::type iq;
+        typename std::conditional<
+            QT == MI_QT_IQ4_XS, Iq4Lds,
+            typename std::conditional<QT == MI_QT_IQ2_S, Iq2Lds,
+                                      typename std::conditional<(QT == MI_QT_Q2_K || QT == MI_QT_Q3_K), KqLds,
+                                                                char>::type>::type>::type>::type iq;
     __shared__ uint4 cbl[QT == MI_QT_CB3 ? kWgWaves * 5 * 64 : 1];   // CB3: per-wavefront codebook slots
     __shared__ int s_tok[kMaxT];
 
@@ -188,6 +194,7 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
     if constexpr (QT == MI_QT_IQ3_S) iq3_fill_lds(iq, kGridConst);
     if constexpr (QT == MI_QT_IQ4_XS) iq4_fill_lds(iq, kKvConst);
     if constexpr (QT == MI_QT_IQ2_S) iq2_fill_lds(iq, kGrid2Const);
+    if constexpr (QT == MI_QT_Q2_K || QT == MI_QT_Q3_K) kq_fill_lds(iq);
 
     // column range of the split; CB3 stages its padded column tiles (columns >= K are zero)
     const int ucols = cb3 ? Cb3Table::kUnitCols : 256;      // IQ formats: 256-weight blocks
@@ -312,6 +319,14 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
         else
             iq3m_run_and_store<false, TCMAX>(tb.iq3, e, rg * WR, u0, u1, c0, iq, xh, xl, xsp, a.t_rows, n, s_tok,
                                              part_base, a.R, stage);
+    } else if constexpr (QT == MI_QT_Q2_K || QT == MI_QT_Q3_K) {
+        constexpr bool q3 = QT == MI_QT_Q3_K;
+        if (hilo)
+            kqm_run_and_store<true, TCMAX, q3>(tb.kq, e, rg * WR, u0, u1, c0, iq, xh, xl, xsp, a.t_rows, n, s_tok,
+                                               part_base, a.R, stage);
+        else
+            kqm_run_and_store<false, TCMAX, q3>(tb.kq, e, rg * WR, u0, u1, c0, iq, xh, xl, xsp, a.t_rows, n, s_tok,
+                                                part_base, a.R, stage);
     } else if constexpr (QT == MI_QT_IQ2_S) {
         if (hilo)
             iq2m_run_and_store<true, TCMAX>(tb.iq2, e, rg * WR, u0, u1, c0, iq, xh, xl, xsp, a.t_rows, n, s_tok,

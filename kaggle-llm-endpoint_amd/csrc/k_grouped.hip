@@ -1,6 +1,6 @@
 // One (mode, format) instantiation set of the grouped kernels, compiled once per combination by build.py with
-// -DMI_KMODE=<0 gate/up, 1 down, 2 matvec> -DMI_KQT=<1 CB3, 2 IQ3_S, 3 IQ4_XS, 4 IQ2_S>; exports
-// launch_grouped_<mode>_<qt>.
+// -DMI_KMODE=<0 gate/up, 1 down, 2 matvec> -DMI_KQT=<1 CB3, 2 IQ3_S, 3 IQ4_XS, 4 IQ2_S, 5 Q2_K, 6 Q3_K>;
+// exports launch_grouped_<mode>_<qt>.
 #include "grouped.h"
 
 #ifndef MI_KMODE

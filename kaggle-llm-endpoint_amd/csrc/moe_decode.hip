@@ -13,11 +13,13 @@ __global__ void dequant_kernel(Table tb, int e, float *out) {
     const int R = tb.qtype == MI_QT_CB3    ? tb.cb3.R
                   : tb.qtype == MI_QT_IQ3_S  ? tb.iq3.R
                   : tb.qtype == MI_QT_IQ4_XS ? tb.iq4.R
-                                             : tb.iq2.R;
+                  : tb.qtype == MI_QT_IQ2_S  ? tb.iq2.R
+                                             : tb.kq.R;
     const int K = tb.qtype == MI_QT_CB3    ? tb.cb3.K
                   : tb.qtype == MI_QT_IQ3_S  ? tb.iq3.K
                   : tb.qtype == MI_QT_IQ4_XS ? tb.iq4.K
-                                             : tb.iq2.K;
+                  : tb.qtype == MI_QT_IQ2_S  ? tb.iq2.K
+                                             : tb.kq.K;
     const int per_row = K / 16;
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (long long)R * per_row) return;
@@ -45,6 +47,25 @@ __global__ void dequant_kernel(Table tb, int e, float *out) {
             const uint32_t lo = cw[code >> 2], hi = cw[2 + (code >> 2)];
             const uint32_t sh = 8 * (code & 3u);
             v = bf16_to_f32(((lo >> sh) & 255u) | (((hi >> sh) & 255u) << 8));
+        } else if (tb.qtype == MI_QT_Q2_K || tb.qtype == MI_QT_Q3_K) {
+            // column c = 256 b + 128 n + 32 s + l (l = 4 q' + j): qs word 16 b + 8 n + q', byte j, shift 2s;
+            // scale byte 8 n + 2 s + (l >= 16); Q3_K hmask byte l, bit 4 n + s
+            const KqTable &t = tb.kq;
+            const int b = c >> 8, n = (c >> 7) & 1, s = (c >> 5) & 3, l = c & 31, j = l & 3;
+            const uint32_t q = t.qs[((size_t)e * 16 * t.nblk + 16 * b + 8 * n + (l >> 2)) * Rz + r];
+            const float vq = (float)((q >> (8 * j + 2 * s)) & 3u);
+            const int is = 8 * n + 2 * s + (l >= 16 ? 1 : 0);
+            const uint32_t scb = (t.sc[((size_t)e * 4 * t.nblk + 4 * b + (is >> 2)) * Rz + r] >> (8 * (is & 3))) & 255u;
+            const uint32_t dw = t.d[((size_t)e * t.nblk + b) * Rz + r];
+            if (tb.qtype == MI_QT_Q2_K) {
+                const float dl = f16_bits_to_f32(dw & 0xffffu) * (float)(scb & 15u);
+                const float ml = f16_bits_to_f32(dw >> 16) * (float)(scb >> 4);
+                v = dl * vq - ml;                                   // dl * vq is exact: one rounding
+            } else {
+                const uint32_t hmb = (t.hm[((size_t)e * 8 * t.nblk + 8 * b + (l >> 2)) * Rz + r] >> (8 * j)) & 255u;
+                const float hb = (float)((hmb >> (4 * n + s)) & 1u);
+                v = f16_bits_to_f32(dw & 0xffffu) * ((float)scb - 32.0f) * (vq - 4.0f * (1.0f - hb));
+            }
         } else if (tb.qtype == MI_QT_IQ2_S) {
             // column c: word w, group j, position k (c = 32 w + 8 j + k); block w / 8
             const Iq2Table &t = tb.iq2;
@@ -203,8 +224,7 @@ __global__ void split_reduce_kernel(const float *__restrict__ part, int S, int N
 // ------------------------------------------------------------------------------------------------ host side
 static int validate_table(const mi_table *t) {
     if (!t) return MI_ERR_NULL;
-    if (t->qtype != MI_QT_CB3 && t->qtype != MI_QT_IQ3_S && t->qtype != MI_QT_IQ4_XS && t->qtype != MI_QT_IQ2_S)
-        return MI_ERR_QTYPE;
+    if (t->qtype < MI_QT_CB3 || t->qtype > MI_QT_Q3_K) return MI_ERR_QTYPE;
     if (t->rows <= 0 || t->rows % (t->qtype == MI_QT_CB3 ? kCb3RowAlign : kIq3WaveRows)) return MI_ERR_SHAPE;
     if (t->n_experts <= 0 || t->n_experts > kMaxExperts) return MI_ERR_SHAPE;
     if (t->qtype == MI_QT_CB3) {
@@ -212,7 +232,8 @@ static int validate_table(const mi_table *t) {
         if (!t->plane[0] || !t->plane[1]) return MI_ERR_NULL;
     } else {
         if (t->cols <= 0 || t->cols % 256) return MI_ERR_SHAPE;
-        for (int i = 0; i < (t->qtype == MI_QT_IQ4_XS ? 4 : 5); ++i)
+        const int np = t->qtype == MI_QT_Q2_K ? 3 : (t->qtype == MI_QT_IQ4_XS || t->qtype == MI_QT_Q3_K) ? 4 : 5;
+        for (int i = 0; i < np; ++i)
             if (!t->plane[i]) return MI_ERR_NULL;
     }
     return MI_OK;
@@ -229,6 +250,15 @@ static Table make_table(const mi_table *t) {
         tb.cb3.CT = (t->cols + kCb3TileCols - 1) / kCb3TileCols;
         tb.cb3.RT = t->rows / 16;
         tb.cb3.G = t->cols / 128;
+    } else if (t->qtype == MI_QT_Q2_K || t->qtype == MI_QT_Q3_K) {
+        const bool q3 = t->qtype == MI_QT_Q3_K;
+        tb.kq.qs = t->plane[0];
+        tb.kq.hm = q3 ? t->plane[1] : nullptr;
+        tb.kq.sc = t->plane[q3 ? 2 : 1];
+        tb.kq.d = t->plane[q3 ? 3 : 2];
+        tb.kq.R = t->rows;
+        tb.kq.K = t->cols;
+        tb.kq.nblk = t->cols / 256;
     } else if (t->qtype == MI_QT_IQ2_S) {
         tb.iq2.qs = t->plane[0];
         tb.iq2.sg = t->plane[1];
@@ -336,21 +366,27 @@ MI_DECL_OCC(0, 1)
 MI_DECL_OCC(0, 2)
 MI_DECL_OCC(0, 3)
 MI_DECL_OCC(0, 4)
+MI_DECL_OCC(0, 5)
+MI_DECL_OCC(0, 6)
 MI_DECL_OCC(1, 1)
 MI_DECL_OCC(1, 2)
 MI_DECL_OCC(1, 3)
 MI_DECL_OCC(1, 4)
+MI_DECL_OCC(1, 5)
+MI_DECL_OCC(1, 6)
 MI_DECL_OCC(2, 1)
 MI_DECL_OCC(2, 2)
 MI_DECL_OCC(2, 3)
 MI_DECL_OCC(2, 4)
+MI_DECL_OCC(2, 5)
+MI_DECL_OCC(2, 6)
 #undef MI_DECL_OCC
 
 // Resident workgroups per CU of a grouped-kernel launch (the runtime's occupancy for that instance and LDS size;
 // 2 when it cannot be queried), cached per (mode, format, token class, rows per wavefront, 512-byte LDS bucket).
 static int wgs_per_cu(int mode, int qtype, int tcmax, int rtw, size_t lds) {
-    static int cache[3][4][5][3][161];
-    const int qi = qtype - 1;                                   // MI_QT_CB3, MI_QT_IQ3_S, MI_QT_IQ4_XS, MI_QT_IQ2_S
+    static int cache[3][6][5][3][161];
+    const int qi = qtype - 1;                                   // MI_QT_CB3 .. MI_QT_Q3_K
     int ti = 0, ri = rtw == 4 ? 2 : rtw - 1;
     while ((1 << ti) < tcmax && ti < 4) ++ti;
     const size_t bucket = (lds + 511) / 512;
@@ -359,10 +395,12 @@ static int wgs_per_cu(int mode, int qtype, int tcmax, int rtw, size_t lds) {
     const size_t l = bucket * 512;
     int n;
     typedef int (*Occ)(int, int, size_t);
-    static const Occ occ[3][4] = {
-        {occupancy_grouped_0_1, occupancy_grouped_0_2, occupancy_grouped_0_3, occupancy_grouped_0_4},
-        {occupancy_grouped_1_1, occupancy_grouped_1_2, occupancy_grouped_1_3, occupancy_grouped_1_4},
-        {occupancy_grouped_2_1, occupancy_grouped_2_2, occupancy_grouped_2_3, occupancy_grouped_2_4}};
+    static const Occ occ[3][6] = {{occupancy_grouped_0_1, occupancy_grouped_0_2, occupancy_grouped_0_3,
+                                   occupancy_grouped_0_4, occupancy_grouped_0_5, occupancy_grouped_0_6},
+                                  {occupancy_grouped_1_1, occupancy_grouped_1_2, occupancy_grouped_1_3,
+                                   occupancy_grouped_1_4, occupancy_grouped_1_5, occupancy_grouped_1_6},
+                                  {occupancy_grouped_2_1, occupancy_grouped_2_2, occupancy_grouped_2_3,
+                                   occupancy_grouped_2_4, occupancy_grouped_2_5, occupancy_grouped_2_6}};
     n = occ[mode][qi](tcmax, rtw, l);
     if (n <= 0) n = 2;
     if (slot) *slot = n;
@@ -401,7 +439,8 @@ static Shape choose_shape(const mi_table *t, int mode, int tcmax, int groups, in
         const int RBG = (RB + rg_per_wg - 1) / rg_per_wg;
         // kilobytes a wavefront streams per unit: CB3 one 1 KB code tile per row tile + codebook; IQ2_S / IQ3_S /
         // IQ4_XS 64 rows of an 82 / 110 / 136-byte block
-        const int block_bytes = t->qtype == MI_QT_IQ3_S ? 110 : t->qtype == MI_QT_IQ2_S ? 82 : 136;
+        const int block_bytes = t->qtype == MI_QT_IQ2_S ? 82 : t->qtype == MI_QT_IQ4_XS ? 136
+                              : t->qtype == MI_QT_Q2_K ? 84 : t->qtype == MI_QT_Q3_K ? 116 : 110;
         const double kb_per_unit = cb3 ? rtw * 1.25 : 64 * block_bytes / 1024.0;
         const int aligns[2] = {cb3 ? 4 : 1, 1};
         for (int ai = 0; ai < 2; ++ai) {
@@ -611,22 +650,31 @@ MI_DECL_LAUNCH(0, 1)
 MI_DECL_LAUNCH(0, 2)
 MI_DECL_LAUNCH(0, 3)
 MI_DECL_LAUNCH(0, 4)
+MI_DECL_LAUNCH(0, 5)
+MI_DECL_LAUNCH(0, 6)
 MI_DECL_LAUNCH(1, 1)
 MI_DECL_LAUNCH(1, 2)
 MI_DECL_LAUNCH(1, 3)
 MI_DECL_LAUNCH(1, 4)
+MI_DECL_LAUNCH(1, 5)
+MI_DECL_LAUNCH(1, 6)
 MI_DECL_LAUNCH(2, 1)
 MI_DECL_LAUNCH(2, 2)
 MI_DECL_LAUNCH(2, 3)
 MI_DECL_LAUNCH(2, 4)
+MI_DECL_LAUNCH(2, 5)
+MI_DECL_LAUNCH(2, 6)
 #undef MI_DECL_LAUNCH
 
 template <int MODE>
 static void launch_grouped(int qtype, int tcmax, int rtw, dim3 grid, size_t lds, hipStream_t s, const KArgs &a) {
     typedef void (*Launch)(int, int, dim3, dim3, size_t, hipStream_t, const KArgs &);
-    static const Launch fn[3][4] = {{launch_grouped_0_1, launch_grouped_0_2, launch_grouped_0_3, launch_grouped_0_4},
-                                    {launch_grouped_1_1, launch_grouped_1_2, launch_grouped_1_3, launch_grouped_1_4},
-                                    {launch_grouped_2_1, launch_grouped_2_2, launch_grouped_2_3, launch_grouped_2_4}};
+    static const Launch fn[3][6] = {{launch_grouped_0_1, launch_grouped_0_2, launch_grouped_0_3, launch_grouped_0_4,
+                                     launch_grouped_0_5, launch_grouped_0_6},
+                                    {launch_grouped_1_1, launch_grouped_1_2, launch_grouped_1_3, launch_grouped_1_4,
+                                     launch_grouped_1_5, launch_grouped_1_6},
+                                    {launch_grouped_2_1, launch_grouped_2_2, launch_grouped_2_3, launch_grouped_2_4,
+                                     launch_grouped_2_5, launch_grouped_2_6}};
     fn[MODE][qtype - 1](tcmax, rtw, grid, dim3(64 * kWgWaves), lds, s, a);
 }
 

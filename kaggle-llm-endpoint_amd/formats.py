@@ -82,6 +82,38 @@ def iq2s_hbm_bytes(R, K):
     return R * (K // QK) * IQ2S_BLOCK_BYTES
 
 
+# ------------------------------------------------------------------------------------------------ Q2_K, Q3_K
+KQ_BLOCK_BYTES = {"Q2_K": 84, "Q3_K": 110}
+
+
+def q3k_unpack_scales(sc12):
+    """Q3_K's 12 packed scale bytes -> the 16 six-bit scales as bytes (iqquant.py:190-201): scale i takes its low 4 bits
+    from byte i % 8 (low nibble for i < 8, high nibble above) and its high 2 bits from byte 8 + i % 4, bits 2 (i // 4)."""
+    sc12 = np.asarray(sc12, np.uint8)
+    out = [((sc12[..., i % 8] >> (0 if i < 8 else 4)) & 15) | (((sc12[..., 8 + i % 4] >> (2 * (i // 4))) & 3) << 4)
+           for i in range(16)]
+    return np.stack(out, axis=-1).astype(np.uint8)
+
+
+def kq_pack_planes(blocks, qtype):
+    """uint8 [E, R, nblk, bb] GGUF Q2_K / Q3_K blocks -> {plane: u32 [E*rows_p, R]} in the reference's planar layout
+    (planes.py:140-150: Q2_K qs | sc | d+dmin; Q3_K qs | hm | unpacked sc | d zero-extended)."""
+    blocks = np.asarray(blocks, dtype=np.uint8)
+    E, R, nblk, bb = blocks.shape
+    if bb != KQ_BLOCK_BYTES[qtype]:
+        raise ValueError("%s blocks are %d bytes, got %d" % (qtype, KQ_BLOCK_BYTES[qtype], bb))
+    if qtype == "Q2_K":
+        raw = {"qs": blocks[..., 16:80], "sc": blocks[..., 0:16], "d": blocks[..., 80:84]}
+        keys = ("qs", "sc", "d")
+    else:
+        d = np.concatenate([blocks[..., 108:110], np.zeros((E, R, nblk, 2), np.uint8)], axis=-1)
+        raw = {"qs": blocks[..., 32:96], "hm": blocks[..., 0:32], "sc": q3k_unpack_scales(blocks[..., 96:108]),
+               "d": d}
+        keys = ("qs", "hm", "sc", "d")
+    out = {k: _expert_major(_le_words(v)) for k, v in raw.items()}
+    return {k: out[k] for k in keys}
+
+
 # ------------------------------------------------------------------------------------------------ IQ4_XS
 IQ4XS_BLOCK_BYTES = 136
 

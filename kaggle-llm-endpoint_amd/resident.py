@@ -20,7 +20,7 @@ QK = 256
 
 
 def _plane_rows(qtype, K):
-    """IQ2_S / IQ3_S / IQ4_XS: rows_p per expert of each plane [E*rows_p, R] (planes.py:56-70)."""
+    """IQ2_S / IQ3_S / IQ4_XS / Q2_K / Q3_K: rows_p per expert of each plane [E*rows_p, R] (planes.py:56-70)."""
     nblk = K // QK
     if qtype == "IQ2_S":
         W = 8 * nblk
@@ -30,6 +30,10 @@ def _plane_rows(qtype, K):
         return {"qs": W, "sg": W // 2, "qh": W // 8, "sc": W // 16, "d": (nblk + 1) // 2}
     if qtype == "IQ4_XS":
         return {"qs": 32 * nblk, "sl": nblk, "sh": nblk, "d": (nblk + 1) // 2}
+    if qtype == "Q2_K":
+        return {"qs": 16 * nblk, "sc": 4 * nblk, "d": nblk}
+    if qtype == "Q3_K":
+        return {"qs": 16 * nblk, "hm": 8 * nblk, "sc": 4 * nblk, "d": nblk}
     raise ValueError(qtype)                     # the reference raises ValueError on an unknown qtype (planes.py:70)
 
 
@@ -54,6 +58,8 @@ class ExpertTable:
             raise ValueError("unsupported qtype %r" % (qtype,))
         self.qtype, self.rows, self.cols = qtype, int(rows), int(cols)
         keys = _lib.PLANE_KEYS[qtype]
+        if qtype != "CB3" and (self.cols <= 0 or self.cols % QK):
+            raise ValueError("%s tables need whole %d-weight blocks per row, got %d columns" % (qtype, QK, self.cols))
         self.planes = {}
         for k in keys:
             a = planes[k]
@@ -150,6 +156,23 @@ def random_iq2s_table(E, R, K, generator, scale=0.02):
     bits = d.to(torch.float16).view(torch.int16).to(torch.int32) & 0xFFFF
     planes["d"] = (bits[..., 0] | (bits[..., 1] << 16)).contiguous()
     return ExpertTable("IQ2_S", planes, R, K)
+
+
+def random_kq_table(qtype, E, R, K, generator, scale=0.02):
+    """An ExpertTable of E random Q2_K or Q3_K experts in the reference's planes, generated on the GPU: uniform random
+    qs (and hm) words, random scale bytes (Q3_K: six-bit), f16 d (and dmin) uniform in [scale / 2, scale]."""
+    rp = _plane_rows(qtype, K)
+    planes = {}
+    for k in ("qs", "hm", "sc"):
+        if k in rp:
+            planes[k] = torch.randint(-2 ** 31, 2 ** 31 - 1, (E * rp[k], R), dtype=torch.int32, device="cuda",
+                                      generator=generator)
+    if qtype == "Q3_K":
+        planes["sc"] &= 0x3F3F3F3F
+    d = torch.rand((E * rp["d"], R, 2), device="cuda", generator=generator) * (0.5 * scale) + 0.5 * scale
+    bits = d.to(torch.float16).view(torch.int16).to(torch.int32) & 0xFFFF
+    planes["d"] = (bits[..., 0] | ((bits[..., 1] << 16) if qtype == "Q2_K" else 0)).contiguous()
+    return ExpertTable(qtype, planes, R, K)
 
 
 def random_iq4xs_table(E, R, K, generator, scale=0.02):

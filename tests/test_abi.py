@@ -134,3 +134,9 @@ def test_route_host_validation(L):
     assert call(x_=P(0x1002)) == 8                               # rows read as bf16 pairs: 4-byte alignment
     assert call(ws_bytes=need - 1) == 5                          # MI_ERR_WORKSPACE
     assert L.mi_moe_route_workspace(0, 6144, 64) == 0
+
+
+def test_expert_table_rejects_partial_blocks(pkg):
+    import torch
+    with pytest.raises(ValueError, match="whole 256-weight blocks"):
+        pkg.ExpertTable("Q2_K", {k: torch.zeros(4, 64, dtype=torch.int32) for k in ("qs", "sc", "d")}, 64, 128)

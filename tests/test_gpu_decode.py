@@ -24,7 +24,8 @@ def _t(a, dtype=None):
 @pytest.mark.parametrize("qtype,R,K", [("CB3", 256, 1280), ("CB3", 512, 2048), ("CB3", 256, 384),
                                        ("IQ3_S", 256, 512), ("IQ3_S", 512, 2048), ("IQ4_XS", 256, 512),
                                        ("IQ4_XS", 512, 2048), ("IQ2_S", 256, 512), ("IQ2_S", 512, 2048),
-                                       ("IQ2_S", 256, 768)])
+                                       ("IQ2_S", 256, 768), ("Q2_K", 256, 512), ("Q2_K", 256, 768),
+                                       ("Q3_K", 256, 512), ("Q3_K", 512, 1280)])
 def test_dequant_bit_exact(pkg, gpu, qtype, R, K):
     rng = np.random.default_rng(11)
     L = Layer(rng, qtype, 3, K, R)                  # gate is R x K
@@ -85,7 +86,7 @@ def test_dequant_real_gguf_iq2s(pkg, gpu):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
-@pytest.mark.parametrize("qtype", ["CB3", "IQ2_S", "IQ3_S", "IQ4_XS"])
+@pytest.mark.parametrize("qtype", ["CB3", "IQ2_S", "IQ3_S", "IQ4_XS", "Q2_K", "Q3_K"])
 @pytest.mark.parametrize("xdt", ["bf16", "f32"])
 def test_matvec_grouped(pkg, gpu, qtype, xdt):
     """moe_matvec semantics (pallas_moe.py:238-307): per-slot outputs, duplicate experts, an out-of-range id."""
@@ -104,7 +105,7 @@ def test_matvec_grouped(pkg, gpu, qtype, xdt):
     assert rel_l2(got, want) < 1e-5
 
 
-@pytest.mark.parametrize("qtype", ["CB3", "IQ2_S", "IQ3_S", "IQ4_XS"])
+@pytest.mark.parametrize("qtype", ["CB3", "IQ2_S", "IQ3_S", "IQ4_XS", "Q2_K", "Q3_K"])
 @pytest.mark.parametrize("N,k,E,routing", [(1, 8, 16, "softmax"), (4, 4, 12, "zipf"), (8, 8, 20, "zipf"),
                                            (16, 8, 24, "zipf"), (3, 2, 2, "zipf")])
 def test_decode_small(pkg, gpu, qtype, N, k, E, routing):
@@ -161,7 +162,8 @@ def test_resident_fetch_apply(pkg, gpu):
 
 
 @pytest.mark.parametrize("qtype,down_qtype", [("IQ3_S", "IQ4_XS"), ("CB3", "IQ3_S"), ("IQ4_XS", "CB3"),
-                                              ("IQ2_S", "IQ4_XS"), ("IQ2_S", "IQ3_S")])
+                                              ("IQ2_S", "IQ4_XS"), ("IQ2_S", "IQ3_S"), ("Q2_K", "Q3_K"),
+                                              ("Q3_K", "Q2_K")])
 @pytest.mark.parametrize("N", [1, 8, 16])
 def test_decode_mixed_formats(pkg, gpu, qtype, down_qtype, N):
     """Gate/up in one format and down in another (the reference's layers mix formats per matrix kind)."""

@@ -101,3 +101,11 @@ def test_planar_bytes():
     assert sum(a.nbytes for a in kq.pack_planes(t, "Q2_K").values()) == t.nbytes
     t = kq.random_blocks(rng, "Q3_K", 1, 8, 2)
     assert sum(a.nbytes for a in kq.pack_planes(t, "Q3_K").values()) == 8 * 2 * (64 + 32 + 16 + 4)
+
+
+@pytest.mark.parametrize("qtype", ["Q2_K", "Q3_K"])
+def test_host_packer_equals_oracle(pkg, qtype):
+    rng = np.random.default_rng(9)
+    t = kq.random_blocks(rng, qtype, 3, 20, 3)
+    a, b = pkg.formats.kq_pack_planes(t, qtype), kq.pack_planes(t, qtype)
+    assert set(a) == set(b) and all(np.array_equal(a[k], b[k]) for k in b)

@@ -1,8 +1,8 @@
-"""Test helpers: seeded expert tables in every format (CB3, IQ2_S, IQ3_S, IQ4_XS), their device planes and the oracle's
-view of them."""
+"""Test helpers: seeded expert tables in every format (CB3, IQ2_S, IQ3_S, IQ4_XS, Q2_K, Q3_K), their device planes
+and the oracle's view of them."""
 import numpy as np
 
-from oracle import cb3 as ocb3, iq2s as oiq2, iq3s as oiq3, iq4xs as oiq4
+from oracle import cb3 as ocb3, iq2s as oiq2, iq3s as oiq3, iq4xs as oiq4, kquant as okq
 
 MATS = ("gate", "up", "down")
 
@@ -25,6 +25,8 @@ class Layer:
                 self.raw[name] = oiq3.random_blocks(rng, E, R, K // 256, scale=scale)
             elif qt == "IQ2_S":
                 self.raw[name] = oiq2.random_blocks(rng, E, R, K // 256, scale=scale)
+            elif qt in ("Q2_K", "Q3_K"):
+                self.raw[name] = okq.random_blocks(rng, qt, E, R, K // 256, scale=scale)
             else:
                 self.raw[name] = oiq4.random_blocks(rng, E, R, K // 256, scale=scale)
         self._cache = {}
@@ -41,6 +43,8 @@ class Layer:
                 w = oiq3.dequant_blocks(self.raw[name][e]).reshape(R, K)
             elif qt == "IQ2_S":
                 w = oiq2.dequant_blocks(self.raw[name][e]).reshape(R, K)
+            elif qt in ("Q2_K", "Q3_K"):
+                w = okq.dequant_blocks(self.raw[name][e], qt).reshape(R, K)
             else:
                 w = oiq4.dequant_blocks(self.raw[name][e]).reshape(R, K)
             if len(self._cache) > 64:
@@ -59,6 +63,8 @@ class Layer:
             return fm.iq3s_pack_planes(self.raw[name])
         if qt == "IQ2_S":
             return fm.iq2s_pack_planes(self.raw[name])
+        if qt in ("Q2_K", "Q3_K"):
+            return fm.kq_pack_planes(self.raw[name], qt)
         return fm.iq4xs_pack_planes(self.raw[name])
 
     def tables(self, pkg, device="cuda"):
