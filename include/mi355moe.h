@@ -186,12 +186,13 @@ int mi_ragged_plan(const int32_t *idx, const float *w, int32_t T, int32_t k, int
                    void *stream);
 
 /*
- * Fused MoE prefill layer (ResidentFetch._apply_ragged_kernel, resident.py:144-165) for CB3, IQ2_S, IQ3_S or IQ4_XS
- * tables (gate and up in one format, down in the same or another), grouped GEMMs on the matrix cores:
+ * Fused MoE prefill layer (ResidentFetch._apply_ragged_kernel, resident.py:144-165) for CB3, IQ2_S, IQ3_S, IQ4_XS,
+ * Q2_K or Q3_K tables (gate and up in one format, down in the same or another), grouped GEMMs on the matrix cores:
  *   plan   = ragged_plan over the T*k slots (+ one shared-expert column of weight 1 if shared_expert >= 0), tm = 80
  *   W      = bf16(dequantized weight): CB3 centroids as stored; IQ2_S bf16(level * f16(d) * (0.5 + sc) * 0.25);
- *            IQ3_S bf16(level * f16(d) * (1 + 2 sc)); IQ4_XS bf16(kvalue * f16(d) * (s - 32)), rounded once to
- *            nearest even as the reference's tiles are (pallas_moe.py:341-350)
+ *            IQ3_S bf16(level * f16(d) * (1 + 2 sc)); IQ4_XS bf16(kvalue * f16(d) * (s - 32)); Q2_K / Q3_K
+ *            bf16 of the f32 dequantized weight; rounded once to nearest even as the reference's tiles are
+ *            (pallas_moe.py:341-350)
  *   h[row] = bf16(silu(min(g, L)) * clip(u, -L, L)),  g, u = Wgate_e x_t, Wup_e x_t in f32   (pallas_moe.py:622-690)
  *   y[row] = bf16(Wdown_e h[row]), f32 accumulation                                           (pallas_moe.py:693-755)
  *   out[t] = sum_j wt(t, j) y[row_slot(t, j)] in f32, wt = bf16(w[t, j]) for MI_COMBINE_MATMUL (resident.py:161-163)

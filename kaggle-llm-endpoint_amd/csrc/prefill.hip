@@ -1,4 +1,4 @@
-// Grouped prefill for CB3, IQ2_S, IQ3_S and IQ4_XS experts on the gfx950 matrix cores (the reference's ragged prefill,
+// Grouped prefill for CB3, IQ2_S, IQ3_S, IQ4_XS, Q2_K and Q3_K experts on the gfx950 matrix cores (the reference's ragged prefill,
 // resident.py:144-165 with pallas_moe.py:564-592,622-755):
 //   ragged_plan_kernel  the reference's slot layout (pallas_moe.py:564-592) built on the device by one workgroup:
 //                       slots stably sorted by expert, every expert padded to whole blocks of tm rows;
@@ -202,6 +202,7 @@ struct PfArgs {
     Iq3Table i0, i1;                       // IQ3_S tables, the same roles
     Iq4Table k0, k1;                       // IQ4_XS tables, the same roles
     Iq2Table j0, j1;                       // IQ2_S tables, the same roles
+    KqTable q0, q1;                        // Q2_K / Q3_K tables, the same roles
     int R, K;                              // output columns (rows of the table), input columns
     const int32_t *blk_expert, *blk_n, *n_blocks, *tok_row;
     const uint16_t *x;                     // gate/up: x [T, K] gathered through tok_row; down: h [Rp, K]
@@ -550,6 +551,114 @@ struct PfIq2 {
             uint4 b[NTT];
 #pragma unroll
             for (int tt = 0; tt < NTT; ++tt) b[tt] = *(const uint4 *)(xt + tt * 16 * kPfXPitch + 4 * j);
+            bf16x8 A = weights8(w, s.v[C & 1][0], ct, j);
+#pragma unroll
+            for (int r = 0; r < kPfRtw; ++r) {
+                bf16x8 An = A;
+                if (r + 1 < kPfRtw) An = weights8(w, s.v[C & 1][r + 1], ct, j);
+#pragma unroll
+                for (int tt = 0; tt < NTT; ++tt) acc[r][tt] = mfma16(A, b[tt], acc[r][tt]);
+                A = An;
+            }
+        }
+        // the slot's next column tile (ct + 2); past the row's end nothing is loaded (the slot is not read again)
+        if (ct + 2 < w.CT) {
+#pragma unroll
+            for (int r = 0; r < kPfRtw; ++r) load(w, ct + 2, s.v[C & 1][r], r);
+        }
+    }
+};
+
+// Q2_K / Q3_K: the reference's planes (planes.py:34-41, 136-170) decoded straight into the A operand.  A column tile
+// is 128 columns = half a block (half n = ct % 2); k-step j is the shift-j stripe of the half: lane (row i, group q)
+// holds columns 32 j + 8 q .. 32 j + 8 q + 7 = bytes 0..3 of plane words q' = 2q, 2q + 1 at shift 2j (natural
+// order), scale byte 8 n + 2 j + (q >= 2).  A weight is the reference's f32 value rounded once to bf16: Q2_K
+// fma(v, d * sc, -dmin * m) (d * sc * v is exact: one rounding, as iqquant.py:213), Q3_K (v + 4 hbit - 4) * d * (sc - 32)
+// (exact) (pallas_moe.py:165-209, 341-350).
+struct PfKqWave {
+    const char *qs, *sc, *dd, *hm;          // expert e's planes (hm: Q3_K)
+    uint32_t rpitch;                        // bytes per plane row (4 R)
+    uint32_t lrow;                          // the lane's byte offset in a plane row (row jt of the wavefront)
+    int q, CT;
+};
+struct PfKqRegs {
+    uint32_t v[2][kPfRtw][7];   // column tile ct in slot ct & 1, per row tile: qs words 2q, 2q + 1, sc x 2, d, hm x 2
+};
+
+template <bool Q3>
+struct PfKq {
+    static constexpr int kCols = 128;
+    static constexpr int kQOff = 4;        // dwords: columns 8q .. 8q+7 of a 32-column stripe
+    using Wave = PfKqWave;
+    using Regs = PfKqRegs;
+    static __device__ __forceinline__ int n_tiles(const PfArgs &a, int mat) { return (mat ? a.q1 : a.q0).K / 128; }
+    static __device__ __forceinline__ void load(const Wave &w, int ct, uint32_t (&u)[7], int r) {
+        const uint32_t o = w.lrow + 64u * (uint32_t)r, P = w.rpitch;
+        const int b = ct >> 1;
+        u[0] = *(const uint32_t *)(w.qs + (uint32_t)(8 * ct + 2 * w.q) * P + o);
+        u[1] = *(const uint32_t *)(w.qs + (uint32_t)(8 * ct + 2 * w.q + 1) * P + o);
+        u[2] = *(const uint32_t *)(w.sc + (uint32_t)(2 * ct) * P + o);
+        u[3] = *(const uint32_t *)(w.sc + (uint32_t)(2 * ct + 1) * P + o);
+        u[4] = *(const uint32_t *)(w.dd + (uint32_t)b * P + o);
+        if (Q3) {
+            u[5] = *(const uint32_t *)(w.hm + (uint32_t)(8 * b + 2 * w.q) * P + o);
+            u[6] = *(const uint32_t *)(w.hm + (uint32_t)(8 * b + 2 * w.q + 1) * P + o);
+        }
+    }
+    static __device__ __forceinline__ void init(Wave &w, Regs &s, const PfArgs &a, PfShared &sh, int mat, int e,
+                                                int rg, int wave, int lane) {
+        const KqTable &tb = mat ? a.q1 : a.q0;
+        const size_t R = (size_t)tb.R;
+        w.qs = (const char *)(tb.qs + (size_t)e * 16 * tb.nblk * R);
+        w.sc = (const char *)(tb.sc + (size_t)e * 4 * tb.nblk * R);
+        w.dd = (const char *)(tb.d + (size_t)e * tb.nblk * R);
+        w.hm = Q3 ? (const char *)(tb.hm + (size_t)e * 8 * tb.nblk * R) : nullptr;
+        w.rpitch = 4u * (uint32_t)tb.R;
+        w.q = lane >> 4;
+        w.lrow = 4u * (uint32_t)(rg * 64 + (lane & 15));
+        w.CT = tb.K / 128;
+        (void)sh;
+        (void)wave;
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int r = 0; r < kPfRtw; ++r) load(w, c, s.v[c][r], r);
+    }
+    // 4 weights from the 4 byte-sized values of t (each 0..3, Q3_K 0..7): f32 -> bf16 pairs
+    static __device__ __forceinline__ uint2 four(uint32_t t, float m, float a) {
+        const float v0 = (float)(t & 255u), v1 = (float)((t >> 8) & 255u);       // v_cvt_f32_ubyte0..3
+        const float v2 = (float)((t >> 16) & 255u), v3 = (float)(t >> 24);
+        return make_uint2(pf_bf16_pair(fmaf(v0, m, a), fmaf(v1, m, a)), pf_bf16_pair(fmaf(v2, m, a), fmaf(v3, m, a)));
+    }
+    // the 8 weights of step j (shift stripe j) for the row tile whose plane words are u
+    static __device__ __forceinline__ bf16x8 weights8(const Wave &w, const uint32_t (&u)[7], int ct, int j) {
+        const int n = ct & 1;
+        const uint32_t sb = ((j >> 1 ? u[3] : u[2]) >> (16 * (j & 1) + 8 * (w.q >> 1))) & 255u;
+        const float d = f16_bits_to_f32(u[4] & 0xffffu);
+        uint32_t t0 = (u[0] >> (2 * j)) & 0x03030303u, t1 = (u[1] >> (2 * j)) & 0x03030303u;
+        float m, a;
+        if (Q3) {
+            t0 |= ((u[5] >> (4 * n + j)) & 0x01010101u) << 2;
+            t1 |= ((u[6] >> (4 * n + j)) & 0x01010101u) << 2;
+            m = d * ((float)sb - 32.0f);                              // exact
+            a = -4.0f * m;
+        } else {
+            m = d * (float)(sb & 15u);
+            a = -(f16_bits_to_f32(u[4] >> 16) * (float)(sb >> 4));
+        }
+        const uint2 l0 = four(t0, m, a), l1 = four(t1, m, a);
+        return __builtin_bit_cast(bf16x8, make_uint4(l0.x, l0.y, l1.x, l1.y));
+    }
+    template <int NTT, int C>
+    static __device__ __forceinline__ void tile(const Wave &w, Regs &s, int st, const uint32_t *xt,
+                                                f32x4 (&acc)[kPfRtw][NTT]) {
+        const int ct = 4 * st + C;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (j > 0) __builtin_amdgcn_sched_barrier(0);
+            uint4 b[NTT];
+#pragma unroll
+            for (int tt = 0; tt < NTT; ++tt) b[tt] = *(const uint4 *)(xt + tt * 16 * kPfXPitch + 16 * j);
             bf16x8 A = weights8(w, s.v[C & 1][0], ct, j);
 #pragma unroll
             for (int r = 0; r < kPfRtw; ++r) {
@@ -951,6 +1060,19 @@ static Iq3Table pf_iq3_table(const mi_table *t) {
     return c;
 }
 
+static KqTable pf_kq_table(const mi_table *t) {
+    const bool q3 = t->qtype == MI_QT_Q3_K;
+    KqTable c{};
+    c.qs = t->plane[0];
+    c.hm = q3 ? t->plane[1] : nullptr;
+    c.sc = t->plane[q3 ? 2 : 1];
+    c.d = t->plane[q3 ? 3 : 2];
+    c.R = t->rows;
+    c.K = t->cols;
+    c.nblk = t->cols / 256;
+    return c;
+}
+
 static Iq2Table pf_iq2_table(const mi_table *t) {
     Iq2Table c{};
     c.qs = t->plane[0];
@@ -978,14 +1100,14 @@ static Iq4Table pf_iq4_table(const mi_table *t) {
     return c;
 }
 
-// Gate and up share one format, down may use another: CB3 (code tiles), IQ2_S, IQ3_S or IQ4_XS (the reference's
-// planes, whole 256-weight blocks).
+// Gate and up share one format, down may use another: CB3 (code tiles), IQ2_S, IQ3_S, IQ4_XS, Q2_K or Q3_K (the
+// reference's planes, whole 256-weight blocks).
 static int pf_validate(const mi_table *g, const mi_table *u, const mi_table *d) {
     if (!g || !u || !d) return MI_ERR_NULL;
     for (const mi_table *t : {g, u, d}) {
-        if (t->qtype != MI_QT_CB3 && t->qtype != MI_QT_IQ3_S && t->qtype != MI_QT_IQ4_XS && t->qtype != MI_QT_IQ2_S)
-            return MI_ERR_QTYPE;
-        const int np = t->qtype == MI_QT_CB3 ? 2 : t->qtype == MI_QT_IQ4_XS ? 4 : 5;
+        if (t->qtype < MI_QT_CB3 || t->qtype > MI_QT_Q3_K) return MI_ERR_QTYPE;
+        const int np = t->qtype == MI_QT_CB3 ? 2 : t->qtype == MI_QT_Q2_K ? 3
+                     : (t->qtype == MI_QT_IQ4_XS || t->qtype == MI_QT_Q3_K) ? 4 : 5;
         for (int i = 0; i < np; ++i)
             if (!t->plane[i]) return MI_ERR_NULL;
         if (t->n_experts <= 0 || t->n_experts > kPlanMaxE || t->cols <= 0 || t->cols % 128 || t->rows <= 0)
@@ -1084,6 +1206,9 @@ int mi_moe_prefill(const mi_table *gate, const mi_table *up, const mi_table *dow
     } else if (gate->qtype == MI_QT_IQ2_S) {
         a.j0 = pf_iq2_table(gate);
         a.j1 = pf_iq2_table(up);
+    } else if (gate->qtype == MI_QT_Q2_K || gate->qtype == MI_QT_Q3_K) {
+        a.q0 = pf_kq_table(gate);
+        a.q1 = pf_kq_table(up);
     } else {
         a.t0 = pf_table(gate);
         a.t1 = pf_table(up);
@@ -1106,6 +1231,8 @@ int mi_moe_prefill(const mi_table *gate, const mi_table *up, const mi_table *dow
     if (gate->qtype == MI_QT_IQ3_S) hipLaunchKernelGGL((prefill_kernel<0, PfIq3>), dim3(g8 * a.RBG), block, 0, s, a);
     else if (gate->qtype == MI_QT_IQ4_XS) hipLaunchKernelGGL((prefill_kernel<0, PfIq4>), dim3(g8 * a.RBG), block, 0, s, a);
     else if (gate->qtype == MI_QT_IQ2_S) hipLaunchKernelGGL((prefill_kernel<0, PfIq2>), dim3(g8 * a.RBG), block, 0, s, a);
+    else if (gate->qtype == MI_QT_Q2_K) hipLaunchKernelGGL((prefill_kernel<0, PfKq<false>>), dim3(g8 * a.RBG), block, 0, s, a);
+    else if (gate->qtype == MI_QT_Q3_K) hipLaunchKernelGGL((prefill_kernel<0, PfKq<true>>), dim3(g8 * a.RBG), block, 0, s, a);
     else hipLaunchKernelGGL((prefill_kernel<0, PfCb3>), dim3(g8 * a.RBG), block, 0, s, a);
     if (hipGetLastError() != hipSuccess) return MI_ERR_LAUNCH;
 
@@ -1113,6 +1240,7 @@ int mi_moe_prefill(const mi_table *gate, const mi_table *up, const mi_table *dow
     if (down->qtype == MI_QT_IQ3_S) b.i0 = b.i1 = pf_iq3_table(down);
     else if (down->qtype == MI_QT_IQ4_XS) b.k0 = b.k1 = pf_iq4_table(down);
     else if (down->qtype == MI_QT_IQ2_S) b.j0 = b.j1 = pf_iq2_table(down);
+    else if (down->qtype == MI_QT_Q2_K || down->qtype == MI_QT_Q3_K) b.q0 = b.q1 = pf_kq_table(down);
     else b.t0 = b.t1 = pf_table(down);
     b.R = D;
     b.K = I;
@@ -1125,6 +1253,8 @@ int mi_moe_prefill(const mi_table *gate, const mi_table *up, const mi_table *dow
     if (down->qtype == MI_QT_IQ3_S) hipLaunchKernelGGL((prefill_kernel<1, PfIq3>), dim3(g8 * b.RBG), block, 0, s, b);
     else if (down->qtype == MI_QT_IQ4_XS) hipLaunchKernelGGL((prefill_kernel<1, PfIq4>), dim3(g8 * b.RBG), block, 0, s, b);
     else if (down->qtype == MI_QT_IQ2_S) hipLaunchKernelGGL((prefill_kernel<1, PfIq2>), dim3(g8 * b.RBG), block, 0, s, b);
+    else if (down->qtype == MI_QT_Q2_K) hipLaunchKernelGGL((prefill_kernel<1, PfKq<false>>), dim3(g8 * b.RBG), block, 0, s, b);
+    else if (down->qtype == MI_QT_Q3_K) hipLaunchKernelGGL((prefill_kernel<1, PfKq<true>>), dim3(g8 * b.RBG), block, 0, s, b);
     else hipLaunchKernelGGL((prefill_kernel<1, PfCb3>), dim3(g8 * b.RBG), block, 0, s, b);
     if (hipGetLastError() != hipSuccess) return MI_ERR_LAUNCH;
 

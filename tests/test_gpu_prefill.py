@@ -1,5 +1,5 @@
 """GPU parity of the grouped prefill path (resident.py:144-165): the device ragged_plan, the grouped GEMMs on
-the matrix cores (CB3, IQ2_S, IQ3_S and IQ4_XS tables, gate/up and down in one format or two) and the combine, against the
+the matrix cores (CB3, IQ2_S, IQ3_S, IQ4_XS, Q2_K and Q3_K tables, gate/up and down in one format or two) and the combine, against the
 CPU oracle.
 
 Bar: the plan is bit-exact against oracle.moe.ragged_plan (pallas_moe.py:564-592 restated in numpy); prefill
@@ -80,7 +80,8 @@ SMALL_IQ3 = [
 
 @pytest.mark.parametrize("qtype,T,k,E,D,I,shared,combine,kind",
                          [("CB3",) + c for c in SMALL] + [("IQ3_S",) + c for c in SMALL_IQ3] +
-                         [("IQ4_XS",) + c for c in SMALL_IQ3] + [("IQ2_S",) + c for c in SMALL_IQ3])
+                         [("IQ4_XS",) + c for c in SMALL_IQ3] + [("IQ2_S",) + c for c in SMALL_IQ3] +
+                         [("Q2_K",) + c for c in SMALL_IQ3] + [("Q3_K",) + c for c in SMALL_IQ3])
 def test_prefill_small(pkg, gpu, qtype, T, k, E, D, I, shared, combine, kind):
     rng = np.random.default_rng(7 * T + E)
     limit = 10.0
@@ -100,7 +101,7 @@ def test_prefill_small(pkg, gpu, qtype, T, k, E, D, I, shared, combine, kind):
     assert torch.equal(of, of2)                      # deterministic
 
 
-@pytest.mark.parametrize("qtype", ["CB3", "IQ2_S", "IQ3_S", "IQ4_XS"])
+@pytest.mark.parametrize("qtype", ["CB3", "IQ2_S", "IQ3_S", "IQ4_XS", "Q2_K", "Q3_K"])
 def test_prefill_limit_clamps(pkg, gpu, qtype):
     """A small swiglu limit makes the clamps of model.py:119-122 active in the gate/up epilogue."""
     rng = np.random.default_rng(4)
@@ -129,7 +130,7 @@ def test_prefill_full_shape(pkg, gpu, full_cb3_layer):
     assert err < TOL, err
 
 
-@pytest.mark.parametrize("qtype", ["CB3", "IQ2_S", "IQ3_S", "IQ4_XS"])
+@pytest.mark.parametrize("qtype", ["CB3", "IQ2_S", "IQ3_S", "IQ4_XS", "Q2_K", "Q3_K"])
 def test_resident_fetch_prefill(pkg, gpu, qtype):
     """ResidentFetch.apply with N*k > gather_max_rows takes the grouped prefill path (resident.py:104-108)."""
     rng = np.random.default_rng(8)
@@ -164,7 +165,8 @@ def test_prefill_full_shape_iq3s(pkg, gpu):
 
 
 @pytest.mark.parametrize("qtype,down_qtype", [("IQ3_S", "IQ4_XS"), ("CB3", "IQ4_XS"), ("IQ4_XS", "IQ3_S"),
-                                              ("IQ2_S", "IQ4_XS"), ("IQ2_S", "IQ3_S")])
+                                              ("IQ2_S", "IQ4_XS"), ("IQ2_S", "IQ3_S"), ("Q2_K", "Q3_K"),
+                                              ("Q3_K", "Q2_K")])
 def test_prefill_mixed_formats(pkg, gpu, qtype, down_qtype):
     """Gate/up in one format, down in another (the reference's layers mix formats per matrix kind)."""
     rng = np.random.default_rng(61)
