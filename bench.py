@@ -66,6 +66,14 @@ def iq2s_bytes(R, K):
     return R * (K // 256) * 82        # 82-byte blocks of 256 weights
 
 
+def q2k_bytes(R, K):
+    return R * (K // 256) * 84        # 84-byte blocks (the planes hold exactly these)
+
+
+def q3k_bytes(R, K):
+    return R * (K // 256) * 116       # 110-byte blocks; the planes hold the scales unpacked and d padded: 116
+
+
 def softmax_topk(rng, N, E, k):
     logits = rng.standard_normal((N, E))
     p = np.exp(logits - logits.max(-1, keepdims=True))
@@ -191,7 +199,9 @@ def main():
     # the reference's GGUF formats, for their own lines; made on demand, one layout at a time.  A layout names the
     # gate/up format and the down format ("iq2s_iq4xs": the production mix of the reference's GGUF layers).
     makers = {"iq3s": (pkg.random_iq3s_table, iq3s_bytes), "iq4xs": (pkg.random_iq4xs_table, iq4xs_bytes),
-              "iq2s": (pkg.random_iq2s_table, iq2s_bytes)}
+              "iq2s": (pkg.random_iq2s_table, iq2s_bytes),
+              "q2k": (lambda *a: pkg.random_kq_table("Q2_K", *a), q2k_bytes),
+              "q3k": (lambda *a: pkg.random_kq_table("Q3_K", *a), q3k_bytes)}
     made = {}
 
     def fmts(layout):
@@ -272,7 +282,7 @@ def main():
                                 "pct_hbm": round(100 * gbs / HBM_PEAK_GBS, 1), "bytes_per_layer": int(b)}
         extra["prefill_t512"] = bench_prefill(torch, pkg, gen, args, layers, rng, per_expert)
         # the reference's GGUF formats: IQ3_S and IQ4_XS tables (decode and prefill on the matrix cores)
-        for fmt in ("iq3s", "iq4xs", "iq2s", "iq2s_iq4xs"):
+        for fmt in ("iq3s", "iq4xs", "iq2s", "iq2s_iq4xs", "q2k_q3k"):
             for N, routing in ((1, softmax_topk), (8, zipf_topk)):
                 ms, b = measure(N, routing, tables=iq_layers(fmt), pe=iq_pe(fmt))
                 gbs = b / (ms * 1e-3) / 1e9

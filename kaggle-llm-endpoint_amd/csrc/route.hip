@@ -5,11 +5,13 @@
 //   idx    = top_k(scores + bias, k)     largest first; equal values: the lower expert id first (lax.top_k)
 //   w      = scores[idx]; with norm_topk w / (sum_j w + 1e-20); times scaling
 // Two launches on the caller's stream:
-//   route_logits_kernel  partial logits per 256-column chunk of D and 16-token block: a lane owns one expert, its
-//                        router column is read coalesced across the wavefront (E consecutive floats per row of
-//                        router_w), the token rows are wave-uniform loads; the 4 wavefronts' column quarters are
-//                        summed in LDS in a fixed order;
-//   route_select_kernel  one wavefront per token: the chunk partials summed in chunk order, sigmoid, bias, k rounds
+//   route_logits_kernel  partial logits per 256-column chunk of D and 16-token block: the block's activation tile
+//                        is staged in LDS (coalesced), a lane owns one expert and reads its router column coalesced
+//                        across the wavefront (E consecutive floats per row of router_w), 8 column pairs of loads in
+//                        flight at a time (all 32 at once measured slower at 512 tokens: fewer resident wavefronts);
+//                        the 4 wavefronts' column quarters are summed in LDS in a fixed order;
+//   route_select_kernel  one wavefront per token: the chunk partials (loaded 8 at a time) summed in chunk order,
+//                        sigmoid, bias, k rounds
 //                        of a wavefront argmax (value, then lower id), the weights normalised and scaled.
 // Deterministic: every sum in a fixed order, no atomics.
 #include <math.h>
@@ -22,7 +24,6 @@ constexpr int kRouteDc = 256;                 // columns of D per logits workgro
 constexpr int kRouteTb = 16;                  // tokens per logits workgroup
 constexpr int kRouteMaxE = 1024;
 constexpr int kRouteMaxK = 32;
-constexpr int kRoutePer = kRouteMaxE / 64;    // experts per lane in the select kernel
 
 __device__ __forceinline__ float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t v) { return __uint_as_float(v & 0xffff0000u); }
@@ -32,25 +33,39 @@ __global__ void __launch_bounds__(256) route_logits_kernel(const uint16_t *__res
                                                            const float *__restrict__ w, int N, int D, int E,
                                                            float *__restrict__ part) {
     __shared__ float red[4][kRouteTb][65];
+    __shared__ uint32_t xs[kRouteTb][kRouteDc / 2];              // the tile's activations as bf16 pairs (zero-padded)
     const int c = blockIdx.x, t0 = blockIdx.y * kRouteTb;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int nt = min(kRouteTb, N - t0);
-    const int d0 = c * kRouteDc + wave * (kRouteDc / 4);
-    const int d1 = min(D, d0 + kRouteDc / 4);
+    const int cb = c * kRouteDc;
+    for (int i = threadIdx.x; i < kRouteTb * kRouteDc / 2; i += 256) {
+        const int t = i / (kRouteDc / 2), p = i - t * (kRouteDc / 2), d = cb + 2 * p;
+        xs[t][p] = (t < nt && d < D) ? *(const uint32_t *)(x + (size_t)(t0 + t) * D + d) : 0u;
+    }
+    __syncthreads();
+    constexpr int kPairs = kRouteDc / 8;                        // column pairs per wavefront
+    const int p0 = wave * kPairs;
     for (int e0 = 0; e0 < E; e0 += 64) {
         const int e = e0 + lane;
         const bool live = e < E;
         float acc[kRouteTb];
 #pragma unroll
         for (int t = 0; t < kRouteTb; ++t) acc[t] = 0.0f;
-        for (int d = d0; d < d1; d += 2) {                       // D is even: whole bf16 pairs
-            const float w0 = live ? w[(size_t)d * E + e] : 0.0f;
-            const float w1 = live ? w[(size_t)(d + 1) * E + e] : 0.0f;
+        for (int pb = 0; pb < kPairs; pb += 8) {
+            float w0[8], w1[8];
 #pragma unroll
-            for (int t = 0; t < kRouteTb; ++t) {
-                if (t < nt) {
-                    const uint32_t xx = *(const uint32_t *)(x + (size_t)(t0 + t) * D + d);
-                    acc[t] = fmaf(bf16_hi(xx), w1, fmaf(bf16_lo(xx), w0, acc[t]));
+            for (int u = 0; u < 8; ++u) {                       // 16 loads in flight; columns past D read as zero
+                const int d = cb + 2 * (p0 + pb + u);
+                const bool in = live && d < D;
+                w0[u] = in ? w[(size_t)d * E + e] : 0.0f;
+                w1[u] = in ? w[(size_t)(d + 1) * E + e] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+#pragma unroll
+                for (int t = 0; t < kRouteTb; ++t) {
+                    const uint32_t xx = xs[t][p0 + pb + u];
+                    acc[t] = fmaf(bf16_hi(xx), w1[u], fmaf(bf16_lo(xx), w0[u], acc[t]));
                 }
             }
         }
@@ -71,21 +86,29 @@ __global__ void __launch_bounds__(256) route_logits_kernel(const uint16_t *__res
 // (value, id) ordering of top_k: larger value first, equal values: lower id first
 __device__ __forceinline__ bool route_better(float v, int i, float v2, int i2) { return v > v2 || (v == v2 && i < i2); }
 
+template <int PER>   // experts per lane: ceil(E / 64)
 __global__ void __launch_bounds__(256) route_select_kernel(const float *__restrict__ part, int nc,
                                                            const float *__restrict__ bias, int N, int E, int k,
                                                            int norm, float scaling, int32_t *__restrict__ idx,
                                                            float *__restrict__ wout) {
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (t >= N) return;                                          // the whole wavefront
-    float sc[kRoutePer], ch[kRoutePer];
+    float sc[PER], ch[PER];
 #pragma unroll
-    for (int j = 0; j < kRoutePer; ++j) {
+    for (int j = 0; j < PER; ++j) {
         const int e = 64 * j + lane;
         sc[j] = 0.0f;
         ch[j] = -INFINITY;
         if (e < E) {
             float l = 0.0f;
-            for (int c = 0; c < nc; ++c) l += part[((size_t)c * N + t) * E + e];
+            for (int c0 = 0; c0 < nc; c0 += 8) {                   // 8 loads in flight, added in chunk order
+                float v[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) v[u] = c0 + u < nc ? part[((size_t)(c0 + u) * N + t) * E + e] : 0.0f;
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (c0 + u < nc) l += v[u];
+            }
             const float s = 1.0f / (1.0f + expf(-l));
             sc[j] = s;
             ch[j] = s + (bias ? bias[e] : 0.0f);
@@ -101,7 +124,7 @@ __global__ void __launch_bounds__(256) route_select_kernel(const float *__restri
         float bv = -INFINITY, bs = 0.0f;
         int bi = 0x7fffffff;
 #pragma unroll
-        for (int j = 0; j < kRoutePer; ++j) {
+        for (int j = 0; j < PER; ++j) {
             const int e = 64 * j + lane;
             if (e < E && route_better(ch[j], e, bv, bi)) {
                 bv = ch[j];
@@ -125,7 +148,7 @@ __global__ void __launch_bounds__(256) route_select_kernel(const float *__restri
         sum += bs;
         // the owner drops the winner from later rounds
 #pragma unroll
-        for (int j = 0; j < kRoutePer; ++j)
+        for (int j = 0; j < PER; ++j)
             if (64 * j + lane == bi) ch[j] = -INFINITY;
     }
     const float inv = norm ? 1.0f / (sum + 1e-20f) : 1.0f;
@@ -167,7 +190,10 @@ extern "C" int mi_moe_route(const uint16_t *x_bf16, const float *router_w, const
     hipLaunchKernelGGL(route_logits_kernel, dim3(nc, (N + kRouteTb - 1) / kRouteTb), dim3(256), 0, s, x_bf16,
                        router_w, N, D, E, part);
     if (hipGetLastError() != hipSuccess) return MI_ERR_LAUNCH;
-    hipLaunchKernelGGL(route_select_kernel, dim3((N + 3) / 4), dim3(256), 0, s, (const float *)part, nc, bias, N, E,
-                       k, norm_topk, scaling, idx_out, w_out);
+    const int per = (E + 63) / 64;
+    auto sel = per <= 1 ? route_select_kernel<1> : per <= 2 ? route_select_kernel<2> : per <= 4 ? route_select_kernel<4>
+             : per <= 8 ? route_select_kernel<8> : route_select_kernel<16>;
+    hipLaunchKernelGGL(sel, dim3((N + 3) / 4), dim3(256), 0, s, (const float *)part, nc, bias, N, E, k, norm_topk,
+                       scaling, idx_out, w_out);
     return hipGetLastError() == hipSuccess ? MI_OK : MI_ERR_LAUNCH;
 }
