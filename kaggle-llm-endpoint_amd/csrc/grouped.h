@@ -66,6 +66,11 @@ struct KArgs {
     const uint16_t *x_lo;      // kDown: bf16 remainder of h [NS, stride] (h = x_bf16 + x_lo to 16 mantissa bits)
     const float *x_f32;        // kMatvec f32: [n_slots, stride] (split into bf16 high + remainder while staging)
     int x_stride;
+    // kDown without a SwiGLU launch: h formed while staging from the gate/up split partials [gu_S][2][NS][stride]
+    // (sum of the splits in order, clamped SwiGLU, bf16 high + remainder: the SwiGLU kernel's arithmetic)
+    const float *gu_part;
+    int gu_S;
+    float limit;
     const int32_t *idx;
     // partial sums
     float *part;               // [S * nmat * NS * R] written by this launch
@@ -220,7 +225,8 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
     // the staging then waits only for these loads, not for the weight ring behind them, and each tile's matrix-core
     // work starts as soon as that tile arrives.
     // (with many staged rows the 4-byte loads outnumber the register path's 8-byte ones: register staging there)
-    const bool dma = cb3 && (MODE != kMatvec || a.x_f32 == nullptr) && a.t_rows <= kDmaStageRows;
+    const bool dma = cb3 && (MODE != kMatvec || a.x_f32 == nullptr) && a.gu_part == nullptr &&
+                     a.t_rows <= kDmaStageRows;
     bool stage_ring = true;     // the wavefront issues its weight ring before staging (false: it only stages)
     if (dma) {
         const __amdgpu_buffer_rsrc_t rh =
@@ -262,6 +268,22 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
                 if (!hilo) {
                     const int row = (MODE == kGateUp) ? slot_token(slot, a.n_route, a.k) : slot;
                     hv = *(const uint2 *)(a.x_bf16 + (size_t)row * a.x_stride + c);
+                } else if (MODE == kDown && a.gu_part != nullptr) {
+                    const size_t plane = (size_t)a.NS * a.x_stride, o = (size_t)slot * a.x_stride + c;
+                    float4 g = make_float4(0.f, 0.f, 0.f, 0.f), u = g;
+                    for (int sp = 0; sp < a.gu_S; ++sp) {
+                        const float4 pg = *(const float4 *)(a.gu_part + (size_t)(2 * sp) * plane + o);
+                        const float4 pu = *(const float4 *)(a.gu_part + (size_t)(2 * sp + 1) * plane + o);
+                        g.x += pg.x; g.y += pg.y; g.z += pg.z; g.w += pg.w;
+                        u.x += pu.x; u.y += pu.y; u.z += pu.z; u.w += pu.w;
+                    }
+                    uint32_t h0, l0, h1, l1, h2, l2, h3, l3;
+                    split_bf16(swiglu_clamped(g.x, u.x, a.limit), h0, l0);
+                    split_bf16(swiglu_clamped(g.y, u.y, a.limit), h1, l1);
+                    split_bf16(swiglu_clamped(g.z, u.z, a.limit), h2, l2);
+                    split_bf16(swiglu_clamped(g.w, u.w, a.limit), h3, l3);
+                    hv = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
+                    lv = make_uint2(l0 | (l1 << 16), l2 | (l3 << 16));
                 } else if (a.x_f32 == nullptr) {
                     hv = *(const uint2 *)(a.x_bf16 + (size_t)slot * a.x_stride + c);
                     lv = *(const uint2 *)(a.x_lo + (size_t)slot * a.x_stride + c);

@@ -779,7 +779,10 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
     // phase 2: h = SwiGLU(sum of the phase-1 partials) [NS, I]; down -> split partials [S2, NS, D]; the
     // routing-weighted combine (+ shared expert) -> out [N, D].  Stream order publishes each launch's results.
     uint16_t *h_hi = (uint16_t *)(ws + p.off_h), *h_lo = h_hi + (size_t)p.NS * gate->rows;
-    {
+    // one workgroup per task (no persistent launches): the down launch forms h itself while staging its activation
+    // rows (the SwiGLU launch's arithmetic, from the gate/up partials); the persistent launches read h
+    const bool fuse_h = !cb3 && env_int("MI355MOE_SWIGLU_LAUNCH", 0) == 0;
+    if (!fuse_h) {
         const size_t n4 = (size_t)p.NS * gate->rows / 4;
         hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n4 + 63) / 64)), dim3(64), 0, s,
                            (const float *)(ws + p.off_part1), p.s1.sp.S, p.NS, gate->rows, limit, h_hi, h_lo);
@@ -802,6 +805,9 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
     b.x_lo = h_lo;
     b.x_f32 = nullptr;
     b.x_stride = gate->rows;
+    b.gu_part = fuse_h ? (const float *)(ws + p.off_part1) : nullptr;
+    b.gu_S = p.s1.sp.S;
+    b.limit = limit;
     b.part = (float *)(ws + p.off_part2);
     size_t lds2 = sizeof(uint32_t) * 2 * (size_t)b.t_rows * b.xs_max;
     if (cb3) {
