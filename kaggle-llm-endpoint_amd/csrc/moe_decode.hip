@@ -779,9 +779,11 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
     // phase 2: h = SwiGLU(sum of the phase-1 partials) [NS, I]; down -> split partials [S2, NS, D]; the
     // routing-weighted combine (+ shared expert) -> out [N, D].  Stream order publishes each launch's results.
     uint16_t *h_hi = (uint16_t *)(ws + p.off_h), *h_lo = h_hi + (size_t)p.NS * gate->rows;
-    // one workgroup per task (no persistent launches): the down launch forms h itself while staging its activation
-    // rows (the SwiGLU launch's arithmetic, from the gate/up partials); the persistent launches read h
-    const bool fuse_h = !cb3 && env_int("MI355MOE_SWIGLU_LAUNCH", 0) == 0;
+    // MI355MOE_FUSE_SWIGLU=1 (one workgroup per task only): the down launch forms h itself while staging its rows
+    // (the SwiGLU launch's arithmetic, from the gate/up partials) instead of a SwiGLU launch.  Measured slower (the
+    // down staging waits for the split partials: +2.5 us on the down launch at batch 1, +14 us per layer at batch 8),
+    // so the SwiGLU launch is the default.
+    const bool fuse_h = !cb3 && env_int("MI355MOE_FUSE_SWIGLU", 0) == 1;
     if (!fuse_h) {
         const size_t n4 = (size_t)p.NS * gate->rows / 4;
         hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n4 + 63) / 64)), dim3(64), 0, s,

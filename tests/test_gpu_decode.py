@@ -181,8 +181,8 @@ def test_decode_mixed_formats(pkg, gpu, qtype, down_qtype, N):
 
 @pytest.mark.parametrize("qtype", ["CB3", "IQ2_S", "IQ4_XS", "Q3_K"])
 def test_down_forms_h_like_the_swiglu_launch(pkg, gpu, qtype, monkeypatch):
-    """The down launch forms h from the gate/up partials while staging; with MI355MOE_SWIGLU_LAUNCH=1 a separate
-    SwiGLU launch writes h first.  Same arithmetic: bit-identical outputs."""
+    """With MI355MOE_FUSE_SWIGLU=1 the down launch forms h from the gate/up partials while staging instead of a
+    SwiGLU launch writing it first.  Same arithmetic: bit-identical outputs."""
     rng = np.random.default_rng(77)
     E, D, I, N, k, limit = 9, 512, 256, 4, 4, 0.5
     L = Layer(rng, qtype, E + 1, D, I)
@@ -190,6 +190,6 @@ def test_down_forms_h_like_the_swiglu_launch(pkg, gpu, qtype, monkeypatch):
     idx, w = zipf_routing(rng, N, E, k)
     x = _t(round_bf16(rng.standard_normal((N, D)).astype(np.float32)), torch.bfloat16)
     a, _ = pkg.moe_decode(tbs["gate"], tbs["up"], tbs["down"], x, _t(idx), _t(w), limit, shared_expert=E)
-    monkeypatch.setenv("MI355MOE_SWIGLU_LAUNCH", "1")
+    monkeypatch.setenv("MI355MOE_FUSE_SWIGLU", "1")
     b, _ = pkg.moe_decode(tbs["gate"], tbs["up"], tbs["down"], x, _t(idx), _t(w), limit, shared_expert=E)
     assert torch.equal(a, b)
