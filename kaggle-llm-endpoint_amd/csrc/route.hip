@@ -5,14 +5,17 @@
 //   idx    = top_k(scores + bias, k)     largest first; equal values: the lower expert id first (lax.top_k)
 //   w      = scores[idx]; with norm_topk w / (sum_j w + 1e-20); times scaling
 // Two launches on the caller's stream:
-//   route_logits_kernel  partial logits per 256-column chunk of D and 16-token block: the block's activation tile
+//   route_logits_kernel  partial logits per 256-column chunk of D and token block (1, 4, 8 or 16 tokens, the smallest
+//                        class holding N): the block's activation tile
 //                        is staged in LDS (coalesced), a lane owns one expert and reads its router column coalesced
 //                        across the wavefront (E consecutive floats per row of router_w), 8 column pairs of loads in
 //                        flight at a time (all 32 at once measured slower at 512 tokens: fewer resident wavefronts);
 //                        the 4 wavefronts' column quarters are summed in LDS in a fixed order;
-//   route_select_kernel  one wavefront per token: the chunk partials (loaded 8 at a time) summed in chunk order,
-//                        sigmoid, bias, k rounds
-//                        of a wavefront argmax (value, then lower id), the weights normalised and scaled.
+//   route_rank_kernel    (E <= 256) one wavefront per token: the chunk partials (loaded 8 at a time) summed in chunk
+//                        order, sigmoid, bias; each candidate's rank in top_k order (larger value, then lower id) is
+//                        counted against every choice in LDS, the k lowest ranks are the selection in order, and the
+//                        weights are summed in that order, normalised and scaled;
+//   route_select_kernel  (E > 256) the same with k rounds of a wavefront argmax instead of ranks.
 // Deterministic: every sum in a fixed order, no atomics.
 #include <math.h>
 
@@ -21,24 +24,26 @@
 namespace mi {
 
 constexpr int kRouteDc = 256;                 // columns of D per logits workgroup (64 per wavefront)
-constexpr int kRouteTb = 16;                  // tokens per logits workgroup
+constexpr int kRouteTb = 16;                  // tokens per logits workgroup (largest class)
 constexpr int kRouteMaxE = 1024;
 constexpr int kRouteMaxK = 32;
 
 __device__ __forceinline__ float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t v) { return __uint_as_float(v & 0xffff0000u); }
 
-// part[c][t][e] = sum over the columns d of chunk c of f32(x[t][d]) * w[d][e]
+// part[c][t][e] = sum over the columns d of chunk c of f32(x[t][d]) * w[d][e]; TB tokens per workgroup (1, 4, 8 or 16:
+// the smallest class holding N, so a single token does not pay for 16 rows of multiply-adds)
+template <int TB>
 __global__ void __launch_bounds__(256) route_logits_kernel(const uint16_t *__restrict__ x,
                                                            const float *__restrict__ w, int N, int D, int E,
                                                            float *__restrict__ part) {
-    __shared__ float red[4][kRouteTb][65];
-    __shared__ uint32_t xs[kRouteTb][kRouteDc / 2];              // the tile's activations as bf16 pairs (zero-padded)
-    const int c = blockIdx.x, t0 = blockIdx.y * kRouteTb;
+    __shared__ float red[4][TB][65];
+    __shared__ uint32_t xs[TB][kRouteDc / 2];                    // the tile's activations as bf16 pairs (zero-padded)
+    const int c = blockIdx.x, t0 = blockIdx.y * TB;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int nt = min(kRouteTb, N - t0);
+    const int nt = min(TB, N - t0);
     const int cb = c * kRouteDc;
-    for (int i = threadIdx.x; i < kRouteTb * kRouteDc / 2; i += 256) {
+    for (int i = threadIdx.x; i < TB * kRouteDc / 2; i += 256) {
         const int t = i / (kRouteDc / 2), p = i - t * (kRouteDc / 2), d = cb + 2 * p;
         xs[t][p] = (t < nt && d < D) ? *(const uint32_t *)(x + (size_t)(t0 + t) * D + d) : 0u;
     }
@@ -48,9 +53,9 @@ __global__ void __launch_bounds__(256) route_logits_kernel(const uint16_t *__res
     for (int e0 = 0; e0 < E; e0 += 64) {
         const int e = e0 + lane;
         const bool live = e < E;
-        float acc[kRouteTb];
+        float acc[TB];
 #pragma unroll
-        for (int t = 0; t < kRouteTb; ++t) acc[t] = 0.0f;
+        for (int t = 0; t < TB; ++t) acc[t] = 0.0f;
         for (int pb = 0; pb < kPairs; pb += 8) {
             float w0[8], w1[8];
 #pragma unroll
@@ -63,14 +68,14 @@ __global__ void __launch_bounds__(256) route_logits_kernel(const uint16_t *__res
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
 #pragma unroll
-                for (int t = 0; t < kRouteTb; ++t) {
+                for (int t = 0; t < TB; ++t) {
                     const uint32_t xx = xs[t][p0 + pb + u];
                     acc[t] = fmaf(bf16_hi(xx), w1[u], fmaf(bf16_lo(xx), w0[u], acc[t]));
                 }
             }
         }
 #pragma unroll
-        for (int t = 0; t < kRouteTb; ++t) red[wave][t][lane] = acc[t];
+        for (int t = 0; t < TB; ++t) red[wave][t][lane] = acc[t];
         __syncthreads();
         for (int i = threadIdx.x; i < nt * 64; i += 256) {
             const int t = i >> 6, l = i & 63;
@@ -86,14 +91,10 @@ __global__ void __launch_bounds__(256) route_logits_kernel(const uint16_t *__res
 // (value, id) ordering of top_k: larger value first, equal values: lower id first
 __device__ __forceinline__ bool route_better(float v, int i, float v2, int i2) { return v > v2 || (v == v2 && i < i2); }
 
-template <int PER>   // experts per lane: ceil(E / 64)
-__global__ void __launch_bounds__(256) route_select_kernel(const float *__restrict__ part, int nc,
-                                                           const float *__restrict__ bias, int N, int E, int k,
-                                                           int norm, float scaling, int32_t *__restrict__ idx,
-                                                           float *__restrict__ wout) {
-    const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    if (t >= N) return;                                          // the whole wavefront
-    float sc[PER], ch[PER];
+// the token's scores and choices (score + bias) of experts 64 j + lane, from the chunk partials summed in order
+template <int PER>
+__device__ __forceinline__ void route_scores(const float *__restrict__ part, int nc, const float *__restrict__ bias,
+                                             int N, int E, int t, int lane, float (&sc)[PER], float (&ch)[PER]) {
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
         const int e = 64 * j + lane;
@@ -114,6 +115,61 @@ __global__ void __launch_bounds__(256) route_select_kernel(const float *__restri
             ch[j] = s + (bias ? bias[e] : 0.0f);
         }
     }
+}
+
+template <int PER>   // experts per lane: ceil(E / 64) <= 4
+__global__ void __launch_bounds__(256) route_rank_kernel(const float *__restrict__ part, int nc,
+                                                         const float *__restrict__ bias, int N, int E, int k, int norm,
+                                                         float scaling, int32_t *__restrict__ idx,
+                                                         float *__restrict__ wout) {
+    __shared__ float4 chs[4][16 * PER];                          // each wavefront's E choices (-inf past E)
+    __shared__ float wsel[4][kRouteMaxK];
+    __shared__ int isel[4][kRouteMaxK];
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int t = blockIdx.x * 4 + wv;
+    const bool live = t < N;                                     // every wavefront reaches the barriers
+    float sc[PER], ch[PER];
+    route_scores<PER>(part, nc, bias, N, E, live ? t : 0, lane, sc, ch);
+    float *cf = (float *)chs[wv];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) cf[64 * j + lane] = ch[j];
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int e = 64 * j + lane;
+        int rank = 0;
+        for (int m4 = 0; m4 < 16 * PER; ++m4) {
+            const float4 v = chs[wv][m4];
+            const int m = 4 * m4;
+            rank += (v.x > ch[j] || (v.x == ch[j] && m < e)) + (v.y > ch[j] || (v.y == ch[j] && m + 1 < e)) +
+                    (v.z > ch[j] || (v.z == ch[j] && m + 2 < e)) + (v.w > ch[j] || (v.w == ch[j] && m + 3 < e));
+        }
+        if (e < E && rank < k) {
+            isel[wv][rank] = e;
+            wsel[wv][rank] = sc[j];
+        }
+    }
+    __syncthreads();
+    if (!live) return;
+    float sum = 0.0f;
+    for (int r = 0; r < k; ++r) sum += wsel[wv][r];             // in top_k order
+    const float inv = norm ? 1.0f / (sum + 1e-20f) : 1.0f;
+    if (lane < k) {
+        idx[(size_t)t * k + lane] = isel[wv][lane];
+        const float v = norm ? wsel[wv][lane] * inv : wsel[wv][lane];
+        wout[(size_t)t * k + lane] = v * scaling;
+    }
+}
+
+template <int PER>   // experts per lane: ceil(E / 64)
+__global__ void __launch_bounds__(256) route_select_kernel(const float *__restrict__ part, int nc,
+                                                           const float *__restrict__ bias, int N, int E, int k,
+                                                           int norm, float scaling, int32_t *__restrict__ idx,
+                                                           float *__restrict__ wout) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (t >= N) return;                                          // the whole wavefront
+    float sc[PER], ch[PER];
+    route_scores<PER>(part, nc, bias, N, E, t, lane, sc, ch);
     int sel_i[kRouteMaxK];
     float sel_w[kRouteMaxK];
     float sum = 0.0f;
@@ -187,11 +243,13 @@ extern "C" int mi_moe_route(const uint16_t *x_bf16, const float *router_w, const
     hipStream_t s = (hipStream_t)stream;
     float *part = (float *)workspace;
     const int nc = route_chunks(D);
-    hipLaunchKernelGGL(route_logits_kernel, dim3(nc, (N + kRouteTb - 1) / kRouteTb), dim3(256), 0, s, x_bf16,
-                       router_w, N, D, E, part);
+    const int tb = N == 1 ? 1 : N <= 4 ? 4 : N <= 8 ? 8 : kRouteTb;
+    auto lk = tb == 1 ? route_logits_kernel<1> : tb == 4 ? route_logits_kernel<4>
+            : tb == 8 ? route_logits_kernel<8> : route_logits_kernel<kRouteTb>;
+    hipLaunchKernelGGL(lk, dim3(nc, (N + tb - 1) / tb), dim3(256), 0, s, x_bf16, router_w, N, D, E, part);
     if (hipGetLastError() != hipSuccess) return MI_ERR_LAUNCH;
     const int per = (E + 63) / 64;
-    auto sel = per <= 1 ? route_select_kernel<1> : per <= 2 ? route_select_kernel<2> : per <= 4 ? route_select_kernel<4>
+    auto sel = per <= 1 ? route_rank_kernel<1> : per <= 2 ? route_rank_kernel<2> : per <= 4 ? route_rank_kernel<4>
              : per <= 8 ? route_select_kernel<8> : route_select_kernel<16>;
     hipLaunchKernelGGL(sel, dim3((N + 3) / 4), dim3(256), 0, s, (const float *)part, nc, bias, N, E, k, norm_topk,
                        scaling, idx_out, w_out);
