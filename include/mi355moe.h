@@ -197,11 +197,11 @@ int mi_ragged_plan(const int32_t *idx, const float *w, int32_t T, int32_t k, int
  *   y[row] = bf16(Wdown_e h[row]), f32 accumulation                                           (pallas_moe.py:693-755)
  *   out[t] = sum_j wt(t, j) y[row_slot(t, j)] in f32, wt = bf16(w[t, j]) for MI_COMBINE_MATMUL (resident.py:161-163)
  *            or w[t, j] for MI_COMBINE_GATHER (resident.py:164-165); the shared column has weight 1.
- * x bf16 [T, D], idx int32 [T, k], w f32 [T, k]; out_f32 and/or out_bf16 [T, D].  Every expert's weights are read
- * once per block of 80 rows.  T*(k+1) <= 2^22, E <= 1024, gate.rows % 128 == 0, down.rows % 256 == 0; the IQ
- * formats also need cols % 256 == 0.  MI_ERR_MISMATCH when gate and up differ in format or shape.
- * Four launches: plan, gate/up, down, combine.  The workspace (mi_moe_prefill_workspace bytes) holds the plan, h and
- * y; it needs no initialisation.
+ * x bf16 [T, D], idx int32 [T, k], w f32 [T, k]; out_f32 and/or out_bf16 [T, D] (16-byte aligned, as the workspace).
+ * Every expert's weights are read once per block of 80 rows. T*(k+1) <= 2^22, E <= 1024, gate.rows % 128 == 0,
+ * down.rows % 256 == 0; the IQ formats also need cols % 256 == 0. MI_ERR_MISMATCH when gate and up differ in format
+ * or shape. Four launches: plan, gate/up, down, combine. The workspace (mi_moe_prefill_workspace bytes) holds the
+ * plan, h and y; it needs no initialisation.
  */
 #define MI_COMBINE_MATMUL 0
 #define MI_COMBINE_GATHER 1

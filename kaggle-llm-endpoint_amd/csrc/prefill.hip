@@ -979,31 +979,51 @@ __global__ void __launch_bounds__(64 * kPfWaves, 2) prefill_kernel(PfArgs a) {
 __global__ void __launch_bounds__(256) prefill_combine(const uint16_t *__restrict__ y, const int32_t *__restrict__ row_slot,
                                                        const float *__restrict__ w, int T, int k, int kk, int D,
                                                        int bf16_weights, float *out_f32, uint16_t *out_bf16) {
-    const int q4 = D >> 2;
+    // one thread per 8 output columns of one token; the rows of up to 8 columns j are loaded before any is added,
+    // and added in column order
+    const int q8 = D >> 3;
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= T * q4) return;
-    const int t = i / q4, c = 4 * (i - t * q4);
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int j = 0; j < kk; ++j) {
-        const int r = row_slot[t * kk + j];
-        if (r < 0) continue;
-        float wt = 1.0f;
-        if (j < k) {
-            wt = w[t * k + j];
-            if (bf16_weights) wt = bf16_to_f32(f32_to_bf16_rne(wt));
+    if (i >= T * q8) return;
+    const int t = i / q8, c = 8 * (i - t * q8);
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int j0 = 0; j0 < kk; j0 += 8) {
+        int r[8];
+        float wt[8];
+        uint4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int j = j0 + u;
+            r[u] = j < kk ? row_slot[t * kk + j] : -1;
+            wt[u] = 1.0f;
+            if (j < k) {
+                wt[u] = w[t * k + j];
+                if (bf16_weights) wt[u] = bf16_to_f32(f32_to_bf16_rne(wt[u]));
+            }
         }
-        const uint2 v = *(const uint2 *)(y + (size_t)r * D + c);
-        acc.x += wt * bf16_to_f32(v.x & 0xffffu);
-        acc.y += wt * bf16_to_f32(v.x >> 16);
-        acc.z += wt * bf16_to_f32(v.y & 0xffffu);
-        acc.w += wt * bf16_to_f32(v.y >> 16);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = r[u] >= 0 ? *(const uint4 *)(y + (size_t)r[u] * D + c) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            if (r[u] < 0) continue;
+            const uint32_t vv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                acc[2 * h] += wt[u] * bf16_to_f32(vv[h] & 0xffffu);
+                acc[2 * h + 1] += wt[u] * bf16_to_f32(vv[h] >> 16);
+            }
+        }
     }
-    if (out_f32) *(float4 *)(out_f32 + (size_t)t * D + c) = acc;
+    if (out_f32) {
+        *(float4 *)(out_f32 + (size_t)t * D + c) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+        *(float4 *)(out_f32 + (size_t)t * D + c + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
+    }
     if (out_bf16) {
-        uint2 b;
-        b.x = f32_to_bf16_rne(acc.x) | (f32_to_bf16_rne(acc.y) << 16);
-        b.y = f32_to_bf16_rne(acc.z) | (f32_to_bf16_rne(acc.w) << 16);
-        *(uint2 *)(out_bf16 + (size_t)t * D + c) = b;
+        uint4 b;
+        b.x = f32_to_bf16_rne(acc[0]) | (f32_to_bf16_rne(acc[1]) << 16);
+        b.y = f32_to_bf16_rne(acc[2]) | (f32_to_bf16_rne(acc[3]) << 16);
+        b.z = f32_to_bf16_rne(acc[4]) | (f32_to_bf16_rne(acc[5]) << 16);
+        b.w = f32_to_bf16_rne(acc[6]) | (f32_to_bf16_rne(acc[7]) << 16);
+        *(uint4 *)(out_bf16 + (size_t)t * D + c) = b;
     }
 }
 
@@ -1176,6 +1196,8 @@ int mi_moe_prefill(const mi_table *gate, const mi_table *up, const mi_table *dow
     int st;
     if ((st = pf_validate(gate, up, down))) return st;
     if (!x_bf16 || !idx || !w || (!out_f32 && !out_bf16)) return MI_ERR_NULL;
+    // the combine writes 8 columns per thread as 16-byte pieces
+    if ((uintptr_t)out_f32 % 16 || (uintptr_t)out_bf16 % 16 || (uintptr_t)workspace % 16) return MI_ERR_ARG;
     const int E = gate->n_experts, I = gate->rows, D = down->rows;
     if (T <= 0 || k <= 0) return MI_ERR_TOKENS;
     if (shared_expert >= E || shared_expert < -1) return MI_ERR_ARG;
@@ -1258,7 +1280,7 @@ int mi_moe_prefill(const mi_table *gate, const mi_table *up, const mi_table *dow
     else hipLaunchKernelGGL((prefill_kernel<1, PfCb3>), dim3(g8 * b.RBG), block, 0, s, b);
     if (hipGetLastError() != hipSuccess) return MI_ERR_LAUNCH;
 
-    const long long nthr = (long long)T * (D / 4);
+    const long long nthr = (long long)T * (D / 8);
     hipLaunchKernelGGL(prefill_combine, dim3((unsigned)((nthr + 255) / 256)), dim3(256), 0, s, (const uint16_t *)y,
                        (const int32_t *)p.row_slot, w, T, k, kk, D, combine == MI_COMBINE_MATMUL ? 1 : 0, out_f32,
                        out_bf16);
