@@ -210,11 +210,13 @@ class GGUFModel:
 def load_layer(gm, layer, threads=8, device="cuda"):
     """One layer's routed experts -> ({"gate_q" | "up_q" | "down_q": ExpertTable}, {key: qtype}) for one GPU
     (resident.py:29-46 with one chip): the raw GGUF blocks are read, copied to the device once, and split into the
-    reference's planar tables there (mi_pack_planes)."""
+    reference's planar tables there (mi_pack_planes); Q2_K / Q3_K tensors (the MTP layer's experts, whose Q3_K scales
+    are unpacked) are split on the host (formats.kq_pack_planes)."""
     import numpy as np
     import torch
 
-    from .resident import ExpertTable, pack_planes_device
+    from . import formats
+    from .resident import ExpertTable, pack_planes_device, to_device_planes
 
     tables, qtypes = {}, {}
     for key, tname in (("gate_q", "gate"), ("up_q", "up"), ("down_q", "down")):
@@ -223,9 +225,12 @@ def load_layer(gm, layer, threads=8, device="cuda"):
         ne0, ne1, E = info["dims"]
         qt = info["type"]
         raws = gm.read_experts(name, range(E), threads=threads)
-        host = torch.from_numpy(np.frombuffer(b"".join(bytes(r) for r in raws), np.uint8).copy())
-        blocks = host.to(device)
-        planes = pack_planes_device(blocks, qt, E, ne1, ne0)
+        flat = np.frombuffer(b"".join(bytes(r) for r in raws), np.uint8)
+        if qt in formats.KQ_BLOCK_BYTES:
+            blk = flat.reshape(E, ne1, ne0 // 256, formats.KQ_BLOCK_BYTES[qt])
+            planes = to_device_planes(formats.kq_pack_planes(blk, qt), device)
+        else:
+            planes = pack_planes_device(torch.from_numpy(flat.copy()).to(device), qt, E, ne1, ne0)
         tables[key] = ExpertTable(qt, planes, ne1, ne0)
         qtypes[key] = qt
     return tables, qtypes

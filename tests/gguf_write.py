@@ -50,9 +50,13 @@ def write_gguf(path, kv, tensors, alignment=32):
             f.write(raw + b"\0" * ((-len(raw)) % alignment))
 
 
+F16_AT = {"Q2_K": (80, 82), "Q3_K": (108,)}       # where the block's f16 scales sit (IQ formats: byte 0)
+
+
 def expert_tensor(rng, qtype, E, out, inn, block_bytes, scale=0.02):
-    """Random expert blocks [E, out, inn/256, block_bytes] with a finite f16 d, and the tensor's GGUF dims."""
+    """Random expert blocks [E, out, inn/256, block_bytes] with finite f16 scales, and the tensor's GGUF dims."""
     raw = rng.integers(0, 256, (E, out, inn // 256, block_bytes), dtype=np.uint8)
-    d = rng.uniform(0.5 * scale, scale, (E, out, inn // 256)).astype(np.float16)
-    raw[..., 0:2] = np.frombuffer(d.tobytes(), np.uint8).reshape(E, out, inn // 256, 2)
+    for o in F16_AT.get(qtype, (0,)):
+        d = rng.uniform(0.5 * scale, scale, (E, out, inn // 256)).astype(np.float16)
+        raw[..., o:o + 2] = np.frombuffer(d.tobytes(), np.uint8).reshape(E, out, inn // 256, 2)
     return raw, [inn, out, E]

@@ -5,13 +5,13 @@ import numpy as np
 import pytest
 import torch
 
-from oracle import iq2s, iq3s, iq4xs, moe as omoe
+from oracle import iq2s, iq3s, iq4xs, kquant, moe as omoe
 from oracle.bf16 import rel_l2, round_bf16
 from tests.gguf_write import expert_tensor, write_gguf
 from tests.util import zipf_routing
 
 pytestmark = pytest.mark.gpu
-BB = {"IQ2_S": 82, "IQ3_S": 110, "IQ4_XS": 136}
+BB = {"IQ2_S": 82, "IQ3_S": 110, "IQ4_XS": 136, "Q2_K": 84, "Q3_K": 110}
 ORACLE = {"IQ2_S": iq2s, "IQ3_S": iq3s, "IQ4_XS": iq4xs}
 
 
@@ -28,12 +28,13 @@ def test_pack_planes_device(pkg, gpu, qtype, E, R, K):
         assert np.array_equal(g, want[k]), k
 
 
-def test_load_layer_from_gguf_and_decode(pkg, gpu, tmp_path):
-    """gate/up IQ2_S, down IQ4_XS (the real GGUF's mix) written to a GGUF file, read, packed on the device and run
-    through the decode and the prefill against the oracle."""
+@pytest.mark.parametrize("gu,dn", [("IQ2_S", "IQ4_XS"), ("Q2_K", "Q3_K")])
+def test_load_layer_from_gguf_and_decode(pkg, gpu, tmp_path, gu, dn):
+    """A layer written to a GGUF file (the real GGUF's IQ2_S/IQ4_XS mix; a K-quant MTP-style layer), read, packed
+    and run through the decode against the oracle."""
     rng = np.random.default_rng(12)
     E, D, I, N, k, limit = 6, 512, 256, 4, 3, 10.0
-    fmts = {"gate": "IQ2_S", "up": "IQ2_S", "down": "IQ4_XS"}
+    fmts = {"gate": gu, "up": gu, "down": dn}
     raws, tensors = {}, []
     for name, (R, K) in (("gate", (I, D)), ("up", (I, D)), ("down", (D, I))):
         raws[name], dims = expert_tensor(rng, fmts[name], E, R, K, BB[fmts[name]])
@@ -41,11 +42,14 @@ def test_load_layer_from_gguf_and_decode(pkg, gpu, tmp_path):
     write_gguf(tmp_path / "layer.gguf", {"general.architecture": "glm5next"}, tensors)
     gm = pkg.gguf.GGUFModel(pkg.gguf.open_mirror([str(tmp_path)]))
     tables, qtypes = pkg.gguf.load_layer(gm, 5, threads=2)
-    assert qtypes == {"gate_q": "IQ2_S", "up_q": "IQ2_S", "down_q": "IQ4_XS"}
+    assert qtypes == {"gate_q": gu, "up_q": gu, "down_q": dn}
 
     def deq(name, e):
         R, K = (D, I) if name == "down" else (I, D)
-        return ORACLE[fmts[name]].dequant_blocks(raws[name][e]).reshape(R, K)
+        qt = fmts[name]
+        if qt in ("Q2_K", "Q3_K"):
+            return kquant.dequant_blocks(raws[name][e], qt).reshape(R, K)
+        return ORACLE[qt].dequant_blocks(raws[name][e]).reshape(R, K)
 
     idx, w = zipf_routing(rng, N, E, k)
     x = round_bf16(rng.standard_normal((N, D)).astype(np.float32))
