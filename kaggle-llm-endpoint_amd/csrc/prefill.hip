@@ -45,6 +45,7 @@ constexpr int kPlanThreads = 1024;
 constexpr int kPlanWaves = kPlanThreads / 64;
 constexpr int kPlanMaxE = 1024;
 constexpr long long kPlanMaxSlots = 1 << 22;
+constexpr int kPlanReg = 8;                 // slots per thread held in registers (S <= kPlanReg * kPlanThreads)
 
 struct PlanOut {
     int32_t *blk_expert;   // [G]   expert of every block (blocks >= n_blocks repeat the last expert)
@@ -103,10 +104,32 @@ __global__ void __launch_bounds__(kPlanThreads) ragged_plan_kernel(const int32_t
         p.tok_row[r] = -1;
         p.w_row[r] = 0.0f;
     }
+    // up to kPlanReg * kPlanThreads slots: every expert id and weight is loaded once, up front, all loads in flight
+    // together, and both passes below read them from registers (no global round trip per round)
+    const bool in_reg = S <= kPlanReg * kPlanThreads;
+    int ereg[kPlanReg];
+    float wreg[kPlanReg];
+#pragma unroll
+    for (int r = 0; r < kPlanReg; ++r) {
+        const int s = tid + r * kPlanThreads;
+        ereg[r] = -1;
+        wreg[r] = 0.0f;
+        if (in_reg && s < S) {
+            ereg[r] = plan_expert(idx, s, k, kk, shared, E);
+            const int t = s / kk, j = s - t * kk;
+            wreg[r] = j < k ? w[t * k + j] : 1.0f;
+        }
+    }
     __syncthreads();
-    for (int s = tid; s < S; s += kPlanThreads) {
-        const int e = plan_expert(idx, s, k, kk, shared, E);
-        if (e >= 0) atomicAdd(&cnt[e], 1);
+    if (in_reg) {
+#pragma unroll
+        for (int r = 0; r < kPlanReg; ++r)
+            if (ereg[r] >= 0) atomicAdd(&cnt[ereg[r]], 1);
+    } else {
+        for (int s = tid; s < S; s += kPlanThreads) {
+            const int e = plan_expert(idx, s, k, kk, shared, E);
+            if (e >= 0) atomicAdd(&cnt[e], 1);
+        }
     }
     __syncthreads();
     // blocks per expert and their inclusive prefix (block end); padded rows start at (bend - nb) * tm
@@ -119,9 +142,22 @@ __global__ void __launch_bounds__(kPlanThreads) ragged_plan_kernel(const int32_t
 
     // rows, in rounds of kPlanThreads slots
     int tot = 0;
-    for (int base = 0; base < S; base += kPlanThreads) {
+    for (int base = 0, round = 0; base < S; base += kPlanThreads, ++round) {
         const int s = base + tid;
-        const int e = s < S ? plan_expert(idx, s, k, kk, shared, E) : -1;
+        int e = -1;
+        float wv = 0.0f;
+        if (in_reg) {
+#pragma unroll
+            for (int r = 0; r < kPlanReg; ++r)
+                if (r == round) {
+                    e = ereg[r];
+                    wv = wreg[r];
+                }
+        } else if (s < S) {
+            e = plan_expert(idx, s, k, kk, shared, E);
+            const int t = s / kk, j = s - t * kk;
+            wv = j < k ? w[t * k + j] : 1.0f;
+        }
         const bool valid = e >= 0;
         uint64_t rem = __ballot(valid);
         int rank = 0, n_same = 0;
@@ -152,9 +188,8 @@ __global__ void __launch_bounds__(kPlanThreads) ragged_plan_kernel(const int32_t
             if (valid) {
                 const int nb = (cnt[e] + tm - 1) / tm;
                 row = (bend[e] - nb) * tm + run[e] + cntw[wave][e] + rank;
-                const int t = s / kk, j = s - t * kk;
-                p.tok_row[row] = t;
-                p.w_row[row] = j < k ? w[t * k + j] : 1.0f;
+                p.tok_row[row] = s / kk;
+                p.w_row[row] = wv;
             }
             p.row_slot[s] = row;
         }
