@@ -50,7 +50,7 @@ __device__ __forceinline__ void kqm_accum(const KqTable &tb, int e, int row0, in
     const uint32_t *qs = tb.qs + (size_t)e * (16 * nblk) * R;
     const uint32_t *sc = tb.sc + (size_t)e * (4 * nblk) * R;
     const uint32_t *dd = tb.d + (size_t)e * nblk * R;
-    const uint32_t *hm = tb.hm + (size_t)e * (8 * nblk) * R;   // Q3_K only
+    const uint32_t *hm = Q3 ? tb.hm + (size_t)e * (8 * nblk) * R : nullptr;   // Q3_K only
     const bool first = q < 2;
     const uint4 z4 = make_uint4(0, 0, 0, 0);
     // half-blocks h = 2 b + n: qs words 8h + 2q, 8h + 2q + 1; sc rows 2h, 2h + 1 (scale bytes 8n .. 8n + 7 of block
