@@ -6,6 +6,7 @@ import re
 import subprocess
 import sys
 
+import numpy as np
 import pytest
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -140,3 +141,16 @@ def test_expert_table_rejects_partial_blocks(pkg):
     import torch
     with pytest.raises(ValueError, match="whole 256-weight blocks"):
         pkg.ExpertTable("Q2_K", {k: torch.zeros(4, 64, dtype=torch.int32) for k in ("qs", "sc", "d")}, 64, 128)
+
+
+def test_python_wrappers_reject_bad_arguments(pkg):
+    """The host side of the new entry points raises before any device work."""
+    import torch
+    with pytest.raises(ValueError):
+        pkg.pack_planes_device(torch.zeros(10, dtype=torch.uint8), "Q2_K", 1, 64, 256)      # K-quants: host packer
+    with pytest.raises(ValueError, match="bytes are not"):
+        pkg.pack_planes_device(torch.zeros(10, dtype=torch.uint8), "IQ2_S", 1, 64, 256)
+    with pytest.raises(ValueError, match="router_w must be"):
+        pkg.route(torch.zeros(2, 64, dtype=torch.bfloat16), torch.zeros(32, 8), None, 2)
+    with pytest.raises(ValueError):
+        pkg.formats.kq_pack_planes(np.zeros((1, 4, 1, 83), np.uint8), "Q2_K")
