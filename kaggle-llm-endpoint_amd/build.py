@@ -42,13 +42,38 @@ def _filter(stderr):
     return "\n".join(l for l in stderr.splitlines() if "packed-fp32-ops" not in l)
 
 
-def build(verbose=False, jobs=None):
-    tmpdir = tempfile.mkdtemp(prefix="mi355moe_build_")
+def _up_to_date(obj, dep):
+    """True when obj exists and is newer than every file its dependency list (hipcc -MD) names."""
+    try:
+        t = os.path.getmtime(obj)
+        text = open(dep).read().replace("\\\n", " ")
+    except OSError:
+        return False
+    files = text.split(":", 1)[1].split() if ":" in text else []
+    try:
+        return bool(files) and all(os.path.getmtime(f) <= t for f in files)
+    except OSError:
+        return False
+
+
+def build(verbose=False, jobs=None, incremental=False):
+    """Compile every unit and link.  ``incremental=True`` (development only) keeps the objects under _build/ at the
+    repository root and recompiles only the units whose sources or headers changed."""
+    if incremental:
+        tmpdir = os.path.join(os.path.dirname(HERE), "_build", "obj")
+        os.makedirs(tmpdir, exist_ok=True)
+    else:
+        tmpdir = tempfile.mkdtemp(prefix="mi355moe_build_")
     try:
         def compile_unit(u):
             src, defs, name = u
             obj = os.path.join(tmpdir, name + ".o")
+            dep = os.path.join(tmpdir, name + ".d")
             cmd = [HIPCC] + FLAGS + defs + ["-I", INCLUDE, "-c", os.path.join(CSRC, src), "-o", obj]
+            if incremental:
+                if _up_to_date(obj, dep):
+                    return name, obj, 0, "", cmd
+                cmd += ["-MD", "-MF", dep]
             res = subprocess.run(cmd, capture_output=True, text=True)
             return name, obj, res.returncode, _filter(res.stderr), cmd
         jobs = jobs or min(len(UNITS), max(1, os.cpu_count() or 1))
@@ -68,9 +93,10 @@ def build(verbose=False, jobs=None):
             raise RuntimeError("link failed (%d):\n%s" % (res.returncode, _filter(res.stderr)))
         os.replace(tmp, LIB)
     finally:
-        shutil.rmtree(tmpdir, ignore_errors=True)
+        if not incremental:
+            shutil.rmtree(tmpdir, ignore_errors=True)
     return LIB
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    print(build(verbose=True, incremental="--incremental" in sys.argv))
