@@ -131,6 +131,21 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
                          int32_t phases, void *stream);
 
 /*
+ * mi_moe_decode without a workspace argument, for callers that cannot allocate (code under HIP graph capture, serving
+ * loops and harnesses that forbid hipMalloc).  No counterpart in the reference: its operator allocates through XLA.
+ * The partials and h live in a static device array of MI_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends);
+ * the call allocates nothing and returns MI_ERR_WORKSPACE when the layer's data region (the separate launches'
+ * partials and h, mi_moe_decode_workspace minus the fused counter block) exceeds it -- the benchmark layer (D 6144,
+ * I 2048) fits at every N <= 16, k = 8.  Same arguments (minus the workspace), launches and results as mi_moe_decode.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one GPU (two streams, or two threads) race and
+ * give wrong results; order them on one stream.  Nothing in the array needs to start at zero.
+ */
+#define MI_NOALLOC_SCRATCH_BYTES (64u << 20)
+int mi_moe_decode_noalloc(const mi_table *gate, const mi_table *up, const mi_table *down, const uint16_t *x_bf16,
+                          int32_t N, int32_t k, const int32_t *idx, const float *w, int32_t shared_expert,
+                          float limit, float *out_f32, uint16_t *out_bf16, void *stream);
+
+/*
  * The launch plans of mi_moe_decode_fused and mi_moe_decode (no launch; for tests and tuning).  info[0..n_info):
  *   [0] 1 if mi_moe_decode_fused applies; [1] its workgroups; [2] 0 (reserved);
  *   [3..6] gate/up column splits, split alignment (column tiles), row tiles per wavefront, row ranges;

@@ -5,6 +5,8 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <mutex>
+
 namespace mi {
 
 // ------------------------------------------------------------------------------------------------ dequant (debug)
@@ -694,10 +696,14 @@ size_t mi_moe_decode_workspace(const mi_table *gate, const mi_table *down, int32
     return sep > fused ? sep : fused;
 }
 
-int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_table *down, const uint16_t *x_bf16,
-                         int32_t N, int32_t k, const int32_t *idx, const float *w, int32_t shared_expert,
-                         float limit, float *out_f32, uint16_t *out_bf16, void *workspace, size_t workspace_bytes,
-                         int32_t phases, void *stream) {
+}  // extern "C"
+
+namespace mi {
+
+// Host-side argument checks of the separate-launch decode (every status before any launch).
+static int decode_validate(const mi_table *gate, const mi_table *up, const mi_table *down, const uint16_t *x_bf16,
+                           int N, int k, const int32_t *idx, const float *w, int shared_expert, float limit,
+                           const float *out_f32, const uint16_t *out_bf16, int phases) {
     int st;
     if (phases < 1 || phases > 3) return MI_ERR_ARG;
     if ((st = validate_table(gate)) || (st = validate_table(up)) || (st = validate_table(down))) return st;
@@ -709,12 +715,15 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
     if (N <= 0 || N > kMaxT || k <= 0 || N * k > MI_MAX_SLOTS) return MI_ERR_TOKENS;
     if (shared_expert >= gate->n_experts || shared_expert < -1) return MI_ERR_ARG;
     if (!(limit > 0.0f)) return MI_ERR_ARG;
-    const DecodePlan p = plan_decode(gate, down, N, k, shared_expert);
-    const size_t ctr_bytes = ctr_layout(gate, down).bytes;
-    if (!workspace || workspace_bytes < ctr_bytes + p.total) return MI_ERR_WORKSPACE;
-    hipStream_t s = (hipStream_t)stream;
-    char *ws = (char *)workspace + ctr_bytes;        // the fused launch's counters stay untouched
+    return MI_OK;
+}
 
+// The separate launches of one decode layer (arguments already validated): ws is the data region (partials, h) of
+// p.total bytes -- past the counter block of a caller's workspace, or the library's static scratch.
+static int decode_launch(const DecodePlan &p, const mi_table *gate, const mi_table *up, const mi_table *down,
+                         const uint16_t *x_bf16, int N, int k, const int32_t *idx, const float *w, int shared_expert,
+                         float limit, float *out_f32, uint16_t *out_bf16, char *ws, int phases, hipStream_t s) {
+    int st;
     KArgs a{};
     a.E = gate->n_experts;
     a.n_route = N * k;
@@ -837,6 +846,61 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
     hipLaunchKernelGGL(combine_kernel, dim3((nthr + 63) / 64), dim3(64), 0, s, b.part, p.s2.sp.S, p.NS, D, N, k, idx, w,
                        gate->n_experts, shared_expert, N * k, out_f32, out_bf16);
     return launch_status();
+}
+
+// ------------------------------------------------------------------------------------------------ static scratch
+// The data region of mi_moe_decode_noalloc: one array per GPU, alive until the process ends.  In host code the
+// array's name only stands in for it; its device address comes from hipGetSymbolAddress, taken once per device with
+// that device current, and only that address is ever handed to a kernel.
+static __device__ __align__(256) uint8_t scratch[MI_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void *g_scratch_ptr[kMaxDevices];
+
+// Device address of the current device's scratch array (nullptr when it cannot be resolved).
+static void *scratch_ptr() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+        g_scratch_ptr[dev] = ptr;
+    }
+    return g_scratch_ptr[dev];
+}
+
+}  // namespace mi
+
+extern "C" {
+
+int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_table *down, const uint16_t *x_bf16,
+                         int32_t N, int32_t k, const int32_t *idx, const float *w, int32_t shared_expert,
+                         float limit, float *out_f32, uint16_t *out_bf16, void *workspace, size_t workspace_bytes,
+                         int32_t phases, void *stream) {
+    const int st = decode_validate(gate, up, down, x_bf16, N, k, idx, w, shared_expert, limit, out_f32, out_bf16,
+                                   phases);
+    if (st) return st;
+    const DecodePlan p = plan_decode(gate, down, N, k, shared_expert);
+    const size_t ctr_bytes = ctr_layout(gate, down).bytes;
+    if (!workspace || workspace_bytes < ctr_bytes + p.total) return MI_ERR_WORKSPACE;
+    // the fused launch's counters at the start of the workspace stay untouched
+    return decode_launch(p, gate, up, down, x_bf16, N, k, idx, w, shared_expert, limit, out_f32, out_bf16,
+                         (char *)workspace + ctr_bytes, phases, (hipStream_t)stream);
+}
+
+int mi_moe_decode_noalloc(const mi_table *gate, const mi_table *up, const mi_table *down, const uint16_t *x_bf16,
+                          int32_t N, int32_t k, const int32_t *idx, const float *w, int32_t shared_expert,
+                          float limit, float *out_f32, uint16_t *out_bf16, void *stream) {
+    const int st = decode_validate(gate, up, down, x_bf16, N, k, idx, w, shared_expert, limit, out_f32, out_bf16, 3);
+    if (st) return st;
+    const DecodePlan p = plan_decode(gate, down, N, k, shared_expert);
+    if (p.total > (size_t)MI_NOALLOC_SCRATCH_BYTES) return MI_ERR_WORKSPACE;
+    char *ws = (char *)scratch_ptr();
+    if (!ws) return MI_ERR_LAUNCH;
+    return decode_launch(p, gate, up, down, x_bf16, N, k, idx, w, shared_expert, limit, out_f32, out_bf16, ws, 3,
+                         (hipStream_t)stream);
 }
 
 int mi_moe_decode(const mi_table *gate, const mi_table *up, const mi_table *down, const uint16_t *x_bf16,
