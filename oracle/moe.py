@@ -112,16 +112,21 @@ def ragged_plan(idx, w, E, tm):
             "row_slot": row_slot.reshape(T, k)}
 
 
-def prefill_apply(deq, x, idx, w, limit, E, tm=32, combine="matmul", deq_is_bf16=False):
+def prefill_apply(deq, x, idx, w, limit, E, tm=32, combine="matmul", out_dtype="bf16", _drop=()):
     """The grouped prefill composition ResidentFetch._apply_ragged_kernel (resident.py:144-165) with the reference's
-    bf16 rounding points: x rows -> bf16 (resident.py:153), dequantized tiles -> bf16 (pallas_moe.py:350),
-    h = bf16(swiglu(f32 dots)) (pallas_moe.py:682), y = bf16(h @ Wd^T) (pallas_moe.py:747, out_dtype = bf16),
-    combine "matmul": bf16(w_row) @ y with f32 accumulation (resident.py:161-163); "gather": f32 sum of
-    y[row_slot] * w (resident.py:164-165).  Returns f64 [T, D].  ``deq`` returns exact weights; they are rounded
-    to bf16 here (a no-op for CB3, whose weights are bf16 already)."""
+    rounding points for ``out_dtype`` "bf16": x rows -> bf16 (resident.py:153), dequantized tiles -> bf16
+    (pallas_moe.py:350), h = bf16(swiglu(f32 dots)) (pallas_moe.py:682), y = bf16(h @ Wd^T) (pallas_moe.py:747,
+    out_dtype = the input's), combine "matmul": bf16(w_row) @ y with f32 accumulation (resident.py:161-163);
+    "gather": f32 sum of y[row_slot] * w (resident.py:164-165).  ``out_dtype`` "f32" (the reference's CPU tests,
+    test_resident_cpu.py:81,124): every one of those values stays f32 (f32 tiles, HIGHEST-precision dots,
+    pallas_moe.py:353-355).  Returns f64 [T, D].  ``deq`` returns exact weights (rounded here for bf16; a no-op for
+    CB3, whose weights are bf16 already).  ``_drop`` names bf16 rounding points to skip ("x", "w", "h", "y", "wc"):
+    for the planted-mistake tests only."""
+    rb = round_bf16 if out_dtype == "bf16" else (lambda a: np.asarray(a, dtype=np.float32))
+    rnd = lambda name, a: np.asarray(a, dtype=np.float32) if name in _drop else rb(a)
     plan = ragged_plan(idx, w, E, tm)
     T, k = np.asarray(idx).shape
-    xb = round_bf16(np.asarray(x, dtype=np.float32)).astype(np.float64)
+    xb = rnd("x", np.asarray(x, dtype=np.float32)).astype(np.float64)
     tok = plan["tok_row"]
     be = plan["blk_expert"]
     nb = int(plan["n_blocks"][0])
@@ -132,19 +137,19 @@ def prefill_apply(deq, x, idx, w, limit, E, tm=32, combine="matmul", deq_is_bf16
         rows = np.arange(g0 * tm, (g0 + 1) * tm)
         t = tok[rows]
         xs = np.where((t >= 0)[:, None], xb[np.maximum(t, 0)], 0.0)
-        Wg = round_bf16(deq("gate", e)).astype(np.float64)
-        Wu = round_bf16(deq("up", e)).astype(np.float64)
-        Wd = round_bf16(deq("down", e)).astype(np.float64)
+        Wg = rnd("w", deq("gate", e)).astype(np.float64)
+        Wu = rnd("w", deq("up", e)).astype(np.float64)
+        Wd = rnd("w", deq("down", e)).astype(np.float64)
         gg = (xs @ Wg.T).astype(np.float32)
         uu = (xs @ Wu.T).astype(np.float32)
-        h = round_bf16(swiglu_clamped(gg, uu, limit)).astype(np.float64)
-        y = round_bf16((h @ Wd.T).astype(np.float32)).astype(np.float64)
+        h = rnd("h", swiglu_clamped(gg, uu, limit)).astype(np.float64)
+        y = rnd("y", (h @ Wd.T).astype(np.float32)).astype(np.float64)
         D = y.shape[1]
         for i, r in enumerate(rows):
             ys[int(r)] = y[i]
     out = np.zeros((T, D), np.float64)
     if combine == "matmul":
-        wr = round_bf16(plan["w_row"]).astype(np.float64)
+        wr = rnd("wc", plan["w_row"]).astype(np.float64)
         for r, t in enumerate(tok):
             if t >= 0 and r in ys:
                 out[t] += wr[r] * ys[r]
@@ -154,3 +159,115 @@ def prefill_apply(deq, x, idx, w, limit, E, tm=32, combine="matmul", deq_is_bf16
             for j in range(k):
                 out[t] += wf[t, j] * ys[int(plan["row_slot"][t, j])]
     return out
+
+
+def routing_weights(idx, w, E):
+    """rw [T, E] = sum_j w[t, j] [idx[t, j] == e] in f32 (the sweeps' one-hot einsum, resident.py:176-177,195-196)."""
+    idx = np.asarray(idx)
+    rw = np.zeros((idx.shape[0], E), np.float32)
+    wf = np.asarray(w, dtype=np.float32)
+    for t in range(idx.shape[0]):
+        for j in range(idx.shape[1]):
+            rw[t, idx[t, j]] += wf[t, j]
+    return rw
+
+
+def sweep_apply(deq, x, idx, w, limit, E, out_dtype="bf16", _drop=()):
+    """The dense-sweep prefill ResidentFetch._apply_sweep_kernel (resident.py:169-187) with moe_sweep_gateup /
+    moe_sweep_down (pallas_moe.py:382-555): for every active expert e (ascending id) and every token t,
+    h = bf16(swiglu(f32 dots of bf16(x) and bf16 tiles)) (pallas_moe.py:467), hk = bf16(f32(h) * rw[t, e])
+    (resident.py:183-184), y[t] = sum_e hk @ bf16(Wd_e)^T with f32 accumulation and f32 output (pallas_moe.py:540,
+    no rounding of y).  rw is the summed routing weight of (t, e); a token not routed to e has rw = 0 and adds
+    exactly zero, so only routed pairs are evaluated.  ``out_dtype`` "f32": no rounding anywhere.  Returns f64
+    [T, D].  ``_drop`` ("x", "w", "h", "hk"): planted-mistake tests only."""
+    rb = round_bf16 if out_dtype == "bf16" else (lambda a: np.asarray(a, dtype=np.float32))
+    rnd = lambda name, a: np.asarray(a, dtype=np.float32) if name in _drop else rb(a)
+    idx = np.asarray(idx)
+    T = idx.shape[0]
+    rw = routing_weights(idx, w, E)
+    xb = rnd("x", np.asarray(x, dtype=np.float32)).astype(np.float64)
+    out = None
+    for e in np.unique(idx):
+        e = int(e)
+        toks = np.flatnonzero(rw[:, e] != 0)
+        if toks.size == 0:
+            continue
+        Wg = rnd("w", deq("gate", e)).astype(np.float64)
+        Wu = rnd("w", deq("up", e)).astype(np.float64)
+        Wd = rnd("w", deq("down", e)).astype(np.float64)
+        xs = xb[toks]
+        gg = (xs @ Wg.T).astype(np.float32)
+        uu = (xs @ Wu.T).astype(np.float32)
+        h = rnd("h", swiglu_clamped(gg, uu, limit))
+        hk = rnd("hk", h.astype(np.float32) * rw[toks, e][:, None]).astype(np.float64)
+        y = hk @ Wd.T
+        if out is None:
+            out = np.zeros((T, y.shape[1]), np.float64)
+        out[toks] += y
+    return out
+
+
+def gather_apply(deq, x, idx, w, limit, out_dtype="bf16"):
+    """The XLA decode path ResidentFetch._apply_gather (resident.py:122-135, use_pallas=False): weights dequantized
+    to out_dtype (resident.py:91), xs = x in out_dtype, g = einsum(xs, Wg) and u likewise in out_dtype (bf16: one
+    rounding of the f32-accumulated dot), h = swiglu_clamped(g, u) rounded to out_dtype, y = einsum(h, Wd) in
+    out_dtype, then f32, out = sum_j w y in f32 (resident.py:133-135).  bf16's h is modelled as one rounding of the
+    f32 SwiGLU of the rounded g and u (XLA's per-op rounding inside silu is not reproducible without XLA).
+    ``out_dtype`` "f32" is the decode composition in f32.  Returns f64 [N, D]."""
+    rb = round_bf16 if out_dtype == "bf16" else (lambda a: np.asarray(a, dtype=np.float32))
+    idx = np.asarray(idx)
+    N, k = idx.shape
+    xb = rb(np.asarray(x, dtype=np.float32)).astype(np.float64)
+    wf = np.asarray(w, dtype=np.float32).astype(np.float64)
+    out = None
+    for n in range(N):
+        for j in range(k):
+            e = int(idx[n, j])
+            Wg = rb(deq("gate", e)).astype(np.float64)
+            Wu = rb(deq("up", e)).astype(np.float64)
+            Wd = rb(deq("down", e)).astype(np.float64)
+            g = rb((Wg @ xb[n]).astype(np.float32))
+            u = rb((Wu @ xb[n]).astype(np.float32))
+            h = rb(swiglu_clamped(g, u, limit)).astype(np.float64)
+            y = rb((Wd @ h).astype(np.float32)).astype(np.float64)
+            if out is None:
+                out = np.zeros((N, y.shape[0]), np.float64)
+            out[n] += wf[n, j] * y
+    return out
+
+
+def sweep_xla_apply(deq, x, idx, w, limit, E, chunk=8, out_dtype="bf16"):
+    """The XLA prefill path ResidentFetch._apply_sweep_xla (resident.py:189-210, use_pallas=False): experts in
+    chunks of ``chunk``; per chunk g = einsum(xg, Wg) and u in out_dtype, h = swiglu (rounded as in
+    ``gather_apply``), h2 = out_dtype(f32(h) * rw) (resident.py:206), and the chunk's contribution
+    einsum("nem,emd->nd", h2, Wd) -- summed over the chunk's experts and the intermediate dimension with one
+    rounding to out_dtype -- is added to an f32 accumulator (resident.py:207).  Experts no token routes to add
+    exactly zero.  Returns f64 [T, D]."""
+    rb = round_bf16 if out_dtype == "bf16" else (lambda a: np.asarray(a, dtype=np.float32))
+    idx = np.asarray(idx)
+    T = idx.shape[0]
+    rw = routing_weights(idx, w, E)
+    xb = rb(np.asarray(x, dtype=np.float32)).astype(np.float64)
+    acc = None
+    for c0 in range(0, E, chunk):
+        part = None
+        for e in range(c0, min(E, c0 + chunk)):
+            toks = np.flatnonzero(rw[:, e] != 0)
+            if toks.size == 0:
+                continue
+            Wg = rb(deq("gate", e)).astype(np.float64)
+            Wu = rb(deq("up", e)).astype(np.float64)
+            Wd = rb(deq("down", e)).astype(np.float64)
+            g = rb((xb[toks] @ Wg.T).astype(np.float32))
+            u = rb((xb[toks] @ Wu.T).astype(np.float32))
+            h = rb(swiglu_clamped(g, u, limit))
+            h2 = rb(h.astype(np.float32) * rw[toks, e][:, None]).astype(np.float64)
+            if part is None:
+                part = np.zeros((T, Wd.shape[0]), np.float64)
+            part[toks] += h2 @ Wd.T
+        if part is None:
+            continue
+        if acc is None:
+            acc = np.zeros_like(part)
+        acc += rb(part.astype(np.float32)).astype(np.float64)
+    return acc
