@@ -105,12 +105,24 @@ size_t mi_moe_decode_workspace(const mi_table *gate, const mi_table *down, int32
                                int32_t shared_expert);
 
 /*
+ * mi_moe_decode with the activations in the layer dtype (the reference's apply takes x as the layer stores it:
+ * bf16 in production, f32 in its CPU tests, test_resident_cpu.py:81; resident.py:114 upcasts it to f32):
+ * x_dtype MI_X_BF16 (x bf16 [N, D], exactly mi_moe_decode) or MI_X_F32 (x f32 [N, D], staged as bf16 high part +
+ * remainder: 16 mantissa bits, ~2^-17 relative, one workgroup per task).  Same workspace size, limits and results.
+ */
+int mi_moe_decode_x(const mi_table *gate, const mi_table *up, const mi_table *down, const void *x, int32_t x_dtype,
+                    int32_t N, int32_t k, const int32_t *idx, const float *w, int32_t shared_expert, float limit,
+                    float *out_f32, uint16_t *out_bf16, void *workspace, size_t workspace_bytes, void *stream);
+
+/*
  * mi_moe_decode as ONE persistent launch (CB3 tables, N <= 8): gate/up, SwiGLU, down and the combine run as ordered
  * tasks that hand their results over through completion counters kept in the workspace; each workgroup streams its
  * gate/up tasks and then its down tasks with the next task's weights in flight.  Same arguments, workspace size and
- * results as mi_moe_decode (up to the f32 summation order of the column splits).  The workspace must be zero-filled
- * before its first use with this entry point; every call leaves its counter block zero again.  MI_ERR_QTYPE for
- * IQ3_S tables, MI_ERR_TOKENS for N > 8.
+ * results as mi_moe_decode (up to the f32 summation order of the column splits).  A small fill kernel zeroes the
+ * workspace's counter block first (so the workspace needs no initialisation): two launches on the stream.  A
+ * bounded wait that gives up (workgroups of the launch not resident together) ends the launch with invalid results
+ * and a nonzero error word, u32 index info[14] of mi_moe_decode_plan in the workspace, until the next call on that
+ * workspace.  MI_ERR_QTYPE for tables other than CB3, MI_ERR_TOKENS for N > 8.
  */
 int mi_moe_decode_fused(const mi_table *gate, const mi_table *up, const mi_table *down, const uint16_t *x_bf16,
                         int32_t N, int32_t k, const int32_t *idx, const float *w, int32_t shared_expert, float limit,

@@ -32,7 +32,7 @@ PLANE_KEYS = {"CB3": ("qs", "cb"), "IQ3_S": ("qs", "sg", "qh", "sc", "d"), "IQ4_
 
 # every symbol the header declares (tests check the library exports them)
 EXPORTS = ("mi_matvec", "mi_matvec_workspace", "mi_moe_decode", "mi_moe_decode_fused", "mi_moe_decode_phases",
-           "mi_moe_decode_workspace", "mi_moe_decode_plan", "mi_moe_decode_noalloc",
+           "mi_moe_decode_workspace", "mi_moe_decode_plan", "mi_moe_decode_noalloc", "mi_moe_decode_x",
            "mi_ragged_plan", "mi_moe_prefill", "mi_moe_prefill_workspace", "mi_dequant", "mi_int8_project", "mi_int8_project_workspace", "mi_int8_project_many",
            "mi_int8_project_many_workspace", "mi_moe_route", "mi_moe_route_workspace", "mi_pack_planes", "mi_strerror",
            "mi_version")
@@ -76,6 +76,7 @@ def lib():
         "mi_moe_decode_phases": (I, [T, T, T, P, I, I, P, P, I, F, P, P, P, Z, I, P]),
         "mi_moe_decode_workspace": (Z, [T, T, I, I, I]),
         "mi_moe_decode_noalloc": (I, [T, T, T, P, I, I, P, P, I, F, P, P, P]),
+        "mi_moe_decode_x": (I, [T, T, T, P, I, I, I, P, P, I, F, P, P, P, Z, P]),
         "mi_moe_decode_plan": (I, [T, T, I, I, I, ctypes.POINTER(ctypes.c_int32), I]),
         "mi_ragged_plan": (I, [P, P, I, I, I, I, P, P, P, P, P, P]),
         "mi_moe_prefill": (I, [T, T, T, P, I, I, P, P, I, F, I, P, P, P, Z, P]),

@@ -30,10 +30,12 @@
 // before its first wait; the grid is sized to what is resident at once (the runtime's occupancy), so every phase-1
 // task is held by a running workgroup that reaches it.
 //
-// Every counter returns to zero by the end of the launch (the last split of a row range, the last consumer of a
-// group's h and the combining workgroup reset what they counted), so the workspace's counter block must be zero
-// before the first call and stays zero between calls.  A wait that exceeds 2^20 polls sets an error word and gives up
-// (the launch then ends with wrong results instead of hanging).
+// The host zero-fills the counter block (counters and the error word) with a small kernel right before every launch,
+// so the workspace needs no initialisation and a launch whose wait gave up leaves no stale count behind; within a
+// launch every counter also returns to zero (the last split of a row range, the last consumer of a group's h and the
+// combining workgroup reset what they counted).  A wait that exceeds its poll limit (2^20 by default; the host may
+// set a smaller one) sets the error word and gives up: the launch then ends with wrong results instead of hanging,
+// and the error word stays set until the next call on that workspace.
 #pragma once
 #include "grouped.h"
 
@@ -41,7 +43,7 @@ namespace mi {
 
 constexpr int kMaxGroups = MI_MAX_SLOTS + kMaxT;   // routed groups (<= routed slots) + shared groups (<= 16)
 constexpr int kCtrStride = 32;                     // u32 words between separately contended counters (128 B)
-constexpr uint32_t kSpinLimit = 1u << 20;          // polls (~1 s) before a wait gives up
+constexpr uint32_t kSpinLimit = 1u << 20;          // polls (~1 s) before a wait gives up (the default)
 
 // All groups of one call, built once per workgroup (same content as find_group's single group).
 struct GroupTable {
@@ -132,6 +134,7 @@ struct FArgs {
     uint32_t *cnt2;                // [RBG2] x kCtrStride: finished down tasks per row range
     uint32_t *cnt1;                // [kMaxGroups * RBG1]: finished gate/up splits per (group, row range)
     uint32_t *err;                 // nonzero: a wait gave up
+    uint32_t spin_limit;           // polls before a wait gives up
     int S1, al1, nu1, RB1, RBG1;
     int S2, al2, nu2, RB2, RBG2;
     int xs_max;                    // LDS row pitch (dwords) of the larger staging
@@ -325,7 +328,7 @@ __global__ void __launch_bounds__(64 * kWgWaves, MI_CB3_WAVES) fused_decode_kern
                 uint32_t spins = 0;
                 while (ld_agent(c) < (uint32_t)a.RBG1) {
                     __builtin_amdgcn_s_sleep(2);
-                    if (++spins > kSpinLimit) {
+                    if (++spins > a.spin_limit) {
                         st_agent(a.err, 1u);
                         break;
                     }

@@ -61,10 +61,11 @@ struct KArgs {
     int xs_max;                // LDS row pitch in dwords (largest over the splits)
     int t_rows;                // LDS rows staged (class of the largest group)
     // activations
-    const uint16_t *x_bf16;    // kGateUp: [N, K] tokens; kDown: bf16 high part of h [NS, stride] by slot;
+    const uint16_t *x_bf16;    // kGateUp bf16: [N, K] tokens; kDown: bf16 high part of h [NS, stride] by slot;
                                // kMatvec bf16: [n_slots, stride]
     const uint16_t *x_lo;      // kDown: bf16 remainder of h [NS, stride] (h = x_bf16 + x_lo to 16 mantissa bits)
-    const float *x_f32;        // kMatvec f32: [n_slots, stride] (split into bf16 high + remainder while staging)
+    const float *x_f32;        // kGateUp f32: [N, stride] tokens; kMatvec f32: [n_slots, stride] (split into bf16
+                               // high + remainder while staging)
     int x_stride;
     // kDown without a SwiGLU launch: h formed while staging from the gate/up split partials [gu_S][2][NS][stride]
     // (sum of the splits in order, clamped SwiGLU, bf16 high + remainder: the SwiGLU kernel's arithmetic)
@@ -212,7 +213,7 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
     const int c1 = cb3 ? u1 * ucols : min(a.K, u1 * ucols);
     const int xs = (c1 - c0) >> 1;            // dwords per staged row
     const int xsp = cb3_row_pitch(xs);        // row pitch: whole 64-dword chunks, skewed by 4 banks per row
-    const bool hilo = (MODE == kDown) || (MODE == kMatvec && a.x_f32 != nullptr);
+    const bool hilo = (MODE == kDown) || a.x_f32 != nullptr;
     uint32_t *xh = xlds;
     uint32_t *xl = xlds + (size_t)a.t_rows * a.xs_max;
 
@@ -225,8 +226,7 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
     // the staging then waits only for these loads, not for the weight ring behind them, and each tile's matrix-core
     // work starts as soon as that tile arrives.
     // (with many staged rows the 4-byte loads outnumber the register path's 8-byte ones: register staging there)
-    const bool dma = cb3 && (MODE != kMatvec || a.x_f32 == nullptr) && a.gu_part == nullptr &&
-                     a.t_rows <= kDmaStageRows;
+    const bool dma = cb3 && a.x_f32 == nullptr && a.gu_part == nullptr && a.t_rows <= kDmaStageRows;
     bool stage_ring = true;     // the wavefront issues its weight ring before staging (false: it only stages)
     if (dma) {
         const __amdgpu_buffer_rsrc_t rh =
@@ -288,7 +288,8 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
                     hv = *(const uint2 *)(a.x_bf16 + (size_t)slot * a.x_stride + c);
                     lv = *(const uint2 *)(a.x_lo + (size_t)slot * a.x_stride + c);
                 } else {
-                    const float4 f = *(const float4 *)(a.x_f32 + (size_t)slot * a.x_stride + c);
+                    const int row = (MODE == kGateUp) ? slot_token(slot, a.n_route, a.k) : slot;
+                    const float4 f = *(const float4 *)(a.x_f32 + (size_t)row * a.x_stride + c);
                     uint32_t h0, l0, h1, l1, h2, l2, h3, l3;
                     split_bf16(f.x, h0, l0);
                     split_bf16(f.y, h1, l1);

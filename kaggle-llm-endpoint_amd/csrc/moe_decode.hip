@@ -210,6 +210,12 @@ __global__ void __launch_bounds__(64) swiglu_kernel(const float *__restrict__ p1
     ((uint2 *)h_lo)[i] = make_uint2(lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16));
 }
 
+// Zero n words (the one-launch decode's counter block, before every launch of it).
+__global__ void zero_words_kernel(uint32_t *__restrict__ p, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
 // Split reduction of a matvec: out[slot] = sum_s part[s][slot], splits in order.
 __global__ void split_reduce_kernel(const float *__restrict__ part, int S, int NS, int R, float *__restrict__ out) {
     const size_t n4 = (size_t)NS * R / 4;
@@ -522,7 +528,9 @@ static void plan_pstream(int mode, int tc, const Shape &sh, int G, size_t stagin
     *P = (int)(p < 1 ? 1 : p);
 }
 
-static DecodePlan plan_decode(const mi_table *gate, const mi_table *down, int N, int k, int shared) {
+// xf32: f32 activations (staged as bf16 high part + remainder, one workgroup per task).
+static DecodePlan plan_decode(const mi_table *gate, const mi_table *down, int N, int k, int shared,
+                              bool xf32 = false) {
     DecodePlan p{};
     const int n_route = N * k;
     // token class of the launch: an expert sees at most one slot per token under top-k routing, so groups are
@@ -533,7 +541,7 @@ static DecodePlan plan_decode(const mi_table *gate, const mi_table *down, int N,
     p.NS = n_route + (shared >= 0 ? N : 0);
     int est = N == 1 ? p.G : (p.G * 6 + 5) / 10;
     if (est < 1) est = 1;
-    p.persistent = gate->qtype == MI_QT_CB3 && down->qtype == MI_QT_CB3 &&
+    p.persistent = gate->qtype == MI_QT_CB3 && down->qtype == MI_QT_CB3 && !xf32 &&
                    N > env_int("MI355MOE_PERSIST_ABOVE", kPersistentMinTokens);
     if (p.persistent) {
         // persistent launches: tasks are pipelined, so the per-task fixed cost is small
@@ -547,7 +555,7 @@ static DecodePlan plan_decode(const mi_table *gate, const mi_table *down, int N,
         plan_pstream(kDown, tc, p.s2, p.G, sizeof(uint32_t) * 2 * (size_t)p.rows2 * max_xs(down, p.s2.sp), scratch,
                      &p.P2, &p.lds2);
     } else {
-        p.s1 = choose_shape(gate, kGateUp, p.rows1, est, p.rows1, 4, "MI355MOE_S1");
+        p.s1 = choose_shape(gate, kGateUp, p.rows1, est, p.rows1, xf32 ? 8 : 4, "MI355MOE_S1");
         p.s2 = choose_shape(down, kDown, p.rows2, est, p.rows2, 8, "MI355MOE_S2");
     }
     size_t off = 0;
@@ -690,8 +698,11 @@ size_t mi_moe_decode_workspace(const mi_table *gate, const mi_table *down, int32
                                int32_t shared_expert) {
     if (validate_table(gate) || validate_table(down) || N <= 0 || k <= 0) return 0;
     if (N > kMaxT || N * k > MI_MAX_SLOTS) return 0;
-    // counter block, then the larger of the two layouts (the fused launch's and the separate launches')
-    const size_t sep = ctr_layout(gate, down).bytes + plan_decode(gate, down, N, k, shared_expert).total;
+    // counter block, then the largest of the layouts (the fused launch's and the separate launches' for bf16 and
+    // f32 activations)
+    const size_t sep_b = plan_decode(gate, down, N, k, shared_expert).total;
+    const size_t sep_f = plan_decode(gate, down, N, k, shared_expert, true).total;
+    const size_t sep = ctr_layout(gate, down).bytes + (sep_b > sep_f ? sep_b : sep_f);
     const size_t fused = plan_fused(gate, down, N, k, shared_expert).total;
     return sep > fused ? sep : fused;
 }
@@ -701,13 +712,13 @@ size_t mi_moe_decode_workspace(const mi_table *gate, const mi_table *down, int32
 namespace mi {
 
 // Host-side argument checks of the separate-launch decode (every status before any launch).
-static int decode_validate(const mi_table *gate, const mi_table *up, const mi_table *down, const uint16_t *x_bf16,
+static int decode_validate(const mi_table *gate, const mi_table *up, const mi_table *down, const void *x,
                            int N, int k, const int32_t *idx, const float *w, int shared_expert, float limit,
                            const float *out_f32, const uint16_t *out_bf16, int phases) {
     int st;
     if (phases < 1 || phases > 3) return MI_ERR_ARG;
     if ((st = validate_table(gate)) || (st = validate_table(up)) || (st = validate_table(down))) return st;
-    if (!x_bf16 || !idx || !w || ((phases & 2) && !out_f32 && !out_bf16)) return MI_ERR_NULL;
+    if (!x || !idx || !w || ((phases & 2) && !out_f32 && !out_bf16)) return MI_ERR_NULL;
     if (up->qtype != gate->qtype || up->rows != gate->rows || up->cols != gate->cols ||
         up->n_experts != gate->n_experts)
         return MI_ERR_MISMATCH;
@@ -720,9 +731,12 @@ static int decode_validate(const mi_table *gate, const mi_table *up, const mi_ta
 
 // The separate launches of one decode layer (arguments already validated): ws is the data region (partials, h) of
 // p.total bytes -- past the counter block of a caller's workspace, or the library's static scratch.
+// x: bf16 [N, D], or f32 [N, D] when xf32 (the plan must have been made for it).
 static int decode_launch(const DecodePlan &p, const mi_table *gate, const mi_table *up, const mi_table *down,
-                         const uint16_t *x_bf16, int N, int k, const int32_t *idx, const float *w, int shared_expert,
-                         float limit, float *out_f32, uint16_t *out_bf16, char *ws, int phases, hipStream_t s) {
+                         const void *x, bool xf32, int N, int k, const int32_t *idx, const float *w,
+                         int shared_expert, float limit, float *out_f32, uint16_t *out_bf16, char *ws, int phases,
+                         hipStream_t s) {
+    const uint16_t *x_bf16 = xf32 ? nullptr : (const uint16_t *)x;
     int st;
     KArgs a{};
     a.E = gate->n_experts;
@@ -747,10 +761,10 @@ static int decode_launch(const DecodePlan &p, const mi_table *gate, const mi_tab
     a.xs_max = max_xs(gate, p.s1.sp);
     a.t_rows = p.rows1;
     a.x_bf16 = x_bf16;
-    a.x_f32 = nullptr;
+    a.x_f32 = xf32 ? (const float *)x : nullptr;
     a.x_stride = gate->cols;
     a.part = (float *)(ws + p.off_part1);
-    size_t lds1 = sizeof(uint32_t) * (size_t)a.t_rows * a.xs_max;
+    size_t lds1 = sizeof(uint32_t) * (xf32 ? 2 : 1) * (size_t)a.t_rows * a.xs_max;
     const bool cb3 = p.persistent;
     const int tc = a.t_rows <= 8 ? 8 : 16;
     PArgs pa{};
@@ -886,8 +900,22 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
     const size_t ctr_bytes = ctr_layout(gate, down).bytes;
     if (!workspace || workspace_bytes < ctr_bytes + p.total) return MI_ERR_WORKSPACE;
     // the fused launch's counters at the start of the workspace stay untouched
-    return decode_launch(p, gate, up, down, x_bf16, N, k, idx, w, shared_expert, limit, out_f32, out_bf16,
+    return decode_launch(p, gate, up, down, x_bf16, false, N, k, idx, w, shared_expert, limit, out_f32, out_bf16,
                          (char *)workspace + ctr_bytes, phases, (hipStream_t)stream);
+}
+
+int mi_moe_decode_x(const mi_table *gate, const mi_table *up, const mi_table *down, const void *x, int32_t x_dtype,
+                    int32_t N, int32_t k, const int32_t *idx, const float *w, int32_t shared_expert, float limit,
+                    float *out_f32, uint16_t *out_bf16, void *workspace, size_t workspace_bytes, void *stream) {
+    if (x_dtype != MI_X_BF16 && x_dtype != MI_X_F32) return MI_ERR_ARG;
+    const int st = decode_validate(gate, up, down, x, N, k, idx, w, shared_expert, limit, out_f32, out_bf16, 3);
+    if (st) return st;
+    const bool xf32 = x_dtype == MI_X_F32;
+    const DecodePlan p = plan_decode(gate, down, N, k, shared_expert, xf32);
+    const size_t ctr_bytes = ctr_layout(gate, down).bytes;
+    if (!workspace || workspace_bytes < ctr_bytes + p.total) return MI_ERR_WORKSPACE;
+    return decode_launch(p, gate, up, down, x, xf32, N, k, idx, w, shared_expert, limit, out_f32, out_bf16,
+                         (char *)workspace + ctr_bytes, 3, (hipStream_t)stream);
 }
 
 int mi_moe_decode_noalloc(const mi_table *gate, const mi_table *up, const mi_table *down, const uint16_t *x_bf16,
@@ -899,8 +927,8 @@ int mi_moe_decode_noalloc(const mi_table *gate, const mi_table *up, const mi_tab
     if (p.total > (size_t)MI_NOALLOC_SCRATCH_BYTES) return MI_ERR_WORKSPACE;
     char *ws = (char *)scratch_ptr();
     if (!ws) return MI_ERR_LAUNCH;
-    return decode_launch(p, gate, up, down, x_bf16, N, k, idx, w, shared_expert, limit, out_f32, out_bf16, ws, 3,
-                         (hipStream_t)stream);
+    return decode_launch(p, gate, up, down, x_bf16, false, N, k, idx, w, shared_expert, limit, out_f32, out_bf16,
+                         ws, 3, (hipStream_t)stream);
 }
 
 int mi_moe_decode(const mi_table *gate, const mi_table *up, const mi_table *down, const uint16_t *x_bf16,
@@ -971,6 +999,13 @@ int mi_moe_decode_fused(const mi_table *gate, const mi_table *up, const mi_table
     a.RBG2 = p.s2.RBG;
     a.xs_max = p.xs_max;
     a.P = p.P;
+    // polls before a wait gives up: MI355MOE_SPIN_LIMIT overrides the default (tests force a give-up with it)
+    const int spin = env_int("MI355MOE_SPIN_LIMIT", -1);
+    a.spin_limit = spin >= 0 ? (uint32_t)spin : kSpinLimit;
+    // a fresh counter block and error word for this launch (a fill kernel: no memset node if the call is captured)
+    const int nw = (int)(cl.bytes / 4);
+    hipLaunchKernelGGL(zero_words_kernel, dim3((nw + 255) / 256), dim3(256), 0, (hipStream_t)stream, ctr, nw);
+    if ((st = launch_status())) return st;
     launch_fused(p.s1.rtw, dim3(p.P), p.lds, (hipStream_t)stream, a);
     return launch_status();
 }

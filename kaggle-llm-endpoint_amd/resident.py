@@ -268,17 +268,29 @@ def decode_plan(gate, down, N, k, shared_expert=-1):
     return {key: int(info[i]) for i, key in enumerate(keys)}
 
 
+def fused_error(workspace, gate, down):
+    """The error word of mi_moe_decode_fused in ``workspace`` (synchronises the current stream): nonzero when a
+    bounded wait of the last call on that workspace gave up, i.e. its results are invalid."""
+    err = decode_plan(gate, down, 1, 1)["err_word"]
+    torch.cuda.current_stream().synchronize()
+    return int(workspace[4 * err:4 * err + 4].view(torch.int32).item())
+
+
 def moe_decode(gate, up, down, x, idx, w, limit, shared_expert=-1, want_f32=True, want_bf16=False, out_f32=None,
-               out_bf16=None, workspace=None, phases=3, fused=False):
+               out_bf16=None, workspace=None, phases=3, fused=False, check_error=False):
     """Fused decode MoE (resident.py:110-120 composition), tokens grouped by expert on the device.
-    x bf16 [N, D]; idx int32 [N, k]; w f32 [N, k] -> (out_f32 [N, D] or None, out_bf16 [N, D] or None).
-    Preallocated ``out_f32`` / ``out_bf16`` / ``workspace`` (a zero-filled uint8 device tensor of
-    decode_workspace_bytes, kept for later calls) make the call allocation-free (graph capture).  ``fused=True``
-    runs the layer as one persistent launch (mi_moe_decode_fused: CB3, N <= 8); ``phases`` 1 / 2 run part of the
-    separate launches (mi_moe_decode_phases): 1 = the gate/up launch only, 2 = SwiGLU + down + combine only (after a
-    phase-1 call on the same workspace), 3 = all (mi_moe_decode)."""
-    if x.dtype != torch.bfloat16:
-        raise ValueError("decode activations are bf16")
+    x bf16 or f32 [N, D] (the layer dtype; f32 through mi_moe_decode_x); idx int32 [N, k]; w f32 [N, k] ->
+    (out_f32 [N, D] or None, out_bf16 [N, D] or None).
+    Preallocated ``out_f32`` / ``out_bf16`` / ``workspace`` (a uint8 device tensor of decode_workspace_bytes, kept
+    for later calls) make the call allocation-free (graph capture).  ``fused=True`` runs the layer as one persistent
+    launch (mi_moe_decode_fused: CB3, N <= 8); with ``check_error=True`` the call then synchronises and raises if a bounded
+    wait of that launch gave up (results invalid; ``fused_error``).  ``phases`` 1 / 2 run part of the separate
+    launches (mi_moe_decode_phases): 1 = the gate/up launch only, 2 = SwiGLU + down + combine only (after a phase-1
+    call on the same workspace), 3 = all (mi_moe_decode)."""
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("decode activations are bf16 or f32")
+    if x.dtype == torch.float32 and (fused or phases != 3):
+        raise ValueError("f32 activations take the separate launches (phases=3, fused=False)")
     N, k = idx.shape
     x = x.contiguous()
     if idx.dtype != torch.int32:
@@ -300,6 +312,13 @@ def moe_decode(gate, up, down, x, idx, w, limit, shared_expert=-1, want_f32=True
         check("mi_moe_decode_fused", lib().mi_moe_decode_fused(gate.c, up.c, down.c, _ptr(x), N, k, _ptr(idx),
                                                                _ptr(w), int(shared_expert), float(limit), _ptr(of),
                                                                _ptr(ob), _ptr(ws), ws.numel(), _stream()))
+        if check_error and fused_error(ws, gate, down):
+            raise RuntimeError("mi_moe_decode_fused: a bounded wait gave up (workgroups of the launch were not "
+                               "resident together); the results of this call are invalid")
+    elif x.dtype == torch.float32:
+        check("mi_moe_decode_x", lib().mi_moe_decode_x(gate.c, up.c, down.c, _ptr(x), _lib.MI_X_F32, N, k, _ptr(idx),
+                                                       _ptr(w), int(shared_expert), float(limit), _ptr(of), _ptr(ob),
+                                                       _ptr(ws), ws.numel(), _stream()))
     elif phases == 3:
         check("mi_moe_decode", lib().mi_moe_decode(gate.c, up.c, down.c, _ptr(x), N, k, _ptr(idx), _ptr(w),
                                                    int(shared_expert), float(limit), _ptr(of), _ptr(ob), _ptr(ws),
@@ -473,19 +492,50 @@ def int8_project_many(x, projections, want_f32=False, outputs=None, workspace=No
 
 
 # ------------------------------------------------------------------------------------------------ the operator
+def _is_f32(dtype):
+    """out_dtype given as a torch dtype, a numpy/JAX dtype or its name: True for float32."""
+    return dtype in (torch.float32, "float32", "f32") or str(dtype).endswith("float32")
+
+
+def decode_chunked(gate, up, down, x, idx, w, limit, shared_expert=-1, out=None):
+    """The decode composition (resident.py:110-120, f32 end to end) for any number of tokens: mi_moe_decode /
+    mi_moe_decode_x over consecutive chunks of at most 16 tokens and 128 slots (tokens are independent, so the
+    chunking does not change any result).  x bf16 or f32 [N, D] -> f32 [N, D]."""
+    N, k = idx.shape
+    if k > _lib.MI_MAX_SLOTS:
+        raise NotImplementedError("top-%d routing exceeds the decode kernels' %d slots per call" % (k, _lib.MI_MAX_SLOTS))
+    step = min(_lib.MAX_DECODE_TOKENS, _lib.MI_MAX_SLOTS // k)
+    if out is None:
+        out = torch.empty((N, down.rows), dtype=torch.float32, device=x.device)
+    for c0 in range(0, N, step):
+        c1 = min(N, c0 + step)
+        moe_decode(gate, up, down, x[c0:c1], idx[c0:c1], w[c0:c1], limit, shared_expert=shared_expert,
+                   out_f32=out[c0:c1])
+    return out
+
+
 class ResidentFetch:
     """Drop-in for glm53.resident.ResidentFetch (resident.py:68-108): same constructor, ``qtypes`` and ``apply``.
 
-    apply(p, x, idx, w, layer, limit): x [N, D]; idx [N, k] int32 into E; w [N, k] f32 -> f32 [N, D] (routed experts
-    only; the caller adds the shared expert, model.py:847-855).  N*k <= gather_max_rows takes the fused decode
-    kernels (f32 end to end, resident.py:110-120); larger calls take the grouped prefill GEMMs with the reference's
-    bf16 rounding points and ``combine`` (resident.py:144-165; CB3, IQ2_S, IQ3_S or IQ4_XS tables; bf16
-    ``out_dtype``).
-    ``use_pallas`` / ``interpret`` / ``sweep_mode`` / ``chunk`` are accepted for signature compatibility; there is a
-    single MI355X kernel path per regime."""
+    apply(p, x, idx, w, layer, limit): x [N, D] (bf16 or f32); idx [N, k] int32 into E; w [N, k] f32 -> f32 [N, D]
+    (routed experts only; the caller adds the shared expert, model.py:847-855).  The branches of the reference's
+    apply (resident.py:100-108,137-143), each with that branch's rounding points:
+      * N*k <= gather_max_rows, use_pallas: _apply_kernel -- the fused decode kernels, f32 end to end
+        (resident.py:110-120), in chunks of <= 16 tokens / 128 slots;
+      * N*k > gather_max_rows, use_pallas, sweep_mode "ragged": _apply_ragged_kernel -- the grouped prefill GEMMs with
+        the bf16 rounding points and ``combine`` (resident.py:144-165);
+      * out_dtype float32, any branch: every value stays f32 (test_resident_cpu.py:81,124), i.e. the decode
+        composition in f32, taken by the decode kernels in chunks.
+    The bf16 forms of the dense sweep (sweep_mode "dense", resident.py:169-187) and of the XLA paths
+    (use_pallas=False, resident.py:122-135,189-210) raise NotImplementedError rather than run with other rounding.
+    ``interpret`` and ``chunk`` only matter to those XLA paths."""
 
     def __init__(self, qtypes, D, ml, out_dtype=torch.bfloat16, gather_max_rows=64, chunk=8, use_pallas=True,
                  interpret=False, sweep_mode="ragged", tm=32, combine="matmul"):
+        if sweep_mode not in ("ragged", "dense"):
+            raise ValueError("sweep_mode must be 'ragged' or 'dense'")
+        if combine not in _lib.COMBINES:
+            raise ValueError("combine must be 'matmul' or 'gather'")
         self.qtypes = qtypes
         self.rows = {"gate_q": ml, "up_q": ml, "down_q": D}
         self.cols = {"gate_q": D, "up_q": D, "down_q": ml}
@@ -510,20 +560,29 @@ class ResidentFetch:
             self._tables = {key: t}
         return t
 
+    def branch(self, N, k):
+        """The reference's branch for an [N, k] routing: "kernel", "gather", "ragged", "sweep" or "sweep_xla"."""
+        if N * k <= self.gather_max_rows:
+            return "kernel" if self.use_pallas else "gather"
+        if not self.use_pallas:
+            return "sweep_xla"
+        return "ragged" if self.sweep_mode == "ragged" else "sweep"
+
     def apply(self, p, x, idx, w, layer, limit):
         gate, up, down = self.tables(p, layer)
         N, k = idx.shape
-        if N * k <= self.gather_max_rows:
-            xb = x if x.dtype == torch.bfloat16 else x.to(torch.bfloat16)
-            if x.dtype != torch.bfloat16 and not torch.equal(xb.to(x.dtype), x):
-                raise ValueError("decode activations must be bf16-representable (the layer dtype)")
-            out, _ = moe_decode(gate, up, down, xb, idx, w, limit)
+        br = self.branch(N, k)
+        if x.dtype not in (torch.bfloat16, torch.float32):
+            x = x.to(torch.float32)
+        if br == "kernel" or _is_f32(self.out_dtype):
+            return decode_chunked(gate, up, down, x, idx, w, limit)
+        if br == "ragged":
+            if gate.qtype != up.qtype:
+                raise NotImplementedError("ResidentFetch.apply: the grouped prefill path takes one format for gate "
+                                          "and up (moe_ragged_gateup decodes both with one qtype)")
+            out, _ = moe_prefill(gate, up, down, x.to(torch.bfloat16), idx, w, limit, combine=self.combine)
             return out
-        if gate.qtype != up.qtype:
-            raise NotImplementedError("ResidentFetch.apply: the grouped prefill path (N*k = %d > gather_max_rows = %d) "
-                                      "takes one format for gate and up" % (N * k, self.gather_max_rows))
-        if self.out_dtype != torch.bfloat16:
-            raise NotImplementedError("ResidentFetch.apply: the grouped prefill path follows the bf16 out_dtype "
-                                      "rounding points (resident.py:153-158)")
-        out, _ = moe_prefill(gate, up, down, x.to(torch.bfloat16), idx, w, limit, combine=self.combine)
-        return out
+        raise NotImplementedError("ResidentFetch.apply: the %s branch with bf16 out_dtype (%s) is not built" %
+                                  (br, {"gather": "use_pallas=False decode, resident.py:122-135",
+                                        "sweep": "sweep_mode='dense', resident.py:169-187",
+                                        "sweep_xla": "use_pallas=False prefill, resident.py:189-210"}[br]))

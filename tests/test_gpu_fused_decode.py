@@ -86,6 +86,36 @@ def test_fused_repeated_calls_one_workspace(pkg, gpu):
         assert rel_l2(of.cpu().numpy(), _want(L, x, idx, w, limit, E)) < 1e-5, "call %d" % it
 
 
+def test_fused_wait_give_up_is_reported_and_the_next_call_is_clean(pkg, gpu, monkeypatch):
+    """A poll limit of 0 set from the host makes a wait give up at its first unsuccessful poll (no kernel is kept
+    from exiting: the launch just ends with invalid results).  The error word reports it; the next call with the
+    default limit on the same workspace -- whose counters the forced calls may have left anywhere, as the garbage it
+    started with -- is correct, with a clear error word and zero counters."""
+    rng = np.random.default_rng(43)
+    E, D, I, N, k, limit = 12, 640, 256, 6, 4, 10.0
+    L = Layer(rng, "CB3", E + 1, D, I)
+    tbs = L.tables(pkg)
+    ws = torch.full((pkg.resident.decode_workspace_bytes(tbs["gate"], tbs["down"], N, k, E),), 0xA5,
+                    dtype=torch.uint8, device="cuda")
+    idx, w = zipf_routing(rng, N, E, k)
+    x = round_bf16(rng.standard_normal((N, D)).astype(np.float32))
+    args = (tbs["gate"], tbs["up"], tbs["down"], _t(x, torch.bfloat16), _t(idx), _t(w), limit)
+    monkeypatch.setenv("MI355MOE_SPIN_LIMIT", "0")
+    gave_up = 0
+    for _ in range(8):
+        pkg.moe_decode(*args, shared_expert=E, workspace=ws, fused=True)
+        gave_up += pkg.resident.fused_error(ws, tbs["gate"], tbs["down"]) != 0
+    assert gave_up > 0, "no wait had to poll in 8 forced calls"
+    with pytest.raises(RuntimeError):
+        for _ in range(8):                           # check_error=True raises on a call whose wait gave up
+            pkg.moe_decode(*args, shared_expert=E, workspace=ws, fused=True, check_error=True)
+    monkeypatch.delenv("MI355MOE_SPIN_LIMIT")
+    of, _ = pkg.moe_decode(*args, shared_expert=E, workspace=ws, fused=True, check_error=True)
+    torch.cuda.synchronize()
+    _counters_clean(pkg, tbs, ws, N, k, E)
+    assert rel_l2(of.cpu().numpy(), _want(L, x, idx, w, limit, E)) < 1e-5
+
+
 @pytest.mark.parametrize("env,Ns,fused", [
     ({"MI355MOE_FS1": "3", "MI355MOE_FS2": "2"}, (1, 5, 8), True),
     ({"MI355MOE_FS1": "5", "MI355MOE_FS1_RTW": "2", "MI355MOE_FS2": "3"}, (1, 5, 8), True),
