@@ -220,6 +220,33 @@ def matvec(table, idx, X):
     return matvec_into(table, idx, X, out, None)
 
 
+def pm_to_natural(qtype, X):
+    """The reference's per-word activation matrix X [..., W, C] (X[w, c] = x[input(w, c)], planes.py:73-112) back in
+    natural input order [..., W*C]: the inverse of pm_x's reshapes and transposes (a view for IQ2_S / IQ3_S, one
+    transposing copy for IQ4_XS and the K-quants).  CB3, which has no reference layout, is in natural order."""
+    lead = tuple(X.shape[:-2])
+    n = X.shape[-2] * X.shape[-1]
+    if qtype in ("IQ2_S", "IQ3_S", "CB3"):
+        return X.reshape(lead + (n,))
+    if qtype == "IQ4_XS":                       # [sub, wq, pos, j] -> [sub, pos, wq, j]
+        return X.reshape(lead + (n // 32, 4, 2, 4)).transpose(-3, -2).reshape(lead + (n,))
+    if qtype in ("Q2_K", "Q3_K"):               # [b, n, q, s, j] -> [b, n, s, q, j]
+        return X.reshape(lead + (n // 256, 2, 8, 4, 4)).transpose(-3, -2).reshape(lead + (n,))
+    raise ValueError(qtype)
+
+
+def moe_matvec(planes, qtype, nblk, idx, X, *, interpret=False, lane_block=None):
+    """moe_matvec (pallas_moe.py:238-307) with the reference's arguments: planes {plane: int32 [1 or none,
+    E*rows_p, R]} in ``qtype``'s planar layout, nblk = K / 256, idx int32 [Nk], X [Nk, W, C] in the planar order
+    (planes.py:96-112) -> f32 [Nk, R], out[i, r] = sum_n W_idx[i][r, n] x_i[n].  ``interpret`` and ``lane_block``
+    are the Pallas call's own options and change nothing here.  Rows of ids outside [0, E) are zero."""
+    R = int(planes["qs"].shape[-1])
+    table = ExpertTable(qtype, planes, R, QK * int(nblk))
+    if X.shape[0] != idx.numel():
+        raise ValueError("X must hold one [W, C] matrix per slot")
+    return matvec(table, idx, pm_to_natural(qtype, X))
+
+
 def matvec_into(table, idx, X, out, workspace):
     """``matvec`` writing into ``out`` f32 [n_slots, R]; a preallocated ``workspace`` (uint8 device tensor of at
     least mi_matvec_workspace bytes) makes the call allocation-free."""

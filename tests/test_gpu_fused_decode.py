@@ -239,7 +239,8 @@ def test_fused_full_shape(pkg, gpu, full_cb3_layer):
                          device="cuda")
         args = (tbs["gate"], tbs["up"], tbs["down"], xt, _t(idx), _t(w), limit)
         sep, _ = pkg.moe_decode(*args, shared_expert=E, workspace=ws)
-        if N > 8:                                  # the separate launches only: persistent at this size
+        if N > 8:                                  # the separate launches only: persistent at this size (checked
+                                                   # against an f64 reference in test_gpu_configs.py)
             assert pkg.resident.decode_plan(tbs["gate"], tbs["down"], N, k, E)["sep_P1"] > 0
             continue
         of, _ = pkg.moe_decode(*args, shared_expert=E, workspace=ws, fused=True)

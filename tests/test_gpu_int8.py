@@ -13,7 +13,8 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("B,n_in,n_out", [(8, 512, 256), (1, 256, 16), (8, 2048, 6144), (16, 1024, 2048),
-                                          (32, 512, 512), (3, 6144, 2048)])
+                                          (32, 512, 512), (3, 6144, 2048),
+                                          (8, 6144, 6144), (8, 6144, 2048)])      # config 3: Q/K/V/O, shared gate/up
 def test_int8_project(pkg, gpu, B, n_in, n_out):
     rng = np.random.default_rng(B * 1000 + n_out)
     q, s = oi8.generate(rng, n_in, n_out)
