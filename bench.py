@@ -391,7 +391,7 @@ def bench_int8(torch, pkg, gen, args):
                 projs.append((qT, s))
                 outs.append((torch.empty((B, n_out), dtype=torch.bfloat16, device="cuda"), None))
             n_outs = (ctypes.c_int32 * len(st))(*[o for _, o in st])
-            ws = torch.zeros(max(256, pkg._lib.lib().mi_int8_project_many_workspace(B, n_in, n_outs, len(st))),
+            ws = torch.zeros(max(256, pkg._lib.lib().mi_int8_project_many_workspace(B, n_in, n_outs, len(st), 1)),
                              dtype=torch.uint8, device="cuda")
             ops.append((x, projs, outs, ws))
         fns.append(lambda ops=ops: [pkg.int8_project_many(x, projs, outputs=outs, workspace=ws)

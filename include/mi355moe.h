@@ -15,6 +15,7 @@
  *   moe_ragged_gateup / moe_ragged_down                    pallas_moe.py:622-755 -> mi_moe_prefill
  *   dequant_planes (XLA dequant of the planar tables)      planes.py:196-206     -> mi_dequant
  *   quant8.dequant_tree + x @ W (int8 projections)         quant8.py:91-99       -> mi_int8_project(_many)
+ *   Engine._logits_local, int8 lm_head (scale after dot)   engine.py:345-351     -> mi_int8_project (MI_I8_COL_AFTER)
  */
 #ifndef MI355MOE_H
 #define MI355MOE_H
@@ -246,22 +247,30 @@ size_t mi_moe_prefill_workspace(const mi_table *gate, const mi_table *down, int3
 int mi_dequant(const mi_table *t, int32_t expert, float *out, void *stream);
 
 /*
- * int8 per-output-channel projection (quant8.py:91-99 + x @ W):
- *   y[b, o] = sum_i x[b, i] * bf16(f32(q[o, i]) * s[o])     f32 accumulation, bf16 out (+ optional f32 out)
- * x bf16 [B, n_in]; qT int8 [n_out, n_in] (the reference's q [in, out] transposed once at load);
- * s f32 [n_out].  1 <= B <= 32, n_in % 256 == 0, n_out % 16 == 0.  The weights are dequantized to bf16 in
- * registers and contracted on the matrix cores (bf16 x bf16 products are exact, f32 accumulation).
+ * int8 projection (quant8.py:91-99 + x @ W) with the reference's scale layouts (quantize_array, quant8.py:26-32;
+ * scale_axis, quant8.py:59-60) and the lm_head form (engine.py:345-351):
+ *   MI_I8_ROW_SCALES (0): s f32 [n_in] (the reference's [in, 1], row-sharded leaves):
+ *                         y[b, o] = sum_i x[b, i] * bf16(f32(q[o, i]) * s[i])
+ *   MI_I8_COL_SCALES (1): s f32 [n_out] (the reference's [1, out]):  y[b, o] = sum_i x[b, i] * bf16(f32(q[o, i]) * s[o])
+ *   MI_I8_COL_AFTER  (2): s f32 [n_out], the scale after the dot:      y[b, o] = (sum_i x[b, i] * q[o, i]) * s[o]
+ * f32 accumulation; bf16 out (one rounding of the f32 result) and/or f32 out.
+ * x bf16 [B, n_in]; qT int8 [n_out, n_in] (the reference's q [in, out] transposed once at load).
+ * 1 <= B <= 32, n_in % 256 == 0, n_out % 16 == 0.  The weights are dequantized to bf16 in registers and contracted
+ * on the matrix cores (bf16 x bf16 products are exact, f32 accumulation).
  * The workspace holds split-K partials (no initialisation needed); a second launch sums them in order.
  */
-int mi_int8_project(const uint16_t *x_bf16, int32_t B, const int8_t *qT, const float *s, int32_t n_in,
-                    int32_t n_out, uint16_t *y_bf16, float *y_f32, void *workspace, size_t workspace_bytes,
-                    void *stream);
-size_t mi_int8_project_workspace(int32_t B, int32_t n_in, int32_t n_out);
+#define MI_I8_ROW_SCALES 0
+#define MI_I8_COL_SCALES 1
+#define MI_I8_COL_AFTER  2
+int mi_int8_project(const uint16_t *x_bf16, int32_t B, const int8_t *qT, const float *s, int32_t scale_axis,
+                    int32_t n_in, int32_t n_out, uint16_t *y_bf16, float *y_f32, void *workspace,
+                    size_t workspace_bytes, void *stream);
+size_t mi_int8_project_workspace(int32_t B, int32_t n_in, int32_t n_out, int32_t scale_axis);
 
 /*
- * Several int8 projections of the same activations in one launch (Q, K, V of x; the shared expert's gate and up):
- * projs[j] = {qT [n_out_j, n_in], s [n_out_j], n_out_j, y_bf16 and/or y_f32 [B, n_out_j]}, 1 <= n_proj <= 8.
- * Each output equals what mi_int8_project gives for that projection alone.
+ * Several int8 projections of the same activations in one launch (Q, K, V of x; the shared expert's gate and up),
+ * all with the same scale layout: projs[j] = {qT [n_out_j, n_in], s (as scale_axis), n_out_j, y_bf16 and/or y_f32
+ * [B, n_out_j]}, 1 <= n_proj <= 8.  Each output equals what mi_int8_project gives for that projection alone.
  */
 typedef struct mi_i8_proj {
     const int8_t *qT;
@@ -271,8 +280,9 @@ typedef struct mi_i8_proj {
     float *y_f32;
 } mi_i8_proj;
 int mi_int8_project_many(const uint16_t *x_bf16, int32_t B, int32_t n_in, const mi_i8_proj *projs, int32_t n_proj,
-                         void *workspace, size_t workspace_bytes, void *stream);
-size_t mi_int8_project_many_workspace(int32_t B, int32_t n_in, const int32_t *n_out, int32_t n_proj);
+                         int32_t scale_axis, void *workspace, size_t workspace_bytes, void *stream);
+size_t mi_int8_project_many_workspace(int32_t B, int32_t n_in, const int32_t *n_out, int32_t n_proj,
+                                      int32_t scale_axis);
 
 const char *mi_strerror(int status);
 int mi_version(void);

@@ -19,6 +19,9 @@ MI_X_BF16 = 0
 MI_X_F32 = 1
 MI_MAX_SLOTS = 128
 MAX_DECODE_TOKENS = 16
+MI_I8_ROW_SCALES = 0         # s [n_in]: the reference's per-row scales [in, 1]
+MI_I8_COL_SCALES = 1         # s [n_out]: per-column scales [1, out]
+MI_I8_COL_AFTER = 2          # s [n_out] applied after the dot (the int8 lm_head)
 MI_COMBINE_MATMUL = 0
 MI_COMBINE_GATHER = 1
 COMBINES = {"matmul": MI_COMBINE_MATMUL, "gather": MI_COMBINE_GATHER}
@@ -82,10 +85,10 @@ def lib():
         "mi_moe_prefill": (I, [T, T, T, P, I, I, P, P, I, F, I, P, P, P, Z, P]),
         "mi_moe_prefill_workspace": (Z, [T, T, I, I, I]),
         "mi_dequant": (I, [T, I, P, P]),
-        "mi_int8_project": (I, [P, I, P, P, I, I, P, P, P, Z, P]),
-        "mi_int8_project_workspace": (Z, [I, I, I]),
-        "mi_int8_project_many": (I, [P, I, I, ctypes.POINTER(MiI8Proj), I, P, Z, P]),
-        "mi_int8_project_many_workspace": (Z, [I, I, ctypes.POINTER(ctypes.c_int32), I]),
+        "mi_int8_project": (I, [P, I, P, P, I, I, I, P, P, P, Z, P]),
+        "mi_int8_project_workspace": (Z, [I, I, I, I]),
+        "mi_int8_project_many": (I, [P, I, I, ctypes.POINTER(MiI8Proj), I, I, P, Z, P]),
+        "mi_int8_project_many_workspace": (Z, [I, I, ctypes.POINTER(ctypes.c_int32), I, I]),
         "mi_moe_route": (I, [P, P, P, I, I, I, I, I, F, P, P, P, Z, P]),
         "mi_moe_route_workspace": (Z, [I, I, I]),
         "mi_pack_planes": (I, [I, P, I, I, I, ctypes.POINTER(ctypes.c_void_p), P]),

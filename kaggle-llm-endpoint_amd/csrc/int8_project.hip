@@ -1,12 +1,15 @@
-// int8 per-output-channel projections for gfx950: y = x @ bf16(f32(q) * s)   (quant8.py:91-99 + the x @ W uses).
+// int8 projections for gfx950: y = x @ bf16(f32(q) * s)   (quant8.py:91-99 + the x @ W uses), with the reference's
+// per-output-column scales s [1, out] or per-input-row scales s [in, 1] (quant8.py:26-32,59-60), and the lm_head
+// form y = (x @ f32(q)) * s[o], the scale applied after the dot (engine.py:345-351).
 //
 // Weights qT [n_out, n_in] int8 (input-contiguous) stream once from HBM; every wavefront owns a 16-row tile of
 // outputs and one column split.  A lane loads 32 consecutive int8 of its row per 128-column block (4 lanes = one
 // 128-byte line per row), dequantizes them in registers to exactly the reference's bf16(f32(q) * s):
 //   f32: fma(q + 128, s, -128 s) rounds q * s once (q + 128 is an unsigned byte, so one v_cvt_f32_ubyte each);
 //   bf16: round to nearest even (v_cvt_pk_bf16_f32)
-// and feeds v_mfma_f32_16x16x32_bf16 (bf16 x bf16 products are exact, f32 accumulation) with the staged activations
-// as the B operand (up to 16 tokens per tile).  Inside a block the lane's 32 bytes are 4 k-steps of 8 columns:
+// (per-row scales: the element's own s[i], staged in LDS beside the activations; the lm_head form: q itself, exact
+// in bf16) and feeds v_mfma_f32_16x16x32_bf16 (bf16 x bf16 products are exact, f32 accumulation) with the staged
+// activations as the B operand (up to 16 tokens per tile).  Inside a block the lane's 32 bytes are 4 k-steps of 8 columns:
 // step c of block p uses columns 128p + 32q + 8c .. +7 (q = lane / 16) for both operands.  Splits write f32
 // partials that split_reduce_i8 sums in order (no counters, deterministic); one split writes y directly.
 #include "common.h"
@@ -23,7 +26,7 @@ constexpr int kI8MaxProj = 8;      // projections sharing one activation matrix 
 
 struct I8Proj {
     const int8_t *q;       // [n_out, n_in]
-    const float *s;        // [n_out]
+    const float *s;        // [n_out] (MI_I8_COL_SCALES, MI_I8_COL_AFTER) or [n_in] (MI_I8_ROW_SCALES)
     int n_out;
     uint16_t *y_bf16;      // [B, n_out] (S == 1)
     float *y_f32;          // [B, n_out] (S == 1)
@@ -33,6 +36,7 @@ struct I8Proj {
 struct I8Args {
     const uint16_t *x;     // bf16 [B, n_in], shared by every projection
     int B, n_in, S;
+    int scale_axis;        // MI_I8_*: one per launch
     int blocks;            // 128-column blocks per split
     int n_proj;
     int wg_start[kI8MaxProj + 1];   // first workgroup of each projection
@@ -59,9 +63,20 @@ __device__ __forceinline__ bf16x8 i8_weights8(uint32_t w0, uint32_t w1, float s,
     return __builtin_bit_cast(bf16x8, v);
 }
 
-template <int TT>   // token tiles of 16 (B <= 16 * TT)
+// 8 int8 weights of one row with their own scales s[0..7] (per-input-row scales) -> bf16(f32(q) * s), as above.
+__device__ __forceinline__ bf16x8 i8_weights8_rs(uint32_t w0, uint32_t w1, float4 sa, float4 sb) {
+    const uint32_t u0 = w0 ^ 0x80808080u, u1 = w1 ^ 0x80808080u;
+    uint4 v;
+    v.x = bf16_pair(fmaf((float)(u0 & 255u), sa.x, -128.0f * sa.x), fmaf((float)((u0 >> 8) & 255u), sa.y, -128.0f * sa.y));
+    v.y = bf16_pair(fmaf((float)((u0 >> 16) & 255u), sa.z, -128.0f * sa.z), fmaf((float)(u0 >> 24), sa.w, -128.0f * sa.w));
+    v.z = bf16_pair(fmaf((float)(u1 & 255u), sb.x, -128.0f * sb.x), fmaf((float)((u1 >> 8) & 255u), sb.y, -128.0f * sb.y));
+    v.w = bf16_pair(fmaf((float)((u1 >> 16) & 255u), sb.z, -128.0f * sb.z), fmaf((float)(u1 >> 24), sb.w, -128.0f * sb.w));
+    return __builtin_bit_cast(bf16x8, v);
+}
+
+template <int TT, int SA>   // token tiles of 16 (B <= 16 * TT); SA: MI_I8_* scale form
 __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
-    extern __shared__ uint32_t xs[];                 // [B][cols / 2] bf16 pairs of the split's columns
+    extern __shared__ uint32_t xs[];                 // [B][cols / 2] bf16 pairs of the split's columns (+ row scales)
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     int pj = 0;
@@ -91,15 +106,20 @@ __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
 #pragma unroll
         for (int d = 0; d < kI8Ring; ++d) load_block(d, ring[d][0], ring[d][1]);
     }
-    // stage the activations of the split (bf16 pairs), rows < B
+    // stage the activations of the split (bf16 pairs), rows < B; per-row scales: the split's s[k0 .. k0 + cols)
     const int cw = cols / 2;                         // dwords per staged row
     for (int e = tid; e < a.B * (cw / 4); e += blockDim.x) {
         const int b = e / (cw / 4), c4 = e - b * (cw / 4);
         *(uint4 *)(xs + b * cw + 4 * c4) = *(const uint4 *)(a.x + (size_t)b * a.n_in + k0 + 8 * c4);
     }
+    float *srow = (float *)(xs + a.B * cw);
+    if constexpr (SA == MI_I8_ROW_SCALES) {
+        for (int e = tid; e < cols / 4; e += blockDim.x) *(float4 *)(srow + 4 * e) = *(const float4 *)(P.s + k0 + 4 * e);
+    }
     __syncthreads();
     if (!active) return;
-    const float sc = P.s[o0 + i];
+    // per-column scales: the row's s; the lm_head form: q itself (scale 1 here, s[o] after the sum)
+    const float sc = SA == MI_I8_COL_SCALES ? P.s[o0 + i] : 1.0f;
     const float ns128 = -128.0f * sc;
 
     f32x4 acc[TT];
@@ -120,7 +140,13 @@ __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
             const uint32_t W[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                const bf16x8 A = i8_weights8(W[2 * c], W[2 * c + 1], sc, ns128);
+                bf16x8 A;
+                if constexpr (SA == MI_I8_ROW_SCALES) {
+                    const float *sp = srow + 128 * p + 32 * q + 8 * c;
+                    A = i8_weights8_rs(W[2 * c], W[2 * c + 1], *(const float4 *)sp, *(const float4 *)(sp + 4));
+                } else {
+                    A = i8_weights8(W[2 * c], W[2 * c + 1], sc, ns128);
+                }
 #pragma unroll
                 for (int t = 0; t < TT; ++t) {
                     const uint4 xv = *(const uint4 *)(xrow[t] + 64 * p + 4 * c);
@@ -131,11 +157,20 @@ __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
         }
     }
     // C layout: lane (jt = lane % 16, q) holds output rows o0 + 4q + r for token 16 t + jt
+    const int o = o0 + 4 * q;
+    if constexpr (SA == MI_I8_COL_AFTER) {          // the lm_head form: scale after the whole sum (one split)
+        if (a.S == 1) {
+            const float4 so = *(const float4 *)(P.s + o);
+#pragma unroll
+            for (int t = 0; t < TT; ++t) {
+                acc[t][0] *= so.x; acc[t][1] *= so.y; acc[t][2] *= so.z; acc[t][3] *= so.w;
+            }
+        }
+    }
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
         const int b = 16 * t + i;
         if (b >= a.B) continue;
-        const int o = o0 + 4 * q;
         if (a.S == 1) {
             if (P.y_f32) *(float4 *)(P.y_f32 + (size_t)b * P.n_out + o) = make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
             if (P.y_bf16) {
@@ -171,6 +206,10 @@ __global__ void __launch_bounds__(256) split_reduce_i8(I8Args a) {
             v.x += p[j].x; v.y += p[j].y; v.z += p[j].z; v.w += p[j].w;
         }
     }
+    if (a.scale_axis == MI_I8_COL_AFTER) {           // the lm_head form: s[o] after the whole sum
+        const float4 so = *(const float4 *)(P.s + 4 * li % P.n_out);
+        v.x *= so.x; v.y *= so.y; v.z *= so.z; v.w *= so.w;
+    }
     if (P.y_f32) ((float4 *)P.y_f32)[li] = v;
     if (P.y_bf16) {
         uint2 b;
@@ -180,18 +219,22 @@ __global__ void __launch_bounds__(256) split_reduce_i8(I8Args a) {
     }
 }
 
+// LDS bytes per staged column: B bf16 activations (+ one f32 scale with per-input-row scales).
+static size_t i8_col_bytes(int B, int scale_axis) { return 2 * (size_t)B + (scale_axis == MI_I8_ROW_SCALES ? 4 : 0); }
+
 // Column splits: enough wavefronts to cover the chip (about 3 per SIMD, 3072 over 256 CUs), every wavefront
-// streaming at least 4 blocks of 128 columns, the split's staged activations within 48 KB of LDS.  `tiles` counts
-// the 16-row tiles of every projection of the launch.
-static int i8_splits(int B, int n_in, int tiles) {
+// streaming at least 4 blocks of 128 columns, the split's staged columns within 48 KB of LDS.  `tiles` counts the
+// 16-row tiles of every projection of the launch.
+static int i8_splits(int B, int n_in, int tiles, int scale_axis) {
     const int nblk = n_in / 128;
+    const size_t cb = i8_col_bytes(B, scale_axis);
     const char *env = getenv("MI355MOE_I8S");      // experiments: a forced split count (must divide n_in / 128)
-    if (env && atoi(env) > 0 && nblk % atoi(env) == 0 && (size_t)B * (n_in / atoi(env)) * 2 <= 48 * 1024)
+    if (env && atoi(env) > 0 && nblk % atoi(env) == 0 && (size_t)(n_in / atoi(env)) * cb <= 48 * 1024)
         return atoi(env);
     int best = 1;
     for (int S = 1; S <= nblk; ++S) {
         if (nblk % S) continue;
-        if ((size_t)B * (n_in / S) * 2 > 48 * 1024) continue;
+        if ((size_t)(n_in / S) * cb > 48 * 1024) continue;
         if (nblk / S < 4 && S > 1) break;
         best = S;
         if ((long long)tiles * S >= 3072) break;
@@ -211,22 +254,25 @@ using namespace mi;
 
 extern "C" {
 
-size_t mi_int8_project_many_workspace(int32_t B, int32_t n_in, const int32_t *n_out, int32_t n_proj) {
+size_t mi_int8_project_many_workspace(int32_t B, int32_t n_in, const int32_t *n_out, int32_t n_proj,
+                                      int32_t scale_axis) {
     if (B <= 0 || B > 32 || n_in <= 0 || n_in % 256 || !n_out || n_proj <= 0 || n_proj > kI8MaxProj) return 0;
+    if (scale_axis < MI_I8_ROW_SCALES || scale_axis > MI_I8_COL_AFTER) return 0;
     size_t total = 0;
     for (int j = 0; j < n_proj; ++j) {
         if (n_out[j] <= 0 || n_out[j] % 16) return 0;
         total += (size_t)n_out[j];
     }
-    const int S = i8_splits(B, n_in, i8_tiles(n_out, n_proj));
+    const int S = i8_splits(B, n_in, i8_tiles(n_out, n_proj), scale_axis);
     return S == 1 ? 256 : sizeof(float) * (size_t)S * B * total;
 }
 
 int mi_int8_project_many(const uint16_t *x_bf16, int32_t B, int32_t n_in, const mi_i8_proj *projs, int32_t n_proj,
-                         void *workspace, size_t workspace_bytes, void *stream) {
+                         int32_t scale_axis, void *workspace, size_t workspace_bytes, void *stream) {
     if (!x_bf16 || !projs) return MI_ERR_NULL;
     if (B <= 0 || B > 32) return MI_ERR_TOKENS;
     if (n_proj <= 0 || n_proj > kI8MaxProj) return MI_ERR_ARG;
+    if (scale_axis < MI_I8_ROW_SCALES || scale_axis > MI_I8_COL_AFTER) return MI_ERR_ARG;
     if (n_in <= 0 || n_in % 256) return MI_ERR_SHAPE;
     int32_t n_out[kI8MaxProj];
     for (int j = 0; j < n_proj; ++j) {
@@ -235,13 +281,14 @@ int mi_int8_project_many(const uint16_t *x_bf16, int32_t B, int32_t n_in, const 
         if (p.n_out <= 0 || p.n_out % 16) return MI_ERR_SHAPE;
         n_out[j] = p.n_out;
     }
-    const size_t need = mi_int8_project_many_workspace(B, n_in, n_out, n_proj);
+    const size_t need = mi_int8_project_many_workspace(B, n_in, n_out, n_proj, scale_axis);
     if (!workspace || workspace_bytes < need) return MI_ERR_WORKSPACE;
     I8Args a{};
     a.x = x_bf16;
     a.B = B;
     a.n_in = n_in;
-    a.S = i8_splits(B, n_in, i8_tiles(n_out, n_proj));
+    a.S = i8_splits(B, n_in, i8_tiles(n_out, n_proj), scale_axis);
+    a.scale_axis = scale_axis;
     a.blocks = n_in / 128 / a.S;
     a.n_proj = n_proj;
     size_t off = 0;
@@ -259,10 +306,12 @@ int mi_int8_project_many(const uint16_t *x_bf16, int32_t B, int32_t n_in, const 
         wg += (p.n_out + 16 * kI8Waves - 1) / (16 * kI8Waves) * a.S;
     }
     a.wg_start[n_proj] = wg;
-    const size_t lds = sizeof(uint16_t) * (size_t)B * 128 * a.blocks;
+    const size_t lds = i8_col_bytes(B, scale_axis) * 128 * a.blocks;
     hipStream_t st = (hipStream_t)stream;
-    if (B <= 16) hipLaunchKernelGGL(int8_project_kernel<1>, dim3(wg), dim3(64 * kI8Waves), lds, st, a);
-    else hipLaunchKernelGGL(int8_project_kernel<2>, dim3(wg), dim3(64 * kI8Waves), lds, st, a);
+    typedef void (*Kern)(I8Args);
+    static const Kern kern[2][3] = {{int8_project_kernel<1, 0>, int8_project_kernel<1, 1>, int8_project_kernel<1, 2>},
+                                    {int8_project_kernel<2, 0>, int8_project_kernel<2, 1>, int8_project_kernel<2, 2>}};
+    hipLaunchKernelGGL(kern[B <= 16 ? 0 : 1][scale_axis], dim3(wg), dim3(64 * kI8Waves), lds, st, a);
     if (hipGetLastError() != hipSuccess) return MI_ERR_LAUNCH;
     if (a.S == 1) return MI_OK;
     int n4 = 0;
@@ -271,18 +320,18 @@ int mi_int8_project_many(const uint16_t *x_bf16, int32_t B, int32_t n_in, const 
     return hipGetLastError() == hipSuccess ? MI_OK : MI_ERR_LAUNCH;
 }
 
-size_t mi_int8_project_workspace(int32_t B, int32_t n_in, int32_t n_out) {
-    return mi_int8_project_many_workspace(B, n_in, &n_out, 1);
+size_t mi_int8_project_workspace(int32_t B, int32_t n_in, int32_t n_out, int32_t scale_axis) {
+    return mi_int8_project_many_workspace(B, n_in, &n_out, 1, scale_axis);
 }
 
-int mi_int8_project(const uint16_t *x_bf16, int32_t B, const int8_t *qT, const float *s, int32_t n_in,
-                    int32_t n_out, uint16_t *y_bf16, float *y_f32, void *workspace, size_t workspace_bytes,
-                    void *stream) {
+int mi_int8_project(const uint16_t *x_bf16, int32_t B, const int8_t *qT, const float *s, int32_t scale_axis,
+                    int32_t n_in, int32_t n_out, uint16_t *y_bf16, float *y_f32, void *workspace,
+                    size_t workspace_bytes, void *stream) {
     if (!x_bf16 || !qT || !s || (!y_bf16 && !y_f32)) return MI_ERR_NULL;
     if (B <= 0 || B > 32) return MI_ERR_TOKENS;
     if (n_in <= 0 || n_out <= 0 || n_in % 256 || n_out % 16) return MI_ERR_SHAPE;
     const mi_i8_proj p{qT, s, n_out, y_bf16, y_f32};
-    return mi_int8_project_many(x_bf16, B, n_in, &p, 1, workspace, workspace_bytes, stream);
+    return mi_int8_project_many(x_bf16, B, n_in, &p, 1, scale_axis, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

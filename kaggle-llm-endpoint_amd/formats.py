@@ -229,9 +229,17 @@ def cb3_hbm_bytes(R, K):
 
 # ------------------------------------------------------------------------------------------------ int8
 def int8_pack(q, s):
-    """Reference leaf {"q": int8 [in, out], "s": f32 [1, out]} (per-column scales) -> (qT int8 [out, in], s [out])."""
+    """Reference leaf {"q": int8 [in, out], "s": f32 [1, out] or [in, 1]} (quant8.py:17-18,26-32) ->
+    (qT int8 [out, in], s flat f32, axis): axis 1 for per-column scales [1, out] (s [out]), 0 for per-row scales
+    [in, 1] (s [in]), as quantize_array's ``axis``."""
     q = np.asarray(q, dtype=np.int8)
     s = np.asarray(s, dtype=np.float32)
-    if s.shape != (1, q.shape[1]):
-        raise ValueError("int8_pack expects per-output-channel scales [1, out], got %s" % (s.shape,))
-    return np.ascontiguousarray(q.T), np.ascontiguousarray(s.reshape(-1))
+    if q.ndim != 2:
+        raise ValueError("int8_pack expects q [in, out]")
+    if s.shape == (1, q.shape[1]):
+        axis = 1
+    elif s.shape == (q.shape[0], 1):
+        axis = 0
+    else:
+        raise ValueError("int8_pack expects scales [1, out] or [in, 1], got %s for q %s" % (s.shape, q.shape))
+    return np.ascontiguousarray(q.T), np.ascontiguousarray(s.reshape(-1)), axis

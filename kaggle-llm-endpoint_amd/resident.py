@@ -471,32 +471,62 @@ def moe_prefill(gate, up, down, x, idx, w, limit, shared_expert=-1, combine="mat
     return of, ob
 
 
-def int8_project(x, qT, s, want_f32=False, y_bf16=None, y_f32=None, workspace=None):
-    """y = x @ bf16(f32(q) * s) (quant8.py:91-99): x bf16 [B, n_in], qT int8 [n_out, n_in], s f32 [n_out].
+def _scale_len(scale_axis, n_in, n_out):
+    if scale_axis not in (_lib.MI_I8_ROW_SCALES, _lib.MI_I8_COL_SCALES, _lib.MI_I8_COL_AFTER):
+        raise ValueError("scale_axis must be MI_I8_ROW_SCALES, MI_I8_COL_SCALES or MI_I8_COL_AFTER")
+    return n_in if scale_axis == _lib.MI_I8_ROW_SCALES else n_out
+
+
+def int8_project(x, qT, s, want_f32=False, y_bf16=None, y_f32=None, workspace=None, scale_axis=_lib.MI_I8_COL_SCALES):
+    """y = x @ bf16(f32(q) * s) (quant8.py:91-99): x bf16 [B, n_in], qT int8 [n_out, n_in], s f32 [n_out]
+    (``scale_axis`` MI_I8_COL_SCALES, the reference's [1, out]) or [n_in] (MI_I8_ROW_SCALES, its [in, 1]);
+    MI_I8_COL_AFTER: y = (x @ f32(q)) * s[o], the int8 lm_head (engine.py:345-351).
     Preallocated outputs / workspace make the call allocation-free."""
     B, n_in = x.shape
     n_out = qT.shape[0]
+    if s.numel() != _scale_len(scale_axis, n_in, n_out):
+        raise ValueError("int8_project: %d scales for scale_axis %d" % (s.numel(), scale_axis))
     x = x.contiguous()
     yb = y_bf16 if y_bf16 is not None else torch.empty((B, n_out), dtype=torch.bfloat16, device=x.device)
     yf = y_f32 if y_f32 is not None else (
         torch.empty((B, n_out), dtype=torch.float32, device=x.device) if want_f32 else None)
-    nbytes = lib().mi_int8_project_workspace(B, n_in, n_out)
+    nbytes = lib().mi_int8_project_workspace(B, n_in, n_out, int(scale_axis))
     if nbytes == 0:
         raise ValueError("mi_int8_project: unsupported shape B=%d n_in=%d n_out=%d" % (B, n_in, n_out))
     ws = workspace if workspace is not None else WORKSPACES.get("int8", nbytes)
-    check("mi_int8_project", lib().mi_int8_project(_ptr(x), B, _ptr(qT), _ptr(s), n_in, n_out, _ptr(yb), _ptr(yf),
-                                                   _ptr(ws), ws.numel(), _stream()))
+    check("mi_int8_project", lib().mi_int8_project(_ptr(x), B, _ptr(qT), _ptr(s), int(scale_axis), n_in, n_out,
+                                                   _ptr(yb), _ptr(yf), _ptr(ws), ws.numel(), _stream()))
     return (yb, yf) if want_f32 else yb
 
 
-def int8_project_many(x, projections, want_f32=False, outputs=None, workspace=None):
+def int8_leaf(leaf, device="cuda"):
+    """A reference int8 leaf {"q": int8 [in, out], "s": f32 [1, out] or [in, 1]} (quant8.py:17-18,26-32) -> the
+    device operands (qT int8 [out, in], s f32 flat, scale_axis) of int8_project."""
+    qT, s, axis = formats.int8_pack(leaf["q"], leaf["s"])
+    return (torch.from_numpy(qT).to(device), torch.from_numpy(s).to(device),
+            _lib.MI_I8_ROW_SCALES if axis == 0 else _lib.MI_I8_COL_SCALES)
+
+
+def int8_logits(h, leaf, **kw):
+    """The int8 lm_head (Engine._logits_local, engine.py:345-351): (h @ f32(q)) * s, then h's dtype (bf16)."""
+    qT, s, axis = int8_leaf(leaf, h.device) if isinstance(leaf, dict) else leaf
+    if axis != _lib.MI_I8_COL_SCALES:
+        raise ValueError("the lm_head's scales are per output column [1, out]")
+    return int8_project(h, qT, s, scale_axis=_lib.MI_I8_COL_AFTER, **kw)
+
+
+def int8_project_many(x, projections, want_f32=False, outputs=None, workspace=None,
+                      scale_axis=_lib.MI_I8_COL_SCALES):
     """Several projections of the same activations in one launch (Q, K, V of x; the shared expert's gate and up):
-    projections = [(qT int8 [n_out_j, n_in], s f32 [n_out_j]), ...] (at most 8) -> a list with, per projection,
-    what ``int8_project`` returns.  ``outputs`` = [(y_bf16, y_f32 or None), ...] preallocated makes the call
-    allocation-free."""
+    projections = [(qT int8 [n_out_j, n_in], s f32), ...] (at most 8, one ``scale_axis`` for all) -> a list with,
+    per projection, what ``int8_project`` returns.  ``outputs`` = [(y_bf16, y_f32 or None), ...] preallocated makes
+    the call allocation-free."""
     B, n_in = x.shape
     x = x.contiguous()
     n = len(projections)
+    for qT, s in projections:
+        if s.numel() != _scale_len(scale_axis, n_in, qT.shape[0]):
+            raise ValueError("int8_project_many: %d scales for scale_axis %d" % (s.numel(), scale_axis))
     arr = (_lib.MiI8Proj * n)()
     outs = []
     for j, (qT, s) in enumerate(projections):
@@ -509,12 +539,12 @@ def int8_project_many(x, projections, want_f32=False, outputs=None, workspace=No
         arr[j] = _lib.MiI8Proj(qT.data_ptr(), s.data_ptr(), n_out, _ptr(yb), _ptr(yf))
         outs.append((yb, yf) if want_f32 else yb)
     n_outs = (ctypes.c_int32 * n)(*[int(qT.shape[0]) for qT, _ in projections])
-    nbytes = lib().mi_int8_project_many_workspace(B, n_in, n_outs, n)
+    nbytes = lib().mi_int8_project_many_workspace(B, n_in, n_outs, n, int(scale_axis))
     if nbytes == 0:
         raise ValueError("mi_int8_project_many: unsupported shapes (B=%d, n_in=%d, n_proj=%d)" % (B, n_in, n))
     ws = workspace if workspace is not None else WORKSPACES.get("int8", nbytes)
-    check("mi_int8_project_many", lib().mi_int8_project_many(_ptr(x), B, n_in, arr, n, _ptr(ws), ws.numel(),
-                                                             _stream()))
+    check("mi_int8_project_many", lib().mi_int8_project_many(_ptr(x), B, n_in, arr, n, int(scale_axis), _ptr(ws),
+                                                             ws.numel(), _stream()))
     return outs
 
 

@@ -38,3 +38,10 @@ def project_f32(x, q, s):
 def project_bf16(x, q, s):
     """The projection's bf16 output, as f32 values."""
     return round_bf16(project_f32(x, q, s))
+
+
+def project_after_f32(x, q, s):
+    """The int8 lm_head (Engine._logits_local, engine.py:345-351): dot(x, f32(q)) with f64 accumulation rounded to
+    f32, times s [1, out] in f32 -> f32 [B, out] (before the cast to x's dtype)."""
+    z = (np.asarray(x, dtype=np.float64) @ np.asarray(q, dtype=np.float64)).astype(np.float32)
+    return (z * np.asarray(s, dtype=np.float32)).astype(np.float32)

@@ -75,12 +75,12 @@ def test_host_validation_codes(L, pkg):
     assert L.mi_matvec(ctypes.byref(g), idx, 4, x, 7, 1280, out, ws, 1 << 30, None) == 8
     assert L.mi_matvec(ctypes.byref(g), idx, 4, x, lib.MI_X_BF16, 1000, out, ws, 1 << 30, None) == 8
     assert L.mi_dequant(ctypes.byref(g), 4, out, None) == 8                        # expert out of range
-    assert L.mi_int8_project(x, 0, P(1), P(2), 256, 64, out, None, ws, 1 << 20, None) == 4
-    assert L.mi_int8_project(x, 8, P(1), P(2), 300, 64, out, None, ws, 1 << 20, None) == 3
-    assert L.mi_int8_project(x, 8, P(1), P(2), 256, 40, out, None, ws, 1 << 20, None) == 3
-    assert L.mi_int8_project(x, 8, P(1), P(2), 256, 64, None, None, ws, 1 << 20, None) == 1
-    assert L.mi_int8_project_workspace(8, 6144, 6144) > 0
-    assert L.mi_int8_project_workspace(8, 300, 64) == 0
+    assert L.mi_int8_project(x, 0, P(1), P(2), 1, 256, 64, out, None, ws, 1 << 20, None) == 4
+    assert L.mi_int8_project(x, 8, P(1), P(2), 1, 300, 64, out, None, ws, 1 << 20, None) == 3
+    assert L.mi_int8_project(x, 8, P(1), P(2), 1, 256, 40, out, None, ws, 1 << 20, None) == 3
+    assert L.mi_int8_project(x, 8, P(1), P(2), 1, 256, 64, None, None, ws, 1 << 20, None) == 1
+    assert L.mi_int8_project_workspace(8, 6144, 6144, 1) > 0
+    assert L.mi_int8_project_workspace(8, 300, 64, 1) == 0
 
 
 def test_prefill_host_validation(L, pkg):

@@ -103,7 +103,13 @@ def test_int8_pack(pkg):
     rng = np.random.default_rng(0)
     q = rng.integers(-127, 128, (64, 32), dtype=np.int8)
     s = rng.uniform(0.5e-3, 2e-3, (1, 32)).astype(np.float32)
-    qT, sv = pkg.formats.int8_pack(q, s)
-    assert qT.shape == (32, 64) and np.array_equal(qT.T, q) and np.array_equal(sv, s[0])
+    qT, sv, axis = pkg.formats.int8_pack(q, s)
+    assert qT.shape == (32, 64) and np.array_equal(qT.T, q) and np.array_equal(sv, s[0]) and axis == 1
+    sr = rng.uniform(0.5e-3, 2e-3, (64, 1)).astype(np.float32)        # per-row scales [in, 1] (quant8.py:26-32)
+    qT, sv, axis = pkg.formats.int8_pack(q, sr)
+    assert np.array_equal(qT.T, q) and np.array_equal(sv, sr[:, 0]) and axis == 0
     with pytest.raises(ValueError):
-        pkg.formats.int8_pack(q, np.ones((64, 1), np.float32))          # per-row scales are not this layout
+        pkg.formats.int8_pack(q, np.ones((64, 32), np.float32))
+    L = pkg._lib.lib()
+    assert L.mi_int8_project_workspace(8, 6144, 6144, 0) > 0 and L.mi_int8_project_workspace(8, 6144, 6144, 2) > 0
+    assert L.mi_int8_project_workspace(8, 6144, 6144, 3) == 0

@@ -35,6 +35,31 @@ def test_int8_dequant_matches_torch():
     assert np.array_equal(oi8.dequant_bf16(q, s).view(np.uint32), want.view(np.uint32))
 
 
+def test_int8_row_scales_match_torch():
+    """Per-row scales [in, 1] (quant8.py:26-32, axis 0): bf16(f32(q) * s[i]), checked with torch's rounding."""
+    rng = np.random.default_rng(11)
+    q = rng.integers(-127, 128, (256, 64), dtype=np.int8)
+    s = rng.uniform(0.5e-3, 2e-3, (256, 1)).astype(np.float32)
+    want = (torch.from_numpy(q).float() * torch.from_numpy(s)).to(torch.bfloat16).float().numpy()
+    got = oi8.dequant_bf16(q, s)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert not np.array_equal(got, oi8.dequant_bf16(q, s.reshape(1, -1)[:, :64]))    # not the per-column form
+    qq, ss = oi8.quantize_array(rng.standard_normal((256, 64)).astype(np.float32), 0)
+    assert ss.shape == (256, 1) and np.abs(qq).max() == 127
+
+
+def test_int8_lm_head_form_matches_torch():
+    """engine.py:345-351: dot(h, q as h's dtype) in f32, times s after the dot."""
+    rng = np.random.default_rng(12)
+    q = rng.integers(-127, 128, (512, 96), dtype=np.int8)
+    s = rng.uniform(0.5e-3, 2e-3, (1, 96)).astype(np.float32)
+    x = ob.round_bf16(rng.standard_normal((3, 512)).astype(np.float32))
+    xt = torch.from_numpy(x).double()
+    want = ((xt @ torch.from_numpy(q).double()).float() * torch.from_numpy(s)).numpy()
+    assert np.array_equal(oi8.project_after_f32(x, q, s), want)
+    assert ob.rel_l2(oi8.project_after_f32(x, q, s), oi8.project_f32(x, q, s)) > 1e-4    # differs from bf16(q*s)
+
+
 def test_int8_projection_matches_torch():
     rng = np.random.default_rng(2)
     q, s = oi8.generate(rng, 512, 64)
