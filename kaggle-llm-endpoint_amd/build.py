@@ -35,6 +35,7 @@ UNITS += [("k_grouped.hip", ["-DMI_KMODE=%d" % m, "-DMI_KQT=%d" % q], "k_grouped
 UNITS += [("k_fused.hip", [], "k_fused")]
 UNITS += [("k_pstream.hip", ["-DMI_PMODE=%d" % m, "-DMI_PTC=%d" % tc], "k_pstream_%d_%d" % (m, tc))
           for m in (0, 1) for tc in (8, 16)]
+UNITS += [("k_custream.hip", ["-DMI_CMODE=%d" % m], "k_custream_%d" % m) for m in (0, 1)]
 
 
 def _filter(stderr):

@@ -1,0 +1,185 @@
+// CU-balanced CB3 streams for single-token decode (gate/up partials, down partials) on gfx950.
+//
+// Measured on MI355X: a CU serves the vector memory requests of its resident workgroups roughly oldest first, so
+// when a launch puts 4 or 5 one-task workgroups on a CU the youngest gets its first tile 15-20 us after the oldest,
+// and CUs holding one workgroup more than others finish last.  At one token the layer's weight stream is short
+// (~20 us at the HBM ceiling), so that imbalance, not the stream itself, set the launch time.
+//
+// Here the grid is one workgroup per CU (the launch holds exactly as many workgroups as the device has CUs, and the
+// workgroup's LDS keeps a second one off the CU), and the ordered list of work units -- (group, matrix, column split,
+// 16 RTW-row tile) -- is cut into equal contiguous shares, one per workgroup: every CU streams the same bytes.  Inside
+// the workgroup, every wavefront claims its next unit from an LDS counter when it starts its current unit's last
+// super tile (cb3_stream refills the ring from the claimed unit while the current one finishes), so a wavefront that
+// the CU serves later simply takes fewer units and the workgroup ends within about one unit of its share.
+//
+// With one token a group is one slot (its expert read straight from the routing ids: no grouping pass before the
+// first weight request), every group of the gate/up launch multiplies the same activation row, and the down launch
+// stages the h rows (bf16 high part and remainder) of the groups its share touches; the rows go to LDS with
+// direct-to-LDS loads issued ahead of the weight ring.  Each unit writes its own f32 partial rows (the next launch
+// reduces them in a fixed order), so no workgroup waits on another.
+#pragma once
+#include <type_traits>
+
+#include "fused_decode.h"
+
+namespace mi {
+
+struct CArgs {
+    Cb3Table t0, t1;           // gate, up (kGateUp) or down (t0 only)
+    int R, K;                  // rows, cols of the table(s)
+    int E, n_route, N, k, shared_expert, NS;
+    int S, al, nu;             // column splits: boundaries at multiples of `al` column tiles over nu tiles
+    int RT;                    // 16 RTW-row tiles per matrix
+    int U;                     // units: groups * nmat * S * RT (upper bound; units past the call's groups are empty)
+    int P;                     // workgroups (= CUs)
+    int gmax;                  // kDown: most groups any workgroup's share touches (staged rows)
+    int xsp;                   // LDS row pitch (dwords) of a staged row
+    const uint16_t *x;         // kGateUp: x bf16 [1, K]; kDown: bf16 high part of h [NS, K]
+    const uint16_t *x_lo;      // kDown: bf16 remainder of h [NS, K]
+    const int32_t *idx;
+    float *part;               // [S][nmat][NS][R]
+};
+
+constexpr int kCuWaves = 12;   // wavefronts per workgroup (3 per SIMD)
+
+template <int MODE, int RTW>
+__global__ void __launch_bounds__(64 * kCuWaves, 1) custream_kernel(CArgs a) {
+    // staged rows, then the wavefronts' codebook slots, all read with 16-byte LDS loads: the dynamic segment must
+    // start 16-byte aligned (at an 8-byte-aligned start this launch measured 2.8x slower)
+    extern __shared__ __attribute__((aligned(16))) uint32_t xlds[];
+    __shared__ uint32_t s_next;
+    __shared__ int s_exp[MI_MAX_SLOTS + 1];         // expert of every slot (group)
+    constexpr bool hilo = MODE == kDown;            // h: hi in columns 0-7 of the tile, lo in 8-15
+    constexpr int nmat = MODE == kGateUp ? 2 : 1;
+    const int tid = threadIdx.x, lane = tid & 63, jt = lane & 15, q = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+    // one token: group gi is slot gi (the k routed slots, then the shared expert's, whose slot is k); a slot with an
+    // expert id outside [0, E) has empty units (the combine leaves it out)
+    const int n_groups = a.NS;
+    const int per_g = nmat * a.S * a.RT;
+    const int U = n_groups * per_g;
+    const int u_begin = (int)((long long)blockIdx.x * U / a.P);
+    const int u_end = (int)((long long)(blockIdx.x + 1) * U / a.P);
+    if (u_begin >= u_end) return;
+    const int g0 = u_begin / per_g;
+    const int ng = hilo ? min(a.gmax, n_groups - g0) : 1;
+    const int rows = hilo ? 2 * ng : 1;             // gate/up: the token's x row; down: hi and lo of each group's h
+    uint4 *cbl = (uint4 *)(xlds + (size_t)rows * a.xsp);    // 16-byte aligned: the pitch is a multiple of 4 dwords
+    if (tid == 0) s_next = (uint32_t)u_begin + kCuWaves;    // the first kCuWaves units are taken without a claim
+    // every slot's expert into LDS (read there after the staging barrier: a claim then touches LDS only -- a global
+    // load inside the stream would make the wavefront wait for every weight load issued before it)
+    if (tid < n_groups) s_exp[tid] = tid < a.n_route ? a.idx[tid] : a.shared_expert;
+
+    // unit u = (group gi, matrix, split, row tile), row tile fastest
+    struct Unit {
+        int gi, mat, split, rt, e;
+    };
+    // from_lds: the expert from s_exp (after the staging barrier), else from the routing ids (the first unit only)
+    auto unit_of = [&](int u, auto from_lds) {
+        Unit k;
+        k.rt = u % a.RT;
+        int r = u / a.RT;
+        k.split = r % a.S;
+        r /= a.S;
+        k.mat = r % nmat;
+        k.gi = r / nmat;
+        int e;
+        if constexpr (decltype(from_lds)::value) e = s_exp[k.gi];
+        else e = k.gi < a.n_route ? a.idx[k.gi] : a.shared_expert;
+        k.e = __builtin_amdgcn_readfirstlane(e);
+        return k;
+    };
+    using Lds = std::true_type;
+    using Glb = std::false_type;
+    auto segment = [&](const Unit &k, Cb3Wave &w) {
+        const Cb3Table &tb = k.mat ? a.t1 : a.t0;
+        const bool ok = k.e >= 0 && k.e < a.E;
+        const uint32_t *qt = tb.qs + (size_t)(ok ? k.e : 0) * tb.CT * tb.RT * 256;
+        const uint32_t *cbe = tb.cb + (size_t)(ok ? k.e : 0) * tb.G * tb.R * 4;
+        w.qb = __builtin_amdgcn_make_buffer_rsrc((void *)qt, (short)0, ok ? 0x7fffffff : 0, kBufferWord3);
+        w.qnull = __builtin_amdgcn_make_buffer_rsrc((void *)qt, (short)0, 0, kBufferWord3);
+        w.cbb = __builtin_amdgcn_make_buffer_rsrc((void *)cbe, (short)0, ok ? 0x7fffffff : 0, kBufferWord3);
+        w.cbnull = __builtin_amdgcn_make_buffer_rsrc((void *)cbe, (short)0, 0, kBufferWord3);
+        const int nb = (a.nu + a.al - 1) / a.al;
+        w.cta = min(a.nu, a.al * (int)((long long)k.split * nb / a.S));
+        w.ctb = min(a.nu, a.al * (int)((long long)(k.split + 1) * nb / a.S));
+        w.ct_bytes = (uint32_t)tb.RT * 1024u;
+        w.rt_bytes = (uint32_t)(k.rt * RTW) * 1024u;
+        w.g_bytes = (uint32_t)tb.R * 16u;
+        w.row_bytes = (uint32_t)(k.rt * 16 * RTW) * 16u;
+        w.g_first = (kCb3TileCols * w.cta) >> 7;
+        w.g_last = min((kCb3TileCols * w.ctb - 1) >> 7, tb.G - 1);
+        w.lane16 = (uint32_t)lane * 16u;
+        w.cblane16 = (uint32_t)(lane & (16 * RTW - 1)) * 16u;
+        w.cbl = cbl + wave * 5 * 64;
+        // B operand: the staged row (down: hi in columns 0-7, lo in 8-15 of the group's two rows), from the column
+        // of the super tile holding cta
+        const int row = hilo ? 2 * (k.gi - g0) + (jt >= 8 ? 1 : 0) : 0;
+        w.xh = xlds + row * a.xsp + 320 * (w.cta >> 2) + 4 * q;
+        w.xl = w.xh;
+    };
+    // staged rows straight into LDS (64 lanes x 4 bytes per load, spread over the wavefronts), issued ahead of every
+    // wavefront's weight ring: columns past K read zeros
+    auto issue = [&]() {
+        const int xs = (a.nu * kCb3TileCols) >> 1, nch = (xs + 63) >> 6;
+        const __amdgpu_buffer_rsrc_t rh =
+            __builtin_amdgcn_make_buffer_rsrc((void *)a.x, (short)0, 0x7fffffff, kBufferWord3);
+        const __amdgpu_buffer_rsrc_t rl =
+            __builtin_amdgcn_make_buffer_rsrc((void *)(hilo ? a.x_lo : a.x), (short)0, 0x7fffffff, kBufferWord3);
+        for (int i = wave; i < rows * nch; i += kCuWaves) {
+            const int r = i / nch, ch = i - r * nch;
+            const int c = 2 * (64 * ch + lane);
+            const int src_row = hilo ? g0 + (r >> 1) : 0;          // slot of group g0 + r / 2 (one token)
+            const uint32_t voff = c < a.K ? (uint32_t)((size_t)src_row * a.K + c) * 2u : kStageOut;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds((hilo && (r & 1)) ? rl : rh,
+                                                     (__attribute__((address_space(3))) void *)(xlds + r * a.xsp +
+                                                                                                 64 * ch),
+                                                     4, voff, 0, 0, 0);
+        }
+    };
+    // the wavefront's first unit, then claims (an empty unit range ends the wavefront after the staging barrier)
+    int u = u_begin + wave;
+    const bool active = u < u_end;
+    Unit cur = unit_of(active ? u : u_begin, Glb{});
+    Cb3Wave w;
+    segment(cur, w);
+    if (!active) {
+        issue();
+        vm_wait<0>();
+        __syncthreads();
+        return;
+    }
+    cb3_stream<false, RTW>(
+        w,
+        [&](Cb3Wave &nw) {
+            const int nu_ = (int)__builtin_amdgcn_readfirstlane(lane == 0 ? atomicAdd(&s_next, 1u) : 0u);
+            if (nu_ >= u_end) return false;
+            u = nu_;
+            segment(unit_of(u, Lds{}), nw);
+            return true;
+        },
+        [&](f32x4 (&acc)[RTW]) {
+            if (hilo) {
+#pragma unroll
+                for (int r = 0; r < RTW; ++r)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[r][i] += __shfl_down(acc[r][i], 8, 16);
+            }
+            if (jt == 0 && cur.e >= 0 && cur.e < a.E) {
+                float *dst = a.part + ((size_t)(cur.split * nmat + cur.mat) * a.NS + cur.gi) * a.R +
+                             cur.rt * 16 * RTW + 4 * q;
+#pragma unroll
+                for (int r = 0; r < RTW; ++r)
+                    *(float4 *)(dst + 16 * r) = make_float4(acc[r][0], acc[r][1], acc[r][2], acc[r][3]);
+            }
+        },
+        [&](const Cb3Wave &) { cur = unit_of(u, Lds{}); },
+        issue,
+        [&]() {
+            vm_wait<4 * RTW + 5>();                 // the staging loads, issued ahead of the ring
+            __syncthreads();
+        });
+}
+
+}  // namespace mi

@@ -1,5 +1,6 @@
 // Grouped codebook-dequant expert matvec: host side of the C ABI (argument validation, split planning, workspace
 // layout, launches) and the exact dequant kernel.  The grouped kernels themselves live in grouped.h.
+#include "custream.h"
 #include "pstream.h"
 
 #include <stdio.h>
@@ -490,6 +491,12 @@ MI_DECL_PSTREAM(1, 8)
 MI_DECL_PSTREAM(1, 16)
 #undef MI_DECL_PSTREAM
 
+void launch_custream_0(int rtw, dim3 grid, size_t lds, hipStream_t s, const CArgs &a);
+void launch_custream_1(int rtw, dim3 grid, size_t lds, hipStream_t s, const CArgs &a);
+static void custream_launch(int mode, int rtw, dim3 grid, size_t lds, hipStream_t s, const CArgs &a) {
+    (mode == kGateUp ? launch_custream_0 : launch_custream_1)(rtw, grid, lds, s, a);
+}
+
 static int pstream_occupancy(int mode, int tc, int rtw, size_t lds) {
     if (mode == kGateUp) return (tc <= 8 ? occupancy_pstream_0_8 : occupancy_pstream_0_16)(rtw, lds);
     return (tc <= 8 ? occupancy_pstream_1_8 : occupancy_pstream_1_16)(rtw, lds);
@@ -506,6 +513,8 @@ constexpr int kPersistentMinTokens = 8;
 
 struct DecodePlan {
     int G, rows1, rows2, NS;
+    int cu;                     // CB3, one token: the CU-balanced launches (custream.h), one workgroup per CU
+    int cgmax;                  // their down launch: most groups one workgroup's share touches
     int persistent;             // CB3 gate/up and down as persistent launches
     Shape s1, s2;
     int P1, P2;                 // persistent: workgroups of the two launches
@@ -514,6 +523,7 @@ struct DecodePlan {
 };
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+constexpr size_t kLdsPerCu = 160 * 1024;
 
 // A persistent CB3 launch: the grid is what stays resident (the runtime's occupancy for the instance and its LDS),
 // never more workgroups than the largest possible task count.
@@ -541,9 +551,41 @@ static DecodePlan plan_decode(const mi_table *gate, const mi_table *down, int N,
     p.NS = n_route + (shared >= 0 ? N : 0);
     int est = N == 1 ? p.G : (p.G * 6 + 5) / 10;
     if (est < 1) est = 1;
-    p.persistent = gate->qtype == MI_QT_CB3 && down->qtype == MI_QT_CB3 && !xf32 &&
+    p.cu = gate->qtype == MI_QT_CB3 && down->qtype == MI_QT_CB3 && !xf32 && N == 1 &&
+           env_int("MI355MOE_CUSTREAM", 1) != 0;
+    p.persistent = !p.cu && gate->qtype == MI_QT_CB3 && down->qtype == MI_QT_CB3 && !xf32 &&
                    N > env_int("MI355MOE_PERSIST_ABOVE", kPersistentMinTokens);
-    if (p.persistent) {
+    if (p.cu) {
+        // equal shares of (group, matrix, split, row tile) units over one workgroup per CU; splits are whole super
+        // tiles (the staged rows are the full activation, so a split never starts inside a super tile)
+        const int P = cu_count();
+        const int nb1 = (n_units_of(gate) + 3) / 4, nb2 = (n_units_of(down) + 3) / 4;
+        int S1 = env_int("MI355MOE_CS1", 2), S2 = env_int("MI355MOE_CS2", 1);      // measured best at D 6144, I 2048
+        int r1 = env_int("MI355MOE_CS1_RTW", 1), r2 = env_int("MI355MOE_CS2_RTW", 1);
+        S1 = S1 < 1 ? 1 : S1 > nb1 ? nb1 : S1;
+        S2 = S2 < 1 ? 1 : S2 > nb2 ? nb2 : S2;
+        r1 = (r1 == 2 || r1 == 4) ? r1 : 1;
+        r2 = (r2 == 2 || r2 == 4) ? r2 : 1;
+        p.s1 = Shape{Split{S1, 4}, r1, gate->rows / (16 * r1), 0};
+        p.s2 = Shape{Split{S2, 4}, r2, down->rows / (16 * r2), 0};
+        p.P1 = p.P2 = P;
+        const long long per_g2 = (long long)S2 * p.s2.RB;
+        const long long share = ((long long)p.NS * per_g2 + P - 1) / P;     // one group per slot
+        p.cgmax = (int)((share + per_g2 - 1) / per_g2) + 1;
+        if (p.cgmax > p.NS) p.cgmax = p.NS;
+        const size_t cbl = sizeof(uint4) * kCuWaves * 5 * 64;
+        const size_t xsp1 = cb3_row_pitch(n_units_of(gate) * kCb3TileCols / 2);
+        const size_t xsp2 = cb3_row_pitch(n_units_of(down) * kCb3TileCols / 2);
+        const size_t scratch = 4 * (2 * (size_t)gate->n_experts + (size_t)n_route);
+        p.lds1 = sizeof(uint32_t) * xsp1 + cbl;
+        p.lds2 = sizeof(uint32_t) * 2 * (size_t)p.cgmax * xsp2 + cbl;
+        if (p.lds1 < scratch) p.lds1 = scratch;
+        if (p.lds2 < scratch) p.lds2 = scratch;
+        // more than half of a CU's LDS: a second workgroup never fits beside the first, whatever the register count
+        const size_t half = kLdsPerCu / 2 + 1024;
+        if (p.lds1 < half) p.lds1 = half;
+        if (p.lds2 < half) p.lds2 = half;
+    } else if (p.persistent) {
         // persistent launches: tasks are pipelined, so the per-task fixed cost is small
         const long long slots = 3LL * cu_count();
         p.s1 = choose_shape(gate, kGateUp, p.rows1, est, p.rows1, 4, "MI355MOE_S1", 48 * 1024, slots, 4, 2.0);
@@ -592,7 +634,6 @@ void launch_fused(int rtw, dim3 grid, size_t lds, hipStream_t s, const FArgs &a)
 
 // Static LDS of the fused kernel besides the dynamic staging area (group table, codebook slots, slot list, flag).
 constexpr size_t kFusedStaticLds = sizeof(GroupTable) + sizeof(uint4) * kWgWaves * 5 * 64 + sizeof(int) * (kMaxT + 1);
-constexpr size_t kLdsPerCu = 160 * 1024;
 
 struct FusedPlan {
     int ok;                     // the one launch applies (CB3, at most 8 tokens per group)
@@ -792,8 +833,34 @@ static int decode_launch(const DecodePlan &p, const mi_table *gate, const mi_tab
         pa.idx = idx;
         pa.part = a.part;
     }
+    // the CU-balanced single-token launches: one workgroup per CU, equal unit shares
+    CArgs ca{};
+    if (p.cu) {
+        ca.t0 = a.t0.cb3;
+        ca.t1 = a.t1.cb3;
+        ca.R = gate->rows;
+        ca.K = gate->cols;
+        ca.E = a.E;
+        ca.n_route = a.n_route;
+        ca.N = N;
+        ca.k = k;
+        ca.shared_expert = shared_expert;
+        ca.NS = p.NS;
+        ca.S = p.s1.sp.S;
+        ca.al = 4;
+        ca.nu = n_units_of(gate);
+        ca.RT = p.s1.RB;
+        ca.P = p.P1;
+        ca.gmax = 1;
+        ca.xsp = cb3_row_pitch(ca.nu * kCb3TileCols / 2);
+        ca.x = x_bf16;
+        ca.x_lo = nullptr;
+        ca.idx = idx;
+        ca.part = a.part;
+    }
     if (phases & 1) {
-        if (cb3) pstream_launch(kGateUp, tc, p.s1.rtw, dim3(p.P1), p.lds1, s, pa);
+        if (p.cu) custream_launch(kGateUp, p.s1.rtw, dim3(p.P1), p.lds1, s, ca);
+        else if (cb3) pstream_launch(kGateUp, tc, p.s1.rtw, dim3(p.P1), p.lds1, s, pa);
         else launch_grouped<kGateUp>(gate->qtype, a.t_rows, p.s1.rtw, dim3(p.G * p.s1.RBG * p.s1.sp.S), lds1, s, a);
         if ((st = launch_status())) return st;
     }
@@ -806,7 +873,7 @@ static int decode_launch(const DecodePlan &p, const mi_table *gate, const mi_tab
     // (the SwiGLU launch's arithmetic, from the gate/up partials) instead of a SwiGLU launch.  Measured slower (the
     // down staging waits for the split partials: +2.5 us on the down launch at batch 1, +14 us per layer at batch 8),
     // so the SwiGLU launch is the default.
-    const bool fuse_h = !cb3 && env_int("MI355MOE_FUSE_SWIGLU", 0) == 1;
+    const bool fuse_h = !cb3 && !p.cu && env_int("MI355MOE_FUSE_SWIGLU", 0) == 1;
     if (!fuse_h) {
         const size_t n4 = (size_t)p.NS * gate->rows / 4;
         hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n4 + 63) / 64)), dim3(64), 0, s,
@@ -835,7 +902,22 @@ static int decode_launch(const DecodePlan &p, const mi_table *gate, const mi_tab
     b.limit = limit;
     b.part = (float *)(ws + p.off_part2);
     size_t lds2 = sizeof(uint32_t) * 2 * (size_t)b.t_rows * b.xs_max;
-    if (cb3) {
+    if (p.cu) {
+        CArgs cb = ca;
+        cb.t0 = cb.t1 = b.t0.cb3;
+        cb.R = down->rows;
+        cb.K = down->cols;
+        cb.S = p.s2.sp.S;
+        cb.nu = n_units_of(down);
+        cb.RT = p.s2.RB;
+        cb.P = p.P2;
+        cb.gmax = p.cgmax;
+        cb.xsp = cb3_row_pitch(cb.nu * kCb3TileCols / 2);
+        cb.x = h_hi;
+        cb.x_lo = h_lo;
+        cb.part = b.part;
+        custream_launch(kDown, p.s2.rtw, dim3(p.P2), p.lds2, s, cb);
+    } else if (cb3) {
         PArgs pb = pa;
         pb.t0 = b.t0.cb3;
         pb.t1 = b.t0.cb3;
@@ -1018,8 +1100,8 @@ int mi_moe_decode_plan(const mi_table *gate, const mi_table *down, int32_t N, in
     int32_t v[24] = {0};
     {
         const DecodePlan d = plan_decode(gate, down, N, k, shared_expert);
-        const int32_t f[8] = {d.s1.sp.S, d.s1.rtw, d.persistent ? d.P1 : 0, d.s2.sp.S, d.s2.rtw,
-                              d.persistent ? d.P2 : 0, (int32_t)d.lds1, (int32_t)d.lds2};
+        const int32_t f[8] = {d.s1.sp.S, d.s1.rtw, (d.persistent || d.cu) ? d.P1 : 0, d.s2.sp.S, d.s2.rtw,
+                              (d.persistent || d.cu) ? d.P2 : 0, (int32_t)d.lds1, (int32_t)d.lds2};
         for (int i = 0; i < 8; ++i) v[16 + i] = f[i];
     }
     const FusedPlan p = plan_fused(gate, down, N, k, shared_expert);
