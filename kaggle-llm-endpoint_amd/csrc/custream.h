@@ -36,6 +36,12 @@ struct CArgs {
     int xsp;                   // LDS row pitch (dwords) of a staged row
     const uint16_t *x;         // kGateUp: x bf16 [1, K]; kDown: bf16 high part of h [NS, K]
     const uint16_t *x_lo;      // kDown: bf16 remainder of h [NS, K]
+    // kDown: h formed while staging from the gate/up split partials [gu_S][2][NS][K] instead of read from x / x_lo
+    // (the splits summed in order, the clamped SwiGLU, bf16 high part + remainder: the SwiGLU launch's arithmetic);
+    // gu_S <= 2 and gmax * (columns / 4) <= 4 * 768 (the host checks both)
+    const float *gu_part;
+    int gu_S;
+    float limit;
     const int32_t *idx;
     float *part;               // [S][nmat][NS][R]
 };
@@ -121,7 +127,9 @@ __global__ void __launch_bounds__(64 * kCuWaves, 1) custream_kernel(CArgs a) {
     };
     // staged rows straight into LDS (64 lanes x 4 bytes per load, spread over the wavefronts), issued ahead of every
     // wavefront's weight ring: columns past K read zeros
+    const bool form_h = hilo && a.gu_part != nullptr;
     auto issue = [&]() {
+        if (form_h) return;                         // h is formed after the ring is issued (stage)
         const int xs = (a.nu * kCb3TileCols) >> 1, nch = (xs + 63) >> 6;
         const __amdgpu_buffer_rsrc_t rh =
             __builtin_amdgcn_make_buffer_rsrc((void *)a.x, (short)0, 0x7fffffff, kBufferWord3);
@@ -144,8 +152,54 @@ __global__ void __launch_bounds__(64 * kCuWaves, 1) custream_kernel(CArgs a) {
     Unit cur = unit_of(active ? u : u_begin, Glb{});
     Cb3Wave w;
     segment(cur, w);
+    // h rows of the share's groups from the gate/up partials: loads issued after the wavefront's ring, so they return
+    // in the same round trip as its first tiles
+    auto form = [&]() {
+        // every thread's partial loads first (at most kFormIt quads of 4 columns, two splits), then the arithmetic:
+        // one round trip
+        constexpr int kFormIt = 4;
+        const int cols = a.nu * kCb3TileCols, q4 = cols >> 2;
+        const size_t plane = (size_t)a.NS * a.K;
+        float4 pg[kFormIt][2], pu[kFormIt][2];
+#pragma unroll
+        for (int it = 0; it < kFormIt; ++it) {
+            const int i = tid + it * (int)blockDim.x, j = i / q4, c = 4 * (i - j * q4);
+            const bool in = i < ng * q4 && c < a.K;
+            const size_t o = in ? (size_t)(g0 + j) * a.K + c : 0;       // slot g0 + j (one token)
+#pragma unroll
+            for (int sp = 0; sp < 2; ++sp) {
+                const bool ld = in && sp < a.gu_S;
+                pg[it][sp] = ld ? *(const float4 *)(a.gu_part + (size_t)(2 * sp) * plane + o) : make_float4(0.f, 0.f, 0.f, 0.f);
+                pu[it][sp] = ld ? *(const float4 *)(a.gu_part + (size_t)(2 * sp + 1) * plane + o)
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
+#pragma unroll
+        for (int it = 0; it < kFormIt; ++it) {
+            const int i = tid + it * (int)blockDim.x, j = i / q4, c = 4 * (i - j * q4);
+            if (i >= ng * q4) break;
+            uint2 hv = make_uint2(0, 0), lv = make_uint2(0, 0);
+            if (c < a.K) {
+                float4 g = pg[it][0], uu = pu[it][0];
+                if (a.gu_S > 1) {                   // the splits summed in order, as the SwiGLU launch sums them
+                    g.x += pg[it][1].x; g.y += pg[it][1].y; g.z += pg[it][1].z; g.w += pg[it][1].w;
+                    uu.x += pu[it][1].x; uu.y += pu[it][1].y; uu.z += pu[it][1].z; uu.w += pu[it][1].w;
+                }
+                uint32_t h0, l0, h1, l1, h2, l2, h3, l3;
+                split_bf16(swiglu_clamped(g.x, uu.x, a.limit), h0, l0);
+                split_bf16(swiglu_clamped(g.y, uu.y, a.limit), h1, l1);
+                split_bf16(swiglu_clamped(g.z, uu.z, a.limit), h2, l2);
+                split_bf16(swiglu_clamped(g.w, uu.w, a.limit), h3, l3);
+                hv = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
+                lv = make_uint2(l0 | (l1 << 16), l2 | (l3 << 16));
+            }
+            *(uint2 *)(xlds + (2 * j) * a.xsp + (c >> 1)) = hv;
+            *(uint2 *)(xlds + (2 * j + 1) * a.xsp + (c >> 1)) = lv;
+        }
+    };
     if (!active) {
         issue();
+        if (form_h) form();
         vm_wait<0>();
         __syncthreads();
         return;
@@ -177,7 +231,8 @@ __global__ void __launch_bounds__(64 * kCuWaves, 1) custream_kernel(CArgs a) {
         [&](const Cb3Wave &) { cur = unit_of(u, Lds{}); },
         issue,
         [&]() {
-            vm_wait<4 * RTW + 5>();                 // the staging loads, issued ahead of the ring
+            if (form_h) form();
+            else vm_wait<4 * RTW + 5>();            // the staging loads, issued ahead of the ring
             __syncthreads();
         });
 }

@@ -134,22 +134,12 @@ __global__ void __launch_bounds__(64) combine_kernel(const float *__restrict__ p
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int j0 = 0; j0 < nj; j0 += kCombineChunk) {
         int slot[kCombineChunk];
-        float wt[kCombineChunk];
+        // the slot of every column: its partials are loaded together with the routing ids and weights, in one round
+        // trip (in bounds for every slot); a slot whose expert id is outside [0, E) is left out of the sum afterwards
 #pragma unroll
         for (int jj = 0; jj < kCombineChunk; ++jj) {
             const int j = j0 + jj;
-            slot[jj] = -1;
-            wt[jj] = 0.f;
-            if (j < k) {
-                const int e = idx[tok * k + j];
-                if (e >= 0 && e < E) {
-                    slot[jj] = tok * k + j;
-                    wt[jj] = w[tok * k + j];
-                }
-            } else if (j < nj) {
-                slot[jj] = n_route + tok;
-                wt[jj] = 1.0f;
-            }
+            slot[jj] = j < k ? tok * k + j : j < nj ? n_route + tok : -1;
         }
         float4 ys[kCombineChunk];
 #pragma unroll
@@ -167,11 +157,15 @@ __global__ void __launch_bounds__(64) combine_kernel(const float *__restrict__ p
         }
 #pragma unroll
         for (int jj = 0; jj < kCombineChunk; ++jj) {
-            if (slot[jj] < 0) continue;
-            if (j0 + jj < k) {
-                acc.x += wt[jj] * ys[jj].x; acc.y += wt[jj] * ys[jj].y;
-                acc.z += wt[jj] * ys[jj].z; acc.w += wt[jj] * ys[jj].w;
-            } else {
+            const int j = j0 + jj;
+            if (j < k) {
+                const int e = idx[tok * k + j];
+                if (e >= 0 && e < E) {
+                    const float wt = w[tok * k + j];
+                    acc.x += wt * ys[jj].x; acc.y += wt * ys[jj].y;
+                    acc.z += wt * ys[jj].z; acc.w += wt * ys[jj].w;
+                }
+            } else if (j < nj) {
                 acc.x += ys[jj].x; acc.y += ys[jj].y; acc.z += ys[jj].z; acc.w += ys[jj].w;
             }
         }
@@ -874,7 +868,11 @@ static int decode_launch(const DecodePlan &p, const mi_table *gate, const mi_tab
     // down staging waits for the split partials: +2.5 us on the down launch at batch 1, +14 us per layer at batch 8),
     // so the SwiGLU launch is the default.
     const bool fuse_h = !cb3 && !p.cu && env_int("MI355MOE_FUSE_SWIGLU", 0) == 1;
-    if (!fuse_h) {
+    // the CU-balanced down launch forms h itself while staging (bit-identical h, one launch fewer: ~2 us at one token;
+    // MI355MOE_CU_FORM_H=0 keeps the SwiGLU launch, for measurement)
+    const bool cu_form = p.cu && env_int("MI355MOE_CU_FORM_H", 1) != 0 && p.s1.sp.S <= 2 &&
+                         (long long)p.cgmax * (n_units_of(down) * kCb3TileCols / 4) <= 4LL * 64 * kCuWaves;
+    if (!fuse_h && !cu_form) {
         const size_t n4 = (size_t)p.NS * gate->rows / 4;
         hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n4 + 63) / 64)), dim3(64), 0, s,
                            (const float *)(ws + p.off_part1), p.s1.sp.S, p.NS, gate->rows, limit, h_hi, h_lo);
@@ -915,6 +913,9 @@ static int decode_launch(const DecodePlan &p, const mi_table *gate, const mi_tab
         cb.xsp = cb3_row_pitch(cb.nu * kCb3TileCols / 2);
         cb.x = h_hi;
         cb.x_lo = h_lo;
+        cb.gu_part = cu_form ? (const float *)(ws + p.off_part1) : nullptr;
+        cb.gu_S = p.s1.sp.S;
+        cb.limit = limit;
         cb.part = b.part;
         custream_launch(kDown, p.s2.rtw, dim3(p.P2), p.lds2, s, cb);
     } else if (cb3) {
