@@ -13,6 +13,9 @@
  *   moe_route(p, x, cfg)                                   model.py:798-808      -> mi_moe_route
  *   pack_layer_from_gguf / pack_planes                     resident.py:29-60, planes.py:136-170 -> mi_pack_planes
  *   moe_ragged_gateup / moe_ragged_down                    pallas_moe.py:622-755 -> mi_moe_prefill
+ *   moe_sweep_gateup / moe_sweep_down, _apply_sweep_kernel  pallas_moe.py:382-555, resident.py:169-187
+ *                                                                                 -> mi_moe_prefill_form (SWEEP)
+ *   _apply_gather / _apply_sweep_xla (use_pallas=False)    resident.py:122-135,189-210 -> mi_moe_prefill_form
  *   dequant_planes (XLA dequant of the planar tables)      planes.py:196-206     -> mi_dequant
  *   quant8.dequant_tree + x @ W (int8 projections)         quant8.py:91-99       -> mi_int8_project(_many)
  *   Engine._logits_local, int8 lm_head (scale after dot)   engine.py:345-351     -> mi_int8_project (MI_I8_COL_AFTER)
@@ -239,6 +242,36 @@ int mi_moe_prefill(const mi_table *gate, const mi_table *up, const mi_table *dow
                    void *stream);
 size_t mi_moe_prefill_workspace(const mi_table *gate, const mi_table *down, int32_t T, int32_t k,
                                 int32_t shared_expert);
+
+/*
+ * The same grouped GEMMs with the rounding points of the reference's other bf16 branches of ResidentFetch.apply
+ * (combine selects the branch; MI_COMBINE_MATMUL / MI_COMBINE_GATHER are mi_moe_prefill's):
+ *   MI_COMBINE_SWEEP      the dense sweep, sweep_mode="dense" (_apply_sweep_kernel, resident.py:169-187, with
+ *                         moe_sweep_gateup / moe_sweep_down, pallas_moe.py:382-555):
+ *                           rw(t, e) = sum of w[t, j] over the token's columns j with idx[t, j] = e, in column order
+ *                           hk = bf16(f32(bf16(swiglu(g, u))) * rw),  y = Wdown_e hk in f32 (not rounded)
+ *                           out[t] = f32 sum of y over the token's experts
+ *   MI_COMBINE_XLA_GATHER the XLA decode path, use_pallas=False (_apply_gather, resident.py:122-135):
+ *                           g, u rounded to bf16 (the einsums' bf16 outputs), h = bf16(swiglu(g, u)),
+ *                           y = bf16(Wdown_e h), out[t] = sum_j w[t, j] y in f32
+ *   MI_COMBINE_XLA_SWEEP  the XLA prefill path, use_pallas=False (_apply_sweep_xla, resident.py:189-210):
+ *                           g, u rounded to bf16, hk = bf16(f32(bf16(swiglu(g, u))) * rw), y = Wdown_e hk in f32;
+ *                           per group of `chunk` consecutive expert ids, the group's y summed in f32, rounded to
+ *                           bf16 once, added to out[t] in f32 in ascending group order
+ * The shared column (shared_expert >= 0) is one more expert of weight 1 in every form. A token's second column of an
+ * expert it names already gets weight 0 in the sweeps (its weight is in the first column's rw) and adds exactly 0.
+ * chunk > 0 for MI_COMBINE_XLA_SWEEP, ignored otherwise. The sweeps keep y in f32: their workspace
+ * (mi_moe_prefill_form_workspace) is larger than mi_moe_prefill_workspace.
+ */
+#define MI_COMBINE_SWEEP 2
+#define MI_COMBINE_XLA_GATHER 3
+#define MI_COMBINE_XLA_SWEEP 4
+int mi_moe_prefill_form(const mi_table *gate, const mi_table *up, const mi_table *down, const uint16_t *x_bf16,
+                        int32_t T, int32_t k, const int32_t *idx, const float *w, int32_t shared_expert, float limit,
+                        int32_t combine, int32_t chunk, float *out_f32, uint16_t *out_bf16, void *workspace,
+                        size_t workspace_bytes, void *stream);
+size_t mi_moe_prefill_form_workspace(const mi_table *gate, const mi_table *down, int32_t T, int32_t k,
+                                     int32_t shared_expert, int32_t combine);
 
 /*
  * Exact dequantized weights of expert e (natural input order): out f32 [R, K].  Restates dequant_planes

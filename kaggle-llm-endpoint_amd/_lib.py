@@ -24,7 +24,12 @@ MI_I8_COL_SCALES = 1         # s [n_out]: per-column scales [1, out]
 MI_I8_COL_AFTER = 2          # s [n_out] applied after the dot (the int8 lm_head)
 MI_COMBINE_MATMUL = 0
 MI_COMBINE_GATHER = 1
+MI_COMBINE_SWEEP = 2         # the dense sweep's rounding points (sweep_mode="dense")
+MI_COMBINE_XLA_GATHER = 3    # the XLA decode path's (use_pallas=False, N*k <= gather_max_rows)
+MI_COMBINE_XLA_SWEEP = 4     # the XLA prefill path's (use_pallas=False), experts summed in chunks
 COMBINES = {"matmul": MI_COMBINE_MATMUL, "gather": MI_COMBINE_GATHER}
+PREFILL_FORMS = {"matmul": MI_COMBINE_MATMUL, "gather": MI_COMBINE_GATHER, "sweep": MI_COMBINE_SWEEP,
+                 "xla_gather": MI_COMBINE_XLA_GATHER, "xla_sweep": MI_COMBINE_XLA_SWEEP}
 PREFILL_TM = 80              # rows per block of mi_moe_prefill's own plan
 NOALLOC_SCRATCH_BYTES = 64 << 20     # MI_NOALLOC_SCRATCH_BYTES: the static data region of mi_moe_decode_noalloc
 
@@ -36,7 +41,8 @@ PLANE_KEYS = {"CB3": ("qs", "cb"), "IQ3_S": ("qs", "sg", "qh", "sc", "d"), "IQ4_
 # every symbol the header declares (tests check the library exports them)
 EXPORTS = ("mi_matvec", "mi_matvec_workspace", "mi_moe_decode", "mi_moe_decode_fused", "mi_moe_decode_phases",
            "mi_moe_decode_workspace", "mi_moe_decode_plan", "mi_moe_decode_noalloc", "mi_moe_decode_x",
-           "mi_ragged_plan", "mi_moe_prefill", "mi_moe_prefill_workspace", "mi_dequant", "mi_int8_project", "mi_int8_project_workspace", "mi_int8_project_many",
+           "mi_ragged_plan", "mi_moe_prefill", "mi_moe_prefill_workspace", "mi_moe_prefill_form",
+           "mi_moe_prefill_form_workspace", "mi_dequant", "mi_int8_project", "mi_int8_project_workspace", "mi_int8_project_many",
            "mi_int8_project_many_workspace", "mi_moe_route", "mi_moe_route_workspace", "mi_pack_planes", "mi_strerror",
            "mi_version")
 
@@ -84,6 +90,8 @@ def lib():
         "mi_ragged_plan": (I, [P, P, I, I, I, I, P, P, P, P, P, P]),
         "mi_moe_prefill": (I, [T, T, T, P, I, I, P, P, I, F, I, P, P, P, Z, P]),
         "mi_moe_prefill_workspace": (Z, [T, T, I, I, I]),
+        "mi_moe_prefill_form": (I, [T, T, T, P, I, I, P, P, I, F, I, I, P, P, P, Z, P]),
+        "mi_moe_prefill_form_workspace": (Z, [T, T, I, I, I, I]),
         "mi_dequant": (I, [T, I, P, P]),
         "mi_int8_project": (I, [P, I, P, P, I, I, I, P, P, P, Z, P]),
         "mi_int8_project_workspace": (Z, [I, I, I, I]),

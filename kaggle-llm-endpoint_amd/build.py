@@ -3,8 +3,9 @@
     python kaggle-llm-endpoint_amd/build.py
 
 The library is a plain C-ABI shared object (include/mi355moe.h) that the package loads with ctypes.  The grouped
-kernels are compiled once per (mode, format: CB3, IQ3_S, IQ4_XS) from k_grouped.hip, the persistent CB3 kernels once per (mode, token
-class) from k_pstream.hip; all units compile in parallel, then link.
+kernels are compiled once per (mode, format) from k_grouped.hip, the persistent CB3 kernels once per (mode, token
+class) from k_pstream.hip, the CU-balanced ones once per mode from k_custream.hip and the prefill GEMMs once per
+(mode, rounding form) from k_prefill.hip; all units compile in parallel, then link.
 """
 import os
 import shutil
@@ -36,6 +37,9 @@ UNITS += [("k_fused.hip", [], "k_fused")]
 UNITS += [("k_pstream.hip", ["-DMI_PMODE=%d" % m, "-DMI_PTC=%d" % tc], "k_pstream_%d_%d" % (m, tc))
           for m in (0, 1) for tc in (8, 16)]
 UNITS += [("k_custream.hip", ["-DMI_CMODE=%d" % m], "k_custream_%d" % m) for m in (0, 1)]
+# prefill GEMMs per (mode, rounding form): gate/up plain, bf16 g/u, weighted h, both; down bf16 y, f32 y
+UNITS += [("k_prefill.hip", ["-DMI_PF_MODE=%d" % m, "-DMI_PF_FORM=%d" % f], "k_prefill_%d_%d" % (m, f))
+          for m, f in ((0, 0), (0, 1), (0, 2), (0, 3), (1, 0), (1, 4))]
 
 
 def _filter(stderr):

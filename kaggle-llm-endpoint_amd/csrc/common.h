@@ -34,6 +34,9 @@ __device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
     return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
 }
 
+// f rounded to bf16 (nearest even) and widened back to f32.
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16_rne(f)); }
+
 // f32 = hi + lo with hi = bf16(f) (truncated) and lo = bf16(f - hi): hi + lo carries 16 mantissa bits of f.
 __device__ __forceinline__ void split_bf16(float f, uint32_t &hi, uint32_t &lo) {
     uint32_t u = __float_as_uint(f) & 0xffff0000u;

@@ -431,24 +431,34 @@ def moe_route(p, x, cfg):
     return route(x, p["router_w"], p.get("router_bias"), cfg.topk, cfg.norm_topk, cfg.scaling)
 
 
-def prefill_workspace_bytes(gate, down, T, k, shared_expert=-1):
-    n = lib().mi_moe_prefill_workspace(gate.c, down.c, int(T), int(k), int(shared_expert))
+def prefill_workspace_bytes(gate, down, T, k, shared_expert=-1, combine="matmul"):
+    n = lib().mi_moe_prefill_form_workspace(gate.c, down.c, int(T), int(k), int(shared_expert),
+                                            _lib.PREFILL_FORMS[combine])
     if n == 0:
         raise ValueError("mi_moe_prefill: invalid tables or token counts (T=%d, k=%d)" % (T, k))
     return n
 
 
 def moe_prefill(gate, up, down, x, idx, w, limit, shared_expert=-1, combine="matmul", want_f32=True,
-                want_bf16=False, out_f32=None, out_bf16=None, workspace=None):
-    """Grouped prefill MoE (resident.py:144-165 composition) on the matrix cores: slots sorted by expert
-    (ragged_plan), h = bf16(swiglu(x Wg^T, x Wu^T)), y = bf16(h Wd^T), out = sum_j wt * y with wt = bf16(w)
-    (``combine="matmul"``) or w (``"gather"``), f32 accumulation throughout.
-    x bf16 [T, D]; idx int32 [T, k]; w f32 [T, k] -> (out_f32 [T, D] or None, out_bf16 [T, D] or None).
-    Preallocated outputs and ``workspace`` (uint8, prefill_workspace_bytes) make the call allocation-free."""
+                want_bf16=False, out_f32=None, out_bf16=None, workspace=None, chunk=8):
+    """Grouped prefill MoE on the matrix cores, slots sorted by expert (ragged_plan), with the rounding points of
+    one of the reference's bf16 branches:
+      "matmul" / "gather": _apply_ragged_kernel (resident.py:144-165): h = bf16(swiglu(x Wg^T, x Wu^T)),
+          y = bf16(h Wd^T), out = sum_j wt * y with wt = bf16(w) ("matmul") or w ("gather");
+      "sweep": _apply_sweep_kernel (resident.py:169-187): hk = bf16(h * rw) with rw the token's summed weight of
+          the expert, y = hk Wd^T in f32, out = f32 sum over the token's experts;
+      "xla_gather": _apply_gather (resident.py:122-135): g, u rounded to bf16, then as "gather";
+      "xla_sweep": _apply_sweep_xla (resident.py:189-210): g, u rounded to bf16, then as "sweep" except that the
+          experts' y are summed per group of ``chunk`` expert ids, each group rounded to bf16 once.
+    f32 accumulation throughout.  x bf16 [T, D]; idx int32 [T, k]; w f32 [T, k] -> (out_f32 [T, D] or None,
+    out_bf16 [T, D] or None).  Preallocated outputs and ``workspace`` (uint8, prefill_workspace_bytes with the same
+    ``combine``) make the call allocation-free."""
     if x.dtype != torch.bfloat16:
         raise ValueError("prefill activations are bf16")
-    if combine not in _lib.COMBINES:
-        raise ValueError("combine must be 'matmul' or 'gather'")
+    if combine not in _lib.PREFILL_FORMS:
+        raise ValueError("combine must be one of %s" % ", ".join(sorted(_lib.PREFILL_FORMS)))
+    if combine == "xla_sweep" and int(chunk) <= 0:
+        raise ValueError("chunk must be positive")
     T, k = idx.shape
     x = x.contiguous()
     if idx.dtype != torch.int32:
@@ -464,10 +474,11 @@ def moe_prefill(gate, up, down, x, idx, w, limit, shared_expert=-1, combine="mat
         ob = torch.empty((T, D), dtype=torch.bfloat16, device=x.device)
     ws = workspace
     if ws is None:
-        ws = WORKSPACES.get("prefill", prefill_workspace_bytes(gate, down, T, k, shared_expert))
-    check("mi_moe_prefill", lib().mi_moe_prefill(gate.c, up.c, down.c, _ptr(x), T, k, _ptr(idx), _ptr(w),
-                                                 int(shared_expert), float(limit), _lib.COMBINES[combine],
-                                                 _ptr(of), _ptr(ob), _ptr(ws), ws.numel(), _stream()))
+        ws = WORKSPACES.get("prefill", prefill_workspace_bytes(gate, down, T, k, shared_expert, combine))
+    check("mi_moe_prefill_form", lib().mi_moe_prefill_form(gate.c, up.c, down.c, _ptr(x), T, k, _ptr(idx), _ptr(w),
+                                                           int(shared_expert), float(limit),
+                                                           _lib.PREFILL_FORMS[combine], int(chunk), _ptr(of),
+                                                           _ptr(ob), _ptr(ws), ws.numel(), _stream()))
     return of, ob
 
 
@@ -581,11 +592,15 @@ class ResidentFetch:
         (resident.py:110-120), in chunks of <= 16 tokens / 128 slots;
       * N*k > gather_max_rows, use_pallas, sweep_mode "ragged": _apply_ragged_kernel -- the grouped prefill GEMMs with
         the bf16 rounding points and ``combine`` (resident.py:144-165);
+      * N*k > gather_max_rows, use_pallas, sweep_mode "dense": _apply_sweep_kernel -- the grouped GEMMs with the
+        dense sweep's rounding points (hk = bf16(h * rw), y f32; resident.py:169-187);
+      * use_pallas=False: _apply_gather (N*k <= gather_max_rows, resident.py:122-135) and _apply_sweep_xla
+        (resident.py:189-210, experts summed in groups of ``chunk``) -- the grouped GEMMs with those paths' bf16
+        rounding points (g and u rounded to bf16);
       * out_dtype float32, any branch: every value stays f32 (test_resident_cpu.py:81,124), i.e. the decode
         composition in f32, taken by the decode kernels in chunks.
-    The bf16 forms of the dense sweep (sweep_mode "dense", resident.py:169-187) and of the XLA paths
-    (use_pallas=False, resident.py:122-135,189-210) raise NotImplementedError rather than run with other rounding.
-    ``interpret`` and ``chunk`` only matter to those XLA paths."""
+    Every prefill form decodes gate and up with one format (mixed formats raise NotImplementedError).
+    ``interpret`` is accepted and has no effect."""
 
     def __init__(self, qtypes, D, ml, out_dtype=torch.bfloat16, gather_max_rows=64, chunk=8, use_pallas=True,
                  interpret=False, sweep_mode="ragged", tm=32, combine="matmul"):
@@ -633,13 +648,12 @@ class ResidentFetch:
             x = x.to(torch.float32)
         if br == "kernel" or _is_f32(self.out_dtype):
             return decode_chunked(gate, up, down, x, idx, w, limit)
-        if br == "ragged":
-            if gate.qtype != up.qtype:
-                raise NotImplementedError("ResidentFetch.apply: the grouped prefill path takes one format for gate "
-                                          "and up (moe_ragged_gateup decodes both with one qtype)")
-            out, _ = moe_prefill(gate, up, down, x.to(torch.bfloat16), idx, w, limit, combine=self.combine)
-            return out
-        raise NotImplementedError("ResidentFetch.apply: the %s branch with bf16 out_dtype (%s) is not built" %
-                                  (br, {"gather": "use_pallas=False decode, resident.py:122-135",
-                                        "sweep": "sweep_mode='dense', resident.py:169-187",
-                                        "sweep_xla": "use_pallas=False prefill, resident.py:189-210"}[br]))
+        if gate.qtype != up.qtype:
+            raise NotImplementedError("ResidentFetch.apply: the grouped GEMMs take one format for gate and up "
+                                      "(moe_ragged_gateup / moe_sweep_gateup decode both with one qtype)")
+        if br == "sweep_xla" and gate.n_experts % self.chunk:
+            raise ValueError("ResidentFetch: %d experts are not whole chunks of %d (resident.py:192)" %
+                             (gate.n_experts, self.chunk))
+        form = {"ragged": self.combine, "sweep": "sweep", "gather": "xla_gather", "sweep_xla": "xla_sweep"}[br]
+        out, _ = moe_prefill(gate, up, down, x.to(torch.bfloat16), idx, w, limit, combine=form, chunk=self.chunk)
+        return out

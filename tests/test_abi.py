@@ -108,7 +108,15 @@ def test_prefill_host_validation(L, pkg):
     assert call(g, u, d, wsb=16) == 5                                            # MI_ERR_WORKSPACE
     assert L.mi_moe_prefill_workspace(ctypes.byref(g), ctypes.byref(d), 512, 8, 3) > 0
     assert L.mi_moe_prefill_workspace(ctypes.byref(g), ctypes.byref(d), 0, 8, -1) == 0
-    outs = [P(0x60000 + 0x1000 * i) for i in range(5)]
+    form = lambda comb, chunk=8, wsb=1 << 30: L.mi_moe_prefill_form(
+        ctypes.byref(g), ctypes.byref(u), ctypes.byref(d), x, 4, 2, idx, w, -1, ctypes.c_float(10.0), comb, chunk,
+        out, None, ws, wsb, None)
+    assert form(5) == 8 and form(-1) == 8 and form(4, chunk=0) == 8            # unknown form; XLA sweep chunk > 0
+    assert form(2, wsb=16) == 5 and form(4, chunk=3, wsb=16) == 5              # the sweeps pass validation
+    fws = lambda comb: L.mi_moe_prefill_form_workspace(ctypes.byref(g), ctypes.byref(d), 512, 8, 3, comb)
+    assert fws(0) == fws(1) == fws(3) == L.mi_moe_prefill_workspace(ctypes.byref(g), ctypes.byref(d), 512, 8, 3)
+    assert fws(2) == fws(4) > fws(0) and fws(5) == 0                             # the sweeps' y is f32
+    outs =[P(0x60000 + 0x1000 * i) for i in range(5)]
     plan = lambda T=4, k=2, E=8, tm=32, i=idx: L.mi_ragged_plan(i, w, T, k, E, tm, *outs, None)
     assert plan(E=0) == 8 and plan(E=1025) == 8 and plan(tm=0) == 8              # MI_ERR_ARG
     assert plan(T=0) == 4 and plan(T=1 << 21, k=4) == 4                          # MI_ERR_TOKENS

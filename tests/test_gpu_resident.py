@@ -82,16 +82,3 @@ def test_f32_out_dtype_every_branch(pkg, gpu, use_pallas, sweep_mode, gmr):
             "gather": lambda: omoe.gather_apply(L.deq, x, idx, w, limit, out_dtype="f32"),
             "kernel": lambda: omoe.decode_apply(L.deq, x, idx, w, limit)}[br]()
     assert rel_l2(y.cpu().numpy(), want) < F32X
-
-
-@pytest.mark.parametrize("use_pallas,sweep_mode,N", [(False, "ragged", 2), (True, "dense", 40), (False, "dense", 40)])
-def test_bf16_branches_not_built_raise(pkg, gpu, use_pallas, sweep_mode, N):
-    rng = np.random.default_rng(5)
-    E, D, I, k = 4, 256, 256, 2
-    L = Layer(rng, "IQ3_S", E, D, I)
-    fetch = pkg.ResidentFetch({0: {"gate_q": "IQ3_S", "up_q": "IQ3_S", "down_q": "IQ3_S"}}, D, I,
-                              use_pallas=use_pallas, sweep_mode=sweep_mode)
-    idx, w = zipf_routing(rng, N, E, k)
-    x = rng.standard_normal((N, D)).astype(np.float32)
-    with pytest.raises(NotImplementedError):
-        fetch.apply(_params(pkg, L), _t(x, torch.bfloat16), _t(idx), _t(w), 0, 10.0)
