@@ -9,8 +9,11 @@ metric: effective weight GB/s = stored bytes of every distinct expert read in th
         (as % of the 8 TB/s HBM peak), plus microseconds per MoE layer at batch 1 / 8 / 16.
 
 Cache: the layer's weights are rotated over several independent copies (> 256 MB Infinity Cache) and the routing
-changes every step, so each step streams cold weights.  Steps are captured as HIP graphs (one per copy) and replayed;
-the timed region is bracketed by device synchronizations and HIP events on the launch stream.
+changes every step, so each step streams cold weights.  Steps are captured back to back in one HIP graph of
+--steps steps and replayed; each timed replay is bracketed by device synchronizations and HIP events on the launch
+stream, and the headline is the median of --replays timed replays (p10 / p90 under "timing").
+CPU baseline: the oracle's C++ OpenMP restatement of the decode (and its NumPy restatement alongside) on the host's
+cores, on a bounded sample of the same layer.
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20]
 """
@@ -41,9 +44,14 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--copies", type=int, default=6, help="independent layer copies rotated between steps")
+    ap.add_argument("--replays", type=int, default=9, help="timed replays of the headline graphs (median, p10/p90)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only-b1", action="store_true", help="headline only (profiling runs)")
+    ap.add_argument("--only-layout", default=None,
+                    help="decode at batch 1 and 8 of one table layout only, e.g. iq2s_iq4xs (profiling runs)")
     ap.add_argument("--only-prefill", action="store_true", help="the 512-token prefill chunk only (profiling runs)")
+    ap.add_argument("--read-ceiling", action="store_true",
+                    help="only the streaming-read probe (the part's practical HBM read rate)")
     ap.add_argument("--calib", action="store_true",
                     help="end with one plain 256 MiB device copy (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
@@ -118,49 +126,107 @@ class Timer:
                 self.fns[i % len(self.fns)]()
         return g
 
-    def run(self, steps, warmup):
+    def run(self, steps, warmup, replays=1):
+        """ms per step of the `steps`-step graph: the median over `replays` timed replays (each replay exactly
+        `steps` steps, timed on its own between device synchronizations); `self.stats` holds that median and the
+        p10 / p90.  The graph's first replay (its one-time upload to the device) is part of the untimed warmup."""
         torch = self.torch
         timed = self._graph(steps)
         if warmup > 0:
             self._graph(warmup).replay()
+            timed.replay()
         torch.cuda.synchronize()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record()
-        timed.replay()
-        end.record()
-        torch.cuda.synchronize()
-        return start.elapsed_time(end) / steps            # ms per step
+        ms = []
+        for _ in range(max(1, replays)):
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            timed.replay()
+            end.record()
+            torch.cuda.synchronize()
+            ms.append(start.elapsed_time(end) / steps)
+        self.stats = stats(ms)
+        return float(np.median(ms))                       # ms per step
+
+
+def stats(values):
+    """median, p10 and p90 of a list of per-step times (ms), and their count."""
+    v = np.asarray(values, dtype=np.float64)
+    return {"n": int(v.size), "median": round(float(np.median(v)), 5), "p10": round(float(np.percentile(v, 10)), 5),
+            "p90": round(float(np.percentile(v, 90)), 5)}
 
 
 # ------------------------------------------------------------------------------------------------ CPU baseline
+def host_cores():
+    """Host cores this process may use: the affinity set, capped by OMP_NUM_THREADS when that is set."""
+    n = len(os.sched_getaffinity(0))
+    try:
+        n = min(n, int(os.environ.get("OMP_NUM_THREADS", n)))
+    except ValueError:
+        pass
+    return max(1, n)
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _timed_reps(fn, budget_s, min_reps=5, max_reps=50):
+    """Times fn() repeatedly (after one untimed warm-up call) until budget_s is spent, at least min_reps times."""
+    fn()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < min_reps or (time.perf_counter() < t_end and len(times) < max_reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return times
+
+
 def cpu_baseline():
-    """The oracle's NumPy restatement of the reference's plain-jnp decode path (gather -> f32 dequant -> matvec,
-    resident.py:122-135 / pallas_moe.py:310-323) on one batch-1 layer of the same workload, one thread."""
+    """The oracle's restatements of the reference's decode path on one batch-1 layer of the same workload (8 routed +
+    1 shared CB3 experts), timed on this host's cores: (1) the C++ OpenMP leg (oracle/cpu_moe.cpp: CB3 decoded per
+    row, f64 dots, threads over rows) -- `value`; (2) the NumPy leg (oracle.moe.decode_apply: gather -> exact
+    dequant to f32 -> f64 matvec, resident.py:122-135 / pallas_moe.py:310-323) with BLAS on the same cores.  Each
+    leg: one warm-up, then >= 5 timed layers within a few seconds; median and p10 / p90."""
     from threadpoolctl import threadpool_limits
-    from oracle import cb3 as ocb3, moe as omoe
+    from oracle import cb3 as ocb3, cpu_moe, moe as omoe
+    cores = host_cores()
     rng = np.random.default_rng(1)
     experts = 9
-    mats = {}
-    for e in range(experts):
-        for name, (R, K) in (("gate", (INTER, D)), ("up", (INTER, D)), ("down", (D, INTER))):
-            mats[(name, e)] = ocb3.generate(rng, R, K)
+    gen = {}
+    for name, (R, K) in (("gate", (INTER, D)), ("up", (INTER, D)), ("down", (D, INTER))):
+        gen[name] = [ocb3.generate(rng, R, K) for _ in range(experts)]
+    packed = {name: (np.stack([ocb3.pack_canonical(c) for c, _ in g]), np.stack([cb for _, cb in g]))
+              for name, g in gen.items()}
     x = ocb3.bf16_normal(rng, (1, D))
     idx = np.arange(8, dtype=np.int32)[None]
     w = np.full((1, 8), 1.0 / 8, np.float32)
-    deq = lambda name, e: ocb3.dequant(*mats[(name, e)])
-    reps = 3
-    with threadpool_limits(1):
-        t0 = time.perf_counter()
-        for _ in range(reps):
-            y = omoe.decode_apply(deq, x, idx, w, LIMIT) + omoe.shared_apply(lambda m: deq(m, 8), x, LIMIT)
-        dt = time.perf_counter() - t0
-    assert np.isfinite(y).all()
     nbytes = experts * (2 * cb3_bytes(INTER, D) + cb3_bytes(D, INTER))
-    return {"value": round(reps * nbytes / dt / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": "%d batch-1 MoE layers (8 routed + 1 shared CB3 experts, D=6144, I=2048): the oracle's NumPy "
-                      "restatement of the plain-jnp decode path (dequant to f32 + f64 matvec), %.2f s on 1 thread"
-                      % (reps, dt),
-            "us_per_layer": round(dt / reps * 1e6, 1)}
+
+    cpp = lambda: cpu_moe.decode_cb3(packed["gate"], packed["up"], packed["down"], x, idx, w, LIMIT, shared=8,
+                                     threads=cores)
+    t_cpp = _timed_reps(cpp, 8.0)
+    deq = lambda name, e: ocb3.dequant(*gen[name][e])
+    npy = lambda: omoe.decode_apply(deq, x, idx, w, LIMIT) + omoe.shared_apply(lambda m: deq(m, 8), x, LIMIT)
+    with threadpool_limits(cores):
+        t_npy = _timed_reps(npy, 8.0, min_reps=5, max_reps=5)
+    # the two legs compute the same layer
+    assert float(np.max(np.abs(cpp() - npy()))) < 1e-6 * float(np.max(np.abs(npy())))
+    leg = lambda t: {"us_per_layer": round(float(np.median(t)) * 1e6, 1),
+                     "GBps": round(nbytes / float(np.median(t)) / 1e9, 4),
+                     "p10_us": round(float(np.percentile(t, 10)) * 1e6, 1),
+                     "p90_us": round(float(np.percentile(t, 90)) * 1e6, 1), "layers": len(t)}
+    return {"value": round(nbytes / float(np.median(t_cpp)) / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": "batch-1 MoE layers (8 routed + 1 shared CB3 experts, D=6144, I=2048, %.0f MB of weights): "
+                      "the oracle's C++ OpenMP restatement of the decode path on %d threads, median of %d layers "
+                      "(%.1f s); NumPy leg alongside" % (nbytes / 1e6, cores, len(t_cpp), sum(t_cpp)),
+            "cpu_model": cpu_model(), "cpp_openmp": leg(t_cpp), "numpy": leg(t_npy)}
 
 
 def measured_traffic():
@@ -186,6 +252,9 @@ def main():
     import __graft_entry__ as ge
     pkg = ge.load_package()
     pkg._lib.lib()
+    if args.read_ceiling:
+        print(json.dumps({"read_ceiling": bench_read_ceiling(torch, pkg, args)}))
+        return
     torch.manual_seed(0)
     gen = torch.Generator(device="cuda")
     gen.manual_seed(1234)
@@ -247,9 +316,14 @@ def main():
             nbytes.append(n_exp * (pe if phases == 3 else pe_gu))
         return fns, nbytes
 
-    def measure(N, routing, phases=3, steps=args.steps, fused=False, **kw):
+    timing = {}
+
+    def measure(N, routing, phases=3, steps=args.steps, fused=False, replays=1, key=None, **kw):
         fns, nbytes = layer_fns(N, routing, phases, fused, **kw)
-        ms = Timer(torch, fns).run(steps, args.warmup)
+        t = Timer(torch, fns)
+        ms = t.run(steps, args.warmup, replays)
+        if key:
+            timing[key] = t.stats
         avg_bytes = float(np.mean([nbytes[i % L] for i in range(steps)]))
         return ms, avg_bytes
 
@@ -262,13 +336,23 @@ def main():
                           "prefill_t512_iq2s_iq4xs": bench_prefill(torch, pkg, gen, args, iq_layers("iq2s_iq4xs"),
                                                                    rng, iq_pe("iq2s_iq4xs"))}))
         return
+    if args.only_layout:
+        fmt = args.only_layout
+        res = {}
+        for N, routing in ((1, softmax_topk), (8, zipf_topk)):
+            ms, b = measure(N, routing, tables=iq_layers(fmt), pe=iq_pe(fmt))
+            res["b%d_%s" % (N, fmt)] = {"us_per_layer": round(ms * 1e3, 2), "GBps": round(b / (ms * 1e-3) / 1e9, 1)}
+        print(json.dumps(res))
+        if args.calib:
+            calib_copy(torch)
+        return
     # headline: batch 1 layer (mi_moe_decode)
-    ms1, bytes1 = measure(1, softmax_topk)
+    ms1, bytes1 = measure(1, softmax_topk, replays=args.replays, key="b1")
     gbs1 = bytes1 / (ms1 * 1e-3) / 1e9
     extra["b1"] = {"us_per_layer": round(ms1 * 1e3, 2), "GBps": round(gbs1, 1), "pct_hbm": round(100 * gbs1 / HBM_PEAK_GBS, 1),
                    "bytes_per_layer": int(bytes1)}
     # dominant kernel alone (the gate/up launch: gate and up partials)
-    msg, bytesg = measure(1, softmax_topk, phases=1)
+    msg, bytesg = measure(1, softmax_topk, phases=1, replays=args.replays, key="b1_gateup_kernel")
     gbsg = bytesg / (msg * 1e-3) / 1e9
     extra["b1_gateup_kernel"] = {"us": round(msg * 1e3, 2), "GBps": round(gbsg, 1), "bytes": int(bytesg)}
     # the same layer as one persistent launch (mi_moe_decode_fused), for comparison
@@ -293,6 +377,9 @@ def main():
         extra["route"] = bench_route(torch, pkg, gen, args)
         extra["cfg0_matvec"] = bench_matvec(torch, pkg, gen, args)
 
+    kind = pkg.resident.decode_plan(layers[0]["gate"], layers[0]["down"], 1, TOPK, SHARED)["sep_kind"]
+    gateup_kernel = {0: "grouped_kernel<gate/up, CB3>", 1: "pstream_kernel<gate/up>",
+                     2: "custream_kernel<gate/up>"}[kind]
     cpu = None if args.no_cpu else cpu_baseline()
     res = {
         "metric": "effective weight GB/s (% of HBM peak) + µs/MoE layer at batch 1/8/16",
@@ -312,17 +399,49 @@ def main():
                    "layer_copies": L, "parallelism": "single-gpu"},
         "roofline": {"bound": "hbm", "achieved": round(gbsg, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbsg / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                     "kernel": "grouped_kernel<gate/up, CB3> (gate + up partials, batch 1)",
+                     "kernel": gateup_kernel + " (CB3 gate + up partials, batch 1)",
                      "bytes_per_launch": int(bytesg), "us_per_launch": round(msg * 1e3, 2)},
+        "timing": {"what": "ms per step over %d timed replays of the %d-step graph (value and ms_per_step: the "
+                           "median replay)" % (args.replays, args.steps), **timing},
         "cpu_baseline": cpu,
         "extra": extra,
     }
     print(json.dumps(res))
     if args.calib:
-        a = torch.empty(64 * 1024 * 1024, dtype=torch.float32, device="cuda")      # 256 MiB
-        b = torch.empty_like(a)
-        b.copy_(a)
-        torch.cuda.synchronize()
+        calib_copy(torch)
+
+
+def calib_copy(torch):
+    """One plain 256 MiB device-to-device copy: a dispatch of known bytes that calibrates FETCH_SIZE / WRITE_SIZE."""
+    a = torch.empty(64 * 1024 * 1024, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    b.copy_(a)
+    torch.cuda.synchronize()
+
+
+def bench_read_ceiling(torch, pkg, args, launches=40):
+    """The part's practical streaming-read rate (mi_read_probe): four regions of one size rotated between launches
+    (three other regions, > the 256 MB last-level cache, are read between two reads of one region), `launches`
+    launches captured in one graph and timed with events; sizes: one gate/up launch of the headline layer
+    (118,996,992 B) and twice that; 1024 .. 16384 workgroups of 256 threads.  GB/s per configuration."""
+    R, P = pkg.resident, pkg._lib
+    res = {}
+    for size in (118996992, 2 * 118996992):
+        regions = [torch.full((size,), i + 1, dtype=torch.uint8, device="cuda") for i in range(4)]
+        sink = torch.empty(16384 * 4, dtype=torch.int32, device="cuda")
+        for wg in (1024, 2048, 4096, 8192, 16384):
+            fns = [lambda r=r, wg=wg: P.check("mi_read_probe", P.lib().mi_read_probe(R._ptr(r), size, R._ptr(sink), wg,
+                                                                                  R._stream()))
+                   for r in regions]
+            t = Timer(torch, fns)
+            t.run(launches, 4, replays=5)
+            ms = t.stats["median"]
+            res["%dMB_wg%d" % (size // 1000000, wg)] = {"GBps": round(size / (ms * 1e-3) / 1e9, 1),
+                                                        "us": round(ms * 1e3, 2)}
+        del regions
+        torch.cuda.empty_cache()
+    best = max(v["GBps"] for v in res.values())
+    return {"best_GBps": best, "pct_hbm": round(100 * best / HBM_PEAK_GBS, 1), "configs": res}
 
 
 def bench_prefill(torch, pkg, gen, args, layers, rng, per_expert, T=512):

@@ -171,6 +171,8 @@ int mi_moe_decode_noalloc(const mi_table *gate, const mi_table *up, const mi_tab
  *   [15] bytes of the counter block at the start of the workspace (zero between calls);
  *   [16..23] mi_moe_decode's launches: gate/up splits, row tiles per wavefront, workgroups (0: one per task), down
  *   splits, row tiles per wavefront, workgroups (0: one per task), gate/up and down dynamic LDS bytes (persistent).
+ *   [24] mi_moe_decode's gate/up and down kernels: 0 grouped (one workgroup per task), 1 persistent streams,
+ *   2 CU-balanced streams (one workgroup per CU, CB3 at one token).
  * Returns MI_OK or MI_ERR_ARG.
  */
 int mi_moe_decode_plan(const mi_table *gate, const mi_table *down, int32_t N, int32_t k, int32_t shared_expert,
@@ -316,6 +318,13 @@ int mi_int8_project_many(const uint16_t *x_bf16, int32_t B, int32_t n_in, const 
                          int32_t scale_axis, void *workspace, size_t workspace_bytes, void *stream);
 size_t mi_int8_project_many_workspace(int32_t B, int32_t n_in, const int32_t *n_out, int32_t n_proj,
                                       int32_t scale_axis);
+
+/*
+ * Streaming-read probe (measurement only; no counterpart in the reference): reads `bytes` (a multiple of 16) from
+ * src with 16-byte loads in a grid-stride loop of `workgroups` 256-thread workgroups and writes one XOR word per
+ * wavefront to sink (workgroups * 4 u32).  The benchmark times it to give the part's practical read rate.
+ */
+int mi_read_probe(const void *src, size_t bytes, uint32_t *sink, int32_t workgroups, void *stream);
 
 const char *mi_strerror(int status);
 int mi_version(void);

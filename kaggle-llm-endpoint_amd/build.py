@@ -30,7 +30,7 @@ FLAGS = [
 # (source, extra defines, object name)
 UNITS = [("moe_decode.hip", [], "moe_decode"), ("int8_project.hip", [], "int8_project"),
          ("prefill.hip", [], "prefill"), ("route.hip", [], "route"),
-         ("pack.hip", [], "pack")]
+         ("pack.hip", [], "pack"), ("probe.hip", [], "probe")]
 UNITS += [("k_grouped.hip", ["-DMI_KMODE=%d" % m, "-DMI_KQT=%d" % q], "k_grouped_%d_%d" % (m, q))
           for m in (0, 1, 2) for q in (1, 2, 3, 4, 5, 6)]
 UNITS += [("k_fused.hip", [], "k_fused")]

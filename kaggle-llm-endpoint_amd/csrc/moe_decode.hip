@@ -1098,12 +1098,13 @@ int mi_moe_decode_plan(const mi_table *gate, const mi_table *down, int32_t N, in
     if (validate_table(gate) || validate_table(down) || !info || N <= 0 || N > kMaxT || k <= 0 ||
         N * k > MI_MAX_SLOTS)
         return MI_ERR_ARG;
-    int32_t v[24] = {0};
+    int32_t v[25] = {0};
     {
         const DecodePlan d = plan_decode(gate, down, N, k, shared_expert);
         const int32_t f[8] = {d.s1.sp.S, d.s1.rtw, (d.persistent || d.cu) ? d.P1 : 0, d.s2.sp.S, d.s2.rtw,
                               (d.persistent || d.cu) ? d.P2 : 0, (int32_t)d.lds1, (int32_t)d.lds2};
         for (int i = 0; i < 8; ++i) v[16 + i] = f[i];
+        v[24] = d.cu ? 2 : d.persistent ? 1 : 0;
     }
     const FusedPlan p = plan_fused(gate, down, N, k, shared_expert);
     if (p.ok) {
@@ -1113,7 +1114,7 @@ int mi_moe_decode_plan(const mi_table *gate, const mi_table *down, int32_t N, in
     }
     v[14] = (int32_t)ctr_layout(gate, down).err;
     v[15] = (int32_t)ctr_layout(gate, down).bytes;
-    for (int i = 0; i < n_info && i < 24; ++i) info[i] = v[i];
+    for (int i = 0; i < n_info && i < 25; ++i) info[i] = v[i];
     return MI_OK;
 }
 
