@@ -50,6 +50,7 @@ def parse():
     ap.add_argument("--only-layout", default=None,
                     help="decode at batch 1 and 8 of one table layout only, e.g. iq2s_iq4xs (profiling runs)")
     ap.add_argument("--only-prefill", action="store_true", help="the 512-token prefill chunk only (profiling runs)")
+    ap.add_argument("--only-int8", action="store_true", help="the int8 projections and shared MLP only")
     ap.add_argument("--read-ceiling", action="store_true",
                     help="only the streaming-read probe (the part's practical HBM read rate)")
     ap.add_argument("--calib", action="store_true",
@@ -254,6 +255,9 @@ def main():
     pkg._lib.lib()
     if args.read_ceiling:
         print(json.dumps({"read_ceiling": bench_read_ceiling(torch, pkg, args)}))
+        return
+    if args.only_int8:
+        print(json.dumps({"int8_b8": bench_int8(torch, pkg, torch.Generator(device="cuda"), args)}))
         return
     torch.manual_seed(0)
     gen = torch.Generator(device="cuda")
@@ -488,16 +492,18 @@ def bench_route(torch, pkg, gen, args):
 
 
 def bench_int8(torch, pkg, gen, args):
-    """Config: the int8 dense projections at batch 8 (Q, K, V, O 6144x6144; shared gate/up 6144->2048; shared down
-    2048->6144), per-output-channel scales, bf16 activations.  A step is the layer's four dependent stages -- Q/K/V of
-    the attention input in one launch, O, the shared expert's gate and up in one launch, its down -- so projections
-    that share their input share a launch, as they can in the model.  3 weight copies rotated (> the last-level
-    cache)."""
-    stages = [[(6144, 6144)] * 3, [(6144, 6144)], [(6144, 2048)] * 2, [(2048, 6144)]]
-    B = 8
+    """Config: the int8 dense projections at batch 8 (Q, K, V, O 6144x6144; the shared expert's MLP 6144 -> 2048 ->
+    6144), per-output-channel scales (the shared down: per-input-row, its row-parallel form), bf16 activations.  A
+    step is the layer's three dependent stages -- Q/K/V of the attention input in one launch, O, and the shared
+    expert's mlp_partial (mi_int8_mlp: gate and up in one launch, SwiGLU, down) -- so projections that share their
+    input share a launch, as they can in the model.  3 weight copies rotated (> the last-level cache)."""
+    stages = [[(6144, 6144)] * 3, [(6144, 6144)]]
+    B, D, I = 8, 6144, 2048
     copies = 3
     fns = []
-    total = sum(i * o + 4 * o for st in stages for i, o in st)
+    total = sum(i * o + 4 * o for st in stages for i, o in st) + 3 * D * I + 4 * (2 * I + I)
+    mk_q = lambda n_out, n_in: torch.randint(-127, 128, (n_out, n_in), dtype=torch.int8, device="cuda", generator=gen)
+    mk_s = lambda n: torch.rand((n,), device="cuda", generator=gen) * 1.5e-3 + 0.5e-3
     for c in range(copies):
         ops = []
         for st in stages:
@@ -505,20 +511,23 @@ def bench_int8(torch, pkg, gen, args):
             x = torch.randn((B, n_in), device="cuda", generator=gen).to(torch.bfloat16)
             projs, outs = [], []
             for (_, n_out) in st:
-                qT = torch.randint(-127, 128, (n_out, n_in), dtype=torch.int8, device="cuda", generator=gen)
-                s = torch.rand((n_out,), device="cuda", generator=gen) * 1.5e-3 + 0.5e-3
-                projs.append((qT, s))
+                projs.append((mk_q(n_out, n_in), mk_s(n_out)))
                 outs.append((torch.empty((B, n_out), dtype=torch.bfloat16, device="cuda"), None))
             n_outs = (ctypes.c_int32 * len(st))(*[o for _, o in st])
             ws = torch.zeros(max(256, pkg._lib.lib().mi_int8_project_many_workspace(B, n_in, n_outs, len(st), 1)),
                              dtype=torch.uint8, device="cuda")
             ops.append((x, projs, outs, ws))
-        fns.append(lambda ops=ops: [pkg.int8_project_many(x, projs, outputs=outs, workspace=ws)
-                                    for (x, projs, outs, ws) in ops])
+        x = torch.randn((B, D), device="cuda", generator=gen).to(torch.bfloat16)
+        mlp = ((mk_q(I, D), mk_s(I), 1), (mk_q(I, D), mk_s(I), 1), (mk_q(D, I), mk_s(I), 0))
+        y = torch.empty((B, D), dtype=torch.bfloat16, device="cuda")
+        wsm = torch.zeros(pkg._lib.lib().mi_int8_mlp_workspace(B, D, I, 1, 0), dtype=torch.uint8, device="cuda")
+        fns.append(lambda ops=ops, x=x, mlp=mlp, y=y, wsm=wsm: (
+            [pkg.int8_project_many(xx, projs, outputs=outs, workspace=ws) for (xx, projs, outs, ws) in ops],
+            pkg.int8_mlp(x, *mlp, LIMIT, y_bf16=y, workspace=wsm)))
     ms = Timer(torch, fns).run(args.steps, args.warmup)
     gbs = total / (ms * 1e-3) / 1e9
-    return {"us_per_7_projections": round(ms * 1e3, 2), "GBps": round(gbs, 1), "pct_hbm": round(100 * gbs / HBM_PEAK_GBS, 1),
-            "bytes": int(total), "launches": "Q+K+V | O | gate+up | down"}
+    return {"us_per_layer_int8": round(ms * 1e3, 2), "GBps": round(gbs, 1), "pct_hbm": round(100 * gbs / HBM_PEAK_GBS, 1),
+            "bytes": int(total), "launches": "Q+K+V | O | shared MLP: gate+up, SwiGLU, down"}
 
 
 def bench_matvec(torch, pkg, gen, args):

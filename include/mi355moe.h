@@ -19,6 +19,7 @@
  *   dequant_planes (XLA dequant of the planar tables)      planes.py:196-206     -> mi_dequant
  *   quant8.dequant_tree + x @ W (int8 projections)         quant8.py:91-99       -> mi_int8_project(_many)
  *   Engine._logits_local, int8 lm_head (scale after dot)   engine.py:345-351     -> mi_int8_project (MI_I8_COL_AFTER)
+ *   mlp_partial over int8 leaves (shared expert, dense MLP) model.py:125-127,855  -> mi_int8_mlp
  */
 #ifndef MI355MOE_H
 #define MI355MOE_H
@@ -318,6 +319,23 @@ int mi_int8_project_many(const uint16_t *x_bf16, int32_t B, int32_t n_in, const 
                          int32_t scale_axis, void *workspace, size_t workspace_bytes, void *stream);
 size_t mi_int8_project_many_workspace(int32_t B, int32_t n_in, const int32_t *n_out, int32_t n_proj,
                                       int32_t scale_axis);
+
+/*
+ * int8 MLP (mlp_partial, model.py:125-127, over quant8.dequant_tree's bf16(f32(q) * s) weights, quant8.py:91-99):
+ * the shared expert of the MoE block (moe_dense, model.py:855) and the dense MLP layers.
+ *   g = bf16(x Wg), u = bf16(x Wu)                  (bf16 matmuls with f32 accumulation)
+ *   h = bf16(silu(min(g, L)) * clip(u, -L, L))      (swiglu_clamped, model.py:119-122, evaluated in f32 once)
+ *   y = h Wd in f32; y_bf16 = bf16(y)               (the reference's output is the bf16 one)
+ * x bf16 [B, D]; gate/up qT int8 [I, D] with s per gu_scale_axis ([I] MI_I8_COL_SCALES or [D] MI_I8_ROW_SCALES);
+ * down qT int8 [D, I] with s per down_scale_axis ([D] or [I]).  1 <= B <= 32, D % 256 == 0, I % 256 == 0.  Three
+ * launches (gate and up together, SwiGLU, down) or four (down split).  Workspace: mi_int8_mlp_workspace bytes,
+ * 256-byte aligned; no initialisation.
+ */
+int mi_int8_mlp(const uint16_t *x_bf16, int32_t B, int32_t D, int32_t I, const int8_t *gate_qT, const float *gate_s,
+                const int8_t *up_qT, const float *up_s, int32_t gu_scale_axis, const int8_t *down_qT,
+                const float *down_s, int32_t down_scale_axis, float limit, uint16_t *y_bf16, float *y_f32,
+                void *workspace, size_t workspace_bytes, void *stream);
+size_t mi_int8_mlp_workspace(int32_t B, int32_t D, int32_t I, int32_t gu_scale_axis, int32_t down_scale_axis);
 
 /*
  * Streaming-read probe (measurement only; no counterpart in the reference): reads `bytes` (a multiple of 16) from

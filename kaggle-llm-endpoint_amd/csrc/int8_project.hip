@@ -41,6 +41,9 @@ struct I8Args {
     int n_proj;
     int wg_start[kI8MaxProj + 1];   // first workgroup of each projection
     I8Proj p[kI8MaxProj];
+    int pair;              // 1: projections 0 and 1 are gate and up of an MLP: partials always (swiglu_pair_i8)
+    float limit;           // pair: the SwiGLU clamp
+    uint16_t *h;           // pair: h [B, n_out of projection 0] bf16
 };
 
 constexpr int kI8Waves = 4;
@@ -171,7 +174,7 @@ __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
     for (int t = 0; t < TT; ++t) {
         const int b = 16 * t + i;
         if (b >= a.B) continue;
-        if (a.S == 1) {
+        if (a.S == 1 && !a.pair) {
             if (P.y_f32) *(float4 *)(P.y_f32 + (size_t)b * P.n_out + o) = make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
             if (P.y_bf16) {
                 uint2 v;
@@ -219,6 +222,38 @@ __global__ void __launch_bounds__(256) split_reduce_i8(I8Args a) {
     }
 }
 
+// h[b, o] = bf16(swiglu_clamped(bf16(g), bf16(u))) with g, u the split sums (in split order) of projections 0 and 1:
+// mlp_partial's x @ gate and x @ up in bf16, then the clamped SwiGLU in bf16 (model.py:119-127).  One thread per 4
+// outputs.
+__global__ void __launch_bounds__(256) swiglu_pair_i8(I8Args a) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    const int no = a.p[0].n_out, n = a.B * no;
+    if (i >= n / 4) return;
+    float4 g = make_float4(0.f, 0.f, 0.f, 0.f), u = g;
+    for (int s0 = 0; s0 < a.S; s0 += 4) {            // 8 independent loads in flight, summed in split order
+        float4 pg[4], pu[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const bool in = s0 + j < a.S;
+            pg[j] = in ? ((const float4 *)(a.p[0].part + (size_t)(s0 + j) * n))[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            pu[j] = in ? ((const float4 *)(a.p[1].part + (size_t)(s0 + j) * n))[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            g.x += pg[j].x; g.y += pg[j].y; g.z += pg[j].z; g.w += pg[j].w;
+            u.x += pu[j].x; u.y += pu[j].y; u.z += pu[j].z; u.w += pu[j].w;
+        }
+    }
+    const float h0 = swiglu_clamped(round_bf16(g.x), round_bf16(u.x), a.limit);
+    const float h1 = swiglu_clamped(round_bf16(g.y), round_bf16(u.y), a.limit);
+    const float h2 = swiglu_clamped(round_bf16(g.z), round_bf16(u.z), a.limit);
+    const float h3 = swiglu_clamped(round_bf16(g.w), round_bf16(u.w), a.limit);
+    uint2 b;
+    b.x = f32_to_bf16_rne(h0) | (f32_to_bf16_rne(h1) << 16);
+    b.y = f32_to_bf16_rne(h2) | (f32_to_bf16_rne(h3) << 16);
+    ((uint2 *)a.h)[i] = b;
+}
+
 // LDS bytes per staged column: B bf16 activations (+ one f32 scale with per-input-row scales).
 static size_t i8_col_bytes(int B, int scale_axis) { return 2 * (size_t)B + (scale_axis == MI_I8_ROW_SCALES ? 4 : 0); }
 
@@ -248,42 +283,44 @@ static int i8_tiles(const int32_t *n_out, int n_proj) {
     return t;
 }
 
+// Workspace bytes of one launch: the f32 split partials (none with one split, except for an MLP's gate/up pair,
+// whose SwiGLU reads them).
+static size_t i8_part_bytes(int B, int n_in, const int32_t *n_out, int n_proj, int scale_axis, int pair) {
+    size_t total = 0;
+    for (int j = 0; j < n_proj; ++j) total += (size_t)n_out[j];
+    const int S = i8_splits(B, n_in, i8_tiles(n_out, n_proj), scale_axis);
+    return S == 1 && !pair ? 256 : sizeof(float) * (size_t)S * B * total;
+}
+
+static size_t al256_i8(size_t v) { return (v + 255) & ~(size_t)255; }
+
 }  // namespace mi
 
 using namespace mi;
 
-extern "C" {
-
-size_t mi_int8_project_many_workspace(int32_t B, int32_t n_in, const int32_t *n_out, int32_t n_proj,
-                                      int32_t scale_axis) {
-    if (B <= 0 || B > 32 || n_in <= 0 || n_in % 256 || !n_out || n_proj <= 0 || n_proj > kI8MaxProj) return 0;
-    if (scale_axis < MI_I8_ROW_SCALES || scale_axis > MI_I8_COL_AFTER) return 0;
-    size_t total = 0;
-    for (int j = 0; j < n_proj; ++j) {
-        if (n_out[j] <= 0 || n_out[j] % 16) return 0;
-        total += (size_t)n_out[j];
-    }
-    const int S = i8_splits(B, n_in, i8_tiles(n_out, n_proj), scale_axis);
-    return S == 1 ? 256 : sizeof(float) * (size_t)S * B * total;
-}
-
-int mi_int8_project_many(const uint16_t *x_bf16, int32_t B, int32_t n_in, const mi_i8_proj *projs, int32_t n_proj,
-                         int32_t scale_axis, void *workspace, size_t workspace_bytes, void *stream) {
+// One launch of the projections of `projs` over x (+ the split reduction, or with `pair` the SwiGLU of gate and
+// up into h).
+static int i8_launch(const uint16_t *x_bf16, int32_t B, int32_t n_in, const mi_i8_proj *projs, int32_t n_proj,
+                     int32_t scale_axis, void *workspace, size_t workspace_bytes, void *stream, int pair, float limit,
+                     uint16_t *h) {
     if (!x_bf16 || !projs) return MI_ERR_NULL;
     if (B <= 0 || B > 32) return MI_ERR_TOKENS;
-    if (n_proj <= 0 || n_proj > kI8MaxProj) return MI_ERR_ARG;
+    if (n_proj <= 0 || n_proj > kI8MaxProj || (pair && n_proj != 2)) return MI_ERR_ARG;
     if (scale_axis < MI_I8_ROW_SCALES || scale_axis > MI_I8_COL_AFTER) return MI_ERR_ARG;
     if (n_in <= 0 || n_in % 256) return MI_ERR_SHAPE;
     int32_t n_out[kI8MaxProj];
     for (int j = 0; j < n_proj; ++j) {
         const mi_i8_proj &p = projs[j];
-        if (!p.qT || !p.s || (!p.y_bf16 && !p.y_f32)) return MI_ERR_NULL;
+        if (!p.qT || !p.s || (!pair && !p.y_bf16 && !p.y_f32)) return MI_ERR_NULL;
         if (p.n_out <= 0 || p.n_out % 16) return MI_ERR_SHAPE;
         n_out[j] = p.n_out;
     }
-    const size_t need = mi_int8_project_many_workspace(B, n_in, n_out, n_proj, scale_axis);
+    const size_t need = i8_part_bytes(B, n_in, n_out, n_proj, scale_axis, pair);
     if (!workspace || workspace_bytes < need) return MI_ERR_WORKSPACE;
     I8Args a{};
+    a.pair = pair;
+    a.limit = limit;
+    a.h = h;
     a.x = x_bf16;
     a.B = B;
     a.n_in = n_in;
@@ -313,11 +350,35 @@ int mi_int8_project_many(const uint16_t *x_bf16, int32_t B, int32_t n_in, const 
                                     {int8_project_kernel<2, 0>, int8_project_kernel<2, 1>, int8_project_kernel<2, 2>}};
     hipLaunchKernelGGL(kern[B <= 16 ? 0 : 1][scale_axis], dim3(wg), dim3(64 * kI8Waves), lds, st, a);
     if (hipGetLastError() != hipSuccess) return MI_ERR_LAUNCH;
+    if (pair) {
+        const int n4 = B * a.p[0].n_out / 4;
+        hipLaunchKernelGGL(swiglu_pair_i8, dim3((n4 + 255) / 256), dim3(256), 0, st, a);
+        return hipGetLastError() == hipSuccess ? MI_OK : MI_ERR_LAUNCH;
+    }
     if (a.S == 1) return MI_OK;
     int n4 = 0;
     for (int j = 0; j < n_proj; ++j) n4 += B * a.p[j].n_out / 4;
     hipLaunchKernelGGL(split_reduce_i8, dim3((n4 + 255) / 256), dim3(256), 0, st, a);
     return hipGetLastError() == hipSuccess ? MI_OK : MI_ERR_LAUNCH;
+}
+
+
+
+extern "C" {
+
+size_t mi_int8_project_many_workspace(int32_t B, int32_t n_in, const int32_t *n_out, int32_t n_proj,
+                                      int32_t scale_axis) {
+    if (B <= 0 || B > 32 || n_in <= 0 || n_in % 256 || !n_out || n_proj <= 0 || n_proj > kI8MaxProj) return 0;
+    if (scale_axis < MI_I8_ROW_SCALES || scale_axis > MI_I8_COL_AFTER) return 0;
+    for (int j = 0; j < n_proj; ++j)
+        if (n_out[j] <= 0 || n_out[j] % 16) return 0;
+    return i8_part_bytes(B, n_in, n_out, n_proj, scale_axis, 0);
+}
+
+int mi_int8_project_many(const uint16_t *x_bf16, int32_t B, int32_t n_in, const mi_i8_proj *projs, int32_t n_proj,
+                         int32_t scale_axis, void *workspace, size_t workspace_bytes, void *stream) {
+    return i8_launch(x_bf16, B, n_in, projs, n_proj, scale_axis, workspace, workspace_bytes, stream, 0, 0.0f,
+                     nullptr);
 }
 
 size_t mi_int8_project_workspace(int32_t B, int32_t n_in, int32_t n_out, int32_t scale_axis) {
@@ -332,6 +393,38 @@ int mi_int8_project(const uint16_t *x_bf16, int32_t B, const int8_t *qT, const f
     if (n_in <= 0 || n_out <= 0 || n_in % 256 || n_out % 16) return MI_ERR_SHAPE;
     const mi_i8_proj p{qT, s, n_out, y_bf16, y_f32};
     return mi_int8_project_many(x_bf16, B, n_in, &p, 1, scale_axis, workspace, workspace_bytes, stream);
+}
+
+size_t mi_int8_mlp_workspace(int32_t B, int32_t D, int32_t I, int32_t gu_scale_axis, int32_t down_scale_axis) {
+    if (B <= 0 || B > 32 || D <= 0 || I <= 0 || D % 256 || I % 256) return 0;
+    if (gu_scale_axis != MI_I8_ROW_SCALES && gu_scale_axis != MI_I8_COL_SCALES) return 0;
+    if (down_scale_axis != MI_I8_ROW_SCALES && down_scale_axis != MI_I8_COL_SCALES) return 0;
+    const int32_t gu[2] = {I, I};
+    return al256_i8(i8_part_bytes(B, D, gu, 2, gu_scale_axis, 1)) + al256_i8(2 * (size_t)B * I) +
+           mi_int8_project_workspace(B, I, D, down_scale_axis);
+}
+
+int mi_int8_mlp(const uint16_t *x_bf16, int32_t B, int32_t D, int32_t I, const int8_t *gate_qT, const float *gate_s,
+                const int8_t *up_qT, const float *up_s, int32_t gu_scale_axis, const int8_t *down_qT,
+                const float *down_s, int32_t down_scale_axis, float limit, uint16_t *y_bf16, float *y_f32,
+                void *workspace, size_t workspace_bytes, void *stream) {
+    if (!x_bf16 || !gate_qT || !gate_s || !up_qT || !up_s || !down_qT || !down_s || (!y_bf16 && !y_f32))
+        return MI_ERR_NULL;
+    if (B <= 0 || B > 32) return MI_ERR_TOKENS;
+    if (D <= 0 || I <= 0 || D % 256 || I % 256) return MI_ERR_SHAPE;
+    if (!(limit > 0.0f)) return MI_ERR_ARG;
+    const size_t need = mi_int8_mlp_workspace(B, D, I, gu_scale_axis, down_scale_axis);
+    if (need == 0) return MI_ERR_ARG;
+    if (!workspace || workspace_bytes < need || (uintptr_t)workspace % 256) return MI_ERR_WORKSPACE;
+    const int32_t gu[2] = {I, I};
+    const size_t part = al256_i8(i8_part_bytes(B, D, gu, 2, gu_scale_axis, 1));
+    uint16_t *h = (uint16_t *)((char *)workspace + part);
+    char *ws_down = (char *)workspace + part + al256_i8(2 * (size_t)B * I);
+    const mi_i8_proj p[2] = {{gate_qT, gate_s, I, nullptr, nullptr}, {up_qT, up_s, I, nullptr, nullptr}};
+    int st = i8_launch(x_bf16, B, D, p, 2, gu_scale_axis, workspace, part, stream, 1, limit, h);
+    if (st) return st;
+    return mi_int8_project(h, B, down_qT, down_s, down_scale_axis, I, D, y_bf16, y_f32, ws_down,
+                           workspace_bytes - (size_t)(ws_down - (char *)workspace), stream);
 }
 
 }  // extern "C"

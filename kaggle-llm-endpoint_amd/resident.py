@@ -559,6 +559,41 @@ def int8_project_many(x, projections, want_f32=False, outputs=None, workspace=No
     return outs
 
 
+def int8_mlp(x, gate, up, down, limit, want_f32=False, y_bf16=None, y_f32=None, workspace=None):
+    """mlp_partial over int8 leaves (model.py:125-127 with quant8.py:91-99): y = bf16(h @ Wd) with
+    h = bf16(swiglu_clamped(bf16(x @ Wg), bf16(x @ Wu))), W = bf16(f32(q) * s).  x bf16 [B, D]; gate, up, down:
+    reference leaves {"q", "s"} or int8_leaf triples (qT, s, scale_axis); gate and up share one scale form.
+    -> y bf16 [B, D] (and y f32, the down projection before its rounding, with want_f32).  Tokens go 32 per call
+    (mi_int8_mlp's limit); preallocated outputs / workspace make each call allocation-free."""
+    g, u, d = [int8_leaf(l, x.device) if isinstance(l, dict) else l for l in (gate, up, down)]
+    if g[2] != u[2]:
+        raise ValueError("int8_mlp: gate and up take one scale form")
+    B, D = x.shape
+    I = g[0].shape[0]
+    x = x.contiguous()
+    yb = y_bf16 if y_bf16 is not None else torch.empty((B, D), dtype=torch.bfloat16, device=x.device)
+    yf = y_f32 if y_f32 is not None else (
+        torch.empty((B, D), dtype=torch.float32, device=x.device) if want_f32 else None)
+    for b0 in range(0, B, 32):
+        n = min(32, B - b0)
+        nbytes = lib().mi_int8_mlp_workspace(n, D, I, int(g[2]), int(d[2]))
+        if nbytes == 0:
+            raise ValueError("mi_int8_mlp: unsupported shape B=%d D=%d I=%d" % (n, D, I))
+        ws = workspace if workspace is not None else WORKSPACES.get("int8", nbytes)
+        check("mi_int8_mlp", lib().mi_int8_mlp(_ptr(x[b0:b0 + n]), n, D, I, _ptr(g[0]), _ptr(g[1]), _ptr(u[0]),
+                                               _ptr(u[1]), int(g[2]), _ptr(d[0]), _ptr(d[1]), int(d[2]),
+                                               float(limit), _ptr(yb[b0:b0 + n]),
+                                               _ptr(yf[b0:b0 + n]) if yf is not None else None, _ptr(ws),
+                                               ws.numel(), _stream()))
+    return (yb, yf) if want_f32 else yb
+
+
+def mlp_partial(p, x, limit):
+    """The reference's mlp_partial(p, x, cfg) (model.py:125-127) for int8 leaves p = {"gate", "up", "down"}
+    (quant8.py:17-18): x bf16 [B, D] -> bf16 [B, D] (cfg.swiglu_limit passed as ``limit``)."""
+    return int8_mlp(x, p["gate"], p["up"], p["down"], limit)
+
+
 # ------------------------------------------------------------------------------------------------ the operator
 def _is_f32(dtype):
     """out_dtype given as a torch dtype, a numpy/JAX dtype or its name: True for float32."""

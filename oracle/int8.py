@@ -45,3 +45,17 @@ def project_after_f32(x, q, s):
     f32, times s [1, out] in f32 -> f32 [B, out] (before the cast to x's dtype)."""
     z = (np.asarray(x, dtype=np.float64) @ np.asarray(q, dtype=np.float64)).astype(np.float32)
     return (z * np.asarray(s, dtype=np.float32)).astype(np.float32)
+
+
+def mlp_partial_f32(x, gate, up, down, limit, _drop=()):
+    """mlp_partial (model.py:125-127) over int8 leaves gate, up, down = (q [in, out], s [1, out] or [in, 1]), as
+    every layer program sees them after dequant_tree (quant8.py:91-99): g = bf16(x @ Wg), u = bf16(x @ Wu) (bf16
+    matmuls with f32 accumulation; f64 here), h = bf16(swiglu_clamped(g, u)) (one rounding of the SwiGLU evaluated
+    in f64), y = h @ Wd -> f32 [B, D] before the output's bf16 rounding.  ``_drop`` ("g", "u", "h") skips a rounding:
+    planted-mistake tests only."""
+    from .moe import swiglu_clamped
+    rnd = lambda name, a: np.asarray(a, dtype=np.float32) if name in _drop else round_bf16(a)
+    g = rnd("g", project_f32(x, *gate))
+    u = rnd("u", project_f32(x, *up))
+    h = rnd("h", swiglu_clamped(g, u, limit).astype(np.float32))
+    return project_f32(h, *down)

@@ -84,3 +84,29 @@ def test_int8_lm_head_form(pkg, gpu, B, n_in, n_out):
     want = oi8.project_after_f32(x, q, s)
     assert rel_l2(yf.cpu().numpy(), want) < 1e-5
     assert rel_l2(yb.float().cpu().numpy(), round_bf16(want)) < 1e-3
+
+
+def _leaf(rng, n_in, n_out, axis):
+    """A reference int8 leaf {"q": [in, out], "s": [1, out] (axis 1) or [in, 1] (axis 0)} of N(0, 0.05) weights."""
+    q, s = oi8.quantize_array(rng.standard_normal((n_in, n_out)).astype(np.float32) * 0.05, axis)
+    return {"q": q, "s": s}
+
+
+@pytest.mark.parametrize("B,D,I,gu_axis,dn_axis,limit", [(1, 512, 256, 1, 1, 7.0), (8, 6144, 2048, 1, 0, 7.0),
+                                                         (32, 1024, 512, 0, 0, 1.5), (40, 512, 768, 1, 0, 7.0),
+                                                         (5, 2048, 1024, 1, 0, 1.5)])
+def test_int8_mlp(pkg, gpu, B, D, I, gu_axis, dn_axis, limit):
+    """mlp_partial over int8 leaves (model.py:125-127; the shared expert at D 6144 / I 2048): g, u, h rounded to bf16
+    as the reference's bf16 matmuls and SwiGLU give them; 40 tokens run as two calls of <= 32.  Bar: the f32 output
+    within rel-L2 1e-4 of oracle.int8.mlp_partial_f32 (a g, u or h element next to a bf16 rounding boundary may round
+    the other way under f32 accumulation), the bf16 output that f32 output rounded once."""
+    rng = np.random.default_rng(B * 7 + I)
+    p = {"gate": _leaf(rng, D, I, gu_axis), "up": _leaf(rng, D, I, gu_axis), "down": _leaf(rng, I, D, dn_axis)}
+    x = round_bf16(rng.standard_normal((B, D)).astype(np.float32) * 2)
+    xt = torch.from_numpy(x).cuda().to(torch.bfloat16)
+    yb, yf = pkg.int8_mlp(xt, p["gate"], p["up"], p["down"], limit, want_f32=True)
+    want = oi8.mlp_partial_f32(x, (p["gate"]["q"], p["gate"]["s"]), (p["up"]["q"], p["up"]["s"]),
+                               (p["down"]["q"], p["down"]["s"]), limit)
+    assert rel_l2(yf.cpu().numpy(), want) < 1e-4
+    assert np.array_equal(yb.float().cpu().numpy(), round_bf16(yf.cpu().numpy()))
+    assert torch.equal(pkg.mlp_partial(p, xt, limit), yb)

@@ -1,0 +1,48 @@
+"""CPU: pins oracle.int8.mlp_partial_f32 (mlp_partial over int8 leaves, model.py:125-127 with quant8.py:91-99)
+against an independent restatement in torch's own bf16 arithmetic -- bf16(f32(q) * s) weights, torch's bf16 matmuls
+for g and u (f32 accumulation, bf16 out), F.silu on the clamped f32 values rounded to bf16, then h @ Wd in f32 --
+and checks that dropping any one of its bf16 roundings (g, u, h), the plausible mistakes, moves it far beyond the
+agreement (planted mistakes, each must fail)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import int8 as oi
+from oracle.bf16 import rel_l2, round_bf16
+
+AGREE = 1e-5        # observed ~2e-7 (f64 against torch's f32 accumulation)
+PLANTED = 1e-3      # observed 1.7e-3 .. 3.2e-3
+
+
+def _case(seed, limit):
+    rng = np.random.default_rng(seed)
+    B, D, I = 8, 512, 256
+    leaf = lambda n_in, n_out, axis: oi.quantize_array(rng.standard_normal((n_in, n_out)).astype(np.float32) * 0.05,
+                                                       axis)
+    g, u, d = leaf(D, I, 1), leaf(D, I, 1), leaf(I, D, 0)
+    x = round_bf16(rng.standard_normal((B, D)).astype(np.float32) * 2)
+    return x, g, u, d, limit
+
+
+def _torch_mlp(x, g, u, d, limit):
+    w = lambda q, s: (torch.tensor(q).float() * torch.tensor(s)).bfloat16()
+    xb = torch.tensor(x).bfloat16()
+    gg, uu = xb @ w(*g), xb @ w(*u)
+    h = (torch.nn.functional.silu(torch.clamp(gg.float(), max=limit)) * torch.clamp(uu.float(), -limit, limit))
+    return (h.bfloat16().float() @ w(*d).float()).numpy(), gg.float().numpy(), uu.float().numpy()
+
+
+@pytest.mark.parametrize("limit", [7.0, 1.5])
+def test_mlp_partial_equals_torch_restatement(limit):
+    x, g, u, d, L = _case(1, limit)
+    want, gg, uu = _torch_mlp(x, g, u, d, L)
+    if limit < 2:
+        assert (gg > L).mean() > 0.05 and (np.abs(uu) > L).mean() > 0.05      # the clamps engage
+    assert rel_l2(oi.mlp_partial_f32(x, g, u, d, L), want) < AGREE
+
+
+@pytest.mark.parametrize("drop", ["g", "u", "h"])
+def test_mlp_partial_planted_rounding_mistakes_fail(drop):
+    x, g, u, d, L = _case(2, 7.0)
+    want, _, _ = _torch_mlp(x, g, u, d, L)
+    assert rel_l2(oi.mlp_partial_f32(x, g, u, d, L, _drop=(drop,)), want) > PLANTED
