@@ -173,7 +173,8 @@ int mi_moe_decode_noalloc(const mi_table *gate, const mi_table *up, const mi_tab
  *   [16..23] mi_moe_decode's launches: gate/up splits, row tiles per wavefront, workgroups (0: one per task), down
  *   splits, row tiles per wavefront, workgroups (0: one per task), gate/up and down dynamic LDS bytes (persistent).
  *   [24] mi_moe_decode's gate/up and down kernels: 0 grouped (one workgroup per task), 1 persistent streams,
- *   2 CU-balanced streams (one workgroup per CU, CB3 at one token).
+ *   2 CU-balanced streams (one workgroup per CU, CB3 at one token), 3 CU-balanced multi-token streams (CB3, 2-16
+ *   tokens).
  * Returns MI_OK or MI_ERR_ARG.
  */
 int mi_moe_decode_plan(const mi_table *gate, const mi_table *down, int32_t N, int32_t k, int32_t shared_expert,

@@ -37,6 +37,7 @@ UNITS += [("k_fused.hip", [], "k_fused")]
 UNITS += [("k_pstream.hip", ["-DMI_PMODE=%d" % m, "-DMI_PTC=%d" % tc], "k_pstream_%d_%d" % (m, tc))
           for m in (0, 1) for tc in (8, 16)]
 UNITS += [("k_custream.hip", ["-DMI_CMODE=%d" % m], "k_custream_%d" % m) for m in (0, 1)]
+UNITS += [("k_cumulti.hip", ["-DMI_UMODE=%d" % m], "k_cumulti_%d" % m) for m in (0, 1)]
 # prefill GEMMs per (mode, rounding form): gate/up plain, bf16 g/u, weighted h, both; down bf16 y, f32 y
 UNITS += [("k_prefill.hip", ["-DMI_PF_MODE=%d" % m, "-DMI_PF_FORM=%d" % f], "k_prefill_%d_%d" % (m, f))
           for m, f in ((0, 0), (0, 1), (0, 2), (0, 3), (1, 0), (1, 4))]

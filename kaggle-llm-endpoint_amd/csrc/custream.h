@@ -46,7 +46,10 @@ struct CArgs {
     float *part;               // [S][nmat][NS][R]
 };
 
-constexpr int kCuWaves = 12;   // wavefronts per workgroup (3 per SIMD)
+#ifndef MI_CU_WAVES
+#define MI_CU_WAVES 12
+#endif
+constexpr int kCuWaves = MI_CU_WAVES;   // wavefronts per workgroup (3 per SIMD)
 
 template <int MODE, int RTW>
 __global__ void __launch_bounds__(64 * kCuWaves, 1) custream_kernel(CArgs a) {

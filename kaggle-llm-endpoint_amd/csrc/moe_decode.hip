@@ -1,11 +1,12 @@
 // Grouped codebook-dequant expert matvec: host side of the C ABI (argument validation, split planning, workspace
 // layout, launches) and the exact dequant kernel.  The grouped kernels themselves live in grouped.h.
-#include "custream.h"
+#include "cumulti.h"
 #include "pstream.h"
 
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <algorithm>
 #include <mutex>
 
 namespace mi {
@@ -490,6 +491,11 @@ void launch_custream_1(int rtw, dim3 grid, size_t lds, hipStream_t s, const CArg
 static void custream_launch(int mode, int rtw, dim3 grid, size_t lds, hipStream_t s, const CArgs &a) {
     (mode == kGateUp ? launch_custream_0 : launch_custream_1)(rtw, grid, lds, s, a);
 }
+void launch_cumulti_0(int rtw, dim3 grid, size_t lds, hipStream_t s, const MArgs &a);
+void launch_cumulti_1(int rtw, dim3 grid, size_t lds, hipStream_t s, const MArgs &a);
+static void cumulti_launch(int mode, int rtw, dim3 grid, size_t lds, hipStream_t s, const MArgs &a) {
+    (mode == kGateUp ? launch_cumulti_0 : launch_cumulti_1)(rtw, grid, lds, s, a);
+}
 
 static int pstream_occupancy(int mode, int tc, int rtw, size_t lds) {
     if (mode == kGateUp) return (tc <= 8 ? occupancy_pstream_0_8 : occupancy_pstream_0_16)(rtw, lds);
@@ -509,6 +515,9 @@ struct DecodePlan {
     int G, rows1, rows2, NS;
     int cu;                     // CB3, one token: the CU-balanced launches (custream.h), one workgroup per CU
     int cgmax;                  // their down launch: most groups one workgroup's share touches
+    int cum;                    // CB3, 2..16 tokens: the CU-balanced multi-token launches (cumulti.h)
+    int mgmax;                  // their down launch: groups staged at a time
+    int xsp1, xsp2;             // their staged row pitches (dwords)
     int persistent;             // CB3 gate/up and down as persistent launches
     Shape s1, s2;
     int P1, P2;                 // persistent: workgroups of the two launches
@@ -532,6 +541,71 @@ static void plan_pstream(int mode, int tc, const Shape &sh, int G, size_t stagin
     *P = (int)(p < 1 ? 1 : p);
 }
 
+// Static LDS of cumulti_kernel besides its dynamic staging and codebook slots (group table, counters).
+constexpr size_t kCumultiStaticLds = 8 * 1024;
+
+// The CU-balanced multi-token launches (cumulti.h): one workgroup per CU, the workgroups dealt to the column splits
+// in proportion to their columns.  gate/up stages every token's x row of its split; down the h rows (high part and
+// remainder) of up to mgmax groups at a time.  False when a split would get no workgroup or the staging cannot fit.
+static bool plan_cumulti(const mi_table *gate, const mi_table *down, int N, DecodePlan &p) {
+    const int P = cu_count();
+    const int nu1 = n_units_of(gate), nu2 = n_units_of(down);
+    const int nb1 = (nu1 + 3) / 4, nb2 = (nu2 + 3) / 4;
+    // measured best at D 6144, I 2048 (8 and 16 tokens)
+    int S1 = env_int("MI355MOE_MS1", N <= 8 ? 2 : 4), S2 = env_int("MI355MOE_MS2", 2);
+    int r1 = env_int("MI355MOE_MS1_RTW", 1), r2 = env_int("MI355MOE_MS2_RTW", 2);
+    S1 = S1 < 1 ? 1 : S1 > nb1 ? nb1 : S1;
+    S2 = S2 < 1 ? 1 : S2 > nb2 ? nb2 : S2;
+    r1 = (r1 == 2 || r1 == 4) ? r1 : 1;
+    r2 = (r2 == 2 || r2 == 4) ? r2 : 1;
+    // the widest split (whole super tiles) and every split's workgroup count
+    auto widest = [&](int nu, int nb, int S, bool *ok) {
+        int w = 0;
+        *ok = true;
+        for (int s = 0; s < S; ++s) {
+            const int a0 = std::min(nu, 4 * (int)((long long)s * nb / S));
+            const int a1 = std::min(nu, 4 * (int)((long long)(s + 1) * nb / S));
+            w = std::max(w, a1 - a0);
+            const long long w0 = (long long)P * a0 / nu, w1 = s + 1 < S ? (long long)P * a1 / nu : P;
+            if (w1 <= w0 || a1 <= a0) *ok = false;
+        }
+        return w;
+    };
+    bool ok1, ok2;
+    const int t1 = widest(nu1, nb1, S1, &ok1), t2 = widest(nu2, nb2, S2, &ok2);
+    if (!ok1 || !ok2) return false;
+    p.s1 = Shape{Split{S1, 4}, r1, gate->rows / (16 * r1), 0};
+    p.s2 = Shape{Split{S2, 4}, r2, down->rows / (16 * r2), 0};
+    p.P1 = p.P2 = P;
+    p.xsp1 = cb3_row_pitch(80 * t1);
+    p.xsp2 = cb3_row_pitch(80 * t2);
+    const size_t cbl = sizeof(uint4) * kCuWaves * 5 * 64;
+    const size_t budget = kLdsPerCu - kCumultiStaticLds;
+    p.lds1 = sizeof(uint32_t) * (size_t)N * p.xsp1 + cbl;
+    // groups a down share touches: at most NS groups (every slot its own), shared by the split's workgroups
+    int ps_min = P;
+    for (int s = 0; s < S2; ++s) {
+        const int a0 = std::min(nu2, 4 * (int)((long long)s * nb2 / S2));
+        const int a1 = std::min(nu2, 4 * (int)((long long)(s + 1) * nb2 / S2));
+        const int w0 = (int)((long long)P * a0 / nu2), w1 = s + 1 < S2 ? (int)((long long)P * a1 / nu2) : P;
+        ps_min = std::min(ps_min, w1 - w0);
+    }
+    const long long units = ((long long)p.NS * p.s2.RB + ps_min - 1) / ps_min;
+    int gmax = (int)((units + p.s2.RB - 1) / p.s2.RB) + 1;
+    const size_t per_g = sizeof(uint32_t) * 2 * (size_t)N * p.xsp2;
+    const int fit = (int)((budget - cbl) / per_g);
+    if (p.lds1 > budget || fit < 1) return false;
+    p.mgmax = gmax < fit ? gmax : fit;
+    const int forced = env_int("MI355MOE_MGMAX", 0);          // tests: fewer groups per epoch (more epochs)
+    if (forced > 0 && forced < p.mgmax) p.mgmax = forced;
+    p.lds2 = per_g * p.mgmax + cbl;
+    // more than half of a CU's LDS: one workgroup per CU
+    const size_t half = kLdsPerCu / 2 + 1024;
+    if (p.lds1 < half) p.lds1 = half;
+    if (p.lds2 < half) p.lds2 = half;
+    return true;
+}
+
 // xf32: f32 activations (staged as bf16 high part + remainder, one workgroup per task).
 static DecodePlan plan_decode(const mi_table *gate, const mi_table *down, int N, int k, int shared,
                               bool xf32 = false) {
@@ -547,9 +621,14 @@ static DecodePlan plan_decode(const mi_table *gate, const mi_table *down, int N,
     if (est < 1) est = 1;
     p.cu = gate->qtype == MI_QT_CB3 && down->qtype == MI_QT_CB3 && !xf32 && N == 1 &&
            env_int("MI355MOE_CUSTREAM", 1) != 0;
-    p.persistent = !p.cu && gate->qtype == MI_QT_CB3 && down->qtype == MI_QT_CB3 && !xf32 &&
+    p.cum = !p.cu && gate->qtype == MI_QT_CB3 && down->qtype == MI_QT_CB3 && !xf32 && N >= 2 &&
+            env_int("MI355MOE_CUMULTI", 1) != 0;
+    if (p.cum && !plan_cumulti(gate, down, N, p)) p.cum = 0;
+    p.persistent = !p.cu && !p.cum && gate->qtype == MI_QT_CB3 && down->qtype == MI_QT_CB3 && !xf32 &&
                    N > env_int("MI355MOE_PERSIST_ABOVE", kPersistentMinTokens);
-    if (p.cu) {
+    if (p.cum) {
+        // planned above
+    } else if (p.cu) {
         // equal shares of (group, matrix, split, row tile) units over one workgroup per CU; splits are whole super
         // tiles (the staged rows are the full activation, so a split never starts inside a super tile)
         const int P = cu_count();
@@ -852,8 +931,34 @@ static int decode_launch(const DecodePlan &p, const mi_table *gate, const mi_tab
         ca.idx = idx;
         ca.part = a.part;
     }
+    // the CU-balanced multi-token launches
+    MArgs ma{};
+    if (p.cum) {
+        ma.t0 = a.t0.cb3;
+        ma.t1 = a.t1.cb3;
+        ma.R = gate->rows;
+        ma.K = gate->cols;
+        ma.E = a.E;
+        ma.n_route = a.n_route;
+        ma.N = N;
+        ma.k = k;
+        ma.shared_expert = shared_expert;
+        ma.NS = p.NS;
+        ma.S = p.s1.sp.S;
+        ma.al = 4;
+        ma.nu = n_units_of(gate);
+        ma.RT = p.s1.RB;
+        ma.P = p.P1;
+        ma.gmax = 0;
+        ma.xsp = p.xsp1;
+        ma.x = x_bf16;
+        ma.x_lo = nullptr;
+        ma.idx = idx;
+        ma.part = a.part;
+    }
     if (phases & 1) {
-        if (p.cu) custream_launch(kGateUp, p.s1.rtw, dim3(p.P1), p.lds1, s, ca);
+        if (p.cum) cumulti_launch(kGateUp, p.s1.rtw, dim3(p.P1), p.lds1, s, ma);
+        else if (p.cu) custream_launch(kGateUp, p.s1.rtw, dim3(p.P1), p.lds1, s, ca);
         else if (cb3) pstream_launch(kGateUp, tc, p.s1.rtw, dim3(p.P1), p.lds1, s, pa);
         else launch_grouped<kGateUp>(gate->qtype, a.t_rows, p.s1.rtw, dim3(p.G * p.s1.RBG * p.s1.sp.S), lds1, s, a);
         if ((st = launch_status())) return st;
@@ -867,7 +972,7 @@ static int decode_launch(const DecodePlan &p, const mi_table *gate, const mi_tab
     // (the SwiGLU launch's arithmetic, from the gate/up partials) instead of a SwiGLU launch.  Measured slower (the
     // down staging waits for the split partials: +2.5 us on the down launch at batch 1, +14 us per layer at batch 8),
     // so the SwiGLU launch is the default.
-    const bool fuse_h = !cb3 && !p.cu && env_int("MI355MOE_FUSE_SWIGLU", 0) == 1;
+    const bool fuse_h = !cb3 && !p.cu && !p.cum && env_int("MI355MOE_FUSE_SWIGLU", 0) == 1;
     // the CU-balanced down launch forms h itself while staging (bit-identical h, one launch fewer: ~2 us at one token;
     // MI355MOE_CU_FORM_H=0 keeps the SwiGLU launch, for measurement)
     const bool cu_form = p.cu && env_int("MI355MOE_CU_FORM_H", 1) != 0 && p.s1.sp.S <= 2 &&
@@ -900,7 +1005,22 @@ static int decode_launch(const DecodePlan &p, const mi_table *gate, const mi_tab
     b.limit = limit;
     b.part = (float *)(ws + p.off_part2);
     size_t lds2 = sizeof(uint32_t) * 2 * (size_t)b.t_rows * b.xs_max;
-    if (p.cu) {
+    if (p.cum) {
+        MArgs mb = ma;
+        mb.t0 = mb.t1 = b.t0.cb3;
+        mb.R = down->rows;
+        mb.K = down->cols;
+        mb.S = p.s2.sp.S;
+        mb.nu = n_units_of(down);
+        mb.RT = p.s2.RB;
+        mb.P = p.P2;
+        mb.gmax = p.mgmax;
+        mb.xsp = p.xsp2;
+        mb.x = h_hi;
+        mb.x_lo = h_lo;
+        mb.part = b.part;
+        cumulti_launch(kDown, p.s2.rtw, dim3(p.P2), p.lds2, s, mb);
+    } else if (p.cu) {
         CArgs cb = ca;
         cb.t0 = cb.t1 = b.t0.cb3;
         cb.R = down->rows;
@@ -1101,10 +1221,11 @@ int mi_moe_decode_plan(const mi_table *gate, const mi_table *down, int32_t N, in
     int32_t v[25] = {0};
     {
         const DecodePlan d = plan_decode(gate, down, N, k, shared_expert);
-        const int32_t f[8] = {d.s1.sp.S, d.s1.rtw, (d.persistent || d.cu) ? d.P1 : 0, d.s2.sp.S, d.s2.rtw,
-                              (d.persistent || d.cu) ? d.P2 : 0, (int32_t)d.lds1, (int32_t)d.lds2};
+        const bool pers = d.persistent || d.cu || d.cum;
+        const int32_t f[8] = {d.s1.sp.S, d.s1.rtw, pers ? d.P1 : 0, d.s2.sp.S, d.s2.rtw, pers ? d.P2 : 0,
+                              (int32_t)d.lds1, (int32_t)d.lds2};
         for (int i = 0; i < 8; ++i) v[16 + i] = f[i];
-        v[24] = d.cu ? 2 : d.persistent ? 1 : 0;
+        v[24] = d.cum ? 3 : d.cu ? 2 : d.persistent ? 1 : 0;
     }
     const FusedPlan p = plan_fused(gate, down, N, k, shared_expert);
     if (p.ok) {

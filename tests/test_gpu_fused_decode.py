@@ -121,8 +121,8 @@ def test_fused_wait_give_up_is_reported_and_the_next_call_is_clean(pkg, gpu, mon
     ({"MI355MOE_FS1": "5", "MI355MOE_FS1_RTW": "2", "MI355MOE_FS2": "3"}, (1, 5, 8), True),
     ({"MI355MOE_FS1": "3", "MI355MOE_FS1_RTW": "4", "MI355MOE_FS2": "1"}, (1, 5, 8), True),
     ({"MI355MOE_FS1": "1", "MI355MOE_FS2": "4"}, (1, 2), True),
-    ({"MI355MOE_S1": "3", "MI355MOE_S2": "2", "MI355MOE_S1_RTW": "2"}, (12, 16), False),
-    ({"MI355MOE_S1": "2", "MI355MOE_S2": "1", "MI355MOE_S2_RTW": "1"}, (9, 16), False)])
+    ({"MI355MOE_S1": "3", "MI355MOE_S2": "2", "MI355MOE_S1_RTW": "2", "MI355MOE_CUMULTI": "0"}, (12, 16), False),
+    ({"MI355MOE_S1": "2", "MI355MOE_S2": "1", "MI355MOE_S2_RTW": "1", "MI355MOE_CUMULTI": "0"}, (9, 16), False)])
 def test_forced_plans(pkg, gpu, env, Ns, fused):
     """Column splits in both phases (the one launch: the last split of a row range forms h, the last down task
     combines; the separate persistent launches: contiguous task ranges that restage when the group or split
