@@ -162,10 +162,9 @@ __host__ __device__ constexpr int wave_rows() { return QT == MI_QT_CB3 ? 16 * RT
 #ifndef MI_CB3_WAVES
 #define MI_CB3_WAVES 3
 #endif
-// IQ2_S holds two partials per row tile and k-step (two scale groups per word) beside its LDS grid entries: 2
-// wavefronts per SIMD (<= 256 VGPRs).  The K-quant decoders fit the common bound.
+// Every decoder fits the common bound.
 template <int QT>
-__host__ __device__ constexpr int min_waves_per_simd() { return QT == MI_QT_IQ2_S ? 2 : MI_CB3_WAVES; }
+__host__ __device__ constexpr int min_waves_per_simd() { return MI_CB3_WAVES; }
 
 template <int MODE, int QT, int TCMAX, int RTW>
 __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) grouped_kernel(KArgs a) {
@@ -259,6 +258,16 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
             return;
         }
         const int q4 = xs >> 1;           // 4-column quads per row
+        // IQ2_S stages f16 (iq2_mfma.h): a second pass at scale 2^-shift when the first met |x| >= 2^15
+        int shift = 0;
+        for (int pass = 0; pass < 2; ++pass) {
+        if (pass == 1) {
+            if constexpr (QT == MI_QT_IQ2_S) {
+                __syncthreads();
+                shift = iq2_xshift(iq.amax);
+            }
+            if (shift == 0) break;
+        }
         for (int i = tid; i < a.t_rows * q4; i += blockDim.x) {
             const int t = i / q4, q = i - t * q4;
             const int slot = s_tok[t];
@@ -299,6 +308,17 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
                     lv = make_uint2(l0 | (l1 << 16), l2 | (l3 << 16));
                 }
             }
+            if constexpr (QT == MI_QT_IQ2_S) {
+                // f16 high part and remainder of each value (the bf16 element, or its high part + remainder)
+                const uint32_t hw[4] = {hv.x & 0xffffu, hv.x >> 16, hv.y & 0xffffu, hv.y >> 16};
+                const uint32_t lw[4] = {lv.x & 0xffffu, lv.x >> 16, lv.y & 0xffffu, lv.y >> 16};
+                uint32_t fh[4], fl[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    iq2_x16(bf16_to_f32(hw[j]) + (hilo ? bf16_to_f32(lw[j]) : 0.0f), shift, iq, fh[j], fl[j]);
+                hv = make_uint2(fh[0] | (fh[1] << 16), fh[2] | (fh[3] << 16));
+                lv = make_uint2(fl[0] | (fl[1] << 16), fl[2] | (fl[3] << 16));
+            }
             if constexpr (QT == MI_QT_IQ4_XS) {
                 // the decoder's column order inside each 32-column group (iq4_stage_pos)
                 uint16_t *dh = (uint16_t *)(xh + t * xsp), *dl = (uint16_t *)(xl + t * xsp);
@@ -314,6 +334,7 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
                 *(uint2 *)(xh + t * xsp + 2 * q) = hv;
                 if (hilo) *(uint2 *)(xl + t * xsp + 2 * q) = lv;
             }
+        }
         }
         __syncthreads();
     };

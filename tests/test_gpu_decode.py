@@ -133,6 +133,28 @@ def test_decode_small(pkg, gpu, qtype, N, k, E, routing):
     assert torch.equal(of2, of3)
 
 
+@pytest.mark.parametrize("N,scale,f32x", [(1, 1e6, False), (3, 3e4, False), (8, 1e9, False), (2, 1e6, True)])
+def test_iq2s_large_activations(pkg, gpu, N, scale, f32x):
+    """IQ2_S decodes on f16 matrix-core operands: a workgroup whose activations reach 2^15 stages them divided by a
+    power of two (and scales its sums back), so activations far outside f16's range still decode exactly.  Half the
+    values are large, the rest N(0, 1); the SwiGLU limit is large enough that h stays unclamped and large too."""
+    rng = np.random.default_rng(17 + N)
+    E, D, I, k = 6, 512, 256, 3
+    L = Layer(rng, "IQ2_S", E, D, I)
+    tbs = L.tables(pkg)
+    idx, w = zipf_routing(rng, N, E, k)
+    x = rng.standard_normal((N, D)).astype(np.float32)
+    x[:, ::2] *= scale
+    if not f32x:
+        x = round_bf16(x)
+    limit = 1e30
+    want = omoe.decode_apply(L.deq, x, idx, w, limit)
+    xt = _t(x) if f32x else _t(x, torch.bfloat16)
+    of, _ = pkg.moe_decode(tbs["gate"], tbs["up"], tbs["down"], xt, _t(idx), _t(w), limit)
+    assert np.isfinite(of.cpu().numpy()).all()
+    assert rel_l2(of.cpu().numpy(), want) < (5e-5 if f32x else 1e-5)
+
+
 def test_decode_limit_clamps(pkg, gpu):
     """A small swiglu limit makes the clamps of model.py:119-122 active."""
     rng = np.random.default_rng(3)
