@@ -47,6 +47,7 @@ def parse():
     ap.add_argument("--replays", type=int, default=9, help="timed replays of the headline graphs (median, p10/p90)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only-b1", action="store_true", help="headline only (profiling runs)")
+    ap.add_argument("--only-b816", action="store_true", help="the CB3 layer at batch 8 and 16 only (profiling runs)")
     ap.add_argument("--only-layout", default=None,
                     help="decode at batch 1 and 8 of one table layout only, e.g. iq2s_iq4xs (profiling runs)")
     ap.add_argument("--only-prefill", action="store_true", help="the 512-token prefill chunk only (profiling runs)")
@@ -339,6 +340,13 @@ def main():
                                                               iq_pe("iq4xs")),
                           "prefill_t512_iq2s_iq4xs": bench_prefill(torch, pkg, gen, args, iq_layers("iq2s_iq4xs"),
                                                                    rng, iq_pe("iq2s_iq4xs"))}))
+        return
+    if args.only_b816:
+        res = {}
+        for N in (8, 16):
+            ms, b = measure(N, zipf_topk)
+            res["b%d" % N] = {"us_per_layer": round(ms * 1e3, 2), "GBps": round(b / (ms * 1e-3) / 1e9, 1)}
+        print(json.dumps(res))
         return
     if args.only_layout:
         fmt = args.only_layout
