@@ -20,6 +20,7 @@ constexpr int kPlanWaves = kPlanThreads / 64;
 constexpr int kPlanMaxE = 1024;
 constexpr long long kPlanMaxSlots = 1 << 22;
 constexpr int kPlanReg = 8;                 // slots per thread held in registers (S <= kPlanReg * kPlanThreads)
+constexpr int kPlanMaskE = 512;             // up to this many experts, pass 2 matches ids through LDS words
 
 struct PlanOut {
     int32_t *blk_expert;   // [G]   expert of every block (blocks >= n_blocks repeat the last expert)
@@ -33,27 +34,24 @@ struct PlanOut {
 };
 
 // Slot s of the plan: token s / kk, column j = s % kk; columns j < k are the routed slots, column k (kk = k + 1) is
-// the shared expert (weight 1) when one is given.
-__device__ __forceinline__ int plan_expert(const int32_t *idx, int s, int k, int kk, int shared, int E) {
-    const int t = s / kk, j = s - t * kk;
-    const int e = j < k ? idx[t * k + j] : shared;
-    return (e >= 0 && e < E) ? e : -1;
-}
+// the shared expert (weight 1) when one is given.  A slot whose expert id is outside [0, E) takes no row.
 
-// Weight of slot s: w[t, j] for a routed column, 1 for the shared one; with merge, the routed weight of (t, expert)
-// summed over the token's columns in order, 0 for a column whose expert an earlier column of the token names.
-__device__ __forceinline__ float plan_weight(const int32_t *idx, const float *w, int s, int k, int kk, bool merge) {
-    const int t = s / kk, j = s - t * kk;
-    if (j >= k) return 1.0f;
-    if (!merge) return w[t * k + j];
-    const int e = idx[t * k + j];
+// Routed weight of column j of token t, expert e, for a plan that merges duplicates: w[t, jj] summed over the token's
+// columns jj naming e, in column order, when j is the first of them; 0 for a later one.  Every load of a group of
+// columns is issued before the group's compares.
+__device__ __forceinline__ float plan_weight_merged(const int32_t *idx, const float *w, int t, int j, int k, int e) {
     float sum = 0.0f;
+    bool first = true;
+#pragma unroll 4
     for (int jj = 0; jj < k; ++jj) {
-        if (idx[t * k + jj] != e) continue;
-        if (jj < j) return 0.0f;
-        sum += w[t * k + jj];
+        const int ej = idx[t * k + jj];
+        const float wj = w[t * k + jj];
+        if (ej == e) {
+            sum += wj;
+            first = first && jj >= j;
+        }
     }
-    return sum;
+    return first ? sum : 0.0f;
 }
 
 // Inclusive prefix sum over the kPlanThreads threads of the workgroup (every thread calls it).
@@ -71,124 +69,160 @@ __device__ int block_inclusive_scan(int v, int *wsum) {
     return v;
 }
 
-// The reference's ragged_plan (pallas_moe.py:564-592), stable: the rows of one expert follow slot order.  Counting
-// is order-free (LDS atomics); the rows are then assigned in rounds of kPlanThreads slots, where a slot's rank is the
-// number of earlier slots of its expert: earlier rounds (a running count), earlier wavefronts of the round (a prefix
-// over per-wavefront counts) and earlier lanes of its wavefront (a ballot match).
+// Lanes of this wavefront holding a valid expert id equal to this lane's: the AND, over the id's nbits (<= 10) bits,
+// of the ballot of the lanes that agree with this lane on the bit (nbits + 1 ballots, whatever the number of
+// distinct ids).
+__device__ __forceinline__ uint64_t match_expert(int e, bool valid, int nbits) {
+    static_assert(kPlanMaxE <= 1024, "expert ids have at most 10 bits");
+    uint64_t m = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < 10; ++b) {
+        if (b >= nbits) break;
+        const uint64_t on = __ballot(valid && ((e >> b) & 1));
+        const uint64_t d = (uint64_t)(int64_t)((e << (31 - b)) >> 31);   // all ones when bit b of e is set
+        m &= ~(on ^ d);
+    }
+    return m;
+}
+
+// The reference's ragged_plan (pallas_moe.py:564-592), stable: the rows of one expert follow slot order.  Wavefront
+// v owns the contiguous slots [v * C, (v + 1) * C), C = 64 * ceil(S / kPlanThreads), walked 64 at a time in slot
+// order.  Pass 1 counts every expert's slots per wavefront (LDS atomics); an exclusive prefix over the wavefronts
+// gives each wavefront its first row within the expert and the expert's total; pass 2 walks the slots again and
+// places slot s at the expert's first padded row + the wavefront's running row + the number of lower lanes of the
+// same id (an LDS word per wavefront and id that the lanes OR their bits into, or ballots of the id's bits past
+// kPlanMaskE experts).  Expert ids and weights of up to kPlanReg * kPlanThreads slots stay in registers between the passes.
 __global__ void __launch_bounds__(kPlanThreads) ragged_plan_kernel(const int32_t *__restrict__ idx,
                                                                    const float *__restrict__ w, int T, int k,
                                                                    int shared, int E, int tm, PlanOut p) {
-    __shared__ int cnt[kPlanMaxE], bend[kPlanMaxE], run[kPlanMaxE];
-    __shared__ uint16_t cntw[kPlanWaves][kPlanMaxE];
+    static_assert(kPlanWaves == 16, "the prefix over wavefronts scans 16 lanes per expert");
+    __shared__ int cntw[kPlanMaxE][kPlanWaves];   // per-wavefront count of every expert, then its running row
+    __shared__ int cnt[kPlanMaxE], bend[kPlanMaxE], rbase[kPlanMaxE];
+    __shared__ unsigned long long lanes[kPlanWaves][kPlanMaskE];   // pass 2: lanes of every id in this step
     __shared__ int wsum[kPlanWaves];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int kk = k + (shared >= 0 ? 1 : 0);
     const int S = T * kk;
     const int G = (S + tm - 1) / tm + E;
     const long long Rp = (long long)G * tm;
+    const int nsub = (S + kPlanThreads - 1) / kPlanThreads;   // 64-slot steps per wavefront
+    const int s0 = wave * nsub * 64 + lane;                  // this lane's slot in step 0
+    int nbits = 0;
+    while ((1 << nbits) < E) ++nbits;
 
-    for (int i = tid; i < kPlanMaxE; i += kPlanThreads) {
-        cnt[i] = 0;
-        run[i] = 0;
-        for (int v = 0; v < kPlanWaves; ++v) cntw[v][i] = 0;
+    for (int i = tid; i < E * kPlanWaves; i += kPlanThreads) (&cntw[0][0])[i] = 0;
+    if (E <= kPlanMaskE)
+        for (int i = tid; i < kPlanWaves * kPlanMaskE; i += kPlanThreads) (&lanes[0][0])[i] = 0ull;
+    // expert ids, weights and tokens of kPlanReg steps at a time, every load issued before any is used
+    int ereg[kPlanReg], treg[kPlanReg];
+    float wreg[kPlanReg];
+    const int q64 = 64 / kk, r64 = 64 - q64 * kk;   // a step of 64 slots advances q64 tokens and r64 columns
+    auto load_steps = [&](int rb) {
+        int col[kPlanReg], raw[kPlanReg];
+        float wraw[kPlanReg];
+        const int sb = s0 + rb * 64;
+        int t = sb / kk, j = sb - t * kk;          // token and column of this lane's slot, step by step
+#pragma unroll
+        for (int r = 0; r < kPlanReg; ++r) {
+            const bool in = rb + r < nsub && sb + r * 64 < S;
+            col[r] = in ? j : k;                   // column k: the shared expert's (or no slot)
+            treg[r] = in ? t : -1;
+            const int q = in && j < k ? t * k + j : 0;
+            raw[r] = idx[q];
+            wraw[r] = w[q];
+            t += q64;
+            j += r64;
+            if (j >= kk) {
+                j -= kk;
+                ++t;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < kPlanReg; ++r) {
+            int e = col[r] < k ? raw[r] : shared;
+            if (treg[r] < 0 || e < 0 || e >= E) e = -1;
+            ereg[r] = e;
+            wreg[r] = col[r] < k ? wraw[r] : 1.0f;
+            if (p.merge_dups && e >= 0 && col[r] < k) wreg[r] = plan_weight_merged(idx, w, treg[r], col[r], k, e);
+        }
+    };
+    __syncthreads();
+
+    // pass 1: count (order-free)
+    for (int rb = 0; rb < nsub; rb += kPlanReg) {
+        load_steps(rb);
+#pragma unroll
+        for (int r = 0; r < kPlanReg; ++r)
+            if (rb + r < nsub && ereg[r] >= 0) atomicAdd(&cntw[ereg[r]][wave], 1);
     }
-    for (long long r = tid; r < Rp; r += kPlanThreads) {
+    // every row starts as padding; the rows of pass 2 overwrite theirs after the wait below
+    for (int r = tid; r < (int)Rp; r += kPlanThreads) {   // Rp < 2^31 (checked on the host)
         p.tok_row[r] = -1;
         p.w_row[r] = 0.0f;
     }
-    // up to kPlanReg * kPlanThreads slots: every expert id and weight is loaded once, up front, all loads in flight
-    // together, and both passes below read them from registers (no global round trip per round)
-    const bool in_reg = S <= kPlanReg * kPlanThreads;
-    int ereg[kPlanReg];
-    float wreg[kPlanReg];
-#pragma unroll
-    for (int r = 0; r < kPlanReg; ++r) {
-        const int s = tid + r * kPlanThreads;
-        ereg[r] = -1;
-        wreg[r] = 0.0f;
-        if (in_reg && s < S) {
-            ereg[r] = plan_expert(idx, s, k, kk, shared, E);
-            wreg[r] = plan_weight(idx, w, s, k, kk, p.merge_dups);
-        }
-    }
     __syncthreads();
-    if (in_reg) {
+    // exclusive prefix over the wavefronts, 16 lanes per expert, and every expert's total
+    for (int eb = 0; eb < E; eb += kPlanThreads / kPlanWaves) {
+        const int e = eb + (tid >> 4), v = tid & 15;
+        const int c = e < E ? cntw[e][v] : 0;
+        int incl = c;
 #pragma unroll
-        for (int r = 0; r < kPlanReg; ++r)
-            if (ereg[r] >= 0) atomicAdd(&cnt[ereg[r]], 1);
-    } else {
-        for (int s = tid; s < S; s += kPlanThreads) {
-            const int e = plan_expert(idx, s, k, kk, shared, E);
-            if (e >= 0) atomicAdd(&cnt[e], 1);
+        for (int d = 1; d < 16; d <<= 1) {
+            const int o = __shfl_up(incl, d, 16);
+            if (v >= d) incl += o;
+        }
+        if (e < E) {
+            cntw[e][v] = incl - c;
+            if (v == 15) cnt[e] = incl;
         }
     }
     __syncthreads();
     // blocks per expert and their inclusive prefix (block end); padded rows start at (bend - nb) * tm
     const int nb_own = tid < E ? (cnt[tid] + tm - 1) / tm : 0;
     const int incl = block_inclusive_scan(nb_own, wsum);
-    if (tid < kPlanMaxE) bend[tid] = incl;
+    if (tid < kPlanMaxE) {
+        bend[tid] = incl;
+        rbase[tid] = (incl - nb_own) * tm;
+    }
     __syncthreads();
     const int n_blocks = bend[kPlanMaxE - 1];
     if (tid == 0) *p.n_blocks = n_blocks;
+    __builtin_amdgcn_s_waitcnt(0x0F70);        // vmcnt(0): this wavefront's padding stores are done ...
+    __syncthreads();                            // ... and every other wavefront's
 
-    // rows, in rounds of kPlanThreads slots
-    int tot = 0;
-    for (int base = 0, round = 0; base < S; base += kPlanThreads, ++round) {
-        const int s = base + tid;
-        int e = -1;
-        float wv = 0.0f;
-        if (in_reg) {
+    // pass 2: rows (the loads of pass 1 are still in registers when one batch held every step)
+    for (int rb = 0; rb < nsub; rb += kPlanReg) {
+        if (nsub > kPlanReg) load_steps(rb);
 #pragma unroll
-            for (int r = 0; r < kPlanReg; ++r)
-                if (r == round) {
-                    e = ereg[r];
-                    wv = wreg[r];
-                }
-        } else if (s < S) {
-            e = plan_expert(idx, s, k, kk, shared, E);
-            wv = plan_weight(idx, w, s, k, kk, p.merge_dups);
-        }
-        const bool valid = e >= 0;
-        uint64_t rem = __ballot(valid);
-        int rank = 0, n_same = 0;
-        while (rem) {
-            const int l = __builtin_ctzll(rem);
-            const int el = __builtin_amdgcn_readlane(e, l);
-            const uint64_t m = __ballot(valid && e == el);
-            if (valid && e == el) {
-                rank = __popcll(m & ((1ull << lane) - 1ull));
-                n_same = __popcll(m);
+        for (int r = 0; r < kPlanReg; ++r) {
+            if (rb + r >= nsub) break;
+            const int s = s0 + (rb + r) * 64;
+            const int e = ereg[r];
+            const bool valid = e >= 0;
+            uint64_t m;
+            if (E <= kPlanMaskE) {
+                // the lanes of each id gather in an LDS word: OR in, read back (LDS operations of one wavefront
+                // complete in order, so the read sees every lane's bit); the lowest lane clears it below
+                if (valid) atomicOr(&lanes[wave][e], 1ull << lane);
+                m = valid ? lanes[wave][e] : 0ull;
+            } else {
+                m = match_expert(e, valid, nbits);
             }
-            rem &= ~m;
-        }
-        if (valid && rank == 0) cntw[wave][e] = (uint16_t)n_same;
-        __syncthreads();
-        if (tid < E) {               // exclusive prefix over the wavefronts of this round
-            int acc = 0;
-            for (int v = 0; v < kPlanWaves; ++v) {
-                const int c = cntw[v][tid];
-                cntw[v][tid] = (uint16_t)acc;
-                acc += c;
-            }
-            tot = acc;
-        }
-        __syncthreads();
-        if (s < S) {
+            const int below = __popcll(m & ((1ull << lane) - 1ull));
             int row = -1;
             if (valid) {
-                const int nb = (cnt[e] + tm - 1) / tm;
-                row = (bend[e] - nb) * tm + run[e] + cntw[wave][e] + rank;
-                p.tok_row[row] = s / kk;
-                p.w_row[row] = wv;
+                row = rbase[e] + cntw[e][wave] + below;
+                p.tok_row[row] = treg[r];
+                p.w_row[row] = wreg[r];
             }
-            p.row_slot[s] = row;
+            if (s < S) p.row_slot[s] = row;
+            // every lane of the wavefront has read the running row above (LDS operations of one wavefront complete
+            // in order) before the lowest lane of each id advances it
+            if (valid && below == 0) {
+                cntw[e][wave] += __popcll(m);
+                if (E <= kPlanMaskE) lanes[wave][e] = 0ull;
+            }
         }
-        __syncthreads();
-        if (tid < E) {               // every wavefront's entry of this expert holds a prefix now: clear them all
-            for (int v = 0; v < kPlanWaves; ++v) cntw[v][tid] = 0;
-            run[tid] += tot;
-        }
-        __syncthreads();             // the clears land before the next round's counts
     }
 
     // block -> expert: the first expert whose block end exceeds g; blocks past n_blocks repeat the last one (the

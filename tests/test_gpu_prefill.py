@@ -39,7 +39,8 @@ def _routing(rng, kind, T, E, k):
                                            (37, 4, 12, 16, "zipf"), (300, 8, 64, 96, "zipf"),
                                            (2000, 8, 64, 32, "uniform"), (50, 2, 3, 1, "zipf"),
                                            (64, 8, 1024, 7, "uniform"), (5, 3, 5, 1000, "zipf"),
-                                           (700, 3, 4, 32, "one")])
+                                           (700, 3, 4, 32, "one"), (100, 4, 1, 16, "uniform"),
+                                           (4096, 9, 65, 80, "zipf"), (911, 9, 257, 80, "uniform")])
 def test_ragged_plan_bit_exact(pkg, gpu, T, k, E, tm, kind):
     rng = np.random.default_rng(T * 31 + E)
     idx, w = _routing(rng, kind, T, E, k)
@@ -48,6 +49,26 @@ def test_ragged_plan_bit_exact(pkg, gpu, T, k, E, tm, kind):
     for key in ("blk_expert", "n_blocks", "tok_row", "row_slot"):
         assert np.array_equal(got[key], want[key]), key
     assert np.array_equal(got["w_row"].view(np.uint32), want["w_row"].view(np.uint32))
+
+
+def test_ragged_plan_invalid_ids(pkg, gpu):
+    """Expert ids outside [0, E) take no row (row_slot -1); the valid slots are placed as the oracle's plan places
+    them when every invalid id is renamed to an extra last expert E, whose rows and blocks come after all others."""
+    T, k, E, tm = 600, 8, 64, 32
+    rng = np.random.default_rng(5)
+    idx, w = _routing(rng, "zipf", T, E, k)
+    bad = rng.random((T, k)) < 0.1
+    idx = np.where(bad, np.where(rng.random((T, k)) < 0.5, -3, E + 7), idx).astype(np.int32)
+    got = {key: v.cpu().numpy() for key, v in pkg.ragged_plan(_t(idx), _t(w), E, tm).items()}
+    want = omoe.ragged_plan(np.where(bad, E, idx).astype(np.int32), w, E + 1, tm)
+    nb = int(got["n_blocks"][0])
+    assert nb == int(want["n_blocks"][0]) - (-(-int(bad.sum()) // tm))
+    assert np.array_equal(got["blk_expert"][:nb], want["blk_expert"][:nb])
+    assert np.all(got["blk_expert"][nb:] == (want["blk_expert"][nb - 1] if nb else E - 1))
+    assert np.array_equal(got["tok_row"][:nb * tm], want["tok_row"][:nb * tm])
+    assert np.all(got["tok_row"][nb * tm:] == -1)
+    assert np.array_equal(got["w_row"][:nb * tm].view(np.uint32), want["w_row"][:nb * tm].view(np.uint32))
+    assert np.array_equal(got["row_slot"], np.where(bad, -1, want["row_slot"]))
 
 
 def _oracle_prefill(L, x, idx, w, limit, E, shared, combine):
