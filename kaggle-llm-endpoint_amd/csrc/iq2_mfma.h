@@ -31,6 +31,7 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 struct Iq2Lds {
     uint4 level[1024];     // grid entry -> its 8 levels as f16 (four pairs)
     uint2 smask[16];       // 4 sign bits -> the sign bits (15, 31) of 2 f16 pairs (32 banks: reads never conflict)
+    uint32_t cf2[16];      // 4-bit scale sc -> the odd factor 2 sc + 1 as an f16 pair
     uint32_t amax;         // bits of the largest |activation| >= 2^15 the staging met (0: none)
 };
 
@@ -51,6 +52,8 @@ __device__ __forceinline__ void iq2_fill_lds(Iq2Lds &t, const uint32_t *grid) {
     if (threadIdx.x < 16) {
         const uint32_t s = threadIdx.x;
         t.smask[s] = make_uint2((s & 1u) << 15 | ((s >> 1) & 1u) << 31, ((s >> 2) & 1u) << 15 | ((s >> 3) & 1u) << 31);
+        const _Float16 c = (_Float16)(float)(2u * s + 1u);
+        t.cf2[s] = __builtin_bit_cast(uint32_t, (f16x2){c, c});
     }
     if (threadIdx.x == 0) t.amax = 0u;
 }
@@ -138,14 +141,13 @@ __device__ __forceinline__ void iq2m_accum(const Iq2Table &tb, int e, int row0, 
                 const uint32_t sb = (u4c(rs[j], r) >> qsh) & 255u;
                 const uint4 g = L.level[idx];
                 const uint2 m0 = L.smask[sb & 15u], m1 = L.smask[sb >> 4];
-                // the lane's scale group's odd factor 2 sc + 1 as an f16 pair
-                const float cf = (float)(2u * ((u4c(sc_c, r) >> (8 * j + scsh)) & 15u) + 1u);
-                const f16x2 c2 = {(_Float16)cf, (_Float16)cf};
-                const f16x2 w0 = __builtin_bit_cast(f16x2, g.x | m0.x) * c2;
-                const f16x2 w1 = __builtin_bit_cast(f16x2, g.y | m0.y) * c2;
-                const f16x2 w2 = __builtin_bit_cast(f16x2, g.z | m1.x) * c2;
-                const f16x2 w3 = __builtin_bit_cast(f16x2, g.w | m1.y) * c2;
-                const f16x8 wb = {w0[0], w0[1], w1[0], w1[1], w2[0], w2[1], w3[0], w3[1]};
+                // the lane's scale group's odd factor 2 sc + 1 as an f16 pair (a table: no conversions)
+                const f16x2 c2 = __builtin_bit_cast(f16x2, L.cf2[(u4c(sc_c, r) >> (8 * j + scsh)) & 15u]);
+                const uint4 wu = make_uint4(__builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, g.x | m0.x) * c2),
+                                            __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, g.y | m0.y) * c2),
+                                            __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, g.z | m1.x) * c2),
+                                            __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, g.w | m1.y) * c2));
+                const f16x8 wb = __builtin_bit_cast(f16x8, wu);
                 ph[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a0), wb, ph[r], 0, 0, 0);
                 if (TWO) ph[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, b0), wb, ph[r], 0, 0, 0);
             }
