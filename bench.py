@@ -501,7 +501,8 @@ def bench_route(torch, pkg, gen, args):
 
 def bench_int8(torch, pkg, gen, args):
     """Config: the int8 dense projections at batch 8 (Q, K, V, O 6144x6144; the shared expert's MLP 6144 -> 2048 ->
-    6144), per-output-channel scales (the shared down: per-input-row, its row-parallel form), bf16 activations.  A
+    6144), per-output-channel scales (the shared down: per-input-row, its row-parallel form), bf16 activations,
+    weights in the tiled layout (MI355MOE_I8_ROWS=1: the row-major qT, for comparison).  A
     step is the layer's three dependent stages -- Q/K/V of the attention input in one launch, O, and the shared
     expert's mlp_partial (mi_int8_mlp: gate and up in one launch, SwiGLU, down) -- so projections that share their
     input share a launch, as they can in the model.  3 weight copies rotated (> the last-level cache)."""
@@ -510,7 +511,10 @@ def bench_int8(torch, pkg, gen, args):
     copies = 3
     fns = []
     total = sum(i * o + 4 * o for st in stages for i, o in st) + 3 * D * I + 4 * (2 * I + I)
-    mk_q = lambda n_out, n_in: torch.randint(-127, 128, (n_out, n_in), dtype=torch.int8, device="cuda", generator=gen)
+    # weights in the tiled layout (mi_int8_tile, repacked once at load as the IQ planes are)
+    tile = (lambda w: w) if os.environ.get("MI355MOE_I8_ROWS") == "1" else pkg.int8_tile
+    mk_q = lambda n_out, n_in: tile(torch.randint(-127, 128, (n_out, n_in), dtype=torch.int8, device="cuda",
+                                                  generator=gen))
     mk_s = lambda n: torch.rand((n,), device="cuda", generator=gen) * 1.5e-3 + 0.5e-3
     for c in range(copies):
         ops = []

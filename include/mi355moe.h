@@ -295,14 +295,25 @@ int mi_dequant(const mi_table *t, int32_t expert, float *out, void *stream);
  * 1 <= B <= 32, n_in % 256 == 0, n_out % 16 == 0.  The weights are dequantized to bf16 in registers and contracted
  * on the matrix cores (bf16 x bf16 products are exact, f32 accumulation).
  * The workspace holds split-K partials (no initialisation needed); a second launch sums them in order.
+ * scale_axis | MI_I8_TILED: qT is in the tiled layout that mi_int8_tile writes (same values, another byte order).
  */
 #define MI_I8_ROW_SCALES 0
 #define MI_I8_COL_SCALES 1
 #define MI_I8_COL_AFTER  2
+#define MI_I8_TILED      0x100
 int mi_int8_project(const uint16_t *x_bf16, int32_t B, const int8_t *qT, const float *s, int32_t scale_axis,
                     int32_t n_in, int32_t n_out, uint16_t *y_bf16, float *y_f32, void *workspace,
                     size_t workspace_bytes, void *stream);
 size_t mi_int8_project_workspace(int32_t B, int32_t n_in, int32_t n_out, int32_t scale_axis);
+
+/*
+ * The tiled layout of an int8 weight (no counterpart in the reference: a load-time repack, as the planar IQ tables
+ * are): qT [n_out, n_in] -> tiled, n_out * n_in bytes, per 16-row tile and 128-column block one 2 KB piece in the
+ * order the projection kernels load it (1 KB contiguous per wavefront load instead of 16 rows x 64 bytes at a
+ * stride of n_in).  n_out % 16 == 0, n_in % 256 == 0, both pointers 16-byte aligned.  Pass MI_I8_TILED in
+ * scale_axis (mi_int8_project, mi_int8_project_many; gu_scale_axis / down_scale_axis of mi_int8_mlp) with it.
+ */
+int mi_int8_tile(const int8_t *qT, int32_t n_out, int32_t n_in, int8_t *tiled, void *stream);
 
 /*
  * Several int8 projections of the same activations in one launch (Q, K, V of x; the shared expert's gate and up),

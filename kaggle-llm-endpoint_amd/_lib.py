@@ -22,6 +22,7 @@ MAX_DECODE_TOKENS = 16
 MI_I8_ROW_SCALES = 0         # s [n_in]: the reference's per-row scales [in, 1]
 MI_I8_COL_SCALES = 1         # s [n_out]: per-column scales [1, out]
 MI_I8_COL_AFTER = 2          # s [n_out] applied after the dot (the int8 lm_head)
+MI_I8_TILED = 0x100          # OR'ed into scale_axis: qT in the tiled layout of mi_int8_tile
 MI_COMBINE_MATMUL = 0
 MI_COMBINE_GATHER = 1
 MI_COMBINE_SWEEP = 2         # the dense sweep's rounding points (sweep_mode="dense")
@@ -43,7 +44,7 @@ EXPORTS = ("mi_matvec", "mi_matvec_workspace", "mi_moe_decode", "mi_moe_decode_f
            "mi_moe_decode_workspace", "mi_moe_decode_plan", "mi_moe_decode_noalloc", "mi_moe_decode_x",
            "mi_ragged_plan", "mi_moe_prefill", "mi_moe_prefill_workspace", "mi_moe_prefill_form",
            "mi_moe_prefill_form_workspace", "mi_dequant", "mi_int8_project", "mi_int8_project_workspace", "mi_int8_project_many",
-           "mi_int8_project_many_workspace", "mi_int8_mlp", "mi_int8_mlp_workspace", "mi_moe_route", "mi_moe_route_workspace", "mi_pack_planes", "mi_read_probe",
+           "mi_int8_project_many_workspace", "mi_int8_mlp", "mi_int8_mlp_workspace", "mi_moe_route", "mi_moe_route_workspace", "mi_pack_planes", "mi_read_probe", "mi_int8_tile",
            "mi_strerror",
            "mi_version")
 
@@ -94,6 +95,7 @@ def lib():
         "mi_moe_prefill_form": (I, [T, T, T, P, I, I, P, P, I, F, I, I, P, P, P, Z, P]),
         "mi_moe_prefill_form_workspace": (Z, [T, T, I, I, I, I]),
         "mi_read_probe": (I, [P, Z, P, I, P]),
+        "mi_int8_tile": (I, [P, I, I, P, P]),
         "mi_int8_mlp": (I, [P, I, I, I, P, P, P, P, I, P, P, I, F, P, P, P, Z, P]),
         "mi_int8_mlp_workspace": (Z, [I, I, I, I, I]),
         "mi_dequant": (I, [T, I, P, P]),

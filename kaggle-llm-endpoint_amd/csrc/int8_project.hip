@@ -16,6 +16,8 @@
 
 #include <stdlib.h>
 
+#include <algorithm>
+
 namespace mi {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -37,6 +39,7 @@ struct I8Args {
     const uint16_t *x;     // bf16 [B, n_in], shared by every projection
     int B, n_in, S;
     int scale_axis;        // MI_I8_*: one per launch
+    int tiled;             // qT in the tiled layout (mi_int8_tile): 2 KB per (16-row tile, 128-column block)
     int blocks;            // 128-column blocks per split
     int n_proj;
     int wg_start[kI8MaxProj + 1];   // first workgroup of each projection
@@ -47,8 +50,8 @@ struct I8Args {
 };
 
 constexpr int kI8Waves = 4;
-constexpr int kBufWord3 = 0x00020000;   // gfx9 buffer descriptor word 3 (32-bit data format)
 constexpr int kI8Ring = 4;          // 128-column blocks in flight per wavefront (2 KB each)
+constexpr int kBufWord3 = 0x00020000;   // gfx9 buffer descriptor word 3 (32-bit data format)
 
 __device__ __forceinline__ uint32_t bf16_pair(float a, float b) {
     const bf16x2 v = {(__bf16)a, (__bf16)b};
@@ -95,14 +98,19 @@ __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
 
     // weights: lane's 32 bytes of block p at row o0 + i, columns k0 + 128 p + 32 q, as buffer loads from the
     // wavefront's tile (blocks past the split use an empty-range descriptor: zeros, no memory traffic)
-    const int8_t *tile = P.q + (size_t)(active ? o0 : 0) * a.n_in + k0;
+    // row layout: row o0 + i at n_in bytes per row, block p at +128 p, the lane's two 16-byte halves 16 apart;
+    // tiled layout: the wavefront's 16-row tile holds each 128-column block as 2 KB, the lane's halves at lane * 16
+    // and 1024 + lane * 16: every load instruction reads 1 KB of contiguous memory
+    const int8_t *tile = a.tiled ? P.q + ((size_t)(active ? o0 / 16 : 0) * (a.n_in / 128) + k0 / 128) * 2048
+                                 : P.q + (size_t)(active ? o0 : 0) * a.n_in + k0;
+    const int bstride = a.tiled ? 2048 : 128, hoff = a.tiled ? 1024 : 16;
     const __amdgpu_buffer_rsrc_t qb = __builtin_amdgcn_make_buffer_rsrc((void *)tile, (short)0, 0x7fffffff, kBufWord3);
     const __amdgpu_buffer_rsrc_t qnull = __builtin_amdgcn_make_buffer_rsrc((void *)tile, (short)0, 0, kBufWord3);
-    const int voff = i * a.n_in + 32 * q;
+    const int voff = a.tiled ? 16 * lane : i * a.n_in + 32 * q;
     auto load_block = [&](int p, uint4 &lo, uint4 &hi) {
         const __amdgpu_buffer_rsrc_t r = p < a.blocks ? qb : qnull;
-        lo = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 128 * p, 0));
-        hi = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16, 128 * p, 0));
+        lo = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, bstride * p, 0));
+        hi = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff + hoff, bstride * p, 0));
     };
     uint4 ring[kI8Ring][2];
     if (active) {
@@ -254,6 +262,23 @@ __global__ void __launch_bounds__(256) swiglu_pair_i8(I8Args a) {
     ((uint2 *)a.h)[i] = b;
 }
 
+// The tiled layout of qT [n_out, n_in]: per 16-row tile t and 128-column block b, 2 KB = two halves of 64 lanes x
+// 16 bytes, lane l = i + 16 q of half h holding row 16 t + i, columns 128 b + 32 q + 16 h .. + 15 -- what lane l of
+// the projection kernel loads for block b, so each load instruction reads 1 KB of contiguous memory.  One thread per
+// 16 bytes.
+__global__ void __launch_bounds__(256) int8_tile_kernel(const int8_t *__restrict__ qT, int n_out, int n_in,
+                                                        int8_t *__restrict__ out) {
+    const int nblk = n_in / 128;
+    const size_t n16 = (size_t)n_out * n_in / 16;
+    for (size_t d = (size_t)blockIdx.x * blockDim.x + threadIdx.x; d < n16; d += (size_t)gridDim.x * blockDim.x) {
+        const int l = (int)(d & 63), h = (int)((d >> 6) & 1);
+        const size_t tb = d >> 7, t = tb / nblk;
+        const int b = (int)(tb - t * nblk);
+        const size_t row = 16 * t + (l & 15), col = 128 * (size_t)b + 32 * (l >> 4) + 16 * h;
+        *(uint4 *)(out + 16 * d) = *(const uint4 *)(qT + row * n_in + col);
+    }
+}
+
 // LDS bytes per staged column: B bf16 activations (+ one f32 scale with per-input-row scales).
 static size_t i8_col_bytes(int B, int scale_axis) { return 2 * (size_t)B + (scale_axis == MI_I8_ROW_SCALES ? 4 : 0); }
 
@@ -286,6 +311,7 @@ static int i8_tiles(const int32_t *n_out, int n_proj) {
 // Workspace bytes of one launch: the f32 split partials (none with one split, except for an MLP's gate/up pair,
 // whose SwiGLU reads them).
 static size_t i8_part_bytes(int B, int n_in, const int32_t *n_out, int n_proj, int scale_axis, int pair) {
+    scale_axis &= ~MI_I8_TILED;
     size_t total = 0;
     for (int j = 0; j < n_proj; ++j) total += (size_t)n_out[j];
     const int S = i8_splits(B, n_in, i8_tiles(n_out, n_proj), scale_axis);
@@ -306,6 +332,8 @@ static int i8_launch(const uint16_t *x_bf16, int32_t B, int32_t n_in, const mi_i
     if (!x_bf16 || !projs) return MI_ERR_NULL;
     if (B <= 0 || B > 32) return MI_ERR_TOKENS;
     if (n_proj <= 0 || n_proj > kI8MaxProj || (pair && n_proj != 2)) return MI_ERR_ARG;
+    const int tiled = (scale_axis & MI_I8_TILED) != 0;
+    scale_axis &= ~MI_I8_TILED;
     if (scale_axis < MI_I8_ROW_SCALES || scale_axis > MI_I8_COL_AFTER) return MI_ERR_ARG;
     if (n_in <= 0 || n_in % 256) return MI_ERR_SHAPE;
     int32_t n_out[kI8MaxProj];
@@ -326,6 +354,7 @@ static int i8_launch(const uint16_t *x_bf16, int32_t B, int32_t n_in, const mi_i
     a.n_in = n_in;
     a.S = i8_splits(B, n_in, i8_tiles(n_out, n_proj), scale_axis);
     a.scale_axis = scale_axis;
+    a.tiled = tiled;
     a.blocks = n_in / 128 / a.S;
     a.n_proj = n_proj;
     size_t off = 0;
@@ -369,6 +398,7 @@ extern "C" {
 size_t mi_int8_project_many_workspace(int32_t B, int32_t n_in, const int32_t *n_out, int32_t n_proj,
                                       int32_t scale_axis) {
     if (B <= 0 || B > 32 || n_in <= 0 || n_in % 256 || !n_out || n_proj <= 0 || n_proj > kI8MaxProj) return 0;
+    scale_axis &= ~MI_I8_TILED;
     if (scale_axis < MI_I8_ROW_SCALES || scale_axis > MI_I8_COL_AFTER) return 0;
     for (int j = 0; j < n_proj; ++j)
         if (n_out[j] <= 0 || n_out[j] % 16) return 0;
@@ -379,6 +409,16 @@ int mi_int8_project_many(const uint16_t *x_bf16, int32_t B, int32_t n_in, const 
                          int32_t scale_axis, void *workspace, size_t workspace_bytes, void *stream) {
     return i8_launch(x_bf16, B, n_in, projs, n_proj, scale_axis, workspace, workspace_bytes, stream, 0, 0.0f,
                      nullptr);
+}
+
+int mi_int8_tile(const int8_t *qT, int32_t n_out, int32_t n_in, int8_t *tiled, void *stream) {
+    if (!qT || !tiled) return MI_ERR_NULL;
+    if (n_out <= 0 || n_in <= 0 || n_out % 16 || n_in % 256) return MI_ERR_SHAPE;
+    if ((uintptr_t)qT % 16 || (uintptr_t)tiled % 16) return MI_ERR_ARG;
+    const size_t n16 = (size_t)n_out * n_in / 16;
+    const unsigned grid = (unsigned)std::min<size_t>((n16 + 255) / 256, 8192);
+    hipLaunchKernelGGL(int8_tile_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, qT, n_out, n_in, tiled);
+    return hipGetLastError() == hipSuccess ? MI_OK : MI_ERR_LAUNCH;
 }
 
 size_t mi_int8_project_workspace(int32_t B, int32_t n_in, int32_t n_out, int32_t scale_axis) {
@@ -397,6 +437,8 @@ int mi_int8_project(const uint16_t *x_bf16, int32_t B, const int8_t *qT, const f
 
 size_t mi_int8_mlp_workspace(int32_t B, int32_t D, int32_t I, int32_t gu_scale_axis, int32_t down_scale_axis) {
     if (B <= 0 || B > 32 || D <= 0 || I <= 0 || D % 256 || I % 256) return 0;
+    gu_scale_axis &= ~MI_I8_TILED;
+    down_scale_axis &= ~MI_I8_TILED;
     if (gu_scale_axis != MI_I8_ROW_SCALES && gu_scale_axis != MI_I8_COL_SCALES) return 0;
     if (down_scale_axis != MI_I8_ROW_SCALES && down_scale_axis != MI_I8_COL_SCALES) return 0;
     const int32_t gu[2] = {I, I};

@@ -488,13 +488,35 @@ def _scale_len(scale_axis, n_in, n_out):
     return n_in if scale_axis == _lib.MI_I8_ROW_SCALES else n_out
 
 
+def int8_tile(qT):
+    """qT int8 [n_out, n_in] (device) -> the same weights in the tiled layout of mi_int8_tile, int8
+    [n_out / 16, n_in / 128, 2048]: per 16-row tile and 128-column block the 2 KB the projection kernels load, 1 KB
+    of contiguous memory per wavefront load.  The int8 entry points take either form (a 3-d weight is a tiled one)."""
+    n_out, n_in = qT.shape
+    if n_out % 16 or n_in % 256:
+        raise ValueError("int8_tile: n_out must be a multiple of 16 and n_in of 256 (got %d x %d)" % (n_out, n_in))
+    qT = qT.contiguous()
+    out = torch.empty((n_out // 16, n_in // 128, 2048), dtype=torch.int8, device=qT.device)
+    check("mi_int8_tile", lib().mi_int8_tile(_ptr(qT), n_out, n_in, _ptr(out), _stream()))
+    return out
+
+
+def _i8_dims(qT):
+    """(n_out, n_in, layout bit) of a weight in either layout (3-d: tiled)."""
+    if qT.dim() == 3:
+        return qT.shape[0] * 16, qT.shape[1] * 128, _lib.MI_I8_TILED
+    return qT.shape[0], qT.shape[1], 0
+
+
 def int8_project(x, qT, s, want_f32=False, y_bf16=None, y_f32=None, workspace=None, scale_axis=_lib.MI_I8_COL_SCALES):
     """y = x @ bf16(f32(q) * s) (quant8.py:91-99): x bf16 [B, n_in], qT int8 [n_out, n_in], s f32 [n_out]
     (``scale_axis`` MI_I8_COL_SCALES, the reference's [1, out]) or [n_in] (MI_I8_ROW_SCALES, its [in, 1]);
     MI_I8_COL_AFTER: y = (x @ f32(q)) * s[o], the int8 lm_head (engine.py:345-351).
     Preallocated outputs / workspace make the call allocation-free."""
     B, n_in = x.shape
-    n_out = qT.shape[0]
+    n_out, w_in, tiled = _i8_dims(qT)
+    if w_in != n_in:
+        raise ValueError("int8_project: x has %d columns, the weight %d" % (n_in, w_in))
     if s.numel() != _scale_len(scale_axis, n_in, n_out):
         raise ValueError("int8_project: %d scales for scale_axis %d" % (s.numel(), scale_axis))
     x = x.contiguous()
@@ -505,8 +527,8 @@ def int8_project(x, qT, s, want_f32=False, y_bf16=None, y_f32=None, workspace=No
     if nbytes == 0:
         raise ValueError("mi_int8_project: unsupported shape B=%d n_in=%d n_out=%d" % (B, n_in, n_out))
     ws = workspace if workspace is not None else WORKSPACES.get("int8", nbytes)
-    check("mi_int8_project", lib().mi_int8_project(_ptr(x), B, _ptr(qT), _ptr(s), int(scale_axis), n_in, n_out,
-                                                   _ptr(yb), _ptr(yf), _ptr(ws), ws.numel(), _stream()))
+    check("mi_int8_project", lib().mi_int8_project(_ptr(x), B, _ptr(qT), _ptr(s), int(scale_axis) | tiled, n_in,
+                                                   n_out, _ptr(yb), _ptr(yf), _ptr(ws), ws.numel(), _stream()))
     return (yb, yf) if want_f32 else yb
 
 
@@ -535,13 +557,18 @@ def int8_project_many(x, projections, want_f32=False, outputs=None, workspace=No
     B, n_in = x.shape
     x = x.contiguous()
     n = len(projections)
-    for qT, s in projections:
-        if s.numel() != _scale_len(scale_axis, n_in, qT.shape[0]):
+    dims = [_i8_dims(qT) for qT, _ in projections]
+    if len({d[2] for d in dims}) != 1:
+        raise ValueError("int8_project_many: the projections of one launch share one weight layout")
+    for (qT, s), (n_out, w_in, _) in zip(projections, dims):
+        if w_in != n_in:
+            raise ValueError("int8_project_many: x has %d columns, a weight %d" % (n_in, w_in))
+        if s.numel() != _scale_len(scale_axis, n_in, n_out):
             raise ValueError("int8_project_many: %d scales for scale_axis %d" % (s.numel(), scale_axis))
     arr = (_lib.MiI8Proj * n)()
     outs = []
     for j, (qT, s) in enumerate(projections):
-        n_out = qT.shape[0]
+        n_out = dims[j][0]
         if outputs is not None:
             yb, yf = outputs[j]
         else:
@@ -549,13 +576,13 @@ def int8_project_many(x, projections, want_f32=False, outputs=None, workspace=No
             yf = torch.empty((B, n_out), dtype=torch.float32, device=x.device) if want_f32 else None
         arr[j] = _lib.MiI8Proj(qT.data_ptr(), s.data_ptr(), n_out, _ptr(yb), _ptr(yf))
         outs.append((yb, yf) if want_f32 else yb)
-    n_outs = (ctypes.c_int32 * n)(*[int(qT.shape[0]) for qT, _ in projections])
+    n_outs = (ctypes.c_int32 * n)(*[int(d[0]) for d in dims])
     nbytes = lib().mi_int8_project_many_workspace(B, n_in, n_outs, n, int(scale_axis))
     if nbytes == 0:
         raise ValueError("mi_int8_project_many: unsupported shapes (B=%d, n_in=%d, n_proj=%d)" % (B, n_in, n))
     ws = workspace if workspace is not None else WORKSPACES.get("int8", nbytes)
-    check("mi_int8_project_many", lib().mi_int8_project_many(_ptr(x), B, n_in, arr, n, int(scale_axis), _ptr(ws),
-                                                             ws.numel(), _stream()))
+    check("mi_int8_project_many", lib().mi_int8_project_many(_ptr(x), B, n_in, arr, n, int(scale_axis) | dims[0][2],
+                                                             _ptr(ws), ws.numel(), _stream()))
     return outs
 
 
@@ -568,8 +595,10 @@ def int8_mlp(x, gate, up, down, limit, want_f32=False, y_bf16=None, y_f32=None, 
     g, u, d = [int8_leaf(l, x.device) if isinstance(l, dict) else l for l in (gate, up, down)]
     if g[2] != u[2]:
         raise ValueError("int8_mlp: gate and up take one scale form")
+    (I, gd, gt), (_, _, ut), (_, _, dt) = _i8_dims(g[0]), _i8_dims(u[0]), _i8_dims(d[0])
+    if gt != ut:
+        raise ValueError("int8_mlp: gate and up take one weight layout")
     B, D = x.shape
-    I = g[0].shape[0]
     x = x.contiguous()
     yb = y_bf16 if y_bf16 is not None else torch.empty((B, D), dtype=torch.bfloat16, device=x.device)
     yf = y_f32 if y_f32 is not None else (
@@ -581,7 +610,7 @@ def int8_mlp(x, gate, up, down, limit, want_f32=False, y_bf16=None, y_f32=None, 
             raise ValueError("mi_int8_mlp: unsupported shape B=%d D=%d I=%d" % (n, D, I))
         ws = workspace if workspace is not None else WORKSPACES.get("int8", nbytes)
         check("mi_int8_mlp", lib().mi_int8_mlp(_ptr(x[b0:b0 + n]), n, D, I, _ptr(g[0]), _ptr(g[1]), _ptr(u[0]),
-                                               _ptr(u[1]), int(g[2]), _ptr(d[0]), _ptr(d[1]), int(d[2]),
+                                               _ptr(u[1]), int(g[2]) | gt, _ptr(d[0]), _ptr(d[1]), int(d[2]) | dt,
                                                float(limit), _ptr(yb[b0:b0 + n]),
                                                _ptr(yf[b0:b0 + n]) if yf is not None else None, _ptr(ws),
                                                ws.numel(), _stream()))
