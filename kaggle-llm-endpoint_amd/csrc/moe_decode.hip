@@ -968,11 +968,12 @@ static int decode_launch(const DecodePlan &p, const mi_table *gate, const mi_tab
     // phase 2: h = SwiGLU(sum of the phase-1 partials) [NS, I]; down -> split partials [S2, NS, D]; the
     // routing-weighted combine (+ shared expert) -> out [N, D].  Stream order publishes each launch's results.
     uint16_t *h_hi = (uint16_t *)(ws + p.off_h), *h_lo = h_hi + (size_t)p.NS * gate->rows;
-    // MI355MOE_FUSE_SWIGLU=1 (one workgroup per task only): the down launch forms h itself while staging its rows
-    // (the SwiGLU launch's arithmetic, from the gate/up partials) instead of a SwiGLU launch.  Measured slower (the
-    // down staging waits for the split partials: +2.5 us on the down launch at batch 1, +14 us per layer at batch 8),
-    // so the SwiGLU launch is the default.
-    const bool fuse_h = !cb3 && !p.cu && !p.cum && env_int("MI355MOE_FUSE_SWIGLU", 0) == 1;
+    // One workgroup per task (the grouped launches): at one token the down launch forms h itself while staging its
+    // rows (the SwiGLU launch's arithmetic, from the gate/up partials) instead of a SwiGLU launch: the down launch
+    // waits ~2.5 us longer for the split partials, the layer is 0.4-1.0 us faster (IQ2_S + IQ4_XS, IQ3_S, IQ4_XS).
+    // At 8 tokens that wait costs 8-18 us per layer, so the SwiGLU launch stays.  MI355MOE_FUSE_SWIGLU=0 / 1
+    // forces either (measurement).
+    const bool fuse_h = !cb3 && !p.cu && !p.cum && env_int("MI355MOE_FUSE_SWIGLU", N == 1 ? 1 : 0) == 1;
     // the CU-balanced down launch forms h itself while staging (bit-identical h, one launch fewer: ~2 us at one token;
     // MI355MOE_CU_FORM_H=0 keeps the SwiGLU launch, for measurement)
     const bool cu_form = p.cu && env_int("MI355MOE_CU_FORM_H", 1) != 0 && p.s1.sp.S <= 2 &&
