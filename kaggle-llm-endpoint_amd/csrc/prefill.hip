@@ -187,7 +187,7 @@ __global__ void __launch_bounds__(kPlanThreads) ragged_plan_kernel(const int32_t
     __syncthreads();
     const int n_blocks = bend[kPlanMaxE - 1];
     if (tid == 0) *p.n_blocks = n_blocks;
-    __builtin_amdgcn_s_waitcnt(0x0F70);        // vmcnt(0): this wavefront's padding stores are done ...
+    vm_wait<0>();                              // this wavefront's padding stores are done ...
     __syncthreads();                            // ... and every other wavefront's
 
     // pass 2: rows (the loads of pass 1 are still in registers when one batch held every step)
