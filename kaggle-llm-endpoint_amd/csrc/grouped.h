@@ -179,6 +179,9 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
                                       typename std::conditional<(QT == MI_QT_Q2_K || QT == MI_QT_Q3_K), KqLds,
                                                                 char>::type>::type>::type>::type iq;
     __shared__ uint4 cbl[QT == MI_QT_CB3 ? kWgWaves * 5 * 64 : 1];   // CB3: per-wavefront codebook slots
+    // IQ4_XS at one token: the plane words stream through per-wavefront LDS rings (iq4m_accum_lds)
+    constexpr bool kIq4Lds = QT == MI_QT_IQ4_XS && TCMAX == 1;
+    __shared__ uint4 iq4ring[kIq4Lds ? kWgWaves * kIq4RingUint4 : 1];
     __shared__ int s_tok[kMaxT];
 
     constexpr bool cb3 = QT == MI_QT_CB3;
@@ -379,12 +382,13 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
             iq2m_run_and_store<false, TCMAX>(tb.iq2, e, rg * WR, u0, u1, c0, iq, xh, xl, xsp, a.t_rows, n, s_tok,
                                              part_base, a.R, stage);
     } else {
+        uint4 *ring = iq4ring + wave * kIq4RingUint4;
         if (hilo)
-            iq4m_run_and_store<true, TCMAX>(tb.iq4, e, rg * WR, u0, u1, c0, iq, xh, xl, xsp, a.t_rows, n, s_tok,
-                                            part_base, a.R, stage);
+            iq4m_run_and_store<true, TCMAX, kIq4Lds>(tb.iq4, e, rg * WR, u0, u1, c0, iq, xh, xl, xsp, a.t_rows, n,
+                                                     s_tok, part_base, a.R, stage, ring);
         else
-            iq4m_run_and_store<false, TCMAX>(tb.iq4, e, rg * WR, u0, u1, c0, iq, xh, xl, xsp, a.t_rows, n, s_tok,
-                                             part_base, a.R, stage);
+            iq4m_run_and_store<false, TCMAX, kIq4Lds>(tb.iq4, e, rg * WR, u0, u1, c0, iq, xh, xl, xsp, a.t_rows, n,
+                                                      s_tok, part_base, a.R, stage, ring);
     }
     // The partials are reduced by the next launch (gate/up: the SwiGLU kernel; down: the combine; matvec: the split
     // reduction): kernel order publishes them, so no completion counters or fences are needed.
