@@ -31,6 +31,8 @@ struct PlanOut {
     int32_t *blk_n;        // [G]   rows of every block that are not padding (NULL: not written)
     int merge_dups;        // w_row of the first slot of a token's expert = the sum of that token's weights of the
                            // expert in column order, 0 for its later slots (the sweeps' summed routing weight)
+    uint32_t *cnt;         // [n_cnt] the grouped GEMMs' split-task counters, zeroed here (NULL: none)
+    int n_cnt;
 };
 
 // Slot s of the plan: token s / kk, column j = s % kk; columns j < k are the routed slots, column k (kk = k + 1) is
@@ -187,6 +189,7 @@ __global__ void __launch_bounds__(kPlanThreads) ragged_plan_kernel(const int32_t
     __syncthreads();
     const int n_blocks = bend[kPlanMaxE - 1];
     if (tid == 0) *p.n_blocks = n_blocks;
+    for (int i = tid; i < p.n_cnt; i += kPlanThreads) p.cnt[i] = 0u;
     vm_wait<0>();                              // this wavefront's padding stores are done ...
     __syncthreads();                            // ... and every other wavefront's
 
@@ -376,10 +379,24 @@ __global__ void __launch_bounds__(256) prefill_combine_f32(const float *__restri
 }
 
 struct PfLayout {
-    int S, G;
+    int S, G, P;
     long long Rp;
-    size_t off_be, off_nb, off_bn, off_tr, off_wr, off_rs, off_h, off_y, total;
+    size_t off_be, off_nb, off_bn, off_tr, off_wr, off_rs, off_h, off_y, off_part, off_cnt, total;
 };
+
+// Workgroups of a grouped GEMM launch resident at once: 2 per CU (the 77 KB of LDS and <= 256 VGPRs per wavefront
+// of prefill_kernel).  The launches split their last round's tasks by it (prefill_gemm.h).
+static int pf_slots() {
+    static int slots = 0;
+    if (!slots) {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+        slots = 2 * cus;
+    }
+    return slots;
+}
 
 static size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
 
@@ -400,6 +417,9 @@ static PfLayout pf_layout(int T, int kk, int E, int I, int D, bool y32) {
     L.off_rs = o; o = al256(o + 4 * (size_t)L.S);
     L.off_h = o; o = al256(o + 2 * (size_t)L.Rp * I);
     L.off_y = o; o = al256(o + (y32 ? 4 : 2) * (size_t)L.Rp * D);
+    L.P = pf_slots();
+    L.off_part = o; o = al256(o + (size_t)L.P * kPfPartBytes);
+    L.off_cnt = o; o = al256(o + 4 * (size_t)L.P);
     L.total = o;
     return L;
 }
@@ -527,7 +547,7 @@ int mi_ragged_plan(const int32_t *idx, const float *w, int32_t T, int32_t k, int
     if (T <= 0 || k <= 0) return MI_ERR_TOKENS;
     if (E <= 0 || E > kPlanMaxE || tm <= 0 || tm > 65536) return MI_ERR_ARG;
     if (!plan_sizes_ok(T, k, E, tm)) return MI_ERR_TOKENS;
-    PlanOut p{blk_expert, n_blocks, tok_row, w_row, row_slot, nullptr};
+    PlanOut p{blk_expert, n_blocks, tok_row, w_row, row_slot, nullptr, 0, nullptr, 0};
     return launch_plan(idx, w, T, k, -1, E, tm, p, (hipStream_t)stream);
 }
 
@@ -582,6 +602,8 @@ int mi_moe_prefill_form(const mi_table *gate, const mi_table *up, const mi_table
     p.w_row = (float *)(ws + L.off_wr);
     p.row_slot = (int32_t *)(ws + L.off_rs);
     p.merge_dups = y32;
+    p.cnt = (uint32_t *)(ws + L.off_cnt);
+    p.n_cnt = L.P;
     uint16_t *h = (uint16_t *)(ws + L.off_h), *y = (uint16_t *)(ws + L.off_y);
     if ((st = launch_plan(idx, w, T, k, shared_expert, E, kPfTm, p, s))) return st;
 
@@ -616,9 +638,13 @@ int mi_moe_prefill_form(const mi_table *gate, const mi_table *up, const mi_table
     a.wg_rows = 2;
     a.RBG = I / 128;
     a.w_row = p.w_row;
-    const int g8 = (L.G + kXcds - 1) / kXcds * kXcds;       // blocks rounded up to whole XCD rounds
+    a.P = L.P;
+    a.part = (float *)(ws + L.off_part);
+    a.cnt = p.cnt;
+    // blocks rounded up to whole XCD rounds, then the split tasks' pieces (at most P)
+    const int g8 = (L.G + kXcds - 1) / kXcds * kXcds;
     const bool round_gu = combine == MI_COMBINE_XLA_GATHER || combine == MI_COMBINE_XLA_SWEEP;
-    const dim3 ggu(g8 * a.RBG);
+    const dim3 ggu(g8 * a.RBG + L.P);
     if ((st = y32 ? (round_gu ? launch_prefill_0_3(gate->qtype, ggu, s, a) : launch_prefill_0_2(gate->qtype, ggu, s, a))
                   : (round_gu ? launch_prefill_0_1(gate->qtype, ggu, s, a) : launch_prefill_0_0(gate->qtype, ggu, s, a))))
         return st;
@@ -638,7 +664,7 @@ int mi_moe_prefill_form(const mi_table *gate, const mi_table *up, const mi_table
     b.wg_rows = 4;
     b.RBG = D / 256;
     b.out32 = (float *)y;
-    const dim3 gdn(g8 * b.RBG);
+    const dim3 gdn(g8 * b.RBG + L.P);
     if ((st = y32 ? launch_prefill_1_4(down->qtype, gdn, s, b) : launch_prefill_1_0(down->qtype, gdn, s, b))) return st;
 
     if (y32) {

@@ -58,7 +58,15 @@ struct PfArgs {
     int RBG;                               // workgroups per block
     const float *w_row;                    // gate/up with kPfScaleH: the plan's routing weight of every row
     float *out32;                          // down with kPfY32: y [Rp, R] in f32
+    int P;                                 // workgroups resident at once over the chip
+    float *part;                           // split tasks' piece sums: P x kPfPartBytes
+    uint32_t *cnt;                         // split tasks' piece counters: P, zero between launches
 };
+
+// A task of the launch's last, partial round is split along K into pieces (at most kPfMaxPieces, whole super tiles
+// each); a piece stores its accumulators here (kPfPartBytes per workgroup).
+constexpr int kPfMaxPieces = 4;
+constexpr int kPfPartBytes = kPfWaves * kPfRtw * kPfTT * 64 * 16;
 
 // Rounding forms of the epilogues (FORM, a compile-time set; the ragged kernels use none):
 constexpr int kPfRoundGU = 1;   // gate/up: g and u rounded to bf16 before the SwiGLU (the XLA einsums' bf16 outputs)
@@ -155,26 +163,30 @@ struct PfShared {
     uint32_t xs[2][kPfTm * kPfXPitch];           // column tiles ct (even/odd) of the block's rows, double-buffered;
                                                  // gate/up epilogue: the gate accumulators of one (gate, up) pair
     uint32_t xrowoff[kPfTm];                     // byte offset of every row's activations, or kXOut
+    int last;                                    // split task: this workgroup's piece arrived last
 };
 
 // ------------------------------------------------------------------------------------------------ weight providers
 // A provider streams the weights of one wavefront's 64 rows (4 row tiles) of expert e, one column tile at a time, and
 // runs the tile's k-steps on the matrix cores against the staged activations.  Its state is two values the workgroup
 // body keeps as locals: Wave (addressing, fixed per wavefront) and Regs (the loads in flight).
-//   init(w, s, a, sh, mat, e, rg, wave, lane)   set up w, issue the first column tiles' loads into s
+//   init(w, s, a, sh, mat, e, rg, wave, lane, st0, st1)   set up w for super tiles [st0, st1) (column tiles
+//                                               [4 st0, 4 st1)), issue the first column tiles' loads into s
 //   n_tiles(a, mat)                             column tiles of a row
 //   tile<NTT, C>(w, s, st, xt, acc)             column tile 4 st + C; xt = the staged tile at row jt, lane group q
 //   kCols, kQOff                                columns per tile; dwords between lane groups' activations in a step
+//   kSplit                                      whether the launch's last round of tasks is split into K pieces
 
 // CB3: 160-column tiles of the code-tile layout; codebook slots per 640-column super tile (cb3_tiles.h).
 struct PfCb3 {
     static constexpr int kCols = kCb3TileCols;
+    static constexpr bool kSplit = false;   // whole tasks only: K pieces measured slower (561 against 536 us)
     static constexpr int kQOff = 4;
     using Wave = Cb3Wave;
     using Regs = PfRegs;
     static __device__ __forceinline__ int n_tiles(const PfArgs &a, int mat) { return (mat ? a.t1 : a.t0).CT; }
     static __device__ __forceinline__ void init(Wave &w, Regs &s, const PfArgs &a, PfShared &sh, int mat, int e,
-                                                int rg, int wave, int lane) {
+                                                int rg, int wave, int lane, int st0, int st1) {
         const Cb3Table &tb = mat ? a.t1 : a.t0;
         const uint32_t *qt = tb.qs + (size_t)e * tb.CT * tb.RT * 256;
         const uint32_t *cbe = tb.cb + (size_t)e * tb.G * tb.R * 4;
@@ -186,10 +198,10 @@ struct PfCb3 {
         w.rt_bytes = (uint32_t)(rg * kPfRtw) * 1024u;
         w.g_bytes = (uint32_t)tb.R * 16u;
         w.row_bytes = (uint32_t)(rg * 64) * 16u;
-        w.cta = 0;
-        w.ctb = tb.CT;
-        w.g_first = 0;
-        w.g_last = tb.G - 1;
+        w.cta = 4 * st0;
+        w.ctb = min(tb.CT, 4 * st1);
+        w.g_first = 5 * st0;
+        w.g_last = min(tb.G, 5 * st1) - 1;
         w.lane16 = (uint32_t)lane * 16u;
         w.cblane16 = (uint32_t)lane * 16u;
         w.xh = w.xl = nullptr;
@@ -197,9 +209,9 @@ struct PfCb3 {
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
-            for (int r = 0; r < kPfRtw; ++r) s.ring[c][r] = cb3_tile(w, c, r);
+            for (int r = 0; r < kPfRtw; ++r) s.ring[c][r] = cb3_tile(w, 4 * st0 + c, r);
 #pragma unroll
-        for (int c = 0; c < 5; ++c) s.cbv[c] = cb3_group(w, c);
+        for (int c = 0; c < 5; ++c) s.cbv[c] = cb3_group(w, 5 * st0 + c);
     }
     template <int NTT, int C>
     static __device__ __forceinline__ void tile(const Wave &w, Regs &s, int st, const uint32_t *xt,
@@ -236,6 +248,7 @@ struct PfIq3Regs {
 };
 
 struct PfIq3 {
+    static constexpr bool kSplit = true;    // the last round's tasks split into K pieces
     static constexpr int kCols = kIq3TileCols;
     static constexpr int kQOff = 8;
     using Wave = PfIq3Wave;
@@ -255,7 +268,7 @@ struct PfIq3 {
         u[6] = *(const uint32_t *)(w.dd + (uint32_t)(ct >> 2) * P + o);
     }
     static __device__ __forceinline__ void init(Wave &w, Regs &s, const PfArgs &a, PfShared &sh, int mat, int e,
-                                                int rg, int wave, int lane) {
+                                                int rg, int wave, int lane, int st0, int st1) {
         const Iq3Table &tb = mat ? a.i1 : a.i0;
         const size_t R = (size_t)tb.R;
         w.qs = (const char *)(tb.qs + (size_t)e * tb.W * R);
@@ -266,14 +279,14 @@ struct PfIq3 {
         w.rpitch = 4u * (uint32_t)tb.R;
         w.q = lane >> 4;
         w.lrow = 4u * (uint32_t)(rg * 64 + (lane & 15));
-        w.CT = tb.K / kIq3TileCols;
+        w.CT = min(tb.K / kIq3TileCols, 4 * st1);          // prefetch no column tile past the range
         w.grid = sh.iq.grid;
         w.smask = sh.iq.smask;
         (void)wave;
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
-            for (int r = 0; r < kPfRtw; ++r) load(w, c, s.v[c][r], r);
+            for (int r = 0; r < kPfRtw; ++r) load(w, 4 * st0 + c, s.v[c][r], r);
     }
     // the 8 weights of step j of column tile ct for the row tile whose plane words are u
     static __device__ __forceinline__ bf16x8 weights8(const Wave &w, const uint32_t (&u)[7], int ct, int j) {
@@ -342,6 +355,7 @@ struct PfIq2Regs {
 };
 
 struct PfIq2 {
+    static constexpr bool kSplit = true;    // the last round's tasks split into K pieces
     static constexpr int kCols = 128;
     static constexpr int kQOff = 16;       // dwords: word q of the tile
     using Wave = PfIq2Wave;
@@ -356,7 +370,7 @@ struct PfIq2 {
         u[4] = *(const uint32_t *)(w.dd + (uint32_t)(ct >> 2) * P + o);
     }
     static __device__ __forceinline__ void init(Wave &w, Regs &s, const PfArgs &a, PfShared &sh, int mat, int e,
-                                                int rg, int wave, int lane) {
+                                                int rg, int wave, int lane, int st0, int st1) {
         const Iq2Table &tb = mat ? a.j1 : a.j0;
         const size_t R = (size_t)tb.R;
         w.qs = (const char *)(tb.qs + (size_t)e * tb.W * R);
@@ -367,14 +381,14 @@ struct PfIq2 {
         w.rpitch = 4u * (uint32_t)tb.R;
         w.q = lane >> 4;
         w.lrow = 4u * (uint32_t)(rg * 64 + (lane & 15));
-        w.CT = tb.K / 128;
+        w.CT = min(tb.K / 128, 4 * st1);                   // prefetch no column tile past the range
         w.level = sh.iq2.level;
         w.smask = sh.iq2.smask;
         (void)wave;
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
-            for (int r = 0; r < kPfRtw; ++r) load(w, c, s.v[c][r], r);
+            for (int r = 0; r < kPfRtw; ++r) load(w, 4 * st0 + c, s.v[c][r], r);
     }
     // the 8 weights of step j (group j of the lane's word) for the row tile whose plane words are u
     static __device__ __forceinline__ bf16x8 weights8(const Wave &w, const uint32_t (&u)[5], int ct, int j) {
@@ -438,6 +452,7 @@ struct PfKqRegs {
 
 template <bool Q3>
 struct PfKq {
+    static constexpr bool kSplit = true;    // the last round's tasks split into K pieces
     static constexpr int kCols = 128;
     static constexpr int kQOff = 4;        // dwords: columns 8q .. 8q+7 of a 32-column stripe
     using Wave = PfKqWave;
@@ -457,7 +472,7 @@ struct PfKq {
         }
     }
     static __device__ __forceinline__ void init(Wave &w, Regs &s, const PfArgs &a, PfShared &sh, int mat, int e,
-                                                int rg, int wave, int lane) {
+                                                int rg, int wave, int lane, int st0, int st1) {
         const KqTable &tb = mat ? a.q1 : a.q0;
         const size_t R = (size_t)tb.R;
         w.qs = (const char *)(tb.qs + (size_t)e * 16 * tb.nblk * R);
@@ -467,13 +482,13 @@ struct PfKq {
         w.rpitch = 4u * (uint32_t)tb.R;
         w.q = lane >> 4;
         w.lrow = 4u * (uint32_t)(rg * 64 + (lane & 15));
-        w.CT = tb.K / 128;
+        w.CT = min(tb.K / 128, 4 * st1);                   // prefetch no column tile past the range
         (void)sh;
         (void)wave;
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
-            for (int r = 0; r < kPfRtw; ++r) load(w, c, s.v[c][r], r);
+            for (int r = 0; r < kPfRtw; ++r) load(w, 4 * st0 + c, s.v[c][r], r);
     }
     // 4 weights from the 4 byte-sized values of t (each 0..3, Q3_K 0..7): f32 -> bf16 pairs
     static __device__ __forceinline__ uint2 four(uint32_t t, float m, float a) {
@@ -546,6 +561,7 @@ struct PfIq4Regs {
 };
 
 struct PfIq4 {
+    static constexpr bool kSplit = true;    // the last round's tasks split into K pieces
     static constexpr int kCols = 128;
     static constexpr int kQOff = 2;        // dwords: columns 4q .. 4q+3 of a 32-column group
     using Wave = PfIq4Wave;
@@ -560,7 +576,7 @@ struct PfIq4 {
         u[6] = *(const uint32_t *)(w.dd + (uint32_t)(ct >> 2) * P + o);
     }
     static __device__ __forceinline__ void init(Wave &w, Regs &s, const PfArgs &a, PfShared &sh, int mat, int e,
-                                                int rg, int wave, int lane) {
+                                                int rg, int wave, int lane, int st0, int st1) {
         const Iq4Table &tb = mat ? a.k1 : a.k0;
         const size_t R = (size_t)tb.R;
         w.qs = (const char *)(tb.qs + (size_t)e * tb.W * R);
@@ -570,13 +586,13 @@ struct PfIq4 {
         w.rpitch = 4u * (uint32_t)tb.R;
         w.q = lane >> 4;
         w.lrow = 4u * (uint32_t)(rg * 64 + (lane & 15));
-        w.CT = tb.K / 128;
+        w.CT = min(tb.K / 128, 4 * st1);                   // prefetch no column tile past the range
         w.pair = sh.iq4pair;
         (void)wave;
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
-            for (int r = 0; r < kPfRtw; ++r) load(w, c, s.v[c][r], r);
+            for (int r = 0; r < kPfRtw; ++r) load(w, 4 * st0 + c, s.v[c][r], r);
     }
     // the 8 weights of step j (sub-block 4 (ct % 2) + j) for the row tile whose plane words are u
     static __device__ __forceinline__ bf16x8 weights8(const Wave &w, const uint32_t (&u)[7], int ct, int j) {
@@ -626,8 +642,11 @@ struct PfIq4 {
 };
 
 // One workgroup: block g (expert e, rows row0 .. row0 + n - 1, NTT = ceil(n / 16) token tiles), row range rbg.
+// piece / np: the workgroup runs super tiles [piece n_st / np, (piece + 1) n_st / np) of the task (np == 1: all of
+// them); sti: the split task's index among the launch's split tasks (counter and piece sums).
 template <int MODE, int NTT, class WP, int FORM>
-__device__ __forceinline__ void prefill_body(const PfArgs &a, PfShared &sh, int g, int rbg, int e, int n) {
+__device__ __forceinline__ void prefill_body(const PfArgs &a, PfShared &sh, int g, int rbg, int e, int n, int piece,
+                                             int np, int sti) {
     uint32_t *xs = &sh.xs[0][0], *xrowoff = sh.xrowoff;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -635,9 +654,13 @@ __device__ __forceinline__ void prefill_body(const PfArgs &a, PfShared &sh, int 
     const int mat = MODE == 0 ? (wave & 1) : 0;
     const int rg = rbg * a.wg_rows + (MODE == 0 ? (wave >> 1) : wave);   // 64-row group of this wavefront
 
+    const int CT = WP::n_tiles(a, mat);
+    const int n_st = (CT + 3) >> 2;                     // super tiles of a row (the last one maybe partial)
+    const int s0 = WP::kSplit ? piece * n_st / np : 0, s1 = WP::kSplit ? (piece + 1) * n_st / np : n_st;
+    const int ct_end = min(CT, 4 * s1);
     typename WP::Wave w;
     typename WP::Regs s;
-    WP::init(w, s, a, sh, mat, e, rg, wave, lane);
+    WP::init(w, s, a, sh, mat, e, rg, wave, lane, s0, s1);
 
     // activation tile: the block's 16 NTT rows x kXU uint4 (WP::kCols columns), staged as buffer loads by
     // kXRows x kXU threads, kXRows rows per pass (thread t: row t / kXU + kXRows j, uint4 column t % kXU), so every
@@ -676,7 +699,7 @@ __device__ __forceinline__ void prefill_body(const PfArgs &a, PfShared &sh, int 
             if (stager && row < 16 * NTT) *(uint4 *)(xs + buf * kXBuf + row * kPfXPitch + 4 * xc8) = xr[j];
         }
     };
-    load_x(0);
+    load_x(4 * s0);
     store_x(0);
 
     f32x4 acc[kPfRtw][NTT];
@@ -686,7 +709,6 @@ __device__ __forceinline__ void prefill_body(const PfArgs &a, PfShared &sh, int 
         for (int t = 0; t < NTT; ++t) acc[r][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
     const int jt = lane & 15, q = lane >> 4;
     const uint32_t *xrow = xs + jt * kPfXPitch + WP::kQOff * q;
-    const int CT = WP::n_tiles(a, mat);
 
     // one barrier per column tile: tile ct sits in buffer ct & 1 (= C & 1); the next tile's loads are issued first
     // (ahead of this tile's code and codebook loads, so waiting for them never waits for those) and stored into the
@@ -695,22 +717,58 @@ __device__ __forceinline__ void prefill_body(const PfArgs &a, PfShared &sh, int 
         constexpr int C = decltype(Cc)::value;
         const int ct = 4 * st + C;
         __syncthreads();
-        if (ct + 1 < CT) load_x(ct + 1);
+        if (ct + 1 < ct_end) load_x(ct + 1);
         WP::template tile<NTT, C>(w, s, st, xrow + (C & 1) * kXBuf, acc);
-        if (ct + 1 < CT) store_x((C + 1) & 1);
+        if (ct + 1 < ct_end) store_x((C + 1) & 1);
     };
-    const int st_full = CT >> 2;
-    int st = 0;
+    const int st_full = min(CT >> 2, s1);
+    int st = s0;
     for (; st < st_full; ++st) {
         step(std::integral_constant<int, 0>{}, st);
         step(std::integral_constant<int, 1>{}, st);
         step(std::integral_constant<int, 2>{}, st);
         step(std::integral_constant<int, 3>{}, st);
     }
-    const int nct = CT - 4 * st;
+    const int nct = ct_end - 4 * st;                    // 0..3 column tiles of a last, partial super tile
     if (nct > 0) step(std::integral_constant<int, 0>{}, st);
     if (nct > 1) step(std::integral_constant<int, 1>{}, st);
     if (nct > 2) step(std::integral_constant<int, 2>{}, st);
+
+    if (WP::kSplit && np > 1) {
+        // a piece of a split task: its sums go to memory (stored through this XCD's L2), then the piece is counted;
+        // the piece that arrives last adds all of them in piece order (the same order whichever arrives last) and
+        // runs the epilogue.  Nothing waits for another workgroup.  The other pieces' sums are read with plain loads:
+        // each 128-byte line is written by one piece only and read once, after its count, so no L2 holds it.
+        const __amdgpu_buffer_rsrc_t pr =
+            __builtin_amdgcn_make_buffer_rsrc((void *)a.part, (short)0, 0x7fffffff, kBufferWord3);
+        const uint32_t lane_off = 16u * (uint32_t)lane;
+        auto piece_off = [&](int pc, int r, int t) {
+            return (uint32_t)(sti * np + pc) * (uint32_t)kPfPartBytes +
+                   (uint32_t)((wave * kPfRtw + r) * kPfTT + t) * 1024u + lane_off;
+        };
+#pragma unroll
+        for (int r = 0; r < kPfRtw; ++r)
+#pragma unroll
+            for (int t = 0; t < NTT; ++t) wt_store4(pr, piece_off(piece, r, t), acc[r][t]);
+        __builtin_amdgcn_s_waitcnt(0);                  // this wavefront's stores have completed
+        __syncthreads();                                // ... and every wavefront's
+        if (tid == 0) sh.last = counter_add(a.cnt + sti, 1u) == (uint32_t)(np - 1);
+        __syncthreads();
+        if (!sh.last) return;
+        if (tid == 0) counter_reset(a.cnt + sti);       // zero again for the next launch
+        // every piece's sums from memory, this one's too (its stores have completed), added in piece order
+#pragma unroll
+        for (int r = 0; r < kPfRtw; ++r)
+#pragma unroll
+            for (int t = 0; t < NTT; ++t) acc[r][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        for (int pc = 0; pc < np; ++pc) {
+#pragma unroll
+            for (int r = 0; r < kPfRtw; ++r)
+#pragma unroll
+                for (int t = 0; t < NTT; ++t)
+                    acc[r][t] += *(const f32x4 *)((const char *)a.part + piece_off(pc, r, t));
+        }
+    }
 
     // epilogue: lane (jt, q) holds rows 16 r + 4 q + i (i = 0..3) of the wavefront's 64 rows for tokens 16 t + jt
     const int rbase = rg * 64;
@@ -790,9 +848,37 @@ __global__ void __launch_bounds__(64 * kPfWaves, 2) prefill_kernel(PfArgs a) {
     __shared__ PfShared sh;
     // workgroups are dispatched to the XCDs round-robin: all workgroups of one block go to the same XCD (block
     // g on XCD g % 8), so the block's activation rows are fetched into one L2 and read there by every workgroup
-    const int xcd = blockIdx.x % kXcds, li = blockIdx.x / kXcds;
-    const int g = (li / a.RBG) * kXcds + xcd, rbg = li % a.RBG;
-    if (g >= *a.n_blocks) return;
+    // A launch runs n_blocks x RBG tasks on P resident workgroups.  The tasks of the last, partial round (its
+    // blocks' tasks: the last sb blocks) are split along K into np pieces each, so that they spread over the slots
+    // that free up: np = P / (their tasks), at most kPfMaxPieces and at most the row's super tiles.  Their
+    // workgroups follow the unsplit tasks' (which keep the XCD mapping above and skip the split blocks).
+    const int nb = *a.n_blocks;
+    const int wpad = (nb + kXcds - 1) / kXcds * kXcds * a.RBG;
+    int sb = 0, np = 1;
+    if constexpr (WP::kSplit) {
+        const int r = (nb * a.RBG) % a.P;
+        if (r > 0) {
+            sb = (r + a.RBG - 1) / a.RBG;
+            const int n_st = (WP::n_tiles(a, 0) + 3) >> 2;
+            np = min(min(a.P / (sb * a.RBG), kPfMaxPieces), n_st);
+            if (np < 2) np = 1, sb = 0;
+        }
+    }
+    int g, rbg, piece = 0, sti = 0, pieces = 1;
+    if ((int)blockIdx.x < wpad) {
+        const int xcd = blockIdx.x % kXcds, li = blockIdx.x / kXcds;
+        g = (li / a.RBG) * kXcds + xcd;
+        rbg = li % a.RBG;
+        if (g >= nb - sb) return;                       // past the last block, or a split block
+    } else {
+        const int i = blockIdx.x - wpad;
+        if (i >= np * sb * a.RBG) return;
+        sti = i / np;
+        piece = i - sti * np;
+        pieces = np;
+        g = nb - sb + sti / a.RBG;
+        rbg = sti % a.RBG;
+    }
     const int e = __builtin_amdgcn_readfirstlane(a.blk_expert[g]);
     const int n = __builtin_amdgcn_readfirstlane(a.blk_n[g]);
     if constexpr (std::is_same<WP, PfIq3>::value) {
@@ -837,11 +923,11 @@ __global__ void __launch_bounds__(64 * kPfWaves, 2) prefill_kernel(PfArgs a) {
             sh.iq4pair[i] = make_float2((float)kPfKv[i & 15], (float)kPfKv[i >> 4]);
     }
     switch ((n + 15) >> 4) {
-        case 1: prefill_body<MODE, 1, WP, FORM>(a, sh, g, rbg, e, n); break;
-        case 2: prefill_body<MODE, 2, WP, FORM>(a, sh, g, rbg, e, n); break;
-        case 3: prefill_body<MODE, 3, WP, FORM>(a, sh, g, rbg, e, n); break;
-        case 4: prefill_body<MODE, 4, WP, FORM>(a, sh, g, rbg, e, n); break;
-        default: prefill_body<MODE, kPfTT, WP, FORM>(a, sh, g, rbg, e, n); break;
+        case 1: prefill_body<MODE, 1, WP, FORM>(a, sh, g, rbg, e, n, piece, pieces, sti); break;
+        case 2: prefill_body<MODE, 2, WP, FORM>(a, sh, g, rbg, e, n, piece, pieces, sti); break;
+        case 3: prefill_body<MODE, 3, WP, FORM>(a, sh, g, rbg, e, n, piece, pieces, sti); break;
+        case 4: prefill_body<MODE, 4, WP, FORM>(a, sh, g, rbg, e, n, piece, pieces, sti); break;
+        default: prefill_body<MODE, kPfTT, WP, FORM>(a, sh, g, rbg, e, n, piece, pieces, sti); break;
     }
 }
 
