@@ -5,9 +5,16 @@
 
 namespace mi {
 
+#ifndef MI_IQ_NT
+#define MI_IQ_NT 1
+#endif
 __device__ __forceinline__ uint4 ldl(const uint32_t *__restrict__ base, uint32_t lane_off) {
-    // wave-uniform base (SGPRs) + the lane's row offset in 32 bits (rows < 2^30): the scalar-base addressing form
-    return *(const uint4 *)((const char *)base + (lane_off << 2));
+    // wave-uniform base (SGPRs) + the lane's row offset in 32 bits (rows < 2^30): the scalar-base addressing form;
+    // the decoders read every plane word once: non-temporal loads
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 *p = (const u32x4 *)((const char *)base + (lane_off << 2));
+    if constexpr (MI_IQ_NT) return __builtin_bit_cast(uint4, __builtin_nontemporal_load(p));
+    else return __builtin_bit_cast(uint4, *p);
 }
 
 // ------------------------------------------------------------------------------------------------ IQ3_S

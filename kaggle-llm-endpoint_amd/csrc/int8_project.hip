@@ -51,6 +51,10 @@ struct I8Args {
 
 constexpr int kI8Waves = 4;
 constexpr int kI8Ring = 4;          // 128-column blocks in flight per wavefront (2 KB each)
+#ifndef MI_I8_NT
+#define MI_I8_NT 1
+#endif
+constexpr int kI8LoadPolicy = MI_I8_NT ? 2 : 0;   // the weights are read once per launch: non-temporal (nt) loads
 constexpr int kBufWord3 = 0x00020000;   // gfx9 buffer descriptor word 3 (32-bit data format)
 
 __device__ __forceinline__ uint32_t bf16_pair(float a, float b) {
@@ -109,8 +113,8 @@ __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
     const int voff = a.tiled ? 16 * lane : i * a.n_in + 32 * q;
     auto load_block = [&](int p, uint4 &lo, uint4 &hi) {
         const __amdgpu_buffer_rsrc_t r = p < a.blocks ? qb : qnull;
-        lo = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, bstride * p, 0));
-        hi = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff + hoff, bstride * p, 0));
+        lo = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, bstride * p, kI8LoadPolicy));
+        hi = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff + hoff, bstride * p, kI8LoadPolicy));
     };
     uint4 ring[kI8Ring][2];
     if (active) {

@@ -145,7 +145,11 @@ __device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t lds, uint32_t voff, u
         "s_mov_b32 %0, m0\n\t"
         "s_mov_b32 m0, %1\n\t"
         "s_nop 0\n\t"
+#if MI_IQ_NT
+        "buffer_load_dwordx4 %2, %3, %4 offen nt lds\n\t"
+#else
         "buffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
+#endif
         "s_mov_b32 m0, %0\n\t"
         "s_nop 0"
         : "=&s"(m0_saved)
