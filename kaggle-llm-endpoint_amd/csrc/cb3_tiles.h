@@ -85,11 +85,11 @@ template <int POL = 0>
 __device__ __forceinline__ uint4 bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, POL));
 }
-// The decode launches read every code tile and codebook once: those loads are non-temporal, so the weight stream
-// does not push out of the caches what is read again (staged activations, partials, the routing).  Measured on
-// MI355X (A/B, one box): batch 8 162 -> 146 us, batch 16 233 -> 214 us, the batch-1 gate/up launch 32.1 -> 29.1 us.
-// The prefill GEMMs read a block's tiles from several workgroups (non-temporal there: CB3 542.7 -> 558.4 us): their
-// translation units define MI_CB3_STREAM_POLICY 0 before including this header.
+// The code tiles and codebooks are streamed (a decode launch reads each once, a prefill block's workgroups each read
+// their own rows): non-temporal loads, so the weight stream does not push out of the caches what is read again
+// (staged activations, partials, the routing).  Measured on MI355X (A/B, one box): batch 8 162 -> 146 us, batch 16
+// 233 -> 214 us, the batch-1 gate/up launch 32.1 -> 29.1 us, the CB3 prefill 525 -> 515 us.  The prefill's
+// activation tiles, read by every workgroup of a block, keep cached loads.
 #ifndef MI_CB3_STREAM_POLICY
 #define MI_CB3_STREAM_POLICY kLoadNonTemporal
 #endif

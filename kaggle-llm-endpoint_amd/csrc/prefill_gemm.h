@@ -14,10 +14,6 @@
 #pragma once
 #include <type_traits>
 
-// the GEMMs read a block's tiles from several workgroups: cached loads (see cb3_tiles.h)
-#ifndef MI_CB3_STREAM_POLICY
-#define MI_CB3_STREAM_POLICY 0
-#endif
 #include "cb3_tiles.h"
 #include "formats.h"
 
