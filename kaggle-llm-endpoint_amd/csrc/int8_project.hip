@@ -11,7 +11,10 @@
 // in bf16) and feeds v_mfma_f32_16x16x32_bf16 (bf16 x bf16 products are exact, f32 accumulation) with the staged
 // activations as the B operand (up to 16 tokens per tile).  Inside a block the lane's 32 bytes are 4 k-steps of 8 columns:
 // step c of block p uses columns 128p + 32q + 8c .. +7 (q = lane / 16) for both operands.  Splits write f32
-// partials that split_reduce_i8 sums in order (no counters, deterministic); one split writes y directly.
+// partials; the workgroup of a row group that completes last adds every split's partial in split order (the same
+// order whichever completes last) and writes y -- or, for an MLP's gate/up pair, h -- so the sums need no launch of
+// their own (completion counters in the workspace; split_reduce_i8 / swiglu_pair_i8 when there are too many row
+// groups for them).  One split writes y directly.
 #include "common.h"
 
 #include <stdlib.h>
@@ -23,6 +26,7 @@ namespace mi {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kI8MaxProj = 8;      // projections sharing one activation matrix per launch
 
@@ -47,7 +51,14 @@ struct I8Args {
     int pair;              // 1: projections 0 and 1 are gate and up of an MLP: partials always (swiglu_pair_i8)
     float limit;           // pair: the SwiGLU clamp
     uint16_t *h;           // pair: h [B, n_out of projection 0] bf16
+    uint32_t *cnt;         // completion counters, one per row group (zero between launches); null: separate sums
+    int ctr_start[kI8MaxProj];      // first counter of each projection (a pair's gate and up share theirs)
 };
+
+// Counter words per launch; an int8 workspace starts with two such blocks (the MLP's gate/up and down launches).
+constexpr int kI8CtrWords = 2048;
+constexpr size_t kI8CtrBytes = 2 * 4 * kI8CtrWords;
+constexpr int kI8StoreThrough = 16;     // sc1 store: through this XCD's L2 to memory
 
 constexpr int kI8Waves = 4;
 constexpr int kI8Ring = 4;          // 128-column blocks in flight per wavefront (2 KB each)
@@ -84,7 +95,8 @@ __device__ __forceinline__ bf16x8 i8_weights8_rs(uint32_t w0, uint32_t w1, float
     return __builtin_bit_cast(bf16x8, v);
 }
 
-template <int TT, int SA>   // token tiles of 16 (B <= 16 * TT); SA: MI_I8_* scale form
+// token tiles of 16 (B <= 16 * TT); SA: MI_I8_* scale form; SUMS: the split sums in the launch (a.cnt set)
+template <int TT, int SA, bool SUMS>
 __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
     extern __shared__ uint32_t xs[];                 // [B][cols / 2] bf16 pairs of the split's columns (+ row scales)
     const int tid = threadIdx.x, lane = tid & 63;
@@ -96,7 +108,7 @@ __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
     const int row_groups = (P.n_out + 16 * kI8Waves - 1) / (16 * kI8Waves);
     const int rg = local % row_groups, split = local / row_groups;
     const int o0 = (rg * kI8Waves + wave) * 16;
-    const bool active = o0 < P.n_out;                // wavefronts past the last 16-row tile only help stage
+    const bool active = o0 < P.n_out;                // wavefronts past the last 16-row tile only stage (and count)
     const int i = lane & 15, q = lane >> 4;
     const int cols = 128 * a.blocks, k0 = split * cols;
 
@@ -132,9 +144,9 @@ __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
         for (int e = tid; e < cols / 4; e += blockDim.x) *(float4 *)(srow + 4 * e) = *(const float4 *)(P.s + k0 + 4 * e);
     }
     __syncthreads();
-    if (!active) return;
+    if (!active && !SUMS) return;
     // per-column scales: the row's s; the lm_head form: q itself (scale 1 here, s[o] after the sum)
-    const float sc = SA == MI_I8_COL_SCALES ? P.s[o0 + i] : 1.0f;
+    const float sc = SA == MI_I8_COL_SCALES && active ? P.s[o0 + i] : 1.0f;
     const float ns128 = -128.0f * sc;
 
     f32x4 acc[TT];
@@ -145,7 +157,7 @@ __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
 #pragma unroll
     for (int t = 0; t < TT; ++t) xrow[t] = xs + min(16 * t + i, a.B - 1) * cw + 16 * q;
 
-    for (int p0 = 0; p0 < a.blocks; p0 += kI8Ring) {
+    for (int p0 = 0; p0 < (active ? a.blocks : 0); p0 += kI8Ring) {
 #pragma unroll
         for (int d = 0; d < kI8Ring; ++d) {
             const int p = p0 + d;
@@ -173,8 +185,85 @@ __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
     }
     // C layout: lane (jt = lane % 16, q) holds output rows o0 + 4q + r for token 16 t + jt
     const int o = o0 + 4 * q;
-    if constexpr (SA == MI_I8_COL_AFTER) {          // the lm_head form: scale after the whole sum (one split)
-        if (a.S == 1) {
+    if constexpr (SUMS) {
+        // the split's partial goes to memory (stored through this XCD's L2), then the row group is counted; the
+        // workgroup that counts last adds all of them in split order.  Nothing waits for another workgroup.  The
+        // partials are read with plain loads: each 128-byte line is written by one workgroup and read once, after
+        // its count, so no L2 holds it.  The flag lives in xs[0]: past the first barrier no wavefront reads the
+        // activations (a static __shared__ word would move xs off its 16-byte alignment).
+        if (active) {
+            const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+                (void *)(P.part + (size_t)split * a.B * P.n_out), (short)0, 0x7fffffff, kBufWord3);
+#pragma unroll
+            for (int t = 0; t < TT; ++t) {
+                const int b = 16 * t + i;
+                if (b < a.B)
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[t]), pr,
+                                                           (b * P.n_out + o) * 4, 0, kI8StoreThrough);
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0);              // this wavefront's stores have completed
+        __syncthreads();                            // ... and every wavefront's
+        uint32_t *ctr = a.cnt + a.ctr_start[pj] + rg;
+        if (tid == 0) xs[0] = counter_add(ctr, 1u) == (uint32_t)((a.pair ? 2 : 1) * a.S - 1);
+        __syncthreads();
+        if (!xs[0]) return;
+        if (tid == 0) counter_reset(ctr);           // zero again for the next launch
+        if (!active) return;
+        if (a.pair) {
+            // h = bf16(swiglu_clamped(bf16(g), bf16(u))), g and u the split sums of projections 0 and 1
+            // (mlp_partial, model.py:119-127), as swiglu_pair_i8
+#pragma unroll
+            for (int t = 0; t < TT; ++t) {
+                const int b = 16 * t + i;
+                if (b >= a.B) continue;
+                f32x4 g = (f32x4){0.f, 0.f, 0.f, 0.f}, u = g;
+                for (int s0 = 0; s0 < a.S; s0 += 4) {      // 8 loads in flight, added in split order
+                    f32x4 pg[4], pu[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const size_t e = ((size_t)(s0 + j) * a.B + b) * P.n_out + o;
+                        const bool in = s0 + j < a.S;
+                        pg[j] = in ? *(const f32x4 *)(a.p[0].part + e) : (f32x4){0.f, 0.f, 0.f, 0.f};
+                        pu[j] = in ? *(const f32x4 *)(a.p[1].part + e) : (f32x4){0.f, 0.f, 0.f, 0.f};
+                    }
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        g += pg[j];
+                        u += pu[j];
+                    }
+                }
+                uint2 v;
+                v.x = f32_to_bf16_rne(swiglu_clamped(round_bf16(g.x), round_bf16(u.x), a.limit)) |
+                      (f32_to_bf16_rne(swiglu_clamped(round_bf16(g.y), round_bf16(u.y), a.limit)) << 16);
+                v.y = f32_to_bf16_rne(swiglu_clamped(round_bf16(g.z), round_bf16(u.z), a.limit)) |
+                      (f32_to_bf16_rne(swiglu_clamped(round_bf16(g.w), round_bf16(u.w), a.limit)) << 16);
+                *(uint2 *)(a.h + (size_t)b * P.n_out + o) = v;
+            }
+            return;
+        }
+        // y = the split sums in split order, as split_reduce_i8
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+            const int b = 16 * t + i;
+            f32x4 v = (f32x4){0.f, 0.f, 0.f, 0.f};
+            if (b < a.B)
+                for (int s0 = 0; s0 < a.S; s0 += 8) {       // 8 loads in flight, added in split order
+                    f32x4 pv[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j)
+                        pv[j] = s0 + j < a.S ? *(const f32x4 *)(P.part + ((size_t)(s0 + j) * a.B + b) * P.n_out + o)
+                                             : (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) v += pv[j];
+                }
+            acc[t] = v;
+        }
+    } else if (!active) {
+        return;
+    }
+    if constexpr (SA == MI_I8_COL_AFTER) {          // the lm_head form: scale after the whole sum
+        if (a.S == 1 || SUMS) {
             const float4 so = *(const float4 *)(P.s + o);
 #pragma unroll
             for (int t = 0; t < TT; ++t) {
@@ -186,7 +275,7 @@ __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
     for (int t = 0; t < TT; ++t) {
         const int b = 16 * t + i;
         if (b >= a.B) continue;
-        if (a.S == 1 && !a.pair) {
+        if ((a.S == 1 && !a.pair) || SUMS) {
             if (P.y_f32) *(float4 *)(P.y_f32 + (size_t)b * P.n_out + o) = make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
             if (P.y_bf16) {
                 uint2 v;
@@ -312,7 +401,7 @@ static int i8_tiles(const int32_t *n_out, int n_proj) {
     return t;
 }
 
-// Workspace bytes of one launch: the f32 split partials (none with one split, except for an MLP's gate/up pair,
+// Partial bytes of one launch: the f32 split partials (none with one split, except for an MLP's gate/up pair,
 // whose SwiGLU reads them).
 static size_t i8_part_bytes(int B, int n_in, const int32_t *n_out, int n_proj, int scale_axis, int pair) {
     scale_axis &= ~MI_I8_TILED;
@@ -328,11 +417,21 @@ static size_t al256_i8(size_t v) { return (v + 255) & ~(size_t)255; }
 
 using namespace mi;
 
-// One launch of the projections of `projs` over x (+ the split reduction, or with `pair` the SwiGLU of gate and
-// up into h).
+// In-launch split sums (completion counters), a bit mask: 1 for projections, 2 for an MLP's gate/up pair (h formed
+// in the launch).  MI355MOE_I8_FUSE overrides it (experiments).
+static int i8_fuse() {
+    static const int on = [] {
+        const char *e = getenv("MI355MOE_I8_FUSE");
+        return e && *e ? atoi(e) : 1;
+    }();
+    return on;
+}
+
+// One launch of the projections of `projs` over x (+ the split sums, or with `pair` the SwiGLU of gate and up into
+// h): partials at `part` (part_bytes), the launch's counter block at `cnt` (kI8CtrWords words, zero).
 static int i8_launch(const uint16_t *x_bf16, int32_t B, int32_t n_in, const mi_i8_proj *projs, int32_t n_proj,
-                     int32_t scale_axis, void *workspace, size_t workspace_bytes, void *stream, int pair, float limit,
-                     uint16_t *h) {
+                     int32_t scale_axis, float *part, size_t part_bytes, uint32_t *cnt, void *stream, int pair,
+                     float limit, uint16_t *h) {
     if (!x_bf16 || !projs) return MI_ERR_NULL;
     if (B <= 0 || B > 32) return MI_ERR_TOKENS;
     if (n_proj <= 0 || n_proj > kI8MaxProj || (pair && n_proj != 2)) return MI_ERR_ARG;
@@ -348,7 +447,7 @@ static int i8_launch(const uint16_t *x_bf16, int32_t B, int32_t n_in, const mi_i
         n_out[j] = p.n_out;
     }
     const size_t need = i8_part_bytes(B, n_in, n_out, n_proj, scale_axis, pair);
-    if (!workspace || workspace_bytes < need) return MI_ERR_WORKSPACE;
+    if (!part || part_bytes < need || (uintptr_t)part % 16) return MI_ERR_WORKSPACE;
     I8Args a{};
     a.pair = pair;
     a.limit = limit;
@@ -362,7 +461,7 @@ static int i8_launch(const uint16_t *x_bf16, int32_t B, int32_t n_in, const mi_i
     a.blocks = n_in / 128 / a.S;
     a.n_proj = n_proj;
     size_t off = 0;
-    int wg = 0;
+    int wg = 0, ctrs = 0;
     for (int j = 0; j < n_proj; ++j) {
         I8Proj &p = a.p[j];
         p.q = projs[j].qT;
@@ -370,19 +469,28 @@ static int i8_launch(const uint16_t *x_bf16, int32_t B, int32_t n_in, const mi_i
         p.n_out = projs[j].n_out;
         p.y_bf16 = projs[j].y_bf16;
         p.y_f32 = projs[j].y_f32;
-        p.part = (float *)workspace + off;
+        p.part = part + off;
         off += (size_t)a.S * B * p.n_out;
         a.wg_start[j] = wg;
-        wg += (p.n_out + 16 * kI8Waves - 1) / (16 * kI8Waves) * a.S;
+        const int row_groups = (p.n_out + 16 * kI8Waves - 1) / (16 * kI8Waves);
+        wg += row_groups * a.S;
+        a.ctr_start[j] = pair ? 0 : ctrs;
+        ctrs = a.ctr_start[j] + row_groups;
     }
     a.wg_start[n_proj] = wg;
+    // the split sums in this launch when its row groups have counters (and there is more than one split or a pair)
+    a.cnt = (a.S > 1 || pair) && ctrs <= kI8CtrWords && (i8_fuse() & (pair ? 2 : 1)) ? cnt : nullptr;
     const size_t lds = i8_col_bytes(B, scale_axis) * 128 * a.blocks;
     hipStream_t st = (hipStream_t)stream;
     typedef void (*Kern)(I8Args);
-    static const Kern kern[2][3] = {{int8_project_kernel<1, 0>, int8_project_kernel<1, 1>, int8_project_kernel<1, 2>},
-                                    {int8_project_kernel<2, 0>, int8_project_kernel<2, 1>, int8_project_kernel<2, 2>}};
-    hipLaunchKernelGGL(kern[B <= 16 ? 0 : 1][scale_axis], dim3(wg), dim3(64 * kI8Waves), lds, st, a);
+    static const Kern kern[2][2][3] = {
+        {{int8_project_kernel<1, 0, false>, int8_project_kernel<1, 1, false>, int8_project_kernel<1, 2, false>},
+         {int8_project_kernel<2, 0, false>, int8_project_kernel<2, 1, false>, int8_project_kernel<2, 2, false>}},
+        {{int8_project_kernel<1, 0, true>, int8_project_kernel<1, 1, true>, int8_project_kernel<1, 2, true>},
+         {int8_project_kernel<2, 0, true>, int8_project_kernel<2, 1, true>, int8_project_kernel<2, 2, true>}}};
+    hipLaunchKernelGGL(kern[a.cnt ? 1 : 0][B <= 16 ? 0 : 1][scale_axis], dim3(wg), dim3(64 * kI8Waves), lds, st, a);
     if (hipGetLastError() != hipSuccess) return MI_ERR_LAUNCH;
+    if (a.cnt) return MI_OK;
     if (pair) {
         const int n4 = B * a.p[0].n_out / 4;
         hipLaunchKernelGGL(swiglu_pair_i8, dim3((n4 + 255) / 256), dim3(256), 0, st, a);
@@ -406,13 +514,16 @@ size_t mi_int8_project_many_workspace(int32_t B, int32_t n_in, const int32_t *n_
     if (scale_axis < MI_I8_ROW_SCALES || scale_axis > MI_I8_COL_AFTER) return 0;
     for (int j = 0; j < n_proj; ++j)
         if (n_out[j] <= 0 || n_out[j] % 16) return 0;
-    return i8_part_bytes(B, n_in, n_out, n_proj, scale_axis, 0);
+    return kI8CtrBytes + i8_part_bytes(B, n_in, n_out, n_proj, scale_axis, 0);
 }
 
+// Every int8 workspace starts with the counter blocks (kI8CtrBytes), then the launch's data.
 int mi_int8_project_many(const uint16_t *x_bf16, int32_t B, int32_t n_in, const mi_i8_proj *projs, int32_t n_proj,
                          int32_t scale_axis, void *workspace, size_t workspace_bytes, void *stream) {
-    return i8_launch(x_bf16, B, n_in, projs, n_proj, scale_axis, workspace, workspace_bytes, stream, 0, 0.0f,
-                     nullptr);
+    const bool ok = workspace && workspace_bytes >= kI8CtrBytes;
+    return i8_launch(x_bf16, B, n_in, projs, n_proj, scale_axis,
+                     ok ? (float *)((char *)workspace + kI8CtrBytes) : nullptr, ok ? workspace_bytes - kI8CtrBytes : 0,
+                     (uint32_t *)workspace, stream, 0, 0.0f, nullptr);
 }
 
 int mi_int8_tile(const int8_t *qT, int32_t n_out, int32_t n_in, int8_t *tiled, void *stream) {
@@ -445,9 +556,9 @@ size_t mi_int8_mlp_workspace(int32_t B, int32_t D, int32_t I, int32_t gu_scale_a
     down_scale_axis &= ~MI_I8_TILED;
     if (gu_scale_axis != MI_I8_ROW_SCALES && gu_scale_axis != MI_I8_COL_SCALES) return 0;
     if (down_scale_axis != MI_I8_ROW_SCALES && down_scale_axis != MI_I8_COL_SCALES) return 0;
-    const int32_t gu[2] = {I, I};
-    return al256_i8(i8_part_bytes(B, D, gu, 2, gu_scale_axis, 1)) + al256_i8(2 * (size_t)B * I) +
-           mi_int8_project_workspace(B, I, D, down_scale_axis);
+    const int32_t gu[2] = {I, I}, dn = D;
+    return kI8CtrBytes + al256_i8(i8_part_bytes(B, D, gu, 2, gu_scale_axis, 1)) + al256_i8(2 * (size_t)B * I) +
+           i8_part_bytes(B, I, &dn, 1, down_scale_axis, 0);
 }
 
 int mi_int8_mlp(const uint16_t *x_bf16, int32_t B, int32_t D, int32_t I, const int8_t *gate_qT, const float *gate_s,
@@ -462,15 +573,20 @@ int mi_int8_mlp(const uint16_t *x_bf16, int32_t B, int32_t D, int32_t I, const i
     const size_t need = mi_int8_mlp_workspace(B, D, I, gu_scale_axis, down_scale_axis);
     if (need == 0) return MI_ERR_ARG;
     if (!workspace || workspace_bytes < need || (uintptr_t)workspace % 256) return MI_ERR_WORKSPACE;
+    // [counter blocks: gate/up's, down's][gate/up partials][h][down partials]
     const int32_t gu[2] = {I, I};
+    uint32_t *cnt = (uint32_t *)workspace;
+    char *gu_part = (char *)workspace + kI8CtrBytes;
     const size_t part = al256_i8(i8_part_bytes(B, D, gu, 2, gu_scale_axis, 1));
-    uint16_t *h = (uint16_t *)((char *)workspace + part);
-    char *ws_down = (char *)workspace + part + al256_i8(2 * (size_t)B * I);
+    uint16_t *h = (uint16_t *)(gu_part + part);
+    char *dn_part = gu_part + part + al256_i8(2 * (size_t)B * I);
     const mi_i8_proj p[2] = {{gate_qT, gate_s, I, nullptr, nullptr}, {up_qT, up_s, I, nullptr, nullptr}};
-    int st = i8_launch(x_bf16, B, D, p, 2, gu_scale_axis, workspace, part, stream, 1, limit, h);
+    int st = i8_launch(x_bf16, B, D, p, 2, gu_scale_axis, (float *)gu_part, part, cnt, stream, 1, limit, h);
     if (st) return st;
-    return mi_int8_project(h, B, down_qT, down_s, down_scale_axis, I, D, y_bf16, y_f32, ws_down,
-                           workspace_bytes - (size_t)(ws_down - (char *)workspace), stream);
+    const mi_i8_proj pd{down_qT, down_s, D, y_bf16, y_f32};
+    return i8_launch(h, B, I, &pd, 1, down_scale_axis, (float *)dn_part,
+                     workspace_bytes - (size_t)(dn_part - (char *)workspace), cnt + kI8CtrWords, stream, 0, 0.0f,
+                     nullptr);
 }
 
 }  // extern "C"

@@ -1,5 +1,6 @@
 """GPU parity of the int8 projection (quant8.py:91-99 + x @ W) against the oracle: bf16(f32(q)*s) weights, exact
 bf16 products, f32 accumulation, bf16 out."""
+import ctypes
 import os
 
 import numpy as np
@@ -52,6 +53,51 @@ def test_int8_project_many_equals_single(pkg, gpu):
         yb1, yf1 = pkg.int8_project(xt, qT, sv, want_f32=True)
         assert rel_l2(yf.cpu().numpy(), yf1.cpu().numpy()) < 1e-6
         assert rel_l2(yf.cpu().numpy(), oi8.project_f32(x, q, s)) < 1e-5
+
+
+def test_int8_split_sums_leave_counters_zero(pkg, gpu):
+    """The split-K sums run in the projection launch (the last workgroup of each row group adds the partials in split
+    order, counted in the workspace's first 16 KB): calls sharing one workspace -- three projections of 6144 x 6144
+    at 8 tokens (3 splits), a smaller call, the MLP -- give the same bits every time and leave the counters zero."""
+    rng = np.random.default_rng(31)
+    B, n_in = 8, 6144
+    qs = [oi8.generate(rng, n_in, 6144) for _ in range(3)]
+    x = round_bf16(rng.standard_normal((B, n_in)).astype(np.float32))
+    xt = torch.from_numpy(x).cuda().to(torch.bfloat16)
+    projs = []
+    for q, s in qs:
+        qT, sv, _ = pkg.formats.int8_pack(q, s)
+        projs.append((torch.from_numpy(qT).cuda(), torch.from_numpy(sv).cuda()))
+    L = pkg._lib.lib()
+    n_outs = (ctypes.c_int32 * 3)(6144, 6144, 6144)
+    nbytes = max(L.mi_int8_project_many_workspace(B, n_in, n_outs, 3, 1), L.mi_int8_mlp_workspace(3, 1024, 512, 1, 0))
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+    first = pkg.int8_project_many(xt, projs, want_f32=True, workspace=ws)
+    for (q, s), (yb, yf) in zip(qs, first):
+        assert rel_l2(yf.cpu().numpy(), oi8.project_f32(x, q, s)) < 1e-5
+    assert int(ws[:16384].count_nonzero()) == 0
+    # a smaller projection, then the MLP, on the same workspace
+    q2, s2 = oi8.generate(rng, 1024, 512)
+    x2 = round_bf16(rng.standard_normal((3, 1024)).astype(np.float32))
+    x2t = torch.from_numpy(x2).cuda().to(torch.bfloat16)
+    qT2, sv2, _ = pkg.formats.int8_pack(q2, s2)
+    y2 = pkg.int8_project(x2t, torch.from_numpy(qT2).cuda(), torch.from_numpy(sv2).cuda(), want_f32=True,
+                          workspace=ws)[1]
+    assert rel_l2(y2.cpu().numpy(), oi8.project_f32(x2, q2, s2)) < 1e-5
+    gq, gs = oi8.generate(rng, 1024, 512)
+    uq, us = oi8.generate(rng, 1024, 512)
+    dq, ds = oi8.generate(rng, 512, 1024)
+    leaves = [pkg.formats.int8_pack(q, s) for q, s in ((gq, gs), (uq, us), (dq, ds))]
+    leaves = [(torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda(), c) for a, b, c in leaves]
+    m1 = pkg.int8_mlp(x2t, *leaves, 7.0, workspace=ws)
+    assert int(ws[:16384].count_nonzero()) == 0
+    m2 = pkg.int8_mlp(x2t, *leaves, 7.0, workspace=ws)
+    assert torch.equal(m1, m2)
+    for _ in range(2):
+        again = pkg.int8_project_many(xt, projs, want_f32=True, workspace=ws)
+        for (yb, yf), (yb1, yf1) in zip(first, again):
+            assert torch.equal(yb, yb1) and torch.equal(yf, yf1)
+    assert int(ws[:16384].count_nonzero()) == 0
 
 
 @pytest.mark.parametrize("B,n_in,n_out", [(8, 6144, 6144), (8, 2048, 6144), (1, 512, 256), (20, 1024, 512)])
