@@ -294,11 +294,11 @@ int mi_dequant(const mi_table *t, int32_t expert, float *out, void *stream);
  * x bf16 [B, n_in]; qT int8 [n_out, n_in] (the reference's q [in, out] transposed once at load).
  * 1 <= B <= 32, n_in % 256 == 0, n_out % 16 == 0.  The weights are dequantized to bf16 in registers and contracted
  * on the matrix cores (bf16 x bf16 products are exact, f32 accumulation).
- * The workspace (mi_int8_project_workspace bytes, 16-byte aligned) starts with 16 KB of completion counters, then
+ * The workspace (mi_int8_project_workspace bytes, 16-byte aligned) starts with 256 KB of completion counters, then
  * the split-K partials.  The counters must be zero before a workspace's first int8 call (allocate it zero-filled);
  * every int8 call leaves them zero, so mi_int8_project, mi_int8_project_many and mi_int8_mlp may share one
  * workspace, ordered on one stream.  One launch: the workgroup that completes a row group's splits last adds the
- * partials in split order (a second, summing launch when a launch has more than 2048 row groups of 64 outputs).
+ * partials in split order (a second, summing launch when a launch has more than 1024 row groups of 64 outputs).
  * scale_axis | MI_I8_TILED: qT is in the tiled layout that mi_int8_tile writes (same values, another byte order).
  */
 #define MI_I8_ROW_SCALES 0
@@ -343,7 +343,7 @@ size_t mi_int8_project_many_workspace(int32_t B, int32_t n_in, const int32_t *n_
  *   h = bf16(silu(min(g, L)) * clip(u, -L, L))      (swiglu_clamped, model.py:119-122, evaluated in f32 once)
  *   y = h Wd in f32; y_bf16 = bf16(y)               (the reference's output is the bf16 one)
  * x bf16 [B, D]; gate/up qT int8 [I, D] with s per gu_scale_axis ([I] MI_I8_COL_SCALES or [D] MI_I8_ROW_SCALES);
- * down qT int8 [D, I] with s per down_scale_axis ([D] or [I]).  1 <= B <= 32, D % 256 == 0, I % 256 == 0.  Three
+ * down qT int8 [D, I] with s per down_scale_axis ([D] or [I]).  1 <= B <= 32, D % 256 == 0, I % 256 == 0.  Two
  * launches: gate and up together (their last workgroups form h), then down with its split sums.  Workspace:
  * mi_int8_mlp_workspace bytes, 256-byte aligned, its counters as for mi_int8_project (zero before the first call).
  */

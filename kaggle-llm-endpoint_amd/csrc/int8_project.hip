@@ -55,9 +55,11 @@ struct I8Args {
     int ctr_start[kI8MaxProj];      // first counter of each projection (a pair's gate and up share theirs)
 };
 
-// Counter words per launch; an int8 workspace starts with two such blocks (the MLP's gate/up and down launches).
-constexpr int kI8CtrWords = 2048;
-constexpr size_t kI8CtrBytes = 2 * 4 * kI8CtrWords;
+// Counters per launch, each on its own 128-byte line (a line's atomics are serialised); an int8 workspace starts
+// with two such blocks (the MLP's gate/up and down launches).
+constexpr int kI8Ctrs = 1024;
+constexpr int kI8CtrStride = 32;        // words
+constexpr size_t kI8CtrBytes = 2 * 4 * (size_t)kI8Ctrs * kI8CtrStride;
 constexpr int kI8StoreThrough = 16;     // sc1 store: through this XCD's L2 to memory
 
 constexpr int kI8Waves = 4;
@@ -204,7 +206,7 @@ __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
         }
         __builtin_amdgcn_s_waitcnt(0);              // this wavefront's stores have completed
         __syncthreads();                            // ... and every wavefront's
-        uint32_t *ctr = a.cnt + a.ctr_start[pj] + rg;
+        uint32_t *ctr = a.cnt + (a.ctr_start[pj] + rg) * kI8CtrStride;
         if (tid == 0) xs[0] = counter_add(ctr, 1u) == (uint32_t)((a.pair ? 2 : 1) * a.S - 1);
         __syncthreads();
         if (!xs[0]) return;
@@ -422,13 +424,13 @@ using namespace mi;
 static int i8_fuse() {
     static const int on = [] {
         const char *e = getenv("MI355MOE_I8_FUSE");
-        return e && *e ? atoi(e) : 1;
+        return e && *e ? atoi(e) : 3;
     }();
     return on;
 }
 
 // One launch of the projections of `projs` over x (+ the split sums, or with `pair` the SwiGLU of gate and up into
-// h): partials at `part` (part_bytes), the launch's counter block at `cnt` (kI8CtrWords words, zero).
+// h): partials at `part` (part_bytes), the launch's counter block at `cnt` (kI8Ctrs counters, zero).
 static int i8_launch(const uint16_t *x_bf16, int32_t B, int32_t n_in, const mi_i8_proj *projs, int32_t n_proj,
                      int32_t scale_axis, float *part, size_t part_bytes, uint32_t *cnt, void *stream, int pair,
                      float limit, uint16_t *h) {
@@ -479,7 +481,7 @@ static int i8_launch(const uint16_t *x_bf16, int32_t B, int32_t n_in, const mi_i
     }
     a.wg_start[n_proj] = wg;
     // the split sums in this launch when its row groups have counters (and there is more than one split or a pair)
-    a.cnt = (a.S > 1 || pair) && ctrs <= kI8CtrWords && (i8_fuse() & (pair ? 2 : 1)) ? cnt : nullptr;
+    a.cnt = (a.S > 1 || pair) && ctrs <= kI8Ctrs && (i8_fuse() & (pair ? 2 : 1)) ? cnt : nullptr;
     const size_t lds = i8_col_bytes(B, scale_axis) * 128 * a.blocks;
     hipStream_t st = (hipStream_t)stream;
     typedef void (*Kern)(I8Args);
@@ -585,7 +587,7 @@ int mi_int8_mlp(const uint16_t *x_bf16, int32_t B, int32_t D, int32_t I, const i
     if (st) return st;
     const mi_i8_proj pd{down_qT, down_s, D, y_bf16, y_f32};
     return i8_launch(h, B, I, &pd, 1, down_scale_axis, (float *)dn_part,
-                     workspace_bytes - (size_t)(dn_part - (char *)workspace), cnt + kI8CtrWords, stream, 0, 0.0f,
+                     workspace_bytes - (size_t)(dn_part - (char *)workspace), cnt + kI8Ctrs * kI8CtrStride, stream, 0, 0.0f,
                      nullptr);
 }
 

@@ -12,6 +12,8 @@ from oracle.bf16 import rel_l2, round_bf16
 
 pytestmark = pytest.mark.gpu
 
+CTR_BYTES = 2 * 1024 * 128      # the int8 workspace's counter blocks
+
 
 @pytest.mark.parametrize("B,n_in,n_out", [(8, 512, 256), (1, 256, 16), (8, 2048, 6144), (16, 1024, 2048),
                                           (32, 512, 512), (3, 6144, 2048),
@@ -57,7 +59,7 @@ def test_int8_project_many_equals_single(pkg, gpu):
 
 def test_int8_split_sums_leave_counters_zero(pkg, gpu):
     """The split-K sums run in the projection launch (the last workgroup of each row group adds the partials in split
-    order, counted in the workspace's first 16 KB): calls sharing one workspace -- three projections of 6144 x 6144
+    order, counted in the workspace's first 256 KB): calls sharing one workspace -- three projections of 6144 x 6144
     at 8 tokens (3 splits), a smaller call, the MLP -- give the same bits every time and leave the counters zero."""
     rng = np.random.default_rng(31)
     B, n_in = 8, 6144
@@ -75,7 +77,7 @@ def test_int8_split_sums_leave_counters_zero(pkg, gpu):
     first = pkg.int8_project_many(xt, projs, want_f32=True, workspace=ws)
     for (q, s), (yb, yf) in zip(qs, first):
         assert rel_l2(yf.cpu().numpy(), oi8.project_f32(x, q, s)) < 1e-5
-    assert int(ws[:16384].count_nonzero()) == 0
+    assert int(ws[:CTR_BYTES].count_nonzero()) == 0
     # a smaller projection, then the MLP, on the same workspace
     q2, s2 = oi8.generate(rng, 1024, 512)
     x2 = round_bf16(rng.standard_normal((3, 1024)).astype(np.float32))
@@ -90,14 +92,14 @@ def test_int8_split_sums_leave_counters_zero(pkg, gpu):
     leaves = [pkg.formats.int8_pack(q, s) for q, s in ((gq, gs), (uq, us), (dq, ds))]
     leaves = [(torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda(), c) for a, b, c in leaves]
     m1 = pkg.int8_mlp(x2t, *leaves, 7.0, workspace=ws)
-    assert int(ws[:16384].count_nonzero()) == 0
+    assert int(ws[:CTR_BYTES].count_nonzero()) == 0
     m2 = pkg.int8_mlp(x2t, *leaves, 7.0, workspace=ws)
     assert torch.equal(m1, m2)
     for _ in range(2):
         again = pkg.int8_project_many(xt, projs, want_f32=True, workspace=ws)
         for (yb, yf), (yb1, yf1) in zip(first, again):
             assert torch.equal(yb, yb1) and torch.equal(yf, yf1)
-    assert int(ws[:16384].count_nonzero()) == 0
+    assert int(ws[:CTR_BYTES].count_nonzero()) == 0
 
 
 @pytest.mark.parametrize("B,n_in,n_out", [(8, 6144, 6144), (8, 2048, 6144), (1, 512, 256), (20, 1024, 512)])
