@@ -386,13 +386,17 @@ static int i8_splits(int B, int n_in, int tiles, int scale_axis) {
     const char *env = getenv("MI355MOE_I8S");      // experiments: a forced split count (must divide n_in / 128)
     if (env && atoi(env) > 0 && nblk % atoi(env) == 0 && (size_t)(n_in / atoi(env)) * cb <= 48 * 1024)
         return atoi(env);
+    static const int target = [] {                 // wavefronts to aim for; MI355MOE_I8_WAVES (experiments)
+        const char *e = getenv("MI355MOE_I8_WAVES");
+        return e && atoi(e) > 0 ? atoi(e) : 3072;
+    }();
     int best = 1;
     for (int S = 1; S <= nblk; ++S) {
         if (nblk % S) continue;
         if ((size_t)(n_in / S) * cb > 48 * 1024) continue;
         if (nblk / S < 4 && S > 1) break;
         best = S;
-        if ((long long)tiles * S >= 3072) break;
+        if ((long long)tiles * S >= target) break;
     }
     return best;
 }
