@@ -504,8 +504,9 @@ def bench_int8(torch, pkg, gen, args):
     6144), per-output-channel scales (the shared down: per-input-row, its row-parallel form), bf16 activations,
     weights in the tiled layout (MI355MOE_I8_ROWS=1: the row-major qT, for comparison).  A
     step is the layer's three dependent stages -- Q/K/V of the attention input in one launch, O, and the shared
-    expert's mlp_partial (mi_int8_mlp: gate and up in one launch, SwiGLU, down) -- so projections that share their
-    input share a launch, as they can in the model.  3 weight copies rotated (> the last-level cache)."""
+    expert's mlp_partial (mi_int8_mlp: gate and up in one launch that forms h, then down) -- so projections that share
+    their input share a launch, as they can in the model; every launch adds its split-K partials itself.  3 weight
+    copies rotated (> the last-level cache)."""
     stages = [[(6144, 6144)] * 3, [(6144, 6144)]]
     B, D, I = 8, 6144, 2048
     copies = 3
@@ -539,7 +540,7 @@ def bench_int8(torch, pkg, gen, args):
     ms = Timer(torch, fns).run(args.steps, args.warmup)
     gbs = total / (ms * 1e-3) / 1e9
     return {"us_per_layer_int8": round(ms * 1e3, 2), "GBps": round(gbs, 1), "pct_hbm": round(100 * gbs / HBM_PEAK_GBS, 1),
-            "bytes": int(total), "launches": "Q+K+V | O | shared MLP: gate+up, SwiGLU, down"}
+            "bytes": int(total), "launches": "Q+K+V | O | shared MLP: gate+up (forms h), down; split sums in each launch"}
 
 
 def bench_matvec(torch, pkg, gen, args):
