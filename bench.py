@@ -442,7 +442,7 @@ def bench_read_ceiling(torch, pkg, args, launches=40):
         regions = [torch.full((size,), i + 1, dtype=torch.uint8, device="cuda") for i in range(4)]
         sink = torch.empty(16384 * 4, dtype=torch.int32, device="cuda")
         for wg in (1024, 2048, 4096, 8192, 16384):
-            fns = [lambda r=r, wg=wg: P.check("mi_read_probe", P.lib().mi_read_probe(R._ptr(r), size, R._ptr(sink), wg,
+            fns = [lambda r=r, wg=wg: P.check("mi_read_probe", P.probe_lib().mi_read_probe(R._ptr(r), size, R._ptr(sink), wg,
                                                                                   R._stream()))
                    for r in regions]
             t = Timer(torch, fns)

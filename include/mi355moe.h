@@ -95,13 +95,15 @@ size_t mi_matvec_workspace(const mi_table *t, int32_t n_slots);
  *     g = Wgate_e x_n, u = Wup_e x_n, h = silu(min(g, limit)) * clip(u, -limit, limit)   (model.py:119-122)
  *     y = Wdown_e h
  *   out[n] = sum_j w[n, j] y_{n,j}  (+ the shared expert's y for every token, weight 1, if shared_expert >= 0)
- * x: bf16 [N, D] (D = gate.cols), idx int32 [N, k], w f32 [N, k].  h and every accumulation stay f32
- * (resident.py:114-120).  out_f32 [N, D] and/or out_bf16 [N, D] (either may be NULL, not both).
- * shared_expert: an expert index of the same tables applied to every token with weight 1, or -1.
+ * x: bf16 [N, D] (D = gate.cols), idx int32 [N, k], w f32 [N, k].  Every product is exact and every accumulation
+ * f32 (resident.py:114-120); x enters the matrix cores exactly, h (f32) as its bf16 high part plus a bf16 remainder,
+ * i.e. 16 mantissa bits (~2^-17 relative per element).  out_f32 [N, D] and/or out_bf16 [N, D] (either may be NULL,
+ * not both).  shared_expert: an expert index of the same tables applied to every token with weight 1, or -1.
  * Limits: N <= 16, N*k <= MI_MAX_SLOTS, E <= 1024.  Deterministic (fixed-order reductions, no float atomics).
- * Four launches on the stream: gate/up partials, SwiGLU, down partials, routing-weighted combine (as
- * mi_moe_decode_phases with phases = 3).  The workspace (mi_moe_decode_workspace bytes) holds the partials and h;
- * calls that share a workspace must be ordered on one stream.
+ * Launches on the stream: gate/up partials, down partials and the routing-weighted combine, with a SwiGLU launch
+ * between gate/up and down except where the down launch forms h itself while staging (CB3 tables at one token:
+ * three launches; otherwise four, as mi_moe_decode_phases with phases = 3).  The workspace (mi_moe_decode_workspace
+ * bytes) holds the partials and h; calls that share a workspace must be ordered on one stream.
  */
 int mi_moe_decode(const mi_table *gate, const mi_table *up, const mi_table *down, const uint16_t *x_bf16,
                   int32_t N, int32_t k, const int32_t *idx, const float *w, int32_t shared_expert, float limit,
@@ -137,7 +139,8 @@ int mi_moe_decode_fused(const mi_table *gate, const mi_table *up, const mi_table
  * mi_moe_decode as separate launches (the reference runs gate/up and down as separate kernels too,
  * resident.py:116-119), any qtype: phases = 1: the gate/up launch only (its partials stay in the workspace);
  * 2: SwiGLU + down + combine only (consumes what a previous phase-1 call left in the same workspace, same arguments);
- * 3: both -- four launches: gate/up partials, SwiGLU, down partials, routing-weighted combine.  CB3 with N > 8: the
+ * 3: both -- the launches of mi_moe_decode (gate/up partials, SwiGLU unless the down launch forms h, down partials,
+ * routing-weighted combine).  CB3 with N > 8: the
  * gate/up and down launches are persistent (resident workgroups working through contiguous task ranges with the next
  * task's weights in flight); otherwise one workgroup per (expert group, row range, column split).  It never touches
  * the counter block of mi_moe_decode_fused.
@@ -354,11 +357,17 @@ int mi_int8_mlp(const uint16_t *x_bf16, int32_t B, int32_t D, int32_t I, const i
 size_t mi_int8_mlp_workspace(int32_t B, int32_t D, int32_t I, int32_t gu_scale_axis, int32_t down_scale_axis);
 
 /*
- * Streaming-read probe (measurement only; no counterpart in the reference): reads `bytes` (a multiple of 16) from
- * src with 16-byte loads in a grid-stride loop of `workgroups` 256-thread workgroups and writes one XOR word per
- * wavefront to sink (workgroups * 4 u32).  The benchmark times it to give the part's practical read rate.
+ * Launch-plan overrides, for tests and measurement runs only (no counterpart in the reference).  The library reads
+ * no environment variables: every call plans its launches from built-in defaults, except for the names set here,
+ * which replace those defaults process-wide until mi_tuning_reset.  Names (an unknown one gives MI_ERR_ARG):
+ * split counts and row tiles of the decode launch families (S1, S2, FS1, FS2, SMV, each with _RTW and _AL; MS1, MS2,
+ * CS1, CS2 with _RTW; MGMAX), launch-family switches (CUSTREAM, CUMULTI, PERSIST_ABOVE, FUSE_SWIGLU, CU_FORM_H), the
+ * one-launch decode's poll limit (SPIN_LIMIT) and the int8 split plan (I8S, I8_WAVES, I8_FUSE).  Overrides change
+ * launch shapes and summation orders, never the result beyond f32 rounding; workspace sizes follow them, so set them
+ * before sizing a workspace.  Not synchronised with calls running on other host threads.
  */
-int mi_read_probe(const void *src, size_t bytes, uint32_t *sink, int32_t workgroups, void *stream);
+int mi_tuning_set(const char *name, int32_t value);
+void mi_tuning_reset(void);
 
 const char *mi_strerror(int status);
 int mi_version(void);

@@ -9,11 +9,11 @@ from .resident import (ExpertTable, ResidentFetch, dequant, int8_mlp, int8_proje
                        int8_tile, matvec, mlp_partial,
                        moe_matvec, moe_decode, moe_prefill, moe_route, pack_planes_device, prefill_workspace_bytes,
                        ragged_plan, random_cb3_table, random_iq2s_table,
-                       random_iq3s_table, random_iq4xs_table, random_kq_table, route, to_device_planes)
+                       random_iq3s_table, random_iq4xs_table, random_kq_table, route, to_device_planes, tuning)
 
 __all__ = ["ExpertTable", "ResidentFetch", "dequant", "int8_mlp", "int8_project", "int8_project_many", "int8_tile",
            "matvec",
            "mlp_partial", "moe_matvec",
            "moe_decode",
            "moe_prefill", "moe_route", "pack_planes_device", "prefill_workspace_bytes", "ragged_plan", "route", "gguf", "random_cb3_table", "random_iq2s_table", "random_iq3s_table",
-           "random_iq4xs_table", "random_kq_table", "to_device_planes", "formats"]
+           "random_iq4xs_table", "random_kq_table", "to_device_planes", "tuning", "formats"]

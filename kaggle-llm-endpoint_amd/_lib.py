@@ -44,7 +44,7 @@ EXPORTS = ("mi_matvec", "mi_matvec_workspace", "mi_moe_decode", "mi_moe_decode_f
            "mi_moe_decode_workspace", "mi_moe_decode_plan", "mi_moe_decode_noalloc", "mi_moe_decode_x",
            "mi_ragged_plan", "mi_moe_prefill", "mi_moe_prefill_workspace", "mi_moe_prefill_form",
            "mi_moe_prefill_form_workspace", "mi_dequant", "mi_int8_project", "mi_int8_project_workspace", "mi_int8_project_many",
-           "mi_int8_project_many_workspace", "mi_int8_mlp", "mi_int8_mlp_workspace", "mi_moe_route", "mi_moe_route_workspace", "mi_pack_planes", "mi_read_probe", "mi_int8_tile",
+           "mi_int8_project_many_workspace", "mi_int8_mlp", "mi_int8_mlp_workspace", "mi_moe_route", "mi_moe_route_workspace", "mi_pack_planes", "mi_int8_tile", "mi_tuning_set", "mi_tuning_reset",
            "mi_strerror",
            "mi_version")
 
@@ -94,7 +94,6 @@ def lib():
         "mi_moe_prefill_workspace": (Z, [T, T, I, I, I]),
         "mi_moe_prefill_form": (I, [T, T, T, P, I, I, P, P, I, F, I, I, P, P, P, Z, P]),
         "mi_moe_prefill_form_workspace": (Z, [T, T, I, I, I, I]),
-        "mi_read_probe": (I, [P, Z, P, I, P]),
         "mi_int8_tile": (I, [P, I, I, P, P]),
         "mi_int8_mlp": (I, [P, I, I, I, P, P, P, P, I, P, P, I, F, P, P, P, Z, P]),
         "mi_int8_mlp_workspace": (Z, [I, I, I, I, I]),
@@ -106,6 +105,8 @@ def lib():
         "mi_moe_route": (I, [P, P, P, I, I, I, I, I, F, P, P, P, Z, P]),
         "mi_moe_route_workspace": (Z, [I, I, I]),
         "mi_pack_planes": (I, [I, P, I, I, I, ctypes.POINTER(ctypes.c_void_p), P]),
+        "mi_tuning_set": (I, [ctypes.c_char_p, I]),
+        "mi_tuning_reset": (None, []),
         "mi_strerror": (ctypes.c_char_p, [I]),
         "mi_version": (I, []),
     }
@@ -115,6 +116,27 @@ def lib():
         fn.argtypes = args
     _LIB = L
     return L
+
+
+PROBE_PATH = os.path.join(HERE, "libmi355probe.so")
+_PROBE = None
+
+
+def probe_lib():
+    """The streaming-read probe (libmi355probe.so: measurement only, not part of the operator's C ABI):
+    mi_read_probe(src, bytes, sink, workgroups, stream) reads `bytes` (a multiple of 16) from src with 16-byte loads
+    in a grid-stride loop of `workgroups` 256-thread workgroups and writes one XOR word per wavefront to sink
+    (workgroups * 4 u32)."""
+    global _PROBE
+    if _PROBE is None:
+        if not os.path.exists(PROBE_PATH):
+            raise RuntimeError("libmi355probe.so is not built: run `python kaggle-llm-endpoint_amd/build.py`")
+        L = ctypes.CDLL(PROBE_PATH)
+        L.mi_read_probe.restype = ctypes.c_int32
+        L.mi_read_probe.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int32,
+                                    ctypes.c_void_p]
+        _PROBE = L
+    return _PROBE
 
 
 def check(fn, status):

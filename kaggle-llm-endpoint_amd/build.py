@@ -2,11 +2,14 @@
 
     python kaggle-llm-endpoint_amd/build.py
 
-The library is a plain C-ABI shared object (include/mi355moe.h) that the package loads with ctypes.  The grouped
+The library is a plain C-ABI shared object (include/mi355moe.h) that the package loads with ctypes.  A second,
+measurement-only library, ``libmi355probe.so`` (the streaming-read probe the benchmark times), is built beside it
+from csrc/probe.hip and is not part of the operator's ABI.  The grouped
 kernels are compiled once per (mode, format) from k_grouped.hip, the persistent CB3 kernels once per (mode, token
 class) from k_pstream.hip, the CU-balanced ones once per mode from k_custream.hip and the prefill GEMMs once per
 (mode, rounding form) from k_prefill.hip; all units compile in parallel, then link.
 """
+import hashlib
 import os
 import shutil
 import subprocess
@@ -18,6 +21,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 LIB = os.path.join(HERE, "libmi355moe.so")
+PROBE_LIB = os.path.join(HERE, "libmi355probe.so")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
@@ -30,7 +34,7 @@ FLAGS = [
 # (source, extra defines, object name)
 UNITS = [("moe_decode.hip", [], "moe_decode"), ("int8_project.hip", [], "int8_project"),
          ("prefill.hip", [], "prefill"), ("route.hip", [], "route"),
-         ("pack.hip", [], "pack"), ("probe.hip", [], "probe")]
+         ("pack.hip", [], "pack"), ("tuning.hip", [], "tuning")]
 UNITS += [("k_grouped.hip", ["-DMI_KMODE=%d" % m, "-DMI_KQT=%d" % q], "k_grouped_%d_%d" % (m, q))
           for m in (0, 1, 2) for q in (1, 2, 3, 4, 5, 6)]
 UNITS += [("k_fused.hip", [], "k_fused")]
@@ -41,6 +45,10 @@ UNITS += [("k_cumulti.hip", ["-DMI_UMODE=%d" % m], "k_cumulti_%d" % m) for m in 
 # prefill GEMMs per (mode, rounding form): gate/up plain, bf16 g/u, weighted h, both; down bf16 y, f32 y
 UNITS += [("k_prefill.hip", ["-DMI_PF_MODE=%d" % m, "-DMI_PF_FORM=%d" % f], "k_prefill_%d_%d" % (m, f))
           for m, f in ((0, 0), (0, 1), (0, 2), (0, 3), (1, 0), (1, 4))]
+
+
+# the measurement-only probe library (libmi355probe.so)
+PROBE_UNIT = ("probe.hip", [], "probe")
 
 
 def _filter(stderr):
@@ -64,7 +72,8 @@ def _up_to_date(obj, dep):
 
 def build(verbose=False, jobs=None, incremental=False):
     """Compile every unit and link.  ``incremental=True`` (development only) keeps the objects under _build/ at the
-    repository root and recompiles only the units whose sources or headers changed."""
+    repository root and recompiles only the units whose sources or headers changed; an object's name carries a hash
+    of its compile command, so a change of flags or defines never reuses it."""
     if incremental:
         tmpdir = os.path.join(os.path.dirname(HERE), "_build", "obj")
         os.makedirs(tmpdir, exist_ok=True)
@@ -73,6 +82,9 @@ def build(verbose=False, jobs=None, incremental=False):
     try:
         def compile_unit(u):
             src, defs, name = u
+            key = hashlib.sha1(" ".join([HIPCC] + FLAGS + defs + [INCLUDE, src]).encode()).hexdigest()[:12]
+            if incremental:
+                name = "%s_%s" % (name, key)
             obj = os.path.join(tmpdir, name + ".o")
             dep = os.path.join(tmpdir, name + ".d")
             cmd = [HIPCC] + FLAGS + defs + ["-I", INCLUDE, "-c", os.path.join(CSRC, src), "-o", obj]
@@ -84,8 +96,9 @@ def build(verbose=False, jobs=None, incremental=False):
             return name, obj, res.returncode, _filter(res.stderr), cmd
         jobs = jobs or min(len(UNITS), max(1, os.cpu_count() or 1))
         with ThreadPoolExecutor(jobs) as ex:
-            results = list(ex.map(compile_unit, UNITS))
-        for name, obj, rc, err, cmd in results:
+            results = list(ex.map(compile_unit, UNITS + [PROBE_UNIT]))
+        probe = results.pop()
+        for name, obj, rc, err, cmd in results + [probe]:
             if verbose:
                 print(" ".join(cmd), flush=True)
             if rc != 0:
@@ -98,6 +111,12 @@ def build(verbose=False, jobs=None, incremental=False):
         if res.returncode != 0:
             raise RuntimeError("link failed (%d):\n%s" % (res.returncode, _filter(res.stderr)))
         os.replace(tmp, LIB)
+        tmp = PROBE_LIB + ".tmp"
+        res = subprocess.run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", probe[1], "-o", tmp],
+                             capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError("probe link failed (%d):\n%s" % (res.returncode, _filter(res.stderr)))
+        os.replace(tmp, PROBE_LIB)
     finally:
         if not incremental:
             shutil.rmtree(tmpdir, ignore_errors=True)

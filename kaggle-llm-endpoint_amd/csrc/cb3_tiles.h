@@ -109,8 +109,7 @@ __device__ __forceinline__ void vm_wait() {
 }
 
 // 16-byte store with the sc1 cache policy: written through this XCD's L2 to memory, so once the store has completed
-// (s_waitcnt vmcnt(0)) a workgroup on any XCD that has not cached the line reads the new value.
-constexpr int kCachePolicySc1 = 16;
+// (s_waitcnt vmcnt(0)) a coherent load (coherent_load4) on any XCD reads the new value.
 __device__ __forceinline__ void wt_store4(__amdgpu_buffer_rsrc_t r, uint32_t voff, f32x4 v) {
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, (int)voff, 0, kCachePolicySc1);

@@ -57,6 +57,23 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
     return (float)__builtin_bit_cast(_Float16, (unsigned short)(h & 0xffffu));
 }
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// The sc1 cache policy (buffer instructions' aux bits): stores are written through this XCD's L2 to memory, loads are
+// coherent at device scope (the cache bits of a relaxed agent-scope atomic load).
+constexpr int kCachePolicySc1 = 16;
+
+// Coherent loads: they return what another workgroup stored through to memory (sc1 stores) earlier in the same launch
+// even when this XCD's L2 holds an older copy of the line (a neighbouring value of the same 128-byte line may have
+// pulled it in).  Every value one workgroup hands another inside a launch is read this way, after the count that
+// publishes it.
+__device__ __forceinline__ f32x4 coherent_load4(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, 0, kCachePolicySc1));
+}
+__device__ __forceinline__ uint2 coherent_load2(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, 0, kCachePolicySc1));
+}
+
 // Completion counters.  On this multi-XCD part an agent-scope release writes back the XCD's L2 and an acquire
 // invalidates it, so they are issued as rarely as possible: after a workgroup barrier (which completes every wave's
 // stores to L2) ONE thread issues the release fence and the relaxed increment; only the workgroup that observes the

@@ -20,10 +20,9 @@
 //   - every value another workgroup reads (partials, h) is stored with the sc1 cache policy (written through to
 //     memory) and the storing waves wait for their stores to complete (s_waitcnt vmcnt(0)) before a workgroup
 //     barrier, after which one thread bumps a counter with a relaxed agent-scope atomic;
-//   - readers spin on the counter (relaxed agent-scope loads, which read memory), then read the data with plain loads.
-//     A plain load returns the new value because no reader has the line in its L2: every 128-byte line of these
-//     buffers is written by exactly one task and read only after that task's counter is published, and the L2s hold
-//     nothing from earlier launches (kernel boundaries write back and invalidate them).
+//   - readers spin on the counter (relaxed agent-scope loads, which read memory), then read the data with
+//     device-coherent (sc1) loads, which return the stored value even if this XCD's L2 held an older copy of the
+//     line; the L2s hold nothing from earlier launches (kernel boundaries write back and invalidate them).
 //
 // Progress.  Each workgroup takes a contiguous slice of the phase-1 tasks, then a contiguous slice of the phase-2
 // tasks.  Phase-2 tasks wait only for phase-1 tasks, which never wait, and every workgroup finishes its phase-1 slice
@@ -168,6 +167,8 @@ __device__ __forceinline__ void wt_store2(__amdgpu_buffer_rsrc_t r, uint32_t vof
 constexpr int kCombineSlots = 3;     // slots per token handled per pass (few registers: the next task's ring is live)
 __device__ __forceinline__ void combine_rows(const FArgs &a, int r0, int nr) {
     const int nr4 = nr >> 2;
+    const __amdgpu_buffer_rsrc_t rp =
+        __builtin_amdgcn_make_buffer_rsrc((void *)a.part2, (short)0, 0x7fffffff, kBufferWord3);
     for (int i = threadIdx.x; i < a.N * nr4; i += blockDim.x) {
         const int tok = i / nr4, r = r0 + 4 * (i - tok * nr4);
         float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -198,8 +199,12 @@ __device__ __forceinline__ void combine_rows(const FArgs &a, int r0, int nr) {
                 float4 p[kCombineSlots];
 #pragma unroll
                 for (int jj = 0; jj < kCombineSlots; ++jj)
-                    p[jj] = slot[jj] >= 0 ? *(const float4 *)(a.part2 + ((size_t)s * a.NS + slot[jj]) * a.D + r)
-                                          : make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (slot[jj] >= 0) {
+                        const f32x4 v = coherent_load4(rp, (uint32_t)((((size_t)s * a.NS + slot[jj]) * a.D + r) * 4));
+                        p[jj] = make_float4(v[0], v[1], v[2], v[3]);
+                    } else {
+                        p[jj] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    }
 #pragma unroll
                 for (int jj = 0; jj < kCombineSlots; ++jj) {
                     ys[jj].x += p[jj].x; ys[jj].y += p[jj].y; ys[jj].z += p[jj].z; ys[jj].w += p[jj].w;
@@ -344,15 +349,20 @@ __global__ void __launch_bounds__(64 * kWgWaves, MI_CB3_WAVES) fused_decode_kern
         const int xs = (k.c1 - k.c0) >> 1, q4 = xs >> 1;
         const int K = k.ph2 ? a.I : a.D;
         const int cend = min(k.c1, K);
+        const __amdgpu_buffer_rsrc_t rh =
+            __builtin_amdgcn_make_buffer_rsrc((void *)a.h_hi, (short)0, 0x7fffffff, kBufferWord3);
+        const __amdgpu_buffer_rsrc_t rl =
+            __builtin_amdgcn_make_buffer_rsrc((void *)a.h_lo, (short)0, 0x7fffffff, kBufferWord3);
         for (int i = tid; i < a.t_rows * q4; i += blockDim.x) {
             const int r = i / q4, qq = i - r * q4;
             const int slot = s_tok[r];
             const int c = k.c0 + 4 * qq;
             uint2 hv = make_uint2(0, 0), lv = make_uint2(0, 0);
             if (slot >= 0 && c >= k.cv && c < cend) {
-                if (k.ph2) {
-                    hv = *(const uint2 *)(a.h_hi + (size_t)slot * a.I + c);
-                    lv = *(const uint2 *)(a.h_lo + (size_t)slot * a.I + c);
+                if (k.ph2) {           // h of other workgroups, published by the group's counter
+                    const uint32_t off = (uint32_t)((size_t)slot * a.I + c) * 2u;
+                    hv = coherent_load2(rh, off);
+                    lv = coherent_load2(rl, off);
                 } else {
                     hv = *(const uint2 *)(a.x + (size_t)slot_token(slot, a.n_route, a.k) * a.D + c);
                 }
@@ -370,18 +380,18 @@ __global__ void __launch_bounds__(64 * kWgWaves, MI_CB3_WAVES) fused_decode_kern
             __builtin_amdgcn_make_buffer_rsrc((void *)a.h_hi, (short)0, 0x7fffffff, kBufferWord3);
         const __amdgpu_buffer_rsrc_t hl =
             __builtin_amdgcn_make_buffer_rsrc((void *)a.h_lo, (short)0, 0x7fffffff, kBufferWord3);
+        const __amdgpu_buffer_rsrc_t rp =
+            __builtin_amdgcn_make_buffer_rsrc((void *)a.part1, (short)0, 0x7fffffff, kBufferWord3);
         for (int i = tid; i < k.n * nr4; i += blockDim.x) {
             const int r_ = i / nr4, r = r0 + 4 * (i - r_ * nr4);
             const int slot = s_tok[r_];
-            float4 g = make_float4(0.f, 0.f, 0.f, 0.f), u = g;
+            f32x4 g = (f32x4){0.f, 0.f, 0.f, 0.f}, u = g;
             for (int s = 0; s < a.S1; ++s) {
-                const float4 pg = *(const float4 *)(a.part1 + ((size_t)(2 * s) * a.NS + slot) * a.I + r);
-                const float4 pu = *(const float4 *)(a.part1 + ((size_t)(2 * s + 1) * a.NS + slot) * a.I + r);
-                g.x += pg.x; g.y += pg.y; g.z += pg.z; g.w += pg.w;
-                u.x += pu.x; u.y += pu.y; u.z += pu.z; u.w += pu.w;
+                g += coherent_load4(rp, (uint32_t)((((size_t)(2 * s) * a.NS + slot) * a.I + r) * 4));
+                u += coherent_load4(rp, (uint32_t)((((size_t)(2 * s + 1) * a.NS + slot) * a.I + r) * 4));
             }
-            const float hv[4] = {swiglu_clamped(g.x, u.x, a.limit), swiglu_clamped(g.y, u.y, a.limit),
-                                 swiglu_clamped(g.z, u.z, a.limit), swiglu_clamped(g.w, u.w, a.limit)};
+            const float hv[4] = {swiglu_clamped(g[0], u[0], a.limit), swiglu_clamped(g[1], u[1], a.limit),
+                                 swiglu_clamped(g[2], u[2], a.limit), swiglu_clamped(g[3], u[3], a.limit)};
             uint32_t hi[4], lo[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) split_bf16(hv[j], hi[j], lo[j]);

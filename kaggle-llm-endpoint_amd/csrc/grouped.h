@@ -261,19 +261,12 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
             return;
         }
         const int q4 = xs >> 1;           // 4-column quads per row
-        // IQ2_S stages f16 (iq2_mfma.h): a second pass at scale 2^-shift when the first met |x| >= 2^15
-        int shift = 0;
-        for (int pass = 0; pass < 2; ++pass) {
-        if (pass == 1) {
-            if constexpr (QT == MI_QT_IQ2_S) {
-                __syncthreads();
-                shift = iq2_xshift(iq.amax);
-            }
-            if (shift == 0) break;
-        }
-        for (int i = tid; i < a.t_rows * q4; i += blockDim.x) {
-            const int t = i / q4, q = i - t * q4;
-            const int slot = s_tok[t];
+        const int nq = a.t_rows * q4;
+        // every lane of a wavefront runs the same trips (IQ2_S reduces each row's maximum across the wavefront)
+        for (int i0 = 0; i0 < nq; i0 += blockDim.x) {
+            const int i = i0 + tid;
+            const int t = min(i, nq - 1) / q4, q = i - t * q4;
+            const int slot = i < nq ? s_tok[t] : -1;
             const int c = c0 + 4 * q;
             uint2 hv = make_uint2(0, 0), lv = make_uint2(0, 0);
             if (slot >= 0 && c >= cv && c < a.K) {
@@ -312,16 +305,26 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
                 }
             }
             if constexpr (QT == MI_QT_IQ2_S) {
-                // f16 high part and remainder of each value (the bf16 element, or its high part + remainder)
-                const uint32_t hw[4] = {hv.x & 0xffffu, hv.x >> 16, hv.y & 0xffffu, hv.y >> 16};
-                const uint32_t lw[4] = {lv.x & 0xffffu, lv.x >> 16, lv.y & 0xffffu, lv.y >> 16};
-                uint32_t fh[4], fl[4];
+                // the row's largest |value| (bf16 element, or high part + remainder): one LDS atomic per wavefront
+                // when its quads lie in one row, per lane otherwise
+                uint32_t m = 0u;
+                if (i < nq) {
+                    const uint32_t hw[4] = {hv.x & 0xffffu, hv.x >> 16, hv.y & 0xffffu, hv.y >> 16};
+                    const uint32_t lw[4] = {lv.x & 0xffffu, lv.x >> 16, lv.y & 0xffffu, lv.y >> 16};
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    iq2_x16(bf16_to_f32(hw[j]) + (hilo ? bf16_to_f32(lw[j]) : 0.0f), shift, iq, fh[j], fl[j]);
-                hv = make_uint2(fh[0] | (fh[1] << 16), fh[2] | (fh[3] << 16));
-                lv = make_uint2(fl[0] | (fl[1] << 16), fl[2] | (fl[3] << 16));
+                    for (int j = 0; j < 4; ++j)
+                        m = max(m, __float_as_uint(fabsf(bf16_to_f32(hw[j]) + (hilo ? bf16_to_f32(lw[j]) : 0.0f))));
+                }
+                const int t0 = __builtin_amdgcn_readfirstlane(t);
+                if (__all(i >= nq || t == t0)) {
+#pragma unroll
+                    for (int o = 32; o > 0; o >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, o));
+                    if (lane == 0 && m != 0u) atomicMax(&iq.amax[t0], m);
+                } else if (m != 0u) {
+                    atomicMax(&iq.amax[t], m);
+                }
             }
+            if (i >= nq) continue;
             if constexpr (QT == MI_QT_IQ4_XS) {
                 // the decoder's column order inside each 32-column group (iq4_stage_pos)
                 uint16_t *dh = (uint16_t *)(xh + t * xsp), *dl = (uint16_t *)(xl + t * xsp);
@@ -338,6 +341,23 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
                 if (hilo) *(uint2 *)(xl + t * xsp + 2 * q) = lv;
             }
         }
+        if constexpr (QT == MI_QT_IQ2_S) {
+            // in place: f16 high part and remainder of each value at its row's power of two (iq2_mfma.h)
+            __syncthreads();
+            for (int i = tid; i < nq; i += blockDim.x) {
+                const int t = i / q4, q = i - t * q4;
+                const int shift = iq2_xshift(iq.amax[t]);
+                uint2 hv = *(const uint2 *)(xh + t * xsp + 2 * q), lv = make_uint2(0, 0);
+                if (hilo) lv = *(const uint2 *)(xl + t * xsp + 2 * q);
+                const uint32_t hw[4] = {hv.x & 0xffffu, hv.x >> 16, hv.y & 0xffffu, hv.y >> 16};
+                const uint32_t lw[4] = {lv.x & 0xffffu, lv.x >> 16, lv.y & 0xffffu, lv.y >> 16};
+                uint32_t fh[4], fl[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    iq2_x16(bf16_to_f32(hw[j]) + (hilo ? bf16_to_f32(lw[j]) : 0.0f), shift, fh[j], fl[j]);
+                *(uint2 *)(xh + t * xsp + 2 * q) = make_uint2(fh[0] | (fh[1] << 16), fh[2] | (fh[3] << 16));
+                if (hilo) *(uint2 *)(xl + t * xsp + 2 * q) = make_uint2(fl[0] | (fl[1] << 16), fl[2] | (fl[3] << 16));
+            }
         }
         __syncthreads();
     };

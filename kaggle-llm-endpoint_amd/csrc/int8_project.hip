@@ -16,6 +16,7 @@
 // their own (completion counters in the workspace; split_reduce_i8 / swiglu_pair_i8 when there are too many row
 // groups for them).  One split writes y directly.
 #include "common.h"
+#include "tuning.h"
 
 #include <stdlib.h>
 
@@ -190,9 +191,11 @@ __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
     if constexpr (SUMS) {
         // the split's partial goes to memory (stored through this XCD's L2), then the row group is counted; the
         // workgroup that counts last adds all of them in split order.  Nothing waits for another workgroup.  The
-        // partials are read with plain loads: each 128-byte line is written by one workgroup and read once, after
-        // its count, so no L2 holds it.  The flag lives in xs[0]: past the first barrier no wavefront reads the
-        // activations (a static __shared__ word would move xs off its 16-byte alignment).
+        // partials are read with device-coherent (sc1) loads after the count: a 128-byte line may hold partials of
+        // two row groups (n_out % 32 == 16, or a workspace aligned to 16 bytes only), and the other row group's last
+        // workgroup may have pulled it into this XCD's L2 before every split had stored its part.  The flag lives in
+        // xs[0]: past the first barrier no wavefront reads the activations (a static __shared__ word would move xs
+        // off its 16-byte alignment).
         if (active) {
             const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
                 (void *)(P.part + (size_t)split * a.B * P.n_out), (short)0, 0x7fffffff, kBufWord3);
@@ -215,6 +218,10 @@ __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
         if (a.pair) {
             // h = bf16(swiglu_clamped(bf16(g), bf16(u))), g and u the split sums of projections 0 and 1
             // (mlp_partial, model.py:119-127), as swiglu_pair_i8
+            const __amdgpu_buffer_rsrc_t rg0 =
+                __builtin_amdgcn_make_buffer_rsrc((void *)a.p[0].part, (short)0, 0x7fffffff, kBufWord3);
+            const __amdgpu_buffer_rsrc_t ru0 =
+                __builtin_amdgcn_make_buffer_rsrc((void *)a.p[1].part, (short)0, 0x7fffffff, kBufWord3);
 #pragma unroll
             for (int t = 0; t < TT; ++t) {
                 const int b = 16 * t + i;
@@ -224,10 +231,10 @@ __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
                     f32x4 pg[4], pu[4];
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        const size_t e = ((size_t)(s0 + j) * a.B + b) * P.n_out + o;
+                        const uint32_t e = (uint32_t)((((size_t)(s0 + j) * a.B + b) * P.n_out + o) * 4);
                         const bool in = s0 + j < a.S;
-                        pg[j] = in ? *(const f32x4 *)(a.p[0].part + e) : (f32x4){0.f, 0.f, 0.f, 0.f};
-                        pu[j] = in ? *(const f32x4 *)(a.p[1].part + e) : (f32x4){0.f, 0.f, 0.f, 0.f};
+                        pg[j] = in ? coherent_load4(rg0, e) : (f32x4){0.f, 0.f, 0.f, 0.f};
+                        pu[j] = in ? coherent_load4(ru0, e) : (f32x4){0.f, 0.f, 0.f, 0.f};
                     }
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
@@ -245,6 +252,8 @@ __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
             return;
         }
         // y = the split sums in split order, as split_reduce_i8
+        const __amdgpu_buffer_rsrc_t rp =
+            __builtin_amdgcn_make_buffer_rsrc((void *)P.part, (short)0, 0x7fffffff, kBufWord3);
 #pragma unroll
         for (int t = 0; t < TT; ++t) {
             const int b = 16 * t + i;
@@ -254,8 +263,9 @@ __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
                     f32x4 pv[8];
 #pragma unroll
                     for (int j = 0; j < 8; ++j)
-                        pv[j] = s0 + j < a.S ? *(const f32x4 *)(P.part + ((size_t)(s0 + j) * a.B + b) * P.n_out + o)
-                                             : (f32x4){0.f, 0.f, 0.f, 0.f};
+                        pv[j] = s0 + j < a.S
+                                    ? coherent_load4(rp, (uint32_t)((((size_t)(s0 + j) * a.B + b) * P.n_out + o) * 4))
+                                    : (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                     for (int j = 0; j < 8; ++j) v += pv[j];
                 }
@@ -383,13 +393,10 @@ static size_t i8_col_bytes(int B, int scale_axis) { return 2 * (size_t)B + (scal
 static int i8_splits(int B, int n_in, int tiles, int scale_axis) {
     const int nblk = n_in / 128;
     const size_t cb = i8_col_bytes(B, scale_axis);
-    const char *env = getenv("MI355MOE_I8S");      // experiments: a forced split count (must divide n_in / 128)
-    if (env && atoi(env) > 0 && nblk % atoi(env) == 0 && (size_t)(n_in / atoi(env)) * cb <= 48 * 1024)
-        return atoi(env);
-    static const int target = [] {                 // wavefronts to aim for; MI355MOE_I8_WAVES (experiments)
-        const char *e = getenv("MI355MOE_I8_WAVES");
-        return e && atoi(e) > 0 ? atoi(e) : 3072;
-    }();
+    const int forced = tuning(kTuneI8S, 0);       // measurements: a forced split count (must divide n_in / 128)
+    if (forced > 0 && nblk % forced == 0 && (size_t)(n_in / forced) * cb <= 48 * 1024) return forced;
+    int target = tuning(kTuneI8Waves, 3072);       // wavefronts to aim for
+    if (target <= 0) target = 3072;
     int best = 1;
     for (int S = 1; S <= nblk; ++S) {
         if (nblk % S) continue;
@@ -424,14 +431,8 @@ static size_t al256_i8(size_t v) { return (v + 255) & ~(size_t)255; }
 using namespace mi;
 
 // In-launch split sums (completion counters), a bit mask: 1 for projections, 2 for an MLP's gate/up pair (h formed
-// in the launch).  MI355MOE_I8_FUSE overrides it (experiments).
-static int i8_fuse() {
-    static const int on = [] {
-        const char *e = getenv("MI355MOE_I8_FUSE");
-        return e && *e ? atoi(e) : 3;
-    }();
-    return on;
-}
+// in the launch).  The I8_FUSE override replaces it (measurements and tests of the separate sum kernels).
+static int i8_fuse() { return tuning(kTuneI8Fuse, 3); }
 
 // One launch of the projections of `projs` over x (+ the split sums, or with `pair` the SwiGLU of gate and up into
 // h): partials at `part` (part_bytes), the launch's counter block at `cnt` (kI8Ctrs counters, zero).

@@ -10,9 +10,11 @@
 // A weight is d * (0.5 + sc) * 0.25 * (+-level) = (d / 8) * ((2 sc + 1) * (+-level)) with level in {8, 25, 43} and
 // 2 sc + 1 <= 31: the integer (2 sc + 1) * level <= 1333 is exact in f16 (11 significant bits), so the B operand is
 // f16 (the lane's scale group's odd factor times its signed levels, one packed f16 multiply per pair) and the
-// matrix cores run v_mfma_f32_16x16x32_f16 with the activations staged as f16 (exact for bf16 values in f16's
-// range; the staging divides a workgroup's activations by a power of two when they reach 2^15 and the scale below
-// multiplies it back).  A whole word (both scale groups) is then one instruction, and the f32 factor d / 8 of the
+// matrix cores run v_mfma_f32_16x16x32_f16 with the activations staged as f16.  Each staged activation row is first
+// scaled by a power of two that puts its largest magnitude in [2^14, 2^15) (up for small rows, down for large ones),
+// so f16 holds the row's values exactly (bf16 values; f32 values as an f16 high part + remainder) whatever their
+// scale; each token's sums are multiplied back by the same power of two, which is exact.  A whole word (both scale
+// groups) is then one instruction, and the f32 factor d / 8 of the
 // 256-weight block is applied once per half-block (4 k-steps) instead of per k-step and scale group.  Products are
 // exact and accumulate in f32: every weight enters exactly as the reference's f32 dequantization defines it
 // (planes.py:246-259, pallas_moe.py:105-124, iqquant.py:110-120).
@@ -27,12 +29,12 @@ namespace mi {
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
-// LDS tables of the decoder, and the staging's activation scale.
+// LDS tables of the decoder, and the staging's activation row scales.
 struct Iq2Lds {
     uint4 level[1024];     // grid entry -> its 8 levels as f16 (four pairs)
     uint2 smask[16];       // 4 sign bits -> the sign bits (15, 31) of 2 f16 pairs (32 banks: reads never conflict)
     uint32_t cf2[16];      // 4-bit scale sc -> the odd factor 2 sc + 1 as an f16 pair
-    uint32_t amax;         // bits of the largest |activation| >= 2^15 the staging met (0: none)
+    uint32_t amax[kMaxT];  // per staged activation row: bits of its largest |value| over the staged columns
 };
 
 // grid: 2 words per entry, byte k of the 8 = level of position k.  Every thread of the workgroup takes part; a
@@ -55,19 +57,19 @@ __device__ __forceinline__ void iq2_fill_lds(Iq2Lds &t, const uint32_t *grid) {
         const _Float16 c = (_Float16)(float)(2u * s + 1u);
         t.cf2[s] = __builtin_bit_cast(uint32_t, (f16x2){c, c});
     }
-    if (threadIdx.x == 0) t.amax = 0u;
+    if (threadIdx.x < kMaxT) t.amax[threadIdx.x] = 0u;
 }
 
-// The power of two p the staging divides the activations by (2^-p): 0 below 2^15, else enough to bring amax below
-// 2^15.
+// The power of two p a row is staged at (values times 2^-p): the row's largest magnitude (as f32 bits, exponent e)
+// lands in [2^14, 2^15).  0 for an all-zero row.  A subnormal maximum (biased exponent 0) takes p = -141, which
+// still leaves every value below 2^15.
 __device__ __forceinline__ int iq2_xshift(uint32_t amax) {
     return amax ? (int)((amax >> 23) & 255u) - 127 - 14 : 0;
 }
 
 // One activation value (the f32 value of the staged bf16 element, or of the bf16 high part + remainder) -> f16 high
-// part and remainder at scale 2^-shift; records values of 2^15 and more in amax.
-__device__ __forceinline__ void iq2_x16(float f, int shift, Iq2Lds &t, uint32_t &hi, uint32_t &lo) {
-    if (shift == 0 && !(fabsf(f) < 32768.0f)) atomicMax(&t.amax, __float_as_uint(fabsf(f)));
+// part and remainder at scale 2^-shift.
+__device__ __forceinline__ void iq2_x16(float f, int shift, uint32_t &hi, uint32_t &lo) {
     f = ldexpf(f, -shift);
     const _Float16 h = (_Float16)f;
     const _Float16 l = (_Float16)(f - (float)h);
@@ -75,13 +77,13 @@ __device__ __forceinline__ void iq2_x16(float f, int shift, Iq2Lds &t, uint32_t 
     lo = __builtin_bit_cast(uint16_t, l);
 }
 
-// Rows row0 .. row0 + 63 of expert e over blocks [u0, u1) (256 columns each), activations staged (f16) from column
-// c0: acc[r][i] += sum_k W[row0 + 4 (lane % 16) + r][k] * x[token 4 (lane / 16) + i][k].  xa / xb as for
-// iq3m_accum.
-template <bool TWO, class Stage>
+// Rows row0 .. row0 + 63 of expert e over blocks [u0, u1) (256 columns each), activations staged (f16, each row at
+// its own power of two) from column c0: acc[r][i] += sum_k W[row0 + 4 (lane % 16) + r][k] * x[token 4 (lane / 16) +
+// i][k].  xa / xb as for iq3m_accum.  PAIR: A rows m >= 8 are the remainders of row m - 8 (iqm_run_and_store).
+template <bool TWO, bool PAIR, class Stage>
 __device__ __forceinline__ void iq2m_accum(const Iq2Table &tb, int e, int row0, int u0, int u1, int c0,
-                                           const Iq2Lds &L, const uint32_t *xa, const uint32_t *xb, f32x4 (&acc)[4],
-                                           Stage &&stage) {
+                                           const Iq2Lds &L, const uint32_t *xa, const uint32_t *xb, int t_rows,
+                                           f32x4 (&acc)[4], Stage &&stage) {
     const int lane = threadIdx.x & 63, q = lane >> 4;
     const size_t R = (size_t)tb.R;
     const int W = tb.W;
@@ -109,8 +111,7 @@ __device__ __forceinline__ void iq2m_accum(const Iq2Table &tb, int e, int row0, 
     uint4 d_c = ldl(dd + (size_t)(h0 >> 2) * R, lo);
     uint4 d_n = (h0 & ~3) + 4 < h1 ? ldl(dd + (size_t)((h0 >> 2) + 1) * R, lo) : z4;
     stage();
-    // d / 8, times the staging's 2^shift
-    const float dmul = ldexpf(0.125f, iq2_xshift(L.amax));
+    const float dmul = 0.125f;                                      // d / 8
     const uint32_t *xa0 = xa - (c0 >> 1), *xb0 = xb - (c0 >> 1);
     for (int h = h0; h < h1; ++h) {
         if (h > h0) {
@@ -164,6 +165,15 @@ __device__ __forceinline__ void iq2m_accum(const Iq2Table &tb, int e, int row0, 
             for (int i = 0; i < 4; ++i) acc[r][i] = fmaf(dv, ph[r][i], acc[r][i]);
         }
     }
+    // undo each row's staging scale: output row 4 q + i of the tile is activation row (PAIR ? m & 7 : m), clamped as
+    // the A operand's rows are
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = 4 * q + i;
+        const int shift = iq2_xshift(L.amax[min(PAIR ? (m & 7) : m, t_rows - 1)]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r][i] = ldexpf(acc[r][i], shift);
+    }
 }
 
 template <bool HILO, int TCMAX, class Stage>
@@ -173,8 +183,9 @@ __device__ __forceinline__ void iq2m_run_and_store(const Iq2Table &tb, int e, in
                                                    Stage &&stage) {
     iqm_run_and_store<HILO, TCMAX>(row0, xh, xl, xsp, t_rows, n, slots, part_base, R,
                                    [&](auto two, const uint32_t *xa, const uint32_t *xb, f32x4(&acc)[4]) {
-                                       iq2m_accum<decltype(two)::value>(tb, e, row0, u0, u1, c0, L, xa, xb, acc,
-                                                                        stage);
+                                       constexpr bool kTwo = decltype(two)::value;
+                                       iq2m_accum<kTwo, HILO && !kTwo>(tb, e, row0, u0, u1, c0, L, xa, xb, t_rows,
+                                                                       acc, stage);
                                    });
 }
 

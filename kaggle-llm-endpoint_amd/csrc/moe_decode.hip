@@ -2,6 +2,7 @@
 // layout, launches) and the exact dequant kernel.  The grouped kernels themselves live in grouped.h.
 #include "cumulti.h"
 #include "pstream.h"
+#include "tuning.h"
 
 #include <stdio.h>
 #include <stdlib.h>
@@ -305,10 +306,6 @@ static int n_units_of(const mi_table *t) {
 static int wave_rows_of(const mi_table *t, int rtw) { return t->qtype == MI_QT_CB3 ? 16 * rtw : kIq3WaveRows; }
 static int unit_cols(const mi_table *t) { return t->qtype == MI_QT_CB3 ? kCb3TileCols : 256; }
 
-static int env_int(const char *name, int dflt) {
-    const char *v = getenv(name);
-    return v ? atoi(v) : dflt;
-}
 
 static int class_rows(int max_slots_per_group) {
     int c = 1;
@@ -423,18 +420,16 @@ struct Shape {
 // as a wavefront's stream: the column units it streams (CB3: from the start of its first super tile) times the
 // kilobytes per unit (rtw for CB3), plus a fixed cost (first loads, staging, partial stores).  Minimise that over
 // S, the boundary alignment (CB3: column tiles or whole super tiles) and rtw, with a split's LDS staging within
-// 48 KB.  Environment overrides (experiments): <env>=S, <env>_AL=alignment (default 1), <env>_RTW=rtw.
+// 48 KB.  Overrides (mi_tuning_set, tests and measurements): knob = S, knob + 1 = rtw, knob + 2 = alignment.
 static Shape choose_shape(const mi_table *t, int mode, int tcmax, int groups, int rows_lds, int bytes_per_col,
-                          const char *env, size_t lds_cap = 48 * 1024, long long fixed_slots = 0, int max_rtw = 4,
+                          Knob knob, size_t lds_cap = 48 * 1024, long long fixed_slots = 0, int max_rtw = 4,
                           double fixed = 8.0, int min_rtw = 1) {
     const int nu = n_units_of(t);
     const bool cb3 = t->qtype == MI_QT_CB3;
     const int rg_per_wg = mode == kGateUp ? 2 : kWgWaves;
     // fixed: per-task cost in kilobyte-units (start, routing, staging, stores; small when tasks are pipelined)
-    char env_rtw[64], env_al[64];
-    snprintf(env_rtw, sizeof env_rtw, "%s_RTW", env);
-    snprintf(env_al, sizeof env_al, "%s_AL", env);
-    const int forced_rtw = env_int(env_rtw, 0), forced_s = env_int(env, 0), forced_al = env_int(env_al, 1);
+    const int forced_rtw = tuning((Knob)(knob + 1), 0), forced_s = tuning(knob, 0),
+              forced_al = tuning((Knob)(knob + 2), 1);
     Shape best{{1, 1}, cb3 ? max_rtw : 1, 0, 0};
     double best_cost = 1e30;
     long long best_tot = 0;
@@ -557,8 +552,8 @@ static bool plan_cumulti(const mi_table *gate, const mi_table *down, int N, Deco
     const int nu1 = n_units_of(gate), nu2 = n_units_of(down);
     const int nb1 = (nu1 + 3) / 4, nb2 = (nu2 + 3) / 4;
     // measured best at D 6144, I 2048 (8 and 16 tokens)
-    int S1 = env_int("MI355MOE_MS1", N <= 8 ? 2 : 4), S2 = env_int("MI355MOE_MS2", 2);
-    int r1 = env_int("MI355MOE_MS1_RTW", 1), r2 = env_int("MI355MOE_MS2_RTW", 2);
+    int S1 = tuning(kTuneMS1, N <= 8 ? 2 : 4), S2 = tuning(kTuneMS2, 2);
+    int r1 = tuning(kTuneMS1Rtw, 1), r2 = tuning(kTuneMS2Rtw, 2);
     S1 = S1 < 1 ? 1 : S1 > nb1 ? nb1 : S1;
     S2 = S2 < 1 ? 1 : S2 > nb2 ? nb2 : S2;
     r1 = (r1 == 2 || r1 == 4) ? r1 : 1;
@@ -601,7 +596,7 @@ static bool plan_cumulti(const mi_table *gate, const mi_table *down, int N, Deco
     const int fit = (int)((budget - cbl) / per_g);
     if (p.lds1 > budget || fit < 1) return false;
     p.mgmax = gmax < fit ? gmax : fit;
-    const int forced = env_int("MI355MOE_MGMAX", 0);          // tests: fewer groups per epoch (more epochs)
+    const int forced = tuning(kTuneMGMax, 0);          // tests: fewer groups per epoch (more epochs)
     if (forced > 0 && forced < p.mgmax) p.mgmax = forced;
     p.lds2 = per_g * p.mgmax + cbl;
     // more than half of a CU's LDS: one workgroup per CU
@@ -625,12 +620,12 @@ static DecodePlan plan_decode(const mi_table *gate, const mi_table *down, int N,
     int est = N == 1 ? p.G : (p.G * 6 + 5) / 10;
     if (est < 1) est = 1;
     p.cu = gate->qtype == MI_QT_CB3 && down->qtype == MI_QT_CB3 && !xf32 && N == 1 &&
-           env_int("MI355MOE_CUSTREAM", 1) != 0;
+           tuning(kTuneCustream, 1) != 0;
     p.cum = !p.cu && gate->qtype == MI_QT_CB3 && down->qtype == MI_QT_CB3 && !xf32 && N >= 2 &&
-            env_int("MI355MOE_CUMULTI", 1) != 0;
+            tuning(kTuneCumulti, 1) != 0;
     if (p.cum && !plan_cumulti(gate, down, N, p)) p.cum = 0;
     p.persistent = !p.cu && !p.cum && gate->qtype == MI_QT_CB3 && down->qtype == MI_QT_CB3 && !xf32 &&
-                   N > env_int("MI355MOE_PERSIST_ABOVE", kPersistentMinTokens);
+                   N > tuning(kTunePersistAbove, kPersistentMinTokens);
     if (p.cum) {
         // planned above
     } else if (p.cu) {
@@ -638,8 +633,8 @@ static DecodePlan plan_decode(const mi_table *gate, const mi_table *down, int N,
         // tiles (the staged rows are the full activation, so a split never starts inside a super tile)
         const int P = cu_count();
         const int nb1 = (n_units_of(gate) + 3) / 4, nb2 = (n_units_of(down) + 3) / 4;
-        int S1 = env_int("MI355MOE_CS1", 2), S2 = env_int("MI355MOE_CS2", 1);      // measured best at D 6144, I 2048
-        int r1 = env_int("MI355MOE_CS1_RTW", 1), r2 = env_int("MI355MOE_CS2_RTW", 1);
+        int S1 = tuning(kTuneCS1, 2), S2 = tuning(kTuneCS2, 1);      // measured best at D 6144, I 2048
+        int r1 = tuning(kTuneCS1Rtw, 1), r2 = tuning(kTuneCS2Rtw, 1);
         S1 = S1 < 1 ? 1 : S1 > nb1 ? nb1 : S1;
         S2 = S2 < 1 ? 1 : S2 > nb2 ? nb2 : S2;
         r1 = (r1 == 2 || r1 == 4) ? r1 : 1;
@@ -666,8 +661,8 @@ static DecodePlan plan_decode(const mi_table *gate, const mi_table *down, int N,
     } else if (p.persistent) {
         // persistent launches: tasks are pipelined, so the per-task fixed cost is small
         const long long slots = 3LL * cu_count();
-        p.s1 = choose_shape(gate, kGateUp, p.rows1, est, p.rows1, 4, "MI355MOE_S1", 48 * 1024, slots, 4, 2.0);
-        p.s2 = choose_shape(down, kDown, p.rows2, est, p.rows2, 8, "MI355MOE_S2", 48 * 1024, slots, 4, 2.0);
+        p.s1 = choose_shape(gate, kGateUp, p.rows1, est, p.rows1, 4, kTuneS1, 48 * 1024, slots, 4, 2.0);
+        p.s2 = choose_shape(down, kDown, p.rows2, est, p.rows2, 8, kTuneS2, 48 * 1024, slots, 4, 2.0);
         const int tc = p.rows1 <= 8 ? 8 : 16;
         const size_t scratch = 4 * (2 * (size_t)gate->n_experts + (size_t)n_route);
         plan_pstream(kGateUp, tc, p.s1, p.G, sizeof(uint32_t) * (size_t)p.rows1 * max_xs(gate, p.s1.sp), scratch,
@@ -675,8 +670,8 @@ static DecodePlan plan_decode(const mi_table *gate, const mi_table *down, int N,
         plan_pstream(kDown, tc, p.s2, p.G, sizeof(uint32_t) * 2 * (size_t)p.rows2 * max_xs(down, p.s2.sp), scratch,
                      &p.P2, &p.lds2);
     } else {
-        p.s1 = choose_shape(gate, kGateUp, p.rows1, est, p.rows1, xf32 ? 8 : 4, "MI355MOE_S1");
-        p.s2 = choose_shape(down, kDown, p.rows2, est, p.rows2, 8, "MI355MOE_S2");
+        p.s1 = choose_shape(gate, kGateUp, p.rows1, est, p.rows1, xf32 ? 8 : 4, kTuneS1);
+        p.s2 = choose_shape(down, kDown, p.rows2, est, p.rows2, 8, kTuneS2);
     }
     size_t off = 0;
     p.off_part1 = off;
@@ -725,7 +720,7 @@ struct FusedPlan {
 // Plan of the fused launch: both phases stream with the same rows per wavefront (32 or 64: the SwiGLU of a row
 // range then fills whole 128-byte lines of h's bf16 planes); the column splits come from the separate launches' cost
 // model with the slots of the persistent grid (3 workgroups per CU) and a small per-task cost (tasks are pipelined).
-// Environment overrides (experiments): MI355MOE_FS1[_AL|_RTW], MI355MOE_FS2[_AL] as for choose_shape.
+// Overrides (mi_tuning_set): FS1[_AL|_RTW], FS2[_AL] as for choose_shape.
 static FusedPlan plan_fused(const mi_table *gate, const mi_table *down, int N, int k, int shared) {
     FusedPlan p{};
     if (gate->qtype != MI_QT_CB3 || down->qtype != MI_QT_CB3 || N > kFusedMaxTokens) return p;
@@ -737,9 +732,9 @@ static FusedPlan plan_fused(const mi_table *gate, const mi_table *down, int N, i
     if (est < 1) est = 1;
     const long long slots = 3LL * cu_count();
     const size_t cap = kLdsPerCu / 3 - kFusedStaticLds - 256;
-    p.s1 = choose_shape(gate, kGateUp, p.rows, est, p.rows, 8, "MI355MOE_FS1", cap, slots, 4, 2.0, 2);
+    p.s1 = choose_shape(gate, kGateUp, p.rows, est, p.rows, 8, kTuneFS1, cap, slots, 4, 2.0, 2);
     const int rtw = p.s1.rtw;
-    p.s2 = choose_shape(down, kDown, p.rows, est, p.rows, 8, "MI355MOE_FS2", cap, slots, rtw, 2.0, rtw);
+    p.s2 = choose_shape(down, kDown, p.rows, est, p.rows, 8, kTuneFS2, cap, slots, rtw, 2.0, rtw);
     if (p.s1.RB == 0 || p.s2.RB == 0 || p.s2.rtw != rtw || rtw < 2) return p;
     const int xs1 = max_xs(gate, p.s1.sp), xs2 = max_xs(down, p.s2.sp);
     p.xs_max = xs1 > xs2 ? xs1 : xs2;
@@ -976,12 +971,12 @@ static int decode_launch(const DecodePlan &p, const mi_table *gate, const mi_tab
     // One workgroup per task (the grouped launches): at one token the down launch forms h itself while staging its
     // rows (the SwiGLU launch's arithmetic, from the gate/up partials) instead of a SwiGLU launch: the down launch
     // waits ~2.5 us longer for the split partials, the layer is 0.4-1.0 us faster (IQ2_S + IQ4_XS, IQ3_S, IQ4_XS).
-    // At 8 tokens that wait costs 8-18 us per layer, so the SwiGLU launch stays.  MI355MOE_FUSE_SWIGLU=0 / 1
+    // At 8 tokens that wait costs 8-18 us per layer, so the SwiGLU launch stays.  The FUSE_SWIGLU override (0 / 1)
     // forces either (measurement).
-    const bool fuse_h = !cb3 && !p.cu && !p.cum && env_int("MI355MOE_FUSE_SWIGLU", N == 1 ? 1 : 0) == 1;
+    const bool fuse_h = !cb3 && !p.cu && !p.cum && tuning(kTuneFuseSwiglu, N == 1 ? 1 : 0) == 1;
     // the CU-balanced down launch forms h itself while staging (bit-identical h, one launch fewer: ~2 us at one token;
-    // MI355MOE_CU_FORM_H=0 keeps the SwiGLU launch, for measurement)
-    const bool cu_form = p.cu && env_int("MI355MOE_CU_FORM_H", 1) != 0 && p.s1.sp.S <= 2 &&
+    // the CU_FORM_H override 0 keeps the SwiGLU launch, for measurement)
+    const bool cu_form = p.cu && tuning(kTuneCuFormH, 1) != 0 && p.s1.sp.S <= 2 &&
                          (long long)p.cgmax * (n_units_of(down) * kCb3TileCols / 4) <= 4LL * 64 * kCuWaves;
     if (!fuse_h && !cu_form) {
         const size_t n4 = (size_t)p.NS * gate->rows / 4;
@@ -1208,8 +1203,8 @@ int mi_moe_decode_fused(const mi_table *gate, const mi_table *up, const mi_table
     a.RBG2 = p.s2.RBG;
     a.xs_max = p.xs_max;
     a.P = p.P;
-    // polls before a wait gives up: MI355MOE_SPIN_LIMIT overrides the default (tests force a give-up with it)
-    const int spin = env_int("MI355MOE_SPIN_LIMIT", -1);
+    // polls before a wait gives up: the SPIN_LIMIT override replaces the default (tests force a give-up with it)
+    const int spin = tuning(kTuneSpinLimit, -1);
     a.spin_limit = spin >= 0 ? (uint32_t)spin : kSpinLimit;
     // a fresh counter block and error word for this launch (a fill kernel: no memset node if the call is captured)
     const int nw = (int)(cl.bytes / 4);
@@ -1250,7 +1245,7 @@ int mi_moe_decode_plan(const mi_table *gate, const mi_table *down, int32_t N, in
 static Shape matvec_shape(const mi_table *t, int n_slots) {
     const int rows = class_rows(n_slots < kMaxT ? n_slots : kMaxT);
     const int G = max_groups(n_slots, t->n_experts, 0, -1, rows);
-    return choose_shape(t, kMatvec, rows, G, rows, 8, "MI355MOE_SMV");
+    return choose_shape(t, kMatvec, rows, G, rows, 8, kTuneSMV);
 }
 
 size_t mi_matvec_workspace(const mi_table *t, int32_t n_slots) {

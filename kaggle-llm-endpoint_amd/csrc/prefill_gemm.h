@@ -737,8 +737,8 @@ __device__ __forceinline__ void prefill_body(const PfArgs &a, PfShared &sh, int 
     if (WP::kSplit && np > 1) {
         // a piece of a split task: its sums go to memory (stored through this XCD's L2), then the piece is counted;
         // the piece that arrives last adds all of them in piece order (the same order whichever arrives last) and
-        // runs the epilogue.  Nothing waits for another workgroup.  The other pieces' sums are read with plain loads:
-        // each 128-byte line is written by one piece only and read once, after its count, so no L2 holds it.
+        // runs the epilogue.  Nothing waits for another workgroup.  The other pieces' sums are read with device-coherent
+        // (sc1) loads after the count, so no older copy of a line in this XCD's L2 can be returned.
         const __amdgpu_buffer_rsrc_t pr =
             __builtin_amdgcn_make_buffer_rsrc((void *)a.part, (short)0, 0x7fffffff, kBufferWord3);
         const uint32_t lane_off = 16u * (uint32_t)lane;
@@ -766,7 +766,7 @@ __device__ __forceinline__ void prefill_body(const PfArgs &a, PfShared &sh, int 
             for (int r = 0; r < kPfRtw; ++r)
 #pragma unroll
                 for (int t = 0; t < NTT; ++t)
-                    acc[r][t] += *(const f32x4 *)((const char *)a.part + piece_off(pc, r, t));
+                    acc[r][t] += coherent_load4(pr, piece_off(pc, r, t));
         }
     }
 

@@ -2,9 +2,16 @@
 // for a plain stream, the ceiling the weight-streaming kernels are compared against.  Every thread reads 16-byte
 // pieces in a grid-stride loop (one wavefront instruction = 1 KB contiguous), four loads in flight per thread, and
 // folds them with XOR; one word per wavefront is written so that no load is dead.
+//
+// Built into its own library, libmi355probe.so, which only the benchmark and its test load: it is not part of the
+// operator's C ABI (include/mi355moe.h), whose status codes it shares.
 #include <hip/hip_runtime.h>
 
 #include "mi355moe.h"
+
+// Reads `bytes` (a multiple of 16) from src with 16-byte loads in a grid-stride loop of `workgroups` 256-thread
+// workgroups and writes one XOR word per wavefront to sink (workgroups * 4 u32).
+extern "C" int mi_read_probe(const void *src, size_t bytes, uint32_t *sink, int32_t workgroups, void *stream);
 
 namespace mi {
 

@@ -211,6 +211,26 @@ class _Workspaces:
 WORKSPACES = _Workspaces()
 
 
+class tuning:
+    """Launch-plan overrides for tests and measurement runs (mi_tuning_set): ``with tuning(S1=3, CUMULTI=0): ...``
+    sets them for the block and clears every override on exit (mi_tuning_reset).  The library reads no environment
+    variables; calls outside such a block use the built-in plans.  Overrides change launch shapes (and with them
+    workspace sizes and f32 summation orders), so workspaces are sized inside the block."""
+
+    def __init__(self, **overrides):
+        self.overrides = overrides
+
+    def __enter__(self):
+        lib().mi_tuning_reset()
+        for name, value in self.overrides.items():
+            check("mi_tuning_set(%s)" % name, lib().mi_tuning_set(name.encode(), int(value)))
+        return self
+
+    def __exit__(self, *exc):
+        lib().mi_tuning_reset()
+        return False
+
+
 # ------------------------------------------------------------------------------------------------ kernel-level ops
 def matvec(table, idx, X):
     """moe_matvec (pallas_moe.py:238-307): out[i, r] = sum_n W_{idx[i]}[r, n] X_i[n].
@@ -512,7 +532,9 @@ def int8_project(x, qT, s, want_f32=False, y_bf16=None, y_f32=None, workspace=No
     """y = x @ bf16(f32(q) * s) (quant8.py:91-99): x bf16 [B, n_in], qT int8 [n_out, n_in], s f32 [n_out]
     (``scale_axis`` MI_I8_COL_SCALES, the reference's [1, out]) or [n_in] (MI_I8_ROW_SCALES, its [in, 1]);
     MI_I8_COL_AFTER: y = (x @ f32(q)) * s[o], the int8 lm_head (engine.py:345-351).
-    Preallocated outputs / workspace make the call allocation-free."""
+    Preallocated outputs / workspace make the call allocation-free.
+    The workspace's first 256 KB are completion counters that must be zero before its first int8 call (a
+    zero-filled allocation; every call leaves them zero again): a workspace left nonzero gives wrong sums, silently."""
     B, n_in = x.shape
     n_out, w_in, tiled = _i8_dims(qT)
     if w_in != n_in:
@@ -553,7 +575,9 @@ def int8_project_many(x, projections, want_f32=False, outputs=None, workspace=No
     """Several projections of the same activations in one launch (Q, K, V of x; the shared expert's gate and up):
     projections = [(qT int8 [n_out_j, n_in], s f32), ...] (at most 8, one ``scale_axis`` for all) -> a list with,
     per projection, what ``int8_project`` returns.  ``outputs`` = [(y_bf16, y_f32 or None), ...] preallocated makes
-    the call allocation-free."""
+    the call allocation-free.
+    The workspace's first 256 KB are completion counters that must be zero before its first int8 call (a
+    zero-filled allocation; every call leaves them zero again): a workspace left nonzero gives wrong sums, silently."""
     B, n_in = x.shape
     x = x.contiguous()
     n = len(projections)
@@ -591,7 +615,9 @@ def int8_mlp(x, gate, up, down, limit, want_f32=False, y_bf16=None, y_f32=None, 
     h = bf16(swiglu_clamped(bf16(x @ Wg), bf16(x @ Wu))), W = bf16(f32(q) * s).  x bf16 [B, D]; gate, up, down:
     reference leaves {"q", "s"} or int8_leaf triples (qT, s, scale_axis); gate and up share one scale form.
     -> y bf16 [B, D] (and y f32, the down projection before its rounding, with want_f32).  Tokens go 32 per call
-    (mi_int8_mlp's limit); preallocated outputs / workspace make each call allocation-free."""
+    (mi_int8_mlp's limit); preallocated outputs / workspace make each call allocation-free.
+    The workspace's first 256 KB are completion counters that must be zero before its first int8 call (a
+    zero-filled allocation; every call leaves them zero again): a workspace left nonzero gives wrong sums, silently."""
     g, u, d = [int8_leaf(l, x.device) if isinstance(l, dict) else l for l in (gate, up, down)]
     if g[2] != u[2]:
         raise ValueError("int8_mlp: gate and up take one scale form")

@@ -4,7 +4,6 @@ and two-instruction forms of h (up to 8 / more than 8 tokens), duplicate experts
 (expert, occurrence)), expert ids outside the table, the shared expert, and a repeated call on one workspace.
 
 Bar: rel-L2 <= 1e-5 against the f64 oracle (f32 throughout, h as bf16 high part + remainder)."""
-import os
 
 import numpy as np
 import pytest
@@ -35,31 +34,28 @@ def _run(pkg, L, tbs, N, k, E, idx, w, limit, shared):
     return of, want
 
 
-ENVS = [{}, {"MI355MOE_MS1": "1", "MI355MOE_MS2": "1"}, {"MI355MOE_MS1": "3", "MI355MOE_MS1_RTW": "2"},
-        {"MI355MOE_MS2": "3", "MI355MOE_MS2_RTW": "4", "MI355MOE_MGMAX": "1"},
-        {"MI355MOE_MS2": "1", "MI355MOE_MGMAX": "1", "MI355MOE_MS1_RTW": "4"}]
+ENVS = [{}, {"MS1": 1, "MS2": 1}, {"MS1": 3, "MS1_RTW": 2}, {"MS2": 3, "MS2_RTW": 4, "MGMAX": 1},
+        {"MS2": 1, "MGMAX": 1, "MS1_RTW": 4}]
 
 
 @pytest.mark.parametrize("env", ENVS)
 @pytest.mark.parametrize("N,k,E,shared", [(2, 8, 16, True), (5, 3, 7, False), (8, 8, 24, True), (9, 4, 12, True),
                                           (16, 8, 40, True), (16, 2, 3, False)])
-def test_cumulti_vs_oracle(pkg, gpu, monkeypatch, env, N, k, E, shared):
-    for key, v in env.items():
-        monkeypatch.setenv(key, v)
+def test_cumulti_vs_oracle(pkg, gpu, env, N, k, E, shared):
     rng = np.random.default_rng(N * 100 + k * 10 + E)
     D, I, limit = 1920, 512, 10.0
     L = Layer(rng, "CB3", E + 1, D, I)
     tbs = L.tables(pkg)
     idx, w = zipf_routing(rng, N, E, k)
-    of, want = _run(pkg, L, tbs, N, k, E, idx, w, limit, shared)
+    with pkg.tuning(**env):
+        of, want = _run(pkg, L, tbs, N, k, E, idx, w, limit, shared)
     assert rel_l2(of.cpu().numpy(), want) < 1e-5
 
 
 @pytest.mark.parametrize("N", [3, 12])
-def test_cumulti_duplicates_and_invalid_ids(pkg, gpu, monkeypatch, N):
+def test_cumulti_duplicates_and_invalid_ids(pkg, gpu, N):
     """A token naming one expert in several columns forms groups (e, 0), (e, 1), ...; ids outside [0, E) add
     nothing (the reference leaves them undefined; the decode skips them)."""
-    monkeypatch.setenv("MI355MOE_MGMAX", "1")
     rng = np.random.default_rng(7 + N)
     E, D, I, k, limit = 5, 640, 256, 6, 10.0
     L = Layer(rng, "CB3", E + 1, D, I)
@@ -69,7 +65,8 @@ def test_cumulti_duplicates_and_invalid_ids(pkg, gpu, monkeypatch, N):
     idx[1, 0] = -1
     idx[N - 1, k - 1] = E + 7
     w = rng.random((N, k)).astype(np.float32)
-    of, want = _run(pkg, L, tbs, N, k, E, idx, w, limit, True)
+    with pkg.tuning(MGMAX=1):
+        of, want = _run(pkg, L, tbs, N, k, E, idx, w, limit, True)
     assert rel_l2(of.cpu().numpy(), want) < 1e-5
 
 

@@ -135,9 +135,9 @@ def test_decode_small(pkg, gpu, qtype, N, k, E, routing):
 
 @pytest.mark.parametrize("N,scale,f32x", [(1, 1e6, False), (3, 3e4, False), (8, 1e9, False), (2, 1e6, True)])
 def test_iq2s_large_activations(pkg, gpu, N, scale, f32x):
-    """IQ2_S decodes on f16 matrix-core operands: a workgroup whose activations reach 2^15 stages them divided by a
-    power of two (and scales its sums back), so activations far outside f16's range still decode exactly.  Half the
-    values are large, the rest N(0, 1); the SwiGLU limit is large enough that h stays unclamped and large too."""
+    """IQ2_S decodes on f16 matrix-core operands, each staged activation row at its own power of two: half of every
+    row is large, the rest N(0, 1), so the row's maximum sets its scale and the small values still count.  The
+    SwiGLU limit is large enough that h stays unclamped and large too."""
     rng = np.random.default_rng(17 + N)
     E, D, I, k = 6, 512, 256, 3
     L = Layer(rng, "IQ2_S", E, D, I)
@@ -153,6 +153,75 @@ def test_iq2s_large_activations(pkg, gpu, N, scale, f32x):
     of, _ = pkg.moe_decode(tbs["gate"], tbs["up"], tbs["down"], xt, _t(idx), _t(w), limit)
     assert np.isfinite(of.cpu().numpy()).all()
     assert rel_l2(of.cpu().numpy(), want) < (5e-5 if f32x else 1e-5)
+
+
+# f32 activations (and h) enter the matrix cores as a bf16 high part + remainder, 16 mantissa bits: 5e-5 there
+def _tol(f32x):
+    return 5e-5 if f32x else 1e-5
+
+
+@pytest.mark.parametrize("f32x", [False, True])
+@pytest.mark.parametrize("N", [1, 8])
+@pytest.mark.parametrize("scale", [1e9, 1e-3, 1e-5, 1e-6, 1e-9, 1e-15])
+def test_iq2s_decode_activation_scale(pkg, gpu, scale, N, f32x):
+    """The reference decodes IQ2_S in f32 (pallas_moe.py:103-124, resident.py:114), so its result scales with the
+    activations: every token's output stays within the bound of the f64 oracle whatever their scale, through the
+    IQ2_S gate/up, h at the matching scale through the IQ2_S down, and the shared expert."""
+    rng = np.random.default_rng(29 + N)
+    E, D, I, k, limit = 6, 512, 256, 3, 1e30
+    L = Layer(rng, "IQ2_S", E + 1, D, I)
+    tbs = L.tables(pkg)
+    idx, w = zipf_routing(rng, N, E, k)
+    x = (rng.standard_normal((N, D)) * scale).astype(np.float32)
+    if not f32x:
+        x = round_bf16(x)
+    want = omoe.decode_apply(L.deq, x, idx, w, limit) + omoe.shared_apply(lambda m: L.deq(m, E), x, limit)
+    xt = _t(x) if f32x else _t(x, torch.bfloat16)
+    of, _ = pkg.moe_decode(tbs["gate"], tbs["up"], tbs["down"], xt, _t(idx), _t(w), limit, shared_expert=E)
+    got = of.cpu().numpy()
+    for n in range(N):
+        assert rel_l2(got[n], want[n]) < _tol(f32x), "token %d" % n
+
+
+@pytest.mark.parametrize("f32x", [False, True])
+def test_iq2s_decode_mixed_token_scales(pkg, gpu, f32x):
+    """Eight tokens of very different scales, routed so that they share expert groups (one workgroup stages them
+    together): each staged row keeps its own scale, so a tiny token beside an O(1) one is as exact as alone."""
+    rng = np.random.default_rng(41)
+    E, D, I, k, limit = 4, 512, 256, 3, 1e30
+    L = Layer(rng, "IQ2_S", E + 1, D, I)
+    tbs = L.tables(pkg)
+    scales = np.array([1.0, 1e-6, 1e-3, 1e4, 1e-9, 1.0, 1e-5, 1e2])
+    N = len(scales)
+    idx, w = zipf_routing(rng, N, E, k)
+    x = (rng.standard_normal((N, D)) * scales[:, None]).astype(np.float32)
+    if not f32x:
+        x = round_bf16(x)
+    want = omoe.decode_apply(L.deq, x, idx, w, limit) + omoe.shared_apply(lambda m: L.deq(m, E), x, limit)
+    xt = _t(x) if f32x else _t(x, torch.bfloat16)
+    of, _ = pkg.moe_decode(tbs["gate"], tbs["up"], tbs["down"], xt, _t(idx), _t(w), limit, shared_expert=E)
+    got = of.cpu().numpy()
+    for n in range(N):
+        assert rel_l2(got[n], want[n]) < _tol(f32x), "token %d (scale %g)" % (n, scales[n])
+
+
+@pytest.mark.parametrize("f32x", [False, True])
+def test_iq2s_matvec_row_scales(pkg, gpu, f32x):
+    """moe_matvec with slots of scales 1e-30 .. 1e30, most of them on one expert (one group, one staging): every
+    slot's output within the bound of the f64 product."""
+    rng = np.random.default_rng(43)
+    E, R, K = 3, 256, 1024
+    L = Layer(rng, "IQ2_S", E, K, R)
+    tb = L.tables(pkg)["gate"]
+    scales = np.array([1.0, 1e-30, 1e-9, 1e6, 1e-5, 1e30, 1e-3, 1e-12, 3e-20, 1.0, 1e-6, 1e15])
+    idx = np.array([0, 0, 0, 0, 0, 0, 0, 0, 1, 2, 1, 0], np.int32)
+    X = (rng.standard_normal((len(idx), K)) * scales[:, None]).astype(np.float32)
+    if not f32x:
+        X = round_bf16(X)
+    got = pkg.matvec(tb, _t(idx), _t(X) if f32x else _t(X, torch.bfloat16)).cpu().numpy()
+    for i, e in enumerate(idx):
+        want = L.deq("gate", int(e)).astype(np.float64) @ X[i].astype(np.float64)
+        assert rel_l2(got[i], want) < _tol(f32x), "slot %d (scale %g)" % (i, scales[i])
 
 
 def test_decode_limit_clamps(pkg, gpu):
@@ -202,8 +271,8 @@ def test_decode_mixed_formats(pkg, gpu, qtype, down_qtype, N):
 
 
 @pytest.mark.parametrize("qtype", ["CB3", "IQ2_S", "IQ4_XS", "Q3_K"])
-def test_down_forms_h_like_the_swiglu_launch(pkg, gpu, qtype, monkeypatch):
-    """With MI355MOE_FUSE_SWIGLU=1 the down launch forms h from the gate/up partials while staging instead of a
+def test_down_forms_h_like_the_swiglu_launch(pkg, gpu, qtype):
+    """With the FUSE_SWIGLU override the down launch forms h from the gate/up partials while staging instead of a
     SwiGLU launch writing it first.  Same arithmetic: bit-identical outputs."""
     rng = np.random.default_rng(77)
     E, D, I, N, k, limit = 9, 512, 256, 4, 4, 0.5
@@ -212,6 +281,6 @@ def test_down_forms_h_like_the_swiglu_launch(pkg, gpu, qtype, monkeypatch):
     idx, w = zipf_routing(rng, N, E, k)
     x = _t(round_bf16(rng.standard_normal((N, D)).astype(np.float32)), torch.bfloat16)
     a, _ = pkg.moe_decode(tbs["gate"], tbs["up"], tbs["down"], x, _t(idx), _t(w), limit, shared_expert=E)
-    monkeypatch.setenv("MI355MOE_FUSE_SWIGLU", "1")
-    b, _ = pkg.moe_decode(tbs["gate"], tbs["up"], tbs["down"], x, _t(idx), _t(w), limit, shared_expert=E)
+    with pkg.tuning(FUSE_SWIGLU=1):
+        b, _ = pkg.moe_decode(tbs["gate"], tbs["up"], tbs["down"], x, _t(idx), _t(w), limit, shared_expert=E)
     assert torch.equal(a, b)

@@ -6,7 +6,6 @@ routing ids, graph replays and the benchmark's full shape.
 Bar: rel-L2 <= 1e-5 against the f64 oracle at small shapes (f32 accumulation throughout, resident.py:114-120); the
 north-star bar is 1e-3 with bf16 output.
 """
-import os
 
 import numpy as np
 import pytest
@@ -86,7 +85,7 @@ def test_fused_repeated_calls_one_workspace(pkg, gpu):
         assert rel_l2(of.cpu().numpy(), _want(L, x, idx, w, limit, E)) < 1e-5, "call %d" % it
 
 
-def test_fused_wait_give_up_is_reported_and_the_next_call_is_clean(pkg, gpu, monkeypatch):
+def test_fused_wait_give_up_is_reported_and_the_next_call_is_clean(pkg, gpu):
     """A poll limit of 0 set from the host makes a wait give up at its first unsuccessful poll (no kernel is kept
     from exiting: the launch just ends with invalid results).  The error word reports it; the next call with the
     default limit on the same workspace -- whose counters the forced calls may have left anywhere, as the garbage it
@@ -100,16 +99,15 @@ def test_fused_wait_give_up_is_reported_and_the_next_call_is_clean(pkg, gpu, mon
     idx, w = zipf_routing(rng, N, E, k)
     x = round_bf16(rng.standard_normal((N, D)).astype(np.float32))
     args = (tbs["gate"], tbs["up"], tbs["down"], _t(x, torch.bfloat16), _t(idx), _t(w), limit)
-    monkeypatch.setenv("MI355MOE_SPIN_LIMIT", "0")
-    gave_up = 0
-    for _ in range(8):
-        pkg.moe_decode(*args, shared_expert=E, workspace=ws, fused=True)
-        gave_up += pkg.resident.fused_error(ws, tbs["gate"], tbs["down"]) != 0
-    assert gave_up > 0, "no wait had to poll in 8 forced calls"
-    with pytest.raises(RuntimeError):
-        for _ in range(8):                           # check_error=True raises on a call whose wait gave up
-            pkg.moe_decode(*args, shared_expert=E, workspace=ws, fused=True, check_error=True)
-    monkeypatch.delenv("MI355MOE_SPIN_LIMIT")
+    with pkg.tuning(SPIN_LIMIT=0):
+        gave_up = 0
+        for _ in range(8):
+            pkg.moe_decode(*args, shared_expert=E, workspace=ws, fused=True)
+            gave_up += pkg.resident.fused_error(ws, tbs["gate"], tbs["down"]) != 0
+        assert gave_up > 0, "no wait had to poll in 8 forced calls"
+        with pytest.raises(RuntimeError):
+            for _ in range(8):                       # check_error=True raises on a call whose wait gave up
+                pkg.moe_decode(*args, shared_expert=E, workspace=ws, fused=True, check_error=True)
     of, _ = pkg.moe_decode(*args, shared_expert=E, workspace=ws, fused=True, check_error=True)
     torch.cuda.synchronize()
     _counters_clean(pkg, tbs, ws, N, k, E)
@@ -117,12 +115,12 @@ def test_fused_wait_give_up_is_reported_and_the_next_call_is_clean(pkg, gpu, mon
 
 
 @pytest.mark.parametrize("env,Ns,fused", [
-    ({"MI355MOE_FS1": "3", "MI355MOE_FS2": "2"}, (1, 5, 8), True),
-    ({"MI355MOE_FS1": "5", "MI355MOE_FS1_RTW": "2", "MI355MOE_FS2": "3"}, (1, 5, 8), True),
-    ({"MI355MOE_FS1": "3", "MI355MOE_FS1_RTW": "4", "MI355MOE_FS2": "1"}, (1, 5, 8), True),
-    ({"MI355MOE_FS1": "1", "MI355MOE_FS2": "4"}, (1, 2), True),
-    ({"MI355MOE_S1": "3", "MI355MOE_S2": "2", "MI355MOE_S1_RTW": "2", "MI355MOE_CUMULTI": "0"}, (12, 16), False),
-    ({"MI355MOE_S1": "2", "MI355MOE_S2": "1", "MI355MOE_S2_RTW": "1", "MI355MOE_CUMULTI": "0"}, (9, 16), False)])
+    ({"FS1": 3, "FS2": 2}, (1, 5, 8), True),
+    ({"FS1": 5, "FS1_RTW": 2, "FS2": 3}, (1, 5, 8), True),
+    ({"FS1": 3, "FS1_RTW": 4, "FS2": 1}, (1, 5, 8), True),
+    ({"FS1": 1, "FS2": 4}, (1, 2), True),
+    ({"S1": 3, "S2": 2, "S1_RTW": 2, "CUMULTI": 0}, (12, 16), False),
+    ({"S1": 2, "S2": 1, "S2_RTW": 1, "CUMULTI": 0}, (9, 16), False)])
 def test_forced_plans(pkg, gpu, env, Ns, fused):
     """Column splits in both phases (the one launch: the last split of a row range forms h, the last down task
     combines; the separate persistent launches: contiguous task ranges that restage when the group or split
@@ -131,9 +129,7 @@ def test_forced_plans(pkg, gpu, env, Ns, fused):
     E, D, I, limit = 10, 1920, 512, 10.0
     L = Layer(rng, "CB3", E + 1, D, I)
     tbs = L.tables(pkg)
-    old = {key: os.environ.get(key) for key in env}
-    os.environ.update(env)
-    try:
+    with pkg.tuning(**env):
         for N in Ns:
             k = 6 if N > 1 else 8
             idx, w = zipf_routing(rng, N, E, k)
@@ -141,9 +137,9 @@ def test_forced_plans(pkg, gpu, env, Ns, fused):
             plan = pkg.resident.decode_plan(tbs["gate"], tbs["down"], N, k, E)
             assert plan["fused"] == int(fused), plan
             if fused:
-                assert plan["S1"] == min(int(env["MI355MOE_FS1"]), 12), plan
+                assert plan["S1"] == min(env["FS1"], 12), plan
             else:
-                assert plan["sep_S1"] == int(env["MI355MOE_S1"]) and plan["sep_P1"] > 0, plan
+                assert plan["sep_S1"] == env["S1"] and plan["sep_P1"] > 0, plan
             ws = torch.zeros(pkg.resident.decode_workspace_bytes(tbs["gate"], tbs["down"], N, k, E),
                              dtype=torch.uint8, device="cuda")
             of, _ = pkg.moe_decode(tbs["gate"], tbs["up"], tbs["down"], _t(x, torch.bfloat16), _t(idx), _t(w),
@@ -151,12 +147,6 @@ def test_forced_plans(pkg, gpu, env, Ns, fused):
             torch.cuda.synchronize()
             _counters_clean(pkg, tbs, ws, N, k, E)
             assert rel_l2(of.cpu().numpy(), _want(L, x, idx, w, limit, E)) < 1e-5, (N, k, plan)
-    finally:
-        for key, v in old.items():
-            if v is None:
-                os.environ.pop(key, None)
-            else:
-                os.environ[key] = v
 
 
 def test_fused_invalid_ids_and_empty(pkg, gpu):

@@ -57,6 +57,38 @@ def test_int8_project_many_equals_single(pkg, gpu):
         assert rel_l2(yf.cpu().numpy(), oi8.project_f32(x, q, s)) < 1e-5
 
 
+def test_int8_split_sums_shared_lines(pkg, gpu):
+    """n_out % 32 == 16 and a workspace aligned to 16 bytes only: one 128-byte line of split partials then holds
+    partials of two row groups with different counters, and each row group's last workgroup must still read every
+    split's stored value (device-coherent loads).  Several projections, many splits, repeated calls."""
+    rng = np.random.default_rng(47)
+    B, n_in = 8, 6144
+    shapes = [80, 48, 112, 80]
+    qs = [oi8.generate(rng, n_in, n) for n in shapes]
+    x = round_bf16(rng.standard_normal((B, n_in)).astype(np.float32))
+    xt = torch.from_numpy(x).cuda().to(torch.bfloat16)
+    projs = []
+    for q, s in qs:
+        qT, sv, _ = pkg.formats.int8_pack(q, s)
+        projs.append((torch.from_numpy(qT).cuda(), torch.from_numpy(sv).cuda()))
+    L = pkg._lib.lib()
+    n_outs = (ctypes.c_int32 * len(shapes))(*shapes)
+    nbytes = L.mi_int8_project_many_workspace(B, n_in, n_outs, len(shapes), 1)
+    raw = torch.zeros(nbytes + 256, dtype=torch.uint8, device="cuda")
+    ws = raw[16:16 + nbytes]                          # 16-byte aligned, not 128
+    first = None
+    for rep in range(3):
+        many = pkg.int8_project_many(xt, projs, want_f32=True, workspace=ws)
+        for (q, s), (yb, yf) in zip(qs, many):
+            assert rel_l2(yf.cpu().numpy(), oi8.project_f32(x, q, s)) < 1e-5, "call %d" % rep
+        if first is None:
+            first = [yf.clone() for _, yf in many]
+        else:
+            for a, (_, yf) in zip(first, many):
+                assert torch.equal(a, yf)
+    assert int(ws[:CTR_BYTES].count_nonzero()) == 0
+
+
 def test_int8_split_sums_leave_counters_zero(pkg, gpu):
     """The split-K sums run in the projection launch (the last workgroup of each row group adds the partials in split
     order, counted in the workspace's first 256 KB): calls sharing one workspace -- three projections of 6144 x 6144
@@ -158,3 +190,24 @@ def test_int8_mlp(pkg, gpu, B, D, I, gu_axis, dn_axis, limit):
     assert rel_l2(yf.cpu().numpy(), want) < 1e-4
     assert np.array_equal(yb.float().cpu().numpy(), round_bf16(yf.cpu().numpy()))
     assert torch.equal(pkg.mlp_partial(p, xt, limit), yb)
+
+
+@pytest.mark.parametrize("fuse", [0, 1, 2])
+def test_int8_separate_sum_kernels_match(pkg, gpu, fuse):
+    """The I8_FUSE override moves the split sums (1: projections, 2: the MLP's gate/up pair) back to the separate
+    reduction and SwiGLU kernels: the same sums in the same split order, so bit-identical results."""
+    rng = np.random.default_rng(53)
+    B, D, I = 8, 2048, 1024
+    x = round_bf16(rng.standard_normal((B, D)).astype(np.float32))
+    xt = torch.from_numpy(x).cuda().to(torch.bfloat16)
+    leaves = [pkg.formats.int8_pack(*oi8.generate(rng, a, b)) for a, b in ((D, I), (D, I), (I, D))]
+    leaves = [(torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda(), c) for a, b, c in leaves]
+    proj = [(leaves[0][0], leaves[0][1]), (leaves[1][0], leaves[1][1])]
+    want_p = pkg.int8_project_many(xt, proj, want_f32=True)
+    want_m = pkg.int8_mlp(xt, *leaves, 7.0, want_f32=True)
+    with pkg.tuning(I8_FUSE=fuse):
+        got_p = pkg.int8_project_many(xt, proj, want_f32=True)
+        got_m = pkg.int8_mlp(xt, *leaves, 7.0, want_f32=True)
+    for (a, b), (c, d) in zip(want_p, got_p):
+        assert torch.equal(a, c) and torch.equal(b, d)
+    assert torch.equal(want_m[0], got_m[0]) and torch.equal(want_m[1], got_m[1])

@@ -14,6 +14,6 @@ def test_read_probe_reads_everything(pkg, gpu, n16, wg):
     src = torch.from_numpy(data.view(np.int32)).cuda()
     sink = torch.zeros(wg * 4, dtype=torch.int32, device="cuda")
     R, P = pkg.resident, pkg._lib
-    P.check("mi_read_probe", P.lib().mi_read_probe(R._ptr(src), 16 * n16, R._ptr(sink), wg, R._stream()))
+    P.check("mi_read_probe", P.probe_lib().mi_read_probe(R._ptr(src), 16 * n16, R._ptr(sink), wg, R._stream()))
     got = np.bitwise_xor.reduce(sink.cpu().numpy().view(np.uint32))
     assert int(got) == int(np.bitwise_xor.reduce(data))
