@@ -162,3 +162,22 @@ def test_python_wrappers_reject_bad_arguments(pkg):
         pkg.route(torch.zeros(2, 64, dtype=torch.bfloat16), torch.zeros(32, 8), None, 2)
     with pytest.raises(ValueError):
         pkg.formats.kq_pack_planes(np.zeros((1, 4, 1, 83), np.uint8), "Q2_K")
+
+
+def test_noalloc_rejects_a_layer_beyond_the_scratch(L, pkg):
+    """mi_moe_decode_noalloc returns MI_ERR_WORKSPACE, before any launch, for a layer whose data region exceeds
+    MI_NOALLOC_SCRATCH_BYTES (D = 262144: the down partials alone do).  Run here, on the CPU, the fabricated
+    pointers can never be dereferenced by a kernel whatever the order of the entry point's checks."""
+    lib = pkg._lib
+    tabs = []
+    for R, K in ((256, 262144), (256, 262144), (262144, 256)):
+        t = lib.MiTable()
+        t.qtype, t.rows, t.cols, t.n_experts = lib.MI_QT_CB3, R, K, 4
+        t.plane[0], t.plane[1] = 0x1000, 0x2000
+        tabs.append(t)
+    P = ctypes.c_void_p
+    assert L.mi_moe_decode_workspace(ctypes.byref(tabs[0]), ctypes.byref(tabs[2]), 16, 4, -1) > \
+        lib.NOALLOC_SCRATCH_BYTES
+    st = L.mi_moe_decode_noalloc(ctypes.byref(tabs[0]), ctypes.byref(tabs[1]), ctypes.byref(tabs[2]), P(0x10000),
+                                 16, 4, P(0x20000), P(0x30000), -1, 10.0, P(0x40000), None, None)
+    assert st == 5                                      # MI_ERR_WORKSPACE

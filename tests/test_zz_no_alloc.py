@@ -67,21 +67,3 @@ def test_noalloc_matches_decode_full_shape(pkg, gpu):
         of, ob, rf, rb = _both(pkg, tbs, x, torch.from_numpy(idx).cuda(), torch.from_numpy(w).cuda(), E - 1, limit)
         assert torch.isfinite(of).all()
         assert torch.equal(of, rf) and torch.equal(ob, rb)
-
-
-def test_noalloc_rejects_a_layer_beyond_the_scratch(pkg, gpu):
-    """D = 262144: the down partials alone exceed MI_NOALLOC_SCRATCH_BYTES (validated before any launch; the
-    pointers are never dereferenced)."""
-    lib = pkg._lib
-    tabs = []
-    for R, K in ((256, 262144), (256, 262144), (262144, 256)):
-        t = lib.MiTable()
-        t.qtype, t.rows, t.cols, t.n_experts = lib.MI_QT_CB3, R, K, 4
-        t.plane[0], t.plane[1] = 0x1000, 0x2000
-        tabs.append(t)
-    P = ctypes.c_void_p
-    assert lib.lib().mi_moe_decode_workspace(ctypes.byref(tabs[0]), ctypes.byref(tabs[2]), 16, 4, -1) > \
-        lib.NOALLOC_SCRATCH_BYTES
-    st = lib.lib().mi_moe_decode_noalloc(ctypes.byref(tabs[0]), ctypes.byref(tabs[1]), ctypes.byref(tabs[2]),
-                                         P(0x10000), 16, 4, P(0x20000), P(0x30000), -1, 10.0, P(0x40000), None, None)
-    assert st == 5                                      # MI_ERR_WORKSPACE
