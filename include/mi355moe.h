@@ -101,9 +101,13 @@ size_t mi_matvec_workspace(const mi_table *t, int32_t n_slots);
  * not both).  shared_expert: an expert index of the same tables applied to every token with weight 1, or -1.
  * Limits: N <= 16, N*k <= MI_MAX_SLOTS, E <= 1024.  Deterministic (fixed-order reductions, no float atomics).
  * Launches on the stream: gate/up partials, down partials and the routing-weighted combine, with a SwiGLU launch
- * between gate/up and down except where the down launch forms h itself while staging (CB3 tables at one token:
- * three launches; otherwise four, as mi_moe_decode_phases with phases = 3).  The workspace (mi_moe_decode_workspace
- * bytes) holds the partials and h; calls that share a workspace must be ordered on one stream.
+ * between gate/up and down (four launches, as mi_moe_decode_phases with phases = 3), except for CB3 tables at one
+ * token: two launches, gate/up, then down, which forms h from the gate/up partials while staging and does the
+ * combine itself (the last workgroup to finish each 16-row tile sums it in the combine launch's order; no waits).
+ * The workspace (mi_moe_decode_workspace bytes) holds a counter block (info[15] of mi_moe_decode_plan, bytes), then
+ * the partials and h; the counter block must be zero before the workspace's first call (a zero-filled allocation),
+ * and every call leaves it zero.
+ * Calls that share a workspace must be ordered on one stream.
  */
 int mi_moe_decode(const mi_table *gate, const mi_table *up, const mi_table *down, const uint16_t *x_bf16,
                   int32_t N, int32_t k, const int32_t *idx, const float *w, int32_t shared_expert, float limit,
@@ -154,11 +158,14 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
  * mi_moe_decode without a workspace argument, for callers that cannot allocate (code under HIP graph capture, serving
  * loops and harnesses that forbid hipMalloc).  No counterpart in the reference: its operator allocates through XLA.
  * The partials and h live in a static device array of MI_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends);
- * the call allocates nothing and returns MI_ERR_WORKSPACE when the layer's data region (the separate launches'
- * partials and h, mi_moe_decode_workspace minus the fused counter block) exceeds it -- the benchmark layer (D 6144,
- * I 2048) fits at every N <= 16, k = 8.  Same arguments (minus the workspace), launches and results as mi_moe_decode.
+ * the call allocates nothing and returns MI_ERR_WORKSPACE when the layer's data region (the partials and h,
+ * mi_moe_decode_workspace minus its counter block) exceeds the array less its first 256 KB -- the benchmark layer
+ * (D 6144, I 2048) fits at every N <= 16, k = 8.  Same arguments (minus the workspace), launches and results as
+ * mi_moe_decode (the first call on a GPU adds one fill launch).
  * Every call on one GPU shares that GPU's array: calls that overlap on one GPU (two streams, or two threads) race and
- * give wrong results; order them on one stream.  Nothing in the array needs to start at zero.
+ * give wrong results; order them on one stream.  The array's first 256 KB hold the down launch's row-tile counters
+ * (CB3 at one token), cleared by a fill kernel on the first call on each GPU and left zero by every call; nothing
+ * else in it needs to start at zero.
  */
 #define MI_NOALLOC_SCRATCH_BYTES (64u << 20)
 int mi_moe_decode_noalloc(const mi_table *gate, const mi_table *up, const mi_table *down, const uint16_t *x_bf16,
@@ -177,7 +184,9 @@ int mi_moe_decode_noalloc(const mi_table *gate, const mi_table *up, const mi_tab
  *   splits, row tiles per wavefront, workgroups (0: one per task), gate/up and down dynamic LDS bytes (persistent).
  *   [24] mi_moe_decode's gate/up and down kernels: 0 grouped (one workgroup per task), 1 persistent streams,
  *   2 CU-balanced streams (one workgroup per CU, CB3 at one token), 3 CU-balanced multi-token streams (CB3, 2-16
- *   tokens).
+ *   tokens);
+ *   [25] 1 if the CU-balanced down launch (CB3 at one token) does the combine itself (no combine launch); [26] 0
+ *   (reserved).
  * Returns MI_OK or MI_ERR_ARG.
  */
 int mi_moe_decode_plan(const mi_table *gate, const mi_table *down, int32_t N, int32_t k, int32_t shared_expert,

@@ -17,6 +17,13 @@
 // stages the h rows (bf16 high part and remainder) of the groups its share touches; the rows go to LDS with
 // direct-to-LDS loads issued ahead of the weight ring.  Each unit writes its own f32 partial rows (the next launch
 // reduces them in a fixed order), so no workgroup waits on another.
+//
+// The down launch can also do the routing-weighted combine itself (no combine launch): when a workgroup has streamed
+// its share, its partials stored through to memory, it counts each of its units on the unit's 16 RTW-row tile (one
+// agent-scope counter per tile, each on its own 128-byte line); the workgroup whose count completes a tile (slots x
+// splits units) sums that tile's partials with device-coherent loads in the combine launch's order (combine4) and
+// writes the output rows, then resets the counter.  Nothing waits for another workgroup, and the result is
+// bit-identical to the combine launch's.
 #pragma once
 #include <type_traits>
 
@@ -44,7 +51,60 @@ struct CArgs {
     float limit;
     const int32_t *idx;
     float *part;               // [S][nmat][NS][R]
+    // kDown with the combine in the launch (rt_ctr not null): routing weights [k], one counter per 16 RTW-row tile
+    // (zero between launches; words 32 rt), the outputs [R] (either may be null)
+    const float *w;
+    uint32_t *rt_ctr;
+    float *out_f32;
+    uint16_t *out_bf16;
 };
+
+// Row tiles one workgroup's down share can complete (the host keeps the share within this many units).
+constexpr int kCuMaxLast = 64;
+constexpr int kRtCtrStride = 32;         // words between row-tile counters (one 128-byte line each)
+
+// out = routing-weighted sum of a row quad's down partials: slots in routing order (an id outside [0, E) adds
+// nothing), splits in order, the shared expert last -- the combine launch's arithmetic (combine_kernel).  Per chunk
+// of 9 slots and split, every partial is loaded before the first add: one round trip per (chunk, split).
+constexpr int kCuCombineChunk = 9;
+__device__ __forceinline__ float4 cu_combine4(const CArgs &a, const int *s_exp, __amdgpu_buffer_rsrc_t rp, int r) {
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    const int nj = a.k + (a.shared_expert >= 0 ? 1 : 0);
+    for (int j0 = 0; j0 < nj; j0 += kCuCombineChunk) {
+        bool on[kCuCombineChunk];
+        float wt[kCuCombineChunk];
+        float4 ys[kCuCombineChunk];
+#pragma unroll
+        for (int jj = 0; jj < kCuCombineChunk; ++jj) {
+            const int j = j0 + jj;
+            on[jj] = j < nj && (j >= a.k || (s_exp[j] >= 0 && s_exp[j] < a.E));
+            wt[jj] = on[jj] && j < a.k ? a.w[j] : 1.0f;
+            ys[jj] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        for (int s = 0; s < a.S; ++s) {
+            f32x4 p[kCuCombineChunk];
+#pragma unroll
+            for (int jj = 0; jj < kCuCombineChunk; ++jj)
+                p[jj] = on[jj] ? coherent_load4(rp, (uint32_t)((((size_t)s * a.NS + j0 + jj) * a.R + r) * 4))
+                               : (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int jj = 0; jj < kCuCombineChunk; ++jj) {
+                ys[jj].x += p[jj][0]; ys[jj].y += p[jj][1]; ys[jj].z += p[jj][2]; ys[jj].w += p[jj][3];
+            }
+        }
+#pragma unroll
+        for (int jj = 0; jj < kCuCombineChunk; ++jj) {
+            if (!on[jj]) continue;
+            if (j0 + jj < a.k) {
+                acc.x = fmaf(wt[jj], ys[jj].x, acc.x); acc.y = fmaf(wt[jj], ys[jj].y, acc.y);
+                acc.z = fmaf(wt[jj], ys[jj].z, acc.z); acc.w = fmaf(wt[jj], ys[jj].w, acc.w);
+            } else {
+                acc.x += ys[jj].x; acc.y += ys[jj].y; acc.z += ys[jj].z; acc.w += ys[jj].w;
+            }
+        }
+    }
+    return acc;
+}
 
 #ifndef MI_CU_WAVES
 #define MI_CU_WAVES 12
@@ -56,8 +116,9 @@ __global__ void __launch_bounds__(64 * kCuWaves, 1) custream_kernel(CArgs a) {
     // staged rows, then the wavefronts' codebook slots, all read with 16-byte LDS loads: the dynamic segment must
     // start 16-byte aligned (at an 8-byte-aligned start this launch measured 2.8x slower)
     extern __shared__ __attribute__((aligned(16))) uint32_t xlds[];
-    __shared__ uint32_t s_next;
+    __shared__ uint32_t s_next, s_nlast;
     __shared__ int s_exp[MI_MAX_SLOTS + 1];         // expert of every slot (group)
+    __shared__ int s_last[MODE == kDown ? kCuMaxLast : 1];     // row tiles this workgroup combines
     constexpr bool hilo = MODE == kDown;            // h: hi in columns 0-7 of the tile, lo in 8-15
     constexpr int nmat = MODE == kGateUp ? 2 : 1;
     const int tid = threadIdx.x, lane = tid & 63, jt = lane & 15, q = lane >> 4;
@@ -71,11 +132,15 @@ __global__ void __launch_bounds__(64 * kCuWaves, 1) custream_kernel(CArgs a) {
     const int u_begin = (int)((long long)blockIdx.x * U / a.P);
     const int u_end = (int)((long long)(blockIdx.x + 1) * U / a.P);
     if (u_begin >= u_end) return;
+    const bool combine = hilo && a.rt_ctr != nullptr;      // uniform over the launch
     const int g0 = u_begin / per_g;
     const int ng = hilo ? min(a.gmax, n_groups - g0) : 1;
     const int rows = hilo ? 2 * ng : 1;             // gate/up: the token's x row; down: hi and lo of each group's h
     uint4 *cbl = (uint4 *)(xlds + (size_t)rows * a.xsp);    // 16-byte aligned: the pitch is a multiple of 4 dwords
-    if (tid == 0) s_next = (uint32_t)u_begin + kCuWaves;    // the first kCuWaves units are taken without a claim
+    if (tid == 0) {
+        s_next = (uint32_t)u_begin + kCuWaves;    // the first kCuWaves units are taken without a claim
+        s_nlast = 0;
+    }
     // every slot's expert into LDS (read there after the staging barrier: a claim then touches LDS only -- a global
     // load inside the stream would make the wavefront wait for every weight load issued before it)
     if (tid < n_groups) s_exp[tid] = tid < a.n_route ? a.idx[tid] : a.shared_expert;
@@ -200,11 +265,44 @@ __global__ void __launch_bounds__(64 * kCuWaves, 1) custream_kernel(CArgs a) {
             *(uint2 *)(xlds + (2 * j + 1) * a.xsp + (c >> 1)) = lv;
         }
     };
+    // the combine in the launch: count the share's units on their row tiles once every partial is stored; the
+    // arrival that completes a tile sums it (all wavefronts reach the barriers)
+    auto combine_share = [&]() __attribute__((always_inline)) {
+        vm_wait<0>();
+        __syncthreads();
+        const uint32_t total = (uint32_t)(a.NS * a.S);
+        for (int u0 = u_begin + tid; u0 < u_end; u0 += blockDim.x) {
+            const int rt = u0 % a.RT;
+            uint32_t *c = a.rt_ctr + kRtCtrStride * rt;
+            if (__hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == total - 1u) {
+                __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const uint32_t n = atomicAdd(&s_nlast, 1u);
+                if (n < (uint32_t)kCuMaxLast) s_last[n] = rt;
+            }
+        }
+        __syncthreads();
+        const int nlast = min((int)s_nlast, kCuMaxLast);
+        const __amdgpu_buffer_rsrc_t rp =
+            __builtin_amdgcn_make_buffer_rsrc((void *)a.part, (short)0, 0x7fffffff, kBufferWord3);
+        constexpr int q4 = 4 * RTW;                 // row quads per row tile
+        for (int i = tid; i < nlast * q4; i += blockDim.x) {
+            const int r = s_last[i / q4] * 16 * RTW + 4 * (i % q4);
+            const float4 o = cu_combine4(a, s_exp, rp, r);
+            if (a.out_f32) *(float4 *)(a.out_f32 + r) = o;
+            if (a.out_bf16) {
+                uint2 bv;
+                bv.x = f32_to_bf16_rne(o.x) | (f32_to_bf16_rne(o.y) << 16);
+                bv.y = f32_to_bf16_rne(o.z) | (f32_to_bf16_rne(o.w) << 16);
+                *(uint2 *)(a.out_bf16 + r) = bv;
+            }
+        }
+    };
     if (!active) {
         issue();
         if (form_h) form();
         vm_wait<0>();
         __syncthreads();
+        if (combine) combine_share();
         return;
     }
     cb3_stream<false, RTW>(
@@ -226,9 +324,16 @@ __global__ void __launch_bounds__(64 * kCuWaves, 1) custream_kernel(CArgs a) {
             if (jt == 0 && cur.e >= 0 && cur.e < a.E) {
                 float *dst = a.part + ((size_t)(cur.split * nmat + cur.mat) * a.NS + cur.gi) * a.R +
                              cur.rt * 16 * RTW + 4 * q;
+                if (combine) {                      // read by other workgroups of this launch
+                    const __amdgpu_buffer_rsrc_t pr =
+                        __builtin_amdgcn_make_buffer_rsrc((void *)dst, (short)0, 0x7fffffff, kBufferWord3);
 #pragma unroll
-                for (int r = 0; r < RTW; ++r)
-                    *(float4 *)(dst + 16 * r) = make_float4(acc[r][0], acc[r][1], acc[r][2], acc[r][3]);
+                    for (int r = 0; r < RTW; ++r) wt_store4(pr, 64u * r, acc[r]);
+                } else {
+#pragma unroll
+                    for (int r = 0; r < RTW; ++r)
+                        *(float4 *)(dst + 16 * r) = make_float4(acc[r][0], acc[r][1], acc[r][2], acc[r][3]);
+                }
             }
         },
         [&](const Cb3Wave &) { cur = unit_of(u, Lds{}); },
@@ -238,6 +343,7 @@ __global__ void __launch_bounds__(64 * kCuWaves, 1) custream_kernel(CArgs a) {
             else vm_wait<4 * RTW + 5>();            // the staging loads, issued ahead of the ring
             __syncthreads();
         });
+    if (combine) combine_share();
 }
 
 }  // namespace mi

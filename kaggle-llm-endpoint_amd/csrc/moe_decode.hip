@@ -164,8 +164,8 @@ __global__ void __launch_bounds__(64) combine_kernel(const float *__restrict__ p
                 const int e = idx[tok * k + j];
                 if (e >= 0 && e < E) {
                     const float wt = w[tok * k + j];
-                    acc.x += wt * ys[jj].x; acc.y += wt * ys[jj].y;
-                    acc.z += wt * ys[jj].z; acc.w += wt * ys[jj].w;
+                    acc.x = fmaf(wt, ys[jj].x, acc.x); acc.y = fmaf(wt, ys[jj].y, acc.y);
+                    acc.z = fmaf(wt, ys[jj].z, acc.z); acc.w = fmaf(wt, ys[jj].w, acc.w);
                 }
             } else if (j < nj) {
                 acc.x += ys[jj].x; acc.y += ys[jj].y; acc.z += ys[jj].z; acc.w += ys[jj].w;
@@ -515,6 +515,7 @@ struct DecodePlan {
     int G, rows1, rows2, NS;
     int cu;                     // CB3, one token: the CU-balanced launches (custream.h), one workgroup per CU
     int cgmax;                  // their down launch: most groups one workgroup's share touches
+    int cu_combine;             // their down launch does the routing-weighted combine (no combine launch)
     int cum;                    // CB3, 2..16 tokens: the CU-balanced multi-token launches (cumulti.h)
     int mgmax;                  // their down launch: groups staged at a time
     int xsp1, xsp2;             // their staged row pitches (dwords)
@@ -658,6 +659,9 @@ static DecodePlan plan_decode(const mi_table *gate, const mi_table *down, int N,
         const size_t half = kLdsPerCu / 2 + 1024;
         if (p.lds1 < half) p.lds1 = half;
         if (p.lds2 < half) p.lds2 = half;
+        // the down launch combines its row tiles itself when no share completes more than kCuMaxLast of them
+        const long long share2 = ((long long)p.NS * S2 * p.s2.RB + P - 1) / P;
+        p.cu_combine = tuning(kTuneCuCombine, 1) != 0 && share2 <= kCuMaxLast;
     } else if (p.persistent) {
         // persistent launches: tasks are pipelined, so the per-task fixed cost is small
         const long long slots = 3LL * cu_count();
@@ -688,8 +692,10 @@ static DecodePlan plan_decode(const mi_table *gate, const mi_table *down, int N,
 // Counter block of the fused decode kernel at the start of the decode workspace (its size depends on the table shapes
 // only, so a workspace sized for any N keeps it in place): per-group h counters, per-row-range down counters, the
 // error word (each on its own 128-byte line), then the dense per-(group, row range) split counters.
+// After them, the row-tile counters of the single-token down launch's combine (custream.h: one per 16 rows of down,
+// each on its own 128-byte line).
 struct CtrLayout {
-    size_t hcnt, cnt2, err, cnt1, bytes;     // word offsets, total bytes
+    size_t hcnt, cnt2, err, cnt1, rt, bytes;     // word offsets, total bytes
 };
 static CtrLayout ctr_layout(const mi_table *gate, const mi_table *down) {
     CtrLayout c{};
@@ -698,7 +704,8 @@ static CtrLayout ctr_layout(const mi_table *gate, const mi_table *down) {
     c.cnt2 = c.hcnt + (size_t)kMaxGroups * kCtrStride;
     c.err = c.cnt2 + rbg2_max * kCtrStride;
     c.cnt1 = c.err + kCtrStride;
-    c.bytes = align256(4 * (c.cnt1 + (size_t)kMaxGroups * rbg1_max));
+    c.rt = (c.cnt1 + (size_t)kMaxGroups * rbg1_max + 63) & ~(size_t)63;
+    c.bytes = align256(4 * (c.rt + (size_t)kRtCtrStride * (down->rows / 16)));
     return c;
 }
 
@@ -846,10 +853,12 @@ static int decode_validate(const mi_table *gate, const mi_table *up, const mi_ta
 // The separate launches of one decode layer (arguments already validated): ws is the data region (partials, h) of
 // p.total bytes -- past the counter block of a caller's workspace, or the library's static scratch.
 // x: bf16 [N, D], or f32 [N, D] when xf32 (the plan must have been made for it).
+// ws: the data region (partials, h); rt_ctr: the row-tile counters of the single-token down launch's combine (zero
+// between launches), or null where that launch is to leave the combine to the combine launch.
 static int decode_launch(const DecodePlan &p, const mi_table *gate, const mi_table *up, const mi_table *down,
                          const void *x, bool xf32, int N, int k, const int32_t *idx, const float *w,
                          int shared_expert, float limit, float *out_f32, uint16_t *out_bf16, char *ws, int phases,
-                         hipStream_t s) {
+                         hipStream_t s, uint32_t *rt_ctr = nullptr) {
     const uint16_t *x_bf16 = xf32 ? nullptr : (const uint16_t *)x;
     int st;
     KArgs a{};
@@ -1038,7 +1047,14 @@ static int decode_launch(const DecodePlan &p, const mi_table *gate, const mi_tab
         cb.gu_S = p.s1.sp.S;
         cb.limit = limit;
         cb.part = b.part;
+        if (p.cu_combine && rt_ctr) {
+            cb.w = w;
+            cb.rt_ctr = rt_ctr;
+            cb.out_f32 = out_f32;
+            cb.out_bf16 = out_bf16;
+        }
         custream_launch(kDown, p.s2.rtw, dim3(p.P2), p.lds2, s, cb);
+        if (cb.rt_ctr) return launch_status();      // the launch combined its row tiles
     } else if (cb3) {
         PArgs pb = pa;
         pb.t0 = b.t0.cb3;
@@ -1067,23 +1083,30 @@ static int decode_launch(const DecodePlan &p, const mi_table *gate, const mi_tab
 }
 
 // ------------------------------------------------------------------------------------------------ static scratch
-// The data region of mi_moe_decode_noalloc: one array per GPU, alive until the process ends.  In host code the
-// array's name only stands in for it; its device address comes from hipGetSymbolAddress, taken once per device with
-// that device current, and only that address is ever handed to a kernel.
+// The working memory of mi_moe_decode_noalloc: one array per GPU, alive until the process ends.  Its first
+// kNoallocCtrBytes hold the single-token down launch's row-tile counters (zeroed once per device, and left zero by
+// every launch), the rest is the data region (partials, h).  In host code the array's name only stands in for it; its device address
+// comes from hipGetSymbolAddress, taken once per device with that device current, and only that address is ever
+// handed to a kernel.
 static __device__ __align__(256) uint8_t scratch[MI_NOALLOC_SCRATCH_BYTES];
+constexpr size_t kNoallocCtrBytes = 256 * 1024;
 
 constexpr int kMaxDevices = 64;
 static std::mutex g_scratch_mu;
 static void *g_scratch_ptr[kMaxDevices];
 
-// Device address of the current device's scratch array (nullptr when it cannot be resolved).
-static void *scratch_ptr() {
+// Device address of the current device's scratch array (nullptr when it cannot be resolved).  The first call on a
+// device also clears the counter region with a fill kernel on `s` (no memset node if the call is captured).
+static void *scratch_ptr(hipStream_t s) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (!g_scratch_ptr[dev]) {
         void *ptr = nullptr;
         if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+        const int nw = (int)(kNoallocCtrBytes / 4);
+        hipLaunchKernelGGL(zero_words_kernel, dim3((nw + 255) / 256), dim3(256), 0, s, (uint32_t *)ptr, nw);
+        if (hipGetLastError() != hipSuccess) return nullptr;
         g_scratch_ptr[dev] = ptr;
     }
     return g_scratch_ptr[dev];
@@ -1101,11 +1124,12 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
                                    phases);
     if (st) return st;
     const DecodePlan p = plan_decode(gate, down, N, k, shared_expert);
-    const size_t ctr_bytes = ctr_layout(gate, down).bytes;
-    if (!workspace || workspace_bytes < ctr_bytes + p.total) return MI_ERR_WORKSPACE;
-    // the fused launch's counters at the start of the workspace stay untouched
+    const CtrLayout cl = ctr_layout(gate, down);
+    if (!workspace || workspace_bytes < cl.bytes + p.total) return MI_ERR_WORKSPACE;
+    // the single-token down launch's combine uses its row-tile counters of the block at the start of the workspace; the
+    // fused launch's counters stay untouched
     return decode_launch(p, gate, up, down, x_bf16, false, N, k, idx, w, shared_expert, limit, out_f32, out_bf16,
-                         (char *)workspace + ctr_bytes, phases, (hipStream_t)stream);
+                         (char *)workspace + cl.bytes, phases, (hipStream_t)stream, (uint32_t *)workspace + cl.rt);
 }
 
 int mi_moe_decode_x(const mi_table *gate, const mi_table *up, const mi_table *down, const void *x, int32_t x_dtype,
@@ -1128,11 +1152,13 @@ int mi_moe_decode_noalloc(const mi_table *gate, const mi_table *up, const mi_tab
     const int st = decode_validate(gate, up, down, x_bf16, N, k, idx, w, shared_expert, limit, out_f32, out_bf16, 3);
     if (st) return st;
     const DecodePlan p = plan_decode(gate, down, N, k, shared_expert);
-    if (p.total > (size_t)MI_NOALLOC_SCRATCH_BYTES) return MI_ERR_WORKSPACE;
-    char *ws = (char *)scratch_ptr();
-    if (!ws) return MI_ERR_LAUNCH;
+    if (p.total > (size_t)MI_NOALLOC_SCRATCH_BYTES - kNoallocCtrBytes) return MI_ERR_WORKSPACE;
+    char *base = (char *)scratch_ptr((hipStream_t)stream);
+    if (!base) return MI_ERR_LAUNCH;
+    // the down launch's row-tile counters in the array's first kNoallocCtrBytes (when the table's row tiles fit there)
+    const bool ctr_fits = 4 * (size_t)kRtCtrStride * (down->rows / 16) <= kNoallocCtrBytes;
     return decode_launch(p, gate, up, down, x_bf16, false, N, k, idx, w, shared_expert, limit, out_f32, out_bf16,
-                         ws, 3, (hipStream_t)stream);
+                         base + kNoallocCtrBytes, 3, (hipStream_t)stream, ctr_fits ? (uint32_t *)base : nullptr);
 }
 
 int mi_moe_decode(const mi_table *gate, const mi_table *up, const mi_table *down, const uint16_t *x_bf16,
@@ -1219,7 +1245,7 @@ int mi_moe_decode_plan(const mi_table *gate, const mi_table *down, int32_t N, in
     if (validate_table(gate) || validate_table(down) || !info || N <= 0 || N > kMaxT || k <= 0 ||
         N * k > MI_MAX_SLOTS)
         return MI_ERR_ARG;
-    int32_t v[25] = {0};
+    int32_t v[27] = {0};
     {
         const DecodePlan d = plan_decode(gate, down, N, k, shared_expert);
         const bool pers = d.persistent || d.cu || d.cum;
@@ -1227,6 +1253,7 @@ int mi_moe_decode_plan(const mi_table *gate, const mi_table *down, int32_t N, in
                               (int32_t)d.lds1, (int32_t)d.lds2};
         for (int i = 0; i < 8; ++i) v[16 + i] = f[i];
         v[24] = d.cum ? 3 : d.cu ? 2 : d.persistent ? 1 : 0;
+        v[25] = d.cu && d.cu_combine ? 1 : 0;
     }
     const FusedPlan p = plan_fused(gate, down, N, k, shared_expert);
     if (p.ok) {
@@ -1236,7 +1263,7 @@ int mi_moe_decode_plan(const mi_table *gate, const mi_table *down, int32_t N, in
     }
     v[14] = (int32_t)ctr_layout(gate, down).err;
     v[15] = (int32_t)ctr_layout(gate, down).bytes;
-    for (int i = 0; i < n_info && i < 25; ++i) info[i] = v[i];
+    for (int i = 0; i < n_info && i < 27; ++i) info[i] = v[i];
     return MI_OK;
 }
 

@@ -14,7 +14,7 @@ enum Knob : int {
     kTuneSMV, kTuneSMVRtw, kTuneSMVAl,       // matvec
     kTuneMS1, kTuneMS1Rtw, kTuneMS2, kTuneMS2Rtw, kTuneMGMax,   // CU-balanced multi-token launches
     kTuneCS1, kTuneCS1Rtw, kTuneCS2, kTuneCS2Rtw,               // CU-balanced one-token launches
-    kTuneCustream, kTuneCumulti, kTunePersistAbove, kTuneFuseSwiglu, kTuneCuFormH, kTuneSpinLimit,
+    kTuneCustream, kTuneCumulti, kTunePersistAbove, kTuneFuseSwiglu, kTuneCuFormH, kTuneSpinLimit, kTuneCuCombine,
     kTuneI8S, kTuneI8Waves, kTuneI8Fuse,
     kTuneCount
 };

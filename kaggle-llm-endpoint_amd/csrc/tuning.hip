@@ -28,6 +28,7 @@ const Entry kNames[] = {
     {"CS1", kTuneCS1}, {"CS1_RTW", kTuneCS1Rtw}, {"CS2", kTuneCS2}, {"CS2_RTW", kTuneCS2Rtw},
     {"CUSTREAM", kTuneCustream}, {"CUMULTI", kTuneCumulti}, {"PERSIST_ABOVE", kTunePersistAbove},
     {"FUSE_SWIGLU", kTuneFuseSwiglu}, {"CU_FORM_H", kTuneCuFormH}, {"SPIN_LIMIT", kTuneSpinLimit},
+    {"CU_COMBINE", kTuneCuCombine},
     {"I8S", kTuneI8S}, {"I8_WAVES", kTuneI8Waves}, {"I8_FUSE", kTuneI8Fuse},
 };
 static_assert(sizeof(kNames) / sizeof(kNames[0]) == kTuneCount, "every knob has a name");

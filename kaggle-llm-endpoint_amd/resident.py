@@ -307,11 +307,11 @@ def decode_workspace_bytes(gate, down, N, k, shared_expert=-1):
 
 def decode_plan(gate, down, N, k, shared_expert=-1):
     """The launch plan of mi_moe_decode (dict), without launching anything."""
-    info = (ctypes.c_int32 * 25)()
-    check("mi_moe_decode_plan", lib().mi_moe_decode_plan(gate.c, down.c, int(N), int(k), int(shared_expert), info, 25))
+    info = (ctypes.c_int32 * 27)()
+    check("mi_moe_decode_plan", lib().mi_moe_decode_plan(gate.c, down.c, int(N), int(k), int(shared_expert), info, 27))
     keys = ("fused", "workgroups", "lists", "S1", "align1", "rtw1", "rbg1", "S2", "align2", "rtw2", "rbg2", "lds",
             "groups", "token_class", "err_word", "ctr_bytes", "sep_S1", "sep_rtw1", "sep_P1", "sep_S2", "sep_rtw2",
-            "sep_P2", "sep_lds1", "sep_lds2", "sep_kind")
+            "sep_P2", "sep_lds1", "sep_lds2", "sep_kind", "cu_combine", "reserved")
     return {key: int(info[i]) for i, key in enumerate(keys)}
 
 
