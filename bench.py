@@ -48,6 +48,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only-b1", action="store_true", help="headline only (profiling runs)")
     ap.add_argument("--only-b816", action="store_true", help="the CB3 layer at batch 8 and 16 only (profiling runs)")
+    ap.add_argument("--only-batch", type=int, default=0,
+                    help="the CB3 layer at this batch only, with its gate/up and down algorithmic bytes (profiling runs)")
     ap.add_argument("--only-layout", default=None,
                     help="decode at batch 1 and 8 of one table layout only, e.g. iq2s_iq4xs (profiling runs)")
     ap.add_argument("--only-prefill", action="store_true", help="the 512-token prefill chunk only (profiling runs)")
@@ -345,6 +347,17 @@ def main():
                                                               iq_pe("iq4xs")),
                           "prefill_t512_iq2s_iq4xs": bench_prefill(torch, pkg, gen, args, iq_layers("iq2s_iq4xs"),
                                                                    rng, iq_pe("iq2s_iq4xs"))}))
+        return
+    if args.only_batch:
+        N = args.only_batch
+        ms, b = measure(N, zipf_topk if N > 1 else softmax_topk)
+        n_exp = b / per_expert          # distinct experts + the shared one, mean over the timed steps
+        print(json.dumps({"b%d" % N: {"us_per_layer": round(ms * 1e3, 2), "GBps": round(b / (ms * 1e-3) / 1e9, 1),
+                                       "experts_read_mean": round(n_exp, 3),
+                                       "gateup_bytes_mean": int(n_exp * 2 * cb3_bytes(INTER, D)),
+                                       "down_bytes_mean": int(n_exp * cb3_bytes(D, INTER))}}))
+        if args.calib:
+            calib_copy(torch)
         return
     if args.only_b816:
         res = {}
