@@ -521,8 +521,8 @@ def bench_route(torch, pkg, gen, args):
 
 def bench_int8(torch, pkg, gen, args):
     """Config: the int8 dense projections at batch 8 (Q, K, V, O 6144x6144; the shared expert's MLP 6144 -> 2048 ->
-    6144), per-output-channel scales (the shared down: per-input-row, its row-parallel form), bf16 activations,
-    weights in the tiled layout (MI355MOE_I8_ROWS=1: the row-major qT, for comparison).  A
+    6144), per-output-channel scales on every projection, bf16 activations, weights in the tiled layout
+    (MI355MOE_I8_ROWS=1: the row-major qT, for comparison).  A
     step is the layer's three dependent stages -- Q/K/V of the attention input in one launch, O, and the shared
     expert's mlp_partial (mi_int8_mlp: gate and up in one launch that forms h, then down) -- so projections that share
     their input share a launch, as they can in the model; every launch adds its split-K partials itself.  3 weight
@@ -531,7 +531,7 @@ def bench_int8(torch, pkg, gen, args):
     B, D, I = 8, 6144, 2048
     copies = 3
     fns = []
-    total = sum(i * o + 4 * o for st in stages for i, o in st) + 3 * D * I + 4 * (2 * I + I)
+    total = sum(i * o + 4 * o for st in stages for i, o in st) + 3 * D * I + 4 * (2 * I + D)
     # weights in the tiled layout (mi_int8_tile, repacked once at load as the IQ planes are)
     tile = (lambda w: w) if os.environ.get("MI355MOE_I8_ROWS") == "1" else pkg.int8_tile
     mk_q = lambda n_out, n_in: tile(torch.randint(-127, 128, (n_out, n_in), dtype=torch.int8, device="cuda",
@@ -551,9 +551,9 @@ def bench_int8(torch, pkg, gen, args):
                              dtype=torch.uint8, device="cuda")
             ops.append((x, projs, outs, ws))
         x = torch.randn((B, D), device="cuda", generator=gen).to(torch.bfloat16)
-        mlp = ((mk_q(I, D), mk_s(I), 1), (mk_q(I, D), mk_s(I), 1), (mk_q(D, I), mk_s(I), 0))
+        mlp = ((mk_q(I, D), mk_s(I), 1), (mk_q(I, D), mk_s(I), 1), (mk_q(D, I), mk_s(D), 1))
         y = torch.empty((B, D), dtype=torch.bfloat16, device="cuda")
-        wsm = torch.zeros(pkg._lib.lib().mi_int8_mlp_workspace(B, D, I, 1, 0), dtype=torch.uint8, device="cuda")
+        wsm = torch.zeros(pkg._lib.lib().mi_int8_mlp_workspace(B, D, I, 1, 1), dtype=torch.uint8, device="cuda")
         fns.append(lambda ops=ops, x=x, mlp=mlp, y=y, wsm=wsm: (
             [pkg.int8_project_many(xx, projs, outputs=outs, workspace=ws) for (xx, projs, outs, ws) in ops],
             pkg.int8_mlp(x, *mlp, LIMIT, y_bf16=y, workspace=wsm)))

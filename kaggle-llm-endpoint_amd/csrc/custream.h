@@ -45,7 +45,7 @@ struct CArgs {
     const uint16_t *x_lo;      // kDown: bf16 remainder of h [NS, K]
     // kDown: h formed while staging from the gate/up split partials [gu_S][2][NS][K] instead of read from x / x_lo
     // (the splits summed in order, the clamped SwiGLU, bf16 high part + remainder: the SwiGLU launch's arithmetic);
-    // gu_S <= 2 and gmax * (columns / 4) <= 4 * 768 (the host checks both)
+    // gmax * (columns / 4) <= 4 * 768 (the host checks it)
     const float *gu_part;
     int gu_S;
     float limit;
@@ -223,24 +223,39 @@ __global__ void __launch_bounds__(64 * kCuWaves, 1) custream_kernel(CArgs a) {
     // h rows of the share's groups from the gate/up partials: loads issued after the wavefront's ring, so they return
     // in the same round trip as its first tiles
     auto form = [&]() {
-        // every thread's partial loads first (at most kFormIt quads of 4 columns, two splits), then the arithmetic:
-        // one round trip
+        // per pair of splits, every thread's partial loads first (at most kFormIt quads of 4 columns), then their
+        // adds: one round trip per pair; the splits are summed in order from zero, as the SwiGLU launch sums them
         constexpr int kFormIt = 4;
         const int cols = a.nu * kCb3TileCols, q4 = cols >> 2;
         const size_t plane = (size_t)a.NS * a.K;
-        float4 pg[kFormIt][2], pu[kFormIt][2];
+        float4 g[kFormIt], uu[kFormIt];
 #pragma unroll
-        for (int it = 0; it < kFormIt; ++it) {
-            const int i = tid + it * (int)blockDim.x, j = i / q4, c = 4 * (i - j * q4);
-            const bool in = i < ng * q4 && c < a.K;
-            const size_t o = in ? (size_t)(g0 + j) * a.K + c : 0;       // slot g0 + j (one token)
+        for (int it = 0; it < kFormIt; ++it) g[it] = uu[it] = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int sp0 = 0; sp0 < a.gu_S; sp0 += 2) {
+            float4 pg[kFormIt][2], pu[kFormIt][2];
 #pragma unroll
-            for (int sp = 0; sp < 2; ++sp) {
-                const bool ld = in && sp < a.gu_S;
-                pg[it][sp] = ld ? *(const float4 *)(a.gu_part + (size_t)(2 * sp) * plane + o) : make_float4(0.f, 0.f, 0.f, 0.f);
-                pu[it][sp] = ld ? *(const float4 *)(a.gu_part + (size_t)(2 * sp + 1) * plane + o)
-                                : make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int it = 0; it < kFormIt; ++it) {
+                const int i = tid + it * (int)blockDim.x, j = i / q4, c = 4 * (i - j * q4);
+                const bool in = i < ng * q4 && c < a.K;
+                const size_t o = in ? (size_t)(g0 + j) * a.K + c : 0;       // slot g0 + j (one token)
+#pragma unroll
+                for (int d = 0; d < 2; ++d) {
+                    const int sp = sp0 + d;
+                    const bool ld = in && sp < a.gu_S;
+                    pg[it][d] = ld ? *(const float4 *)(a.gu_part + (size_t)(2 * sp) * plane + o)
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+                    pu[it][d] = ld ? *(const float4 *)(a.gu_part + (size_t)(2 * sp + 1) * plane + o)
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+                }
             }
+#pragma unroll
+            for (int it = 0; it < kFormIt; ++it)
+#pragma unroll
+                for (int d = 0; d < 2; ++d) {
+                    if (sp0 + d >= a.gu_S) break;
+                    g[it].x += pg[it][d].x; g[it].y += pg[it][d].y; g[it].z += pg[it][d].z; g[it].w += pg[it][d].w;
+                    uu[it].x += pu[it][d].x; uu[it].y += pu[it][d].y; uu[it].z += pu[it][d].z; uu[it].w += pu[it][d].w;
+                }
         }
 #pragma unroll
         for (int it = 0; it < kFormIt; ++it) {
@@ -248,16 +263,11 @@ __global__ void __launch_bounds__(64 * kCuWaves, 1) custream_kernel(CArgs a) {
             if (i >= ng * q4) break;
             uint2 hv = make_uint2(0, 0), lv = make_uint2(0, 0);
             if (c < a.K) {
-                float4 g = pg[it][0], uu = pu[it][0];
-                if (a.gu_S > 1) {                   // the splits summed in order, as the SwiGLU launch sums them
-                    g.x += pg[it][1].x; g.y += pg[it][1].y; g.z += pg[it][1].z; g.w += pg[it][1].w;
-                    uu.x += pu[it][1].x; uu.y += pu[it][1].y; uu.z += pu[it][1].z; uu.w += pu[it][1].w;
-                }
                 uint32_t h0, l0, h1, l1, h2, l2, h3, l3;
-                split_bf16(swiglu_clamped(g.x, uu.x, a.limit), h0, l0);
-                split_bf16(swiglu_clamped(g.y, uu.y, a.limit), h1, l1);
-                split_bf16(swiglu_clamped(g.z, uu.z, a.limit), h2, l2);
-                split_bf16(swiglu_clamped(g.w, uu.w, a.limit), h3, l3);
+                split_bf16(swiglu_clamped(g[it].x, uu[it].x, a.limit), h0, l0);
+                split_bf16(swiglu_clamped(g[it].y, uu[it].y, a.limit), h1, l1);
+                split_bf16(swiglu_clamped(g[it].z, uu[it].z, a.limit), h2, l2);
+                split_bf16(swiglu_clamped(g[it].w, uu[it].w, a.limit), h3, l3);
                 hv = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
                 lv = make_uint2(l0 | (l1 << 16), l2 | (l3 << 16));
             }

@@ -985,7 +985,7 @@ static int decode_launch(const DecodePlan &p, const mi_table *gate, const mi_tab
     const bool fuse_h = !cb3 && !p.cu && !p.cum && tuning(kTuneFuseSwiglu, N == 1 ? 1 : 0) == 1;
     // the CU-balanced down launch forms h itself while staging (bit-identical h, one launch fewer: ~2 us at one token;
     // the CU_FORM_H override 0 keeps the SwiGLU launch, for measurement)
-    const bool cu_form = p.cu && tuning(kTuneCuFormH, 1) != 0 && p.s1.sp.S <= 2 &&
+    const bool cu_form = p.cu && tuning(kTuneCuFormH, 1) != 0 &&
                          (long long)p.cgmax * (n_units_of(down) * kCb3TileCols / 4) <= 4LL * 64 * kCuWaves;
     if (!fuse_h && !cu_form) {
         const size_t n4 = (size_t)p.NS * gate->rows / 4;

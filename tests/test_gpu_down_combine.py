@@ -125,3 +125,27 @@ def test_in_launch_combine_graph_replays(pkg, gpu):
         assert torch.equal(out, ref), "replay %d" % rep
         _ = (x.float() * 2).sum().item()                 # eager work between replays
     assert np.count_nonzero(_block_words(pkg, tbs, ws, k, E)) == 0
+
+
+@pytest.mark.parametrize("cs1", [1, 3, 4])
+def test_down_forms_h_from_any_split_count(pkg, gpu, cs1):
+    """The batch-1 down launch forms h from the gate/up partials of any number of column splits (summed in order
+    from zero, as the SwiGLU launch sums them): bit-identical to the SwiGLU launch (CU_FORM_H override 0)."""
+    rng = np.random.default_rng(60 + cs1)
+    E, D, I, k = 9, 3200, 512, 8
+    L = Layer(rng, "CB3", E + 1, D, I)
+    tbs = L.tables(pkg)
+    idx, w = softmax_topk_routing(rng, 1, E, k)
+    x = _t(round_bf16(rng.standard_normal((1, D)).astype(np.float32)), torch.bfloat16)
+    outs = []
+    for form in (1, 0):
+        with pkg.tuning(CS1=cs1, CU_FORM_H=form):
+            assert pkg.resident.decode_plan(tbs["gate"], tbs["down"], 1, k, E)["sep_S1"] == cs1
+            ws = torch.zeros(pkg.resident.decode_workspace_bytes(tbs["gate"], tbs["down"], 1, k, E),
+                             dtype=torch.uint8, device="cuda")
+            outs.append(pkg.moe_decode(tbs["gate"], tbs["up"], tbs["down"], x, _t(idx), _t(w), 10.0,
+                                       shared_expert=E, workspace=ws)[0])
+    assert torch.equal(outs[0], outs[1])
+    want = omoe.decode_apply(L.deq, x.float().cpu().numpy(), idx, w, 10.0)
+    want = want + omoe.shared_apply(lambda m: L.deq(m, E), x.float().cpu().numpy(), 10.0)
+    assert rel_l2(outs[0].cpu().numpy(), want) < 1e-5
