@@ -54,6 +54,7 @@ def parse():
                     help="decode at batch 1 and 8 of one table layout only, e.g. iq2s_iq4xs (profiling runs)")
     ap.add_argument("--only-prefill", action="store_true", help="the 512-token prefill chunk only (profiling runs)")
     ap.add_argument("--only-int8", action="store_true", help="the int8 projections and shared MLP only")
+    ap.add_argument("--only-bf16", action="store_true", help="the shared expert's MLP over bf16 leaves only")
     ap.add_argument("--read-ceiling", action="store_true",
                     help="only the streaming-read probe (the part's practical HBM read rate)")
     ap.add_argument("--tune", action="append", default=[], metavar="NAME=VALUE",
@@ -267,6 +268,9 @@ def main():
     if args.only_int8:
         print(json.dumps({"int8_b8": bench_int8(torch, pkg, torch.Generator(device="cuda"), args)}))
         return
+    if args.only_bf16:
+        print(json.dumps({"bf16_mlp": bench_bf16_mlp(torch, pkg, torch.Generator(device="cuda"), args)}))
+        return
     torch.manual_seed(0)
     gen = torch.Generator(device="cuda")
     gen.manual_seed(1234)
@@ -404,6 +408,7 @@ def main():
                                              "pct_hbm": round(100 * gbs / HBM_PEAK_GBS, 1), "bytes_per_layer": int(b)}
             extra["prefill_t512_" + fmt] = bench_prefill(torch, pkg, gen, args, iq_layers(fmt), rng, iq_pe(fmt))
         extra["int8_b8"] = bench_int8(torch, pkg, gen, args)
+        extra["bf16_mlp"] = bench_bf16_mlp(torch, pkg, gen, args)
         extra["route"] = bench_route(torch, pkg, gen, args)
         extra["cfg0_matvec"] = bench_matvec(torch, pkg, gen, args)
 
@@ -561,6 +566,30 @@ def bench_int8(torch, pkg, gen, args):
     gbs = total / (ms * 1e-3) / 1e9
     return {"us_per_layer_int8": round(ms * 1e3, 2), "GBps": round(gbs, 1), "pct_hbm": round(100 * gbs / HBM_PEAK_GBS, 1),
             "bytes": int(total), "launches": "Q+K+V | O | shared MLP: gate+up (forms h), down; split sums in each launch"}
+
+
+def bench_bf16_mlp(torch, pkg, gen, args, copies=6):
+    """The shared expert's mlp_partial over bf16 leaves (the engine's default non-expert weights): D 6144 -> I 2048
+    -> 6144, bf16 activations, at batch 1 and 8 (mi_bf16_mlp: gate and up in one launch that forms h, then down).
+    A step is one call; `copies` weight copies (75.5 MB each) rotated, more than the last-level cache holds."""
+    D, I = 6144, 2048
+    total = 3 * D * I * 2
+    out = {}
+    for B in (1, 8):
+        fns = []
+        for c in range(copies):
+            mk = lambda n_in, n_out: pkg.bf16_leaf(
+                (torch.randn((n_in, n_out), device="cuda", generator=gen) * 0.05).to(torch.bfloat16))
+            w = (mk(D, I), mk(D, I), mk(I, D))
+            x = torch.randn((B, D), device="cuda", generator=gen).to(torch.bfloat16)
+            y = torch.empty((B, D), dtype=torch.bfloat16, device="cuda")
+            ws = torch.zeros(pkg._lib.lib().mi_bf16_mlp_workspace(B, D, I), dtype=torch.uint8, device="cuda")
+            fns.append(lambda x=x, w=w, y=y, ws=ws: pkg.bf16_mlp(x, *w, LIMIT, y_bf16=y, workspace=ws))
+        ms = Timer(torch, fns).run(args.steps, args.warmup)
+        gbs = total / (ms * 1e-3) / 1e9
+        out["b%d" % B] = {"us": round(ms * 1e3, 2), "GBps": round(gbs, 1), "pct_hbm": round(100 * gbs / HBM_PEAK_GBS, 1),
+                          "bytes": int(total)}
+    return out
 
 
 def bench_matvec(torch, pkg, gen, args):

@@ -366,6 +366,26 @@ int mi_int8_mlp(const uint16_t *x_bf16, int32_t B, int32_t D, int32_t I, const i
 size_t mi_int8_mlp_workspace(int32_t B, int32_t D, int32_t I, int32_t gu_scale_axis, int32_t down_scale_axis);
 
 /*
+ * bf16 projection and MLP: the same contractions over the reference's non-int8 leaves, a bf16 W [in, out] used as
+ * x @ W (model.py:125-127; the shared expert of moe_dense, model.py:855, and the dense MLP layers, model.py:131, when
+ * the engine keeps its non-expert weights in bf16, int8_nonexpert=False, engine.py:281,305).
+ *   mi_bf16_project: y = x W, f32 accumulation; bf16 out (one rounding of the f32 result) and/or f32 out.
+ *   mi_bf16_mlp:     g = bf16(x Wg), u = bf16(x Wu), h = bf16(swiglu_clamped(g, u)) evaluated in f32 once,
+ *                    y = h Wd in f32, y_bf16 = bf16(y) -- mi_int8_mlp's steps with W the bf16 leaf itself.
+ * Weights are wT bf16 [n_out, n_in] (gate/up [I, D], down [D, I]): the reference's leaf transposed once at load,
+ * 16-byte aligned.  Shapes, token limit, workspace layout and counter rule as for the int8 entry points (the
+ * workspace's first 256 KB are counters that must be zero before its first call; every call leaves them zero, so
+ * one workspace may serve the int8 and bf16 calls ordered on one stream).  No tiled form.
+ */
+int mi_bf16_project(const uint16_t *x_bf16, int32_t B, const uint16_t *wT, int32_t n_in, int32_t n_out,
+                    uint16_t *y_bf16, float *y_f32, void *workspace, size_t workspace_bytes, void *stream);
+size_t mi_bf16_project_workspace(int32_t B, int32_t n_in, int32_t n_out);
+int mi_bf16_mlp(const uint16_t *x_bf16, int32_t B, int32_t D, int32_t I, const uint16_t *gate_wT,
+                const uint16_t *up_wT, const uint16_t *down_wT, float limit, uint16_t *y_bf16, float *y_f32,
+                void *workspace, size_t workspace_bytes, void *stream);
+size_t mi_bf16_mlp_workspace(int32_t B, int32_t D, int32_t I);
+
+/*
  * Launch-plan overrides, for tests and measurement runs only (no counterpart in the reference).  The library reads
  * no environment variables: every call plans its launches from built-in defaults, except for the names set here,
  * which replace those defaults process-wide until mi_tuning_reset.  Names (an unknown one gives MI_ERR_ARG):

@@ -5,13 +5,14 @@ The directory name is not a Python identifier; it is imported as ``kaggle_llm_en
 ``load_package()`` of ``__graft_entry__`` / ``tests/conftest.py``.
 """
 from . import _lib, formats, gguf  # noqa: F401
-from .resident import (ExpertTable, ResidentFetch, dequant, int8_mlp, int8_project, int8_project_many,  # noqa: F401
-                       int8_tile, matvec, mlp_partial,
+from .resident import (Bf16Leaf, ExpertTable, ResidentFetch, bf16_leaf, bf16_mlp, bf16_project,  # noqa: F401
+                       dequant, int8_mlp, int8_project, int8_project_many, int8_tile, matvec, mlp_partial,
                        moe_matvec, moe_decode, moe_prefill, moe_route, pack_planes_device, prefill_workspace_bytes,
                        ragged_plan, random_cb3_table, random_iq2s_table,
                        random_iq3s_table, random_iq4xs_table, random_kq_table, route, to_device_planes, tuning)
 
-__all__ = ["ExpertTable", "ResidentFetch", "dequant", "int8_mlp", "int8_project", "int8_project_many", "int8_tile",
+__all__ = ["Bf16Leaf", "ExpertTable", "ResidentFetch", "bf16_leaf", "bf16_mlp", "bf16_project", "dequant",
+           "int8_mlp", "int8_project", "int8_project_many", "int8_tile",
            "matvec",
            "mlp_partial", "moe_matvec",
            "moe_decode",

@@ -44,7 +44,8 @@ EXPORTS = ("mi_matvec", "mi_matvec_workspace", "mi_moe_decode", "mi_moe_decode_f
            "mi_moe_decode_workspace", "mi_moe_decode_plan", "mi_moe_decode_noalloc", "mi_moe_decode_x",
            "mi_ragged_plan", "mi_moe_prefill", "mi_moe_prefill_workspace", "mi_moe_prefill_form",
            "mi_moe_prefill_form_workspace", "mi_dequant", "mi_int8_project", "mi_int8_project_workspace", "mi_int8_project_many",
-           "mi_int8_project_many_workspace", "mi_int8_mlp", "mi_int8_mlp_workspace", "mi_moe_route", "mi_moe_route_workspace", "mi_pack_planes", "mi_int8_tile", "mi_tuning_set", "mi_tuning_reset",
+           "mi_int8_project_many_workspace", "mi_int8_mlp", "mi_int8_mlp_workspace", "mi_moe_route", "mi_moe_route_workspace", "mi_pack_planes", "mi_int8_tile", "mi_bf16_project", "mi_bf16_project_workspace",
+           "mi_bf16_mlp", "mi_bf16_mlp_workspace", "mi_tuning_set", "mi_tuning_reset",
            "mi_strerror",
            "mi_version")
 
@@ -102,6 +103,10 @@ def lib():
         "mi_int8_project_workspace": (Z, [I, I, I, I]),
         "mi_int8_project_many": (I, [P, I, I, ctypes.POINTER(MiI8Proj), I, I, P, Z, P]),
         "mi_int8_project_many_workspace": (Z, [I, I, ctypes.POINTER(ctypes.c_int32), I, I]),
+        "mi_bf16_project": (I, [P, I, P, I, I, P, P, P, Z, P]),
+        "mi_bf16_project_workspace": (Z, [I, I, I]),
+        "mi_bf16_mlp": (I, [P, I, I, I, P, P, P, F, P, P, P, Z, P]),
+        "mi_bf16_mlp_workspace": (Z, [I, I, I]),
         "mi_moe_route": (I, [P, P, P, I, I, I, I, I, F, P, P, P, Z, P]),
         "mi_moe_route_workspace": (Z, [I, I, I]),
         "mi_pack_planes": (I, [I, P, I, I, I, ctypes.POINTER(ctypes.c_void_p), P]),

@@ -15,6 +15,10 @@
 // order whichever completes last) and writes y -- or, for an MLP's gate/up pair, h -- so the sums need no launch of
 // their own (completion counters in the workspace; split_reduce_i8 / swiglu_pair_i8 when there are too many row
 // groups for them).  One split writes y directly.
+//
+// The same kernels take bf16 weights wT [n_out, n_in] (the reference's non-int8 leaves, x @ W with W bf16 [in, out]
+// transposed once at load): blocks of 64 columns (the same 128 bytes per row), a lane's two 16-byte loads are its two
+// k-steps directly -- step c of block p uses columns 64p + 32c + 8q .. +7 -- with no scale and no conversion.
 #include "common.h"
 #include "tuning.h"
 
@@ -30,10 +34,11 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kI8MaxProj = 8;      // projections sharing one activation matrix per launch
+constexpr int kW16 = 3;            // weight form beside the MI_I8_* scale forms: bf16 weights, no scales
 
 struct I8Proj {
-    const int8_t *q;       // [n_out, n_in]
-    const float *s;        // [n_out] (MI_I8_COL_SCALES, MI_I8_COL_AFTER) or [n_in] (MI_I8_ROW_SCALES)
+    const int8_t *q;       // [n_out, n_in] (int8; bf16 with the kW16 form: 2 n_in bytes per row)
+    const float *s;        // [n_out] (MI_I8_COL_SCALES, MI_I8_COL_AFTER) or [n_in] (MI_I8_ROW_SCALES); kW16: unused
     int n_out;
     uint16_t *y_bf16;      // [B, n_out] (S == 1)
     float *y_f32;          // [B, n_out] (S == 1)
@@ -43,9 +48,9 @@ struct I8Proj {
 struct I8Args {
     const uint16_t *x;     // bf16 [B, n_in], shared by every projection
     int B, n_in, S;
-    int scale_axis;        // MI_I8_*: one per launch
+    int scale_axis;        // MI_I8_* or kW16: one per launch
     int tiled;             // qT in the tiled layout (mi_int8_tile): 2 KB per (16-row tile, 128-column block)
-    int blocks;            // 128-column blocks per split
+    int blocks;            // blocks per split: 128 columns (int8) or 64 (kW16), 2 KB per 16-row tile either way
     int n_proj;
     int wg_start[kI8MaxProj + 1];   // first workgroup of each projection
     I8Proj p[kI8MaxProj];
@@ -98,9 +103,12 @@ __device__ __forceinline__ bf16x8 i8_weights8_rs(uint32_t w0, uint32_t w1, float
     return __builtin_bit_cast(bf16x8, v);
 }
 
-// token tiles of 16 (B <= 16 * TT); SA: MI_I8_* scale form; SUMS: the split sums in the launch (a.cnt set)
+// token tiles of 16 (B <= 16 * TT); SA: MI_I8_* scale form or kW16 (bf16 weights); SUMS: the split sums in the
+// launch (a.cnt set)
 template <int TT, int SA, bool SUMS>
 __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
+    constexpr bool W16 = SA == kW16;
+    constexpr int kCols = W16 ? 64 : 128;            // columns per block
     extern __shared__ uint32_t xs[];                 // [B][cols / 2] bf16 pairs of the split's columns (+ row scales)
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -113,19 +121,21 @@ __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
     const int o0 = (rg * kI8Waves + wave) * 16;
     const bool active = o0 < P.n_out;                // wavefronts past the last 16-row tile only stage (and count)
     const int i = lane & 15, q = lane >> 4;
-    const int cols = 128 * a.blocks, k0 = split * cols;
+    const int cols = kCols * a.blocks, k0 = split * cols;
 
     // weights: lane's 32 bytes of block p at row o0 + i, columns k0 + 128 p + 32 q, as buffer loads from the
     // wavefront's tile (blocks past the split use an empty-range descriptor: zeros, no memory traffic)
     // row layout: row o0 + i at n_in bytes per row, block p at +128 p, the lane's two 16-byte halves 16 apart;
     // tiled layout: the wavefront's 16-row tile holds each 128-column block as 2 KB, the lane's halves at lane * 16
-    // and 1024 + lane * 16: every load instruction reads 1 KB of contiguous memory
-    const int8_t *tile = a.tiled ? P.q + ((size_t)(active ? o0 / 16 : 0) * (a.n_in / 128) + k0 / 128) * 2048
-                                 : P.q + (size_t)(active ? o0 : 0) * a.n_in + k0;
-    const int bstride = a.tiled ? 2048 : 128, hoff = a.tiled ? 1024 : 16;
+    // and 1024 + lane * 16: every load instruction reads 1 KB of contiguous memory;
+    // bf16 rows: row o0 + i at 2 n_in bytes per row, block p at +128 p, the lane's k-steps at +16 q and +64 + 16 q
+    const int8_t *tile = W16 ? P.q + 2 * ((size_t)(active ? o0 : 0) * a.n_in + k0)
+                         : a.tiled ? P.q + ((size_t)(active ? o0 / 16 : 0) * (a.n_in / 128) + k0 / 128) * 2048
+                                   : P.q + (size_t)(active ? o0 : 0) * a.n_in + k0;
+    const int bstride = a.tiled ? 2048 : 128, hoff = a.tiled ? 1024 : W16 ? 64 : 16;
     const __amdgpu_buffer_rsrc_t qb = __builtin_amdgcn_make_buffer_rsrc((void *)tile, (short)0, 0x7fffffff, kBufWord3);
     const __amdgpu_buffer_rsrc_t qnull = __builtin_amdgcn_make_buffer_rsrc((void *)tile, (short)0, 0, kBufWord3);
-    const int voff = a.tiled ? 16 * lane : i * a.n_in + 32 * q;
+    const int voff = W16 ? 2 * i * a.n_in + 16 * q : a.tiled ? 16 * lane : i * a.n_in + 32 * q;
     auto load_block = [&](int p, uint4 &lo, uint4 &hi) {
         const __amdgpu_buffer_rsrc_t r = p < a.blocks ? qb : qnull;
         lo = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, bstride * p, kI8LoadPolicy));
@@ -158,7 +168,7 @@ __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
     // B-operand rows: token jt of tile t (rows >= B read row B-1; those accumulator columns are not stored)
     const uint32_t *xrow[TT];
 #pragma unroll
-    for (int t = 0; t < TT; ++t) xrow[t] = xs + min(16 * t + i, a.B - 1) * cw + 16 * q;
+    for (int t = 0; t < TT; ++t) xrow[t] = xs + min(16 * t + i, a.B - 1) * cw + (W16 ? 4 : 16) * q;
 
     for (int p0 = 0; p0 < (active ? a.blocks : 0); p0 += kI8Ring) {
 #pragma unroll
@@ -167,6 +177,19 @@ __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
             if (p >= a.blocks) break;
             const uint4 w0 = ring[d][0], w1 = ring[d][1];
             load_block(p + kI8Ring, ring[d][0], ring[d][1]);
+            if constexpr (W16) {                      // the loads are the A operands (columns 64p + 32c + 8q ..)
+#pragma unroll
+                for (int c = 0; c < 2; ++c) {
+                    const bf16x8 A = __builtin_bit_cast(bf16x8, c ? w1 : w0);
+#pragma unroll
+                    for (int t = 0; t < TT; ++t) {
+                        const uint4 xv = *(const uint4 *)(xrow[t] + 32 * p + 16 * c);
+                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, __builtin_bit_cast(bf16x8, xv), acc[t],
+                                                                         0, 0, 0);
+                    }
+                }
+                continue;
+            }
             const uint32_t W[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
@@ -387,13 +410,16 @@ __global__ void __launch_bounds__(256) int8_tile_kernel(const int8_t *__restrict
 // LDS bytes per staged column: B bf16 activations (+ one f32 scale with per-input-row scales).
 static size_t i8_col_bytes(int B, int scale_axis) { return 2 * (size_t)B + (scale_axis == MI_I8_ROW_SCALES ? 4 : 0); }
 
+// Columns per 2 KB block of a 16-row tile: 128 int8 or 64 bf16 weights.
+static int i8_block_cols(int form) { return form == kW16 ? 64 : 128; }
+
 // Column splits: enough wavefronts to cover the chip (about 3 per SIMD, 3072 over 256 CUs), every wavefront
-// streaming at least 4 blocks of 128 columns, the split's staged columns within 48 KB of LDS.  `tiles` counts the
-// 16-row tiles of every projection of the launch.
+// streaming at least 4 blocks (8 KB), the split's staged columns within 48 KB of LDS.  `tiles` counts the 16-row
+// tiles of every projection of the launch.
 static int i8_splits(int B, int n_in, int tiles, int scale_axis) {
-    const int nblk = n_in / 128;
+    const int nblk = n_in / i8_block_cols(scale_axis);
     const size_t cb = i8_col_bytes(B, scale_axis);
-    const int forced = tuning(kTuneI8S, 0);       // measurements: a forced split count (must divide n_in / 128)
+    const int forced = tuning(kTuneI8S, 0);       // measurements: a forced split count (must divide the blocks)
     if (forced > 0 && nblk % forced == 0 && (size_t)(n_in / forced) * cb <= 48 * 1024) return forced;
     int target = tuning(kTuneI8Waves, 3072);       // wavefronts to aim for
     if (target <= 0) target = 3072;
@@ -435,7 +461,8 @@ using namespace mi;
 static int i8_fuse() { return tuning(kTuneI8Fuse, 3); }
 
 // One launch of the projections of `projs` over x (+ the split sums, or with `pair` the SwiGLU of gate and up into
-// h): partials at `part` (part_bytes), the launch's counter block at `cnt` (kI8Ctrs counters, zero).
+// h): partials at `part` (part_bytes), the launch's counter block at `cnt` (kI8Ctrs counters, zero).  scale_axis:
+// MI_I8_* (| MI_I8_TILED) for int8 weights, kW16 for bf16 ones (row layout, no scales).
 static int i8_launch(const uint16_t *x_bf16, int32_t B, int32_t n_in, const mi_i8_proj *projs, int32_t n_proj,
                      int32_t scale_axis, float *part, size_t part_bytes, uint32_t *cnt, void *stream, int pair,
                      float limit, uint16_t *h) {
@@ -444,12 +471,12 @@ static int i8_launch(const uint16_t *x_bf16, int32_t B, int32_t n_in, const mi_i
     if (n_proj <= 0 || n_proj > kI8MaxProj || (pair && n_proj != 2)) return MI_ERR_ARG;
     const int tiled = (scale_axis & MI_I8_TILED) != 0;
     scale_axis &= ~MI_I8_TILED;
-    if (scale_axis < MI_I8_ROW_SCALES || scale_axis > MI_I8_COL_AFTER) return MI_ERR_ARG;
+    if (scale_axis < MI_I8_ROW_SCALES || scale_axis > kW16 || (tiled && scale_axis == kW16)) return MI_ERR_ARG;
     if (n_in <= 0 || n_in % 256) return MI_ERR_SHAPE;
     int32_t n_out[kI8MaxProj];
     for (int j = 0; j < n_proj; ++j) {
         const mi_i8_proj &p = projs[j];
-        if (!p.qT || !p.s || (!pair && !p.y_bf16 && !p.y_f32)) return MI_ERR_NULL;
+        if (!p.qT || (!p.s && scale_axis != kW16) || (!pair && !p.y_bf16 && !p.y_f32)) return MI_ERR_NULL;
         if (p.n_out <= 0 || p.n_out % 16) return MI_ERR_SHAPE;
         n_out[j] = p.n_out;
     }
@@ -465,7 +492,7 @@ static int i8_launch(const uint16_t *x_bf16, int32_t B, int32_t n_in, const mi_i
     a.S = i8_splits(B, n_in, i8_tiles(n_out, n_proj), scale_axis);
     a.scale_axis = scale_axis;
     a.tiled = tiled;
-    a.blocks = n_in / 128 / a.S;
+    a.blocks = n_in / i8_block_cols(scale_axis) / a.S;
     a.n_proj = n_proj;
     size_t off = 0;
     int wg = 0, ctrs = 0;
@@ -487,14 +514,18 @@ static int i8_launch(const uint16_t *x_bf16, int32_t B, int32_t n_in, const mi_i
     a.wg_start[n_proj] = wg;
     // the split sums in this launch when its row groups have counters (and there is more than one split or a pair)
     a.cnt = (a.S > 1 || pair) && ctrs <= kI8Ctrs && (i8_fuse() & (pair ? 2 : 1)) ? cnt : nullptr;
-    const size_t lds = i8_col_bytes(B, scale_axis) * 128 * a.blocks;
+    const size_t lds = i8_col_bytes(B, scale_axis) * i8_block_cols(scale_axis) * a.blocks;
     hipStream_t st = (hipStream_t)stream;
     typedef void (*Kern)(I8Args);
-    static const Kern kern[2][2][3] = {
-        {{int8_project_kernel<1, 0, false>, int8_project_kernel<1, 1, false>, int8_project_kernel<1, 2, false>},
-         {int8_project_kernel<2, 0, false>, int8_project_kernel<2, 1, false>, int8_project_kernel<2, 2, false>}},
-        {{int8_project_kernel<1, 0, true>, int8_project_kernel<1, 1, true>, int8_project_kernel<1, 2, true>},
-         {int8_project_kernel<2, 0, true>, int8_project_kernel<2, 1, true>, int8_project_kernel<2, 2, true>}}};
+    static const Kern kern[2][2][4] = {
+        {{int8_project_kernel<1, 0, false>, int8_project_kernel<1, 1, false>, int8_project_kernel<1, 2, false>,
+          int8_project_kernel<1, kW16, false>},
+         {int8_project_kernel<2, 0, false>, int8_project_kernel<2, 1, false>, int8_project_kernel<2, 2, false>,
+          int8_project_kernel<2, kW16, false>}},
+        {{int8_project_kernel<1, 0, true>, int8_project_kernel<1, 1, true>, int8_project_kernel<1, 2, true>,
+          int8_project_kernel<1, kW16, true>},
+         {int8_project_kernel<2, 0, true>, int8_project_kernel<2, 1, true>, int8_project_kernel<2, 2, true>,
+          int8_project_kernel<2, kW16, true>}}};
     hipLaunchKernelGGL(kern[a.cnt ? 1 : 0][B <= 16 ? 0 : 1][scale_axis], dim3(wg), dim3(64 * kI8Waves), lds, st, a);
     if (hipGetLastError() != hipSuccess) return MI_ERR_LAUNCH;
     if (a.cnt) return MI_OK;
@@ -512,6 +543,39 @@ static int i8_launch(const uint16_t *x_bf16, int32_t B, int32_t n_in, const mi_i
 
 
 
+// mlp_partial's two launches over weights of one form per launch (int8 with scales, or kW16): gate and up together
+// (their last workgroups form h), then down with its split sums.  Workspace: [counter blocks: gate/up's, down's]
+// [gate/up partials][h][down partials].
+static size_t mlp_workspace(int32_t B, int32_t D, int32_t I, int32_t gu_form, int32_t dn_form) {
+    if (B <= 0 || B > 32 || D <= 0 || I <= 0 || D % 256 || I % 256) return 0;
+    const int32_t gu[2] = {I, I}, dn = D;
+    return kI8CtrBytes + al256_i8(i8_part_bytes(B, D, gu, 2, gu_form, 1)) + al256_i8(2 * (size_t)B * I) +
+           i8_part_bytes(B, I, &dn, 1, dn_form, 0);
+}
+
+static int mlp_launches(const uint16_t *x_bf16, int32_t B, int32_t D, int32_t I, const int8_t *gate_w,
+                        const float *gate_s, const int8_t *up_w, const float *up_s, int32_t gu_form,
+                        const int8_t *down_w, const float *down_s, int32_t dn_form, float limit, uint16_t *y_bf16,
+                        float *y_f32, void *workspace, size_t workspace_bytes, void *stream) {
+    if (!(limit > 0.0f)) return MI_ERR_ARG;
+    const size_t need = mlp_workspace(B, D, I, gu_form & ~MI_I8_TILED, dn_form & ~MI_I8_TILED);
+    if (need == 0) return MI_ERR_ARG;
+    if (!workspace || workspace_bytes < need || (uintptr_t)workspace % 256) return MI_ERR_WORKSPACE;
+    const int32_t gu[2] = {I, I};
+    uint32_t *cnt = (uint32_t *)workspace;
+    char *gu_part = (char *)workspace + kI8CtrBytes;
+    const size_t part = al256_i8(i8_part_bytes(B, D, gu, 2, gu_form, 1));
+    uint16_t *h = (uint16_t *)(gu_part + part);
+    char *dn_part = gu_part + part + al256_i8(2 * (size_t)B * I);
+    const mi_i8_proj p[2] = {{gate_w, gate_s, I, nullptr, nullptr}, {up_w, up_s, I, nullptr, nullptr}};
+    int st = i8_launch(x_bf16, B, D, p, 2, gu_form, (float *)gu_part, part, cnt, stream, 1, limit, h);
+    if (st) return st;
+    const mi_i8_proj pd{down_w, down_s, D, y_bf16, y_f32};
+    return i8_launch(h, B, I, &pd, 1, dn_form, (float *)dn_part,
+                     workspace_bytes - (size_t)(dn_part - (char *)workspace), cnt + kI8Ctrs * kI8CtrStride, stream, 0,
+                     0.0f, nullptr);
+}
+
 extern "C" {
 
 size_t mi_int8_project_many_workspace(int32_t B, int32_t n_in, const int32_t *n_out, int32_t n_proj,
@@ -527,6 +591,7 @@ size_t mi_int8_project_many_workspace(int32_t B, int32_t n_in, const int32_t *n_
 // Every int8 workspace starts with the counter blocks (kI8CtrBytes), then the launch's data.
 int mi_int8_project_many(const uint16_t *x_bf16, int32_t B, int32_t n_in, const mi_i8_proj *projs, int32_t n_proj,
                          int32_t scale_axis, void *workspace, size_t workspace_bytes, void *stream) {
+    if ((scale_axis & ~MI_I8_TILED) > MI_I8_COL_AFTER) return MI_ERR_ARG;      // int8 scale forms only
     const bool ok = workspace && workspace_bytes >= kI8CtrBytes;
     return i8_launch(x_bf16, B, n_in, projs, n_proj, scale_axis,
                      ok ? (float *)((char *)workspace + kI8CtrBytes) : nullptr, ok ? workspace_bytes - kI8CtrBytes : 0,
@@ -558,14 +623,11 @@ int mi_int8_project(const uint16_t *x_bf16, int32_t B, const int8_t *qT, const f
 }
 
 size_t mi_int8_mlp_workspace(int32_t B, int32_t D, int32_t I, int32_t gu_scale_axis, int32_t down_scale_axis) {
-    if (B <= 0 || B > 32 || D <= 0 || I <= 0 || D % 256 || I % 256) return 0;
     gu_scale_axis &= ~MI_I8_TILED;
     down_scale_axis &= ~MI_I8_TILED;
     if (gu_scale_axis != MI_I8_ROW_SCALES && gu_scale_axis != MI_I8_COL_SCALES) return 0;
     if (down_scale_axis != MI_I8_ROW_SCALES && down_scale_axis != MI_I8_COL_SCALES) return 0;
-    const int32_t gu[2] = {I, I}, dn = D;
-    return kI8CtrBytes + al256_i8(i8_part_bytes(B, D, gu, 2, gu_scale_axis, 1)) + al256_i8(2 * (size_t)B * I) +
-           i8_part_bytes(B, I, &dn, 1, down_scale_axis, 0);
+    return mlp_workspace(B, D, I, gu_scale_axis, down_scale_axis);
 }
 
 int mi_int8_mlp(const uint16_t *x_bf16, int32_t B, int32_t D, int32_t I, const int8_t *gate_qT, const float *gate_s,
@@ -576,24 +638,40 @@ int mi_int8_mlp(const uint16_t *x_bf16, int32_t B, int32_t D, int32_t I, const i
         return MI_ERR_NULL;
     if (B <= 0 || B > 32) return MI_ERR_TOKENS;
     if (D <= 0 || I <= 0 || D % 256 || I % 256) return MI_ERR_SHAPE;
-    if (!(limit > 0.0f)) return MI_ERR_ARG;
-    const size_t need = mi_int8_mlp_workspace(B, D, I, gu_scale_axis, down_scale_axis);
-    if (need == 0) return MI_ERR_ARG;
-    if (!workspace || workspace_bytes < need || (uintptr_t)workspace % 256) return MI_ERR_WORKSPACE;
-    // [counter blocks: gate/up's, down's][gate/up partials][h][down partials]
-    const int32_t gu[2] = {I, I};
-    uint32_t *cnt = (uint32_t *)workspace;
-    char *gu_part = (char *)workspace + kI8CtrBytes;
-    const size_t part = al256_i8(i8_part_bytes(B, D, gu, 2, gu_scale_axis, 1));
-    uint16_t *h = (uint16_t *)(gu_part + part);
-    char *dn_part = gu_part + part + al256_i8(2 * (size_t)B * I);
-    const mi_i8_proj p[2] = {{gate_qT, gate_s, I, nullptr, nullptr}, {up_qT, up_s, I, nullptr, nullptr}};
-    int st = i8_launch(x_bf16, B, D, p, 2, gu_scale_axis, (float *)gu_part, part, cnt, stream, 1, limit, h);
-    if (st) return st;
-    const mi_i8_proj pd{down_qT, down_s, D, y_bf16, y_f32};
-    return i8_launch(h, B, I, &pd, 1, down_scale_axis, (float *)dn_part,
-                     workspace_bytes - (size_t)(dn_part - (char *)workspace), cnt + kI8Ctrs * kI8CtrStride, stream, 0, 0.0f,
-                     nullptr);
+    if (mi_int8_mlp_workspace(B, D, I, gu_scale_axis, down_scale_axis) == 0) return MI_ERR_ARG;
+    return mlp_launches(x_bf16, B, D, I, gate_qT, gate_s, up_qT, up_s, gu_scale_axis, down_qT, down_s,
+                        down_scale_axis, limit, y_bf16, y_f32, workspace, workspace_bytes, stream);
+}
+
+size_t mi_bf16_project_workspace(int32_t B, int32_t n_in, int32_t n_out) {
+    if (B <= 0 || B > 32 || n_in <= 0 || n_in % 256 || n_out <= 0 || n_out % 16) return 0;
+    return kI8CtrBytes + i8_part_bytes(B, n_in, &n_out, 1, kW16, 0);
+}
+
+int mi_bf16_project(const uint16_t *x_bf16, int32_t B, const uint16_t *wT, int32_t n_in, int32_t n_out,
+                    uint16_t *y_bf16, float *y_f32, void *workspace, size_t workspace_bytes, void *stream) {
+    if (!x_bf16 || !wT || (!y_bf16 && !y_f32)) return MI_ERR_NULL;
+    if (B <= 0 || B > 32) return MI_ERR_TOKENS;
+    if (n_in <= 0 || n_out <= 0 || n_in % 256 || n_out % 16) return MI_ERR_SHAPE;
+    if ((uintptr_t)wT % 16) return MI_ERR_ARG;
+    const bool ok = workspace && workspace_bytes >= kI8CtrBytes;
+    const mi_i8_proj p{(const int8_t *)wT, nullptr, n_out, y_bf16, y_f32};
+    return i8_launch(x_bf16, B, n_in, &p, 1, kW16, ok ? (float *)((char *)workspace + kI8CtrBytes) : nullptr,
+                     ok ? workspace_bytes - kI8CtrBytes : 0, (uint32_t *)workspace, stream, 0, 0.0f, nullptr);
+}
+
+size_t mi_bf16_mlp_workspace(int32_t B, int32_t D, int32_t I) { return mlp_workspace(B, D, I, kW16, kW16); }
+
+int mi_bf16_mlp(const uint16_t *x_bf16, int32_t B, int32_t D, int32_t I, const uint16_t *gate_wT,
+                const uint16_t *up_wT, const uint16_t *down_wT, float limit, uint16_t *y_bf16, float *y_f32,
+                void *workspace, size_t workspace_bytes, void *stream) {
+    if (!x_bf16 || !gate_wT || !up_wT || !down_wT || (!y_bf16 && !y_f32)) return MI_ERR_NULL;
+    if (B <= 0 || B > 32) return MI_ERR_TOKENS;
+    if (D <= 0 || I <= 0 || D % 256 || I % 256) return MI_ERR_SHAPE;
+    if ((uintptr_t)gate_wT % 16 || (uintptr_t)up_wT % 16 || (uintptr_t)down_wT % 16) return MI_ERR_ARG;
+    return mlp_launches(x_bf16, B, D, I, (const int8_t *)gate_wT, nullptr, (const int8_t *)up_wT, nullptr, kW16,
+                        (const int8_t *)down_wT, nullptr, kW16, limit, y_bf16, y_f32, workspace, workspace_bytes,
+                        stream);
 }
 
 }  // extern "C"

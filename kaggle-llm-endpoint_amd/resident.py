@@ -9,6 +9,7 @@ naming each table's format.  The same call works here with the planes held as to
 Everything runs on the current torch (HIP) stream; there is no CPU path.
 """
 import ctypes
+from typing import NamedTuple
 
 import numpy as np
 import torch
@@ -643,10 +644,91 @@ def int8_mlp(x, gate, up, down, limit, want_f32=False, y_bf16=None, y_f32=None, 
     return (yb, yf) if want_f32 else yb
 
 
+class Bf16Leaf(NamedTuple):
+    """A bf16 weight prepared for bf16_project / bf16_mlp: wT bf16 [n_out, n_in] on the device (the reference's
+    W [in, out] transposed once)."""
+    wT: torch.Tensor
+
+
+def bf16_leaf(w, device="cuda"):
+    """A reference bf16 leaf W [in, out] (x @ W, model.py:125-127; int8_nonexpert=False keeps the non-expert weights
+    so, engine.py:281,305) -> Bf16Leaf.  Only torch.bfloat16 tensors: any other dtype would be a rounding the
+    reference does not make."""
+    if isinstance(w, Bf16Leaf):
+        return w
+    if not isinstance(w, torch.Tensor) or w.dtype != torch.bfloat16 or w.dim() != 2:
+        raise TypeError("bf16_leaf expects a 2-d torch.bfloat16 tensor W [in, out]")
+    return Bf16Leaf(w.to(device).t().contiguous())
+
+
+def bf16_project(x, w, want_f32=False, y_bf16=None, y_f32=None, workspace=None):
+    """y = x @ W (the reference's bf16 matmul: f32 accumulation, bf16 out): x bf16 [B, n_in]; w the reference's W
+    bf16 [n_in, n_out] or a Bf16Leaf.  Returns y bf16 [B, n_out] (and y f32 with want_f32); 32 tokens per launch.
+    The workspace's first 256 KB are completion counters that must be zero before its first call (a zero-filled
+    allocation; every call leaves them zero again)."""
+    wT = bf16_leaf(w, x.device).wT
+    B, n_in = x.shape
+    n_out, w_in = wT.shape
+    if w_in != n_in:
+        raise ValueError("bf16_project: x has %d columns, the weight %d rows" % (n_in, w_in))
+    x = x.contiguous()
+    yb = y_bf16 if y_bf16 is not None else torch.empty((B, n_out), dtype=torch.bfloat16, device=x.device)
+    yf = y_f32 if y_f32 is not None else (
+        torch.empty((B, n_out), dtype=torch.float32, device=x.device) if want_f32 else None)
+    for b0 in range(0, B, 32):
+        n = min(32, B - b0)
+        nbytes = lib().mi_bf16_project_workspace(n, n_in, n_out)
+        if nbytes == 0:
+            raise ValueError("mi_bf16_project: unsupported shape B=%d n_in=%d n_out=%d" % (n, n_in, n_out))
+        ws = workspace if workspace is not None else WORKSPACES.get("int8", nbytes)
+        check("mi_bf16_project", lib().mi_bf16_project(_ptr(x[b0:b0 + n]), n, _ptr(wT), n_in, n_out,
+                                                       _ptr(yb[b0:b0 + n]),
+                                                       _ptr(yf[b0:b0 + n]) if yf is not None else None, _ptr(ws),
+                                                       ws.numel(), _stream()))
+    return (yb, yf) if want_f32 else yb
+
+
+def bf16_mlp(x, gate, up, down, limit, want_f32=False, y_bf16=None, y_f32=None, workspace=None):
+    """mlp_partial over bf16 leaves (model.py:125-127): y = bf16(h @ Wd) with h = bf16(swiglu_clamped(bf16(x @ Wg),
+    bf16(x @ Wu))).  x bf16 [B, D]; gate, up: W bf16 [D, I], down: W bf16 [I, D] (reference leaves) or Bf16Leaf.
+    -> y bf16 [B, D] (and y f32, the down projection before its rounding, with want_f32).  Tokens go 32 per call
+    (mi_bf16_mlp's limit); preallocated outputs / workspace make each call allocation-free.
+    The workspace's first 256 KB are completion counters that must be zero before its first call (a zero-filled
+    allocation; every call leaves them zero again)."""
+    g, u, d = [bf16_leaf(l, x.device).wT for l in (gate, up, down)]
+    B, D = x.shape
+    I = g.shape[0]
+    if g.shape != (I, D) or u.shape != (I, D) or d.shape != (D, I):
+        raise ValueError("bf16_mlp: gate/up must be [D, I] and down [I, D] with D = %d (got %s, %s, %s)"
+                         % (D, tuple(g.shape[::-1]), tuple(u.shape[::-1]), tuple(d.shape[::-1])))
+    x = x.contiguous()
+    yb = y_bf16 if y_bf16 is not None else torch.empty((B, D), dtype=torch.bfloat16, device=x.device)
+    yf = y_f32 if y_f32 is not None else (
+        torch.empty((B, D), dtype=torch.float32, device=x.device) if want_f32 else None)
+    for b0 in range(0, B, 32):
+        n = min(32, B - b0)
+        nbytes = lib().mi_bf16_mlp_workspace(n, D, I)
+        if nbytes == 0:
+            raise ValueError("mi_bf16_mlp: unsupported shape B=%d D=%d I=%d" % (n, D, I))
+        ws = workspace if workspace is not None else WORKSPACES.get("int8", nbytes)
+        check("mi_bf16_mlp", lib().mi_bf16_mlp(_ptr(x[b0:b0 + n]), n, D, I, _ptr(g), _ptr(u), _ptr(d), float(limit),
+                                               _ptr(yb[b0:b0 + n]), _ptr(yf[b0:b0 + n]) if yf is not None else None,
+                                               _ptr(ws), ws.numel(), _stream()))
+    return (yb, yf) if want_f32 else yb
+
+
 def mlp_partial(p, x, limit):
-    """The reference's mlp_partial(p, x, cfg) (model.py:125-127) for int8 leaves p = {"gate", "up", "down"}
-    (quant8.py:17-18): x bf16 [B, D] -> bf16 [B, D] (cfg.swiglu_limit passed as ``limit``)."""
-    return int8_mlp(x, p["gate"], p["up"], p["down"], limit)
+    """The reference's mlp_partial(p, x, cfg) (model.py:125-127) for p = {"gate", "up", "down"}: int8 leaves
+    {"q", "s"} (quant8.py:17-18, int8_nonexpert on) or int8_leaf triples go to int8_mlp; bf16 leaves (W [in, out]
+    torch.bfloat16, the engine's default, engine.py:281) or Bf16Leaf to bf16_mlp.  x bf16 [B, D] -> bf16 [B, D]
+    (cfg.swiglu_limit passed as ``limit``)."""
+    kinds = {"int8" if isinstance(p[k], (dict, tuple)) and not isinstance(p[k], Bf16Leaf) else "bf16"
+             for k in ("gate", "up", "down")}
+    if len(kinds) != 1:
+        raise ValueError("mlp_partial: gate, up and down must be all int8 or all bf16 leaves")
+    if kinds == {"int8"}:
+        return int8_mlp(x, p["gate"], p["up"], p["down"], limit)
+    return bf16_mlp(x, p["gate"], p["up"], p["down"], limit)
 
 
 # ------------------------------------------------------------------------------------------------ the operator

@@ -2,6 +2,8 @@
 
 Reference: a quantized leaf is {"q": int8 [in, out], "s": f32 [1, out]} (quant8.py:17-18,26-32); every layer program
 replaces it by W = bf16(f32(q) * s) (quant8.py:91-99) and the projection is x @ W with f32 accumulation, bf16 out.
+A non-int8 leaf (the engine's default, int8_nonexpert=False, engine.py:281) is W itself, bf16 [in, out]; mlp_partial
+takes either kind.
 """
 import numpy as np
 
@@ -47,15 +49,26 @@ def project_after_f32(x, q, s):
     return (z * np.asarray(s, dtype=np.float32)).astype(np.float32)
 
 
+def project_w_f32(x, W):
+    """x [B, in] (bf16 values) @ W [in, out] (bf16 values: the reference's non-int8 leaf, model.py:125-127) with f64
+    accumulation -> f32 [B, out] (before the bf16 output rounding)."""
+    return (np.asarray(x, dtype=np.float64) @ np.asarray(W, dtype=np.float64)).astype(np.float32)
+
+
+def _project_leaf(x, leaf):
+    return project_f32(x, *leaf) if isinstance(leaf, tuple) else project_w_f32(x, leaf)
+
+
 def mlp_partial_f32(x, gate, up, down, limit, _drop=()):
     """mlp_partial (model.py:125-127) over int8 leaves gate, up, down = (q [in, out], s [1, out] or [in, 1]), as
-    every layer program sees them after dequant_tree (quant8.py:91-99): g = bf16(x @ Wg), u = bf16(x @ Wu) (bf16
-    matmuls with f32 accumulation; f64 here), h = bf16(swiglu_clamped(g, u)) (one rounding of the SwiGLU evaluated
-    in f64), y = h @ Wd -> f32 [B, D] before the output's bf16 rounding.  ``_drop`` ("g", "u", "h") skips a rounding:
+    every layer program sees them after dequant_tree (quant8.py:91-99), or over bf16 leaves W [in, out] (arrays of
+    bf16 values; int8_nonexpert off, engine.py:281): g = bf16(x @ Wg), u = bf16(x @ Wu) (bf16 matmuls with f32
+    accumulation; f64 here), h = bf16(swiglu_clamped(g, u)) (one rounding of the SwiGLU evaluated in f64),
+    y = h @ Wd -> f32 [B, D] before the output's bf16 rounding.  ``_drop`` ("g", "u", "h") skips a rounding:
     planted-mistake tests only."""
     from .moe import swiglu_clamped
     rnd = lambda name, a: np.asarray(a, dtype=np.float32) if name in _drop else round_bf16(a)
-    g = rnd("g", project_f32(x, *gate))
-    u = rnd("u", project_f32(x, *up))
+    g = rnd("g", _project_leaf(x, gate))
+    u = rnd("u", _project_leaf(x, up))
     h = rnd("h", swiglu_clamped(g, u, limit).astype(np.float32))
-    return project_f32(h, *down)
+    return _project_leaf(h, down)

@@ -81,6 +81,22 @@ def test_host_validation_codes(L, pkg):
     assert L.mi_int8_project(x, 8, P(1), P(2), 1, 256, 64, None, None, ws, 1 << 20, None) == 1
     assert L.mi_int8_project_workspace(8, 6144, 6144, 1) > 0
     assert L.mi_int8_project_workspace(8, 300, 64, 1) == 0
+    assert L.mi_int8_project(x, 8, P(1), P(2), 3, 256, 64, out, None, ws, 1 << 20, None) == 8   # int8 forms only
+    assert L.mi_bf16_project(x, 0, P(0x1000), 256, 64, out, None, ws, 1 << 20, None) == 4
+    assert L.mi_bf16_project(x, 8, P(0x1000), 300, 64, out, None, ws, 1 << 20, None) == 3
+    assert L.mi_bf16_project(x, 8, P(0x1000), 256, 40, out, None, ws, 1 << 20, None) == 3
+    assert L.mi_bf16_project(x, 8, P(0x1002), 256, 64, out, None, ws, 1 << 20, None) == 8     # 16-byte aligned
+    assert L.mi_bf16_project(x, 8, None, 256, 64, out, None, ws, 1 << 20, None) == 1
+    assert L.mi_bf16_project(x, 8, P(0x1000), 256, 64, None, None, ws, 1 << 20, None) == 1
+    assert L.mi_bf16_project(x, 8, P(0x1000), 6144, 2048, out, None, ws, 16, None) == 5         # workspace
+    assert L.mi_bf16_project_workspace(8, 6144, 2048) > 0 and L.mi_bf16_project_workspace(33, 6144, 2048) == 0
+    mlp = lambda B=4, D=512, I=256, limit=7.0, g=P(0x1000), wsb=1 << 30: L.mi_bf16_mlp(
+        x, B, D, I, g, P(0x2000), P(0x3000), ctypes.c_float(limit), out, None, P(0x100000), wsb, None)
+    assert mlp(B=0) == 4 and mlp(B=33) == 4                                        # MI_ERR_TOKENS
+    assert mlp(D=640) == 3 and mlp(I=300) == 3                                     # MI_ERR_SHAPE
+    assert mlp(limit=0.0) == 8 and mlp(g=P(0x1008)) == 8                           # MI_ERR_ARG
+    assert mlp(g=None) == 1 and mlp(wsb=16) == 5
+    assert L.mi_bf16_mlp_workspace(8, 6144, 2048) > 0 and L.mi_bf16_mlp_workspace(8, 6144, 2000) == 0
 
 
 def test_prefill_host_validation(L, pkg):
