@@ -101,13 +101,6 @@ __host__ __device__ constexpr int cb3_row_pitch(int xs) { return ((xs + 63) & ~6
 // Byte offset past every staged source's range: a buffer load there returns zeros (columns outside the split).
 constexpr uint32_t kStageOut = 0x80000000u;
 
-// s_waitcnt vmcnt(N) (expcnt and lgkmcnt left alone): N vector memory operations may still be outstanding.
-template <int N>
-__device__ __forceinline__ void vm_wait() {
-    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
 // 16-byte store with the sc1 cache policy: written through this XCD's L2 to memory, so once the store has completed
 // (s_waitcnt vmcnt(0)) a coherent load (coherent_load4) on any XCD reads the new value.
 __device__ __forceinline__ void wt_store4(__amdgpu_buffer_rsrc_t r, uint32_t voff, f32x4 v) {

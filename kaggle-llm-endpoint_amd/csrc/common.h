@@ -59,6 +59,25 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// s_waitcnt vmcnt(N) (expcnt and lgkmcnt left alone): N vector memory operations may still be outstanding.
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier for LDS data only, leaving global loads in flight: __syncthreads() waits for every outstanding
+// vector memory operation first (its fence covers global memory and direct-to-LDS loads, all counted by vmcnt),
+// which drains a weight ring issued ahead of it.  Here the wave's LDS stores complete (lgkmcnt 0), compiler-only
+// fences keep every memory access on its side, and the barrier joins the waves.  Data that direct-to-LDS loads
+// wrote must be waited for (vm_wait) before it; global memory is not published by it.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);                   // lgkmcnt(0); vmcnt and expcnt not waited for
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // The sc1 cache policy (buffer instructions' aux bits): stores are written through this XCD's L2 to memory, loads are
 // coherent at device scope (the cache bits of a relaxed agent-scope atomic load).
 constexpr int kCachePolicySc1 = 16;

@@ -75,6 +75,11 @@ constexpr int kI8Ring = 4;          // 128-column blocks in flight per wavefront
 #endif
 constexpr int kI8LoadPolicy = MI_I8_NT ? 2 : 0;   // the weights are read once per launch: non-temporal (nt) loads
 constexpr int kBufWord3 = 0x00020000;   // gfx9 buffer descriptor word 3 (32-bit data format)
+constexpr uint32_t kI8Out = 0x80000000u; // buffer offset past every source's range: the load returns zeros
+
+// LDS pitch (dwords) of a staged activation row of cw dwords: whole 64-dword chunks (a direct-to-LDS load writes 64
+// lanes x 4 bytes) plus a 4-dword skew, so the 16 rows of a B-operand read spread over the LDS banks.
+__host__ __device__ constexpr int i8_pitch(int cw) { return ((cw + 63) & ~63) + 4; }
 
 __device__ __forceinline__ uint32_t bf16_pair(float a, float b) {
     const bf16x2 v = {(__bf16)a, (__bf16)b};
@@ -124,7 +129,8 @@ __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
     const int cols = kCols * a.blocks, k0 = split * cols;
 
     // weights: lane's 32 bytes of block p at row o0 + i, columns k0 + 128 p + 32 q, as buffer loads from the
-    // wavefront's tile (blocks past the split use an empty-range descriptor: zeros, no memory traffic)
+    // wavefront's tile (blocks past the split, and every block of a wavefront past the last row tile, use an
+    // empty-range descriptor: zeros, no memory traffic)
     // row layout: row o0 + i at n_in bytes per row, block p at +128 p, the lane's two 16-byte halves 16 apart;
     // tiled layout: the wavefront's 16-row tile holds each 128-column block as 2 KB, the lane's halves at lane * 16
     // and 1024 + lane * 16: every load instruction reads 1 KB of contiguous memory;
@@ -133,7 +139,8 @@ __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
                          : a.tiled ? P.q + ((size_t)(active ? o0 / 16 : 0) * (a.n_in / 128) + k0 / 128) * 2048
                                    : P.q + (size_t)(active ? o0 : 0) * a.n_in + k0;
     const int bstride = a.tiled ? 2048 : 128, hoff = a.tiled ? 1024 : W16 ? 64 : 16;
-    const __amdgpu_buffer_rsrc_t qb = __builtin_amdgcn_make_buffer_rsrc((void *)tile, (short)0, 0x7fffffff, kBufWord3);
+    const __amdgpu_buffer_rsrc_t qb =
+        __builtin_amdgcn_make_buffer_rsrc((void *)tile, (short)0, active ? 0x7fffffff : 0, kBufWord3);
     const __amdgpu_buffer_rsrc_t qnull = __builtin_amdgcn_make_buffer_rsrc((void *)tile, (short)0, 0, kBufWord3);
     const int voff = W16 ? 2 * i * a.n_in + 16 * q : a.tiled ? 16 * lane : i * a.n_in + 32 * q;
     auto load_block = [&](int p, uint4 &lo, uint4 &hi) {
@@ -141,25 +148,38 @@ __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
         lo = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, bstride * p, kI8LoadPolicy));
         hi = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff + hoff, bstride * p, kI8LoadPolicy));
     };
-    uint4 ring[kI8Ring][2];
-    if (active) {
-#pragma unroll
-        for (int d = 0; d < kI8Ring; ++d) load_block(d, ring[d][0], ring[d][1]);
-    }
-    // stage the activations of the split (bf16 pairs), rows < B; per-row scales: the split's s[k0 .. k0 + cols)
-    const int cw = cols / 2;                         // dwords per staged row
-    for (int e = tid; e < a.B * (cw / 4); e += blockDim.x) {
-        const int b = e / (cw / 4), c4 = e - b * (cw / 4);
-        *(uint4 *)(xs + b * cw + 4 * c4) = *(const uint4 *)(a.x + (size_t)b * a.n_in + k0 + 8 * c4);
-    }
-    float *srow = (float *)(xs + a.B * cw);
-    if constexpr (SA == MI_I8_ROW_SCALES) {
-        for (int e = tid; e < cols / 4; e += blockDim.x) *(float4 *)(srow + 4 * e) = *(const float4 *)(P.s + k0 + 4 * e);
-    }
-    __syncthreads();
-    if (!active && !SUMS) return;
-    // per-column scales: the row's s; the lm_head form: q itself (scale 1 here, s[o] after the sum)
+    // per-column scales: the row's s; the lm_head form: q itself (scale 1 here, s[o] after the sum).  Loaded first:
+    // a load issued after the ring could only be waited for together with it.
     const float sc = SA == MI_I8_COL_SCALES && active ? P.s[o0 + i] : 1.0f;
+    // stage the split's activations (bf16 pairs, rows < B, row pitch xsp dwords) and, with per-row scales, its
+    // s[k0 .. k0 + cols) straight into LDS -- direct-to-LDS loads, 64 lanes x 4 bytes each, no registers -- issued
+    // ahead of the weight ring: loads complete in issue order, so waiting for all but the ring's loads waits for the
+    // activations only, and the ring keeps streaming while the workgroup meets at the barrier
+    const int cw = cols / 2, xsp = i8_pitch(cw), nch = (cw + 63) >> 6;
+    float *srow = (float *)(xs + a.B * xsp);
+    {
+        const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void *)a.x, (short)0, 0x7fffffff, kBufWord3);
+        const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc((void *)P.s, (short)0, 0x7fffffff, kBufWord3);
+        const int nrow = a.B * nch, n = nrow + (SA == MI_I8_ROW_SCALES ? cols / 64 : 0);
+        for (int e = wave; e < n; e += kI8Waves) {
+            if (e < nrow) {
+                const int b = e / nch, ch = e - b * nch, d = 64 * ch + lane;
+                const uint32_t voff = d < cw ? (uint32_t)(((size_t)b * a.n_in + k0) * 2 + 4 * d) : kI8Out;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (__attribute__((address_space(3))) void *)(xs + b * xsp + 64 * ch),
+                                                         4, voff, 0, 0, 0);
+            } else {
+                const int ch = e - nrow;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (__attribute__((address_space(3))) void *)(srow + 64 * ch), 4,
+                                                         (k0 + 64 * ch + lane) * 4, 0, 0, 0);
+            }
+        }
+    }
+    uint4 ring[kI8Ring][2];
+#pragma unroll
+    for (int d = 0; d < kI8Ring; ++d) load_block(d, ring[d][0], ring[d][1]);
+    vm_wait<2 * kI8Ring>();                          // every load but the ring's
+    lds_barrier();                                   // the ring stays in flight
+    if (!active && !SUMS) return;
     const float ns128 = -128.0f * sc;
 
     f32x4 acc[TT];
@@ -168,28 +188,22 @@ __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
     // B-operand rows: token jt of tile t (rows >= B read row B-1; those accumulator columns are not stored)
     const uint32_t *xrow[TT];
 #pragma unroll
-    for (int t = 0; t < TT; ++t) xrow[t] = xs + min(16 * t + i, a.B - 1) * cw + (W16 ? 4 : 16) * q;
+    for (int t = 0; t < TT; ++t) xrow[t] = xs + min(16 * t + i, a.B - 1) * xsp + (W16 ? 4 : 16) * q;
 
-    for (int p0 = 0; p0 < (active ? a.blocks : 0); p0 += kI8Ring) {
+    // block p of the split against the staged activations
+    auto consume = [&](int p, uint4 w0, uint4 w1) {
+        if constexpr (W16) {                          // the loads are the A operands (columns 64p + 32c + 8q ..)
 #pragma unroll
-        for (int d = 0; d < kI8Ring; ++d) {
-            const int p = p0 + d;
-            if (p >= a.blocks) break;
-            const uint4 w0 = ring[d][0], w1 = ring[d][1];
-            load_block(p + kI8Ring, ring[d][0], ring[d][1]);
-            if constexpr (W16) {                      // the loads are the A operands (columns 64p + 32c + 8q ..)
+            for (int c = 0; c < 2; ++c) {
+                const bf16x8 A = __builtin_bit_cast(bf16x8, c ? w1 : w0);
 #pragma unroll
-                for (int c = 0; c < 2; ++c) {
-                    const bf16x8 A = __builtin_bit_cast(bf16x8, c ? w1 : w0);
-#pragma unroll
-                    for (int t = 0; t < TT; ++t) {
-                        const uint4 xv = *(const uint4 *)(xrow[t] + 32 * p + 16 * c);
-                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, __builtin_bit_cast(bf16x8, xv), acc[t],
-                                                                         0, 0, 0);
-                    }
+                for (int t = 0; t < TT; ++t) {
+                    const uint4 xv = *(const uint4 *)(xrow[t] + 32 * p + 16 * c);
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, __builtin_bit_cast(bf16x8, xv), acc[t], 0, 0,
+                                                                     0);
                 }
-                continue;
             }
+        } else {
             const uint32_t W[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
@@ -208,7 +222,25 @@ __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
                 }
             }
         }
+    };
+    // whole groups of kI8Ring blocks: each slot refilled right after it is consumed (blocks past the split load zeros
+    // from the empty-range descriptor), no branch inside a group and the order pinned, so every slot keeps its
+    // registers and a block waits only for its own loads; then the 0 .. kI8Ring - 1 blocks left, already in the ring
+    const int groups = active ? a.blocks / kI8Ring : 0;
+    for (int g = 0; g < groups; ++g) {
+#pragma unroll
+        for (int d = 0; d < kI8Ring; ++d) {
+            const int p = g * kI8Ring + d;
+            __builtin_amdgcn_sched_barrier(0);
+            consume(p, ring[d][0], ring[d][1]);
+            __builtin_amdgcn_sched_barrier(0);
+            load_block(p + kI8Ring, ring[d][0], ring[d][1]);
+        }
     }
+    const int rest = active ? a.blocks - groups * kI8Ring : 0;
+#pragma unroll
+    for (int d = 0; d < kI8Ring - 1; ++d)
+        if (d < rest) consume(groups * kI8Ring + d, ring[d][0], ring[d][1]);
     // C layout: lane (jt = lane % 16, q) holds output rows o0 + 4q + r for token 16 t + jt
     const int o = o0 + 4 * q;
     if constexpr (SUMS) {
@@ -407,8 +439,11 @@ __global__ void __launch_bounds__(256) int8_tile_kernel(const int8_t *__restrict
     }
 }
 
-// LDS bytes per staged column: B bf16 activations (+ one f32 scale with per-input-row scales).
-static size_t i8_col_bytes(int B, int scale_axis) { return 2 * (size_t)B + (scale_axis == MI_I8_ROW_SCALES ? 4 : 0); }
+// LDS bytes of a split of `cols` columns: B staged activation rows at the padded pitch (+ one f32 scale per column
+// with per-input-row scales).
+static size_t i8_lds_bytes(int B, int cols, int scale_axis) {
+    return 4 * ((size_t)B * i8_pitch(cols / 2) + (scale_axis == MI_I8_ROW_SCALES ? (size_t)cols : 0));
+}
 
 // Columns per 2 KB block of a 16-row tile: 128 int8 or 64 bf16 weights.
 static int i8_block_cols(int form) { return form == kW16 ? 64 : 128; }
@@ -418,15 +453,14 @@ static int i8_block_cols(int form) { return form == kW16 ? 64 : 128; }
 // tiles of every projection of the launch.
 static int i8_splits(int B, int n_in, int tiles, int scale_axis) {
     const int nblk = n_in / i8_block_cols(scale_axis);
-    const size_t cb = i8_col_bytes(B, scale_axis);
     const int forced = tuning(kTuneI8S, 0);       // measurements: a forced split count (must divide the blocks)
-    if (forced > 0 && nblk % forced == 0 && (size_t)(n_in / forced) * cb <= 48 * 1024) return forced;
+    if (forced > 0 && nblk % forced == 0 && i8_lds_bytes(B, n_in / forced, scale_axis) <= 48 * 1024) return forced;
     int target = tuning(kTuneI8Waves, 3072);       // wavefronts to aim for
     if (target <= 0) target = 3072;
     int best = 1;
     for (int S = 1; S <= nblk; ++S) {
         if (nblk % S) continue;
-        if ((size_t)(n_in / S) * cb > 48 * 1024) continue;
+        if (i8_lds_bytes(B, n_in / S, scale_axis) > 48 * 1024) continue;
         if (nblk / S < 4 && S > 1) break;
         best = S;
         if ((long long)tiles * S >= target) break;
@@ -514,7 +548,7 @@ static int i8_launch(const uint16_t *x_bf16, int32_t B, int32_t n_in, const mi_i
     a.wg_start[n_proj] = wg;
     // the split sums in this launch when its row groups have counters (and there is more than one split or a pair)
     a.cnt = (a.S > 1 || pair) && ctrs <= kI8Ctrs && (i8_fuse() & (pair ? 2 : 1)) ? cnt : nullptr;
-    const size_t lds = i8_col_bytes(B, scale_axis) * i8_block_cols(scale_axis) * a.blocks;
+    const size_t lds = i8_lds_bytes(B, i8_block_cols(scale_axis) * a.blocks, scale_axis);
     hipStream_t st = (hipStream_t)stream;
     typedef void (*Kern)(I8Args);
     static const Kern kern[2][2][4] = {
