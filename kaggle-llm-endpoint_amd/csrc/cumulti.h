@@ -230,7 +230,7 @@ __global__ void __launch_bounds__(64 * kCuWaves, 1) cumulti_kernel(MArgs a) {
             [&]() { issue_rows(ge, ge_end - ge); },
             [&]() {
                 vm_wait<4 * RTW + 5>();             // the staging loads, issued ahead of the ring
-                __syncthreads();
+                lds_barrier();                      // ... which stays in flight
             });
     }
 }

@@ -351,7 +351,7 @@ __global__ void __launch_bounds__(64 * kCuWaves, 1) custream_kernel(CArgs a) {
         [&]() {
             if (form_h) form();
             else vm_wait<4 * RTW + 5>();            // the staging loads, issued ahead of the ring
-            __syncthreads();
+            lds_barrier();                          // ... which stays in flight
         });
     if (combine) combine_share();
 }

@@ -495,7 +495,7 @@ __global__ void __launch_bounds__(64 * kWgWaves, MI_CB3_WAVES) fused_decode_kern
                 stage_rows(cur);
             } else {
                 vm_wait<4 * RTW + 5>();   // the staging loads, issued ahead of the ring
-                __syncthreads();
+                lds_barrier();            // ... which stays in flight
             }
         });
     __syncthreads();              // the next stream restages the activation rows

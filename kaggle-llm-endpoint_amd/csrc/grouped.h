@@ -257,7 +257,7 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
             __builtin_amdgcn_sched_barrier(0);
             if (stage_ring) vm_wait<4 * RTW + 5>();
             else vm_wait<0>();
-            __syncthreads();
+            lds_barrier();                          // the weight ring stays in flight
             return;
         }
         const int q4 = xs >> 1;           // 4-column quads per row

@@ -162,7 +162,7 @@ __global__ void __launch_bounds__(64 * kWgWaves, MI_CB3_WAVES) pstream_kernel(PA
         },
         [&]() {
             vm_wait<4 * RTW + 5>();       // the staging loads, issued ahead of the ring
-            __syncthreads();
+            lds_barrier();                // ... which stays in flight
         });
 }
 
