@@ -20,6 +20,8 @@
  *   quant8.dequant_tree + x @ W (int8 projections)         quant8.py:91-99       -> mi_int8_project(_many)
  *   Engine._logits_local, int8 lm_head (scale after dot)   engine.py:345-351     -> mi_int8_project (MI_I8_COL_AFTER)
  *   mlp_partial over int8 leaves (shared expert, dense MLP) model.py:125-127,855  -> mi_int8_mlp
+ *   mlp_partial / x @ W over bf16 leaves (int8_nonexpert off) model.py:125-127,855, engine.py:281 -> mi_bf16_mlp,
+ *                                                                                   mi_bf16_project
  */
 #ifndef MI355MOE_H
 #define MI355MOE_H
@@ -324,9 +326,9 @@ size_t mi_int8_project_workspace(int32_t B, int32_t n_in, int32_t n_out, int32_t
 
 /*
  * The tiled layout of an int8 weight (no counterpart in the reference: a load-time repack, as the planar IQ tables
- * are): qT [n_out, n_in] -> tiled, n_out * n_in bytes, per 16-row tile and 128-column block one 2 KB piece in the
- * order the projection kernels load it (1 KB contiguous per wavefront load instead of 16 rows x 64 bytes at a
- * stride of n_in).  n_out % 16 == 0, n_in % 256 == 0, both pointers 16-byte aligned.  Pass MI_I8_TILED in
+ * are): qT [n_out, n_in] -> tiled, n_out * n_in bytes, per 128-column block b and 16-row tile t one 2 KB piece at
+ * (b * n_out / 16 + t) * 2048 in the order the projection kernels load it (1 KB contiguous per wavefront load
+ * instead of 16 rows x 64 bytes at a stride of n_in).  n_out % 16 == 0, n_in % 256 == 0, both pointers 16-byte aligned.  Pass MI_I8_TILED in
  * scale_axis (mi_int8_project, mi_int8_project_many; gu_scale_axis / down_scale_axis of mi_int8_mlp) with it.
  */
 int mi_int8_tile(const int8_t *qT, int32_t n_out, int32_t n_in, int8_t *tiled, void *stream);

@@ -511,13 +511,13 @@ def _scale_len(scale_axis, n_in, n_out):
 
 def int8_tile(qT):
     """qT int8 [n_out, n_in] (device) -> the same weights in the tiled layout of mi_int8_tile, int8
-    [n_out / 16, n_in / 128, 2048]: per 16-row tile and 128-column block the 2 KB the projection kernels load, 1 KB
+    [n_in / 128, n_out / 16, 2048]: per 128-column block and 16-row tile the 2 KB the projection kernels load, 1 KB
     of contiguous memory per wavefront load.  The int8 entry points take either form (a 3-d weight is a tiled one)."""
     n_out, n_in = qT.shape
     if n_out % 16 or n_in % 256:
         raise ValueError("int8_tile: n_out must be a multiple of 16 and n_in of 256 (got %d x %d)" % (n_out, n_in))
     qT = qT.contiguous()
-    out = torch.empty((n_out // 16, n_in // 128, 2048), dtype=torch.int8, device=qT.device)
+    out = torch.empty((n_in // 128, n_out // 16, 2048), dtype=torch.int8, device=qT.device)
     check("mi_int8_tile", lib().mi_int8_tile(_ptr(qT), n_out, n_in, _ptr(out), _stream()))
     return out
 
@@ -525,7 +525,7 @@ def int8_tile(qT):
 def _i8_dims(qT):
     """(n_out, n_in, layout bit) of a weight in either layout (3-d: tiled)."""
     if qT.dim() == 3:
-        return qT.shape[0] * 16, qT.shape[1] * 128, _lib.MI_I8_TILED
+        return qT.shape[1] * 16, qT.shape[0] * 128, _lib.MI_I8_TILED
     return qT.shape[0], qT.shape[1], 0
 
 

@@ -17,15 +17,15 @@ def _bits(t):
 
 @pytest.mark.parametrize("n_out,n_in", [(16, 256), (48, 512), (2048, 6144)])
 def test_int8_tile_layout(pkg, gpu, n_out, n_in):
-    """tiled[t, b, h * 1024 + l * 16 + j] = qT[16 t + l % 16, 128 b + 32 (l // 16) + 16 h + j]."""
+    """tiled[b, t, h * 1024 + l * 16 + j] = qT[16 t + l % 16, 128 b + 32 (l // 16) + 16 h + j]."""
     rng = np.random.default_rng(n_out + n_in)
     qT = rng.integers(-128, 128, (n_out, n_in), dtype=np.int8)
     got = pkg.int8_tile(torch.from_numpy(qT).cuda()).cpu().numpy()
-    assert got.shape == (n_out // 16, n_in // 128, 2048)
+    assert got.shape == (n_in // 128, n_out // 16, 2048)
     t, i, b, q, h, j = np.meshgrid(np.arange(n_out // 16), np.arange(16), np.arange(n_in // 128), np.arange(4),
                                    np.arange(2), np.arange(16), indexing="ij")
     want = np.zeros_like(got)
-    want[t, b, h * 1024 + (i + 16 * q) * 16 + j] = qT[16 * t + i, 128 * b + 32 * q + 16 * h + j]
+    want[b, t, h * 1024 + (i + 16 * q) * 16 + j] = qT[16 * t + i, 128 * b + 32 * q + 16 * h + j]
     assert np.array_equal(got, want)
 
 
