@@ -55,6 +55,7 @@ def parse():
     ap.add_argument("--only-prefill", action="store_true", help="the 512-token prefill chunk only (profiling runs)")
     ap.add_argument("--only-int8", action="store_true", help="the int8 projections and shared MLP only")
     ap.add_argument("--only-bf16", action="store_true", help="the shared expert's MLP over bf16 leaves only")
+    ap.add_argument("--only-route", action="store_true", help="the router at 1, 8 and 512 tokens only")
     ap.add_argument("--read-ceiling", action="store_true",
                     help="only the streaming-read probe (the part's practical HBM read rate)")
     ap.add_argument("--tune", action="append", default=[], metavar="NAME=VALUE",
@@ -270,6 +271,9 @@ def main():
         return
     if args.only_bf16:
         print(json.dumps({"bf16_mlp": bench_bf16_mlp(torch, pkg, torch.Generator(device="cuda"), args)}))
+        return
+    if args.only_route:
+        print(json.dumps({"route": bench_route(torch, pkg, torch.Generator(device="cuda"), args)}))
         return
     torch.manual_seed(0)
     gen = torch.Generator(device="cuda")

@@ -106,9 +106,11 @@ size_t mi_matvec_workspace(const mi_table *t, int32_t n_slots);
  * between gate/up and down (four launches, as mi_moe_decode_phases with phases = 3), except for CB3 tables at one
  * token: two launches, gate/up, then down, which forms h from the gate/up partials while staging and does the
  * combine itself (the last workgroup to finish each 16-row tile sums it in the combine launch's order; no waits).
- * The workspace (mi_moe_decode_workspace bytes) holds a counter block (info[15] of mi_moe_decode_plan, bytes), then
- * the partials and h; the counter block must be zero before the workspace's first call (a zero-filled allocation),
- * and every call leaves it zero.
+ * The workspace (mi_moe_decode_workspace bytes) holds a counter region of max(1 MiB, the layer's counter block)
+ * bytes (the block: info[15] of mi_moe_decode_plan), then the partials and h; the counter region must be zero before
+ * the workspace's first call (a zero-filled allocation), and every call leaves it zero.  The data never enters the
+ * first MiB, so layers of different shapes (whose counters sit at different offsets) may share one workspace when
+ * their counter blocks fit in it.
  * Calls that share a workspace must be ordered on one stream.
  */
 int mi_moe_decode(const mi_table *gate, const mi_table *up, const mi_table *down, const uint16_t *x_bf16,
@@ -161,7 +163,7 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
  * loops and harnesses that forbid hipMalloc).  No counterpart in the reference: its operator allocates through XLA.
  * The partials and h live in a static device array of MI_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends);
  * the call allocates nothing and returns MI_ERR_WORKSPACE when the layer's data region (the partials and h,
- * mi_moe_decode_workspace minus its counter block) exceeds the array less its first 256 KB -- the benchmark layer
+ * mi_moe_decode_workspace minus its counter region) exceeds the array less its first 256 KB -- the benchmark layer
  * (D 6144, I 2048) fits at every N <= 16, k = 8.  Same arguments (minus the workspace), launches and results as
  * mi_moe_decode (the first call on a GPU adds one fill launch).
  * Every call on one GPU shares that GPU's array: calls that overlap on one GPU (two streams, or two threads) race and

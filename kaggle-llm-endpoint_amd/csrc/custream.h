@@ -332,13 +332,16 @@ __global__ void __launch_bounds__(64 * kCuWaves, 1) custream_kernel(CArgs a) {
                     for (int i = 0; i < 4; ++i) acc[r][i] += __shfl_down(acc[r][i], 8, 16);
             }
             if (jt == 0 && cur.e >= 0 && cur.e < a.E) {
-                float *dst = a.part + ((size_t)(cur.split * nmat + cur.mat) * a.NS + cur.gi) * a.R +
-                             cur.rt * 16 * RTW + 4 * q;
+                const size_t off = ((size_t)(cur.split * nmat + cur.mat) * a.NS + cur.gi) * a.R +
+                                   cur.rt * 16 * RTW + 4 * q;
+                float *dst = a.part + off;
                 if (combine) {                      // read by other workgroups of this launch
+                    // the descriptor from the wave-uniform base, the lane's position as its offset: a descriptor
+                    // built per lane would need a loop over the lanes' distinct values
                     const __amdgpu_buffer_rsrc_t pr =
-                        __builtin_amdgcn_make_buffer_rsrc((void *)dst, (short)0, 0x7fffffff, kBufferWord3);
+                        __builtin_amdgcn_make_buffer_rsrc((void *)a.part, (short)0, 0x7fffffff, kBufferWord3);
 #pragma unroll
-                    for (int r = 0; r < RTW; ++r) wt_store4(pr, 64u * r, acc[r]);
+                    for (int r = 0; r < RTW; ++r) wt_store4(pr, (uint32_t)(4 * off) + 64u * r, acc[r]);
                 } else {
 #pragma unroll
                     for (int r = 0; r < RTW; ++r)

@@ -709,6 +709,16 @@ static CtrLayout ctr_layout(const mi_table *gate, const mi_table *down) {
     return c;
 }
 
+// The counter region at the start of a decode workspace: at least kDecodeCtrRegion bytes, so the partials and h start
+// at one offset for every layer shape whose counters fit.  A workspace shared by layers of different shapes then
+// never holds one shape's data where another keeps counters, which must be zero when its call starts (the counter
+// positions depend on the shape; every call leaves its own zero).
+constexpr size_t kDecodeCtrRegion = (size_t)1 << 20;
+static size_t ctr_region(const mi_table *gate, const mi_table *down) {
+    const size_t b = ctr_layout(gate, down).bytes;
+    return b > kDecodeCtrRegion ? b : kDecodeCtrRegion;
+}
+
 int occupancy_fused(int rtw, size_t lds);
 void launch_fused(int rtw, dim3 grid, size_t lds, hipStream_t s, const FArgs &a);
 
@@ -755,8 +765,7 @@ static FusedPlan plan_fused(const mi_table *gate, const mi_table *down, int N, i
     const long long tasks = (long long)p.G * (p.s1.RBG * p.s1.sp.S + p.s2.RBG * p.s2.sp.S);
     if (P > tasks) P = tasks;
     p.P = (int)(P < 1 ? 1 : P);
-    const CtrLayout cl = ctr_layout(gate, down);
-    size_t off = cl.bytes;
+    size_t off = ctr_region(gate, down);
     p.off_part1 = off;
     off = align256(off + sizeof(float) * (size_t)p.s1.sp.S * 2 * p.NS * gate->rows);
     p.off_h = off;
@@ -823,7 +832,7 @@ size_t mi_moe_decode_workspace(const mi_table *gate, const mi_table *down, int32
     // f32 activations)
     const size_t sep_b = plan_decode(gate, down, N, k, shared_expert).total;
     const size_t sep_f = plan_decode(gate, down, N, k, shared_expert, true).total;
-    const size_t sep = ctr_layout(gate, down).bytes + (sep_b > sep_f ? sep_b : sep_f);
+    const size_t sep = ctr_region(gate, down) + (sep_b > sep_f ? sep_b : sep_f);
     const size_t fused = plan_fused(gate, down, N, k, shared_expert).total;
     return sep > fused ? sep : fused;
 }
@@ -1125,11 +1134,12 @@ int mi_moe_decode_phases(const mi_table *gate, const mi_table *up, const mi_tabl
     if (st) return st;
     const DecodePlan p = plan_decode(gate, down, N, k, shared_expert);
     const CtrLayout cl = ctr_layout(gate, down);
-    if (!workspace || workspace_bytes < cl.bytes + p.total) return MI_ERR_WORKSPACE;
+    const size_t region = ctr_region(gate, down);
+    if (!workspace || workspace_bytes < region + p.total) return MI_ERR_WORKSPACE;
     // the single-token down launch's combine uses its row-tile counters of the block at the start of the workspace; the
     // fused launch's counters stay untouched
     return decode_launch(p, gate, up, down, x_bf16, false, N, k, idx, w, shared_expert, limit, out_f32, out_bf16,
-                         (char *)workspace + cl.bytes, phases, (hipStream_t)stream, (uint32_t *)workspace + cl.rt);
+                         (char *)workspace + region, phases, (hipStream_t)stream, (uint32_t *)workspace + cl.rt);
 }
 
 int mi_moe_decode_x(const mi_table *gate, const mi_table *up, const mi_table *down, const void *x, int32_t x_dtype,
@@ -1140,7 +1150,7 @@ int mi_moe_decode_x(const mi_table *gate, const mi_table *up, const mi_table *do
     if (st) return st;
     const bool xf32 = x_dtype == MI_X_F32;
     const DecodePlan p = plan_decode(gate, down, N, k, shared_expert, xf32);
-    const size_t ctr_bytes = ctr_layout(gate, down).bytes;
+    const size_t ctr_bytes = ctr_region(gate, down);
     if (!workspace || workspace_bytes < ctr_bytes + p.total) return MI_ERR_WORKSPACE;
     return decode_launch(p, gate, up, down, x, xf32, N, k, idx, w, shared_expert, limit, out_f32, out_bf16,
                          (char *)workspace + ctr_bytes, 3, (hipStream_t)stream);

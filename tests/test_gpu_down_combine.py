@@ -73,6 +73,28 @@ def test_in_launch_combine_full_shape_repeated_calls(pkg, gpu, full_cb3_layer):
         assert np.count_nonzero(_block_words(pkg, tbs, ws, 2, 2)) == 0, "call %d" % rep
 
 
+def test_workspace_shared_by_layer_shapes(pkg, gpu, full_cb3_layer):
+    """One decode workspace used by layers of two shapes in turn (a smaller layer, then the benchmark's matrices, and
+    again): the counter positions depend on the shape, so the partials of one shape must never land where the other
+    keeps its counters (a fixed counter region).  Every call equals the combine launch's result on a fresh
+    workspace and leaves its counters zero."""
+    _, big = full_cb3_layer
+    rng = np.random.default_rng(91)
+    small = Layer(rng, "CB3", 41, 2560, 1024).tables(pkg)
+    shapes = ((small, 2560, 40, 8, 40), (big, 6144, 2, 2, 2))
+    nbytes = max(pkg.resident.decode_workspace_bytes(t["gate"], t["down"], 1, k, se) for t, _, _, k, se in shapes)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+    for rep in range(4):
+        tbs, D, E, k, se = shapes[rep % 2]
+        idx, w = softmax_topk_routing(rng, 1, E, k)
+        x = _t(round_bf16(rng.standard_normal((1, D)).astype(np.float32)), torch.bfloat16)
+        of, ob = _run(pkg, tbs, x, _t(idx), _t(w), 10.0, se, ws, True)
+        fresh = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+        rf, rb = _run(pkg, tbs, x, _t(idx), _t(w), 10.0, se, fresh, False)
+        assert torch.equal(of, rf) and torch.equal(ob, rb), "call %d" % rep
+        assert np.count_nonzero(_block_words(pkg, tbs, ws, k, se)) == 0, "call %d" % rep
+
+
 def test_in_launch_combine_invalid_ids(pkg, gpu):
     """Ids outside [0, E) add nothing, as in the combine launch."""
     rng = np.random.default_rng(8)
