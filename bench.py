@@ -396,6 +396,10 @@ def main():
     # the same layer as one persistent launch (mi_moe_decode_fused), for comparison
     msf, bytesf = measure(1, softmax_topk, fused=True)
     extra["b1_one_launch"] = {"us_per_layer": round(msf * 1e3, 2), "GBps": round(bytesf / (msf * 1e-3) / 1e9, 1)}
+    # this box's streaming-read rate for the gate/up launch's bytes (parts differ by box): what the launch reaches of it
+    rc = bench_read_ceiling(torch, pkg, args, sizes=(118996992,), wgs=(1024, 16384))
+    extra["read_ceiling_gateup_bytes"] = {"GBps": rc["best_GBps"], "pct_hbm": rc["pct_hbm"],
+                                          "gateup_pct_of_it": round(100 * gbsg / rc["best_GBps"], 1)}
     if not args.only_b1:
         for N in (8, 16):
             ms, b = measure(N, zipf_topk)
@@ -460,17 +464,18 @@ def calib_copy(torch):
     torch.cuda.synchronize()
 
 
-def bench_read_ceiling(torch, pkg, args, launches=40):
+def bench_read_ceiling(torch, pkg, args, launches=40, sizes=(118996992, 2 * 118996992),
+                       wgs=(1024, 2048, 4096, 8192, 16384)):
     """The part's practical streaming-read rate (mi_read_probe): four regions of one size rotated between launches
     (three other regions, > the 256 MB last-level cache, are read between two reads of one region), `launches`
     launches captured in one graph and timed with events; sizes: one gate/up launch of the headline layer
     (118,996,992 B) and twice that; 1024 .. 16384 workgroups of 256 threads.  GB/s per configuration."""
     R, P = pkg.resident, pkg._lib
     res = {}
-    for size in (118996992, 2 * 118996992):
+    for size in sizes:
         regions = [torch.full((size,), i + 1, dtype=torch.uint8, device="cuda") for i in range(4)]
         sink = torch.empty(16384 * 4, dtype=torch.int32, device="cuda")
-        for wg in (1024, 2048, 4096, 8192, 16384):
+        for wg in wgs:
             fns = [lambda r=r, wg=wg: P.check("mi_read_probe", P.probe_lib().mi_read_probe(R._ptr(r), size, R._ptr(sink), wg,
                                                                                   R._stream()))
                    for r in regions]
