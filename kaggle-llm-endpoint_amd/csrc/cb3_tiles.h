@@ -274,21 +274,32 @@ __device__ __forceinline__ void dma_stage(uint32_t *xh, uint32_t *xl, int xsp, i
 
 // Column tile C of super tile st of segment w: publish / reload the codebook slots and refill the ring from segment
 // `src` at its super tile src_st (w's next super tile, or the next segment's first); decode only if `dec` (the
-// column tiles of a last, partial super tile that lie past the segment are not decoded).
-template <bool TWO, int RTW, int C>
+// column tiles of a last, partial super tile that lie past the segment are not decoded).  INNER: src_st is a super
+// tile of src that ends inside its split and is not its first (every refill load is in range: no per-load range
+// test, whose scalar selects otherwise cost about a quarter of the instructions of a super tile).
+template <bool TWO, int RTW, int C, bool INNER = false>
 __device__ __forceinline__ void cb3_ctile_src(const Cb3Wave &w, const Cb3Wave &src, int src_st, Cb3Regs<RTW> &s,
                                               int st, bool dec) {
     const int lane = threadIdx.x & 63;
     const int gn = 5 * src_st;
+    auto group = [&](int g) {
+        return INNER ? bload<MI_CB3_STREAM_POLICY>(src.cbb, src.cblane16, (uint32_t)g * src.g_bytes + src.row_bytes)
+                     : cb3_group(src, g);
+    };
+    auto tile = [&](int ct, int r) {
+        return INNER ? bload<MI_CB3_STREAM_POLICY>(src.qb, src.lane16,
+                                                    (uint32_t)ct * src.ct_bytes + src.rt_bytes + 1024u * r)
+                     : cb3_tile(src, ct, r);
+    };
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (C == 0) {
         w.cbl[0 * 64 + lane] = s.cbv[0];
         w.cbl[1 * 64 + lane] = s.cbv[1];
-        s.cbv[0] = cb3_group(src, gn);
-        s.cbv[1] = cb3_group(src, gn + 1);
+        s.cbv[0] = group(gn);
+        s.cbv[1] = group(gn + 1);
     } else {
         w.cbl[(C + 1) * 64 + lane] = s.cbv[C + 1];
-        s.cbv[C + 1] = cb3_group(src, gn + C + 1);
+        s.cbv[C + 1] = group(gn + C + 1);
     }
     const int ct = 4 * st + C, nct = 4 * src_st + C;
     if (dec) {
@@ -304,11 +315,11 @@ __device__ __forceinline__ void cb3_ctile_src(const Cb3Wave &w, const Cb3Wave &s
 #pragma unroll
         for (int r = 0; r < RTW; ++r) {
             cb3_steps<TWO, C, 0>(s.ring[C][r], cbrow, r, xb, xl, s.acc[r]);
-            s.ring[C][r] = cb3_tile(src, nct, r);
+            s.ring[C][r] = tile(nct, r);
         }
     } else {
 #pragma unroll
-        for (int r = 0; r < RTW; ++r) s.ring[C][r] = cb3_tile(src, nct, r);
+        for (int r = 0; r < RTW; ++r) s.ring[C][r] = tile(nct, r);
     }
 }
 
@@ -343,11 +354,20 @@ __device__ __forceinline__ void cb3_stream(Cb3Wave w, Next &&next, Store &&store
     for (;;) {
         const int st_last = (w.ctb - 1) >> 2;       // the segment's last super tile (maybe partial)
         int st = w.cta >> 2;
-        for (; st < st_last; ++st) {
+        // refills of super tiles st + 1 < st_last: whole super tiles inside the split (ct < 4 st_last <= ctb - 1, and
+        // their codebook groups <= 5 st_last - 1 <= g_last), none the split's first (ct > cta, groups > g_first)
+        for (; st + 1 < st_last; ++st) {
+            cb3_ctile_src<TWO, RTW, 0, true>(w, w, st + 1, s, st, true);
+            cb3_ctile_src<TWO, RTW, 1, true>(w, w, st + 1, s, st, true);
+            cb3_ctile_src<TWO, RTW, 2, true>(w, w, st + 1, s, st, true);
+            cb3_ctile_src<TWO, RTW, 3, true>(w, w, st + 1, s, st, true);
+        }
+        if (st < st_last) {                         // the refills of the last super tile, which may end early
             cb3_ctile_src<TWO, RTW, 0>(w, w, st + 1, s, st, true);
             cb3_ctile_src<TWO, RTW, 1>(w, w, st + 1, s, st, true);
             cb3_ctile_src<TWO, RTW, 2>(w, w, st + 1, s, st, true);
             cb3_ctile_src<TWO, RTW, 3>(w, w, st + 1, s, st, true);
+            ++st;
         }
         Cb3Wave nw = w;
         const bool more = next(nw);
