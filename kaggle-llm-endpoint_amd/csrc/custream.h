@@ -109,10 +109,19 @@ __device__ __forceinline__ float4 cu_combine4(const CArgs &a, const int *s_exp, 
 #ifndef MI_CU_WAVES
 #define MI_CU_WAVES 12
 #endif
-constexpr int kCuWaves = MI_CU_WAVES;   // wavefronts per workgroup (3 per SIMD)
+constexpr int kCuWaves = MI_CU_WAVES;   // wavefronts per workgroup (3 per SIMD): gate/up, and the multi-token launches
+// The single-token down launch: 16 wavefronts (4 per SIMD, within 128 registers).  Its share is ~13.5 units of 16
+// rows, so with 12 wavefronts some stream two units back to back and set the workgroup's end; with 16 each streams
+// at most one.  Measured: layer 47.8-47.9 against 48.2-48.5 µs (seven alternations on two boxes).
+constexpr int kCuDownWaves = 16;
+template <int MODE>
+__host__ __device__ constexpr int cu_waves() { return MODE == kDown ? kCuDownWaves : kCuWaves; }
+// h formation in the down launch: each thread forms at most kCuFormIt quads of 4 columns (two keep the launch within
+// 128 registers), so a workgroup forms up to kCuFormIt * 64 * kCuDownWaves quads (the host checks it)
+constexpr int kCuFormIt = 2;
 
 template <int MODE, int RTW>
-__global__ void __launch_bounds__(64 * kCuWaves, 1) custream_kernel(CArgs a) {
+__global__ void __launch_bounds__(64 * cu_waves<MODE>(), 1) custream_kernel(CArgs a) {
     // staged rows, then the wavefronts' codebook slots, all read with 16-byte LDS loads: the dynamic segment must
     // start 16-byte aligned (at an 8-byte-aligned start this launch measured 2.8x slower)
     extern __shared__ __attribute__((aligned(16))) uint32_t xlds[];
@@ -121,6 +130,7 @@ __global__ void __launch_bounds__(64 * kCuWaves, 1) custream_kernel(CArgs a) {
     __shared__ int s_last[MODE == kDown ? kCuMaxLast : 1];     // row tiles this workgroup combines
     constexpr bool hilo = MODE == kDown;            // h: hi in columns 0-7 of the tile, lo in 8-15
     constexpr int nmat = MODE == kGateUp ? 2 : 1;
+    constexpr int kWaves = cu_waves<MODE>();
     const int tid = threadIdx.x, lane = tid & 63, jt = lane & 15, q = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
@@ -138,7 +148,7 @@ __global__ void __launch_bounds__(64 * kCuWaves, 1) custream_kernel(CArgs a) {
     const int rows = hilo ? 2 * ng : 1;             // gate/up: the token's x row; down: hi and lo of each group's h
     uint4 *cbl = (uint4 *)(xlds + (size_t)rows * a.xsp);    // 16-byte aligned: the pitch is a multiple of 4 dwords
     if (tid == 0) {
-        s_next = (uint32_t)u_begin + kCuWaves;    // the first kCuWaves units are taken without a claim
+        s_next = (uint32_t)u_begin + kWaves;      // the first kWaves units are taken without a claim
         s_nlast = 0;
     }
     // every slot's expert into LDS (read there after the staging barrier: a claim then touches LDS only -- a global
@@ -203,7 +213,7 @@ __global__ void __launch_bounds__(64 * kCuWaves, 1) custream_kernel(CArgs a) {
             __builtin_amdgcn_make_buffer_rsrc((void *)a.x, (short)0, 0x7fffffff, kBufferWord3);
         const __amdgpu_buffer_rsrc_t rl =
             __builtin_amdgcn_make_buffer_rsrc((void *)(hilo ? a.x_lo : a.x), (short)0, 0x7fffffff, kBufferWord3);
-        for (int i = wave; i < rows * nch; i += kCuWaves) {
+        for (int i = wave; i < rows * nch; i += kWaves) {
             const int r = i / nch, ch = i - r * nch;
             const int c = 2 * (64 * ch + lane);
             const int src_row = hilo ? g0 + (r >> 1) : 0;          // slot of group g0 + r / 2 (one token)
@@ -225,7 +235,7 @@ __global__ void __launch_bounds__(64 * kCuWaves, 1) custream_kernel(CArgs a) {
     auto form = [&]() {
         // per pair of splits, every thread's partial loads first (at most kFormIt quads of 4 columns), then their
         // adds: one round trip per pair; the splits are summed in order from zero, as the SwiGLU launch sums them
-        constexpr int kFormIt = 4;
+        constexpr int kFormIt = kCuFormIt;
         const int cols = a.nu * kCb3TileCols, q4 = cols >> 2;
         const size_t plane = (size_t)a.NS * a.K;
         float4 g[kFormIt], uu[kFormIt];

@@ -607,6 +607,47 @@ static bool plan_cumulti(const mi_table *gate, const mi_table *down, int N, Deco
     return true;
 }
 
+// Plan of the single-token CU-balanced launches (custream.h); false when a launch's LDS would not fit a CU.
+static bool plan_custream(const mi_table *gate, const mi_table *down, int n_route, DecodePlan &p) {
+    // equal shares of (group, matrix, split, row tile) units over one workgroup per CU; splits are whole super
+    // tiles (the staged rows are the full activation, so a split never starts inside a super tile)
+    const int P = cu_count();
+    const int nb1 = (n_units_of(gate) + 3) / 4, nb2 = (n_units_of(down) + 3) / 4;
+    int S1 = tuning(kTuneCS1, 2), S2 = tuning(kTuneCS2, 1);      // measured best at D 6144, I 2048
+    int r1 = tuning(kTuneCS1Rtw, 1), r2 = tuning(kTuneCS2Rtw, 1);
+    S1 = S1 < 1 ? 1 : S1 > nb1 ? nb1 : S1;
+    S2 = S2 < 1 ? 1 : S2 > nb2 ? nb2 : S2;
+    r1 = (r1 == 2 || r1 == 4) ? r1 : 1;
+    r2 = (r2 == 2 || r2 == 4) ? r2 : 1;
+    p.s1 = Shape{Split{S1, 4}, r1, gate->rows / (16 * r1), 0};
+    p.s2 = Shape{Split{S2, 4}, r2, down->rows / (16 * r2), 0};
+    p.P1 = p.P2 = P;
+    const long long per_g2 = (long long)S2 * p.s2.RB;
+    const long long share = ((long long)p.NS * per_g2 + P - 1) / P;     // one group per slot
+    p.cgmax = (int)((share + per_g2 - 1) / per_g2) + 1;
+    if (p.cgmax > p.NS) p.cgmax = p.NS;
+    // codebook slots: 5 groups x 64 lanes per wavefront (the down launch has more wavefronts)
+    const size_t cbl1 = sizeof(uint4) * cu_waves<kGateUp>() * 5 * 64;
+    const size_t cbl2 = sizeof(uint4) * cu_waves<kDown>() * 5 * 64;
+    const size_t xsp1 = cb3_row_pitch(n_units_of(gate) * kCb3TileCols / 2);
+    const size_t xsp2 = cb3_row_pitch(n_units_of(down) * kCb3TileCols / 2);
+    const size_t scratch = 4 * (2 * (size_t)gate->n_experts + (size_t)n_route);
+    p.lds1 = sizeof(uint32_t) * xsp1 + cbl1;
+    p.lds2 = sizeof(uint32_t) * 2 * (size_t)p.cgmax * xsp2 + cbl2;
+    if (p.lds1 < scratch) p.lds1 = scratch;
+    if (p.lds2 < scratch) p.lds2 = scratch;
+    // more than half of a CU's LDS: a second workgroup never fits beside the first, whatever the register count
+    const size_t half = kLdsPerCu / 2 + 1024;
+    if (p.lds1 < half) p.lds1 = half;
+    if (p.lds2 < half) p.lds2 = half;
+    // the down launch combines its row tiles itself when no share completes more than kCuMaxLast of them
+    const long long share2 = ((long long)p.NS * S2 * p.s2.RB + P - 1) / P;
+    p.cu_combine = tuning(kTuneCuCombine, 1) != 0 && share2 <= kCuMaxLast;
+    // the launches' static LDS (routing copy, counters, row-tile list) is < 2 KB
+    const size_t cap = kLdsPerCu - 2048;
+    return p.lds1 <= cap && p.lds2 <= cap;
+}
+
 // xf32: f32 activations (staged as bf16 high part + remainder, one workgroup per task).
 static DecodePlan plan_decode(const mi_table *gate, const mi_table *down, int N, int k, int shared,
                               bool xf32 = false) {
@@ -622,46 +663,17 @@ static DecodePlan plan_decode(const mi_table *gate, const mi_table *down, int N,
     if (est < 1) est = 1;
     p.cu = gate->qtype == MI_QT_CB3 && down->qtype == MI_QT_CB3 && !xf32 && N == 1 &&
            tuning(kTuneCustream, 1) != 0;
+    if (p.cu && !plan_custream(gate, down, n_route, p)) {
+        p.cu = p.cu_combine = p.cgmax = 0;
+        p.lds1 = p.lds2 = 0;
+    }
     p.cum = !p.cu && gate->qtype == MI_QT_CB3 && down->qtype == MI_QT_CB3 && !xf32 && N >= 2 &&
             tuning(kTuneCumulti, 1) != 0;
     if (p.cum && !plan_cumulti(gate, down, N, p)) p.cum = 0;
     p.persistent = !p.cu && !p.cum && gate->qtype == MI_QT_CB3 && down->qtype == MI_QT_CB3 && !xf32 &&
                    N > tuning(kTunePersistAbove, kPersistentMinTokens);
-    if (p.cum) {
+    if (p.cum || p.cu) {
         // planned above
-    } else if (p.cu) {
-        // equal shares of (group, matrix, split, row tile) units over one workgroup per CU; splits are whole super
-        // tiles (the staged rows are the full activation, so a split never starts inside a super tile)
-        const int P = cu_count();
-        const int nb1 = (n_units_of(gate) + 3) / 4, nb2 = (n_units_of(down) + 3) / 4;
-        int S1 = tuning(kTuneCS1, 2), S2 = tuning(kTuneCS2, 1);      // measured best at D 6144, I 2048
-        int r1 = tuning(kTuneCS1Rtw, 1), r2 = tuning(kTuneCS2Rtw, 1);
-        S1 = S1 < 1 ? 1 : S1 > nb1 ? nb1 : S1;
-        S2 = S2 < 1 ? 1 : S2 > nb2 ? nb2 : S2;
-        r1 = (r1 == 2 || r1 == 4) ? r1 : 1;
-        r2 = (r2 == 2 || r2 == 4) ? r2 : 1;
-        p.s1 = Shape{Split{S1, 4}, r1, gate->rows / (16 * r1), 0};
-        p.s2 = Shape{Split{S2, 4}, r2, down->rows / (16 * r2), 0};
-        p.P1 = p.P2 = P;
-        const long long per_g2 = (long long)S2 * p.s2.RB;
-        const long long share = ((long long)p.NS * per_g2 + P - 1) / P;     // one group per slot
-        p.cgmax = (int)((share + per_g2 - 1) / per_g2) + 1;
-        if (p.cgmax > p.NS) p.cgmax = p.NS;
-        const size_t cbl = sizeof(uint4) * kCuWaves * 5 * 64;
-        const size_t xsp1 = cb3_row_pitch(n_units_of(gate) * kCb3TileCols / 2);
-        const size_t xsp2 = cb3_row_pitch(n_units_of(down) * kCb3TileCols / 2);
-        const size_t scratch = 4 * (2 * (size_t)gate->n_experts + (size_t)n_route);
-        p.lds1 = sizeof(uint32_t) * xsp1 + cbl;
-        p.lds2 = sizeof(uint32_t) * 2 * (size_t)p.cgmax * xsp2 + cbl;
-        if (p.lds1 < scratch) p.lds1 = scratch;
-        if (p.lds2 < scratch) p.lds2 = scratch;
-        // more than half of a CU's LDS: a second workgroup never fits beside the first, whatever the register count
-        const size_t half = kLdsPerCu / 2 + 1024;
-        if (p.lds1 < half) p.lds1 = half;
-        if (p.lds2 < half) p.lds2 = half;
-        // the down launch combines its row tiles itself when no share completes more than kCuMaxLast of them
-        const long long share2 = ((long long)p.NS * S2 * p.s2.RB + P - 1) / P;
-        p.cu_combine = tuning(kTuneCuCombine, 1) != 0 && share2 <= kCuMaxLast;
     } else if (p.persistent) {
         // persistent launches: tasks are pipelined, so the per-task fixed cost is small
         const long long slots = 3LL * cu_count();
@@ -995,7 +1007,8 @@ static int decode_launch(const DecodePlan &p, const mi_table *gate, const mi_tab
     // the CU-balanced down launch forms h itself while staging (bit-identical h, one launch fewer: ~2 us at one token;
     // the CU_FORM_H override 0 keeps the SwiGLU launch, for measurement)
     const bool cu_form = p.cu && tuning(kTuneCuFormH, 1) != 0 &&
-                         (long long)p.cgmax * (n_units_of(down) * kCb3TileCols / 4) <= 4LL * 64 * kCuWaves;
+                         (long long)p.cgmax * (n_units_of(down) * kCb3TileCols / 4) <=
+                             (long long)kCuFormIt * 64 * cu_waves<kDown>();
     if (!fuse_h && !cu_form) {
         const size_t n4 = (size_t)p.NS * gate->rows / 4;
         hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n4 + 63) / 64)), dim3(64), 0, s,
