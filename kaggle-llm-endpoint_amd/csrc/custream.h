@@ -203,11 +203,93 @@ __global__ void __launch_bounds__(64 * cu_waves<MODE>(), 1) custream_kernel(CArg
         w.xh = xlds + row * a.xsp + 320 * (w.cta >> 2) + 4 * q;
         w.xl = w.xh;
     };
+    // h rows of the share's groups from the gate/up partials.  The first pair of splits' partial loads are issued
+    // ahead of the wavefront's weight ring (issue): they come from the last-level cache while the ring's first tiles
+    // come from HBM, so h is formed before those land (issued behind the ring, the formation waited for them: the
+    // staging barrier came ~7 us into the launch)
+    constexpr int kFormIt = kCuFormIt;
+    float4 fg[kFormIt][2], fu[kFormIt][2];          // a pair of splits' gate / up partials, at most kFormIt quads
+    const int fq4 = (a.nu * kCb3TileCols) >> 2;     // quads of 4 columns per staged row
+    // buffer loads whose offset leaves the range where no partial is needed (they return zeros): no branch around
+    // a load, so the compiler never drains the loads in flight at a join (the partials are < 2 GB)
+    auto form_load = [&](int sp0) {
+        const __amdgpu_buffer_rsrc_t rgu =
+            __builtin_amdgcn_make_buffer_rsrc((void *)a.gu_part, (short)0, 0x7fffffff, kBufferWord3);
+        const uint32_t plane = (uint32_t)(a.NS * a.K);
+#pragma unroll
+        for (int it = 0; it < kFormIt; ++it) {
+            const int i = tid + it * (int)blockDim.x, j = i / fq4, c = 4 * (i - j * fq4);
+            const bool in = i < ng * fq4 && c < a.K;
+            const uint32_t o = (uint32_t)((g0 + j) * a.K + c);          // slot g0 + j (one token)
+#pragma unroll
+            for (int d = 0; d < 2; ++d) {
+                const int sp = sp0 + d;
+                const bool ld = in && sp < a.gu_S;
+                const uint32_t og = ld ? 4u * ((uint32_t)(2 * sp) * plane + o) : kStageOut;
+                const uint32_t ou = ld ? 4u * ((uint32_t)(2 * sp + 1) * plane + o) : kStageOut;
+                fg[it][d] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rgu, (int)og, 0, 0));
+                fu[it][d] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rgu, (int)ou, 0, 0));
+            }
+        }
+    };
+    // h = SwiGLU of the summed partials, as bf16 high part + remainder, into the staged rows
+    auto form_write = [&](const float4 (&g)[kFormIt], const float4 (&uu)[kFormIt]) {
+#pragma unroll
+        for (int it = 0; it < kFormIt; ++it) {
+            const int i = tid + it * (int)blockDim.x, j = i / fq4, c = 4 * (i - j * fq4);
+            if (i >= ng * fq4) break;
+            uint2 hv = make_uint2(0, 0), lv = make_uint2(0, 0);
+            if (c < a.K) {
+                uint32_t h0, l0, h1, l1, h2, l2, h3, l3;
+                split_bf16(swiglu_clamped(g[it].x, uu[it].x, a.limit), h0, l0);
+                split_bf16(swiglu_clamped(g[it].y, uu[it].y, a.limit), h1, l1);
+                split_bf16(swiglu_clamped(g[it].z, uu[it].z, a.limit), h2, l2);
+                split_bf16(swiglu_clamped(g[it].w, uu[it].w, a.limit), h3, l3);
+                hv = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
+                lv = make_uint2(l0 | (l1 << 16), l2 | (l3 << 16));
+            }
+            *(uint2 *)(xlds + (2 * j) * a.xsp + (c >> 1)) = hv;
+            *(uint2 *)(xlds + (2 * j + 1) * a.xsp + (c >> 1)) = lv;
+        }
+    };
+    // the adds of a loaded pair of splits, in split order (sp0 + d < gu_S)
+    auto form_add = [&](int sp0, float4 (&g)[kFormIt], float4 (&uu)[kFormIt]) {
+#pragma unroll
+        for (int it = 0; it < kFormIt; ++it)
+#pragma unroll
+            for (int d = 0; d < 2; ++d) {
+                if (sp0 + d >= a.gu_S) break;
+                g[it].x += fg[it][d].x; g[it].y += fg[it][d].y; g[it].z += fg[it][d].z; g[it].w += fg[it][d].w;
+                uu[it].x += fu[it][d].x; uu[it].y += fu[it][d].y; uu[it].z += fu[it][d].z; uu[it].w += fu[it][d].w;
+            }
+    };
+    // the splits summed in order from zero, as the SwiGLU launch sums them.  Up to 2 splits (the default) the pair
+    // loaded by issue is all there is: straight-line code, so the only loads it waits for are those partials, not
+    // the weight ring behind them.  More splits load each later pair here (a round trip each, behind the ring).
+    auto form_finish = [&]() {
+        float4 g[kFormIt], uu[kFormIt];
+#pragma unroll
+        for (int it = 0; it < kFormIt; ++it) g[it] = uu[it] = make_float4(0.f, 0.f, 0.f, 0.f);
+        form_add(0, g, uu);
+        if (a.gu_S > 2) {
+            for (int sp0 = 2; sp0 < a.gu_S; sp0 += 2) {
+                form_load(sp0);
+                form_add(sp0, g, uu);
+            }
+            form_write(g, uu);
+            vm_wait<0>();
+        } else {
+            form_write(g, uu);
+        }
+    };
     // staged rows straight into LDS (64 lanes x 4 bytes per load, spread over the wavefronts), issued ahead of every
     // wavefront's weight ring: columns past K read zeros
     const bool form_h = hilo && a.gu_part != nullptr;
     auto issue = [&]() {
-        if (form_h) return;                         // h is formed after the ring is issued (stage)
+        if (form_h) {                               // h: the partials' first loads now, formed in stage
+            form_load(0);
+            return;
+        }
         const int xs = (a.nu * kCb3TileCols) >> 1, nch = (xs + 63) >> 6;
         const __amdgpu_buffer_rsrc_t rh =
             __builtin_amdgcn_make_buffer_rsrc((void *)a.x, (short)0, 0x7fffffff, kBufferWord3);
@@ -230,61 +312,6 @@ __global__ void __launch_bounds__(64 * cu_waves<MODE>(), 1) custream_kernel(CArg
     Unit cur = unit_of(active ? u : u_begin, Glb{});
     Cb3Wave w;
     segment(cur, w);
-    // h rows of the share's groups from the gate/up partials: loads issued after the wavefront's ring, so they return
-    // in the same round trip as its first tiles
-    auto form = [&]() {
-        // per pair of splits, every thread's partial loads first (at most kFormIt quads of 4 columns), then their
-        // adds: one round trip per pair; the splits are summed in order from zero, as the SwiGLU launch sums them
-        constexpr int kFormIt = kCuFormIt;
-        const int cols = a.nu * kCb3TileCols, q4 = cols >> 2;
-        const size_t plane = (size_t)a.NS * a.K;
-        float4 g[kFormIt], uu[kFormIt];
-#pragma unroll
-        for (int it = 0; it < kFormIt; ++it) g[it] = uu[it] = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int sp0 = 0; sp0 < a.gu_S; sp0 += 2) {
-            float4 pg[kFormIt][2], pu[kFormIt][2];
-#pragma unroll
-            for (int it = 0; it < kFormIt; ++it) {
-                const int i = tid + it * (int)blockDim.x, j = i / q4, c = 4 * (i - j * q4);
-                const bool in = i < ng * q4 && c < a.K;
-                const size_t o = in ? (size_t)(g0 + j) * a.K + c : 0;       // slot g0 + j (one token)
-#pragma unroll
-                for (int d = 0; d < 2; ++d) {
-                    const int sp = sp0 + d;
-                    const bool ld = in && sp < a.gu_S;
-                    pg[it][d] = ld ? *(const float4 *)(a.gu_part + (size_t)(2 * sp) * plane + o)
-                                   : make_float4(0.f, 0.f, 0.f, 0.f);
-                    pu[it][d] = ld ? *(const float4 *)(a.gu_part + (size_t)(2 * sp + 1) * plane + o)
-                                   : make_float4(0.f, 0.f, 0.f, 0.f);
-                }
-            }
-#pragma unroll
-            for (int it = 0; it < kFormIt; ++it)
-#pragma unroll
-                for (int d = 0; d < 2; ++d) {
-                    if (sp0 + d >= a.gu_S) break;
-                    g[it].x += pg[it][d].x; g[it].y += pg[it][d].y; g[it].z += pg[it][d].z; g[it].w += pg[it][d].w;
-                    uu[it].x += pu[it][d].x; uu[it].y += pu[it][d].y; uu[it].z += pu[it][d].z; uu[it].w += pu[it][d].w;
-                }
-        }
-#pragma unroll
-        for (int it = 0; it < kFormIt; ++it) {
-            const int i = tid + it * (int)blockDim.x, j = i / q4, c = 4 * (i - j * q4);
-            if (i >= ng * q4) break;
-            uint2 hv = make_uint2(0, 0), lv = make_uint2(0, 0);
-            if (c < a.K) {
-                uint32_t h0, l0, h1, l1, h2, l2, h3, l3;
-                split_bf16(swiglu_clamped(g[it].x, uu[it].x, a.limit), h0, l0);
-                split_bf16(swiglu_clamped(g[it].y, uu[it].y, a.limit), h1, l1);
-                split_bf16(swiglu_clamped(g[it].z, uu[it].z, a.limit), h2, l2);
-                split_bf16(swiglu_clamped(g[it].w, uu[it].w, a.limit), h3, l3);
-                hv = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
-                lv = make_uint2(l0 | (l1 << 16), l2 | (l3 << 16));
-            }
-            *(uint2 *)(xlds + (2 * j) * a.xsp + (c >> 1)) = hv;
-            *(uint2 *)(xlds + (2 * j + 1) * a.xsp + (c >> 1)) = lv;
-        }
-    };
     // the combine in the launch: count the share's units on their row tiles once every partial is stored; the
     // arrival that completes a tile sums it (all wavefronts reach the barriers)
     auto combine_share = [&]() __attribute__((always_inline)) {
@@ -319,7 +346,7 @@ __global__ void __launch_bounds__(64 * cu_waves<MODE>(), 1) custream_kernel(CArg
     };
     if (!active) {
         issue();
-        if (form_h) form();
+        if (form_h) form_finish();
         vm_wait<0>();
         __syncthreads();
         if (combine) combine_share();
@@ -362,7 +389,7 @@ __global__ void __launch_bounds__(64 * cu_waves<MODE>(), 1) custream_kernel(CArg
         [&](const Cb3Wave &) { cur = unit_of(u, Lds{}); },
         issue,
         [&]() {
-            if (form_h) form();
+            if (form_h) form_finish();
             else vm_wait<4 * RTW + 5>();            // the staging loads, issued ahead of the ring
             lds_barrier();                          // ... which stays in flight
         });
