@@ -151,9 +151,6 @@ __global__ void __launch_bounds__(64 * cu_waves<MODE>(), 1) custream_kernel(CArg
         s_next = (uint32_t)u_begin + kWaves;      // the first kWaves units are taken without a claim
         s_nlast = 0;
     }
-    // every slot's expert into LDS (read there after the staging barrier: a claim then touches LDS only -- a global
-    // load inside the stream would make the wavefront wait for every weight load issued before it)
-    if (tid < n_groups) s_exp[tid] = tid < a.n_route ? a.idx[tid] : a.shared_expert;
 
     // unit u = (group gi, matrix, split, row tile), row tile fastest
     struct Unit {
@@ -286,10 +283,6 @@ __global__ void __launch_bounds__(64 * cu_waves<MODE>(), 1) custream_kernel(CArg
     // wavefront's weight ring: columns past K read zeros
     const bool form_h = hilo && a.gu_part != nullptr;
     auto issue = [&]() {
-        if (form_h) {                               // h: the partials' first loads now, formed in stage
-            form_load(0);
-            return;
-        }
         const int xs = (a.nu * kCb3TileCols) >> 1, nch = (xs + 63) >> 6;
         const __amdgpu_buffer_rsrc_t rh =
             __builtin_amdgcn_make_buffer_rsrc((void *)a.x, (short)0, 0x7fffffff, kBufferWord3);
@@ -306,6 +299,14 @@ __global__ void __launch_bounds__(64 * cu_waves<MODE>(), 1) custream_kernel(CArg
                                                      4, voff, 0, 0, 0);
         }
     };
+    // Gate/up: the x staging loads go first, before the routing is read (x does not depend on it), so they are in
+    // flight during the routing round trip and ahead of every weight load.  The down launch issues its partial
+    // loads after the routing, just ahead of the ring: issued here, their registers stayed live across the set-up
+    // and the launch spilled at its 128-register bound.
+    if (!form_h) issue();
+    // every slot's expert into LDS (read there after the staging barrier: a claim then touches LDS only -- a global
+    // load inside the stream would make the wavefront wait for every weight load issued before it)
+    if (tid < n_groups) s_exp[tid] = tid < a.n_route ? a.idx[tid] : a.shared_expert;
     // the wavefront's first unit, then claims (an empty unit range ends the wavefront after the staging barrier)
     int u = u_begin + wave;
     const bool active = u < u_end;
@@ -345,8 +346,10 @@ __global__ void __launch_bounds__(64 * cu_waves<MODE>(), 1) custream_kernel(CArg
         }
     };
     if (!active) {
-        issue();
-        if (form_h) form_finish();
+        if (form_h) {
+            form_load(0);
+            form_finish();
+        }
         vm_wait<0>();
         __syncthreads();
         if (combine) combine_share();
@@ -387,7 +390,9 @@ __global__ void __launch_bounds__(64 * cu_waves<MODE>(), 1) custream_kernel(CArg
             }
         },
         [&](const Cb3Wave &) { cur = unit_of(u, Lds{}); },
-        issue,
+        [&]() {                                     // gate/up: the staging loads were issued above
+            if (form_h) form_load(0);
+        },
         [&]() {
             if (form_h) form_finish();
             else vm_wait<4 * RTW + 5>();            // the staging loads, issued ahead of the ring
