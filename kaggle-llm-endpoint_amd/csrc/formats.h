@@ -17,6 +17,18 @@ __device__ __forceinline__ uint4 ldl(const uint32_t *__restrict__ base, uint32_t
     else return __builtin_bit_cast(uint4, *p);
 }
 
+// ldl's 16 bytes when `use` (wave-uniform), else zeros: a buffer load through a descriptor whose range is empty
+// when unused returns zeros without touching memory, so no branch surrounds the load.  (A load under a branch
+// makes the compiler wait for every load in flight where the branch rejoins: in the decoders' loops that drained
+// the next half-block's prefetched words at every half-block.)  NT: non-temporal (words read once); the scale and
+// d words, read again by the next half-block, keep the default policy.
+template <bool NT = MI_IQ_NT>
+__device__ __forceinline__ uint4 ldl_if(const uint32_t *base, uint32_t lane_off, bool use) {
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, use ? 0x7fffffff : 0, 0x00020000);
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)(lane_off << 2), 0, NT ? 2 : 0));
+}
+
 // ------------------------------------------------------------------------------------------------ IQ3_S
 // The reference's planar IQ3_S tables (planes.py:22-25): word w of a row covers inputs 16w .. 16w+15, group
 // j = 0..3 of the word covers 4 inputs 16w+4j .. 16w+4j+3.

@@ -98,34 +98,26 @@ __device__ __forceinline__ void iq2m_accum(const Iq2Table &tb, int e, int row0, 
     // half-blocks h (4 words, 4 k-steps): word 4h + j in step j; its qh and sc bytes are byte j of row h of those
     // planes; d in row h / 4 (half (h / 2) % 2)
     const int h0 = 2 * u0, h1 = 2 * u1;
-    const uint4 z4 = make_uint4(0, 0, 0, 0);
     uint4 rq[4], rs[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         rq[j] = ldl(qs + (size_t)(4 * h0 + j) * R, lo);
         rs[j] = ldl(sg + (size_t)(4 * h0 + j) * R, lo);
     }
-    uint4 qh_c = ldl(qh + (size_t)h0 * R, lo), sc_c = ldl(sc + (size_t)h0 * R, lo);
-    uint4 qh_n = h0 + 1 < h1 ? ldl(qh + (size_t)(h0 + 1) * R, lo) : z4;
-    uint4 sc_n = h0 + 1 < h1 ? ldl(sc + (size_t)(h0 + 1) * R, lo) : z4;
-    uint4 d_c = ldl(dd + (size_t)(h0 >> 2) * R, lo);
-    uint4 d_n = (h0 & ~3) + 4 < h1 ? ldl(dd + (size_t)((h0 >> 2) + 1) * R, lo) : z4;
+    // half-block h's qh, sc and d words, each loaded one half-block ahead (d again for every half-block: the loads
+    // never sit under a branch)
+    uint4 qh_n = ldl(qh + (size_t)h0 * R, lo), sc_n = ldl(sc + (size_t)h0 * R, lo);
+    uint4 d_n = ldl_if<false>(dd + (size_t)(h0 >> 2) * R, lo, true);
     stage();
     const float dmul = 0.125f;                                      // d / 8
     const uint32_t *xa0 = xa - (c0 >> 1), *xb0 = xb - (c0 >> 1);
     for (int h = h0; h < h1; ++h) {
-        if (h > h0) {
-            qh_c = qh_n;
-            sc_c = sc_n;
-            qh_n = h + 1 < h1 ? ldl(qh + (size_t)(h + 1) * R, lo) : z4;
-            sc_n = h + 1 < h1 ? ldl(sc + (size_t)(h + 1) * R, lo) : z4;
-            if ((h & 3) == 0) {
-                d_c = d_n;
-                d_n = h + 4 < h1 ? ldl(dd + (size_t)((h >> 2) + 1) * R, lo) : z4;
-            }
-        }
-        const uint32_t *xr = xa0 + 64 * h, *xr2 = xb0 + 64 * h;    // 64 dwords: the half-block's 128 columns
+        const uint4 qh_c = qh_n, sc_c = sc_n, d_c = d_n;
         const bool more = h + 1 < h1;
+        qh_n = ldl_if(qh + (size_t)(h + 1) * R, lo, more);
+        sc_n = ldl_if(sc + (size_t)(h + 1) * R, lo, more);
+        d_n = ldl_if<false>(dd + (size_t)((h + 1) >> 2) * R, lo, more);
+        const uint32_t *xr = xa0 + 64 * h, *xr2 = xb0 + 64 * h;    // 64 dwords: the half-block's 128 columns
         f32x4 ph[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) ph[r] = (f32x4){0.f, 0.f, 0.f, 0.f};
@@ -152,11 +144,9 @@ __device__ __forceinline__ void iq2m_accum(const Iq2Table &tb, int e, int row0, 
                 ph[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a0), wb, ph[r], 0, 0, 0);
                 if (TWO) ph[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, b0), wb, ph[r], 0, 0, 0);
             }
-            // the ring slot takes step j of the next half-block
-            if (more) {
-                rq[j] = ldl(qs + (size_t)(4 * (h + 1) + j) * R, lo);
-                rs[j] = ldl(sg + (size_t)(4 * (h + 1) + j) * R, lo);
-            }
+            // the ring slot takes step j of the next half-block (zeros past the split)
+            rq[j] = ldl_if(qs + (size_t)(4 * (h + 1) + j) * R, lo, more);
+            rs[j] = ldl_if(sg + (size_t)(4 * (h + 1) + j) * R, lo, more);
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {

@@ -68,34 +68,27 @@ __device__ __forceinline__ void iq3m_accum(const Iq3Table &tb, int e, int row0, 
     // bits in qh row h (nibble 2j + wsel), its scale in sc row h / 2 (nibble 4 (h % 2) + j), d in row h / 4
     // (half h / 2 % 2)
     const int h0 = 2 * u0, h1 = 2 * u1;
-    const uint4 z4 = make_uint4(0, 0, 0, 0);
     uint4 rq[4], rs[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         rq[j] = ldl(qs + (size_t)(8 * h0 + 2 * j + wsel) * R, lo);
         rs[j] = ldl(sg + (size_t)(4 * h0 + j) * R, lo);
     }
-    uint4 qh_c = ldl(qh + (size_t)h0 * R, lo);
-    uint4 qh_n = h0 + 1 < h1 ? ldl(qh + (size_t)(h0 + 1) * R, lo) : z4;
-    uint4 sc_c = ldl(sc + (size_t)(h0 >> 1) * R, lo);
-    uint4 sc_n = (h0 & ~1) + 2 < h1 ? ldl(sc + (size_t)((h0 >> 1) + 1) * R, lo) : z4;
-    uint4 d_c = ldl(dd + (size_t)(h0 >> 2) * R, lo);
-    uint4 d_n = (h0 & ~3) + 4 < h1 ? ldl(dd + (size_t)((h0 >> 2) + 1) * R, lo) : z4;
+    // half-block h's qh, sc and d words, each loaded one half-block ahead (sc and d again for every half-block: the
+    // loads never sit under a branch)
+    // the lane's word (wsel) goes into its offset: a buffer load's descriptor must be wave-uniform
+    const uint32_t lo_w = lo + (uint32_t)(wsel * R);
+    uint4 qh_n = ldl(qh + (size_t)h0 * R, lo);
+    uint4 sc_n = ldl_if<false>(sc + (size_t)(h0 >> 1) * R, lo, true);
+    uint4 d_n = ldl_if<false>(dd + (size_t)(h0 >> 2) * R, lo, true);
     stage();
     const uint32_t *xa0 = xa - (c0 >> 1), *xb0 = xb - (c0 >> 1);
     for (int h = h0; h < h1; ++h) {
-        if (h > h0) {
-            qh_c = qh_n;
-            qh_n = h + 1 < h1 ? ldl(qh + (size_t)(h + 1) * R, lo) : z4;
-            if ((h & 1) == 0) {
-                sc_c = sc_n;
-                sc_n = h + 2 < h1 ? ldl(sc + (size_t)((h >> 1) + 1) * R, lo) : z4;
-            }
-            if ((h & 3) == 0) {
-                d_c = d_n;
-                d_n = h + 4 < h1 ? ldl(dd + (size_t)((h >> 2) + 1) * R, lo) : z4;
-            }
-        }
+        const uint4 qh_c = qh_n, sc_c = sc_n, d_c = d_n;
+        const bool more = h + 1 < h1;
+        qh_n = ldl_if(qh + (size_t)(h + 1) * R, lo, more);
+        sc_n = ldl_if<false>(sc + (size_t)((h + 1) >> 1) * R, lo, more);
+        d_n = ldl_if<false>(dd + (size_t)((h + 1) >> 2) * R, lo, more);
         float dv[4];
         uint32_t qhl[4];                                            // the lane's high index bits, step j at bit 8j
 #pragma unroll
@@ -104,7 +97,6 @@ __device__ __forceinline__ void iq3m_accum(const Iq3Table &tb, int e, int row0, 
             qhl[r] = u4c(qh_c, r) >> qh_sh;
         }
         const int xo = 64 * h;                                      // dwords of the half-block's first column
-        const bool more = h + 1 < h1;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             __builtin_amdgcn_sched_barrier(0);
@@ -133,11 +125,9 @@ __device__ __forceinline__ void iq3m_accum(const Iq3Table &tb, int e, int row0, 
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[r][i] = fmaf(scale, p[i], acc[r][i]);
             }
-            // the ring slot takes step j of the next half-block
-            if (more) {
-                rq[j] = ldl(qs + (size_t)(8 * (h + 1) + 2 * j + wsel) * R, lo);
-                rs[j] = ldl(sg + (size_t)(4 * (h + 1) + j) * R, lo);
-            }
+            // the ring slot takes step j of the next half-block (zeros past the split)
+            rq[j] = ldl_if(qs + (size_t)(8 * (h + 1) + 2 * j) * R, lo_w, more);
+            rs[j] = ldl_if(sg + (size_t)(4 * (h + 1) + j) * R, lo, more);
         }
     }
 }

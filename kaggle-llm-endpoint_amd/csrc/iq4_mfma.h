@@ -90,35 +90,28 @@ __device__ __forceinline__ void iq4m_accum(const Iq4Table &tb, int e, int row0, 
     const uint32_t *sl = tb.sl + (size_t)e * tb.nblk * R;
     const uint32_t *sh = tb.sh + (size_t)e * tb.nblk * R;
     const uint32_t *dd = tb.d + (size_t)e * ((tb.nblk + 1) / 2) * R;
-    const uint4 z4 = make_uint4(0, 0, 0, 0);
     // half-blocks h (4 sub-blocks): the lane's word in sub-block 4 (h % 2) + j of block h / 2 is 16 h + 4 j + q
     const int h0 = 2 * u0, h1 = 2 * u1;
     uint4 ring[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) ring[j] = ldl(qs + (size_t)(16 * h0 + 4 * j + q) * R, lo);
-    uint4 sl_c = ldl(sl + (size_t)u0 * R, lo), sh_c = ldl(sh + (size_t)u0 * R, lo);
-    uint4 sl_n = u0 + 1 < u1 ? ldl(sl + (size_t)(u0 + 1) * R, lo) : z4;
-    uint4 sh_n = u0 + 1 < u1 ? ldl(sh + (size_t)(u0 + 1) * R, lo) : z4;
-    uint4 d_c = ldl(dd + (size_t)(u0 >> 1) * R, lo);
-    uint4 d_n = (u0 & ~1) + 2 < u1 ? ldl(dd + (size_t)((u0 >> 1) + 1) * R, lo) : z4;
+    // half-block h's block scales and d, each loaded one half-block ahead (again for a block's second half-block:
+    // the loads never sit under a branch)
+    // the lane's word (q) goes into its offset: a buffer load's descriptor must be wave-uniform
+    const uint32_t lo_q = lo + (uint32_t)(q * R);
+    uint4 sl_n = ldl_if<false>(sl + (size_t)u0 * R, lo, true), sh_n = ldl_if<false>(sh + (size_t)u0 * R, lo, true);
+    uint4 d_n = ldl_if<false>(dd + (size_t)(u0 >> 1) * R, lo, true);
     stage();
     const uint32_t *xa0 = xa - (c0 >> 1), *xb0 = xb - (c0 >> 1);
     for (int h = h0; h < h1; ++h) {
-        const int b = h >> 1;
-        if (h > h0 && (h & 1) == 0) {                               // a new block: its scales (and d)
-            sl_c = sl_n;
-            sh_c = sh_n;
-            sl_n = b + 1 < u1 ? ldl(sl + (size_t)(b + 1) * R, lo) : z4;
-            sh_n = b + 1 < u1 ? ldl(sh + (size_t)(b + 1) * R, lo) : z4;
-            if ((b & 1) == 0) {
-                d_c = d_n;
-                d_n = b + 2 < u1 ? ldl(dd + (size_t)((b >> 1) + 1) * R, lo) : z4;
-            }
-        }
+        const uint4 sl_c = sl_n, sh_c = sh_n, d_c = d_n;
         const bool more = h + 1 < h1;
+        sl_n = ldl_if<false>(sl + (size_t)((h + 1) >> 1) * R, lo, more);
+        sh_n = ldl_if<false>(sh + (size_t)((h + 1) >> 1) * R, lo, more);
+        d_n = ldl_if<false>(dd + (size_t)((h + 1) >> 2) * R, lo, more);
         iq4m_half<TWO>(L, h, d_c, sl_c, sh_c, xa0, xb0, acc, [&](int j) { return ring[j]; }, [&](int j) {
-            // the ring slot takes step j of the next half-block
-            if (more) ring[j] = ldl(qs + (size_t)(16 * (h + 1) + 4 * j + q) * R, lo);
+            // the ring slot takes step j of the next half-block (zeros past the split)
+            ring[j] = ldl_if(qs + (size_t)(16 * (h + 1) + 4 * j) * R, lo_q, more);
         });
     }
 }

@@ -56,6 +56,8 @@ __device__ __forceinline__ void kqm_accum(const KqTable &tb, int e, int row0, in
     // half-blocks h = 2 b + n: qs words 8h + 2q, 8h + 2q + 1; sc rows 2h, 2h + 1 (scale bytes 8n .. 8n + 7 of block
     // b); d row b; hm rows 8b + 2q, 8b + 2q + 1 (the hmask bytes of columns 4 q' + j, both halves)
     const int h0 = 2 * u0, h1 = 2 * u1;
+    // the lane's words (2 q, 2 q + 1) go into its offsets: a buffer load's descriptor must be wave-uniform
+    const uint32_t lo_a = lo + (uint32_t)(2 * q * R), lo_b = lo_a + (uint32_t)R;
     uint4 qa = ldl(qs + (size_t)(8 * h0 + 2 * q) * R, lo), qb = ldl(qs + (size_t)(8 * h0 + 2 * q + 1) * R, lo);
     uint4 sa = ldl(sc + (size_t)(2 * h0) * R, lo), sb = ldl(sc + (size_t)(2 * h0 + 1) * R, lo);
     uint4 d_c = ldl(dd + (size_t)(h0 >> 1) * R, lo);
@@ -70,18 +72,18 @@ __device__ __forceinline__ void kqm_accum(const KqTable &tb, int e, int row0, in
     const uint4 ones4 = make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
     for (int h = h0; h < h1; ++h) {
         const int n = h & 1;
-        // next half-block's words (and the next block's d and hmask), one half-block ahead
+        // next half-block's words and its block's d (and hmask), one half-block ahead: zeros past the split, and a
+        // block's d and hmask read again for its second half-block, so no load sits under a branch
         const bool more = h + 1 < h1;
-        const uint4 qa_n = more ? ldl(qs + (size_t)(8 * (h + 1) + 2 * q) * R, lo) : z4;
-        const uint4 qb_n = more ? ldl(qs + (size_t)(8 * (h + 1) + 2 * q + 1) * R, lo) : z4;
-        const uint4 sa_n = more ? ldl(sc + (size_t)(2 * (h + 1)) * R, lo) : z4;
-        const uint4 sb_n = more ? ldl(sc + (size_t)(2 * (h + 1) + 1) * R, lo) : z4;
-        const bool nb = more && n == 1;                             // the next half-block starts a new block
-        const uint4 d_n = nb ? ldl(dd + (size_t)((h + 1) >> 1) * R, lo) : d_c;
+        const uint4 qa_n = ldl_if(qs + (size_t)(8 * (h + 1)) * R, lo_a, more);
+        const uint4 qb_n = ldl_if(qs + (size_t)(8 * (h + 1)) * R, lo_b, more);
+        const uint4 sa_n = ldl_if(sc + (size_t)(2 * (h + 1)) * R, lo, more);
+        const uint4 sb_n = ldl_if(sc + (size_t)(2 * (h + 1) + 1) * R, lo, more);
+        const uint4 d_n = ldl_if<false>(dd + (size_t)((h + 1) >> 1) * R, lo, more);
         uint4 ha_n = ha, hb_n = hb;
-        if (Q3 && nb) {
-            ha_n = ldl(hm + (size_t)(8 * ((h + 1) >> 1) + 2 * q) * R, lo);
-            hb_n = ldl(hm + (size_t)(8 * ((h + 1) >> 1) + 2 * q + 1) * R, lo);
+        if constexpr (Q3) {
+            ha_n = ldl_if<false>(hm + (size_t)(8 * ((h + 1) >> 1)) * R, lo_a, more);
+            hb_n = ldl_if<false>(hm + (size_t)(8 * ((h + 1) >> 1)) * R, lo_b, more);
         }
         float dv[4], mv[4];
 #pragma unroll
