@@ -179,6 +179,7 @@ struct PfShared {
 
 // CB3: 160-column tiles of the code-tile layout; codebook slots per 640-column super tile (cb3_tiles.h).
 struct PfCb3 {
+    static constexpr bool kLdsOnlyBarrier = false;
     static constexpr int kCols = kCb3TileCols;
     static constexpr bool kSplit = false;   // whole tasks only: K pieces measured slower (561 against 536 us)
     static constexpr int kQOff = 4;
@@ -233,6 +234,16 @@ __device__ __forceinline__ uint32_t pf_bf16_pair(float a, float b) {   // round 
     return __builtin_bit_cast(uint32_t, v);
 }
 
+// One plane word (4 bytes) per lane at base + off if `use`, else zero: a buffer load through a descriptor whose
+// range is empty when unused (no memory touched), so no branch surrounds the load and the compiler's wait counts
+// stay exact (a load under a branch made it wait for every load in flight where the branch rejoins).  base must be
+// wave-uniform: the lane's word and row go into off.
+__device__ __forceinline__ uint32_t pf_word(const char *base, uint32_t off, bool use) {
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, use ? 0x7fffffff : 0, kBufferWord3);
+    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+}
+
 struct PfIq3Wave {
     const char *qs, *sg, *qh, *sc, *dd;     // expert e's planes
     uint32_t rpitch;                        // bytes per plane row (4 R)
@@ -248,6 +259,7 @@ struct PfIq3Regs {
 };
 
 struct PfIq3 {
+    static constexpr bool kLdsOnlyBarrier = true;
     static constexpr bool kSplit = true;    // the last round's tasks split into K pieces
     static constexpr int kCols = kIq3TileCols;
     static constexpr int kQOff = 8;
@@ -256,16 +268,16 @@ struct PfIq3 {
     static __device__ __forceinline__ int n_tiles(const PfArgs &a, int mat) {
         return (mat ? a.i1 : a.i0).K / kIq3TileCols;
     }
-    static __device__ __forceinline__ void load(const Wave &w, int ct, uint32_t (&u)[7], int r) {
+    static __device__ __forceinline__ void load(const Wave &w, int ct, uint32_t (&u)[7], int r, bool use) {
         const uint32_t o = w.lrow + 64u * (uint32_t)r, P = w.rpitch;
-        const int q = w.q;
-        u[0] = *(const uint32_t *)(w.qs + (uint32_t)(8 * ct + q) * P + o);
-        u[1] = *(const uint32_t *)(w.qs + (uint32_t)(8 * ct + 4 + q) * P + o);
-        u[2] = *(const uint32_t *)(w.sg + (uint32_t)(4 * ct + (q >> 1)) * P + o);
-        u[3] = *(const uint32_t *)(w.sg + (uint32_t)(4 * ct + 2 + (q >> 1)) * P + o);
-        u[4] = *(const uint32_t *)(w.qh + (uint32_t)ct * P + o);
-        u[5] = *(const uint32_t *)(w.sc + (uint32_t)(ct >> 1) * P + o);
-        u[6] = *(const uint32_t *)(w.dd + (uint32_t)(ct >> 2) * P + o);
+        const uint32_t oq = (uint32_t)w.q * P + o, oq2 = (uint32_t)(w.q >> 1) * P + o;
+        u[0] = pf_word(w.qs + (size_t)(8 * ct) * P, oq, use);
+        u[1] = pf_word(w.qs + (size_t)(8 * ct + 4) * P, oq, use);
+        u[2] = pf_word(w.sg + (size_t)(4 * ct) * P, oq2, use);
+        u[3] = pf_word(w.sg + (size_t)(4 * ct + 2) * P, oq2, use);
+        u[4] = pf_word(w.qh + (size_t)ct * P, o, use);
+        u[5] = pf_word(w.sc + (size_t)(ct >> 1) * P, o, use);
+        u[6] = pf_word(w.dd + (size_t)(ct >> 2) * P, o, use);
     }
     static __device__ __forceinline__ void init(Wave &w, Regs &s, const PfArgs &a, PfShared &sh, int mat, int e,
                                                 int rg, int wave, int lane, int st0, int st1) {
@@ -286,7 +298,7 @@ struct PfIq3 {
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
-            for (int r = 0; r < kPfRtw; ++r) load(w, 4 * st0 + c, s.v[c][r], r);
+            for (int r = 0; r < kPfRtw; ++r) load(w, 4 * st0 + c, s.v[c][r], r, true);
     }
     // the 8 weights of step j of column tile ct for the row tile whose plane words are u
     static __device__ __forceinline__ bf16x8 weights8(const Wave &w, const uint32_t (&u)[7], int ct, int j) {
@@ -328,11 +340,9 @@ struct PfIq3 {
                 A = An;
             }
         }
-        // the slot's next column tile (ct + 2); past the row's end nothing is loaded (the slot is not read again)
-        if (ct + 2 < w.CT) {
+        // the slot's next column tile (ct + 2); past the row's end the loads read zeros (the slot is not read again)
 #pragma unroll
-            for (int r = 0; r < kPfRtw; ++r) load(w, ct + 2, s.v[C & 1][r], r);
-        }
+        for (int r = 0; r < kPfRtw; ++r) load(w, ct + 2, s.v[C & 1][r], r, ct + 2 < w.CT);
     }
 };
 
@@ -355,19 +365,20 @@ struct PfIq2Regs {
 };
 
 struct PfIq2 {
+    static constexpr bool kLdsOnlyBarrier = true;
     static constexpr bool kSplit = true;    // the last round's tasks split into K pieces
     static constexpr int kCols = 128;
     static constexpr int kQOff = 16;       // dwords: word q of the tile
     using Wave = PfIq2Wave;
     using Regs = PfIq2Regs;
     static __device__ __forceinline__ int n_tiles(const PfArgs &a, int mat) { return (mat ? a.j1 : a.j0).K / 128; }
-    static __device__ __forceinline__ void load(const Wave &w, int ct, uint32_t (&u)[5], int r) {
-        const uint32_t o = w.lrow + 64u * (uint32_t)r, P = w.rpitch;
-        u[0] = *(const uint32_t *)(w.qs + (uint32_t)(4 * ct + w.q) * P + o);
-        u[1] = *(const uint32_t *)(w.sg + (uint32_t)(4 * ct + w.q) * P + o);
-        u[2] = *(const uint32_t *)(w.qh + (uint32_t)ct * P + o);        // byte q: word 4 ct + q
-        u[3] = *(const uint32_t *)(w.sc + (uint32_t)ct * P + o);
-        u[4] = *(const uint32_t *)(w.dd + (uint32_t)(ct >> 2) * P + o);
+    static __device__ __forceinline__ void load(const Wave &w, int ct, uint32_t (&u)[5], int r, bool use) {
+        const uint32_t o = w.lrow + 64u * (uint32_t)r, P = w.rpitch, oq = (uint32_t)w.q * P + o;
+        u[0] = pf_word(w.qs + (size_t)(4 * ct) * P, oq, use);
+        u[1] = pf_word(w.sg + (size_t)(4 * ct) * P, oq, use);
+        u[2] = pf_word(w.qh + (size_t)ct * P, o, use);                  // byte q: word 4 ct + q
+        u[3] = pf_word(w.sc + (size_t)ct * P, o, use);
+        u[4] = pf_word(w.dd + (size_t)(ct >> 2) * P, o, use);
     }
     static __device__ __forceinline__ void init(Wave &w, Regs &s, const PfArgs &a, PfShared &sh, int mat, int e,
                                                 int rg, int wave, int lane, int st0, int st1) {
@@ -388,7 +399,7 @@ struct PfIq2 {
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
-            for (int r = 0; r < kPfRtw; ++r) load(w, 4 * st0 + c, s.v[c][r], r);
+            for (int r = 0; r < kPfRtw; ++r) load(w, 4 * st0 + c, s.v[c][r], r, true);
     }
     // the 8 weights of step j (group j of the lane's word) for the row tile whose plane words are u
     static __device__ __forceinline__ bf16x8 weights8(const Wave &w, const uint32_t (&u)[5], int ct, int j) {
@@ -426,11 +437,9 @@ struct PfIq2 {
                 A = An;
             }
         }
-        // the slot's next column tile (ct + 2); past the row's end nothing is loaded (the slot is not read again)
-        if (ct + 2 < w.CT) {
+        // the slot's next column tile (ct + 2); past the row's end the loads read zeros (the slot is not read again)
 #pragma unroll
-            for (int r = 0; r < kPfRtw; ++r) load(w, ct + 2, s.v[C & 1][r], r);
-        }
+        for (int r = 0; r < kPfRtw; ++r) load(w, ct + 2, s.v[C & 1][r], r, ct + 2 < w.CT);
     }
 };
 
@@ -452,23 +461,25 @@ struct PfKqRegs {
 
 template <bool Q3>
 struct PfKq {
+    static constexpr bool kLdsOnlyBarrier = true;
     static constexpr bool kSplit = true;    // the last round's tasks split into K pieces
     static constexpr int kCols = 128;
     static constexpr int kQOff = 4;        // dwords: columns 8q .. 8q+7 of a 32-column stripe
     using Wave = PfKqWave;
     using Regs = PfKqRegs;
     static __device__ __forceinline__ int n_tiles(const PfArgs &a, int mat) { return (mat ? a.q1 : a.q0).K / 128; }
-    static __device__ __forceinline__ void load(const Wave &w, int ct, uint32_t (&u)[7], int r) {
+    static __device__ __forceinline__ void load(const Wave &w, int ct, uint32_t (&u)[7], int r, bool use) {
         const uint32_t o = w.lrow + 64u * (uint32_t)r, P = w.rpitch;
+        const uint32_t oa = (uint32_t)(2 * w.q) * P + o, ob = oa + P;
         const int b = ct >> 1;
-        u[0] = *(const uint32_t *)(w.qs + (uint32_t)(8 * ct + 2 * w.q) * P + o);
-        u[1] = *(const uint32_t *)(w.qs + (uint32_t)(8 * ct + 2 * w.q + 1) * P + o);
-        u[2] = *(const uint32_t *)(w.sc + (uint32_t)(2 * ct) * P + o);
-        u[3] = *(const uint32_t *)(w.sc + (uint32_t)(2 * ct + 1) * P + o);
-        u[4] = *(const uint32_t *)(w.dd + (uint32_t)b * P + o);
-        if (Q3) {
-            u[5] = *(const uint32_t *)(w.hm + (uint32_t)(8 * b + 2 * w.q) * P + o);
-            u[6] = *(const uint32_t *)(w.hm + (uint32_t)(8 * b + 2 * w.q + 1) * P + o);
+        u[0] = pf_word(w.qs + (size_t)(8 * ct) * P, oa, use);
+        u[1] = pf_word(w.qs + (size_t)(8 * ct) * P, ob, use);
+        u[2] = pf_word(w.sc + (size_t)(2 * ct) * P, o, use);
+        u[3] = pf_word(w.sc + (size_t)(2 * ct + 1) * P, o, use);
+        u[4] = pf_word(w.dd + (size_t)b * P, o, use);
+        if constexpr (Q3) {
+            u[5] = pf_word(w.hm + (size_t)(8 * b) * P, oa, use);
+            u[6] = pf_word(w.hm + (size_t)(8 * b) * P, ob, use);
         }
     }
     static __device__ __forceinline__ void init(Wave &w, Regs &s, const PfArgs &a, PfShared &sh, int mat, int e,
@@ -488,7 +499,7 @@ struct PfKq {
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
-            for (int r = 0; r < kPfRtw; ++r) load(w, 4 * st0 + c, s.v[c][r], r);
+            for (int r = 0; r < kPfRtw; ++r) load(w, 4 * st0 + c, s.v[c][r], r, true);
     }
     // 4 weights from the 4 byte-sized values of t (each 0..3, Q3_K 0..7): f32 -> bf16 pairs
     static __device__ __forceinline__ uint2 four(uint32_t t, float m, float a) {
@@ -535,11 +546,9 @@ struct PfKq {
                 A = An;
             }
         }
-        // the slot's next column tile (ct + 2); past the row's end nothing is loaded (the slot is not read again)
-        if (ct + 2 < w.CT) {
+        // the slot's next column tile (ct + 2); past the row's end the loads read zeros (the slot is not read again)
 #pragma unroll
-            for (int r = 0; r < kPfRtw; ++r) load(w, ct + 2, s.v[C & 1][r], r);
-        }
+        for (int r = 0; r < kPfRtw; ++r) load(w, ct + 2, s.v[C & 1][r], r, ct + 2 < w.CT);
     }
 };
 
@@ -561,19 +570,20 @@ struct PfIq4Regs {
 };
 
 struct PfIq4 {
+    static constexpr bool kLdsOnlyBarrier = true;
     static constexpr bool kSplit = true;    // the last round's tasks split into K pieces
     static constexpr int kCols = 128;
     static constexpr int kQOff = 2;        // dwords: columns 4q .. 4q+3 of a 32-column group
     using Wave = PfIq4Wave;
     using Regs = PfIq4Regs;
     static __device__ __forceinline__ int n_tiles(const PfArgs &a, int mat) { return (mat ? a.k1 : a.k0).K / 128; }
-    static __device__ __forceinline__ void load(const Wave &w, int ct, uint32_t (&u)[7], int r) {
-        const uint32_t o = w.lrow + 64u * (uint32_t)r, P = w.rpitch;
+    static __device__ __forceinline__ void load(const Wave &w, int ct, uint32_t (&u)[7], int r, bool use) {
+        const uint32_t o = w.lrow + 64u * (uint32_t)r, P = w.rpitch, oq = (uint32_t)w.q * P + o;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) u[j] = *(const uint32_t *)(w.qs + (uint32_t)(16 * ct + 4 * j + w.q) * P + o);
-        u[4] = *(const uint32_t *)(w.sl + (uint32_t)(ct >> 1) * P + o);
-        u[5] = *(const uint32_t *)(w.sh + (uint32_t)(ct >> 1) * P + o);
-        u[6] = *(const uint32_t *)(w.dd + (uint32_t)(ct >> 2) * P + o);
+        for (int j = 0; j < 4; ++j) u[j] = pf_word(w.qs + (size_t)(16 * ct + 4 * j) * P, oq, use);
+        u[4] = pf_word(w.sl + (size_t)(ct >> 1) * P, o, use);
+        u[5] = pf_word(w.sh + (size_t)(ct >> 1) * P, o, use);
+        u[6] = pf_word(w.dd + (size_t)(ct >> 2) * P, o, use);
     }
     static __device__ __forceinline__ void init(Wave &w, Regs &s, const PfArgs &a, PfShared &sh, int mat, int e,
                                                 int rg, int wave, int lane, int st0, int st1) {
@@ -592,7 +602,7 @@ struct PfIq4 {
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
-            for (int r = 0; r < kPfRtw; ++r) load(w, 4 * st0 + c, s.v[c][r], r);
+            for (int r = 0; r < kPfRtw; ++r) load(w, 4 * st0 + c, s.v[c][r], r, true);
     }
     // the 8 weights of step j (sub-block 4 (ct % 2) + j) for the row tile whose plane words are u
     static __device__ __forceinline__ bf16x8 weights8(const Wave &w, const uint32_t (&u)[7], int ct, int j) {
@@ -633,11 +643,9 @@ struct PfIq4 {
                 A = An;
             }
         }
-        // the slot's next column tile (ct + 2); past the row's end nothing is loaded (the slot is not read again)
-        if (ct + 2 < w.CT) {
+        // the slot's next column tile (ct + 2); past the row's end the loads read zeros (the slot is not read again)
 #pragma unroll
-            for (int r = 0; r < kPfRtw; ++r) load(w, ct + 2, s.v[C & 1][r], r);
-        }
+        for (int r = 0; r < kPfRtw; ++r) load(w, ct + 2, s.v[C & 1][r], r, ct + 2 < w.CT);
     }
 };
 
@@ -681,13 +689,14 @@ __device__ __forceinline__ void prefill_body(const PfArgs &a, PfShared &sh, int 
     const int xr0 = tid / kXU, xc8 = tid - xr0 * kXU;
     const bool stager = tid < kXRows * kXU;
     uint4 xr[kXJ];
-    auto load_x = [&](int ct) {
+    // use: whether the tile is staged at all (no branch around the loads: past the range they read zeros)
+    auto load_x = [&](int ct, bool use) {
         const int lim = (a.K - WP::kCols * ct) >> 3;          // uint4 columns of this tile inside the row
 #pragma unroll
         for (int j = 0; j < kXJ; ++j) {
             const int row = xr0 + kXRows * j;
             uint32_t o = kXOut;
-            if (stager && row < 16 * NTT && xc8 < lim)
+            if (use && stager && row < 16 * NTT && xc8 < lim)
                 o = xrowoff[row] + 16u * (uint32_t)xc8 + (uint32_t)(2 * WP::kCols * ct);
             xr[j] = bload(xbuf, o, 0);
         }
@@ -699,7 +708,7 @@ __device__ __forceinline__ void prefill_body(const PfArgs &a, PfShared &sh, int 
             if (stager && row < 16 * NTT) *(uint4 *)(xs + buf * kXBuf + row * kPfXPitch + 4 * xc8) = xr[j];
         }
     };
-    load_x(4 * s0);
+    load_x(4 * s0, true);
     store_x(0);
 
     f32x4 acc[kPfRtw][NTT];
@@ -712,12 +721,20 @@ __device__ __forceinline__ void prefill_body(const PfArgs &a, PfShared &sh, int 
 
     // one barrier per column tile: tile ct sits in buffer ct & 1 (= C & 1); the next tile's loads are issued first
     // (ahead of this tile's code and codebook loads, so waiting for them never waits for those) and stored into the
-    // other buffer after this tile's matrix-core work, which every wavefront finished reading one barrier earlier
+    // other buffer after this tile's matrix-core work, which every wavefront finished reading one barrier earlier.
+    // The block formats' barrier orders LDS only (lds_barrier): a full __syncthreads also waits for every weight
+    // load in flight, the prefetched next tiles included (IQ3_S 831 -> 761 us at 512 tokens with it).  CB3 keeps the
+    // full barrier and the branch around its staging loads: without them its GEMMs measured slower.
     auto step = [&](auto Cc, int st) {
         constexpr int C = decltype(Cc)::value;
         const int ct = 4 * st + C;
-        __syncthreads();
-        if (ct + 1 < ct_end) load_x(ct + 1);
+        if constexpr (WP::kLdsOnlyBarrier) {
+            lds_barrier();
+            load_x(ct + 1, ct + 1 < ct_end);                // no branch around the loads
+        } else {
+            __syncthreads();
+            if (ct + 1 < ct_end) load_x(ct + 1, true);
+        }
         WP::template tile<NTT, C>(w, s, st, xrow + (C & 1) * kXBuf, acc);
         if (ct + 1 < ct_end) store_x((C + 1) & 1);
     };
