@@ -313,14 +313,12 @@ __device__ __forceinline__ void cb3_ctile_src(const Cb3Wave &w, const Cb3Wave &s
         }
         const uint4 *cbrow = w.cbl + (lane & 15);
 #pragma unroll
-        for (int r = 0; r < RTW; ++r) {
-            cb3_steps<TWO, C, 0>(s.ring[C][r], cbrow, r, xb, xl, s.acc[r]);
-            s.ring[C][r] = tile(nct, r);
-        }
-    } else {
-#pragma unroll
-        for (int r = 0; r < RTW; ++r) s.ring[C][r] = tile(nct, r);
+        for (int r = 0; r < RTW; ++r) cb3_steps<TWO, C, 0>(s.ring[C][r], cbrow, r, xb, xl, s.acc[r]);
     }
+    // the refills outside the branch: a load under a branch makes the compiler wait for every load in flight where
+    // the branch rejoins, which drained the ring at every segment's last super tile (its dec is a run-time value)
+#pragma unroll
+    for (int r = 0; r < RTW; ++r) s.ring[C][r] = tile(nct, r);
 }
 
 // Streams segment w and the ones `next` hands out.
