@@ -121,64 +121,61 @@ __global__ void dequant_kernel(Table tb, int e, float *out) {
 // ------------------------------------------------------------------------------------------------ finishing kernels
 // Routing-weighted combine of the down partials: out[n] = sum_j w[n, j] * sum_s part[s][n*k + j]  (+ the shared
 // expert's sum_s part[s][n_route + n]), experts in routing order, splits in order.  Invalid ids (outside [0, E))
-// contribute nothing.  One thread per 4 output rows of one token; the contributing slots are listed first so every
-// partial load of a chunk of experts is issued before the first add (the loads are independent).
+// contribute nothing.  One thread per output row of one token, so a wave reads 256 contiguous bytes per partial and
+// even one token spreads over D/64 waves.  The work is a few MB at most, so the launch is bound by round trips:
+// every load of a chunk of experts -- up to kCombineSplits splits of each, the routing ids and the weights -- is issued
+// in bounds and without a branch before the first add (a missing split or slot reads split s0 / slot 0, whose value
+// is then left out), one round trip per chunk instead of one per split plus two for the ids and weights.
 constexpr int kCombineChunk = 9;
+constexpr int kCombineSplits = 8;
 __global__ void __launch_bounds__(64) combine_kernel(const float *__restrict__ part, int S, int NS, int D, int N,
                                                      int k, const int32_t *__restrict__ idx,
                                                      const float *__restrict__ w, int E, int shared, int n_route,
                                                      float *out_f32, uint16_t *out_bf16) {
-    const int q4 = D >> 2;
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= N * q4) return;
-    const int tok = i / q4, r = 4 * (i - tok * q4);
+    if (i >= N * D) return;
+    const int tok = i / D, r = i - tok * D;
     const int nj = k + (shared >= 0 ? 1 : 0);
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    float acc = 0.f;
     for (int j0 = 0; j0 < nj; j0 += kCombineChunk) {
-        int slot[kCombineChunk];
-        // the slot of every column: its partials are loaded together with the routing ids and weights, in one round
-        // trip (in bounds for every slot); a slot whose expert id is outside [0, E) is left out of the sum afterwards
+        int slot[kCombineChunk], e[kCombineChunk];
+        float wt[kCombineChunk], ys[kCombineChunk];
 #pragma unroll
         for (int jj = 0; jj < kCombineChunk; ++jj) {
             const int j = j0 + jj;
-            slot[jj] = j < k ? tok * k + j : j < nj ? n_route + tok : -1;
+            slot[jj] = j < k ? tok * k + j : j < nj ? n_route + tok : 0;
+            const int rj = tok * k + (j < k ? j : 0);          // in bounds: k >= 1
+            e[jj] = idx[rj];
+            wt[jj] = w[rj];
+            ys[jj] = 0.f;
         }
-        float4 ys[kCombineChunk];
+        for (int s0 = 0; s0 < S; s0 += kCombineSplits) {
+            float p[kCombineSplits][kCombineChunk];
 #pragma unroll
-        for (int jj = 0; jj < kCombineChunk; ++jj) ys[jj] = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int s = 0; s < S; ++s) {
-            float4 p[kCombineChunk];
+            for (int ss = 0; ss < kCombineSplits; ++ss) {
+                const int s = s0 + ss < S ? s0 + ss : s0;
 #pragma unroll
-            for (int jj = 0; jj < kCombineChunk; ++jj)
-                p[jj] = slot[jj] >= 0 ? *(const float4 *)(part + ((size_t)s * NS + slot[jj]) * D + r)
-                                      : make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-            for (int jj = 0; jj < kCombineChunk; ++jj) {
-                ys[jj].x += p[jj].x; ys[jj].y += p[jj].y; ys[jj].z += p[jj].z; ys[jj].w += p[jj].w;
+                for (int jj = 0; jj < kCombineChunk; ++jj) p[ss][jj] = part[((size_t)s * NS + slot[jj]) * D + r];
             }
+#pragma unroll
+            for (int ss = 0; ss < kCombineSplits; ++ss)
+                if (s0 + ss < S) {
+#pragma unroll
+                    for (int jj = 0; jj < kCombineChunk; ++jj) ys[jj] += p[ss][jj];
+                }
         }
 #pragma unroll
         for (int jj = 0; jj < kCombineChunk; ++jj) {
             const int j = j0 + jj;
             if (j < k) {
-                const int e = idx[tok * k + j];
-                if (e >= 0 && e < E) {
-                    const float wt = w[tok * k + j];
-                    acc.x = fmaf(wt, ys[jj].x, acc.x); acc.y = fmaf(wt, ys[jj].y, acc.y);
-                    acc.z = fmaf(wt, ys[jj].z, acc.z); acc.w = fmaf(wt, ys[jj].w, acc.w);
-                }
+                if (e[jj] >= 0 && e[jj] < E) acc = fmaf(wt[jj], ys[jj], acc);
             } else if (j < nj) {
-                acc.x += ys[jj].x; acc.y += ys[jj].y; acc.z += ys[jj].z; acc.w += ys[jj].w;
+                acc += ys[jj];
             }
         }
     }
-    if (out_f32) *(float4 *)(out_f32 + (size_t)tok * D + r) = acc;
-    if (out_bf16) {
-        uint2 b;
-        b.x = f32_to_bf16_rne(acc.x) | (f32_to_bf16_rne(acc.y) << 16);
-        b.y = f32_to_bf16_rne(acc.z) | (f32_to_bf16_rne(acc.w) << 16);
-        *(uint2 *)(out_bf16 + (size_t)tok * D + r) = b;
-    }
+    if (out_f32) out_f32[(size_t)tok * D + r] = acc;
+    if (out_bf16) out_bf16[(size_t)tok * D + r] = (uint16_t)f32_to_bf16_rne(acc);
 }
 
 // h = silu(min(g, L)) * clip(u, -L, L) (model.py:119-122) of the gate/up split partials, splits summed in order:
@@ -1098,7 +1095,7 @@ static int decode_launch(const DecodePlan &p, const mi_table *gate, const mi_tab
         launch_grouped<kDown>(down->qtype, b.t_rows, p.s2.rtw, dim3(p.G * p.s2.RBG * p.s2.sp.S), lds2, s, b);
     }
     if ((st = launch_status())) return st;
-    const int D = down->rows, nthr = N * (D / 4);
+    const int D = down->rows, nthr = N * D;
     hipLaunchKernelGGL(combine_kernel, dim3((nthr + 63) / 64), dim3(64), 0, s, b.part, p.s2.sp.S, p.NS, D, N, k, idx, w,
                        gate->n_experts, shared_expert, N * k, out_f32, out_bf16);
     return launch_status();
