@@ -155,29 +155,47 @@ __global__ void __launch_bounds__(64 * kCuWaves, 1) cumulti_kernel(MArgs a) {
         w.xh = xlds + row * a.xsp + 4 * q;
         w.xl = hilo && TWO ? w.xh + N * a.xsp : w.xh;
     };
-    // staged rows straight into LDS (64 lanes x 4 bytes per load, spread over the wavefronts), issued ahead of every
-    // wavefront's weight ring: columns past the split read zeros
+    // staged rows straight into LDS, spread over the wavefronts, issued ahead of every wavefront's weight ring:
+    // columns past the split read zeros.  Whole 256-dword chunks of a row load 16 bytes per lane, the rest 4 (an
+    // LDS-bound load costs about as much per instruction whatever its width)
     auto issue_rows = [&](int g_first_st, int n_st) {
-        const int xs = 80 * (ctb - cta), nch = (xs + 63) >> 6;     // whole column tiles (past K: zeros)
+        const int xs = 80 * (ctb - cta);                            // whole column tiles (past K: zeros)
+        const int n16 = (a.K & 7) == 0 ? xs >> 8 : 0, nt = (xs - 256 * n16 + 63) >> 6;
         const __amdgpu_buffer_rsrc_t rh =
             __builtin_amdgcn_make_buffer_rsrc((void *)a.x, (short)0, 0x7fffffff, kBufferWord3);
         const __amdgpu_buffer_rsrc_t rl =
             __builtin_amdgcn_make_buffer_rsrc((void *)(hilo ? a.x_lo : a.x), (short)0, 0x7fffffff, kBufferWord3);
         const int rows = hilo ? n_st * rows_per_g : N;
-        for (int i = wave; i < rows * nch; i += kCuWaves) {
-            const int r = i / nch, ch = i - r * nch;
-            const int c = c0 + 2 * (64 * ch + lane);
+        auto src_of = [&](int r, bool &lo) {
             int src = r;                            // gate/up: token r
-            bool lo = false;
+            lo = false;
             if constexpr (hilo) {                   // down: group g_first_st + r / 2N, token (r % 2N) % N
                 const int lg = r / rows_per_g, rr = r - lg * rows_per_g;
                 lo = rr >= N;
                 src = s_gslot[g_first_st + lg][rr - (lo ? N : 0)];
             }
+            return src;
+        };
+        // columns c .. c + 7 (c0, c1 and K multiples of 8: a lane is wholly inside the split or wholly past it)
+        for (int i = wave; i < rows * n16; i += kCuWaves) {
+            const int r = i / n16, ch = i - r * n16;
+            const int c = c0 + 512 * ch + 8 * lane;
+            bool lo;
+            const int src = src_of(r, lo);
             const uint32_t voff = (src >= 0 && c < c1) ? (uint32_t)((size_t)src * a.K + c) * 2u : kStageOut;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(lo ? rl : rh,
                                                      (__attribute__((address_space(3))) void *)(xlds + r * a.xsp +
-                                                                                                 64 * ch),
+                                                                                                 256 * ch),
+                                                     16, voff, 0, 0, 0);
+        }
+        for (int i = wave; i < rows * nt; i += kCuWaves) {
+            const int r = i / nt, d0 = 256 * n16 + 64 * (i - r * nt);
+            const int c = c0 + 2 * (d0 + lane);
+            bool lo;
+            const int src = src_of(r, lo);
+            const uint32_t voff = (src >= 0 && c < c1) ? (uint32_t)((size_t)src * a.K + c) * 2u : kStageOut;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(lo ? rl : rh,
+                                                     (__attribute__((address_space(3))) void *)(xlds + r * a.xsp + d0),
                                                      4, voff, 0, 0, 0);
         }
     };

@@ -279,23 +279,36 @@ __global__ void __launch_bounds__(64 * cu_waves<MODE>(), 1) custream_kernel(CArg
             form_write(g, uu);
         }
     };
-    // staged rows straight into LDS (64 lanes x 4 bytes per load, spread over the wavefronts), issued ahead of every
-    // wavefront's weight ring: columns past K read zeros
+    // staged rows straight into LDS, spread over the wavefronts, issued ahead of every wavefront's weight ring:
+    // columns past K read zeros.  Whole 256-dword chunks of a row load 16 bytes per lane, the rest 4: an LDS-bound
+    // load costs about as much per instruction whatever its width (a one-token down launch that loaded 64 KB of
+    // partials this way per workgroup took 7.4 us longer with 4-byte lanes, 1.7 with 16-byte lanes).
     const bool form_h = hilo && a.gu_part != nullptr;
     auto issue = [&]() {
-        const int xs = (a.nu * kCb3TileCols) >> 1, nch = (xs + 63) >> 6;
+        const int xs = (a.nu * kCb3TileCols) >> 1;
+        const int n16 = (a.K & 7) == 0 ? xs >> 8 : 0, nt = (xs - 256 * n16 + 63) >> 6;
         const __amdgpu_buffer_rsrc_t rh =
             __builtin_amdgcn_make_buffer_rsrc((void *)a.x, (short)0, 0x7fffffff, kBufferWord3);
         const __amdgpu_buffer_rsrc_t rl =
             __builtin_amdgcn_make_buffer_rsrc((void *)(hilo ? a.x_lo : a.x), (short)0, 0x7fffffff, kBufferWord3);
-        for (int i = wave; i < rows * nch; i += kWaves) {
-            const int r = i / nch, ch = i - r * nch;
-            const int c = 2 * (64 * ch + lane);
+        // columns c .. c + 7 (c and K multiples of 8: a lane is wholly inside K or wholly past it)
+        for (int i = wave; i < rows * n16; i += kWaves) {
+            const int r = i / n16, ch = i - r * n16;
+            const int c = 512 * ch + 8 * lane;
             const int src_row = hilo ? g0 + (r >> 1) : 0;          // slot of group g0 + r / 2 (one token)
             const uint32_t voff = c < a.K ? (uint32_t)((size_t)src_row * a.K + c) * 2u : kStageOut;
             __builtin_amdgcn_raw_ptr_buffer_load_lds((hilo && (r & 1)) ? rl : rh,
                                                      (__attribute__((address_space(3))) void *)(xlds + r * a.xsp +
-                                                                                                 64 * ch),
+                                                                                                 256 * ch),
+                                                     16, voff, 0, 0, 0);
+        }
+        for (int i = wave; i < rows * nt; i += kWaves) {
+            const int r = i / nt, d0 = 256 * n16 + 64 * (i - r * nt);
+            const int c = 2 * (d0 + lane);
+            const int src_row = hilo ? g0 + (r >> 1) : 0;
+            const uint32_t voff = c < a.K ? (uint32_t)((size_t)src_row * a.K + c) * 2u : kStageOut;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds((hilo && (r & 1)) ? rl : rh,
+                                                     (__attribute__((address_space(3))) void *)(xlds + r * a.xsp + d0),
                                                      4, voff, 0, 0, 0);
         }
     };
