@@ -242,8 +242,8 @@ __device__ __forceinline__ void cb3_accum_mfma(const Cb3Wave &w, f32x4 (&acc)[RT
 
 // ------------------------------------------------------------------------------------------------ staging
 // Stages activation rows r < t_rows of columns [c0, c1) (dword d of a row = columns c0 + 2d, c0 + 2d + 1) of one or
-// two bf16 planes into LDS (row pitch xsp dwords) with direct-to-LDS loads -- 64 lanes x 4 bytes per instruction, no
-// registers -- spread over the workgroup's wavefronts.  Row r reads plane row row_of(r) (negative: zeros); columns
+// two bf16 planes into LDS (row pitch xsp dwords) with direct-to-LDS loads -- 64 lanes x 16 or 4 bytes per
+// instruction, no registers -- spread over the workgroup's wavefronts.  Row r reads plane row row_of(r) (negative: zeros); columns
 // outside [cv, cend) read zeros.  The loads complete in issue order with the wavefront's other loads, so a wait for
 // "all but the N loads issued since" (vm_wait<N>) followed by a workgroup barrier publishes the rows.
 template <bool HILO, class RowOf>
@@ -253,14 +253,29 @@ __device__ __forceinline__ void dma_stage(uint32_t *xh, uint32_t *xl, int xsp, i
     const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc((void *)ph, (short)0, 0x7fffffff, kBufferWord3);
     const __amdgpu_buffer_rsrc_t rl =
         __builtin_amdgcn_make_buffer_rsrc((void *)(HILO ? pl : ph), (short)0, 0x7fffffff, kBufferWord3);
-    const int xs = (c1 - c0) >> 1, nch = (xs + 63) >> 6, per_row = (HILO ? 2 : 1) * nch;
-    for (int i = wave; i < t_rows * per_row; i += 4) {
-        const int t = i / per_row, r = i - t * per_row, plane = r / nch, ch = r - plane * nch;
+    // whole 256-dword chunks of a row with 16 bytes per lane when every bound is a multiple of 8 columns (a lane is
+    // then wholly inside or wholly outside [cv, cend)), the rest with 4: an LDS-bound load costs about as much per
+    // instruction whatever its width
+    const int xs = (c1 - c0) >> 1;
+    const int n16 = ((c0 | cv | cend | stride) & 7) == 0 ? xs >> 8 : 0, nt = (xs - 256 * n16 + 63) >> 6;
+    const int per16 = (HILO ? 2 : 1) * n16, pert = (HILO ? 2 : 1) * nt;
+    for (int i = wave; i < t_rows * per16; i += 4) {
+        const int t = i / per16, r = i - t * per16, plane = r / n16, ch = r - plane * n16;
         const int row = row_of(t);
-        const int c = c0 + 2 * (64 * ch + lane);
+        const int c = c0 + 512 * ch + 8 * lane;
         const uint32_t voff =
             (row >= 0 && c >= cv && c < cend) ? (uint32_t)((size_t)row * stride + c) * 2u : kStageOut;
-        uint32_t *dst = (plane ? xl : xh) + t * xsp + 64 * ch;
+        uint32_t *dst = (plane ? xl : xh) + t * xsp + 256 * ch;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(plane ? rl : rh, (__attribute__((address_space(3))) void *)dst, 16,
+                                                 voff, 0, 0, 0);
+    }
+    for (int i = wave; i < t_rows * pert; i += 4) {
+        const int t = i / pert, r = i - t * pert, plane = r / nt, d0 = 256 * n16 + 64 * (r - plane * nt);
+        const int row = row_of(t);
+        const int c = c0 + 2 * (d0 + lane);
+        const uint32_t voff =
+            (row >= 0 && c >= cv && c < cend) ? (uint32_t)((size_t)row * stride + c) * 2u : kStageOut;
+        uint32_t *dst = (plane ? xl : xh) + t * xsp + d0;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(plane ? rl : rh, (__attribute__((address_space(3))) void *)dst, 4,
                                                  voff, 0, 0, 0);
     }

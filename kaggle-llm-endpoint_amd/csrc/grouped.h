@@ -227,7 +227,7 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
     // (buffer_load ... lds), issued BEFORE the first weight loads.  A wavefront's loads complete in issue order, so
     // the staging then waits only for these loads, not for the weight ring behind them, and each tile's matrix-core
     // work starts as soon as that tile arrives.
-    // (with many staged rows the 4-byte loads outnumber the register path's 8-byte ones: register staging there)
+    // (with many staged rows the direct loads outnumber the register path's 8-byte ones: register staging there)
     const bool dma = cb3 && a.x_f32 == nullptr && a.gu_part == nullptr && a.t_rows <= kDmaStageRows;
     bool stage_ring = true;     // the wavefront issues its weight ring before staging (false: it only stages)
     if (dma) {
@@ -236,15 +236,28 @@ __global__ void __launch_bounds__(64 * kWgWaves, min_waves_per_simd<QT>()) group
         const __amdgpu_buffer_rsrc_t rl =
             __builtin_amdgcn_make_buffer_rsrc((void *)(hilo ? a.x_lo : a.x_bf16), (short)0, 0x7fffffff, kBufferWord3);
         const int cend = min(c1, a.K);
-        const int nch = (xs + 63) >> 6, per_row = (hilo ? 2 : 1) * nch;
-        for (int i = wave; i < a.t_rows * per_row; i += kWgWaves) {
-            const int t = i / per_row, r = i - t * per_row, plane = r / nch, ch = r - plane * nch;
+        // whole 256-dword chunks with 16 bytes per lane when every bound is a multiple of 8 columns, the rest with 4
+        const int n16 = ((c0 | cv | cend | a.x_stride) & 7) == 0 ? xs >> 8 : 0, nt = (xs - 256 * n16 + 63) >> 6;
+        const int per16 = (hilo ? 2 : 1) * n16, pert = (hilo ? 2 : 1) * nt;
+        for (int i = wave; i < a.t_rows * per16; i += kWgWaves) {
+            const int t = i / per16, r = i - t * per16, plane = r / n16, ch = r - plane * n16;
             const int slot = s_tok[t];
-            const int c = c0 + 2 * (64 * ch + lane);
+            const int c = c0 + 512 * ch + 8 * lane;
             const int row = (MODE == kGateUp) ? slot_token(slot, a.n_route, a.k) : slot;
             const uint32_t voff = (slot >= 0 && c >= cv && c < cend) ? (uint32_t)((size_t)row * a.x_stride + c) * 2u
                                                                      : kStageOut;
-            uint32_t *dst = (plane ? xl : xh) + t * xsp + 64 * ch;
+            uint32_t *dst = (plane ? xl : xh) + t * xsp + 256 * ch;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(plane ? rl : rh, (__attribute__((address_space(3))) void *)dst,
+                                                     16, voff, 0, 0, 0);
+        }
+        for (int i = wave; i < a.t_rows * pert; i += kWgWaves) {
+            const int t = i / pert, r = i - t * pert, plane = r / nt, d0 = 256 * n16 + 64 * (r - plane * nt);
+            const int slot = s_tok[t];
+            const int c = c0 + 2 * (d0 + lane);
+            const int row = (MODE == kGateUp) ? slot_token(slot, a.n_route, a.k) : slot;
+            const uint32_t voff = (slot >= 0 && c >= cv && c < cend) ? (uint32_t)((size_t)row * a.x_stride + c) * 2u
+                                                                     : kStageOut;
+            uint32_t *dst = (plane ? xl : xh) + t * xsp + d0;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(plane ? rl : rh, (__attribute__((address_space(3))) void *)dst,
                                                      4, voff, 0, 0, 0);
         }

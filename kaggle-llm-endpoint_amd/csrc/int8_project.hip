@@ -153,20 +153,30 @@ __global__ void __launch_bounds__(64 * kI8Waves) int8_project_kernel(I8Args a) {
     // a load issued after the ring could only be waited for together with it.
     const float sc = SA == MI_I8_COL_SCALES && active ? P.s[o0 + i] : 1.0f;
     // stage the split's activations (bf16 pairs, rows < B, row pitch xsp dwords) and, with per-row scales, its
-    // s[k0 .. k0 + cols) straight into LDS -- direct-to-LDS loads, 64 lanes x 4 bytes each, no registers -- issued
+    // s[k0 .. k0 + cols) straight into LDS -- direct-to-LDS loads, 64 lanes x 16 or 4 bytes each, no registers -- issued
     // ahead of the weight ring: loads complete in issue order, so waiting for all but the ring's loads waits for the
     // activations only, and the ring keeps streaming while the workgroup meets at the barrier
-    const int cw = cols / 2, xsp = i8_pitch(cw), nch = (cw + 63) >> 6;
+    const int cw = cols / 2, xsp = i8_pitch(cw);
     float *srow = (float *)(xs + a.B * xsp);
     {
         const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void *)a.x, (short)0, 0x7fffffff, kBufWord3);
         const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc((void *)P.s, (short)0, 0x7fffffff, kBufWord3);
-        const int nrow = a.B * nch, n = nrow + (SA == MI_I8_ROW_SCALES ? cols / 64 : 0);
+        // whole 256-dword chunks of a row with 16 bytes per lane when the row start and the columns are multiples of 8
+        // (a lane then wholly inside or past the columns), the rest with 4: an LDS-bound load costs about as much
+        // per instruction whatever its width
+        const int n16 = ((a.n_in | k0 | cols) & 7) == 0 ? cw >> 8 : 0, nt = (cw - 256 * n16 + 63) >> 6;
+        for (int e = wave; e < a.B * n16; e += kI8Waves) {
+            const int b = e / n16, ch = e - b * n16, d = 256 * ch + 4 * lane;
+            const uint32_t voff = d < cw ? (uint32_t)(((size_t)b * a.n_in + k0) * 2 + 4 * d) : kI8Out;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (__attribute__((address_space(3))) void *)(xs + b * xsp + 256 * ch),
+                                                     16, voff, 0, 0, 0);
+        }
+        const int nrow = a.B * nt, n = nrow + (SA == MI_I8_ROW_SCALES ? cols / 64 : 0);
         for (int e = wave; e < n; e += kI8Waves) {
             if (e < nrow) {
-                const int b = e / nch, ch = e - b * nch, d = 64 * ch + lane;
+                const int b = e / nt, d0 = 256 * n16 + 64 * (e - b * nt), d = d0 + lane;
                 const uint32_t voff = d < cw ? (uint32_t)(((size_t)b * a.n_in + k0) * 2 + 4 * d) : kI8Out;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (__attribute__((address_space(3))) void *)(xs + b * xsp + 64 * ch),
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (__attribute__((address_space(3))) void *)(xs + b * xsp + d0),
                                                          4, voff, 0, 0, 0);
             } else {
                 const int ch = e - nrow;
