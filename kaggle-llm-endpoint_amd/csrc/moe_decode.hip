@@ -549,8 +549,9 @@ static bool plan_cumulti(const mi_table *gate, const mi_table *down, int N, Deco
     const int P = cu_count();
     const int nu1 = n_units_of(gate), nu2 = n_units_of(down);
     const int nb1 = (nu1 + 3) / 4, nb2 = (nu2 + 3) / 4;
-    // measured best at D 6144, I 2048 (8 and 16 tokens)
-    int S1 = tuning(kTuneMS1, N <= 8 ? 2 : 4), S2 = tuning(kTuneMS2, 2);
+    // measured best at D 6144, I 2048 (8 and 16 tokens; with the rows staged by 16-byte loads, 3 gate/up splits at
+    // 16 tokens: 199.3-199.6 against 202.0-202.4 us with 4, and 2 at 8: 140.3-141.2 against 142.0-142.5 with 3)
+    int S1 = tuning(kTuneMS1, N <= 8 ? 2 : 3), S2 = tuning(kTuneMS2, 2);
     int r1 = tuning(kTuneMS1Rtw, 1), r2 = tuning(kTuneMS2Rtw, 2);
     S1 = S1 < 1 ? 1 : S1 > nb1 ? nb1 : S1;
     S2 = S2 < 1 ? 1 : S2 > nb2 ? nb2 : S2;
